@@ -1,0 +1,153 @@
+/*
+ * inquant_hip.h -- C ABI of libinquant_hip.so, the MI355X (gfx950) packed-KV
+ * hot path of InQuant: K4 neighbor-slot codec, V2/V4 group-wise value codec,
+ * incremental decode-metadata append, fused packed-KV decode attention and
+ * the paged (vLLM page layout) variants.
+ *
+ * Conventions
+ *   - Every entry point returns IQ_OK (0) or a negative status; the message
+ *     of the last failure on the calling thread is iq_last_error().
+ *   - All tensor arguments are raw device pointers plus element strides;
+ *     streams are hipStream_t passed as void*.  Nothing here allocates
+ *     device memory, synchronizes, or keeps state between calls: the caller
+ *     (the Python host layer, torch-owned buffers) owns every buffer.
+ *   - Work is enqueued asynchronously on `stream`.  Device-side data errors
+ *     (non-finite inputs, f16 overflow) are reported through a caller-owned
+ *     device int `bad_flag` that the kernel sets to 1; callers read it where
+ *     the reference already synchronizes.
+ *   - dtype codes: IQ_F32, IQ_BF16, IQ_F16, IQ_F64 (inputs only).
+ *
+ * Reference interfaces replaced (paths into the reference checkout):
+ *   iq_k4_quantize      src/inquant/codec.py:181-243        quantize()
+ *   iq_reuse_map        src/inquant/triton_selection.py:46-60 reuse_map(),
+ *                       src/inquant/codec.py:137-178         _reuse_map()
+ *   iq_k4_dequantize    src/inquant/codec.py:112-134         PackedTensor.dequantize()
+ *   iq_v_quantize       src/inquant/value_codec.py:51-72     quantize_values()
+ *   iq_v_dequantize     src/inquant/value_codec.py:38-48     PackedValues.dequantize()
+ *   iq_decode_append    src/inquant/triton_attention.py:234-309 PackedDecodeState.extend/_write_maps
+ *   iq_decode_attention src/inquant/triton_attention.py:317-388 PackedDecodeState.decode
+ *                       (_attention_partials :67-165 + _reduce_partials :168-181)
+ *   iq_write_pages      extensions/vllm/src/inquant_vllm/packing.py:41-55 write_codec_pages
+ *                       (+ the role-map part of layout.py:66-81 pack_pages)
+ *   iq_paged_decode     extensions/vllm/src/inquant_vllm/kernels.py:66-88 paged_decode
+ */
+#ifndef INQUANT_HIP_H
+#define INQUANT_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define IQ_ABI_VERSION 1
+
+enum iq_status { IQ_OK = 0, IQ_ERR_ARG = -1, IQ_ERR_DEVICE = -2, IQ_ERR_UNSUPPORTED = -3 };
+enum iq_dtype { IQ_F32 = 0, IQ_BF16 = 1, IQ_F16 = 2, IQ_F64 = 3 };
+
+/* Library ABI version (IQ_ABI_VERSION) and last error text of this thread. */
+int iq_abi_version(void);
+const char *iq_last_error(void);
+
+/*
+ * K4 neighbor-slot encode of x[B, H, T, D] (element strides x_strides[4]).
+ * count = floor(D * salient_fraction) (<= D/2); sample_stride >= 1;
+ * min_error != 0 selects the "min_error" donor policy, else "neighbors".
+ * Outputs (contiguous): payload u8 [B,H,T,D/2]; scales f32 [B,H,D];
+ * src/don [B,H,count] of desc_bytes (1 = u8, 4 = i32, 8 = i64);
+ * padding f32 [B,H,count].  D even, 2 <= D <= 1024.
+ * Replaces codec.py:181-243 (statistics, selection, scales, 4/8-bit slots,
+ * nibble packing, padding); bit-exact with the reference's CPU torch path.
+ */
+int iq_k4_quantize(const void *x, int x_dtype, const int64_t *x_strides,
+                   int64_t B, int64_t H, int64_t T, int64_t D,
+                   int64_t count, int64_t sample_stride, int min_error,
+                   uint8_t *payload, float *scales, void *src, void *don, int desc_bytes,
+                   float *padding, int *bad_flag, void *stream);
+
+/*
+ * Donor selection alone: saliency (and optional donor error) f32 [rows, D]
+ * contiguous -> src/don i64 [rows, count].  Replaces reuse_map /
+ * _reuse_map (triton_selection.py:46-60, codec.py:137-178).
+ */
+int iq_reuse_map(const float *saliency, const float *donor_error, int64_t rows, int64_t D,
+                 int64_t count, int64_t *src, int64_t *don, void *stream);
+
+/*
+ * K4 decode to a dense tensor: out [rows, T, D] of out_dtype (rows = B*H).
+ * Replaces PackedTensor.dequantize (codec.py:112-134).
+ */
+int iq_k4_dequantize(const uint8_t *payload, const float *scales, const void *src, const void *don,
+                     int desc_bytes, const float *padding, int64_t rows, int64_t T, int64_t D,
+                     int64_t count, void *out, int out_dtype, void *stream);
+
+/*
+ * Group-wise affine value encode of x[B, H, T, D] (strides x_strides[4]):
+ * bits in {2, 4}, group in {32, 64, 128}, D % group == 0.  Outputs
+ * payload u8 [B,H,T,D*bits/8]; scales/offsets f16 bits [B,H,T,D/group].
+ * Replaces quantize_values (value_codec.py:51-72).
+ */
+int iq_v_quantize(const void *x, int x_dtype, const int64_t *x_strides,
+                  int64_t B, int64_t H, int64_t T, int64_t D, int bits, int group,
+                  uint8_t *payload, uint16_t *scales, uint16_t *offsets, int *bad_flag, void *stream);
+
+/* Value decode: out [rows, D] of out_dtype (rows = B*H*T); value_codec.py:38-48. */
+int iq_v_dequantize(const uint8_t *payload, const uint16_t *scales, const uint16_t *offsets,
+                    int64_t rows, int64_t D, int bits, int group, void *out, int out_dtype, void *stream);
+
+/*
+ * One sealed block's device addresses, as recorded in the decode state's
+ * pointer table (triton_attention.py:337-340), plus its descriptors.
+ * v_scales/v_offsets hold the V2 scales/offsets, or for a K4-coded V its
+ * scales/padding; v_src/v_don are 0 unless V is K4-coded.
+ */
+typedef struct iq_block_ptrs {
+    uint64_t k_payload, k_scales, k_padding;
+    uint64_t v_payload, v_scales, v_offsets;
+    uint64_t k_src, k_don, v_src, v_don;
+} iq_block_ptrs;
+
+/*
+ * Append `count` blocks to a decode state: writes tables[first + i] (i64 [cap, 6])
+ * and the int8 role maps key_map / value_map [cap, H, 128] (value_map may be
+ * NULL for V2/V4 values).  Roles: -1 normal, donor channel for a source,
+ * -2 - i for donor i.  `blocks` is a HOST array; its contents travel as
+ * kernel arguments (no host-to-device copy).  Replaces
+ * PackedDecodeState.extend / _write_maps (triton_attention.py:294-369).
+ */
+int iq_decode_append(int64_t *tables, int8_t *key_map, int8_t *value_map, int64_t first, int64_t count,
+                     const iq_block_ptrs *blocks, int64_t H, int64_t S, int desc_bytes, void *stream);
+
+/*
+ * Fused single-query GQA decode over [sink | packed blocks | tail].
+ *   q [Hq, 128] (row stride q_stride_h) of q_dtype (f32, bf16, f16);
+ *   tables i64 [n_blocks, 6], key_map/value_map int8 [n_blocks, H, 128]
+ *   (value_map used only when value_bits == 0, i.e. K4-coded V);
+ *   block_tokens tokens per packed block, S salient channels per block;
+ *   value_bits in {0, 2, 4}, value_group in {32, 64, 128};
+ *   sink/tail K/V of q_dtype with (head, token) element strides, lengths
+ *   sink_t / tail_t (pointers may be NULL when the length is 0);
+ *   workspace f32 with at least iq_decode_workspace_floats(...) elements;
+ *   out [Hq, 128] contiguous of out_dtype.
+ * Keys/values are decoded and rounded to q_dtype exactly as the reference's
+ * dequantize-then-attend path does; logits, softmax and P.V accumulate in
+ * fp32.  Replaces PackedDecodeState.decode (triton_attention.py:377-448).
+ */
+int64_t iq_decode_workspace_floats(int64_t Hq, int64_t n_blocks, int64_t sink_t, int64_t tail_t);
+
+int iq_decode_attention(const void *q, int q_dtype, int64_t q_stride_h, int64_t Hq,
+                        const int64_t *tables, const int8_t *key_map, const int8_t *value_map,
+                        int64_t n_blocks, int64_t block_tokens, int64_t H, int64_t S,
+                        int value_bits, int value_group,
+                        const void *sink_k, const void *sink_v, int64_t sink_k_sh, int64_t sink_k_st,
+                        int64_t sink_v_sh, int64_t sink_v_st, int64_t sink_t,
+                        const void *tail_k, const void *tail_v, int64_t tail_k_sh, int64_t tail_k_st,
+                        int64_t tail_v_sh, int64_t tail_v_st, int64_t tail_t,
+                        float scale, float *workspace, int64_t workspace_floats,
+                        void *out, int out_dtype, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* INQUANT_HIP_H */

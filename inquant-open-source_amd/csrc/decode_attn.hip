@@ -1,0 +1,291 @@
+// Fused single-query GQA decode attention over [sink | packed blocks | tail].
+//
+// Semantics follow PackedDecodeState.decode (triton_attention.py:377-448):
+// one partition per packed block and per 256-token slice of the dense
+// sink and tail; keys and values are decoded from the K4 / V2 / V4 formats
+// (_decode_tile :33-50, _decode_value_tile :53-64), rounded to the query
+// dtype exactly as the dequantize-then-attend path does, and each
+// partition's (acc[128], m, l) online-softmax partial is merged by a
+// log-sum-exp reduction (_reduce_partials :168-181).  Softmax weights stay
+// in fp32 for the P.V product.
+//
+// This file holds the general kernel (any query dtype, K4- or V2/V4-coded
+// values, G <= 16 query heads per KV head, VALU arithmetic).
+#include "iq_common.h"
+
+namespace {
+
+constexpr int DA_THREADS = 256;
+constexpr int TILE = 32;
+constexpr int D = 128;
+constexpr int GMAX = 16;
+constexpr int DENSE_SPLIT = 256;
+
+struct DecodeArgs {
+    const void *q;
+    int qdt;
+    int64_t q_sh, Hq;
+    const int64_t *tables;
+    const int8_t *kmap, *vmap;
+    int64_t nblk, BT, H, S;
+    int vbits, vgroup;
+    const void *sk, *sv;
+    int64_t sk_sh, sk_st, sv_sh, sv_st, sink_t;
+    const void *tk, *tv;
+    int64_t tk_sh, tk_st, tv_sh, tv_st, tail_t;
+    float scale;
+    float *ws;
+    int64_t P;
+    int G;
+    void *out;
+    int odt;
+};
+
+// K4 element: role >= 0 source (partner = role), role <= -2 donor, -1 normal.
+__device__ __forceinline__ float k4_element(const uint8_t *row, const float *scales, const float *padding,
+                                            int role, int c)
+{
+    const int slot = (row[c >> 1] >> ((c & 1) * 4)) & 15;
+    if (role >= 0) {
+        const int lo = (row[role >> 1] >> ((role & 1) * 4)) & 15;
+        return __fmul_rn((float)(((slot << 4) | lo) - 128), scales[c]);
+    }
+    if (role <= -2) return padding[-role - 2];
+    return __fmul_rn((float)(slot - 8), scales[c]);
+}
+
+__global__ __launch_bounds__(DA_THREADS) void decode_partials_generic(DecodeArgs a)
+{
+    __shared__ float s_q[GMAX][D];
+    __shared__ float s_k[TILE][D + 1];
+    __shared__ float s_v[TILE][D];
+    __shared__ float s_p[GMAX][TILE];
+    __shared__ float s_m[GMAX], s_l[GMAX], s_alpha[GMAX];
+    __shared__ int8_t s_krole[D], s_vrole[D];
+    __shared__ float s_kscale[D], s_vscale[D];
+    __shared__ float s_kpad[64], s_vpad[64];
+
+    const int tid = threadIdx.x;
+    const int h = blockIdx.x;
+    const int64_t p = blockIdx.y;
+    const int G = a.G;
+
+    for (int i = tid; i < GMAX * D; i += DA_THREADS) {
+        const int g = i / D, d = i % D;
+        s_q[g][d] = g < G ? iq_load_f32(a.q, (int64_t)(h * G + g) * a.q_sh + d, a.qdt) : 0.0f;
+    }
+    if (tid < GMAX) {
+        s_m[tid] = -__uint_as_float(0x7f800000u);
+        s_l[tid] = 0.0f;
+    }
+
+    // Partition geometry.
+    const bool packed = p < a.nblk;
+    const uint8_t *kpay = nullptr, *vpay = nullptr;
+    const uint16_t *vsc16 = nullptr, *voff16 = nullptr;
+    const void *dk = nullptr, *dv = nullptr;
+    int64_t dk_sh = 0, dk_st = 0, dv_sh = 0, dv_st = 0, start = 0, length = 0;
+    if (packed) {
+        const int64_t *row = a.tables + p * 6;
+        kpay = (const uint8_t *)row[0] + (int64_t)h * a.BT * (D / 2);
+        const float *ksc = (const float *)row[1] + h * D;
+        const float *kpad = (const float *)row[2] + h * a.S;
+        vpay = (const uint8_t *)row[3];
+        for (int c = tid; c < D; c += DA_THREADS) {
+            s_krole[c] = a.kmap[(p * a.H + h) * D + c];
+            s_kscale[c] = ksc[c];
+        }
+        for (int i = tid; i < a.S; i += DA_THREADS) s_kpad[i] = kpad[i];
+        if (a.vbits == 0) {
+            vpay += (int64_t)h * a.BT * (D / 2);
+            const float *vsc = (const float *)row[4] + h * D;
+            const float *vpad = (const float *)row[5] + h * a.S;
+            for (int c = tid; c < D; c += DA_THREADS) {
+                s_vrole[c] = a.vmap[(p * a.H + h) * D + c];
+                s_vscale[c] = vsc[c];
+            }
+            for (int i = tid; i < a.S; i += DA_THREADS) s_vpad[i] = vpad[i];
+        } else {
+            vsc16 = (const uint16_t *)row[4];
+            voff16 = (const uint16_t *)row[5];
+        }
+        start = 0;
+        length = a.BT;
+    } else {
+        const int64_t dp = p - a.nblk;
+        const int64_t sink_parts = (a.sink_t + DENSE_SPLIT - 1) / DENSE_SPLIT;
+        if (dp < sink_parts) {
+            dk = a.sk; dv = a.sv;
+            dk_sh = a.sk_sh; dk_st = a.sk_st; dv_sh = a.sv_sh; dv_st = a.sv_st;
+            start = dp * DENSE_SPLIT;
+            length = a.sink_t;
+        } else {
+            dk = a.tk; dv = a.tv;
+            dk_sh = a.tk_sh; dk_st = a.tk_st; dv_sh = a.tv_sh; dv_st = a.tv_st;
+            start = (dp - sink_parts) * DENSE_SPLIT;
+            length = a.tail_t;
+        }
+    }
+    const int64_t stop = packed ? a.BT : (start + DENSE_SPLIT < length ? start + DENSE_SPLIT : length);
+    __syncthreads();
+
+    // Accumulators: thread owns channel d and query rows g0, g0 + 2, ...
+    const int d = tid % D;
+    const int g0 = tid / D;
+    float acc[GMAX / 2];
+#pragma unroll
+    for (int k = 0; k < GMAX / 2; ++k) acc[k] = 0.0f;
+
+    for (int64_t base = start; base < stop; base += TILE) {
+        // decode K and V tiles (rounded to the query dtype)
+        for (int i = tid; i < TILE * D; i += DA_THREADS) {
+            const int t = i / D, c = i % D;
+            const int64_t tok = base + t;
+            float kv = 0.0f, vv = 0.0f;
+            if (tok < stop) {
+                if (packed) {
+                    kv = k4_element(kpay + tok * (D / 2), s_kscale, s_kpad, s_krole[c], c);
+                    if (a.vbits == 0) {
+                        vv = k4_element(vpay + tok * (D / 2), s_vscale, s_vpad, s_vrole[c], c);
+                    } else {
+                        const int per_byte = 8 / a.vbits;
+                        const int64_t vr = (int64_t)h * a.BT + tok;
+                        const int code = (vpay[vr * (D / per_byte) + c / per_byte] >> ((c % per_byte) * a.vbits)) &
+                                         ((1 << a.vbits) - 1);
+                        const int64_t pi = vr * (D / a.vgroup) + c / a.vgroup;
+                        vv = __fadd_rn(__fmul_rn((float)code, iq_f16_to_f32(vsc16[pi])), iq_f16_to_f32(voff16[pi]));
+                    }
+                    kv = iq_round_to(kv, a.qdt);
+                    vv = iq_round_to(vv, a.qdt);
+                } else {
+                    kv = iq_load_f32(dk, h * dk_sh + tok * dk_st + c, a.qdt);
+                    vv = iq_load_f32(dv, h * dv_sh + tok * dv_st + c, a.qdt);
+                }
+            }
+            s_k[t][c] = kv;
+            s_v[t][c] = vv;
+        }
+        __syncthreads();
+        // logits
+        for (int i = tid; i < GMAX * TILE; i += DA_THREADS) {
+            const int g = i / TILE, t = i % TILE;
+            float s = -__uint_as_float(0x7f800000u);
+            if (g < G && base + t < stop) {
+                float dot = 0.0f;
+                for (int c = 0; c < D; ++c) dot = fmaf(s_q[g][c], s_k[t][c], dot);
+                s = dot * a.scale;
+            }
+            s_p[g][t] = s;
+        }
+        __syncthreads();
+        // online softmax, one thread per query row
+        if (tid < G) {
+            const int g = tid;
+            float mx = s_m[g];
+            for (int t = 0; t < TILE; ++t) mx = fmaxf(mx, s_p[g][t]);
+            const float alpha = expf(s_m[g] - mx);
+            float sum = 0.0f;
+            for (int t = 0; t < TILE; ++t) {
+                const float e = expf(s_p[g][t] - mx);
+                s_p[g][t] = e;
+                sum += e;
+            }
+            s_l[g] = s_l[g] * alpha + sum;
+            s_m[g] = mx;
+            s_alpha[g] = alpha;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int k = 0; k < GMAX / 2; ++k) {
+            const int g = g0 + 2 * k;
+            if (g < G) {
+                float sacc = 0.0f;
+                for (int t = 0; t < TILE; ++t) sacc = fmaf(s_p[g][t], s_v[t][d], sacc);
+                acc[k] = acc[k] * s_alpha[g] + sacc;
+            }
+        }
+        __syncthreads();
+    }
+
+    float *ws = a.ws;
+#pragma unroll
+    for (int k = 0; k < GMAX / 2; ++k) {
+        const int g = g0 + 2 * k;
+        if (g < G) ws[((int64_t)(h * G + g) * a.P + p) * (D + 2) + d] = acc[k];
+    }
+    if (tid < G) {
+        ws[((int64_t)(h * G + tid) * a.P + p) * (D + 2) + D] = s_m[tid];
+        ws[((int64_t)(h * G + tid) * a.P + p) * (D + 2) + D + 1] = s_l[tid];
+    }
+}
+
+// Log-sum-exp merge of the partition partials, one workgroup per query head.
+__global__ __launch_bounds__(D) void decode_reduce(const float *ws, int64_t P, void *out, int odt)
+{
+    const int64_t hq = blockIdx.x;
+    const int d = threadIdx.x;
+    const float *base = ws + hq * P * (D + 2);
+    float mx = -__uint_as_float(0x7f800000u);
+    for (int64_t p = 0; p < P; ++p) mx = fmaxf(mx, base[p * (D + 2) + D]);
+    float num = 0.0f, den = 0.0f;
+    for (int64_t p = 0; p < P; ++p) {
+        const float w = expf(base[p * (D + 2) + D] - mx);
+        num += base[p * (D + 2) + d] * w;
+        den += base[p * (D + 2) + D + 1] * w;
+    }
+    iq_store_as(out, hq * D + d, num / den, odt);
+}
+
+int64_t partitions(int64_t n_blocks, int64_t sink_t, int64_t tail_t)
+{
+    return n_blocks + (sink_t + DENSE_SPLIT - 1) / DENSE_SPLIT + (tail_t + DENSE_SPLIT - 1) / DENSE_SPLIT;
+}
+
+}  // namespace
+
+extern "C" int64_t iq_decode_workspace_floats(int64_t Hq, int64_t n_blocks, int64_t sink_t, int64_t tail_t)
+{
+    return Hq * partitions(n_blocks, sink_t, tail_t) * (D + 2);
+}
+
+extern "C" int iq_decode_attention(const void *q, int q_dtype, int64_t q_stride_h, int64_t Hq,
+                                   const int64_t *tables, const int8_t *key_map, const int8_t *value_map,
+                                   int64_t n_blocks, int64_t block_tokens, int64_t H, int64_t S, int value_bits,
+                                   int value_group, const void *sink_k, const void *sink_v, int64_t sink_k_sh,
+                                   int64_t sink_k_st, int64_t sink_v_sh, int64_t sink_v_st, int64_t sink_t,
+                                   const void *tail_k, const void *tail_v, int64_t tail_k_sh, int64_t tail_k_st,
+                                   int64_t tail_v_sh, int64_t tail_v_st, int64_t tail_t, float scale,
+                                   float *workspace, int64_t workspace_floats, void *out, int out_dtype,
+                                   void *stream)
+{
+    IQ_CHECK_ARG(q && out && workspace, "iq_decode_attention: null pointer");
+    IQ_CHECK_ARG(q_dtype >= IQ_F32 && q_dtype <= IQ_F16, "iq_decode_attention: bad query dtype");
+    IQ_CHECK_ARG(out_dtype >= IQ_F32 && out_dtype <= IQ_F16, "iq_decode_attention: bad output dtype");
+    IQ_CHECK_ARG(H >= 1 && Hq >= 1 && Hq % H == 0, "iq_decode_attention: Hq %% H != 0");
+    const int64_t G = Hq / H;
+    IQ_CHECK_ARG(G <= GMAX, "iq_decode_attention: %lld query heads per KV head exceeds %d", (long long)G, GMAX);
+    IQ_CHECK_ARG(n_blocks >= 0 && sink_t >= 0 && tail_t >= 0, "iq_decode_attention: negative length");
+    IQ_CHECK_ARG(n_blocks == 0 || (tables && key_map && block_tokens >= 1), "iq_decode_attention: no tables");
+    IQ_CHECK_ARG(S >= 0 && S <= 64, "iq_decode_attention: S out of range");
+    IQ_CHECK_ARG(value_bits == 0 || value_bits == 2 || value_bits == 4, "iq_decode_attention: value_bits");
+    IQ_CHECK_ARG(value_bits == 0 || value_group == 32 || value_group == 64 || value_group == 128,
+                 "iq_decode_attention: value_group");
+    IQ_CHECK_ARG(value_bits != 0 || n_blocks == 0 || value_map, "iq_decode_attention: K4 values need a map");
+    IQ_CHECK_ARG(sink_t == 0 || (sink_k && sink_v), "iq_decode_attention: null sink");
+    IQ_CHECK_ARG(tail_t == 0 || (tail_k && tail_v), "iq_decode_attention: null tail");
+    const int64_t P = partitions(n_blocks, sink_t, tail_t);
+    IQ_CHECK_ARG(P >= 1, "iq_decode_attention: attention requires at least one key/value token");
+    IQ_CHECK_ARG(P <= 65535, "iq_decode_attention: too many partitions");
+    IQ_CHECK_ARG(workspace_floats >= Hq * P * (D + 2), "iq_decode_attention: workspace too small");
+    DecodeArgs a{q, q_dtype, q_stride_h, Hq, tables, key_map, value_map, n_blocks, block_tokens, H, S,
+                 value_bits, value_group, sink_k, sink_v, sink_k_sh, sink_k_st, sink_v_sh, sink_v_st, sink_t,
+                 tail_k, tail_v, tail_k_sh, tail_k_st, tail_v_sh, tail_v_st, tail_t, scale, workspace, P,
+                 (int)G, out, out_dtype};
+    hipLaunchKernelGGL(decode_partials_generic, dim3((unsigned)H, (unsigned)P), dim3(DA_THREADS), 0,
+                       (hipStream_t)stream, a);
+    IQ_CHECK_LAUNCH("decode_partials_generic");
+    hipLaunchKernelGGL(decode_reduce, dim3((unsigned)Hq), dim3(D), 0, (hipStream_t)stream, workspace, P, out,
+                       out_dtype);
+    IQ_CHECK_LAUNCH("decode_reduce");
+    return IQ_OK;
+}

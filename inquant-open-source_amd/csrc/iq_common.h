@@ -1,0 +1,124 @@
+// Shared device/host helpers for the InQuant HIP library (gfx950 / CDNA4).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/inquant_hip.h"
+
+// ---------------------------------------------------------------- errors
+
+// Records a message for iq_last_error() and returns the status code.
+int iq_fail(int status, const char *fmt, ...);
+
+#define IQ_CHECK_ARG(cond, ...)                                   \
+    do {                                                          \
+        if (!(cond)) return iq_fail(IQ_ERR_ARG, __VA_ARGS__);     \
+    } while (0)
+
+#define IQ_CHECK_LAUNCH(what)                                                         \
+    do {                                                                              \
+        hipError_t e_ = hipGetLastError();                                            \
+        if (e_ != hipSuccess) return iq_fail(IQ_ERR_DEVICE, "%s launch: %s", what,    \
+                                             hipGetErrorString(e_));                  \
+    } while (0)
+
+// ---------------------------------------------------------------- scalars
+
+__device__ __forceinline__ float iq_bf16_to_f32(uint16_t h) { return __uint_as_float((uint32_t)h << 16); }
+
+__device__ __forceinline__ uint16_t iq_f32_to_bf16(float f)
+{
+    // gfx950 lowers this to v_cvt_pk_bf16_f32 (round to nearest even).
+    return __builtin_bit_cast(uint16_t, (__bf16)f);
+}
+
+__device__ __forceinline__ float iq_f16_to_f32(uint16_t h) { return (float)__builtin_bit_cast(_Float16, h); }
+
+__device__ __forceinline__ uint16_t iq_f32_to_f16(float f) { return __builtin_bit_cast(uint16_t, (_Float16)f); }
+
+// Load element i of a tensor of dtype `dt` as fp32 (exact for bf16/f16/f32).
+__device__ __forceinline__ float iq_load_f32(const void *p, int64_t i, int dt)
+{
+    switch (dt) {
+    case IQ_BF16: return iq_bf16_to_f32(((const uint16_t *)p)[i]);
+    case IQ_F16: return iq_f16_to_f32(((const uint16_t *)p)[i]);
+    case IQ_F64: return (float)((const double *)p)[i];
+    default: return ((const float *)p)[i];
+    }
+}
+
+// Round an fp32 value to the nearest value of dtype `dt` (fp32 result).
+__device__ __forceinline__ float iq_round_to(float v, int dt)
+{
+    if (dt == IQ_BF16) return iq_bf16_to_f32(iq_f32_to_bf16(v));
+    if (dt == IQ_F16) return iq_f16_to_f32(iq_f32_to_f16(v));
+    return v;
+}
+
+__device__ __forceinline__ void iq_store_as(void *p, int64_t i, float v, int dt)
+{
+    switch (dt) {
+    case IQ_BF16: ((uint16_t *)p)[i] = iq_f32_to_bf16(v); break;
+    case IQ_F16: ((uint16_t *)p)[i] = iq_f32_to_f16(v); break;
+    case IQ_F64: ((double *)p)[i] = (double)v; break;
+    default: ((float *)p)[i] = v; break;
+    }
+}
+
+__device__ __forceinline__ bool iq_isfinite(float x) { return (__float_as_uint(x) & 0x7f800000u) != 0x7f800000u; }
+
+// ---------------------------------------------------------------- torch CPU reduction orders
+
+// Columns [0, iq_cascade_columns(D)) of an outer reduction are summed by
+// torch's cascade; the rest by its interleaved row_sum (8-float vectors).
+__host__ __device__ __forceinline__ int64_t iq_cascade_columns(int64_t D)
+{
+    return D >= 8 ? (D / 32) * 32 : (D / 4) * 4;
+}
+
+__device__ __forceinline__ int iq_ceil_log2(int64_t x)
+{
+    int r = 0;
+    if (x <= 1) return 0;
+    x -= 1;
+    while (x) { ++r; x >>= 1; }
+    return r;
+}
+
+// Incremental form of torch's 4-level cascade sum (aten multi_row_sum).
+struct IqCascade {
+    float acc[4];
+    int64_t i;      // values consumed
+    int lp;         // log2 of the chunk length
+    __device__ void init(int64_t n)
+    {
+        acc[0] = acc[1] = acc[2] = acc[3] = 0.0f;
+        i = 0;
+        lp = iq_ceil_log2(n) / 4;
+        if (lp < 4) lp = 4;
+        full = (n >> lp) << lp;   // values that belong to complete chunks
+    }
+    int64_t full;
+    __device__ void add(float x)
+    {
+        acc[0] = __fadd_rn(acc[0], x);
+        ++i;
+        if (i <= full && (i & (((int64_t)1 << lp) - 1)) == 0) {
+            const int64_t mask = ((int64_t)1 << lp) - 1;
+            for (int j = 1; j < 4; ++j) {
+                acc[j] = __fadd_rn(acc[j], acc[j - 1]);
+                acc[j - 1] = 0.0f;
+                if ((i & (mask << (j * lp))) != 0) break;
+            }
+        }
+    }
+    __device__ float finish() const
+    {
+        float s = acc[0];
+        s = __fadd_rn(s, acc[1]);
+        s = __fadd_rn(s, acc[2]);
+        s = __fadd_rn(s, acc[3]);
+        return s;
+    }
+};

@@ -1,0 +1,252 @@
+// K4 neighbor-slot encoder and standalone donor selector (gfx950).
+//
+// One 256-thread workgroup encodes one (batch, head) row of x[B, H, T, D]:
+//   phase 1  per-channel statistics: sampled saliency and mean in torch's
+//            CPU summation order, full-block amax, and for min_error the
+//            fp64 Welford var_mean (codec.py:200-210);
+//   phase 2  donor selection by wavefront 0 (select_dev.h);
+//   phase 3  scales, 4-bit slots, 8-bit salient codes split across the
+//            source and donor slots, nibble packing, padding (codec.py:218-233).
+// Results are bit-identical to the reference CPU implementation.
+#include "select_dev.h"
+
+#include <cstdarg>
+#include <cstdio>
+
+namespace {
+
+constexpr int K4_THREADS = 256;
+
+struct K4Args {
+    const void *x;
+    int dt;
+    int64_t sb, sh, st, sc;   // element strides
+    int64_t H, T, D, count, stride;
+    int min_error;
+    uint8_t *payload;
+    float *scales;
+    void *src, *don;
+    int desc_bytes;
+    float *padding;
+    int *bad;
+};
+
+__device__ __forceinline__ void store_desc(void *p, int64_t i, int v, int bytes)
+{
+    if (bytes == 1) ((uint8_t *)p)[i] = (uint8_t)v;
+    else if (bytes == 4) ((int32_t *)p)[i] = v;
+    else ((int64_t *)p)[i] = v;
+}
+
+// Sampled sums of one channel in torch's order (cascade, or interleaved row_sum).
+__device__ void sampled_sums(const void *x, int dt, int64_t base, int64_t step, int64_t ns, bool cascade_col,
+                             float &sum_abs, float &sum)
+{
+    if (cascade_col) {
+        IqCascade a, s;
+        a.init(ns);
+        s.init(ns);
+        for (int64_t r = 0; r < ns; ++r) {
+            const float v = iq_load_f32(x, base + r * step, dt);
+            a.add(fabsf(v));
+            s.add(v);
+        }
+        sum_abs = a.finish();
+        sum = s.finish();
+    } else {
+        const int64_t g = ns / 4;
+        float pa[4], ps[4];
+        for (int k = 0; k < 4; ++k) {
+            IqCascade a, s;
+            a.init(g);
+            s.init(g);
+            for (int64_t r = 0; r < g; ++r) {
+                const float v = iq_load_f32(x, base + (4 * r + k) * step, dt);
+                a.add(fabsf(v));
+                s.add(v);
+            }
+            pa[k] = a.finish();
+            ps[k] = s.finish();
+        }
+        for (int64_t r = 4 * g; r < ns; ++r) {
+            const float v = iq_load_f32(x, base + r * step, dt);
+            pa[0] = __fadd_rn(pa[0], fabsf(v));
+            ps[0] = __fadd_rn(ps[0], v);
+        }
+        sum_abs = __fadd_rn(__fadd_rn(__fadd_rn(pa[0], pa[1]), pa[2]), pa[3]);
+        sum = __fadd_rn(__fadd_rn(__fadd_rn(ps[0], ps[1]), ps[2]), ps[3]);
+    }
+}
+
+__global__ __launch_bounds__(K4_THREADS) void k4_encode_kernel(K4Args a)
+{
+    __shared__ float s_sal[IQ_MAXD];
+    __shared__ float s_smean[IQ_MAXD];
+    __shared__ float s_err[IQ_MAXD];
+    __shared__ float s_scale[IQ_MAXD];
+    __shared__ int16_t s_src_of[IQ_MAXD];
+    __shared__ uint8_t s_is_src[IQ_MAXD];
+    __shared__ int16_t s_src[IQ_MAXD / 2];
+    __shared__ int16_t s_don[IQ_MAXD / 2];
+    __shared__ int s_bad;
+
+    const int tid = threadIdx.x;
+    const int64_t row = blockIdx.x;
+    const int64_t b = row / a.H, h = row % a.H;
+    const int64_t base = b * a.sb + h * a.sh;
+    const int64_t T = a.T, D = a.D;
+    const int64_t ns = (T + a.stride - 1) / a.stride;
+    const int64_t ncasc = iq_cascade_columns(D);
+
+    if (tid == 0) s_bad = 0;
+    __syncthreads();
+
+    // ---- phase 1: per-channel statistics (one thread per channel)
+    for (int64_t c = tid; c < D; c += K4_THREADS) {
+        const int64_t cb = base + c * a.sc;
+        float sum_abs, sum;
+        sampled_sums(a.x, a.dt, cb, a.st * a.stride, ns, c < ncasc, sum_abs, sum);
+        const float smean = sum / (float)ns;
+        s_sal[c] = sum_abs / (float)ns;
+        s_smean[c] = smean;
+        float amax = 0.0f;
+        bool bad = false;
+        double mean = 0.0, m2 = 0.0;
+        for (int64_t t = 0; t < T; ++t) {
+            const float v = iq_load_f32(a.x, cb + t * a.st, a.dt);
+            bad |= !iq_isfinite(v);
+            amax = fmaxf(amax, fabsf(v));
+            if (a.min_error) {
+                const double dv = (double)v;
+                const double delta = __dsub_rn(dv, mean);
+                mean = __dadd_rn(mean, delta / (double)(t + 1));
+                const double nd = __dsub_rn(dv, mean);
+                m2 = __dadd_rn(m2, __dmul_rn(delta, nd));
+            }
+        }
+        if (a.min_error) {
+            const float var = (float)(m2 / (double)T);
+            const float diff = __fsub_rn((float)mean, smean);
+            s_err[c] = __fadd_rn(var, __fmul_rn(diff, diff));
+        }
+        s_scale[c] = amax;
+        if (bad) s_bad = 1;
+    }
+    __syncthreads();
+
+    // ---- phase 2: selection by wavefront 0
+    if (tid < 64) {
+        iq_select_wave(s_sal, a.min_error ? s_err : nullptr, (int)D, (int)a.count, s_src, s_don, s_is_src,
+                       s_src_of);
+    }
+    __syncthreads();
+
+    // ---- scales and descriptors
+    const float flt_min = 1.17549435e-38f;
+    for (int64_t c = tid; c < D; c += K4_THREADS) {
+        const float s = s_scale[c] / (s_is_src[c] ? 127.0f : 7.0f);
+        const float sc = s < flt_min ? flt_min : s;
+        s_scale[c] = sc;
+        a.scales[row * D + c] = sc;
+    }
+    for (int64_t i = tid; i < a.count; i += K4_THREADS) {
+        store_desc(a.src, row * a.count + i, s_src[i], a.desc_bytes);
+        store_desc(a.don, row * a.count + i, s_don[i], a.desc_bytes);
+        a.padding[row * a.count + i] = s_smean[s_don[i]];
+    }
+    if (tid == 0 && s_bad) atomicOr(a.bad, 1);
+    __syncthreads();
+
+    // ---- phase 3: slots and nibble packing, one payload byte per step
+    const int64_t half = D / 2;
+    uint8_t *out = a.payload + row * T * half;
+    for (int64_t idx = tid; idx < T * half; idx += K4_THREADS) {
+        const int64_t t = idx / half, j = idx - t * half;
+        const int64_t tb = base + t * a.st;
+        uint32_t slots[2];
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+            const int64_t c = 2 * j + e;
+            const int16_t owner = s_src_of[c];
+            float q;
+            if (s_is_src[c] || owner >= 0) {
+                const int64_t sc = s_is_src[c] ? c : owner;
+                q = rintf(iq_load_f32(a.x, tb + sc * a.sc, a.dt) / s_scale[sc]);
+                q = fminf(fmaxf(q, -127.0f), 127.0f);
+                const uint32_t code = (uint32_t)(q + 128.0f);
+                slots[e] = s_is_src[c] ? (code >> 4) : (code & 15u);
+            } else {
+                q = rintf(iq_load_f32(a.x, tb + c * a.sc, a.dt) / s_scale[c]);
+                q = fminf(fmaxf(q, -7.0f), 7.0f);
+                slots[e] = (uint32_t)(q + 8.0f);
+            }
+        }
+        out[idx] = (uint8_t)(slots[0] | (slots[1] << 4));
+    }
+}
+
+struct SelectArgs {
+    const float *sal, *err;
+    int64_t D, count;
+    int64_t *src, *don;
+};
+
+__global__ __launch_bounds__(64) void reuse_map_kernel(SelectArgs a)
+{
+    __shared__ float s_sal[IQ_MAXD];
+    __shared__ float s_err[IQ_MAXD];
+    __shared__ int16_t s_src_of[IQ_MAXD];
+    __shared__ uint8_t s_is_src[IQ_MAXD];
+    __shared__ int16_t s_src[IQ_MAXD / 2];
+    __shared__ int16_t s_don[IQ_MAXD / 2];
+    const int64_t row = blockIdx.x;
+    for (int64_t c = threadIdx.x; c < a.D; c += 64) {
+        s_sal[c] = a.sal[row * a.D + c];
+        if (a.err) s_err[c] = a.err[row * a.D + c];
+    }
+    __syncthreads();
+    iq_select_wave(s_sal, a.err ? s_err : nullptr, (int)a.D, (int)a.count, s_src, s_don, s_is_src, s_src_of);
+    __syncthreads();
+    for (int64_t i = threadIdx.x; i < a.count; i += 64) {
+        a.src[row * a.count + i] = s_src[i];
+        a.don[row * a.count + i] = s_don[i];
+    }
+}
+
+}  // namespace
+
+extern "C" int iq_k4_quantize(const void *x, int x_dtype, const int64_t *x_strides, int64_t B, int64_t H,
+                              int64_t T, int64_t D, int64_t count, int64_t sample_stride, int min_error,
+                              uint8_t *payload, float *scales, void *src, void *don, int desc_bytes,
+                              float *padding, int *bad_flag, void *stream)
+{
+    IQ_CHECK_ARG(x && x_strides && payload && scales && bad_flag, "iq_k4_quantize: null pointer");
+    IQ_CHECK_ARG(x_dtype >= IQ_F32 && x_dtype <= IQ_F64, "iq_k4_quantize: bad dtype %d", x_dtype);
+    IQ_CHECK_ARG(B >= 1 && H >= 1 && T >= 1, "iq_k4_quantize: empty shape");
+    IQ_CHECK_ARG(D >= 2 && D % 2 == 0 && D <= IQ_MAXD, "iq_k4_quantize: D=%lld must be even and <= %d",
+                 (long long)D, IQ_MAXD);
+    IQ_CHECK_ARG(count >= 0 && 2 * count <= D, "iq_k4_quantize: count=%lld out of range", (long long)count);
+    IQ_CHECK_ARG(count == 0 || (src && don && padding), "iq_k4_quantize: null descriptor output");
+    IQ_CHECK_ARG(sample_stride >= 1, "iq_k4_quantize: sample_stride must be positive");
+    IQ_CHECK_ARG(desc_bytes == 1 || desc_bytes == 4 || desc_bytes == 8, "iq_k4_quantize: desc_bytes");
+    IQ_CHECK_ARG(B * H <= 0x7fffffffLL, "iq_k4_quantize: too many rows");
+    K4Args a{x, x_dtype, x_strides[0], x_strides[1], x_strides[2], x_strides[3], H, T, D, count, sample_stride,
+             min_error ? 1 : 0, payload, scales, src, don, desc_bytes, padding, bad_flag};
+    hipLaunchKernelGGL(k4_encode_kernel, dim3((unsigned)(B * H)), dim3(K4_THREADS), 0, (hipStream_t)stream, a);
+    IQ_CHECK_LAUNCH("k4_encode_kernel");
+    return IQ_OK;
+}
+
+extern "C" int iq_reuse_map(const float *saliency, const float *donor_error, int64_t rows, int64_t D,
+                            int64_t count, int64_t *src, int64_t *don, void *stream)
+{
+    IQ_CHECK_ARG(rows >= 0 && D >= 1 && D <= IQ_MAXD, "iq_reuse_map: D=%lld unsupported", (long long)D);
+    IQ_CHECK_ARG(count >= 0 && 2 * count <= D, "iq_reuse_map: count=%lld out of range", (long long)count);
+    IQ_CHECK_ARG(rows <= 0x7fffffffLL, "iq_reuse_map: too many rows");
+    if (rows == 0 || count == 0) return IQ_OK;
+    IQ_CHECK_ARG(saliency && src && don, "iq_reuse_map: null pointer");
+    SelectArgs a{saliency, donor_error, D, count, src, don};
+    hipLaunchKernelGGL(reuse_map_kernel, dim3((unsigned)rows), dim3(64), 0, (hipStream_t)stream, a);
+    IQ_CHECK_LAUNCH("reuse_map_kernel");
+    return IQ_OK;
+}

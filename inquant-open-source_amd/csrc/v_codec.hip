@@ -1,0 +1,200 @@
+// Group-wise affine value codec (V2 / V4) and the K4/V dequantizers (gfx950).
+//
+// Encode (value_codec.py:51-72), per (token, group of `group` channels):
+//   lo = min, hi = max;  offset = f16(lo);
+//   scale = f16(max((hi - lo) / levels, 2^-14));
+//   code = clamp(rint((x - f32(offset)) / f32(scale)), 0, levels);
+//   codes packed LSB-first, 8/bits per byte.
+// Decode (value_codec.py:38-48): code * f32(scale) + f32(offset).  The
+// product of a <=4-bit code and an f16 scale is exact in fp32, so the
+// reference's separate multiply and add round exactly once.
+#include "iq_common.h"
+
+namespace {
+
+constexpr int V_THREADS = 256;
+
+struct VEncArgs {
+    const void *x;
+    int dt;
+    int64_t sb, sh, st, sc;
+    int64_t H, T, D;
+    int bits, group;
+    int64_t units;          // B*H*T*(D/group)
+    uint8_t *payload;
+    uint16_t *scales, *offsets;
+    int *bad;
+};
+
+// One thread per (row, group).
+__global__ __launch_bounds__(V_THREADS) void v_encode_kernel(VEncArgs a)
+{
+    const int64_t u = (int64_t)blockIdx.x * V_THREADS + threadIdx.x;
+    if (u >= a.units) return;
+    const int64_t groups = a.D / a.group;
+    const int64_t r = u / groups, g = u - r * groups;      // r = (b*H + h)*T + t
+    const int64_t t = r % a.T, bh = r / a.T;
+    const int64_t b = bh / a.H, h = bh % a.H;
+    const int64_t base = b * a.sb + h * a.sh + t * a.st + g * a.group * a.sc;
+    const int levels = (1 << a.bits) - 1;
+
+    float lo = iq_load_f32(a.x, base, a.dt), hi = lo;
+    bool bad = false;
+    for (int j = 0; j < a.group; ++j) {
+        const float v = iq_load_f32(a.x, base + j * a.sc, a.dt);
+        bad |= !iq_isfinite(v);
+        lo = fminf(lo, v);
+        hi = fmaxf(hi, v);
+    }
+    const uint16_t off_h = iq_f32_to_f16(lo);
+    float s = __fsub_rn(hi, lo) / (float)levels;
+    const float tiny = 6.103515625e-05f;
+    s = s < tiny ? tiny : s;
+    const uint16_t sc_h = iq_f32_to_f16(s);
+    const float off = iq_f16_to_f32(off_h), sc = iq_f16_to_f32(sc_h);
+    bad |= !iq_isfinite(off) || !iq_isfinite(sc);
+    a.offsets[u] = off_h;
+    a.scales[u] = sc_h;
+
+    const int per_byte = 8 / a.bits;
+    uint8_t *out = a.payload + r * (a.D / per_byte) + g * (a.group / per_byte);
+    for (int j = 0; j < a.group; j += per_byte) {
+        uint32_t byte = 0;
+        for (int e = 0; e < per_byte; ++e) {
+            const float v = iq_load_f32(a.x, base + (j + e) * a.sc, a.dt);
+            float q = rintf(__fsub_rn(v, off) / sc);
+            q = fminf(fmaxf(q, 0.0f), (float)levels);
+            byte |= (uint32_t)q << (e * a.bits);
+        }
+        out[j / per_byte] = (uint8_t)byte;
+    }
+    if (bad) atomicOr(a.bad, 1);
+}
+
+struct VDecArgs {
+    const uint8_t *payload;
+    const uint16_t *scales, *offsets;
+    int64_t rows, D;
+    int bits, group;
+    void *out;
+    int out_dt;
+};
+
+__global__ __launch_bounds__(V_THREADS) void v_decode_kernel(VDecArgs a)
+{
+    const int64_t i = (int64_t)blockIdx.x * V_THREADS + threadIdx.x;
+    if (i >= a.rows * a.D) return;
+    const int64_t r = i / a.D, c = i - r * a.D;
+    const int per_byte = 8 / a.bits;
+    const int code = (a.payload[r * (a.D / per_byte) + c / per_byte] >> ((c % per_byte) * a.bits)) &
+                     ((1 << a.bits) - 1);
+    const int64_t p = r * (a.D / a.group) + c / a.group;
+    const float v = __fadd_rn(__fmul_rn((float)code, iq_f16_to_f32(a.scales[p])), iq_f16_to_f32(a.offsets[p]));
+    iq_store_as(a.out, i, v, a.out_dt);
+}
+
+struct KDecArgs {
+    const uint8_t *payload;
+    const float *scales;
+    const void *src, *don;
+    int desc_bytes;
+    const float *padding;
+    int64_t rows, T, D, count;
+    void *out;
+    int out_dt;
+};
+
+__device__ __forceinline__ int load_desc(const void *p, int64_t i, int bytes)
+{
+    if (bytes == 1) return ((const uint8_t *)p)[i];
+    if (bytes == 4) return ((const int32_t *)p)[i];
+    return (int)((const int64_t *)p)[i];
+}
+
+// One workgroup per (row, token); roles are rebuilt per workgroup in LDS.
+__global__ __launch_bounds__(V_THREADS) void k4_decode_kernel(KDecArgs a)
+{
+    __shared__ int16_t s_role[1024];
+    const int64_t rt = blockIdx.x;            // row * T + t
+    const int64_t row = rt / a.T;
+    for (int64_t c = threadIdx.x; c < a.D; c += V_THREADS) s_role[c] = -1;
+    __syncthreads();
+    for (int64_t i = threadIdx.x; i < a.count; i += V_THREADS) {
+        const int s = load_desc(a.src, row * a.count + i, a.desc_bytes);
+        const int d = load_desc(a.don, row * a.count + i, a.desc_bytes);
+        s_role[s] = (int16_t)d;
+        s_role[d] = (int16_t)(-2 - i);
+    }
+    __syncthreads();
+    const uint8_t *pt = a.payload + rt * (a.D / 2);
+    for (int64_t c = threadIdx.x; c < a.D; c += V_THREADS) {
+        const int role = s_role[c];
+        const int slot = (pt[c >> 1] >> ((c & 1) * 4)) & 15;
+        float v;
+        if (role >= 0) {
+            const int lo = (pt[role >> 1] >> ((role & 1) * 4)) & 15;
+            v = __fmul_rn((float)(((slot << 4) | lo) - 128), a.scales[row * a.D + c]);
+        } else if (role <= -2) {
+            v = a.padding[row * a.count + (-role - 2)];
+        } else {
+            v = __fmul_rn((float)(slot - 8), a.scales[row * a.D + c]);
+        }
+        iq_store_as(a.out, rt * a.D + c, v, a.out_dt);
+    }
+}
+
+}  // namespace
+
+extern "C" int iq_v_quantize(const void *x, int x_dtype, const int64_t *x_strides, int64_t B, int64_t H,
+                             int64_t T, int64_t D, int bits, int group, uint8_t *payload, uint16_t *scales,
+                             uint16_t *offsets, int *bad_flag, void *stream)
+{
+    IQ_CHECK_ARG(x && x_strides && payload && scales && offsets && bad_flag, "iq_v_quantize: null pointer");
+    IQ_CHECK_ARG(x_dtype >= IQ_F32 && x_dtype <= IQ_F64, "iq_v_quantize: bad dtype");
+    IQ_CHECK_ARG(bits == 2 || bits == 4, "iq_v_quantize: bits must be 2 or 4");
+    IQ_CHECK_ARG(group == 32 || group == 64 || group == 128, "iq_v_quantize: group must be 32, 64 or 128");
+    IQ_CHECK_ARG(B >= 1 && H >= 1 && T >= 1 && D >= group && D % group == 0, "iq_v_quantize: bad shape");
+    const int64_t units = B * H * T * (D / group);
+    IQ_CHECK_ARG((units + V_THREADS - 1) / V_THREADS <= 0x7fffffffLL, "iq_v_quantize: too large");
+    VEncArgs a{x, x_dtype, x_strides[0], x_strides[1], x_strides[2], x_strides[3], H, T, D, bits, group, units,
+               payload, scales, offsets, bad_flag};
+    hipLaunchKernelGGL(v_encode_kernel, dim3((unsigned)((units + V_THREADS - 1) / V_THREADS)), dim3(V_THREADS), 0,
+                       (hipStream_t)stream, a);
+    IQ_CHECK_LAUNCH("v_encode_kernel");
+    return IQ_OK;
+}
+
+extern "C" int iq_v_dequantize(const uint8_t *payload, const uint16_t *scales, const uint16_t *offsets,
+                               int64_t rows, int64_t D, int bits, int group, void *out, int out_dtype, void *stream)
+{
+    IQ_CHECK_ARG(bits == 2 || bits == 4, "iq_v_dequantize: bits must be 2 or 4");
+    IQ_CHECK_ARG(group == 32 || group == 64 || group == 128, "iq_v_dequantize: bad group");
+    IQ_CHECK_ARG(rows >= 0 && D >= group && D % group == 0, "iq_v_dequantize: bad shape");
+    IQ_CHECK_ARG(out_dtype >= IQ_F32 && out_dtype <= IQ_F16, "iq_v_dequantize: bad out dtype");
+    if (rows == 0) return IQ_OK;
+    IQ_CHECK_ARG(payload && scales && offsets && out, "iq_v_dequantize: null pointer");
+    const int64_t n = rows * D;
+    VDecArgs a{payload, scales, offsets, rows, D, bits, group, out, out_dtype};
+    hipLaunchKernelGGL(v_decode_kernel, dim3((unsigned)((n + V_THREADS - 1) / V_THREADS)), dim3(V_THREADS), 0,
+                       (hipStream_t)stream, a);
+    IQ_CHECK_LAUNCH("v_decode_kernel");
+    return IQ_OK;
+}
+
+extern "C" int iq_k4_dequantize(const uint8_t *payload, const float *scales, const void *src, const void *don,
+                                int desc_bytes, const float *padding, int64_t rows, int64_t T, int64_t D,
+                                int64_t count, void *out, int out_dtype, void *stream)
+{
+    IQ_CHECK_ARG(D >= 2 && D % 2 == 0 && D <= 1024, "iq_k4_dequantize: bad D");
+    IQ_CHECK_ARG(count >= 0 && 2 * count <= D, "iq_k4_dequantize: bad count");
+    IQ_CHECK_ARG(desc_bytes == 1 || desc_bytes == 4 || desc_bytes == 8, "iq_k4_dequantize: desc_bytes");
+    IQ_CHECK_ARG(out_dtype >= IQ_F32 && out_dtype <= IQ_F16, "iq_k4_dequantize: bad out dtype");
+    IQ_CHECK_ARG(rows >= 0 && T >= 0, "iq_k4_dequantize: bad shape");
+    if (rows == 0 || T == 0) return IQ_OK;
+    IQ_CHECK_ARG(payload && scales && out && (count == 0 || (src && don && padding)), "iq_k4_dequantize: null");
+    IQ_CHECK_ARG(rows * T <= 0x7fffffffLL, "iq_k4_dequantize: too large");
+    KDecArgs a{payload, scales, src, don, desc_bytes, padding, rows, T, D, count, out, out_dtype};
+    hipLaunchKernelGGL(k4_decode_kernel, dim3((unsigned)(rows * T)), dim3(V_THREADS), 0, (hipStream_t)stream, a);
+    IQ_CHECK_LAUNCH("k4_decode_kernel");
+    return IQ_OK;
+}

@@ -1,0 +1,175 @@
+"""ctypes binding of the CPU restatement in iq_oracle.c.
+
+TEST INFRASTRUCTURE ONLY: imported by tests/, __graft_entry__.smoke() and the
+cpu_baseline leg of bench.py, always as the checker or the timed CPU port,
+never as part of the product path.  Inputs and outputs are numpy arrays.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+_LIB_PATH = os.path.join(_HERE, "libiq_oracle.so")
+_lib = None
+
+c_i64 = ctypes.c_int64
+c_p = ctypes.c_void_p
+
+
+def build() -> str:
+    subprocess.run(["make", "-s", "-C", _HERE], check=True)
+    return _LIB_PATH
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(_LIB_PATH):
+            build()
+        _lib = ctypes.CDLL(_LIB_PATH)
+        _lib.iqo_f32_to_bf16.restype = ctypes.c_uint16
+        _lib.iqo_f32_to_bf16.argtypes = [ctypes.c_float]
+        _lib.iqo_f32_to_f16.restype = ctypes.c_uint16
+        _lib.iqo_f32_to_f16.argtypes = [ctypes.c_float]
+        _lib.iqo_k4_quantize.restype = ctypes.c_int
+        _lib.iqo_k4_quantize.argtypes = [c_p, c_i64, c_i64, c_i64, c_i64, c_i64, ctypes.c_int,
+                                         c_p, c_p, c_p, c_p, c_p]
+        _lib.iqo_k4_stats.argtypes = [c_p, c_i64, c_i64, c_i64, ctypes.c_int, c_p, c_p, c_p, c_p]
+        _lib.iqo_reuse_map.argtypes = [c_p, c_p, c_i64, c_i64, c_i64, c_p, c_p]
+        _lib.iqo_k4_dequantize.argtypes = [c_p, c_p, c_p, c_p, c_p, c_i64, c_i64, c_i64, c_i64,
+                                           ctypes.c_int, c_p]
+        _lib.iqo_v_quantize.restype = ctypes.c_int
+        _lib.iqo_v_quantize.argtypes = [c_p, c_i64, c_i64, ctypes.c_int, ctypes.c_int, c_p, c_p, c_p]
+        _lib.iqo_v_dequantize.argtypes = [c_p, c_p, c_p, c_i64, c_i64, ctypes.c_int, ctypes.c_int,
+                                          ctypes.c_int, c_p]
+        _lib.iqo_role_map.argtypes = [c_p, c_p, c_i64, c_i64, c_i64, c_p]
+        _lib.iqo_attend.argtypes = [c_p, c_p, c_p, c_i64, c_i64, c_i64, c_i64, ctypes.c_double, c_p]
+    return _lib
+
+
+def _ptr(a: np.ndarray):
+    return a.ctypes.data_as(c_p)
+
+
+DTYPE_CODE = {"float32": 0, "bfloat16": 1, "float16": 2}
+
+
+def k4_stats(x: np.ndarray, stride: int, min_error: bool):
+    """x fp32 [T, D] -> (saliency, sampled_mean, err or None, amax)."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    T, D = x.shape
+    out = [np.empty(D, np.float32) for _ in range(4)]
+    lib().iqo_k4_stats(_ptr(x), T, D, stride, int(min_error), *[_ptr(o) for o in out])
+    return out[0], out[1], (out[2] if min_error else None), out[3]
+
+
+def reuse_map(saliency: np.ndarray, count: int, donor_error: np.ndarray | None = None):
+    """saliency fp32 [..., D] -> (sources, donors) int64 [..., count] (codec.py:137-178)."""
+    sal = np.ascontiguousarray(saliency, dtype=np.float32)
+    D = sal.shape[-1]
+    rows = sal.size // D if D else 0
+    err = None if donor_error is None else np.ascontiguousarray(donor_error, dtype=np.float32)
+    src = np.zeros((*sal.shape[:-1], count), np.int64)
+    don = np.zeros_like(src)
+    if count and rows:
+        lib().iqo_reuse_map(_ptr(sal), None if err is None else _ptr(err), rows, D, count,
+                            _ptr(src), _ptr(don))
+    return src, don
+
+
+def k4_quantize(x: np.ndarray, sample_stride: int = 8, salient_fraction: float = 0.125,
+                donor_policy: str = "neighbors"):
+    """x fp32 [B, H, T, D] -> dict of payload/scales/src/don/padding (codec.py:181-243)."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    B, H, T, D = x.shape
+    count = int(np.floor(D * salient_fraction))
+    rows = B * H
+    payload = np.empty((B, H, T, D // 2), np.uint8)
+    scales = np.empty((B, H, D), np.float32)
+    src = np.empty((B, H, count), np.int64)
+    don = np.empty((B, H, count), np.int64)
+    padding = np.empty((B, H, count), np.float32)
+    rc = lib().iqo_k4_quantize(_ptr(x), rows, T, D, count, sample_stride, int(donor_policy == "min_error"),
+                               _ptr(payload), _ptr(scales), _ptr(src), _ptr(don), _ptr(padding))
+    if rc:
+        raise ValueError("x must contain finite values representable in float32")
+    return {"payload": payload, "scales": scales, "salient_channels": src, "donor_channels": don,
+            "padding": padding}
+
+
+def k4_dequantize(packed: dict, dtype: str = "float32") -> np.ndarray:
+    payload = np.ascontiguousarray(packed["payload"], np.uint8)
+    B, H, T, half = payload.shape
+    D = half * 2
+    src = np.ascontiguousarray(packed["salient_channels"], np.int64)
+    count = src.shape[-1]
+    out = np.empty((B, H, T, D), np.float32)
+    lib().iqo_k4_dequantize(_ptr(payload), _ptr(np.ascontiguousarray(packed["scales"], np.float32)),
+                            _ptr(src), _ptr(np.ascontiguousarray(packed["donor_channels"], np.int64)),
+                            _ptr(np.ascontiguousarray(packed["padding"], np.float32)),
+                            B * H, T, D, count, DTYPE_CODE[dtype], _ptr(out))
+    return out
+
+
+def v_quantize(x: np.ndarray, bits: int = 2, group_size: int = 64):
+    """x fp32 [..., D] -> payload u8, scales/offsets as float16 arrays (value_codec.py:51-72)."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    D = x.shape[-1]
+    rows = x.size // D
+    payload = np.empty((*x.shape[:-1], D * bits // 8), np.uint8)
+    scales = np.empty((*x.shape[:-1], D // group_size), np.uint16)
+    offsets = np.empty_like(scales)
+    rc = lib().iqo_v_quantize(_ptr(x), rows, D, bits, group_size, _ptr(payload), _ptr(scales), _ptr(offsets))
+    if rc:
+        raise ValueError("Values and stored FP16 quantization parameters must be finite")
+    return {"payload": payload, "scales": scales.view(np.float16), "offsets": offsets.view(np.float16)}
+
+
+def v_dequantize(packed: dict, bits: int, group_size: int, dtype: str = "float32") -> np.ndarray:
+    payload = np.ascontiguousarray(packed["payload"], np.uint8)
+    D = payload.shape[-1] * 8 // bits
+    rows = payload.size // payload.shape[-1]
+    out = np.empty((*payload.shape[:-1], D), np.float32)
+    lib().iqo_v_dequantize(_ptr(payload), _ptr(np.ascontiguousarray(packed["scales"]).view(np.uint16)),
+                           _ptr(np.ascontiguousarray(packed["offsets"]).view(np.uint16)),
+                           rows, D, bits, group_size, DTYPE_CODE[dtype], _ptr(out))
+    return out
+
+
+def role_map(src: np.ndarray, don: np.ndarray, D: int = 128) -> np.ndarray:
+    """src/don int64 [heads, count] -> int16 [heads, D] roles (triton_attention.py:361-369)."""
+    src = np.ascontiguousarray(src, np.int64)
+    don = np.ascontiguousarray(don, np.int64)
+    heads, count = src.shape
+    out = np.empty((heads, D), np.int16)
+    lib().iqo_role_map(_ptr(src), _ptr(don), heads, D, count, _ptr(out))
+    return out
+
+
+def attend(q: np.ndarray, k: np.ndarray, v: np.ndarray, scale: float) -> np.ndarray:
+    """fp64 attention: q [Hq, D], k/v [H, T, D] -> [Hq, D] float64 (qwen_fused.py:21-30)."""
+    q = np.ascontiguousarray(q, np.float32)
+    k = np.ascontiguousarray(k, np.float32)
+    v = np.ascontiguousarray(v, np.float32)
+    Hq, D = q.shape
+    H, T, _ = k.shape
+    out = np.empty((Hq, D), np.float64)
+    lib().iqo_attend(_ptr(q), _ptr(k), _ptr(v), Hq, H, T, D, float(scale), _ptr(out))
+    return out
+
+
+def to_bf16(x: np.ndarray) -> np.ndarray:
+    """Round fp32 values to bf16 (RNE) and return them as fp32."""
+    u = np.ascontiguousarray(x, np.float32).view(np.uint32).astype(np.uint64)
+    nan = (u & 0x7FFFFFFF) > 0x7F800000
+    r = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16) << 16
+    r = np.where(nan, (u | 0x400000) & 0xFFFF0000, r)
+    return r.astype(np.uint32).view(np.float32)
+
+
+def to_f16(x: np.ndarray) -> np.ndarray:
+    return np.asarray(x, np.float32).astype(np.float16).astype(np.float32)
