@@ -164,7 +164,13 @@ class PackedDecodeState:
 
     @torch.no_grad()
     def decode(self, query, *, sink_key=None, sink_value=None, residual_key=None, residual_value=None,
-               scale=None):
+               scale=None, output=None):
+        """Attention of `query` over sink, packed blocks and tail.
+
+        `output` (an extension of the reference signature) may be a
+        contiguous [1, Hq, 1, 128] tensor of the query dtype or float32 to
+        receive the result, e.g. to read the unrounded fp32 value.
+        """
         if query.ndim != 4 or query.shape[0] != 1 or query.shape[1] < 1 or tuple(query.shape[-2:]) != (1, 128):
             raise ValueError("query must have shape [1, query_heads, 1, 128]")
         if query.device.type != "cuda" or query.dtype not in (torch.float16, torch.bfloat16, torch.float32):
@@ -211,7 +217,11 @@ class PackedDecodeState:
             if self._workspace is None or tuple(self._workspace.shape) != shape or self._workspace.device != query.device:
                 self._workspace = torch.empty(shape, dtype=torch.float32, device=query.device)
             workspace = self._workspace
-        output = torch.empty_like(query, memory_format=torch.contiguous_format)
+        if output is None:
+            output = torch.empty_like(query, memory_format=torch.contiguous_format)
+        elif (tuple(output.shape) != tuple(query.shape) or not output.is_contiguous()
+              or output.dtype not in (query.dtype, torch.float32) or output.device != query.device):
+            raise ValueError("output must be a contiguous query-shaped tensor of the query dtype or float32")
         if self._tables is None:
             # zero-element placeholders keep nbytes accounting identical to the reference
             self._tables = torch.empty((0, 6), dtype=torch.int64, device=query.device)

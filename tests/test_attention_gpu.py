@@ -1,0 +1,186 @@
+"""GPU parity of fused packed decode attention against the fp64
+dequantize-then-attend oracle (qwen_fused.py:21-30 semantics).
+
+Bar: max |out_fp32 - oracle| <= 2e-3, with keys and
+values decoded and rounded to the query dtype exactly as the reference does.
+"""
+import numpy as np
+import pytest
+import torch
+
+from kvcase import make_case, oracle_decode, to_np
+
+pytestmark = pytest.mark.gpu
+
+ATOL = 2e-3
+
+
+def _decode_f32(state, case, scale=None):
+    out = torch.empty(case.query.shape, dtype=torch.float32, device="cuda")
+    state.decode(case.query, scale=scale, output=out, **case.kwargs())
+    return to_np(out)[0, :, 0]
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+@pytest.mark.parametrize("fraction", [0.0, 0.125, 0.5])
+@pytest.mark.parametrize("policy", ["neighbors", "min_error"])
+def test_k4_values_with_sink_and_unsealed_tail(dtype, fraction, policy):
+    # restates test_triton_attention.py:23-46 (K4-coded values, 281-token tail)
+    from inquant.triton_attention import PackedDecodeState
+    case = make_case(921, n_blocks=3, tail=281, dtype=dtype, fraction=fraction, policy=policy, value_bits=0)
+    state = PackedDecodeState(case.key_blocks, case.value_blocks)
+    descriptor_bytes = state.nbytes
+    got = _decode_f32(state, case)
+    np.testing.assert_allclose(got, case.expected(), atol=ATOL, rtol=0)
+    typed = state.decode(case.query, **case.kwargs())
+    assert typed.shape == case.query.shape and typed.dtype == dtype and torch.isfinite(typed).all()
+    # the typed result is the fp32 result rounded once
+    expect_typed = torch.from_numpy(got).to("cuda").to(dtype).view_as(typed)
+    assert torch.equal(typed, expect_typed)
+    assert state.nbytes == descriptor_bytes + state._workspace.numel() * 4
+    pointer = state._workspace.data_ptr()
+    state.decode(case.query, **case.kwargs())
+    assert state._workspace.data_ptr() == pointer
+
+
+@pytest.mark.parametrize("bits,group", [(2, 32), (2, 64), (2, 128), (4, 64)])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_k4v2_gqa_matches_oracle(bits, group, dtype):
+    from inquant.triton_attention import PackedDecodeState
+    case = make_case(125, n_blocks=2, sink=0, tail=267, dtype=dtype, value_bits=bits, group=group)
+    state = PackedDecodeState(case.key_blocks, case.value_blocks)
+    np.testing.assert_allclose(_decode_f32(state, case), case.expected(), atol=ATOL, rtol=0)
+    assert state._value_map.numel() == 0
+
+
+def test_qwen_shape_8k_context_cfg1():
+    # 28 query heads over 4 KV heads, 32 packed blocks, 4 sink, 128 tail
+    from inquant.triton_attention import PackedDecodeState
+    case = make_case(1, n_blocks=32, sink=4, tail=128)
+    state = PackedDecodeState(case.key_blocks, case.value_blocks)
+    got = _decode_f32(state, case)
+    err = np.abs(got - case.expected()).max()
+    assert err <= ATOL, err
+
+
+def test_mistral_shape_dense_outliers_cfg3():
+    # BASELINE config 3 shape: G = 4 over 8 KV heads, 8% outliers in 3-wide runs
+    from inquant.triton_attention import PackedDecodeState
+    case = make_case(3, H=8, G=4, n_blocks=8, groups=(3, 3, 3, 1))
+    state = PackedDecodeState(case.key_blocks, case.value_blocks)
+    np.testing.assert_allclose(_decode_f32(state, case), case.expected(), atol=ATOL, rtol=0)
+
+
+@pytest.mark.parametrize("tokens", [1, 4, 257])
+def test_dense_only_before_any_block_is_sealed(tokens):
+    from inquant.triton_attention import packed_decode, PackedDecodeState
+    case = make_case(7, H=2, G=7, n_blocks=0, sink=0, tail=tokens)
+    out = packed_decode(case.query, [], [], residual_key=case.tail_k, residual_value=case.tail_v)
+    state = PackedDecodeState([], [])
+    got = _decode_f32(state, case)
+    np.testing.assert_allclose(got, case.expected(), atol=ATOL, rtol=0)
+    assert torch.equal(out, torch.from_numpy(got).to("cuda").to(out.dtype).view_as(out))
+
+
+def test_nondefault_block_length_and_no_dense_tensors():
+    from inquant.triton_attention import PackedDecodeState
+    case = make_case(41, H=1, G=3, n_blocks=1, block=41, sink=0, tail=0, dtype=torch.float16, value_bits=0)
+    state = PackedDecodeState(case.key_blocks, case.value_blocks)
+    np.testing.assert_allclose(_decode_f32(state, case), case.expected(), atol=ATOL, rtol=0)
+
+
+def test_extreme_softmax_and_zero_blocks_remain_finite():
+    from inquant.codec import quantize
+    from inquant.triton_attention import packed_decode
+    key = torch.zeros((1, 1, 256, 128), device="cuda", dtype=torch.bfloat16)
+    key[..., 0, :] = 30
+    value = torch.randn(key.shape, device="cuda", dtype=torch.bfloat16)
+    query = torch.full((1, 7, 1, 128), 20, device="cuda", dtype=torch.bfloat16)
+    keys, values = [quantize(key)], [quantize(value)]
+    out = packed_decode(query, keys, values)
+    assert torch.isfinite(out).all()
+    expected = oracle_decode(query, keys, values)
+    np.testing.assert_allclose(to_np(out)[0, :, 0], expected, atol=ATOL + 2 ** -8 * np.abs(expected).max(), rtol=0)
+
+
+def test_growing_tail_with_runtime_strides():
+    # test_triton_attention.py:79-97: compact tails change head stride every step
+    from inquant.triton_attention import PackedDecodeState
+    case = make_case(79, n_blocks=1, sink=0, tail=192)
+    state = PackedDecodeState(case.key_blocks, case.value_blocks)
+    for length in (129, 150, 192):
+        tk = case.tail_k[:, :, :length].contiguous()
+        tv = case.tail_v[:, :, :length].contiguous()
+        out = torch.empty(case.query.shape, dtype=torch.float32, device="cuda")
+        state.decode(case.query, residual_key=tk, residual_value=tv, output=out)
+        exp = oracle_decode(case.query, case.key_blocks, case.value_blocks, tail_k=tk, tail_v=tv)
+        np.testing.assert_allclose(to_np(out)[0, :, 0], exp, atol=ATOL, rtol=0)
+
+
+def test_growing_state_matches_fresh_state_and_rejects_replacement():
+    # test_incremental_state.py:8-34
+    from inquant.codec import CodecConfig, quantize
+    from inquant.value_codec import quantize_values
+    from inquant.triton_attention import PackedDecodeState
+    torch.manual_seed(831)
+    keys, values = [], []
+    state = PackedDecodeState([], [])
+    q = torch.randn(1, 8, 1, 128, device="cuda", dtype=torch.bfloat16)
+    for i in range(11):
+        k = torch.randn(1, 2, 32, 128, device="cuda", dtype=torch.bfloat16)
+        k[..., 127] *= 20
+        keys.append(quantize(k, CodecConfig(donor_policy="min_error")))
+        values.append(quantize_values(torch.randn_like(k)))
+        state.extend(keys, values)
+        fresh = PackedDecodeState(keys, values)
+        assert torch.equal(state.decode(q), fresh.decode(q))
+        assert state._key_map.dtype == torch.int8
+        assert torch.equal(state._key_map[:i + 1], fresh._key_map[:i + 1])
+        assert state.nbytes == sum(x.untyped_storage().nbytes() for x in
+                                   (state._tables, state._key_map, state._value_map, state._workspace)
+                                   if x is not None)
+    with pytest.raises(ValueError, match="append-only"):
+        state.extend(keys[:-1], values[:-1])
+    with pytest.raises(ValueError, match="append-only"):
+        state.extend(list(reversed(keys)), values)
+    state.extend(keys, values)
+    assert torch.equal(state.decode(q), fresh.decode(q))
+
+
+def test_role_maps_and_tables_match_oracle():
+    from oracle import oracle
+    from inquant.triton_attention import PackedDecodeState
+    case = make_case(5, n_blocks=3, value_bits=0)
+    state = PackedDecodeState(case.key_blocks[:1], case.value_blocks[:1])
+    state.extend(case.key_blocks, case.value_blocks)
+    for i, (k, v) in enumerate(zip(case.key_blocks, case.value_blocks)):
+        for blk, table in ((k, state._key_map), (v, state._value_map)):
+            roles = oracle.role_map(blk.salient_channels[0].long().cpu().numpy(),
+                                    blk.donor_channels[0].long().cpu().numpy())
+            np.testing.assert_array_equal(table[i].cpu().numpy().astype(np.int16), roles)
+        row = state._tables[i].cpu().tolist()
+        assert row == [k.payload.data_ptr(), k.scales.data_ptr(), k.padding.data_ptr(), v.payload.data_ptr(),
+                       v.scales.data_ptr(), v.padding.data_ptr()]
+
+
+def test_workspace_pool_is_shared_once_and_rejects_other_stream():
+    from inquant.triton_attention import PackedDecodeState, SharedDecodeWorkspace
+    pool = SharedDecodeWorkspace()
+    q = torch.randn(1, 28, 1, 128, device="cuda", dtype=torch.bfloat16)
+    k, v = [torch.randn(1, 4, 19, 128, device="cuda", dtype=torch.bfloat16) for _ in range(2)]
+    states = [PackedDecodeState([], [], workspace_pool=pool) for _ in range(3)]
+    for i, state in enumerate(states):
+        out = torch.empty(q.shape, dtype=torch.float32, device="cuda")
+        state.decode(q, residual_key=k, residual_value=v + i, output=out)
+        exp = oracle_decode(q, [], [], tail_k=k, tail_v=v + i)
+        np.testing.assert_allclose(to_np(out)[0, :, 0], exp, atol=ATOL, rtol=0)
+        assert state._workspace is None and state.nbytes == 0
+    assert pool.nbytes == 28 * 130 * 4
+    first = pool.tensor.data_ptr()
+    states[0].decode(q, residual_key=k, residual_value=v)
+    assert pool.tensor.data_ptr() == first
+    torch.cuda.synchronize()
+    with torch.cuda.stream(torch.cuda.Stream()):
+        with pytest.raises(RuntimeError, match="one CUDA stream"):
+            states[0].decode(q, residual_key=k, residual_value=v)
+    torch.cuda.synchronize()

@@ -1,0 +1,130 @@
+"""CPU checks of the drop-in boundary: the C-ABI library loads and exports what
+include/inquant_hip.h declares, and host-side validation mirrors the reference."""
+import ctypes
+import math
+import os
+import re
+
+import pytest
+import torch
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def _declared_functions():
+    with open(os.path.join(ROOT, "include", "inquant_hip.h")) as f:
+        text = f.read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(iq_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_symbol():
+    from inquant import _native
+    lib = _native.lib()
+    declared = _declared_functions()
+    assert declared, "no declarations parsed"
+    for name in declared:
+        assert hasattr(lib, name), name
+    assert set(declared) == set(_native.exported_symbols())
+    assert lib.iq_abi_version() == 1
+
+
+def test_invalid_arguments_return_errors_without_a_gpu():
+    from inquant import _native
+    lib = _native.lib()
+    # argument checks run on the host before any launch
+    assert lib.iq_reuse_map(None, None, 4, 2000, 4, None, None, None) == -1
+    assert b"D=2000" in lib.iq_last_error()
+    assert lib.iq_v_dequantize(None, None, None, 1, 128, 3, 64, None, 0, None) == -1
+    assert lib.iq_decode_workspace_floats(28, 128, 4, 128) == 28 * 130 * 130
+
+
+@pytest.mark.parametrize("bad", [-0.1, 0.51, float("nan")])
+def test_invalid_fraction_rejected(bad):
+    from inquant.codec import CodecConfig
+    with pytest.raises(ValueError, match="salient_fraction"):
+        CodecConfig(salient_fraction=bad)
+
+
+@pytest.mark.parametrize("bad", [0, -1, 1.5, True])
+def test_invalid_sample_stride_rejected(bad):
+    from inquant.codec import CodecConfig
+    with pytest.raises(ValueError, match="sample_stride"):
+        CodecConfig(sample_stride=bad)
+
+
+def test_config_rejects_unknown_policy_and_backend():
+    from inquant.codec import CodecConfig
+    with pytest.raises(ValueError, match="donor_policy"):
+        CodecConfig(donor_policy="nearest")
+    with pytest.raises(ValueError, match="donor_backend"):
+        CodecConfig(donor_backend="cuda")
+
+
+def test_quantize_validation_precedes_device_dispatch():
+    from inquant.codec import quantize
+    with pytest.raises(ValueError, match="even"):
+        quantize(torch.ones(1, 1, 8, 7))
+    with pytest.raises(ValueError, match="nonempty"):
+        quantize(torch.ones(1, 1, 0, 8))
+    with pytest.raises(ValueError, match="floating"):
+        quantize(torch.ones(1, 1, 8, 8, dtype=torch.int32))
+
+
+def test_cpu_tensors_are_rejected_not_served_by_a_fallback():
+    from inquant.codec import quantize
+    from inquant.value_codec import quantize_values
+    with pytest.raises(RuntimeError, match="ROCm GPU"):
+        quantize(torch.ones(1, 1, 8, 8))
+    with pytest.raises(RuntimeError, match="ROCm GPU"):
+        quantize_values(torch.ones(1, 1, 8, 128))
+
+
+def test_value_codec_argument_validation():
+    from inquant.value_codec import quantize_values
+    with pytest.raises(ValueError, match="bits"):
+        quantize_values(torch.zeros(1, 1, 2, 128), bits=3)
+    with pytest.raises(ValueError, match="group"):
+        quantize_values(torch.zeros(1, 1, 2, 128), group_size=16)
+    with pytest.raises(ValueError):
+        quantize_values(torch.zeros(1, 1, 2, 48))
+
+
+def test_cache_config_validation():
+    from inquant.cache import CacheConfig
+    with pytest.raises(ValueError, match="block_size"):
+        CacheConfig(block_size=0)
+    with pytest.raises(ValueError, match="integer"):
+        CacheConfig(residual_length=1.5)
+    with pytest.raises(ValueError, match="value_bits"):
+        CacheConfig(value_bits=3)
+    with pytest.raises(ValueError, match="value_group_size"):
+        CacheConfig(value_group_size=16)
+    with pytest.raises(ValueError, match="boolean"):
+        CacheConfig(shared_workspace=1)
+
+
+def test_cache_update_validation_runs_on_host():
+    from inquant.cache import CacheConfig, InQuantCache
+    cache = InQuantCache(CacheConfig())
+    with pytest.raises(NotImplementedError):
+        cache.update(torch.zeros(2, 1, 3, 8), torch.zeros(2, 1, 3, 8), 0)
+    with pytest.raises(ValueError, match="even"):
+        cache.update(torch.zeros(1, 1, 3, 7), torch.zeros(1, 1, 3, 7), 0)
+    with pytest.raises(ValueError, match="layer_idx"):
+        cache.update(torch.zeros(1, 1, 3, 8), torch.zeros(1, 1, 3, 8), -1)
+    with pytest.raises(ValueError, match="cache_position"):
+        cache.update(torch.zeros(1, 1, 3, 8), torch.zeros(1, 1, 3, 8), 0, {"cache_position": torch.arange(2)})
+    assert cache.get_seq_length() == 0 and cache.nbytes == 0
+
+
+def test_decode_state_validation_without_gpu():
+    from inquant.triton_attention import PackedDecodeState
+    state = PackedDecodeState([], [])
+    with pytest.raises(ValueError, match="query must have shape"):
+        state.decode(torch.zeros(1, 4, 2, 128))
+    with pytest.raises(ValueError, match="CUDA"):
+        state.decode(torch.zeros(1, 4, 1, 128))
+    with pytest.raises(ValueError, match="counts must match"):
+        PackedDecodeState([1], [])
+    assert math.isclose(128 ** -0.5, 0.08838834764831845)

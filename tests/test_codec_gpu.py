@@ -1,0 +1,182 @@
+"""GPU parity of the HIP codec kernels: bit-exact against the reference's
+golden vectors and the pinned CPU oracle (tests/test_oracle.py)."""
+import hashlib
+import json
+import os
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle
+from recipes import K4_CASES, build_input
+import synth
+
+pytestmark = pytest.mark.gpu
+
+GOLDEN_DIR = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+TORCH_DTYPES = {"bfloat16": torch.bfloat16, "float16": torch.float16, "float32": torch.float32}
+
+
+def _dev(x: np.ndarray, dtype=torch.float32):
+    t = torch.from_numpy(np.ascontiguousarray(x)).to("cuda")
+    return t.to(dtype)
+
+
+def _np(t):
+    return t.detach().cpu().numpy()
+
+
+def _same_bits(a, b, what=""):
+    a, b = np.ascontiguousarray(a), np.ascontiguousarray(b)
+    if a.dtype == np.float32:
+        a, b = a.view(np.uint32), b.astype(np.float32).view(np.uint32)
+    np.testing.assert_array_equal(a, b, err_msg=what)
+
+
+@pytest.fixture(scope="module")
+def golden():
+    with open(os.path.join(GOLDEN_DIR, "k4_quantize.json")) as f:
+        meta = json.load(f)["cases"]
+    return meta, np.load(os.path.join(GOLDEN_DIR, "k4_quantize.npz"))
+
+
+@pytest.mark.parametrize("name", sorted(K4_CASES))
+def test_k4_quantize_matches_reference_golden(golden, name):
+    from inquant.codec import CodecConfig, quantize
+    meta, arrays = golden
+    recipe, cfg = K4_CASES[name]
+    x = build_input(recipe)
+    dtype = TORCH_DTYPES.get(recipe.get("dtype", "float32"), torch.float32)
+    packed = quantize(_dev(x, dtype), CodecConfig(**cfg))
+    assert hashlib.sha256(_np(packed.payload).tobytes()).hexdigest() == meta[name]["payload_sha256"]
+    assert str(packed.salient_channels.dtype).replace("torch.", "") == meta[name]["descriptor_dtype"]
+    for field in ("scales", "salient_channels", "donor_channels", "padding"):
+        _same_bits(_np(packed.tensors[field]).astype(arrays[f"{name}/{field}"].dtype), arrays[f"{name}/{field}"],
+                   field)
+    assert packed.shape == tuple(x.shape) and packed.original_dtype == dtype
+
+
+@pytest.mark.parametrize("policy", ["neighbors", "min_error"])
+def test_k4_blocked_strided_view_matches_golden(golden, policy):
+    # the cache encodes a strided [nb, H, B, D] view of the prefill in place
+    from inquant.codec import CodecConfig, quantize
+    meta, arrays = golden
+    name = f"cfg0_blocks_{policy}"
+    recipe, cfg = K4_CASES[name]
+    flat = build_input({k: v for k, v in recipe.items() if k != "block"})
+    t = _dev(flat, torch.bfloat16)
+    view = t[0].reshape(4, 16, 256, 128).permute(1, 0, 2, 3)
+    assert not view.is_contiguous()
+    packed = quantize(view, CodecConfig(**cfg))
+    assert hashlib.sha256(_np(packed.payload).tobytes()).hexdigest() == meta[name]["payload_sha256"]
+    _same_bits(_np(packed.padding), arrays[f"{name}/padding"])
+
+
+@pytest.mark.parametrize("D,T,stride,policy,frac,dtype", [
+    (128, 256, 8, "min_error", 0.125, torch.bfloat16),
+    (128, 200, 8, "neighbors", 0.125, torch.float16),
+    (64, 77, 5, "min_error", 0.25, torch.float32),
+    (130, 33, 2, "neighbors", 0.5, torch.float32),
+    (258, 9, 3, "min_error", 0.5, torch.bfloat16),
+    (512, 16, 1, "neighbors", 0.125, torch.float32),
+    (16, 4100, 1, "min_error", 0.25, torch.float32),
+    (8, 16, 8, "neighbors", 0.125, torch.float64),
+])
+def test_k4_quantize_matches_oracle(D, T, stride, policy, frac, dtype):
+    from inquant.codec import CodecConfig, quantize
+    x = synth.normal(D * 1000 + T, (2, 3, T, D)) * np.exp(synth.normal(7, (2, 3, T, 1)))
+    x[..., 1:3] *= 25
+    xt = _dev(x, torch.float64).to(dtype)
+    ref = oracle.k4_quantize(_np(xt.float()), stride, frac, policy)
+    got = quantize(xt, CodecConfig(sample_stride=stride, salient_fraction=frac, donor_policy=policy))
+    for field in ("payload", "scales", "salient_channels", "donor_channels", "padding"):
+        _same_bits(_np(got.tensors[field]).astype(ref[field].dtype), ref[field], field)
+
+
+def test_k4_rejects_nonfinite_values():
+    from inquant.codec import quantize
+    for bad in (float("nan"), float("inf")):
+        with pytest.raises(ValueError, match="finite"):
+            quantize(torch.full((1, 1, 8, 8), bad, device="cuda"))
+
+
+@pytest.mark.parametrize("count", [0, 1, 8, 16, 32, 64])
+@pytest.mark.parametrize("policy", ["neighbors", "min_error"])
+def test_reuse_map_with_ties_and_adjacent_outliers(count, policy):
+    # restates test_triton_selection.py:9-22 with the oracle as the expectation
+    from inquant.codec import _reuse_map
+    from inquant.triton_selection import reuse_map
+    gen = np.random.default_rng(112)
+    score = gen.random((3, 4, 128)).astype(np.float32)
+    score[0] = 0
+    score[1, :, 30:70] = 5
+    score[2, :, 127] = 9
+    error = gen.integers(0, 4, score.shape).astype(np.float32) if policy == "min_error" else None
+    ref = oracle.reuse_map(score, count, error)
+    for fn in (reuse_map, _reuse_map):
+        got = fn(_dev(score), count, None if error is None else _dev(error))
+        for a, b in zip(got, ref):
+            assert a.dtype == torch.int64
+            np.testing.assert_array_equal(_np(a), b)
+
+
+@pytest.mark.parametrize("bits,group", [(2, 32), (2, 64), (2, 128), (4, 64), (4, 32)])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_value_codec_matches_oracle(bits, group, dtype):
+    from inquant.value_codec import quantize_values
+    x = synth.kv_like(11 + bits, 4, 300, groups=(2, 2, 1))
+    xt = _dev(x).to(dtype)
+    ref = oracle.v_quantize(_np(xt.float()), bits, group)
+    got = quantize_values(xt, bits, group)
+    np.testing.assert_array_equal(_np(got.payload), ref["payload"])
+    np.testing.assert_array_equal(_np(got.scales).view(np.uint16), ref["scales"].view(np.uint16))
+    np.testing.assert_array_equal(_np(got.offsets).view(np.uint16), ref["offsets"].view(np.uint16))
+    for out in ("float32", "bfloat16", "float16"):
+        dec = got.dequantize(TORCH_DTYPES[out])
+        _same_bits(_np(dec.float()), oracle.v_dequantize(ref, bits, group, out), out)
+
+
+def test_value_codec_known_answers_and_rejections():
+    from inquant.value_codec import quantize_values
+    for bits in (2, 4):
+        codes = torch.arange(1 << bits).repeat(128 // (1 << bits))
+        x = (codes.float() * 2 - 3).view(1, 1, 1, 128).expand(2, 3, 7, 128).cuda()
+        q = quantize_values(x, bits, 64)
+        assert q.payload[0, 0, 0, 0].item() == sum(i << (bits * i) for i in range(8 // bits))
+        assert q.payload_nbytes == x.numel() * bits // 8
+        assert q.metadata_nbytes == x.numel() // 64 * 4
+        assert torch.equal(q.dequantize(), x)
+    for value in (float("nan"), float("inf"), 1e6):
+        with pytest.raises(ValueError, match="finite"):
+            quantize_values(torch.full((1, 1, 2, 128), value, device="cuda"))
+
+
+@pytest.mark.parametrize("frac,policy", [(0.0, "neighbors"), (0.125, "min_error"), (0.5, "neighbors")])
+def test_k4_dequantize_matches_oracle(frac, policy):
+    from inquant.codec import CodecConfig, quantize
+    x = synth.kv_like(21, 4, 96)
+    packed = quantize(_dev(x, torch.bfloat16), CodecConfig(salient_fraction=frac, donor_policy=policy))
+    fields = {k: _np(v) for k, v in packed.tensors.items()}
+    fields["salient_channels"] = fields["salient_channels"].astype(np.int64)
+    fields["donor_channels"] = fields["donor_channels"].astype(np.int64)
+    for out in ("float32", "bfloat16", "float16"):
+        got = packed.dequantize(TORCH_DTYPES[out])
+        assert got.dtype == TORCH_DTYPES[out]
+        _same_bits(_np(got.float()), oracle.k4_dequantize(fields, out), out)
+    assert packed.dequantize().dtype == torch.bfloat16
+
+
+def test_k4_storage_accounting():
+    # test_codec.py:18-33
+    from inquant.codec import CodecConfig, quantize
+    x = torch.randn(2, 3, 41, 16, device="cuda", dtype=torch.float16)
+    packed = quantize(x, CodecConfig(salient_fraction=0.25))
+    assert packed.payload.shape == (2, 3, 41, 8) and packed.payload.dtype == torch.uint8
+    assert packed.payload_nbytes == x.numel() // 2
+    assert packed.metadata_nbytes == 2 * 3 * (16 * 4 + 4 * (1 + 1 + 4))
+    assert all(t.device == x.device and t.is_contiguous() for t in packed.tensors.values())
+    stats = packed.storage_stats()
+    assert stats["source_nbytes"] == x.numel() * 2 and stats["compression_ratio"] < 4
+    big = quantize(torch.randn(1, 1, 3, 258, device="cuda"), CodecConfig(salient_fraction=0.5))
+    assert big.donor_channels.dtype == torch.int32 and big.donor_channels.unique().numel() == 129
