@@ -258,7 +258,7 @@ def main():
         "decode_tokens_per_s": round(1e3 / ms, 2),
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
-                     "kernel": "decode_partials + decode_reduce (one decode call per layer)",
+                     "kernel": "decode_fast (matrix-core decode with in-kernel partition merge; one launch per layer)",
                      "bytes_per_launch": per_layer},
         "encode_mtok_s": round(enc["encode_mtok_s"], 2),
         "encode": {k: round(v, 3) for k, v in enc.items()},

@@ -45,6 +45,11 @@ extern "C" {
 enum iq_status { IQ_OK = 0, IQ_ERR_ARG = -1, IQ_ERR_DEVICE = -2, IQ_ERR_UNSUPPORTED = -3 };
 enum iq_dtype { IQ_F32 = 0, IQ_BF16 = 1, IQ_F16 = 2, IQ_F64 = 3 };
 
+/* Columns of a decode state's pointer table: the reference's six (K payload,
+ * K scales, K padding, V payload, V scales, V offsets-or-padding,
+ * triton_attention.py:337-340) plus the K source and donor descriptors. */
+#define IQ_TABLE_COLS 8
+
 /* Library ABI version (IQ_ABI_VERSION) and last error text of this thread. */
 int iq_abi_version(void);
 const char *iq_last_error(void);
@@ -108,7 +113,7 @@ typedef struct iq_block_ptrs {
 } iq_block_ptrs;
 
 /*
- * Append `count` blocks to a decode state: writes tables[first + i] (i64 [cap, 6])
+ * Append `count` blocks to a decode state: writes tables[first + i] (i64 [cap, IQ_TABLE_COLS])
  * and the int8 role maps key_map / value_map [cap, H, 128] (value_map may be
  * NULL for V2/V4 values).  Roles: -1 normal, donor channel for a source,
  * -2 - i for donor i.  `blocks` is a HOST array; its contents travel as
@@ -121,19 +126,28 @@ int iq_decode_append(int64_t *tables, int8_t *key_map, int8_t *value_map, int64_
 /*
  * Fused single-query GQA decode over [sink | packed blocks | tail].
  *   q [Hq, 128] (row stride q_stride_h) of q_dtype (f32, bf16, f16);
- *   tables i64 [n_blocks, 6], key_map/value_map int8 [n_blocks, H, 128]
+ *   tables i64 [n_blocks, IQ_TABLE_COLS], key_map/value_map int8 [n_blocks, H, 128]
  *   (value_map used only when value_bits == 0, i.e. K4-coded V);
  *   block_tokens tokens per packed block, S salient channels per block;
  *   value_bits in {0, 2, 4}, value_group in {32, 64, 128};
  *   sink/tail K/V of q_dtype with (head, token) element strides, lengths
  *   sink_t / tail_t (pointers may be NULL when the length is 0);
  *   workspace f32 with at least iq_decode_workspace_floats(...) elements;
+ *   merge_counters (may be NULL) with iq_decode_merge_counter_ints(...) ints;
  *   out [Hq, 128] contiguous of out_dtype.
  * Keys/values are decoded and rounded to q_dtype exactly as the reference's
  * dequantize-then-attend path does; logits, softmax and P.V accumulate in
  * fp32.  Replaces PackedDecodeState.decode (triton_attention.py:377-448).
  */
 int64_t iq_decode_workspace_floats(int64_t Hq, int64_t n_blocks, int64_t sink_t, int64_t tail_t);
+
+/*
+ * int32 merge counters needed by iq_decode_attention to merge partitions
+ * in-kernel (last-arriving workgroups).  The caller allocates them zeroed
+ * once; every launch leaves them zero again.  Calls that share counters must
+ * be ordered on one stream.  Without counters a second kernel merges.
+ */
+int64_t iq_decode_merge_counter_ints(int64_t H, int64_t n_blocks, int64_t sink_t, int64_t tail_t);
 
 int iq_decode_attention(const void *q, int q_dtype, int64_t q_stride_h, int64_t Hq,
                         const int64_t *tables, const int8_t *key_map, const int8_t *value_map,
@@ -144,6 +158,7 @@ int iq_decode_attention(const void *q, int q_dtype, int64_t q_stride_h, int64_t 
                         const void *tail_k, const void *tail_v, int64_t tail_k_sh, int64_t tail_k_st,
                         int64_t tail_v_sh, int64_t tail_v_st, int64_t tail_t,
                         float scale, float *workspace, int64_t workspace_floats,
+                        int *merge_counters, int64_t merge_counter_ints,
                         void *out, int out_dtype, void *stream);
 
 #ifdef __cplusplus

@@ -86,7 +86,7 @@ __global__ __launch_bounds__(DA_THREADS) void decode_partials_generic(DecodeArgs
     const void *dk = nullptr, *dv = nullptr;
     int64_t dk_sh = 0, dk_st = 0, dv_sh = 0, dv_st = 0, start = 0, length = 0;
     if (packed) {
-        const int64_t *row = a.tables + p * 6;
+        const int64_t *row = a.tables + p * IQ_TABLE_COLS;
         kpay = (const uint8_t *)row[0] + (int64_t)h * a.BT * (D / 2);
         const float *ksc = (const float *)row[1] + h * D;
         const float *kpad = (const float *)row[2] + h * a.S;
@@ -219,22 +219,85 @@ __global__ __launch_bounds__(DA_THREADS) void decode_partials_generic(DecodeArgs
     }
 }
 
-// Log-sum-exp merge of the partition partials, one workgroup per query head.
-__global__ __launch_bounds__(D) void decode_reduce(const float *ws, int64_t P, void *out, int odt)
+// Log-sum-exp merge of the partition partials (_reduce_partials, triton_attention.py:168-181).
+// grid (Hq, D / 32): each workgroup merges 32 output channels of one query
+// head; its 256 threads split the partitions 8 ways per channel.
+constexpr int RED_THREADS = 256;
+constexpr int RED_COLS = 32;
+constexpr int RED_PARTS = RED_THREADS / RED_COLS;
+
+// Each thread merges every 8th partition of one channel: all loads of a
+// round of 16 partitions are issued before any dependent arithmetic, then the
+// 8 running (max, weighted sum, normalizer) states merge through LDS.
+constexpr int RED_BATCH = 16;
+
+__global__ __launch_bounds__(RED_THREADS) void decode_reduce(const float *ws, int64_t P, void *out, int odt)
 {
+    __shared__ float s_m[RED_THREADS], s_n[RED_THREADS], s_l[RED_THREADS];
     const int64_t hq = blockIdx.x;
-    const int d = threadIdx.x;
+    const int c0 = blockIdx.y * RED_COLS;
+    const int tid = threadIdx.x, c = tid % RED_COLS, part = tid / RED_COLS;
     const float *base = ws + hq * P * (D + 2);
-    float mx = -__uint_as_float(0x7f800000u);
-    for (int64_t p = 0; p < P; ++p) mx = fmaxf(mx, base[p * (D + 2) + D]);
-    float num = 0.0f, den = 0.0f;
-    for (int64_t p = 0; p < P; ++p) {
-        const float w = expf(base[p * (D + 2) + D] - mx);
-        num += base[p * (D + 2) + d] * w;
-        den += base[p * (D + 2) + D + 1] * w;
+    const float ninf = -__uint_as_float(0x7f800000u);
+    float m = ninf, num = 0.0f, den = 0.0f;
+    for (int64_t p0 = part; p0 < P; p0 += RED_PARTS * RED_BATCH) {
+        float mv[RED_BATCH], lv[RED_BATCH], av[RED_BATCH];
+#pragma unroll
+        for (int k = 0; k < RED_BATCH; ++k) {
+            const int64_t pp = p0 + (int64_t)RED_PARTS * k;
+            const bool ok = pp < P;
+            const float *r = base + (ok ? pp : 0) * (D + 2);
+            mv[k] = ok ? r[D] : ninf;
+            lv[k] = ok ? r[D + 1] : 0.0f;
+            av[k] = ok ? r[c0 + c] : 0.0f;
+        }
+        float mm = m;
+#pragma unroll
+        for (int k = 0; k < RED_BATCH; ++k) mm = fmaxf(mm, mv[k]);
+        if (mm == ninf) continue;
+        const float wo = m == ninf ? 0.0f : __expf(m - mm);
+        num *= wo;
+        den *= wo;
+#pragma unroll
+        for (int k = 0; k < RED_BATCH; ++k) {
+            const float w = mv[k] == ninf ? 0.0f : __expf(mv[k] - mm);
+            num = fmaf(av[k], w, num);
+            den = fmaf(lv[k], w, den);
+        }
+        m = mm;
     }
-    iq_store_as(out, hq * D + d, num / den, odt);
+    s_m[tid] = m;
+    s_n[tid] = num;
+    s_l[tid] = den;
+    __syncthreads();
+    if (tid < RED_COLS) {
+        float mm = ninf;
+        for (int k = 0; k < RED_PARTS; ++k) mm = fmaxf(mm, s_m[k * RED_COLS + tid]);
+        float nn = 0.0f, dd = 0.0f;
+        for (int k = 0; k < RED_PARTS; ++k) {
+            const float mk = s_m[k * RED_COLS + tid];
+            if (mk == ninf) continue;
+            const float w = __expf(mk - mm);
+            nn = fmaf(s_n[k * RED_COLS + tid], w, nn);
+            dd = fmaf(s_l[k * RED_COLS + tid], w, dd);
+        }
+        iq_store_as(out, hq * D + c0 + tid, nn / dd, odt);
+    }
 }
+
+}  // namespace
+
+int iq_decode_fast_launch(const void *q, int q_dtype, int64_t q_stride_h, int64_t Hq, const int64_t *tables,
+                          const int8_t *key_map, int64_t n_blocks, int64_t block_tokens, int64_t H, int64_t S,
+                          int value_bits, int value_group, const void *sink_k, const void *sink_v, int64_t sink_k_sh,
+                          int64_t sink_k_st, int64_t sink_v_sh, int64_t sink_v_st, int64_t sink_t,
+                          const void *tail_k, const void *tail_v, int64_t tail_k_sh, int64_t tail_k_st,
+                          int64_t tail_v_sh, int64_t tail_v_st, int64_t tail_t, float scale, float *workspace,
+                          int64_t P, int *counters, int64_t counter_ints, void *out, int out_dtype,
+                          int *merged, hipStream_t stream);
+int64_t iq_decode_merge_ints(int64_t H, int64_t P);
+
+namespace {
 
 int64_t partitions(int64_t n_blocks, int64_t sink_t, int64_t tail_t)
 {
@@ -248,6 +311,11 @@ extern "C" int64_t iq_decode_workspace_floats(int64_t Hq, int64_t n_blocks, int6
     return Hq * partitions(n_blocks, sink_t, tail_t) * (D + 2);
 }
 
+extern "C" int64_t iq_decode_merge_counter_ints(int64_t H, int64_t n_blocks, int64_t sink_t, int64_t tail_t)
+{
+    return iq_decode_merge_ints(H, partitions(n_blocks, sink_t, tail_t));
+}
+
 extern "C" int iq_decode_attention(const void *q, int q_dtype, int64_t q_stride_h, int64_t Hq,
                                    const int64_t *tables, const int8_t *key_map, const int8_t *value_map,
                                    int64_t n_blocks, int64_t block_tokens, int64_t H, int64_t S, int value_bits,
@@ -255,8 +323,8 @@ extern "C" int iq_decode_attention(const void *q, int q_dtype, int64_t q_stride_
                                    int64_t sink_k_st, int64_t sink_v_sh, int64_t sink_v_st, int64_t sink_t,
                                    const void *tail_k, const void *tail_v, int64_t tail_k_sh, int64_t tail_k_st,
                                    int64_t tail_v_sh, int64_t tail_v_st, int64_t tail_t, float scale,
-                                   float *workspace, int64_t workspace_floats, void *out, int out_dtype,
-                                   void *stream)
+                                   float *workspace, int64_t workspace_floats, int *merge_counters,
+                                   int64_t merge_counter_ints, void *out, int out_dtype, void *stream)
 {
     IQ_CHECK_ARG(q && out && workspace, "iq_decode_attention: null pointer");
     IQ_CHECK_ARG(q_dtype >= IQ_F32 && q_dtype <= IQ_F16, "iq_decode_attention: bad query dtype");
@@ -277,15 +345,28 @@ extern "C" int iq_decode_attention(const void *q, int q_dtype, int64_t q_stride_
     IQ_CHECK_ARG(P >= 1, "iq_decode_attention: attention requires at least one key/value token");
     IQ_CHECK_ARG(P <= 65535, "iq_decode_attention: too many partitions");
     IQ_CHECK_ARG(workspace_floats >= Hq * P * (D + 2), "iq_decode_attention: workspace too small");
-    DecodeArgs a{q, q_dtype, q_stride_h, Hq, tables, key_map, value_map, n_blocks, block_tokens, H, S,
-                 value_bits, value_group, sink_k, sink_v, sink_k_sh, sink_k_st, sink_v_sh, sink_v_st, sink_t,
-                 tail_k, tail_v, tail_k_sh, tail_k_st, tail_v_sh, tail_v_st, tail_t, scale, workspace, P,
-                 (int)G, out, out_dtype};
-    hipLaunchKernelGGL(decode_partials_generic, dim3((unsigned)H, (unsigned)P), dim3(DA_THREADS), 0,
-                       (hipStream_t)stream, a);
-    IQ_CHECK_LAUNCH("decode_partials_generic");
-    hipLaunchKernelGGL(decode_reduce, dim3((unsigned)Hq), dim3(D), 0, (hipStream_t)stream, workspace, P, out,
-                       out_dtype);
+    // Matrix-core path for bf16/f16 queries with V2/V4 values; the general
+    // kernel covers fp32 queries and K4-coded values.
+    int merged = 0;
+    const int fast = iq_decode_fast_launch(q, q_dtype, q_stride_h, Hq, tables, key_map, n_blocks, block_tokens, H,
+                                           S, value_bits, value_group, sink_k, sink_v, sink_k_sh, sink_k_st,
+                                           sink_v_sh, sink_v_st, sink_t, tail_k, tail_v, tail_k_sh, tail_k_st,
+                                           tail_v_sh, tail_v_st, tail_t, scale, workspace, P, merge_counters,
+                                           merge_counter_ints, out, out_dtype, &merged, (hipStream_t)stream);
+    if (fast == IQ_OK) {
+        IQ_CHECK_LAUNCH("decode_fast");
+        if (merged) return IQ_OK;
+    } else {
+        DecodeArgs a{q, q_dtype, q_stride_h, Hq, tables, key_map, value_map, n_blocks, block_tokens, H, S,
+                     value_bits, value_group, sink_k, sink_v, sink_k_sh, sink_k_st, sink_v_sh, sink_v_st, sink_t,
+                     tail_k, tail_v, tail_k_sh, tail_k_st, tail_v_sh, tail_v_st, tail_t, scale, workspace, P,
+                     (int)G, out, out_dtype};
+        hipLaunchKernelGGL(decode_partials_generic, dim3((unsigned)H, (unsigned)P), dim3(DA_THREADS), 0,
+                           (hipStream_t)stream, a);
+        IQ_CHECK_LAUNCH("decode_partials_generic");
+    }
+    hipLaunchKernelGGL(decode_reduce, dim3((unsigned)Hq, D / RED_COLS), dim3(RED_THREADS), 0, (hipStream_t)stream,
+                       workspace, P, out, out_dtype);
     IQ_CHECK_LAUNCH("decode_reduce");
     return IQ_OK;
 }

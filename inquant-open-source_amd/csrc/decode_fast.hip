@@ -1,0 +1,745 @@
+// Fused packed-KV decode attention on matrix cores (gfx950, bf16/f16 queries).
+//
+// Same semantics and partial format as decode_partials_generic
+// (triton_attention.py:67-165): one workgroup per (KV head, partition),
+// partitions = packed blocks then 256-token slices of sink and tail; keys and
+// values are decoded and rounded to the query dtype exactly as the
+// dequantize-then-attend path does.  Each of the 4 wavefronts owns a
+// 64-token chunk of the partition.
+//
+//   * Every global load of a workgroup (pointer-table row, then payload,
+//     scales, roles, descriptors, query rows) is issued up front; one
+//     barrier publishes the block metadata in LDS before any arithmetic.
+//   * K payload rows arrive as 16-byte loads: lane (t = l%16, q = l/16) holds
+//     channels 32q..32q+31 of token t, which is exactly the A operand of four
+//     v_mfma_f32_16x16x32 (rows = tokens, k = channels, B = Q^T).
+//   * Normal channels decode with one fma per element: the fp8 converter maps
+//     a nibble byte n to n * 2^-9 exactly, so fma(v, s * 2^9, -8 s) is the
+//     single rounding of (n - 8) * s, as the reference's fp32 multiply.
+//   * Salient and donor channels are masked out of Q; an extra
+//     v_mfma_f32_16x16x16 over the gathered 8-bit codes adds the salient
+//     terms, and a per-block constant adds q . round(padding) for donors.
+//   * Online softmax in the log2 domain; P = hi + lo (two bf16/f16 terms) so
+//     the P.V product keeps ~16 significant bits of the weights.
+//   * V half-rows decode with the same fp8 trick into a 32-row LDS tile that
+//     is read back transposed as the A operand of O^T = V^T P^T.
+#include "iq_common.h"
+
+namespace {
+
+typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8;
+typedef __attribute__((ext_vector_type(8))) _Float16 f16x8;
+typedef __attribute__((ext_vector_type(4))) short s16x4;
+typedef __attribute__((ext_vector_type(4))) _Float16 f16x4;
+typedef __attribute__((ext_vector_type(2))) __bf16 bf16x2;
+typedef __attribute__((ext_vector_type(2))) _Float16 f16x2;
+typedef __attribute__((ext_vector_type(4))) float f32x4;
+typedef __attribute__((ext_vector_type(2))) float f32x2;
+typedef __attribute__((ext_vector_type(4))) uint32_t u32x4;
+typedef __attribute__((ext_vector_type(2))) uint32_t u32x2;
+
+constexpr int D = 128;
+constexpr int WAVES = 4;
+constexpr int CHUNK = 64;              // tokens per wavefront per pass
+constexpr int VR = 136;                // dwords per staged token-pair row of decoded V (128 + 8: two passes per read)
+constexpr int KROW = 17;               // dwords per staged K row (16 + 1: conflict-free byte gathers)
+constexpr int KC_STRIDE = 68;          // float2 slots per 32-channel group of K constants (+4: no bank overlap)
+constexpr int DENSE_SPLIT = 256;
+constexpr float LN2 = 0.693147180559945309f;
+constexpr int MERGE_GROUP = 16;        // partitions merged by the last-arriving workgroup of a group
+
+struct FastArgs {
+    const uint16_t *q;
+    int64_t q_sh;
+    int G;
+    const int64_t *tables;
+    const int8_t *kmap;
+    int64_t nblk, BT, H, S;
+    int vgroup;
+    const uint16_t *sk, *sv;
+    int64_t sk_sh, sk_st, sv_sh, sv_st, sink_t;
+    const uint16_t *tk, *tv;
+    int64_t tk_sh, tk_st, tv_sh, tv_st, tail_t;
+    float c_log2;    // softmax scale * log2(e)
+    float *ws;
+    int64_t P;
+    int *cnt;        // merge counters [H][ngrp + 1] (zero between launches), or null
+    int ngrp;        // partition groups of MERGE_GROUP per KV head
+    void *out;       // final [Hq, 128] output when merged in this kernel
+    int odt;
+};
+
+template <bool F16>
+__device__ __forceinline__ uint32_t pack2(float a, float b)
+{
+    if constexpr (F16) {
+        f16x2 v = {(_Float16)a, (_Float16)b};
+        return __builtin_bit_cast(uint32_t, v);
+    } else {
+        bf16x2 v = {(__bf16)a, (__bf16)b};
+        return __builtin_bit_cast(uint32_t, v);
+    }
+}
+
+template <bool F16>
+__device__ __forceinline__ float to_f32(uint32_t h16)
+{
+    if constexpr (F16) return (float)__builtin_bit_cast(_Float16, (uint16_t)h16);
+    else return __uint_as_float(h16 << 16);
+}
+
+template <bool F16>
+__device__ __forceinline__ float round_q(float v)
+{
+    return to_f32<F16>(pack2<F16>(v, 0.0f) & 0xffffu);
+}
+
+template <bool F16>
+__device__ __forceinline__ f32x4 mma32(u32x4 a, u32x4 b, f32x4 c)
+{
+    if constexpr (F16)
+        return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c,
+                                                      0, 0, 0);
+    else
+        return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b),
+                                                       c, 0, 0, 0);
+}
+
+template <bool F16>
+__device__ __forceinline__ f32x4 mma16(u32x2 a, u32x2 b, f32x4 c)
+{
+    if constexpr (F16)
+        return __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(f16x4, a), __builtin_bit_cast(f16x4, b), c,
+                                                     0, 0, 0);
+    else
+        return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(s16x4, a), __builtin_bit_cast(s16x4, b),
+                                                        c, 0, 0, 0);
+}
+
+template <bool HI>
+__device__ __forceinline__ f32x2 fp8x2(uint32_t bytes) { return __builtin_amdgcn_cvt_pk_f32_fp8(bytes, HI); }
+
+__device__ __forceinline__ float xmax16(float v)
+{
+    v = fmaxf(v, __shfl_xor(v, 16, 64));
+    return fmaxf(v, __shfl_xor(v, 32, 64));
+}
+
+__device__ __forceinline__ float xsum16(float v)
+{
+    v += __shfl_xor(v, 16, 64);
+    return v + __shfl_xor(v, 32, 64);
+}
+
+__device__ __forceinline__ u32x4 ld16(const void *p) { return *(const u32x4 *)p; }
+
+// Partials exchanged between workgroups use agent-coherent stores and loads
+// (sc1: written through / read past the per-XCD L2), so publishing them costs
+// a wait for store completion instead of an L2 write-back fence.
+__device__ __forceinline__ void st_agent(float *p, float v)
+{
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ __forceinline__ float ld_agent(const float *p)
+{
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Returns true in the workgroup whose arrival completes `expected` arrivals.
+// Every thread's agent-coherent stores have completed before the increment.
+__device__ __forceinline__ bool arrive_last(int *counter, int expected, int *flag)
+{
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (threadIdx.x == 0)
+        *flag = __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == expected - 1;
+    __syncthreads();
+    return *flag;
+}
+
+constexpr float NEG_INF = -__builtin_inff();
+
+// Log-sum-exp merge of `count` partitions (p_first, p_first + stride, ...) of
+// the G query rows of KV head h.  Results go to the partial slot p_first, or
+// to the final output when `final_out`.  All reads finish before any write
+// (the destination slot is also a source).
+// Reduction over the 16 consecutive lanes that share one query row.
+__device__ __forceinline__ float rowmax16(float v)
+{
+#pragma unroll
+    for (int o = 1; o < 16; o <<= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+    return v;
+}
+
+__device__ __forceinline__ float rowsum16(float v)
+{
+#pragma unroll
+    for (int o = 1; o < 16; o <<= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+
+// Log-sum-exp merge of `count` partials of kv head h (partition p_first + k *
+// stride), in chunks of MERGE_GROUP.  Thread (g, k) = (tid / 16, tid % 16)
+// loads one partial's (m, l) and keeps the running max / denominator of row g
+// replicated over its 16 lanes; the chunk's weights go through LDS to the
+// threads that own output channels, whose sixteen independent loads per chunk
+// are all in flight together.  Writes the merged row to partition p_first,
+// or the normalized output when final_out.
+__device__ void merge_partials(const FastArgs &a, int h, int G, int64_t p_first, int64_t stride, int count,
+                               bool final_out)
+{
+    constexpr int ITEMS = 16 * D / 256;
+    __shared__ float s_w[16 * MERGE_GROUP];
+    __shared__ float s_alpha[16], s_den[16], s_mx[16];
+    const int tid = threadIdx.x;
+    const int mg = tid >> 4, mk = tid & 15;
+    const int64_t pstride = stride * (D + 2);
+    float mx = NEG_INF, den = 0.0f;
+    float num[ITEMS];
+#pragma unroll
+    for (int it = 0; it < ITEMS; ++it) num[it] = 0.0f;
+
+    for (int k0 = 0; k0 < count; k0 += MERGE_GROUP) {
+        const int n = min(MERGE_GROUP, count - k0);
+        float m = NEG_INF, l = 0.0f;
+        if (mg < G && mk < n) {
+            const float *r = a.ws + ((int64_t)(h * G + mg) * a.P + p_first) * (D + 2) + (k0 + mk) * pstride;
+            m = ld_agent(r + D);
+            l = ld_agent(r + D + 1);
+        }
+        const float nm = fmaxf(mx, rowmax16(m));
+        const float alpha = mx == nm ? 1.0f : __expf(mx - nm);
+        const float w = m == NEG_INF ? 0.0f : __expf(m - nm);
+        den = fmaf(den, alpha, rowsum16(w * l));
+        mx = nm;
+        s_w[tid] = w;
+        if (mk == 0) s_alpha[mg] = alpha;
+        __syncthreads();
+#pragma unroll
+        for (int it = 0; it < ITEMS; ++it) {
+            const int i = tid + 256 * it;
+            if (i >= G * D) continue;
+            const int g = i >> 7, c = i & (D - 1);
+            const float *r = a.ws + ((int64_t)(h * G + g) * a.P + p_first) * (D + 2) + k0 * pstride + c;
+            float v[MERGE_GROUP];
+#pragma unroll
+            for (int k = 0; k < MERGE_GROUP; ++k) v[k] = ld_agent(r + min(k, n - 1) * pstride);
+            float acc = num[it] * s_alpha[g];
+#pragma unroll
+            for (int k = 0; k < MERGE_GROUP; ++k) acc = fmaf(v[k], s_w[g * MERGE_GROUP + k], acc);
+            num[it] = acc;
+        }
+        __syncthreads();
+    }
+    if (mk == 0 && mg < G) {
+        s_den[mg] = den;
+        s_mx[mg] = mx;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int it = 0; it < ITEMS; ++it) {
+        const int i = tid + 256 * it;
+        if (i >= G * D) continue;
+        const int g = i >> 7, c = i & (D - 1);
+        if (final_out) {
+            iq_store_as(a.out, (int64_t)(h * G + g) * D + c, num[it] / s_den[g], a.odt);
+        } else {
+            float *row = a.ws + ((int64_t)(h * G + g) * a.P + p_first) * (D + 2);
+            st_agent(row + c, num[it]);
+            if (c == 0) {
+                st_agent(row + D, s_mx[g]);
+                st_agent(row + D + 1, s_den[g]);
+            }
+        }
+    }
+}
+
+template <bool F16, int VBITS>
+__global__ __launch_bounds__(256, 3) void decode_fast(FastArgs a)
+{
+    constexpr int VROW = D * VBITS / 8;          // V payload bytes per token
+    constexpr int VQ = VROW / 4;                 // bytes per 32-channel quarter row
+    constexpr int VQW = VQ / 4;                  // dwords per quarter row
+
+    // per wavefront: staged decoded V as [token pair][channel] dwords (two
+    // tokens of one channel per dword); also K staging and the final combine
+    __shared__ __attribute__((aligned(16))) uint32_t s_v[WAVES][16 * VR];
+    __shared__ __attribute__((aligned(16))) uint16_t s_q[16 * D];     // query rows (dtype bits), zero beyond G
+    __shared__ __attribute__((aligned(16))) uint16_t s_qm[16 * D];    // query rows masked at salient/donor channels
+    __shared__ __attribute__((aligned(16))) f32x2 s_kc[4 * KC_STRIDE]; // per channel (s * 2^9, -8 s)
+    __shared__ __attribute__((aligned(16))) int8_t s_role[D];
+    __shared__ __attribute__((aligned(16))) uint32_t s_sal[64];       // src | don << 8
+    __shared__ __attribute__((aligned(16))) uint32_t s_salw[64];      // gather offsets: src byte, shift, don byte, shift
+    __shared__ __attribute__((aligned(16))) f32x2 s_salf[64];         // (s_src, -128 s_src)
+    __shared__ __attribute__((aligned(16))) uint16_t s_qsal[16 * 64]; // Q[g][src_k], zero beyond S
+    __shared__ float s_dpad[64];                                      // padding of donor k, rounded to the query dtype
+    __shared__ float s_wm[WAVES][16], s_wl[WAVES][16];
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int gl = lane & 15, ql = lane >> 4;     // MFMA column (query row / channel) and k-slot group
+    const int pl = lane >> 2, qq = lane & 3;      // V writer: token pair and 32-channel quarter
+    const int h = blockIdx.x;
+    const int64_t p = blockIdx.y;
+    const int G = a.G;
+    const float unit = fp8x2<false>(1u).x;        // fp8 byte 1 == 2^-9 (exact power of two)
+    const float inv_unit = 1.0f / unit;
+    const int ngroups = D / a.vgroup;
+
+    // ---------------- geometry (wave-uniform) and every global load up front
+    const bool packed = p < a.nblk;
+    const uint8_t *kpay = nullptr, *vpay = nullptr;
+    const uint16_t *vsc = nullptr, *voff = nullptr;
+    const uint16_t *dk = nullptr, *dv = nullptr;
+    int dk_st = 0, dv_st = 0, start = 0, stop = 0;
+    const int S = packed ? (int)a.S : 0;
+    const int sal_groups = (S + 15) / 16;
+    if (packed) {
+        const int64_t *row = a.tables + p * IQ_TABLE_COLS;
+        kpay = (const uint8_t *)row[0] + (int64_t)h * a.BT * (D / 2);
+        vpay = (const uint8_t *)row[3] + (int64_t)h * a.BT * VROW;
+        vsc = (const uint16_t *)row[4] + (int64_t)h * a.BT * ngroups;
+        voff = (const uint16_t *)row[5] + (int64_t)h * a.BT * ngroups;
+        stop = (int)a.BT;
+        if (tid < D) {
+            const float s = ((const float *)row[1])[h * D + tid];
+            s_kc[(tid >> 5) * KC_STRIDE + (tid & 31)] = f32x2{s * inv_unit, -8.0f * s};
+            s_role[tid] = a.kmap[(p * a.H + h) * D + tid];
+        }
+        if (tid < S) {
+            const uint32_t src = ((const uint8_t *)row[6])[h * S + tid];
+            const uint32_t don = ((const uint8_t *)row[7])[h * S + tid];
+            s_sal[tid] = src | (don << 8);
+            s_dpad[tid] = round_q<F16>(((const float *)row[2])[h * S + tid]);
+        }
+    } else {
+        const int64_t dp = p - a.nblk;
+        const int64_t sink_parts = (a.sink_t + DENSE_SPLIT - 1) / DENSE_SPLIT;
+        int64_t length;
+        if (dp < sink_parts) {
+            dk = a.sk + h * a.sk_sh; dv = a.sv + h * a.sv_sh; dk_st = (int)a.sk_st; dv_st = (int)a.sv_st;
+            start = (int)(dp * DENSE_SPLIT);
+            length = a.sink_t;
+        } else {
+            dk = a.tk + h * a.tk_sh; dv = a.tv + h * a.tv_sh; dk_st = (int)a.tk_st; dv_st = (int)a.tv_st;
+            start = (int)((dp - sink_parts) * DENSE_SPLIT);
+            length = a.tail_t;
+        }
+        stop = (int)(start + DENSE_SPLIT < length ? start + DENSE_SPLIT : length);
+    }
+    const int qg = tid >> 4, qc = (tid & 15) * 8;  // this thread's 8 query elements
+    const u32x4 qraw = qg < G ? ld16(a.q + (int64_t)(h * G + qg) * a.q_sh + qc) : u32x4{0u, 0u, 0u, 0u};
+    *(u32x4 *)(s_q + qg * D + qc) = qraw;
+
+    // first chunk of this wavefront: K rows (lane t = gl, channels 32 ql..), V quarter rows
+    int base = start + CHUNK * wave;
+    u32x4 kw[4];
+    uint32_t vw[2][2][VQW];                        // [half chunk][token of the pair][dword]
+    uint16_t vp[2][2][2];                          // [half chunk][token of the pair][scale, offset]
+#define IQ_LOAD_CHUNK(b_)                                                                             \
+    do {                                                                                              \
+        const int b0 = (b_);                                                                          \
+        _Pragma("unroll") for (int j = 0; j < 4; ++j) {                                               \
+            const int t = b0 + 16 * j + gl;                                                           \
+            kw[j] = t < stop ? ld16(kpay + t * (D / 2) + 16 * ql) : u32x4{0u, 0u, 0u, 0u};            \
+        }                                                                                             \
+        const int gi = (32 * qq) / a.vgroup;                                                          \
+        _Pragma("unroll") for (int m = 0; m < 2; ++m) {                                               \
+            _Pragma("unroll") for (int u = 0; u < 2; ++u) {                                           \
+                const int t = b0 + 32 * m + 2 * pl + u;                                               \
+                const bool ok = t < stop;                                                             \
+                const uint8_t *src = vpay + (int64_t)t * VROW + VQ * qq;                              \
+                if constexpr (VQW == 2) {                                                             \
+                    const u32x2 r = ok ? *(const u32x2 *)src : u32x2{0u, 0u};                         \
+                    vw[m][u][0] = r[0];                                                               \
+                    vw[m][u][1] = r[1];                                                               \
+                } else {                                                                              \
+                    const u32x4 r = ok ? ld16(src) : u32x4{0u, 0u, 0u, 0u};                           \
+                    _Pragma("unroll") for (int w = 0; w < VQW; ++w) vw[m][u][w] = r[w];               \
+                }                                                                                     \
+                vp[m][u][0] = ok ? vsc[t * ngroups + gi] : (uint16_t)0;                               \
+                vp[m][u][1] = ok ? voff[t * ngroups + gi] : (uint16_t)0;                              \
+            }                                                                                         \
+        }                                                                                             \
+    } while (0)
+    if (packed && base < stop) IQ_LOAD_CHUNK(base);
+    __syncthreads();
+
+    // ---------------- cooperative per-workgroup constants
+    {   // masked query rows: role != -1 (salient or donor) -> 0
+        u32x4 v = qraw;
+        if (packed) {
+            const uint32_t r0 = *(const uint32_t *)(s_role + qc), r1 = *(const uint32_t *)(s_role + qc + 4);
+#pragma unroll
+            for (int w = 0; w < 4; ++w) {
+                const uint32_t r2 = (w < 2 ? r0 : r1) >> (16 * (w & 1));
+                const uint32_t keep = ((r2 & 0xffu) == 0xffu ? 0x0000ffffu : 0u) |
+                                      (((r2 >> 8) & 0xffu) == 0xffu ? 0xffff0000u : 0u);
+                v[w] &= keep;
+            }
+        }
+        *(u32x4 *)(s_qm + qg * D + qc) = v;
+    }
+    if (tid < S) {
+        const uint32_t sd = s_sal[tid];
+        const uint32_t src = sd & 0xffu, don = sd >> 8;
+        const float m8 = s_kc[(src >> 5) * KC_STRIDE + (src & 31)].y;   // -8 s_src
+        s_salf[tid] = f32x2{-0.125f * m8, 16.0f * m8};                   // (s_src, -128 s_src), exact
+        s_salw[tid] = (src >> 1) | (((src & 1) * 4) << 8) | ((don >> 1) << 16) | (((don & 1) * 4) << 24);
+    }
+    for (int i = tid; i < 16 * 16 * sal_groups; i += 256) {
+        const int g = i / (16 * sal_groups), k = i % (16 * sal_groups);
+        s_qsal[g * 64 + k] = k < S ? s_q[g * D + (s_sal[k] & 0xffu)] : (uint16_t)0;
+    }
+    __syncthreads();
+
+    // ---------------- per-lane constants
+    u32x4 qb[4];                                   // B operand: Q[g = gl][32 ql + 8 d + e], masked
+#pragma unroll
+    for (int d = 0; d < 4; ++d) qb[d] = *(const u32x4 *)(s_qm + gl * D + 32 * ql + 8 * d);
+    float bias = 0.0f;                             // sum_k q[gl][don_k] * round(pad_k)
+    for (int grp = 0; grp < sal_groups; ++grp)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const int k = 16 * grp + 4 * ql + e;
+            if (k < S) bias = fmaf(to_f32<F16>(s_q[gl * D + (s_sal[k] >> 8)]), s_dpad[k], bias);
+        }
+    bias = xsum16(bias);
+
+    float m_run = NEG_INF, l_run = 0.0f;
+    f32x4 acc[8];
+#pragma unroll
+    for (int n = 0; n < 8; ++n) acc[n] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+
+    uint32_t *vt = s_v[wave];
+
+    for (; base < stop; base += CHUNK * WAVES) {
+        const bool full = base + CHUNK <= stop;
+        // ---------------- logits S^T[token, g] for four 16-token tiles
+        f32x4 sc[4];
+        if (packed) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                // re-read the per-channel constants from LDS for every tile rather
+                // than keeping all 64 of them live in registers
+                asm volatile("" ::: "memory");
+                f32x4 s = {bias, bias, bias, bias};
+#pragma unroll
+                for (int d = 0; d < 4; ++d) {
+                    const f32x2 *kc = s_kc + ql * KC_STRIDE + 8 * d;
+                    const u32x4 c01 = *(const u32x4 *)(kc + 0), c23 = *(const u32x4 *)(kc + 2);
+                    const u32x4 c45 = *(const u32x4 *)(kc + 4), c67 = *(const u32x4 *)(kc + 6);
+                    const uint32_t x = kw[j][d];
+                    const uint32_t lo = x & 0x0f0f0f0fu, hi = (x >> 4) & 0x0f0f0f0fu;
+                    const f32x2 e01 = fp8x2<false>(lo), e23 = fp8x2<true>(lo);
+                    const f32x2 o01 = fp8x2<false>(hi), o23 = fp8x2<true>(hi);
+#define KF(cv, i) __uint_as_float(cv[i])
+                    u32x4 kv;
+                    kv[0] = pack2<F16>(fmaf(e01.x, KF(c01, 0), KF(c01, 1)), fmaf(o01.x, KF(c01, 2), KF(c01, 3)));
+                    kv[1] = pack2<F16>(fmaf(e01.y, KF(c23, 0), KF(c23, 1)), fmaf(o01.y, KF(c23, 2), KF(c23, 3)));
+                    kv[2] = pack2<F16>(fmaf(e23.x, KF(c45, 0), KF(c45, 1)), fmaf(o23.x, KF(c45, 2), KF(c45, 3)));
+                    kv[3] = pack2<F16>(fmaf(e23.y, KF(c67, 0), KF(c67, 1)), fmaf(o23.y, KF(c67, 2), KF(c67, 3)));
+#undef KF
+                    s = mma32<F16>(kv, qb[d], s);
+                }
+                sc[j] = s;
+            }
+            if (sal_groups) {
+                // stage the four K tiles as [64 tokens][17 dwords] for the salient gathers
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+#pragma unroll
+                    for (int w = 0; w < 4; ++w) vt[(16 * j + gl) * KROW + 4 * ql + w] = kw[j][w];
+                const uint8_t *kt = (const uint8_t *)vt;
+                for (int grp = 0; grp < sal_groups; ++grp) {
+                    uint32_t sw[4];
+                    f32x2 sf[4];
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        const int k = 16 * grp + 4 * ql + e;
+                        sw[e] = k < S ? s_salw[k] : 0u;
+                        sf[e] = k < S ? s_salf[k] : f32x2{0.0f, 0.0f};
+                    }
+                    const u32x2 qs = *(const u32x2 *)(s_qsal + gl * 64 + 16 * grp + 4 * ql);
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        const uint8_t *rowp = kt + (16 * j + gl) * (4 * KROW);
+                        float v[4];
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) {
+                            const uint32_t w = sw[e];
+                            const uint32_t hi = (rowp[w & 0xffu] >> ((w >> 8) & 0xffu)) & 15u;
+                            const uint32_t lo = (rowp[(w >> 16) & 0xffu] >> (w >> 24)) & 15u;
+                            v[e] = fmaf((float)((hi << 4) | lo), sf[e].x, sf[e].y);
+                        }
+                        const u32x2 ka = {pack2<F16>(v[0], v[1]), pack2<F16>(v[2], v[3])};
+                        sc[j] = mma16<F16>(ka, qs, sc[j]);
+                    }
+                }
+            }
+        } else {
+            // dense sink / tail: K rows of the query dtype are the A operand directly
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int t = base + 16 * j + gl;
+                f32x4 s = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+                for (int d = 0; d < 4; ++d) {
+                    const u32x4 kv = t < stop ? ld16(dk + (int64_t)t * dk_st + 32 * ql + 8 * d)
+                                              : u32x4{0u, 0u, 0u, 0u};
+                    s = mma32<F16>(kv, qb[d], s);
+                }
+                sc[j] = s;
+            }
+        }
+
+        // ---------------- online softmax (log2 domain); lane holds g = gl, tokens 16 j + 4 ql + r
+        float cmax = NEG_INF;
+        if (full) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    sc[j][r] *= a.c_log2;
+                    cmax = fmaxf(cmax, sc[j][r]);
+                }
+        } else {
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const float v = base + 16 * j + 4 * ql + r < stop ? sc[j][r] * a.c_log2 : NEG_INF;
+                    sc[j][r] = v;
+                    cmax = fmaxf(cmax, v);
+                }
+        }
+        cmax = xmax16(cmax);
+        const float m_new = fmaxf(m_run, cmax);
+        const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
+        float lsum = 0.0f;
+        u32x4 phi[2], plo[2];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            float pr[4];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                pr[r] = __builtin_amdgcn_exp2f(sc[j][r] - m_new);
+                lsum += pr[r];
+            }
+            const uint32_t h01 = pack2<F16>(pr[0], pr[1]), h23 = pack2<F16>(pr[2], pr[3]);
+            phi[j >> 1][2 * (j & 1)] = h01;
+            phi[j >> 1][2 * (j & 1) + 1] = h23;
+            plo[j >> 1][2 * (j & 1)] =
+                pack2<F16>(pr[0] - to_f32<F16>(h01 & 0xffffu), pr[1] - to_f32<F16>(h01 >> 16));
+            plo[j >> 1][2 * (j & 1) + 1] =
+                pack2<F16>(pr[2] - to_f32<F16>(h23 & 0xffffu), pr[3] - to_f32<F16>(h23 >> 16));
+        }
+        l_run = l_run * alpha + lsum;
+        m_run = m_new;
+#pragma unroll
+        for (int n = 0; n < 8; ++n) acc[n] *= alpha;
+
+        // ---------------- two half chunks: decode 32 V rows to LDS, then O^T += V^T P^T
+#pragma unroll
+        for (int m = 0; m < 2; ++m) {
+            uint32_t *dst = vt + pl * VR + 32 * qq;    // token pair pl, channels 32 qq .. 32 qq + 31
+            if (packed) {
+                float s9[2], of[2];
+#pragma unroll
+                for (int u = 0; u < 2; ++u) {
+                    s9[u] = iq_f16_to_f32(vp[m][u][0]) * inv_unit;
+                    of[u] = iq_f16_to_f32(vp[m][u][1]);
+                }
+                if constexpr (VBITS == 2) {
+#pragma unroll
+                    for (int w = 0; w < 2; ++w) {          // 16 channels 32 qq + 16 w + (4 b + k)
+                        float val[2][16];
+#pragma unroll
+                        for (int u = 0; u < 2; ++u) {
+                            const uint32_t x = vw[m][u][w];
+#pragma unroll
+                            for (int k = 0; k < 4; ++k) {
+                                const uint32_t b = (x >> (2 * k)) & 0x03030303u;
+                                const f32x2 c0 = fp8x2<false>(b), c1 = fp8x2<true>(b);
+                                val[u][k] = fmaf(c0.x, s9[u], of[u]);
+                                val[u][4 + k] = fmaf(c0.y, s9[u], of[u]);
+                                val[u][8 + k] = fmaf(c1.x, s9[u], of[u]);
+                                val[u][12 + k] = fmaf(c1.y, s9[u], of[u]);
+                            }
+                        }
+#pragma unroll
+                        for (int c4 = 0; c4 < 4; ++c4) {
+                            u32x4 o;
+#pragma unroll
+                            for (int i = 0; i < 4; ++i) o[i] = pack2<F16>(val[0][4 * c4 + i], val[1][4 * c4 + i]);
+                            *(u32x4 *)(dst + 16 * w + 4 * c4) = o;
+                        }
+                    }
+                } else {
+#pragma unroll
+                    for (int w = 0; w < 4; ++w) {          // 8 channels 32 qq + 8 w + (2 b + {0, 1})
+                        float val[2][8];
+#pragma unroll
+                        for (int u = 0; u < 2; ++u) {
+                            const uint32_t x = vw[m][u][w];
+                            const uint32_t lo = x & 0x0f0f0f0fu, hi = (x >> 4) & 0x0f0f0f0fu;
+                            const f32x2 e01 = fp8x2<false>(lo), e23 = fp8x2<true>(lo);
+                            const f32x2 o01 = fp8x2<false>(hi), o23 = fp8x2<true>(hi);
+                            val[u][0] = fmaf(e01.x, s9[u], of[u]);
+                            val[u][1] = fmaf(o01.x, s9[u], of[u]);
+                            val[u][2] = fmaf(e01.y, s9[u], of[u]);
+                            val[u][3] = fmaf(o01.y, s9[u], of[u]);
+                            val[u][4] = fmaf(e23.x, s9[u], of[u]);
+                            val[u][5] = fmaf(o23.x, s9[u], of[u]);
+                            val[u][6] = fmaf(e23.y, s9[u], of[u]);
+                            val[u][7] = fmaf(o23.y, s9[u], of[u]);
+                        }
+#pragma unroll
+                        for (int c4 = 0; c4 < 2; ++c4) {
+                            u32x4 o;
+#pragma unroll
+                            for (int i = 0; i < 4; ++i) o[i] = pack2<F16>(val[0][4 * c4 + i], val[1][4 * c4 + i]);
+                            *(u32x4 *)(dst + 8 * w + 4 * c4) = o;
+                        }
+                    }
+                }
+            } else {
+                const int t0 = base + 32 * m + 2 * pl;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const u32x4 r0 = t0 < stop ? ld16(dv + (int64_t)t0 * dv_st + 32 * qq + 8 * i)
+                                               : u32x4{0u, 0u, 0u, 0u};
+                    const u32x4 r1 = t0 + 1 < stop ? ld16(dv + (int64_t)(t0 + 1) * dv_st + 32 * qq + 8 * i)
+                                                   : u32x4{0u, 0u, 0u, 0u};
+                    u32x4 lo, hi;
+#pragma unroll
+                    for (int w = 0; w < 4; ++w) {
+                        lo[w] = __builtin_amdgcn_perm(r1[w], r0[w], 0x05040100u);   // (r0.lo, r1.lo)
+                        hi[w] = __builtin_amdgcn_perm(r1[w], r0[w], 0x07060302u);   // (r0.hi, r1.hi)
+                    }
+                    *(u32x4 *)(dst + 8 * i) = u32x4{lo[0], hi[0], lo[1], hi[1]};
+                    *(u32x4 *)(dst + 8 * i + 4) = u32x4{lo[2], hi[2], lo[3], hi[3]};
+                }
+            }
+#pragma unroll
+            for (int n = 0; n < 8; ++n) {
+                u32x4 va;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const int pp = e < 2 ? 2 * ql + e : 8 + 2 * ql + (e - 2);
+                    va[e] = vt[pp * VR + 16 * n + gl];
+                }
+                acc[n] = mma32<F16>(va, phi[m], acc[n]);
+                acc[n] = mma32<F16>(va, plo[m], acc[n]);
+            }
+        }
+        // blocks longer than one pass load their next chunk here
+        if (packed && base + CHUNK * WAVES < stop) IQ_LOAD_CHUNK(base + CHUNK * WAVES);
+    }
+#undef IQ_LOAD_CHUNK
+
+    // ---------------- combine the four wavefronts, write this partition's partial
+    l_run = xsum16(l_run);
+    if (ql == 0) {
+        s_wm[wave][gl] = m_run;
+        s_wl[wave][gl] = l_run;
+    }
+    float *ot = (float *)vt;        // O^T[c][g] of this wavefront, row stride 17
+#pragma unroll
+    for (int n = 0; n < 8; ++n)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) ot[(16 * n + 4 * ql + r) * 17 + gl] = acc[n][r];
+    __syncthreads();
+    for (int i = tid; i < G * D; i += 256) {
+        const int g = i >> 7, c = i & (D - 1);
+        float mx = NEG_INF;
+#pragma unroll
+        for (int w = 0; w < WAVES; ++w) mx = fmaxf(mx, s_wm[w][g]);
+        float num = 0.0f, den = 0.0f;
+#pragma unroll
+        for (int w = 0; w < WAVES; ++w) {
+            const float mw = s_wm[w][g];
+            const float wt = mw == NEG_INF ? 0.0f : __builtin_amdgcn_exp2f(mw - mx);
+            num = fmaf(((const float *)s_v[w])[c * 17 + g], wt, num);
+            den = fmaf(s_wl[w][g], wt, den);
+        }
+        if (a.P == 1) {
+            iq_store_as(a.out, (int64_t)(h * G + g) * D + c, num / den, a.odt);
+            continue;
+        }
+        float *out = a.ws + ((int64_t)(h * G + g) * a.P + p) * (D + 2);
+        st_agent(out + c, num);
+        if (c == 0) {
+            st_agent(out + D, mx * LN2);
+            st_agent(out + D + 1, den);
+        }
+    }
+    if (a.P == 1 || a.cnt == nullptr) return;
+
+    // ---------------- last-arriving workgroups merge: first per group of
+    // MERGE_GROUP partitions (into the group's first slot), then per KV head
+    __shared__ int s_last;
+    const int grp = (int)(p / MERGE_GROUP);
+    const int gsize = (int)min((int64_t)MERGE_GROUP, a.P - (int64_t)grp * MERGE_GROUP);
+    int *cnt = a.cnt + h * (a.ngrp + 1);
+    if (!arrive_last(cnt + grp, gsize, &s_last)) return;
+    if (tid == 0) __hip_atomic_store(cnt + grp, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    merge_partials(a, h, G, (int64_t)grp * MERGE_GROUP, 1, gsize, a.ngrp == 1);
+    if (a.ngrp == 1) return;
+    if (!arrive_last(cnt + a.ngrp, a.ngrp, &s_last)) return;
+    if (tid == 0) __hip_atomic_store(cnt + a.ngrp, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    merge_partials(a, h, G, 0, MERGE_GROUP, a.ngrp, true);
+}
+
+}  // namespace
+
+#undef IQ_LOAD_CHUNK
+
+int64_t iq_decode_merge_ints(int64_t H, int64_t P) { return H * ((P + MERGE_GROUP - 1) / MERGE_GROUP + 1); }
+
+// Launches the matrix-core decode; returns IQ_ERR_UNSUPPORTED for layouts it
+// does not cover.  *merged = 1 when the output was written in-kernel,
+// 0 when the caller must run the separate partial reduction.
+int iq_decode_fast_launch(const void *q, int q_dtype, int64_t q_stride_h, int64_t Hq, const int64_t *tables,
+                          const int8_t *key_map, int64_t n_blocks, int64_t block_tokens, int64_t H, int64_t S,
+                          int value_bits, int value_group, const void *sink_k, const void *sink_v, int64_t sink_k_sh,
+                          int64_t sink_k_st, int64_t sink_v_sh, int64_t sink_v_st, int64_t sink_t,
+                          const void *tail_k, const void *tail_v, int64_t tail_k_sh, int64_t tail_k_st,
+                          int64_t tail_v_sh, int64_t tail_v_st, int64_t tail_t, float scale, float *workspace,
+                          int64_t P, int *counters, int64_t counter_ints, void *out, int out_dtype,
+                          int *merged, hipStream_t stream)
+{
+    if (q_dtype != IQ_BF16 && q_dtype != IQ_F16) return IQ_ERR_UNSUPPORTED;
+    if (out_dtype != IQ_F32 && out_dtype != IQ_BF16 && out_dtype != IQ_F16) return IQ_ERR_UNSUPPORTED;
+    if (n_blocks > 0 && value_bits != 2 && value_bits != 4) return IQ_ERR_UNSUPPORTED;
+    if (Hq / H > 16 || S > 64) return IQ_ERR_UNSUPPORTED;
+    // query, dense rows and packed rows are read as 16-byte vectors
+    auto aligned = [](const void *ptr, int64_t sh, int64_t st) {
+        return ((uintptr_t)ptr % 16 == 0) && (sh % 8 == 0) && (st % 8 == 0);
+    };
+    if (!aligned(q, q_stride_h, 8)) return IQ_ERR_UNSUPPORTED;
+    if (sink_t && !(aligned(sink_k, sink_k_sh, sink_k_st) && aligned(sink_v, sink_v_sh, sink_v_st)))
+        return IQ_ERR_UNSUPPORTED;
+    if (tail_t && !(aligned(tail_k, tail_k_sh, tail_k_st) && aligned(tail_v, tail_v_sh, tail_v_st)))
+        return IQ_ERR_UNSUPPORTED;
+    FastArgs a{(const uint16_t *)q, q_stride_h, (int)(Hq / H), tables, key_map, n_blocks, block_tokens, H, S,
+               value_group ? value_group : 64, (const uint16_t *)sink_k, (const uint16_t *)sink_v, sink_k_sh,
+               sink_k_st, sink_v_sh, sink_v_st, sink_t, (const uint16_t *)tail_k, (const uint16_t *)tail_v,
+               tail_k_sh, tail_k_st, tail_v_sh, tail_v_st, tail_t, scale * 1.44269504088896341f, workspace, P,
+               nullptr, 0, out, out_dtype};
+    const int64_t ngrp = (P + MERGE_GROUP - 1) / MERGE_GROUP;
+    *merged = P == 1;
+    if (P > 1 && counters && counter_ints >= H * (ngrp + 1)) {
+        a.cnt = counters;       // merged in-kernel by the last-arriving workgroups
+        a.ngrp = (int)ngrp;
+        *merged = 1;
+    }
+    const dim3 grid((unsigned)H, (unsigned)P), block(256);
+    const bool f16 = q_dtype == IQ_F16;
+    const int vb = n_blocks > 0 ? value_bits : 2;
+    if (f16 && vb == 2) hipLaunchKernelGGL((decode_fast<true, 2>), grid, block, 0, stream, a);
+    else if (f16) hipLaunchKernelGGL((decode_fast<true, 4>), grid, block, 0, stream, a);
+    else if (vb == 2) hipLaunchKernelGGL((decode_fast<false, 2>), grid, block, 0, stream, a);
+    else hipLaunchKernelGGL((decode_fast<false, 4>), grid, block, 0, stream, a);
+    return IQ_OK;
+}

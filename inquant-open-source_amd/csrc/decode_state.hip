@@ -3,7 +3,8 @@
 // Restates PackedDecodeState.extend / _write_maps (triton_attention.py:294-369):
 // for each newly sealed block, one row of the i64 pointer table
 // (K payload, K scales, K padding, V payload, V scales-or-K4-scales,
-// V offsets-or-padding) and an int8 [H, 128] role map per coded tensor:
+// V offsets-or-padding, then the K source and donor descriptor addresses
+// that the decode kernel reads directly) and an int8 [H, 128] role map per coded tensor:
 // -1 normal, donor channel for a source, -2 - i for donor i.
 // The block addresses travel as kernel arguments, so no host-to-device copy
 // of a pageable pointer list is needed.
@@ -35,9 +36,10 @@ __global__ __launch_bounds__(128) void append_kernel(AppendArgs a)
     const int blk = blockIdx.x, h = blockIdx.y, c = threadIdx.x;
     const iq_block_ptrs &p = a.blocks[blk];
     const int64_t slot = a.first + blk;
-    if (h == 0 && c < 6) {
-        const uint64_t v[6] = {p.k_payload, p.k_scales, p.k_padding, p.v_payload, p.v_scales, p.v_offsets};
-        a.tables[slot * 6 + c] = (int64_t)v[c];
+    if (h == 0 && c < IQ_TABLE_COLS) {
+        const uint64_t v[IQ_TABLE_COLS] = {p.k_payload, p.k_scales, p.k_padding, p.v_payload,
+                                           p.v_scales,  p.v_offsets, p.k_src, p.k_don};
+        a.tables[slot * IQ_TABLE_COLS + c] = (int64_t)v[c];
     }
     s_k[c] = -1;
     s_v[c] = -1;

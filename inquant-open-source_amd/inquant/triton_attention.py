@@ -2,7 +2,8 @@
 
 Module and class names are kept from the reference (src/inquant/triton_attention.py)
 so callers switch without edits; no Triton is used.  PackedDecodeState keeps
-the reference's reusable metadata -- an i64 pointer table [cap, 6] and int8
+the reference's reusable metadata -- an i64 pointer table [cap, 8] (the
+reference's six block addresses plus the K descriptor addresses) and int8
 role maps [cap, H, 128] appended incrementally (:294-369) -- and decode()
 runs the fused HIP kernel over [sink | packed blocks | tail] followed by the
 log-sum-exp merge (:377-448).  Keys and values are decoded and rounded to the
@@ -24,6 +25,9 @@ from .codec import PackedTensor
 from .value_codec import PackedValues
 
 _DENSE_SPLIT = 256
+# pointer-table columns: the reference's six block addresses plus the K
+# source/donor descriptor addresses read directly by the decode kernel
+_TABLE_COLS = 8
 
 
 def _cdiv(a: int, b: int) -> int:
@@ -74,6 +78,9 @@ class PackedDecodeState:
         self._value_group = 64
         self._capacity = 0
         self._stream_identity = None
+        # int32 counters that let the last-arriving workgroups merge partitions
+        # inside the decode kernel; zero between calls (each launch resets them)
+        self._merge = None
         self.extend(key_blocks, value_blocks)
 
     def extend(self, key_blocks, value_blocks):
@@ -127,7 +134,7 @@ class PackedDecodeState:
         count = len(key_blocks)
         if count > self._capacity:
             capacity = count if not self._capacity else max(count, min(self._capacity * 2, count + 7))
-            tables = torch.empty((capacity, 6), dtype=torch.int64, device=self._device)
+            tables = torch.empty((capacity, _TABLE_COLS), dtype=torch.int64, device=self._device)
             key_map = torch.empty((capacity, self._kv_heads, 128), dtype=torch.int8, device=self._device)
             value_map = (torch.empty((0,), dtype=torch.int8, device=self._device) if self._value_bits
                          else torch.empty_like(key_map))
@@ -160,7 +167,7 @@ class PackedDecodeState:
     def nbytes(self) -> int:
         """Auxiliary GPU allocations of this state (tables, maps, private workspace)."""
         return sum(t.untyped_storage().nbytes() for t in
-                   (self._tables, self._key_map, self._value_map, self._workspace) if t is not None)
+                   (self._tables, self._key_map, self._value_map, self._workspace, self._merge) if t is not None)
 
     @torch.no_grad()
     def decode(self, query, *, sink_key=None, sink_value=None, residual_key=None, residual_value=None,
@@ -224,25 +231,31 @@ class PackedDecodeState:
             raise ValueError("output must be a contiguous query-shaped tensor of the query dtype or float32")
         if self._tables is None:
             # zero-element placeholders keep nbytes accounting identical to the reference
-            self._tables = torch.empty((0, 6), dtype=torch.int64, device=query.device)
+            self._tables = torch.empty((0, _TABLE_COLS), dtype=torch.int64, device=query.device)
             self._key_map = torch.empty((0, kv_heads, 128), dtype=torch.int8, device=query.device)
             self._value_map = torch.empty_like(self._key_map)
             self._device = query.device
         n_blocks = len(self.key_blocks)
         stream = nat.stream_handle(query.device)
+        lib = nat.lib()
+        need = lib.iq_decode_merge_counter_ints(kv_heads, n_blocks, sink_t, tail_t)
+        if partitions > 1 and (self._merge is None or self._merge.numel() < need
+                               or self._merge.device != query.device):
+            self._merge = torch.zeros(-(-need // 64) * 64, dtype=torch.int32, device=query.device)
+        merge = self._merge if partitions > 1 else None
 
         def st(t, dim):
             return 0 if t is None else t.stride(dim)
 
-        nat.check(nat.lib().iq_decode_attention(
+        nat.check(lib.iq_decode_attention(
             query.data_ptr(), nat.dtype_code(query.dtype), query.stride(1), query.shape[1],
             self._tables.data_ptr() if n_blocks else None, self._key_map.data_ptr() if n_blocks else None,
             self._value_map.data_ptr() if (n_blocks and not self._value_bits) else None,
             n_blocks, self._packed_tokens, kv_heads, self._salient, self._value_bits, self._value_group,
             nat.ptr(sk), nat.ptr(sv), st(sk, 1), st(sk, 2), st(sv, 1), st(sv, 2), sink_t,
             nat.ptr(tk), nat.ptr(tv), st(tk, 1), st(tk, 2), st(tv, 1), st(tv, 2), tail_t,
-            float(scale), workspace.data_ptr(), workspace.numel(), output.data_ptr(),
-            nat.dtype_code(output.dtype), stream))
+            float(scale), workspace.data_ptr(), workspace.numel(), nat.ptr(merge),
+            0 if merge is None else merge.numel(), output.data_ptr(), nat.dtype_code(output.dtype), stream))
         return output
 
 

@@ -37,7 +37,8 @@ def test_k4_values_with_sink_and_unsealed_tail(dtype, fraction, policy):
     # the typed result is the fp32 result rounded once
     expect_typed = torch.from_numpy(got).to("cuda").to(dtype).view_as(typed)
     assert torch.equal(typed, expect_typed)
-    assert state.nbytes == descriptor_bytes + state._workspace.numel() * 4
+    merge_bytes = 0 if state._merge is None else state._merge.numel() * 4
+    assert state.nbytes == descriptor_bytes + state._workspace.numel() * 4 + merge_bytes
     pointer = state._workspace.data_ptr()
     state.decode(case.query, **case.kwargs())
     assert state._workspace.data_ptr() == pointer
@@ -137,8 +138,8 @@ def test_growing_state_matches_fresh_state_and_rejects_replacement():
         assert state._key_map.dtype == torch.int8
         assert torch.equal(state._key_map[:i + 1], fresh._key_map[:i + 1])
         assert state.nbytes == sum(x.untyped_storage().nbytes() for x in
-                                   (state._tables, state._key_map, state._value_map, state._workspace)
-                                   if x is not None)
+                                   (state._tables, state._key_map, state._value_map, state._workspace,
+                                    state._merge) if x is not None)
     with pytest.raises(ValueError, match="append-only"):
         state.extend(keys[:-1], values[:-1])
     with pytest.raises(ValueError, match="append-only"):
@@ -160,7 +161,8 @@ def test_role_maps_and_tables_match_oracle():
             np.testing.assert_array_equal(table[i].cpu().numpy().astype(np.int16), roles)
         row = state._tables[i].cpu().tolist()
         assert row == [k.payload.data_ptr(), k.scales.data_ptr(), k.padding.data_ptr(), v.payload.data_ptr(),
-                       v.scales.data_ptr(), v.padding.data_ptr()]
+                       v.scales.data_ptr(), v.padding.data_ptr(), k.salient_channels.data_ptr(),
+                       k.donor_channels.data_ptr()]
 
 
 def test_workspace_pool_is_shared_once_and_rejects_other_stream():
@@ -174,7 +176,7 @@ def test_workspace_pool_is_shared_once_and_rejects_other_stream():
         state.decode(q, residual_key=k, residual_value=v + i, output=out)
         exp = oracle_decode(q, [], [], tail_k=k, tail_v=v + i)
         np.testing.assert_allclose(to_np(out)[0, :, 0], exp, atol=ATOL, rtol=0)
-        assert state._workspace is None and state.nbytes == 0
+        assert state._workspace is None and state.nbytes == 0   # one partition: no merge counters
     assert pool.nbytes == 28 * 130 * 4
     first = pool.tensor.data_ptr()
     states[0].decode(q, residual_key=k, residual_value=v)
@@ -184,3 +186,50 @@ def test_workspace_pool_is_shared_once_and_rejects_other_stream():
         with pytest.raises(RuntimeError, match="one CUDA stream"):
             states[0].decode(q, residual_key=k, residual_value=v)
     torch.cuda.synchronize()
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("fraction", [0.0, 0.125, 0.5])
+@pytest.mark.parametrize("block,sink,tail", [(256, 4, 128), (41, 0, 281), (32, 4, 0), (300, 3, 1)])
+def test_matrix_core_path_matches_oracle(dtype, fraction, block, sink, tail):
+    # bf16/f16 queries with V2 values take the MFMA kernel: partial tiles,
+    # 0..64 salient channels, blocks longer than one 256-token pass
+    from inquant.triton_attention import PackedDecodeState
+    case = make_case(17 + block, n_blocks=3, block=block, sink=sink, tail=tail, dtype=dtype, fraction=fraction)
+    state = PackedDecodeState(case.key_blocks, case.value_blocks)
+    got = _decode_f32(state, case)
+    np.testing.assert_allclose(got, case.expected(), atol=ATOL, rtol=0)
+    typed = state.decode(case.query, **case.kwargs())
+    assert torch.equal(typed, torch.from_numpy(got).to("cuda").to(dtype).view_as(typed))
+
+
+def test_matrix_core_path_peaked_attention_keeps_precision():
+    # one dominant token with large outlier values: P must keep more than
+    # bf16 precision for the 2e-3 bound to hold
+    from inquant.codec import quantize
+    from inquant.value_codec import quantize_values
+    from inquant.triton_attention import PackedDecodeState
+    from kvcase import oracle_decode
+    import synth
+    k = torch.from_numpy(synth.kv_like(5, 4, 256)).cuda().to(torch.bfloat16)
+    v = torch.from_numpy(synth.kv_like(6, 4, 256, scale=40.0)).cuda().to(torch.bfloat16)
+    q = (k[:, :, 77:78, :].repeat_interleave(7, dim=1) * 0.5).contiguous()
+    kp, vp = quantize(k), quantize_values(v)
+    state = PackedDecodeState([kp], [vp])
+    out = torch.empty(q.shape, dtype=torch.float32, device="cuda")
+    state.decode(q, output=out)
+    exp = oracle_decode(q, [kp], [vp])
+    np.testing.assert_allclose(to_np(out)[0, :, 0], exp, atol=ATOL, rtol=0)
+
+
+def test_cfg2_full_context_matches_oracle_and_is_repeatable():
+    # BASELINE config 2 layer: 128 packed blocks (32768 tokens) + 4 sink + 128 tail;
+    # 130 partitions merged in-kernel by the last-arriving workgroups
+    from inquant.triton_attention import PackedDecodeState
+    case = make_case(2, n_blocks=128, sink=4, tail=128)
+    state = PackedDecodeState(case.key_blocks, case.value_blocks)
+    outs = [_decode_f32(state, case) for _ in range(4)]
+    for o in outs[1:]:
+        assert np.array_equal(o, outs[0])            # merge order is fixed, not arrival order
+    assert state._merge is not None and not state._merge.any()   # counters reset by every launch
+    np.testing.assert_allclose(outs[0], case.expected(), atol=ATOL, rtol=0)
