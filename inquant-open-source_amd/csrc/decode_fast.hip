@@ -131,7 +131,16 @@ __device__ __forceinline__ float xsum16(float v)
     return v + __shfl_xor(v, 32, 64);
 }
 
-__device__ __forceinline__ u32x4 ld16(const void *p) { return *(const u32x4 *)p; }
+// Loads through global-address-space pointers: the pointer table holds plain
+// addresses, which would otherwise be dereferenced with flat instructions
+// that every LDS wait must also drain.
+template <class T>
+__device__ __forceinline__ T ldg(const void *p)
+{
+    return *(const __attribute__((address_space(1))) T *)p;
+}
+
+__device__ __forceinline__ u32x4 ld16(const void *p) { return ldg<u32x4>(p); }
 
 // Partials exchanged between workgroups use agent-coherent stores and loads
 // (sc1: written through / read past the per-XCD L2), so publishing them costs
@@ -186,7 +195,7 @@ __device__ __forceinline__ float rowsum16(float v)
 // threads that own output channels, whose sixteen independent loads per chunk
 // are all in flight together.  Writes the merged row to partition p_first,
 // or the normalized output when final_out.
-__device__ void merge_partials(const FastArgs &a, int h, int G, int64_t p_first, int64_t stride, int count,
+__device__ __forceinline__ void merge_partials(const FastArgs &a, int h, int G, int64_t p_first, int64_t stride, int count,
                                bool final_out)
 {
     constexpr int ITEMS = 16 * D / 256;
@@ -302,15 +311,15 @@ __global__ __launch_bounds__(256, 3) void decode_fast(FastArgs a)
         voff = (const uint16_t *)row[5] + (int64_t)h * a.BT * ngroups;
         stop = (int)a.BT;
         if (tid < D) {
-            const float s = ((const float *)row[1])[h * D + tid];
+            const float s = ldg<float>((const float *)row[1] + h * D + tid);
             s_kc[(tid >> 5) * KC_STRIDE + (tid & 31)] = f32x2{s * inv_unit, -8.0f * s};
-            s_role[tid] = a.kmap[(p * a.H + h) * D + tid];
+            s_role[tid] = ldg<int8_t>(a.kmap + (p * a.H + h) * D + tid);
         }
         if (tid < S) {
-            const uint32_t src = ((const uint8_t *)row[6])[h * S + tid];
-            const uint32_t don = ((const uint8_t *)row[7])[h * S + tid];
+            const uint32_t src = ldg<uint8_t>((const uint8_t *)row[6] + h * S + tid);
+            const uint32_t don = ldg<uint8_t>((const uint8_t *)row[7] + h * S + tid);
             s_sal[tid] = src | (don << 8);
-            s_dpad[tid] = round_q<F16>(((const float *)row[2])[h * S + tid]);
+            s_dpad[tid] = round_q<F16>(ldg<float>((const float *)row[2] + h * S + tid));
         }
     } else {
         const int64_t dp = p - a.nblk;
@@ -350,15 +359,15 @@ __global__ __launch_bounds__(256, 3) void decode_fast(FastArgs a)
                 const bool ok = t < stop;                                                             \
                 const uint8_t *src = vpay + (int64_t)t * VROW + VQ * qq;                              \
                 if constexpr (VQW == 2) {                                                             \
-                    const u32x2 r = ok ? *(const u32x2 *)src : u32x2{0u, 0u};                         \
+                    const u32x2 r = ok ? ldg<u32x2>(src) : u32x2{0u, 0u};                             \
                     vw[m][u][0] = r[0];                                                               \
                     vw[m][u][1] = r[1];                                                               \
                 } else {                                                                              \
                     const u32x4 r = ok ? ld16(src) : u32x4{0u, 0u, 0u, 0u};                           \
                     _Pragma("unroll") for (int w = 0; w < VQW; ++w) vw[m][u][w] = r[w];               \
                 }                                                                                     \
-                vp[m][u][0] = ok ? vsc[t * ngroups + gi] : (uint16_t)0;                               \
-                vp[m][u][1] = ok ? voff[t * ngroups + gi] : (uint16_t)0;                              \
+                vp[m][u][0] = ok ? ldg<uint16_t>(vsc + t * ngroups + gi) : (uint16_t)0;               \
+                vp[m][u][1] = ok ? ldg<uint16_t>(voff + t * ngroups + gi) : (uint16_t)0;              \
             }                                                                                         \
         }                                                                                             \
     } while (0)
@@ -478,18 +487,27 @@ __global__ __launch_bounds__(256, 3) void decode_fast(FastArgs a)
                 }
             }
         } else {
-            // dense sink / tail: K rows of the query dtype are the A operand directly
+            // dense sink / tail: K rows of the query dtype are the A operand
+            // directly; two tiles' rows (clamped in range, zeroed past the
+            // end) are in flight together
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const int t = base + 16 * j + gl;
-                f32x4 s = {0.0f, 0.0f, 0.0f, 0.0f};
+            for (int j2 = 0; j2 < 4; j2 += 2) {
+                u32x4 kd[2][4];
 #pragma unroll
-                for (int d = 0; d < 4; ++d) {
-                    const u32x4 kv = t < stop ? ld16(dk + (int64_t)t * dk_st + 32 * ql + 8 * d)
-                                              : u32x4{0u, 0u, 0u, 0u};
-                    s = mma32<F16>(kv, qb[d], s);
+                for (int jj = 0; jj < 2; ++jj) {
+                    const int t = base + 16 * (j2 + jj) + gl;
+                    const int tc = t < stop ? t : stop - 1;
+#pragma unroll
+                    for (int d = 0; d < 4; ++d) kd[jj][d] = ld16(dk + (int64_t)tc * dk_st + 32 * ql + 8 * d);
                 }
-                sc[j] = s;
+#pragma unroll
+                for (int jj = 0; jj < 2; ++jj) {
+                    const bool ok = base + 16 * (j2 + jj) + gl < stop;
+                    f32x4 s = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+                    for (int d = 0; d < 4; ++d) s = mma32<F16>(ok ? kd[jj][d] : u32x4{0u, 0u, 0u, 0u}, qb[d], s);
+                    sc[j2 + jj] = s;
+                }
             }
         }
 
@@ -605,17 +623,22 @@ __global__ __launch_bounds__(256, 3) void decode_fast(FastArgs a)
                 }
             } else {
                 const int t0 = base + 32 * m + 2 * pl;
+                const int ta = t0 < stop ? t0 : stop - 1, tb = t0 + 1 < stop ? t0 + 1 : stop - 1;
+                u32x4 r0[4], r1[4];
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
-                    const u32x4 r0 = t0 < stop ? ld16(dv + (int64_t)t0 * dv_st + 32 * qq + 8 * i)
-                                               : u32x4{0u, 0u, 0u, 0u};
-                    const u32x4 r1 = t0 + 1 < stop ? ld16(dv + (int64_t)(t0 + 1) * dv_st + 32 * qq + 8 * i)
-                                                   : u32x4{0u, 0u, 0u, 0u};
+                    r0[i] = ld16(dv + (int64_t)ta * dv_st + 32 * qq + 8 * i);
+                    r1[i] = ld16(dv + (int64_t)tb * dv_st + 32 * qq + 8 * i);
+                }
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    if (t0 >= stop) r0[i] = u32x4{0u, 0u, 0u, 0u};
+                    if (t0 + 1 >= stop) r1[i] = u32x4{0u, 0u, 0u, 0u};
                     u32x4 lo, hi;
 #pragma unroll
                     for (int w = 0; w < 4; ++w) {
-                        lo[w] = __builtin_amdgcn_perm(r1[w], r0[w], 0x05040100u);   // (r0.lo, r1.lo)
-                        hi[w] = __builtin_amdgcn_perm(r1[w], r0[w], 0x07060302u);   // (r0.hi, r1.hi)
+                        lo[w] = __builtin_amdgcn_perm(r1[i][w], r0[i][w], 0x05040100u);   // (r0.lo, r1.lo)
+                        hi[w] = __builtin_amdgcn_perm(r1[i][w], r0[i][w], 0x07060302u);   // (r0.hi, r1.hi)
                     }
                     *(u32x4 *)(dst + 8 * i) = u32x4{lo[0], hi[0], lo[1], hi[1]};
                     *(u32x4 *)(dst + 8 * i + 4) = u32x4{lo[2], hi[2], lo[3], hi[3]};

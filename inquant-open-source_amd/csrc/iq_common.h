@@ -66,6 +66,19 @@ __device__ __forceinline__ void iq_store_as(void *p, int64_t i, float v, int dt)
     }
 }
 
+// rint(RN(a / b)) for normal b, given rcp_b = v_rcp_f32(b) (within 1 ulp of
+// 1 / b): the reciprocal product q is within 2^-21 |q|
+// of the quotient, so its rounding equals that of the IEEE quotient unless q
+// lies within 2^-20 |q| of a half-integer, where the IEEE division decides.
+__device__ __forceinline__ float iq_rint_div(float a, float b, float rcp_b)
+{
+    const float q = __fmul_rn(a, rcp_b);
+    const float r = rintf(q);
+    const float d = 0.5f - fabsf(__fsub_rn(q, r));
+    if (d > fabsf(q) * 0x1p-20f) return r;
+    return rintf(a / b);
+}
+
 __device__ __forceinline__ bool iq_isfinite(float x) { return (__float_as_uint(x) & 0x7f800000u) != 0x7f800000u; }
 
 // ---------------------------------------------------------------- torch CPU reduction orders

@@ -16,6 +16,7 @@
 namespace {
 
 constexpr int K4_THREADS = 256;
+typedef __attribute__((ext_vector_type(4))) uint32_t u32x4_t;
 
 struct K4Args {
     const void *x;
@@ -39,7 +40,7 @@ __device__ __forceinline__ void store_desc(void *p, int64_t i, int v, int bytes)
 }
 
 // Sampled sums of one channel in torch's order (cascade, or interleaved row_sum).
-__device__ void sampled_sums(const void *x, int dt, int64_t base, int64_t step, int64_t ns, bool cascade_col,
+__device__ __forceinline__ void sampled_sums(const void *x, int dt, int64_t base, int64_t step, int64_t ns, bool cascade_col,
                              float &sum_abs, float &sum)
 {
     if (cascade_col) {
@@ -185,6 +186,207 @@ __global__ __launch_bounds__(K4_THREADS) void k4_encode_kernel(K4Args a)
     }
 }
 
+// ---------------------------------------------------------------------------
+// Tile encoder for the cache shapes: D = 128, 16-bit input, T <= 256 tokens,
+// channel-contiguous rows.  The whole [T, 128] block is staged in LDS with
+// 16-byte loads (64 KiB at T = 256), then
+//   waves 0-1  the fp64 Welford var_mean of channel tid (min_error only);
+//              delta / n uses a table of RN(1/n) and one remainder fma,
+//              which is the correctly rounded quotient for n <= 256;
+//   waves 2-3  sampled sums (torch cascade order), amax, finiteness;
+// wave 0 selects donors, and every thread quantizes 8 channels of a token
+// per step from LDS, writing 4 payload bytes.  Bit-identical to
+// k4_encode_kernel.
+constexpr int TILE_D = 128;
+constexpr int TILE_T = 256;
+
+template <bool F16IN>
+__device__ __forceinline__ float tile_f32(uint32_t bits16)
+{
+    if constexpr (F16IN) return iq_f16_to_f32((uint16_t)bits16);
+    else return __uint_as_float(bits16 << 16);
+}
+
+template <bool F16IN>
+__global__ __launch_bounds__(K4_THREADS) void k4_encode_tile(K4Args a)
+{
+    __shared__ __attribute__((aligned(16))) uint16_t s_x[TILE_T * TILE_D];
+    __shared__ double s_rcp[TILE_T];    // RN(1 / n), n = 1 .. T
+    __shared__ float s_sal[TILE_D], s_smean[TILE_D], s_err[TILE_D], s_amax[TILE_D], s_scale[TILE_D];
+    __shared__ int16_t s_src_of[TILE_D];
+    __shared__ uint8_t s_is_src[TILE_D];
+    __shared__ int16_t s_src[TILE_D / 2], s_don[TILE_D / 2];
+    __shared__ int s_bad;
+
+    const int tid = threadIdx.x;
+    const int64_t row = blockIdx.x;
+    const int64_t b = row / a.H, h = row % a.H;
+    const uint16_t *xr = (const uint16_t *)a.x + b * a.sb + h * a.sh;
+    const int T = (int)a.T;
+    const int ns = (int)((T + a.stride - 1) / a.stride);
+
+    // ---- stage the block: T rows x 16 segments of 8 channels
+    {
+        u32x4_t v[TILE_T * 16 / K4_THREADS];
+        // unconditional (clamped) loads so that all of them are in flight at once
+#pragma unroll
+        for (int k = 0; k < TILE_T * 16 / K4_THREADS; ++k) {
+            const int i = min(tid + K4_THREADS * k, T * 16 - 1);
+            v[k] = *(const u32x4_t *)(xr + (int64_t)(i >> 4) * a.st + 8 * (i & 15));
+        }
+        // rows at and beyond T receive copies of the last segment and are never read
+#pragma unroll
+        for (int k = 0; k < TILE_T * 16 / K4_THREADS; ++k) *(u32x4_t *)(s_x + 8 * (tid + K4_THREADS * k)) = v[k];
+    }
+    if (tid < T) s_rcp[tid] = 1.0 / (double)(tid + 1);
+    if (tid == 0) s_bad = 0;
+    __syncthreads();
+
+    if (tid < TILE_D) {
+        if (a.min_error) {
+            const int c = tid;
+            double mean = 0.0, m2 = 0.0;
+            auto step = [&](float xf, double y, int t) {
+                const double dv = (double)xf;
+                const double delta = __dsub_rn(dv, mean);
+                const double q0 = __dmul_rn(delta, y);
+                const double r = __builtin_fma(-q0, (double)(t + 1), delta);
+                mean = __dadd_rn(mean, __builtin_fma(r, y, q0));
+                const double nd = __dsub_rn(dv, mean);
+                m2 = __dadd_rn(m2, __dmul_rn(delta, nd));
+            };
+            // groups of eight tokens, the next group's LDS reads in flight
+            // while the current group's dependent steps run
+            const int Tg = T & ~7;
+            float cur[8], nxt[8];
+            double ycur[8], ynxt[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                cur[u] = Tg ? tile_f32<F16IN>(s_x[u * TILE_D + c]) : 0.0f;
+                ycur[u] = s_rcp[u];
+            }
+            for (int t0 = 0; t0 < Tg; t0 += 8) {
+                const int tn = t0 + 8 < Tg ? t0 + 8 : t0;
+#pragma unroll
+                for (int u = 0; u < 8; ++u) {
+                    nxt[u] = tile_f32<F16IN>(s_x[(tn + u) * TILE_D + c]);
+                    ynxt[u] = s_rcp[tn + u];
+                }
+#pragma unroll
+                for (int u = 0; u < 8; ++u) step(cur[u], ycur[u], t0 + u);
+#pragma unroll
+                for (int u = 0; u < 8; ++u) {
+                    cur[u] = nxt[u];
+                    ycur[u] = ynxt[u];
+                }
+            }
+            for (int t = Tg; t < T; ++t) step(tile_f32<F16IN>(s_x[t * TILE_D + c]), s_rcp[t], t);
+            s_err[c] = (float)(m2 / (double)T);     // var; the mean term is added below
+            s_smean[c] = (float)mean;                                // full mean, replaced below
+        }
+    } else {
+        const int c = tid - TILE_D;
+        IqCascade sa, sm;
+        sa.init(ns);
+        sm.init(ns);
+#pragma unroll 8
+        for (int r = 0; r < ns; ++r) {
+            const float v = tile_f32<F16IN>(s_x[(int)(r * a.stride) * TILE_D + c]);
+            sa.add(fabsf(v));
+            sm.add(v);
+        }
+        float amax = 0.0f;
+        bool bad = false;
+#pragma unroll 16
+        for (int t = 0; t < T; ++t) {
+            const float v = tile_f32<F16IN>(s_x[t * TILE_D + c]);
+            bad |= !iq_isfinite(v);
+            amax = fmaxf(amax, fabsf(v));
+        }
+        s_amax[c] = amax;
+        s_sal[c] = sa.finish() / (float)ns;
+        if (bad) s_bad = 1;
+        // stash the sampled mean until the Welford waves are done with s_smean
+        s_scale[c] = sm.finish() / (float)ns;
+    }
+    __syncthreads();
+    if (tid < TILE_D) {
+        const float smean = s_scale[tid];
+        if (a.min_error) {
+            const float diff = __fsub_rn(s_smean[tid], smean);
+            s_err[tid] = __fadd_rn(s_err[tid], __fmul_rn(diff, diff));
+        }
+        s_smean[tid] = smean;
+    }
+    __syncthreads();
+
+    if (tid < 64)
+        iq_select_wave_t<2>(s_sal, a.min_error ? s_err : nullptr, TILE_D, (int)a.count, s_src, s_don, s_is_src,
+                       s_src_of);
+    __syncthreads();
+
+    const float flt_min = 1.17549435e-38f;
+    if (tid < TILE_D) {
+        const float s = s_amax[tid] / (s_is_src[tid] ? 127.0f : 7.0f);
+        const float sc = s < flt_min ? flt_min : s;
+        s_scale[tid] = sc;
+        a.scales[row * TILE_D + tid] = sc;
+    }
+    if (tid < a.count) {
+        store_desc(a.src, row * a.count + tid, s_src[tid], a.desc_bytes);
+        store_desc(a.don, row * a.count + tid, s_don[tid], a.desc_bytes);
+        a.padding[row * a.count + tid] = s_smean[s_don[tid]];
+    }
+    if (tid == 0 && s_bad) atomicOr(a.bad, 1);
+    __syncthreads();
+
+    // ---- quantize: thread owns channels 8 j .. 8 j + 7 of tokens t0, t0 + 16, ...
+    const int j = tid & 15;
+    float scl[8], rscl[8], lim[8];
+    int shift[8], srcc[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        const int c = 8 * j + e;
+        const bool hi = s_is_src[c];
+        const int owner = s_src_of[c];
+        const bool lo = !hi && owner >= 0;
+        srcc[e] = lo ? owner : c;
+        scl[e] = s_scale[srcc[e]];
+        rscl[e] = __builtin_amdgcn_rcpf(scl[e]);
+        lim[e] = (hi || lo) ? 127.0f : 7.0f;
+        shift[e] = hi ? 4 : 0;
+    }
+    uint32_t *out = (uint32_t *)(a.payload + row * (int64_t)T * (TILE_D / 2));
+    for (int t = tid >> 4; t < T; t += K4_THREADS / 16) {
+        const uint16_t *xt = s_x + t * TILE_D;
+        // branch-free: every channel reads the value it encodes (its own, or
+        // for a donor slot its source's), the reciprocal quotient decides the
+        // rounding, and only a token with a near-tie quotient divides exactly
+        float v[8], q[8];
+        bool near = false;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[e] = tile_f32<F16IN>(xt[srcc[e]]);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const float f = __fmul_rn(v[e], rscl[e]);
+            q[e] = rintf(f);
+            near |= !(0.5f - fabsf(__fsub_rn(f, q[e])) > fabsf(f) * 0x1p-20f);
+        }
+        if (near) {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) q[e] = iq_rint_div(v[e], scl[e], rscl[e]);
+        }
+        uint32_t word = 0;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const float qc = fminf(fmaxf(q[e], -lim[e]), lim[e]);
+            const uint32_t code = (uint32_t)(int)(qc + lim[e] + 1.0f);
+            word |= ((code >> shift[e]) & 15u) << (4 * e);
+        }
+        out[t * (TILE_D / 8) + j] = word;
+    }
+}
+
 struct SelectArgs {
     const float *sal, *err;
     int64_t D, count;
@@ -232,6 +434,19 @@ extern "C" int iq_k4_quantize(const void *x, int x_dtype, const int64_t *x_strid
     IQ_CHECK_ARG(B * H <= 0x7fffffffLL, "iq_k4_quantize: too many rows");
     K4Args a{x, x_dtype, x_strides[0], x_strides[1], x_strides[2], x_strides[3], H, T, D, count, sample_stride,
              min_error ? 1 : 0, payload, scales, src, don, desc_bytes, padding, bad_flag};
+    const bool tile = (x_dtype == IQ_BF16 || x_dtype == IQ_F16) && D == TILE_D && T <= TILE_T &&
+                      x_strides[3] == 1 && x_strides[2] % 8 == 0 && x_strides[1] % 8 == 0 &&
+                      x_strides[0] % 8 == 0 && ((uintptr_t)x & 15) == 0;
+    if (tile) {
+        if (x_dtype == IQ_F16)
+            hipLaunchKernelGGL(k4_encode_tile<true>, dim3((unsigned)(B * H)), dim3(K4_THREADS), 0,
+                               (hipStream_t)stream, a);
+        else
+            hipLaunchKernelGGL(k4_encode_tile<false>, dim3((unsigned)(B * H)), dim3(K4_THREADS), 0,
+                               (hipStream_t)stream, a);
+        IQ_CHECK_LAUNCH("k4_encode_tile");
+        return IQ_OK;
+    }
     hipLaunchKernelGGL(k4_encode_kernel, dim3((unsigned)(B * H)), dim3(K4_THREADS), 0, (hipStream_t)stream, a);
     IQ_CHECK_LAUNCH("k4_encode_kernel");
     return IQ_OK;

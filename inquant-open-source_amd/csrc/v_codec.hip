@@ -20,31 +20,70 @@ struct VEncArgs {
     int64_t sb, sh, st, sc;
     int64_t H, T, D;
     int bits, group;
-    int64_t units;          // B*H*T*(D/group)
+    int64_t units;          // B*H*T*(D/8): eight channels of one token each
+    int vec;                // rows are channel-contiguous and 16-byte aligned
     uint8_t *payload;
     uint16_t *scales, *offsets;
     int *bad;
 };
 
-// One thread per (row, group).
+typedef __attribute__((ext_vector_type(4))) uint32_t u32x4_t;
+
+// Eight consecutive channels of x as fp32.
+__device__ __forceinline__ void v_load8(const VEncArgs &a, int64_t base, float v[8])
+{
+    if (a.vec && (a.dt == IQ_BF16 || a.dt == IQ_F16)) {
+        const u32x4_t r = *(const u32x4_t *)((const uint16_t *)a.x + base);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const uint16_t h = (uint16_t)(r[e >> 1] >> (16 * (e & 1)));
+            v[e] = a.dt == IQ_F16 ? iq_f16_to_f32(h) : iq_bf16_to_f32(h);
+        }
+    } else if (a.vec && a.dt == IQ_F32) {
+        const u32x4_t r0 = *(const u32x4_t *)((const float *)a.x + base);
+        const u32x4_t r1 = *(const u32x4_t *)((const float *)a.x + base + 4);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            v[e] = __uint_as_float(r0[e]);
+            v[4 + e] = __uint_as_float(r1[e]);
+        }
+    } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[e] = iq_load_f32(a.x, base + e * a.sc, a.dt);
+    }
+}
+
+// One thread per eight channels of one token; the group/8 lanes of a group
+// reduce min and max with cross-lane exchanges and the group's first lane
+// writes its f16 scale and offset.
 __global__ __launch_bounds__(V_THREADS) void v_encode_kernel(VEncArgs a)
 {
     const int64_t u = (int64_t)blockIdx.x * V_THREADS + threadIdx.x;
-    if (u >= a.units) return;
-    const int64_t groups = a.D / a.group;
-    const int64_t r = u / groups, g = u - r * groups;      // r = (b*H + h)*T + t
+    const bool live = u < a.units;
+    const int64_t per_row = a.D / 8;
+    const int64_t r = live ? u / per_row : 0, j = live ? u - r * per_row : 0;   // r = (b*H + h)*T + t
     const int64_t t = r % a.T, bh = r / a.T;
     const int64_t b = bh / a.H, h = bh % a.H;
-    const int64_t base = b * a.sb + h * a.sh + t * a.st + g * a.group * a.sc;
+    const int64_t base = b * a.sb + h * a.sh + t * a.st + 8 * j * a.sc;
     const int levels = (1 << a.bits) - 1;
+    const int lanes = a.group / 8;
 
-    float lo = iq_load_f32(a.x, base, a.dt), hi = lo;
+    float v[8];
+    if (live) v_load8(a, base, v);
+    else
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[e] = 0.0f;
     bool bad = false;
-    for (int j = 0; j < a.group; ++j) {
-        const float v = iq_load_f32(a.x, base + j * a.sc, a.dt);
-        bad |= !iq_isfinite(v);
-        lo = fminf(lo, v);
-        hi = fmaxf(hi, v);
+    float lo = v[0], hi = v[0];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        bad |= !iq_isfinite(v[e]);
+        lo = fminf(lo, v[e]);
+        hi = fmaxf(hi, v[e]);
+    }
+    for (int o = 1; o < lanes; o <<= 1) {
+        lo = fminf(lo, __shfl_xor(lo, o, 64));
+        hi = fmaxf(hi, __shfl_xor(hi, o, 64));
     }
     const uint16_t off_h = iq_f32_to_f16(lo);
     float s = __fsub_rn(hi, lo) / (float)levels;
@@ -53,22 +92,34 @@ __global__ __launch_bounds__(V_THREADS) void v_encode_kernel(VEncArgs a)
     const uint16_t sc_h = iq_f32_to_f16(s);
     const float off = iq_f16_to_f32(off_h), sc = iq_f16_to_f32(sc_h);
     bad |= !iq_isfinite(off) || !iq_isfinite(sc);
-    a.offsets[u] = off_h;
-    a.scales[u] = sc_h;
 
-    const int per_byte = 8 / a.bits;
-    uint8_t *out = a.payload + r * (a.D / per_byte) + g * (a.group / per_byte);
-    for (int j = 0; j < a.group; j += per_byte) {
-        uint32_t byte = 0;
-        for (int e = 0; e < per_byte; ++e) {
-            const float v = iq_load_f32(a.x, base + (j + e) * a.sc, a.dt);
-            float q = rintf(__fsub_rn(v, off) / sc);
-            q = fminf(fmaxf(q, 0.0f), (float)levels);
-            byte |= (uint32_t)q << (e * a.bits);
-        }
-        out[j / per_byte] = (uint8_t)byte;
+    const float rsc = __builtin_amdgcn_rcpf(sc);
+    float d[8], q[8];
+    bool near = false;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        d[e] = __fsub_rn(v[e], off);
+        const float f = __fmul_rn(d[e], rsc);
+        q[e] = rintf(f);
+        near |= !(0.5f - fabsf(__fsub_rn(f, q[e])) > fabsf(f) * 0x1p-20f);
     }
-    if (bad) atomicOr(a.bad, 1);
+    if (near) {            // a quotient near a rounding boundary: exact division decides
+#pragma unroll
+        for (int e = 0; e < 8; ++e) q[e] = iq_rint_div(d[e], sc, rsc);
+    }
+    uint32_t word = 0;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) word |= (uint32_t)fminf(fmaxf(q[e], 0.0f), (float)levels) << (e * a.bits);
+    if (live) {
+        if (j % lanes == 0) {
+            const int64_t gi = r * (a.D / a.group) + j / lanes;
+            a.offsets[gi] = off_h;
+            a.scales[gi] = sc_h;
+        }
+        if (a.bits == 2) ((uint16_t *)a.payload)[u] = (uint16_t)word;
+        else ((uint32_t *)a.payload)[u] = word;
+    }
+    if (__ballot(live && bad) != 0 && (threadIdx.x & 63) == 0) atomicOr(a.bad, 1);
 }
 
 struct VDecArgs {
@@ -154,10 +205,14 @@ extern "C" int iq_v_quantize(const void *x, int x_dtype, const int64_t *x_stride
     IQ_CHECK_ARG(bits == 2 || bits == 4, "iq_v_quantize: bits must be 2 or 4");
     IQ_CHECK_ARG(group == 32 || group == 64 || group == 128, "iq_v_quantize: group must be 32, 64 or 128");
     IQ_CHECK_ARG(B >= 1 && H >= 1 && T >= 1 && D >= group && D % group == 0, "iq_v_quantize: bad shape");
-    const int64_t units = B * H * T * (D / group);
+    const int64_t units = B * H * T * (D / 8);
     IQ_CHECK_ARG((units + V_THREADS - 1) / V_THREADS <= 0x7fffffffLL, "iq_v_quantize: too large");
+    const int64_t elt = x_dtype == IQ_F32 ? 4 : x_dtype == IQ_F64 ? 8 : 2;
+    const int64_t vmul = 16 / elt;         // elements per 16 bytes
+    const int vec = x_dtype != IQ_F64 && x_strides[3] == 1 && x_strides[0] % vmul == 0 &&
+                    x_strides[1] % vmul == 0 && x_strides[2] % vmul == 0 && ((uintptr_t)x & 15) == 0;
     VEncArgs a{x, x_dtype, x_strides[0], x_strides[1], x_strides[2], x_strides[3], H, T, D, bits, group, units,
-               payload, scales, offsets, bad_flag};
+               vec, payload, scales, offsets, bad_flag};
     hipLaunchKernelGGL(v_encode_kernel, dim3((unsigned)((units + V_THREADS - 1) / V_THREADS)), dim3(V_THREADS), 0,
                        (hipStream_t)stream, a);
     IQ_CHECK_LAUNCH("v_encode_kernel");

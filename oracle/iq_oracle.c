@@ -513,3 +513,40 @@ IQO_EXPORT void iqo_attend(const float *q, const float *k, const float *v, int64
         free(s);
     }
 }
+
+/*
+ * Test support for the GPU tile encoder, not part of the reference's
+ * algorithm: the Welford step's delta / n is computed on the GPU as
+ *   q0 = delta * RN(1/n);  r = fma(-q0, n, delta);  q = fma(r, RN(1/n), q0)
+ * which must equal the IEEE quotient for every n <= n_max.  Checks
+ * `samples` deltas per n drawn as differences of random floats and a
+ * running double mean (the operands the recurrence produces); returns the
+ * number of mismatches.
+ */
+int64_t iqo_check_recip_division(int64_t n_max, int64_t samples, uint64_t seed)
+{
+    int64_t bad = 0;
+    uint64_t s = seed;
+    for (int64_t n = 1; n <= n_max; ++n) {
+        const double nd = (double)n, y = 1.0 / nd;
+        for (int64_t i = 0; i < samples; ++i) {
+            s += 0x9E3779B97F4A7C15ull;
+            uint64_t z = s;
+            z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+            z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+            z ^= z >> 31;
+            /* a float of random sign, exponent in [-40, 40) and mantissa, minus a double "mean" */
+            uint32_t fb = (uint32_t)(z & 0x807fffffu) | ((uint32_t)(87 + ((z >> 32) % 80)) << 23);
+            float xf;
+            memcpy(&xf, &fb, 4);
+            double mean = (double)(int64_t)(z >> 40) * 0x1p-20 * ((z >> 39) & 1 ? 1.0 : 1e-9);
+            const double delta = (double)xf - mean;
+            const double q0 = delta * y;
+            const double r = fma(-q0, nd, delta);
+            const double q = fma(r, y, q0);
+            const double ref = delta / nd;
+            if (memcmp(&q, &ref, 8) != 0) ++bad;
+        }
+    }
+    return bad;
+}

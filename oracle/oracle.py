@@ -47,6 +47,8 @@ def lib():
         _lib.iqo_v_dequantize.argtypes = [c_p, c_p, c_p, c_i64, c_i64, ctypes.c_int, ctypes.c_int,
                                           ctypes.c_int, c_p]
         _lib.iqo_role_map.argtypes = [c_p, c_p, c_i64, c_i64, c_i64, c_p]
+        _lib.iqo_check_recip_division.argtypes = [c_i64, c_i64, ctypes.c_uint64]
+        _lib.iqo_check_recip_division.restype = c_i64
         _lib.iqo_attend.argtypes = [c_p, c_p, c_p, c_i64, c_i64, c_i64, c_i64, ctypes.c_double, c_p]
     return _lib
 
@@ -173,3 +175,9 @@ def to_bf16(x: np.ndarray) -> np.ndarray:
 
 def to_f16(x: np.ndarray) -> np.ndarray:
     return np.asarray(x, np.float32).astype(np.float16).astype(np.float32)
+
+
+def check_recip_division(n_max: int = 256, samples: int = 20000, seed: int = 1) -> int:
+    """Mismatches of the GPU tile encoder's reciprocal-and-remainder quotient
+    against IEEE division (test support, see iqo_check_recip_division)."""
+    return int(lib().iqo_check_recip_division(n_max, samples, seed))

@@ -76,6 +76,14 @@ def test_k4_blocked_strided_view_matches_golden(golden, policy):
 @pytest.mark.parametrize("D,T,stride,policy,frac,dtype", [
     (128, 256, 8, "min_error", 0.125, torch.bfloat16),
     (128, 200, 8, "neighbors", 0.125, torch.float16),
+    # LDS tile encoder (16-bit input, D = 128, T <= 256): edge lengths and counts
+    (128, 256, 8, "min_error", 0.125, torch.float16),
+    (128, 256, 16, "neighbors", 0.5, torch.bfloat16),
+    (128, 256, 1, "min_error", 0.5, torch.bfloat16),
+    (128, 255, 7, "min_error", 0.25, torch.bfloat16),
+    (128, 17, 8, "min_error", 0.0, torch.bfloat16),
+    (128, 1, 8, "min_error", 0.125, torch.float16),
+    (128, 257, 8, "min_error", 0.125, torch.bfloat16),
     (64, 77, 5, "min_error", 0.25, torch.float32),
     (130, 33, 2, "neighbors", 0.5, torch.float32),
     (258, 9, 3, "min_error", 0.5, torch.bfloat16),
@@ -180,3 +188,30 @@ def test_k4_storage_accounting():
     assert stats["source_nbytes"] == x.numel() * 2 and stats["compression_ratio"] < 4
     big = quantize(torch.randn(1, 1, 3, 258, device="cuda"), CodecConfig(salient_fraction=0.5))
     assert big.donor_channels.dtype == torch.int32 and big.donor_channels.unique().numel() == 129
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_codecs_round_half_to_even_on_exact_ties(dtype):
+    # quotients landing exactly on half-integers (and one ulp either side)
+    # must round like the IEEE division followed by rint (half to even)
+    from inquant.codec import CodecConfig, quantize
+    from inquant.value_codec import quantize_values
+    gen = np.random.default_rng(5)
+    halves = gen.integers(-14, 15, (2, 4, 256, 128)).astype(np.float32) * 0.5
+    halves[..., 0, :] = 7.0                      # amax 7 -> normal-channel scale exactly 1
+    halves[..., 9:12] *= 16                      # salient run: scale 112 / 127
+    k = _dev(halves, dtype)
+    for policy in ("neighbors", "min_error"):
+        ref = oracle.k4_quantize(_np(k.float()), 8, 0.125, policy)
+        got = quantize(k, CodecConfig(donor_policy=policy))
+        for field in ("payload", "scales", "salient_channels", "donor_channels", "padding"):
+            _same_bits(_np(got.tensors[field]).astype(ref[field].dtype), ref[field], field)
+    v = gen.integers(0, 7, (2, 4, 256, 128)).astype(np.float32) * 0.5   # groups span [0, 3]: scale 1
+    v[..., ::64] = 0.0
+    v[..., 1::64] = 3.0
+    v[1, 1, 5, 7] = np.nextafter(np.float32(1.5), np.float32(2))
+    vt = _dev(v, dtype)
+    for bits in (2, 4):
+        ref = oracle.v_quantize(_np(vt.float()), bits, 64)
+        got = quantize_values(vt, bits, 64)
+        np.testing.assert_array_equal(_np(got.payload), ref["payload"])

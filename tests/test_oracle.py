@@ -242,3 +242,9 @@ def test_attention_oracle_against_torch_sdpa_and_closed_forms():
     out = oracle.attend(q.numpy()[:2], kk, v.numpy()[:1, :50], 0.1)
     np.testing.assert_allclose(out, np.broadcast_to(v.numpy()[0, :50].astype(np.float64).mean(0), (2, 128)),
                                rtol=1e-12, atol=1e-12)
+
+
+def test_tile_encoder_quotient_identity():
+    # the GPU tile encoder's Welford step replaces delta / n by a reciprocal
+    # product with one remainder correction; it must be the IEEE quotient
+    assert oracle.check_recip_division(256, 20000, 11) == 0
