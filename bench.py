@@ -38,7 +38,37 @@ def parse():
     ap.add_argument("--blocks", type=int, default=128)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-graph", action="store_true", help="launch layer by layer instead of a HIP graph")
+    ap.add_argument("--copy-probe", action="store_true",
+                    help="only run a 1 GiB device-to-device copy (calibrates rocprofv3 FETCH_SIZE / WRITE_SIZE)")
     return ap.parse_args()
+
+
+COPY_PROBE_BYTES = 1 << 30
+TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "decode_fast_cfg2_traffic.txt")
+
+
+def copy_probe() -> None:
+    """Three copies of 1 GiB with torch's elementwise copy kernel: the known
+    byte count against which rocprofv3's FETCH_SIZE and WRITE_SIZE are scaled."""
+    import torch
+    src = torch.ones(COPY_PROBE_BYTES // 4, dtype=torch.float32, device="cuda:0")
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_probe_bytes": COPY_PROBE_BYTES, "copies": 3}))
+
+
+def measured_traffic():
+    """HBM bytes per decode_fast launch from the committed rocprofv3 summary
+    (FETCH_SIZE and WRITE_SIZE passes scaled by the copy calibration), or None."""
+    import re
+    try:
+        text = open(TRAFFIC_PROFILE).read()
+    except OSError:
+        return None
+    m = re.search(r"^traffic_bytes_per_launch\s*=\s*(\d+)", text, re.M)
+    return int(m.group(1)) if m else None
 
 
 def kv_tensor(gen, heads, tokens, device, frac_groups=(2, 2, 1), scale=20.0):
@@ -232,6 +262,9 @@ def cpu_baseline(layer):
 
 def main():
     args = parse()
+    if args.copy_probe:
+        copy_probe()
+        return
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported on this single-GPU build "
               "(the decode shards over KV heads with no exchange; see DESIGN.md)", file=sys.stderr)
@@ -271,7 +304,7 @@ def main():
         "decode_us_per_layer": round(layer_us, 3),
         "decode_tokens_per_s": round(1e3 / ms, 2),
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": measured_traffic(),
                      "kernel": "decode_fast (matrix-core decode with in-kernel partition merge; one launch per layer)",
                      "bytes_per_launch": per_layer},
         "encode_mtok_s": round(enc["encode_mtok_s"], 2),

@@ -188,22 +188,24 @@ __device__ __forceinline__ float rowsum16(float v)
     return v;
 }
 
-// Log-sum-exp merge of `count` partials of kv head h (partition p_first + k *
-// stride), in chunks of MERGE_GROUP.  Thread (g, k) = (tid / 16, tid % 16)
-// loads one partial's (m, l) and keeps the running max / denominator of row g
-// replicated over its 16 lanes; the chunk's weights go through LDS to the
-// threads that own output channels, whose sixteen independent loads per chunk
-// are all in flight together.  Writes the merged row to partition p_first,
-// or the normalized output when final_out.
-__device__ __forceinline__ void merge_partials(const FastArgs &a, int h, int G, int64_t p_first, int64_t stride, int count,
-                               bool final_out)
+// Log-sum-exp merge of `count` partials (partition p_first + k * stride) of
+// query rows g0 .. g0 + gn - 1 of kv head h (gn <= 8), in chunks of
+// MERGE_GROUP.  Every load of a chunk is issued before any of its arithmetic:
+// the accumulator values of this thread's output channels first, then the
+// (m, l) pair of partial k = tid % 16 of row g0 + tid / 16.  Row maxima and
+// denominators reduce over the 16 lanes of a row; the weights reach the
+// threads that own the channels through LDS (`sm`, 16 * MERGE_GROUP + 48
+// floats of the caller's free staging memory).  Writes the merged rows to
+// partition p_first, or the normalized output when final_out.
+template <int ITEMS>
+__device__ __forceinline__ void merge_rows(const FastArgs &a, float *sm, int h, int G, int g0, int gn,
+                                           int64_t p_first, int64_t stride, int count, bool final_out)
 {
-    constexpr int ITEMS = 16 * D / 256;
-    __shared__ float s_w[16 * MERGE_GROUP];
-    __shared__ float s_alpha[16], s_den[16], s_mx[16];
+    float *s_w = sm, *s_alpha = sm + 16 * MERGE_GROUP, *s_den = s_alpha + 16, *s_mx = s_den + 16;
     const int tid = threadIdx.x;
     const int mg = tid >> 4, mk = tid & 15;
     const int64_t pstride = stride * (D + 2);
+    const float *hbase = a.ws + ((int64_t)(h * G + g0) * a.P + p_first) * (D + 2);
     float mx = NEG_INF, den = 0.0f;
     float num[ITEMS];
 #pragma unroll
@@ -211,12 +213,18 @@ __device__ __forceinline__ void merge_partials(const FastArgs &a, int h, int G, 
 
     for (int k0 = 0; k0 < count; k0 += MERGE_GROUP) {
         const int n = min(MERGE_GROUP, count - k0);
-        float m = NEG_INF, l = 0.0f;
-        if (mg < G && mk < n) {
-            const float *r = a.ws + ((int64_t)(h * G + mg) * a.P + p_first) * (D + 2) + (k0 + mk) * pstride;
-            m = ld_agent(r + D);
-            l = ld_agent(r + D + 1);
+        float v[ITEMS][MERGE_GROUP];
+#pragma unroll
+        for (int it = 0; it < ITEMS; ++it) {
+            const int i = min(tid + 256 * it, gn * D - 1);
+            const float *r = hbase + (int64_t)(i >> 7) * a.P * (D + 2) + k0 * pstride + (i & (D - 1));
+#pragma unroll
+            for (int k = 0; k < MERGE_GROUP; ++k) v[it][k] = ld_agent(r + min(k, n - 1) * pstride);
         }
+        const bool mine = mg < gn && mk < n;
+        const float *rm = hbase + (int64_t)(mine ? mg : 0) * a.P * (D + 2) + (k0 + (mine ? mk : 0)) * pstride + D;
+        const float m0 = ld_agent(rm), l0 = ld_agent(rm + 1);
+        const float m = mine ? m0 : NEG_INF, l = mine ? l0 : 0.0f;
         const float nm = fmaxf(mx, rowmax16(m));
         const float alpha = mx == nm ? 1.0f : __expf(mx - nm);
         const float w = m == NEG_INF ? 0.0f : __expf(m - nm);
@@ -227,21 +235,15 @@ __device__ __forceinline__ void merge_partials(const FastArgs &a, int h, int G, 
         __syncthreads();
 #pragma unroll
         for (int it = 0; it < ITEMS; ++it) {
-            const int i = tid + 256 * it;
-            if (i >= G * D) continue;
-            const int g = i >> 7, c = i & (D - 1);
-            const float *r = a.ws + ((int64_t)(h * G + g) * a.P + p_first) * (D + 2) + k0 * pstride + c;
-            float v[MERGE_GROUP];
-#pragma unroll
-            for (int k = 0; k < MERGE_GROUP; ++k) v[k] = ld_agent(r + min(k, n - 1) * pstride);
+            const int g = min(tid + 256 * it, gn * D - 1) >> 7;
             float acc = num[it] * s_alpha[g];
 #pragma unroll
-            for (int k = 0; k < MERGE_GROUP; ++k) acc = fmaf(v[k], s_w[g * MERGE_GROUP + k], acc);
+            for (int k = 0; k < MERGE_GROUP; ++k) acc = fmaf(v[it][k], s_w[g * MERGE_GROUP + k], acc);
             num[it] = acc;
         }
         __syncthreads();
     }
-    if (mk == 0 && mg < G) {
+    if (mk == 0 && mg < gn) {
         s_den[mg] = den;
         s_mx[mg] = mx;
     }
@@ -249,12 +251,12 @@ __device__ __forceinline__ void merge_partials(const FastArgs &a, int h, int G, 
 #pragma unroll
     for (int it = 0; it < ITEMS; ++it) {
         const int i = tid + 256 * it;
-        if (i >= G * D) continue;
+        if (i >= gn * D) continue;
         const int g = i >> 7, c = i & (D - 1);
         if (final_out) {
-            iq_store_as(a.out, (int64_t)(h * G + g) * D + c, num[it] / s_den[g], a.odt);
+            iq_store_as(a.out, (int64_t)(h * G + g0 + g) * D + c, num[it] / s_den[g], a.odt);
         } else {
-            float *row = a.ws + ((int64_t)(h * G + g) * a.P + p_first) * (D + 2);
+            float *row = a.ws + ((int64_t)(h * G + g0 + g) * a.P + p_first) * (D + 2);
             st_agent(row + c, num[it]);
             if (c == 0) {
                 st_agent(row + D, s_mx[g]);
@@ -262,6 +264,17 @@ __device__ __forceinline__ void merge_partials(const FastArgs &a, int h, int G, 
             }
         }
     }
+    __syncthreads();
+}
+
+__device__ __forceinline__ void merge_partials(const FastArgs &a, float *sm, int h, int G, int64_t p_first,
+                                               int64_t stride, int count, bool final_out)
+{
+    if (G <= 2) merge_rows<1>(a, sm, h, G, 0, G, p_first, stride, count, final_out);
+    else if (G <= 4) merge_rows<2>(a, sm, h, G, 0, G, p_first, stride, count, final_out);
+    else
+        for (int g0 = 0; g0 < G; g0 += 8)
+            merge_rows<4>(a, sm, h, G, g0, min(8, G - g0), p_first, stride, count, final_out);
 }
 
 template <bool F16, int VBITS>
@@ -422,7 +435,8 @@ __global__ __launch_bounds__(256, 3) void decode_fast(FastArgs a)
 
     uint32_t *vt = s_v[wave];
 
-    for (; base < stop; base += CHUNK * WAVES) {
+    // one pass: a partition holds at most CHUNK * WAVES tokens
+    if (base < stop) {
         const bool full = base + CHUNK <= stop;
         // ---------------- logits S^T[token, g] for four 16-token tiles
         f32x4 sc[4];
@@ -656,8 +670,6 @@ __global__ __launch_bounds__(256, 3) void decode_fast(FastArgs a)
                 acc[n] = mma32<F16>(va, plo[m], acc[n]);
             }
         }
-        // blocks longer than one pass load their next chunk here
-        if (packed && base + CHUNK * WAVES < stop) IQ_LOAD_CHUNK(base + CHUNK * WAVES);
     }
 #undef IQ_LOAD_CHUNK
 
@@ -702,16 +714,17 @@ __global__ __launch_bounds__(256, 3) void decode_fast(FastArgs a)
     // ---------------- last-arriving workgroups merge: first per group of
     // MERGE_GROUP partitions (into the group's first slot), then per KV head
     __shared__ int s_last;
+    float *sm = (float *)s_v[0];           // free once every wave is past its combine reads
     const int grp = (int)(p / MERGE_GROUP);
     const int gsize = (int)min((int64_t)MERGE_GROUP, a.P - (int64_t)grp * MERGE_GROUP);
     int *cnt = a.cnt + h * (a.ngrp + 1);
     if (!arrive_last(cnt + grp, gsize, &s_last)) return;
     if (tid == 0) __hip_atomic_store(cnt + grp, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    merge_partials(a, h, G, (int64_t)grp * MERGE_GROUP, 1, gsize, a.ngrp == 1);
+    merge_partials(a, sm, h, G, (int64_t)grp * MERGE_GROUP, 1, gsize, a.ngrp == 1);
     if (a.ngrp == 1) return;
     if (!arrive_last(cnt + a.ngrp, a.ngrp, &s_last)) return;
     if (tid == 0) __hip_atomic_store(cnt + a.ngrp, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    merge_partials(a, h, G, 0, MERGE_GROUP, a.ngrp, true);
+    merge_partials(a, sm, h, G, 0, MERGE_GROUP, a.ngrp, true);
 }
 
 }  // namespace
@@ -736,6 +749,7 @@ int iq_decode_fast_launch(const void *q, int q_dtype, int64_t q_stride_h, int64_
     if (out_dtype != IQ_F32 && out_dtype != IQ_BF16 && out_dtype != IQ_F16) return IQ_ERR_UNSUPPORTED;
     if (n_blocks > 0 && value_bits != 2 && value_bits != 4) return IQ_ERR_UNSUPPORTED;
     if (Hq / H > 16 || S > 64) return IQ_ERR_UNSUPPORTED;
+    if (n_blocks > 0 && block_tokens > CHUNK * WAVES) return IQ_ERR_UNSUPPORTED;   // one pass per workgroup
     // query, dense rows and packed rows are read as 16-byte vectors
     auto aligned = [](const void *ptr, int64_t sh, int64_t st) {
         return ((uintptr_t)ptr % 16 == 0) && (sh % 8 == 0) && (st % 8 == 0);
