@@ -29,6 +29,7 @@
  *                       (_attention_partials :67-165 + _reduce_partials :168-181)
  *   iq_write_pages      extensions/vllm/src/inquant_vllm/packing.py:41-55 write_codec_pages
  *                       (+ the role-map part of layout.py:66-81 pack_pages)
+ *   iq_unpack_pages     extensions/vllm/src/inquant_vllm/layout.py:84-100 unpack_pages_reference
  *   iq_paged_decode     extensions/vllm/src/inquant_vllm/kernels.py:66-88 paged_decode
  */
 #ifndef INQUANT_HIP_H
@@ -160,6 +161,66 @@ int iq_decode_attention(const void *q, int q_dtype, int64_t q_stride_h, int64_t 
                         float scale, float *workspace, int64_t workspace_floats,
                         int *merge_counters, int64_t merge_counter_ints,
                         void *out, int out_dtype, void *stream);
+
+/*
+ * ---------------------------------------------------------------- paged cache
+ * Page layout of the vLLM plugin (extensions/vllm/src/inquant_vllm/layout.py:8-53),
+ * field-major per page, B tokens per page, H KV heads, D = 128, 16 salient channels:
+ *   key_payload u8 [H,B,64] | key_scales f32 [H,128] | key_map i16 [H,128] |
+ *   key_padding f32 [H,16] | value_payload u8 [H,B,32] | value_scales f16 [H,B,2] |
+ *   value_offsets f16 [H,B,2];  page bytes = H * (104 B + 832).
+ * key_map: -1 normal, the donor channel for a source, -2 - j for donor j.
+ * B in {64, 128, 256} as in the reference, plus 16 and 32.
+ */
+int64_t iq_page_bytes(int64_t H, int64_t block_tokens);
+
+/*
+ * Scatter n_pages encoded pages into the pool by physical id (ids i32 or i64
+ * per id_bytes; ids outside [0, pool_pages) are skipped).  Inputs are the
+ * codec outputs of [n, H, B, 128] K (K4, 16 salient channels) and V (V2, group 64):
+ * k_payload [n,H,B,64], k_scales [n,H,128], k_padding [n,H,16], k_src/k_don
+ * [n,H,16] of desc_bytes, v_payload [n,H,B,32], v_scales/v_offsets f16 [n,H,B,2].
+ * Replaces write_codec_pages (packing.py:7-55) and the field copies and role map
+ * of pack_pages (layout.py:56-81).
+ */
+int iq_write_pages(const uint8_t *k_payload, const float *k_scales, const float *k_padding,
+                   const void *k_src, const void *k_don, int desc_bytes, const uint8_t *v_payload,
+                   const uint16_t *v_scales, const uint16_t *v_offsets, int64_t n_pages, int64_t H,
+                   int64_t block_tokens, uint8_t *pool, int64_t pool_pages, const void *page_ids,
+                   int id_bytes, void *stream);
+
+/*
+ * Decode n_pages contiguous pages to keys/values [n, H, B, 128] of out_dtype.
+ * Replaces unpack_pages_reference (layout.py:84-100).
+ */
+int iq_unpack_pages(const uint8_t *pages, int64_t n_pages, int64_t H, int64_t block_tokens, void *keys,
+                    void *values, int out_dtype, void *stream);
+
+/* fp32 workspace elements iq_paged_decode needs: [n_seq, Hq, partitions, 130]. */
+int64_t iq_paged_workspace_floats(int64_t Hq, int64_t n_seq, int64_t max_pages, int64_t block_tokens);
+
+/*
+ * Fused single-query decode over paged K4/V2 history plus a dense BF16 buffer,
+ * for n_seq sequences in one launch.
+ *   q bf16 [n_seq, Hq, 128] (element strides q_stride_seq, q_stride_h);
+ *   block_tables i32 [n_seq, bt_stride] of physical page ids (ids outside the
+ *   pool contribute nothing); max_pages bounds every sequence's page count;
+ *   seq_info i32 [n_seq, 3] = (pages, tail tokens, sink tokens) on the device,
+ *   or NULL with n_seq == 1 and the host values n_pages, tail_t, sink_t;
+ *   dense bf16 [n_seq, 2, H, B + 4, 128] (stride dense_stride_seq elements):
+ *   slots 0..3 the sink, 4.. the current partial page (kernels.py:37-48 masks:
+ *   packed tokens before the sink length and tail slots inside the sink are skipped);
+ *   out [n_seq, Hq, 128] (stride out_stride_seq) of out_dtype.
+ * Keys/values are decoded and rounded to bf16 as dequantize-then-attend does;
+ * logits, softmax and P.V accumulate in fp32.  Replaces paged_decode
+ * (kernels.py:66-88, _paged_partials :8-63, which handles one sequence per launch).
+ */
+int iq_paged_decode(const void *q, int64_t q_stride_seq, int64_t q_stride_h, int64_t Hq, int64_t n_seq,
+                    const uint8_t *pool, int64_t pool_pages, int64_t H, int64_t block_tokens,
+                    const int32_t *block_tables, int64_t bt_stride, int64_t max_pages,
+                    const int32_t *seq_info, int64_t n_pages, int64_t tail_t, int64_t sink_t,
+                    const void *dense, int64_t dense_stride_seq, float scale, float *workspace,
+                    int64_t workspace_floats, void *out, int64_t out_stride_seq, int out_dtype, void *stream);
 
 #ifdef __cplusplus
 }

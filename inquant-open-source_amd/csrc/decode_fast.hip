@@ -23,20 +23,9 @@
 //     the P.V product keeps ~16 significant bits of the weights.
 //   * V half-rows decode with the same fp8 trick into a 32-row LDS tile that
 //     is read back transposed as the A operand of O^T = V^T P^T.
-#include "iq_common.h"
+#include "decode_common.h"
 
 namespace {
-
-typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8;
-typedef __attribute__((ext_vector_type(8))) _Float16 f16x8;
-typedef __attribute__((ext_vector_type(4))) short s16x4;
-typedef __attribute__((ext_vector_type(4))) _Float16 f16x4;
-typedef __attribute__((ext_vector_type(2))) __bf16 bf16x2;
-typedef __attribute__((ext_vector_type(2))) _Float16 f16x2;
-typedef __attribute__((ext_vector_type(4))) float f32x4;
-typedef __attribute__((ext_vector_type(2))) float f32x2;
-typedef __attribute__((ext_vector_type(4))) uint32_t u32x4;
-typedef __attribute__((ext_vector_type(2))) uint32_t u32x2;
 
 constexpr int D = 128;
 constexpr int WAVES = 4;
@@ -68,125 +57,6 @@ struct FastArgs {
     void *out;       // final [Hq, 128] output when merged in this kernel
     int odt;
 };
-
-template <bool F16>
-__device__ __forceinline__ uint32_t pack2(float a, float b)
-{
-    if constexpr (F16) {
-        f16x2 v = {(_Float16)a, (_Float16)b};
-        return __builtin_bit_cast(uint32_t, v);
-    } else {
-        bf16x2 v = {(__bf16)a, (__bf16)b};
-        return __builtin_bit_cast(uint32_t, v);
-    }
-}
-
-template <bool F16>
-__device__ __forceinline__ float to_f32(uint32_t h16)
-{
-    if constexpr (F16) return (float)__builtin_bit_cast(_Float16, (uint16_t)h16);
-    else return __uint_as_float(h16 << 16);
-}
-
-template <bool F16>
-__device__ __forceinline__ float round_q(float v)
-{
-    return to_f32<F16>(pack2<F16>(v, 0.0f) & 0xffffu);
-}
-
-template <bool F16>
-__device__ __forceinline__ f32x4 mma32(u32x4 a, u32x4 b, f32x4 c)
-{
-    if constexpr (F16)
-        return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c,
-                                                      0, 0, 0);
-    else
-        return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b),
-                                                       c, 0, 0, 0);
-}
-
-template <bool F16>
-__device__ __forceinline__ f32x4 mma16(u32x2 a, u32x2 b, f32x4 c)
-{
-    if constexpr (F16)
-        return __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(f16x4, a), __builtin_bit_cast(f16x4, b), c,
-                                                     0, 0, 0);
-    else
-        return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(s16x4, a), __builtin_bit_cast(s16x4, b),
-                                                        c, 0, 0, 0);
-}
-
-template <bool HI>
-__device__ __forceinline__ f32x2 fp8x2(uint32_t bytes) { return __builtin_amdgcn_cvt_pk_f32_fp8(bytes, HI); }
-
-__device__ __forceinline__ float xmax16(float v)
-{
-    v = fmaxf(v, __shfl_xor(v, 16, 64));
-    return fmaxf(v, __shfl_xor(v, 32, 64));
-}
-
-__device__ __forceinline__ float xsum16(float v)
-{
-    v += __shfl_xor(v, 16, 64);
-    return v + __shfl_xor(v, 32, 64);
-}
-
-// Loads through global-address-space pointers: the pointer table holds plain
-// addresses, which would otherwise be dereferenced with flat instructions
-// that every LDS wait must also drain.
-template <class T>
-__device__ __forceinline__ T ldg(const void *p)
-{
-    return *(const __attribute__((address_space(1))) T *)p;
-}
-
-__device__ __forceinline__ u32x4 ld16(const void *p) { return ldg<u32x4>(p); }
-
-// Partials exchanged between workgroups use agent-coherent stores and loads
-// (sc1: written through / read past the per-XCD L2), so publishing them costs
-// a wait for store completion instead of an L2 write-back fence.
-__device__ __forceinline__ void st_agent(float *p, float v)
-{
-    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-__device__ __forceinline__ float ld_agent(const float *p)
-{
-    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-// Returns true in the workgroup whose arrival completes `expected` arrivals.
-// Every thread's agent-coherent stores have completed before the increment.
-__device__ __forceinline__ bool arrive_last(int *counter, int expected, int *flag)
-{
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
-    if (threadIdx.x == 0)
-        *flag = __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == expected - 1;
-    __syncthreads();
-    return *flag;
-}
-
-constexpr float NEG_INF = -__builtin_inff();
-
-// Log-sum-exp merge of `count` partitions (p_first, p_first + stride, ...) of
-// the G query rows of KV head h.  Results go to the partial slot p_first, or
-// to the final output when `final_out`.  All reads finish before any write
-// (the destination slot is also a source).
-// Reduction over the 16 consecutive lanes that share one query row.
-__device__ __forceinline__ float rowmax16(float v)
-{
-#pragma unroll
-    for (int o = 1; o < 16; o <<= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
-    return v;
-}
-
-__device__ __forceinline__ float rowsum16(float v)
-{
-#pragma unroll
-    for (int o = 1; o < 16; o <<= 1) v += __shfl_xor(v, o, 64);
-    return v;
-}
 
 // Log-sum-exp merge of `count` partials (partition p_first + k * stride) of
 // query rows g0 .. g0 + gn - 1 of kv head h (gn <= 8), in chunks of

@@ -1,0 +1,763 @@
+// Paged packed-KV cache in the vLLM plugin's page layout (gfx950).
+//
+// Page format (extensions/vllm/src/inquant_vllm/layout.py:8-53), field-major
+// within one page of H * (104 B + 832) bytes, B tokens per page, D = 128:
+//   key_payload u8 [H, B, 64] | key_scales f32 [H, 128] | key_map i16 [H, 128]
+//   | key_padding f32 [H, 16] | value_payload u8 [H, B, 32]
+//   | value_scales f16 [H, B, 2] | value_offsets f16 [H, B, 2]
+// key_map: -1 normal, the donor channel for a source, -2 - j for donor j.
+//
+// Kernels:
+//   write_pages_kernel   codec outputs -> physical pages by id
+//                        (packing.py:7-55 and the role map of layout.py:66-81)
+//   unpack_pages_kernel  pages -> dense K/V of any dtype (layout.py:84-100)
+//   decode_paged         fused single-query decode over a block table,
+//                        batched over sequences (kernels.py:8-88)
+//   paged_reduce         log-sum-exp merge of the per-partition partials
+//
+// decode_paged follows decode_fast: every load of a workgroup is issued up
+// front, Q.K runs on matrix cores with the K tile decoded exactly in
+// registers, salient codes are gathered into an extra 16x16x16 MFMA, the
+// online softmax runs in the log2 domain and P.V uses hi + lo weights.  Pages
+// shorter than a partition get their own per-channel constants: the
+// salient/donor channels of a page decode to zero through a zero scale
+// (instead of a masked query), and the donor padding enters as a per-page
+// bias on the logits.
+#include "decode_common.h"
+
+namespace {
+
+constexpr int D = 128;
+constexpr int WAVES = 4;
+constexpr int PART = 256;              // tokens per partition
+constexpr int VR = 136;                // dwords per staged token-pair row of decoded V
+constexpr int KROW = 17;               // dwords per staged K row (salient byte gathers)
+constexpr int KG = 36;                 // floats per 32-channel group of page scales (+4: no bank overlap)
+constexpr int SPG = 16;                // salient channels per page (the layout's key_padding width)
+constexpr float LN2 = 0.693147180559945309f;
+
+struct PageOffsets {
+    int64_t ks, km, kp, vp, vs, vo;    // byte offsets of the fields after key_payload
+};
+
+__host__ __device__ inline PageOffsets page_offsets(int64_t H, int64_t B)
+{
+    PageOffsets o;
+    o.ks = H * B * 64;
+    o.km = o.ks + H * D * 4;
+    o.kp = o.km + H * D * 2;
+    o.vp = o.kp + H * SPG * 4;
+    o.vs = o.vp + H * B * 32;
+    o.vo = o.vs + H * B * 4;
+    return o;
+}
+
+__device__ __forceinline__ int load_index(const void *p, int64_t i, int bytes)
+{
+    if (bytes == 1) return ((const uint8_t *)p)[i];
+    if (bytes == 4) return ((const int32_t *)p)[i];
+    return (int)((const int64_t *)p)[i];
+}
+
+__device__ __forceinline__ int64_t load_id(const void *p, int64_t i, int bytes)
+{
+    return bytes == 4 ? (int64_t)((const int32_t *)p)[i] : ((const int64_t *)p)[i];
+}
+
+// ------------------------------------------------------------------ writer
+
+struct WriteArgs {
+    const uint8_t *kp;                 // [n, H, B, 64]
+    const float *ks;                   // [n, H, 128]
+    const float *kpad;                 // [n, H, 16]
+    const void *src, *don;             // [n, H, 16]
+    int desc_bytes;
+    const uint8_t *vp;                 // [n, H, B, 32]
+    const uint16_t *vs, *vo;           // [n, H, B, 2]
+    int64_t H, B, page_bytes, pool_pages;
+    uint8_t *pool;
+    const void *ids;
+    int id_bytes;
+    PageOffsets off;
+};
+
+// grid (n, H): one workgroup copies one (page, head) slice with 16-byte
+// stores and builds its role map.  Ids outside the pool are skipped.
+__global__ __launch_bounds__(256) void write_pages_kernel(WriteArgs a)
+{
+    __shared__ int16_t s_role[D];
+    const int64_t n = blockIdx.x, h = blockIdx.y;
+    const int tid = threadIdx.x;
+    const int64_t id = load_id(a.ids, n, a.id_bytes);
+    if (id < 0 || id >= a.pool_pages) return;
+    uint8_t *page = a.pool + id * a.page_bytes;
+    const int64_t nh = n * a.H + h;
+    typedef __attribute__((ext_vector_type(4))) uint32_t v4;
+    const v4 *ksrc = (const v4 *)(a.kp + nh * a.B * 64);
+    v4 *kdst = (v4 *)(page + h * a.B * 64);
+    for (int64_t i = tid; i < a.B * 4; i += 256) kdst[i] = ksrc[i];
+    const v4 *vsrc = (const v4 *)(a.vp + nh * a.B * 32);
+    v4 *vdst = (v4 *)(page + a.off.vp + h * a.B * 32);
+    for (int64_t i = tid; i < a.B * 2; i += 256) vdst[i] = vsrc[i];
+    uint16_t *vs = (uint16_t *)(page + a.off.vs) + h * a.B * 2;
+    uint16_t *vo = (uint16_t *)(page + a.off.vo) + h * a.B * 2;
+    for (int64_t i = tid; i < a.B * 2; i += 256) {
+        vs[i] = a.vs[nh * a.B * 2 + i];
+        vo[i] = a.vo[nh * a.B * 2 + i];
+    }
+    if (tid < D) {
+        ((float *)(page + a.off.ks))[h * D + tid] = a.ks[nh * D + tid];
+        s_role[tid] = -1;
+    }
+    if (tid < SPG) ((float *)(page + a.off.kp))[h * SPG + tid] = a.kpad[nh * SPG + tid];
+    __syncthreads();
+    if (tid < SPG) {
+        const int s = load_index(a.src, nh * SPG + tid, a.desc_bytes);
+        const int d = load_index(a.don, nh * SPG + tid, a.desc_bytes);
+        if (s >= 0 && s < D) s_role[s] = (int16_t)d;
+    }
+    __syncthreads();
+    if (tid < SPG) {
+        const int d = load_index(a.don, nh * SPG + tid, a.desc_bytes);
+        if (d >= 0 && d < D) s_role[d] = (int16_t)(-2 - tid);
+    }
+    __syncthreads();
+    if (tid < D) ((int16_t *)(page + a.off.km))[h * D + tid] = s_role[tid];
+}
+
+// ------------------------------------------------------------------ unpack
+
+struct UnpackArgs {
+    const uint8_t *pages;              // [n, page_bytes] contiguous
+    int64_t H, B, page_bytes;
+    PageOffsets off;
+    void *k, *v;                       // [n, H, B, 128] of out_dt
+    int out_dt;
+};
+
+// grid (n * H, B): one workgroup decodes one token of one (page, head).
+__global__ __launch_bounds__(128) void unpack_pages_kernel(UnpackArgs a)
+{
+    const int64_t nh = blockIdx.x, t = blockIdx.y;
+    const int64_t n = nh / a.H, h = nh % a.H;
+    const int c = threadIdx.x;
+    const uint8_t *page = a.pages + n * a.page_bytes;
+    const uint8_t *row = page + (h * a.B + t) * 64;
+    const int16_t role = ((const int16_t *)(page + a.off.km))[h * D + c];
+    const float scale = ((const float *)(page + a.off.ks))[h * D + c];
+    const int slot = (row[c >> 1] >> ((c & 1) * 4)) & 15;
+    float kv;
+    if (role >= 0 && role < D) {
+        const int lo = (row[role >> 1] >> ((role & 1) * 4)) & 15;
+        kv = __fmul_rn((float)(((slot << 4) | lo) - 128), scale);
+    } else if (role <= -2 && role >= -2 - (SPG - 1)) {
+        kv = ((const float *)(page + a.off.kp))[h * SPG + (-2 - role)];
+    } else {
+        kv = __fmul_rn((float)(slot - 8), scale);
+    }
+    const int64_t o = (nh * a.B + t) * D + c;
+    iq_store_as(a.k, o, kv, a.out_dt);
+    const uint8_t vb = page[a.off.vp + (h * a.B + t) * 32 + (c >> 2)];
+    const int code = (vb >> (2 * (c & 3))) & 3;
+    const int64_t pi = (h * a.B + t) * 2 + (c >> 6);
+    const float sc = iq_f16_to_f32(((const uint16_t *)(page + a.off.vs))[pi]);
+    const float of = iq_f16_to_f32(((const uint16_t *)(page + a.off.vo))[pi]);
+    iq_store_as(a.v, o, __fadd_rn(__fmul_rn((float)code, sc), of), a.out_dt);
+}
+
+// ------------------------------------------------------------------ decode
+
+struct PagedArgs {
+    const uint16_t *q;                 // [seq, Hq, 128] bf16 (element strides below)
+    int64_t q_ss, q_sh;
+    int G, H, B;
+    const uint8_t *pool;
+    int64_t page_bytes, pool_pages;
+    PageOffsets off;
+    const int32_t *bt;                 // block tables [seq, bt_ss]
+    int64_t bt_ss, max_pages;
+    const int32_t *seq_info;           // [seq, 3] (pages, tail, sink) or null
+    int npg0, tail0, sink0;            // used when seq_info is null
+    const uint16_t *dense;             // [seq, 2, H, B + 4, 128] bf16
+    int64_t dense_ss;
+    int max_parts;
+    float c_log2;                      // softmax scale * log2(e)
+    float *ws;                         // [seq, Hq, max_parts, 130]
+};
+
+struct SeqGeom {
+    int npg, tail, sink, npp, ndp;
+};
+
+__device__ __forceinline__ SeqGeom seq_geom(const PagedArgs &a, int s)
+{
+    SeqGeom g;
+    if (a.seq_info) {
+        g.npg = a.seq_info[3 * s];
+        g.tail = a.seq_info[3 * s + 1];
+        g.sink = a.seq_info[3 * s + 2];
+    } else {
+        g.npg = a.npg0;
+        g.tail = a.tail0;
+        g.sink = a.sink0;
+    }
+    g.npg = max(0, min(g.npg, (int)a.max_pages));
+    g.tail = max(0, min(g.tail, a.B));
+    g.sink = max(0, min(g.sink, 4));
+    g.npp = (g.npg * a.B + PART - 1) / PART;
+    g.ndp = (a.B + 4 + PART - 1) / PART;
+    return g;
+}
+
+// One workgroup per (KV head, partition, sequence); NPG = pages per packed
+// partition (PART / B).
+template <int NPG>
+__global__ __launch_bounds__(256, 2) void decode_paged(PagedArgs a)
+{
+    constexpr int B = PART / NPG;
+    constexpr int VQW = 2;                       // dwords per 32-channel quarter of a V2 row
+
+    __shared__ __attribute__((aligned(16))) uint32_t s_v[WAVES][16 * VR];
+    __shared__ __attribute__((aligned(16))) uint16_t s_q[16 * D];
+    __shared__ __attribute__((aligned(16))) float s_ka[NPG][4 * KG];      // s * 2^9, zero at salient/donor channels
+    __shared__ __attribute__((aligned(16))) uint32_t s_salw[NPG][SPG];   // gather offsets per page
+    __shared__ __attribute__((aligned(16))) f32x2 s_salf[NPG][SPG];      // (s_src, -128 s_src)
+    __shared__ __attribute__((aligned(16))) uint16_t s_qsal[NPG][16 * SPG];
+    __shared__ float s_bias[NPG][16];                                    // sum_k q[g][don_k] * round(pad_k)
+    __shared__ int16_t s_src[NPG][SPG], s_don[NPG][SPG];
+    __shared__ float s_ssc[NPG][SPG], s_pad[NPG][SPG];
+    __shared__ uint64_t s_page[NPG];
+    __shared__ int s_pok[NPG];
+    __shared__ float s_wm[WAVES][16], s_wl[WAVES][16];
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int gl = lane & 15, ql = lane >> 4;
+    const int pl = lane >> 2, qq = lane & 3;
+    const int h = blockIdx.x, p = blockIdx.y, sq = blockIdx.z;
+    const int G = a.G;
+    const SeqGeom geo = seq_geom(a, sq);
+    if (p >= geo.npp + geo.ndp) return;
+    const bool packed = p < geo.npp;
+    const float unit = fp8x2<false>(1u).x;       // fp8 byte 1 == 2^-9
+    const float inv_unit = 1.0f / unit;
+
+    // ---------------- geometry
+    int ntok, tok0 = 0, slot0 = 0;
+    const uint16_t *dk = nullptr, *dv = nullptr;
+    if (packed) {
+        tok0 = p * PART;
+        ntok = min(PART, geo.npg * B - tok0);
+    } else {
+        slot0 = (p - geo.npp) * PART;
+        ntok = min(PART, B + 4 - slot0);
+        const uint16_t *dn = a.dense + sq * a.dense_ss;
+        dk = dn + ((int64_t)h * (B + 4) + slot0) * D;
+        dv = dn + ((int64_t)(a.H + h) * (B + 4) + slot0) * D;
+    }
+    const int npg_here = packed ? (ntok + B - 1) / B : 0;
+
+    // ---------------- query rows; page addresses and per-page constants
+    const int qg = tid >> 4, qc = (tid & 15) * 8;
+    const u32x4 qraw = qg < G ? ld16(a.q + sq * a.q_ss + (int64_t)(h * G + qg) * a.q_sh + qc)
+                              : u32x4{0u, 0u, 0u, 0u};
+    *(u32x4 *)(s_q + qg * D + qc) = qraw;
+    if (tid < npg_here) {
+        const int64_t id = a.bt[sq * a.bt_ss + (int64_t)p * NPG + tid];
+        const bool ok = id >= 0 && id < a.pool_pages;
+        s_page[tid] = (uint64_t)(a.pool + (ok ? id : 0) * a.page_bytes);
+        s_pok[tid] = ok;
+    }
+    if (tid < NPG * SPG) {
+        (&s_src[0][0])[tid] = 0;
+        (&s_don[0][0])[tid] = 0;
+        (&s_ssc[0][0])[tid] = 0.0f;
+        (&s_pad[0][0])[tid] = 0.0f;
+    }
+    __syncthreads();
+    for (int i = tid; i < npg_here * D; i += 256) {
+        const int lp = i >> 7, c = i & (D - 1);
+        const uint8_t *page = (const uint8_t *)s_page[lp];
+        const float sc = ldg<float>(page + a.off.ks + ((int64_t)h * D + c) * 4);
+        const int role = ldg<int16_t>(page + a.off.km + ((int64_t)h * D + c) * 2);
+        s_ka[lp][(c >> 5) * KG + (c & 31)] = role == -1 ? sc * inv_unit : 0.0f;
+        if (role >= 0 && role < D) {                    // source: its donor's descriptor index
+            const int j = -2 - (int)ldg<int16_t>(page + a.off.km + ((int64_t)h * D + role) * 2);
+            if (j >= 0 && j < SPG) {
+                s_src[lp][j] = (int16_t)c;
+                s_ssc[lp][j] = sc;
+            }
+        } else if (role <= -2 && role >= -2 - (SPG - 1)) {  // donor j
+            const int j = -2 - role;
+            s_don[lp][j] = (int16_t)c;
+            s_pad[lp][j] = round_q<false>(ldg<float>(page + a.off.kp + ((int64_t)h * SPG + j) * 4));
+        }
+    }
+
+    // ---------------- every global load of this wavefront's 64 tokens
+    const int base = 64 * wave;
+    u32x4 kw[4];
+    uint32_t vw[2][2][VQW];
+    uint16_t vp[2][2][2];
+    if (packed && base < ntok) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int t = min(base + 16 * j + gl, ntok - 1);
+            const uint8_t *page = (const uint8_t *)s_page[t / B];
+            kw[j] = ld16(page + ((int64_t)h * B + t % B) * 64 + 16 * ql);
+        }
+#pragma unroll
+        for (int m = 0; m < 2; ++m)
+#pragma unroll
+            for (int u = 0; u < 2; ++u) {
+                const int t = min(base + 32 * m + 2 * pl + u, ntok - 1);
+                const uint8_t *page = (const uint8_t *)s_page[t / B];
+                const int64_t r = (int64_t)h * B + t % B;
+                const u32x2 w = ldg<u32x2>(page + a.off.vp + r * 32 + 8 * qq);
+                vw[m][u][0] = w[0];
+                vw[m][u][1] = w[1];
+                vp[m][u][0] = ldg<uint16_t>(page + a.off.vs + (r * 2 + (qq >> 1)) * 2);
+                vp[m][u][1] = ldg<uint16_t>(page + a.off.vo + (r * 2 + (qq >> 1)) * 2);
+            }
+    }
+    __syncthreads();
+
+    // ---------------- per-page salient tables and donor bias
+    for (int i = tid; i < npg_here * SPG; i += 256) {
+        const int lp = i / SPG, k = i % SPG;
+        const uint32_t src = (uint32_t)s_src[lp][k], don = (uint32_t)s_don[lp][k];
+        s_salw[lp][k] = (src >> 1) | (((src & 1) * 4) << 8) | ((don >> 1) << 16) | (((don & 1) * 4) << 24);
+        const float ssc = s_ssc[lp][k];
+        s_salf[lp][k] = f32x2{ssc, -128.0f * ssc};
+    }
+    for (int i = tid; i < npg_here * 16; i += 256) {
+        const int lp = i >> 4, g = i & 15;
+        float b = 0.0f;
+        for (int k = 0; k < SPG; ++k) b = fmaf(to_f32<false>(s_q[g * D + s_don[lp][k]]), s_pad[lp][k], b);
+        s_bias[lp][g] = b;
+    }
+    for (int i = tid; i < npg_here * 16 * SPG; i += 256) {
+        const int lp = i / (16 * SPG), r = i % (16 * SPG), g = r / SPG, k = r % SPG;
+        s_qsal[lp][g * SPG + k] = s_q[g * D + s_src[lp][k]];
+    }
+    __syncthreads();
+
+    u32x4 qb[4];                                   // B operand: Q[g = gl][32 ql + 8 d + e]
+#pragma unroll
+    for (int d = 0; d < 4; ++d) qb[d] = *(const u32x4 *)(s_q + gl * D + 32 * ql + 8 * d);
+
+    float m_run = NEG_INF, l_run = 0.0f;
+    f32x4 acc[8];
+#pragma unroll
+    for (int n = 0; n < 8; ++n) acc[n] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    uint32_t *vt = s_v[wave];
+
+    if (base < ntok) {
+        // a token is live when it exists in this partition and (packed) lies
+        // past the sink, or (dense) is a sink slot or a tail slot whose
+        // position is past the sink (kernels.py:37,48)
+        auto live = [&](int t) -> bool {
+            if (t >= ntok) return false;
+            if (packed) return s_pok[t / B] && tok0 + t >= geo.sink;
+            const int slot = slot0 + t;
+            return slot < geo.sink || (slot >= 4 && slot < 4 + geo.tail && geo.npg * B + slot - 4 >= geo.sink);
+        };
+        f32x4 sc[4];
+        if (packed) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int lp = (base + 16 * j) / B;
+                asm volatile("" ::: "memory");
+                const float bias = s_bias[lp][gl];
+                f32x4 s = {bias, bias, bias, bias};
+#pragma unroll
+                for (int d = 0; d < 4; ++d) {
+                    const float *ka = &s_ka[lp][ql * KG + 8 * d];
+                    const u32x4 a03 = *(const u32x4 *)ka, a47 = *(const u32x4 *)(ka + 4);
+                    float A[8], Bc[8];
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        A[e] = __uint_as_float(a03[e]);
+                        A[4 + e] = __uint_as_float(a47[e]);
+                    }
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) Bc[e] = A[e] * -0.015625f;   // -8 s, exact
+                    const uint32_t x = kw[j][d];
+                    const uint32_t lo = x & 0x0f0f0f0fu, hi = (x >> 4) & 0x0f0f0f0fu;
+                    const f32x2 e01 = fp8x2<false>(lo), e23 = fp8x2<true>(lo);
+                    const f32x2 o01 = fp8x2<false>(hi), o23 = fp8x2<true>(hi);
+                    u32x4 kv;
+                    kv[0] = pack2<false>(fmaf(e01.x, A[0], Bc[0]), fmaf(o01.x, A[1], Bc[1]));
+                    kv[1] = pack2<false>(fmaf(e01.y, A[2], Bc[2]), fmaf(o01.y, A[3], Bc[3]));
+                    kv[2] = pack2<false>(fmaf(e23.x, A[4], Bc[4]), fmaf(o23.x, A[5], Bc[5]));
+                    kv[3] = pack2<false>(fmaf(e23.y, A[6], Bc[6]), fmaf(o23.y, A[7], Bc[7]));
+                    s = mma32<false>(kv, qb[d], s);
+                }
+                sc[j] = s;
+            }
+            // salient terms: stage the K tiles as [64 tokens][17 dwords], gather codes
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+#pragma unroll
+                for (int w = 0; w < 4; ++w) vt[(16 * j + gl) * KROW + 4 * ql + w] = kw[j][w];
+            const uint8_t *kt = (const uint8_t *)vt;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int lp = (base + 16 * j) / B;
+                const uint8_t *rowp = kt + (16 * j + gl) * (4 * KROW);
+                const u32x2 qs = *(const u32x2 *)(&s_qsal[lp][gl * SPG + 4 * ql]);
+                float v[4];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const uint32_t w = s_salw[lp][4 * ql + e];
+                    const f32x2 sf = s_salf[lp][4 * ql + e];
+                    const uint32_t hi = (rowp[w & 0xffu] >> ((w >> 8) & 0xffu)) & 15u;
+                    const uint32_t lo = (rowp[(w >> 16) & 0xffu] >> (w >> 24)) & 15u;
+                    v[e] = fmaf((float)((hi << 4) | lo), sf.x, sf.y);
+                }
+                const u32x2 ka = {pack2<false>(v[0], v[1]), pack2<false>(v[2], v[3])};
+                sc[j] = mma16<false>(ka, qs, sc[j]);
+            }
+        } else {
+            // dense sink / tail slots: bf16 rows are the A operand directly;
+            // rows of dead slots are zeroed (the buffer may hold NaN there)
+#pragma unroll
+            for (int j2 = 0; j2 < 4; j2 += 2) {
+                u32x4 kd[2][4];
+#pragma unroll
+                for (int jj = 0; jj < 2; ++jj) {
+                    const int t = min(base + 16 * (j2 + jj) + gl, ntok - 1);
+#pragma unroll
+                    for (int d = 0; d < 4; ++d) kd[jj][d] = ld16(dk + (int64_t)t * D + 32 * ql + 8 * d);
+                }
+#pragma unroll
+                for (int jj = 0; jj < 2; ++jj) {
+                    const bool ok = live(base + 16 * (j2 + jj) + gl);
+                    f32x4 s = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+                    for (int d = 0; d < 4; ++d) s = mma32<false>(ok ? kd[jj][d] : u32x4{0u, 0u, 0u, 0u}, qb[d], s);
+                    sc[j2 + jj] = s;
+                }
+            }
+        }
+
+        // ---------------- online softmax (log2 domain); lane holds g = gl, tokens 16 j + 4 ql + r
+        float cmax = NEG_INF;
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const float v = live(base + 16 * j + 4 * ql + r) ? sc[j][r] * a.c_log2 : NEG_INF;
+                sc[j][r] = v;
+                cmax = fmaxf(cmax, v);
+            }
+        cmax = xmax16(cmax);
+        const float m_new = fmaxf(m_run, cmax);
+        const float m_use = m_new == NEG_INF ? 0.0f : m_new;
+        float lsum = 0.0f;
+        u32x4 phi[2], plo[2];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            float pr[4];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                pr[r] = __builtin_amdgcn_exp2f(sc[j][r] - m_use);
+                lsum += pr[r];
+            }
+            const uint32_t h01 = pack2<false>(pr[0], pr[1]), h23 = pack2<false>(pr[2], pr[3]);
+            phi[j >> 1][2 * (j & 1)] = h01;
+            phi[j >> 1][2 * (j & 1) + 1] = h23;
+            plo[j >> 1][2 * (j & 1)] =
+                pack2<false>(pr[0] - to_f32<false>(h01 & 0xffffu), pr[1] - to_f32<false>(h01 >> 16));
+            plo[j >> 1][2 * (j & 1) + 1] =
+                pack2<false>(pr[2] - to_f32<false>(h23 & 0xffffu), pr[3] - to_f32<false>(h23 >> 16));
+        }
+        l_run = lsum;
+        m_run = m_new;
+
+        // ---------------- two half chunks: decode 32 V rows to LDS, then O^T += V^T P^T
+#pragma unroll
+        for (int m = 0; m < 2; ++m) {
+            uint32_t *dst = vt + pl * VR + 32 * qq;    // token pair pl, channels 32 qq .. 32 qq + 31
+            if (packed) {
+                // dead tokens decode to zero: a zero weight times a non-finite
+                // value (a page id outside the pool) would still poison P.V
+                float s9[2], of[2];
+#pragma unroll
+                for (int u = 0; u < 2; ++u) {
+                    const bool ok = live(base + 32 * m + 2 * pl + u);
+                    s9[u] = ok ? iq_f16_to_f32(vp[m][u][0]) * inv_unit : 0.0f;
+                    of[u] = ok ? iq_f16_to_f32(vp[m][u][1]) : 0.0f;
+                }
+#pragma unroll
+                for (int w = 0; w < 2; ++w) {          // 16 channels 32 qq + 16 w + (4 b + k)
+                    float val[2][16];
+#pragma unroll
+                    for (int u = 0; u < 2; ++u) {
+                        const uint32_t x = vw[m][u][w];
+#pragma unroll
+                        for (int k = 0; k < 4; ++k) {
+                            const uint32_t b = (x >> (2 * k)) & 0x03030303u;
+                            const f32x2 c0 = fp8x2<false>(b), c1 = fp8x2<true>(b);
+                            val[u][k] = fmaf(c0.x, s9[u], of[u]);
+                            val[u][4 + k] = fmaf(c0.y, s9[u], of[u]);
+                            val[u][8 + k] = fmaf(c1.x, s9[u], of[u]);
+                            val[u][12 + k] = fmaf(c1.y, s9[u], of[u]);
+                        }
+                    }
+#pragma unroll
+                    for (int c4 = 0; c4 < 4; ++c4) {
+                        u32x4 o;
+#pragma unroll
+                        for (int i = 0; i < 4; ++i) o[i] = pack2<false>(val[0][4 * c4 + i], val[1][4 * c4 + i]);
+                        *(u32x4 *)(dst + 16 * w + 4 * c4) = o;
+                    }
+                }
+            } else {
+                const int t0 = base + 32 * m + 2 * pl;
+                const int ta = min(t0, ntok - 1), tb = min(t0 + 1, ntok - 1);
+                const bool oka = live(t0), okb = live(t0 + 1);
+                u32x4 r0[4], r1[4];
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    r0[i] = ld16(dv + (int64_t)ta * D + 32 * qq + 8 * i);
+                    r1[i] = ld16(dv + (int64_t)tb * D + 32 * qq + 8 * i);
+                }
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    if (!oka) r0[i] = u32x4{0u, 0u, 0u, 0u};
+                    if (!okb) r1[i] = u32x4{0u, 0u, 0u, 0u};
+                    u32x4 lo, hi;
+#pragma unroll
+                    for (int w = 0; w < 4; ++w) {
+                        lo[w] = __builtin_amdgcn_perm(r1[i][w], r0[i][w], 0x05040100u);
+                        hi[w] = __builtin_amdgcn_perm(r1[i][w], r0[i][w], 0x07060302u);
+                    }
+                    *(u32x4 *)(dst + 8 * i) = u32x4{lo[0], hi[0], lo[1], hi[1]};
+                    *(u32x4 *)(dst + 8 * i + 4) = u32x4{lo[2], hi[2], lo[3], hi[3]};
+                }
+            }
+#pragma unroll
+            for (int n = 0; n < 8; ++n) {
+                u32x4 va;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const int pp = e < 2 ? 2 * ql + e : 8 + 2 * ql + (e - 2);
+                    va[e] = vt[pp * VR + 16 * n + gl];
+                }
+                acc[n] = mma32<false>(va, phi[m], acc[n]);
+                acc[n] = mma32<false>(va, plo[m], acc[n]);
+            }
+        }
+    }
+
+    // ---------------- combine the four wavefronts, write this partition's partial
+    l_run = xsum16(l_run);
+    if (ql == 0) {
+        s_wm[wave][gl] = m_run;
+        s_wl[wave][gl] = l_run;
+    }
+    __syncthreads();
+    float *ot = (float *)vt;        // O^T[c][g] of this wavefront, row stride 17
+#pragma unroll
+    for (int n = 0; n < 8; ++n)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) ot[(16 * n + 4 * ql + r) * 17 + gl] = acc[n][r];
+    __syncthreads();
+    for (int i = tid; i < G * D; i += 256) {
+        const int g = i >> 7, c = i & (D - 1);
+        float mx = NEG_INF;
+#pragma unroll
+        for (int w = 0; w < WAVES; ++w) mx = fmaxf(mx, s_wm[w][g]);
+        float num = 0.0f, den = 0.0f;
+#pragma unroll
+        for (int w = 0; w < WAVES; ++w) {
+            const float mw = s_wm[w][g];
+            const float wt = mw == NEG_INF ? 0.0f : __builtin_amdgcn_exp2f(mw - mx);
+            num = fmaf(((const float *)s_v[w])[c * 17 + g], wt, num);
+            den = fmaf(s_wl[w][g], wt, den);
+        }
+        float *out = a.ws + (((int64_t)sq * a.H * G + h * G + g) * a.max_parts + p) * (D + 2);
+        out[c] = num;
+        if (c == 0) {
+            out[D] = mx == NEG_INF ? NEG_INF : mx * LN2;
+            out[D + 1] = den;
+        }
+    }
+}
+
+// grid (Hq, D / 32, seq): merges the partitions of one sequence.
+__global__ __launch_bounds__(256) void paged_reduce(PagedArgs a, void *out, int64_t out_ss, int odt)
+{
+    __shared__ float s_m[256], s_n[256], s_l[256];
+    const int hq = blockIdx.x, c0 = blockIdx.y * 32, sq = blockIdx.z;
+    const int tid = threadIdx.x, c = tid & 31, part = tid >> 5;
+    const SeqGeom geo = seq_geom(a, sq);
+    const int P = geo.npp + geo.ndp;
+    const float *base = a.ws + ((int64_t)sq * a.H * a.G + hq) * a.max_parts * (D + 2);
+    float m = NEG_INF, num = 0.0f, den = 0.0f;
+    for (int p0 = part; p0 < P; p0 += 8 * 16) {
+        float mv[16], lv[16], av[16];
+#pragma unroll
+        for (int k = 0; k < 16; ++k) {
+            const int pp = p0 + 8 * k;
+            const bool ok = pp < P;
+            const float *r = base + (int64_t)(ok ? pp : 0) * (D + 2);
+            mv[k] = ok ? r[D] : NEG_INF;
+            lv[k] = ok ? r[D + 1] : 0.0f;
+            av[k] = ok ? r[c0 + c] : 0.0f;
+        }
+        float mm = m;
+#pragma unroll
+        for (int k = 0; k < 16; ++k) mm = fmaxf(mm, mv[k]);
+        if (mm == NEG_INF) continue;
+        const float wo = m == NEG_INF ? 0.0f : __expf(m - mm);
+        num *= wo;
+        den *= wo;
+#pragma unroll
+        for (int k = 0; k < 16; ++k) {
+            const float w = mv[k] == NEG_INF ? 0.0f : __expf(mv[k] - mm);
+            num = fmaf(av[k], w, num);
+            den = fmaf(lv[k], w, den);
+        }
+        m = mm;
+    }
+    s_m[tid] = m;
+    s_n[tid] = num;
+    s_l[tid] = den;
+    __syncthreads();
+    if (tid < 32) {
+        float mm = NEG_INF;
+        for (int k = 0; k < 8; ++k) mm = fmaxf(mm, s_m[k * 32 + tid]);
+        float nn = 0.0f, dd = 0.0f;
+        for (int k = 0; k < 8; ++k) {
+            const float mk = s_m[k * 32 + tid];
+            if (mk == NEG_INF) continue;
+            const float w = __expf(mk - mm);
+            nn = fmaf(s_n[k * 32 + tid], w, nn);
+            dd = fmaf(s_l[k * 32 + tid], w, dd);
+        }
+        iq_store_as(out, sq * out_ss + (int64_t)hq * D + c0 + tid, nn / dd, odt);
+    }
+}
+
+}  // namespace
+
+static bool valid_block(int64_t B) { return B == 16 || B == 32 || B == 64 || B == 128 || B == 256; }
+
+extern "C" int64_t iq_page_bytes(int64_t H, int64_t block_tokens)
+{
+    return H * (104 * block_tokens + 832);
+}
+
+extern "C" int iq_write_pages(const uint8_t *k_payload, const float *k_scales, const float *k_padding,
+                              const void *k_src, const void *k_don, int desc_bytes, const uint8_t *v_payload,
+                              const uint16_t *v_scales, const uint16_t *v_offsets, int64_t n_pages, int64_t H,
+                              int64_t block_tokens, uint8_t *pool, int64_t pool_pages, const void *page_ids,
+                              int id_bytes, void *stream)
+{
+    IQ_CHECK_ARG(n_pages >= 0 && H >= 1 && H <= 65535, "iq_write_pages: bad shape");
+    IQ_CHECK_ARG(valid_block(block_tokens), "iq_write_pages: block_tokens %lld unsupported", (long long)block_tokens);
+    IQ_CHECK_ARG(desc_bytes == 1 || desc_bytes == 4 || desc_bytes == 8, "iq_write_pages: desc_bytes");
+    IQ_CHECK_ARG(id_bytes == 4 || id_bytes == 8, "iq_write_pages: id_bytes");
+    if (n_pages == 0) return IQ_OK;
+    IQ_CHECK_ARG(k_payload && k_scales && k_padding && k_src && k_don && v_payload && v_scales && v_offsets &&
+                     pool && page_ids, "iq_write_pages: null pointer");
+    IQ_CHECK_ARG(n_pages <= 0x7fffffffLL, "iq_write_pages: too many pages");
+    IQ_CHECK_ARG(((uintptr_t)k_payload & 15) == 0 && ((uintptr_t)v_payload & 15) == 0 && ((uintptr_t)pool & 15) == 0,
+                 "iq_write_pages: payloads and pool must be 16-byte aligned");
+    WriteArgs a{k_payload, k_scales, k_padding, k_src, k_don, desc_bytes, v_payload, v_scales, v_offsets, H,
+                block_tokens, iq_page_bytes(H, block_tokens), pool_pages, pool, page_ids, id_bytes,
+                page_offsets(H, block_tokens)};
+    hipLaunchKernelGGL(write_pages_kernel, dim3((unsigned)n_pages, (unsigned)H), dim3(256), 0, (hipStream_t)stream, a);
+    IQ_CHECK_LAUNCH("write_pages_kernel");
+    return IQ_OK;
+}
+
+extern "C" int iq_unpack_pages(const uint8_t *pages, int64_t n_pages, int64_t H, int64_t block_tokens, void *keys,
+                               void *values, int out_dtype, void *stream)
+{
+    IQ_CHECK_ARG(n_pages >= 0 && H >= 1, "iq_unpack_pages: bad shape");
+    IQ_CHECK_ARG(valid_block(block_tokens), "iq_unpack_pages: block_tokens %lld unsupported", (long long)block_tokens);
+    IQ_CHECK_ARG(out_dtype >= IQ_F32 && out_dtype <= IQ_F16, "iq_unpack_pages: bad out dtype");
+    if (n_pages == 0) return IQ_OK;
+    IQ_CHECK_ARG(pages && keys && values, "iq_unpack_pages: null pointer");
+    IQ_CHECK_ARG(n_pages * H <= 0x7fffffffLL, "iq_unpack_pages: too many pages");
+    UnpackArgs a{pages, H, block_tokens, iq_page_bytes(H, block_tokens), page_offsets(H, block_tokens), keys, values,
+                 out_dtype};
+    hipLaunchKernelGGL(unpack_pages_kernel, dim3((unsigned)(n_pages * H), (unsigned)block_tokens), dim3(D), 0,
+                       (hipStream_t)stream, a);
+    IQ_CHECK_LAUNCH("unpack_pages_kernel");
+    return IQ_OK;
+}
+
+static int64_t paged_parts(int64_t max_pages, int64_t B)
+{
+    return (max_pages * B + PART - 1) / PART + (B + 4 + PART - 1) / PART;
+}
+
+extern "C" int64_t iq_paged_workspace_floats(int64_t Hq, int64_t n_seq, int64_t max_pages, int64_t block_tokens)
+{
+    return n_seq * Hq * paged_parts(max_pages, block_tokens) * (D + 2);
+}
+
+extern "C" int iq_paged_decode(const void *q, int64_t q_stride_seq, int64_t q_stride_h, int64_t Hq, int64_t n_seq,
+                               const uint8_t *pool, int64_t pool_pages, int64_t H, int64_t block_tokens,
+                               const int32_t *block_tables, int64_t bt_stride, int64_t max_pages,
+                               const int32_t *seq_info, int64_t n_pages, int64_t tail_t, int64_t sink_t,
+                               const void *dense, int64_t dense_stride_seq, float scale, float *workspace,
+                               int64_t workspace_floats, void *out, int64_t out_stride_seq, int out_dtype,
+                               void *stream)
+{
+    IQ_CHECK_ARG(q && pool && dense && workspace && out, "iq_paged_decode: null pointer");
+    IQ_CHECK_ARG(H >= 1 && Hq >= H && Hq % H == 0 && Hq / H <= 16, "iq_paged_decode: expected 1..16 query heads per KV head");
+    IQ_CHECK_ARG(valid_block(block_tokens), "iq_paged_decode: block_tokens %lld unsupported", (long long)block_tokens);
+    IQ_CHECK_ARG(n_seq >= 1 && n_seq <= 65535, "iq_paged_decode: bad sequence count");
+    IQ_CHECK_ARG(max_pages >= 0 && (max_pages == 0 || block_tables), "iq_paged_decode: missing block table");
+    IQ_CHECK_ARG(seq_info || n_seq == 1, "iq_paged_decode: batches need per-sequence lengths");
+    IQ_CHECK_ARG(seq_info || (n_pages >= 0 && n_pages <= max_pages && tail_t >= 0 && tail_t <= block_tokens &&
+                              sink_t >= 0 && sink_t <= 4), "iq_paged_decode: bad lengths");
+    IQ_CHECK_ARG(out_dtype >= IQ_F32 && out_dtype <= IQ_F16, "iq_paged_decode: bad out dtype");
+    IQ_CHECK_ARG(((uintptr_t)q & 15) == 0 && q_stride_h % 8 == 0 && q_stride_seq % 8 == 0 &&
+                     ((uintptr_t)dense & 15) == 0 && dense_stride_seq % 8 == 0,
+                 "iq_paged_decode: query and dense rows must be 16-byte aligned");
+    const int64_t parts = paged_parts(max_pages, block_tokens);
+    IQ_CHECK_ARG(parts <= 65535, "iq_paged_decode: too many partitions");
+    IQ_CHECK_ARG(workspace_floats >= n_seq * Hq * parts * (D + 2), "iq_paged_decode: workspace too small");
+    PagedArgs a{};
+    a.q = (const uint16_t *)q;
+    a.q_ss = q_stride_seq;
+    a.q_sh = q_stride_h;
+    a.G = (int)(Hq / H);
+    a.H = (int)H;
+    a.B = (int)block_tokens;
+    a.pool = pool;
+    a.page_bytes = iq_page_bytes(H, block_tokens);
+    a.pool_pages = pool_pages;
+    a.off = page_offsets(H, block_tokens);
+    a.bt = block_tables;
+    a.bt_ss = bt_stride;
+    a.max_pages = max_pages;
+    a.seq_info = seq_info;
+    a.npg0 = (int)n_pages;
+    a.tail0 = (int)tail_t;
+    a.sink0 = (int)sink_t;
+    a.dense = (const uint16_t *)dense;
+    a.dense_ss = dense_stride_seq;
+    a.max_parts = (int)parts;
+    a.c_log2 = scale * 1.4426950408889634f;
+    a.ws = workspace;
+    const dim3 grid((unsigned)H, (unsigned)parts, (unsigned)n_seq);
+    hipStream_t st = (hipStream_t)stream;
+    switch (block_tokens) {
+    case 16: hipLaunchKernelGGL(decode_paged<16>, grid, dim3(256), 0, st, a); break;
+    case 32: hipLaunchKernelGGL(decode_paged<8>, grid, dim3(256), 0, st, a); break;
+    case 64: hipLaunchKernelGGL(decode_paged<4>, grid, dim3(256), 0, st, a); break;
+    case 128: hipLaunchKernelGGL(decode_paged<2>, grid, dim3(256), 0, st, a); break;
+    default: hipLaunchKernelGGL(decode_paged<1>, grid, dim3(256), 0, st, a); break;
+    }
+    IQ_CHECK_LAUNCH("decode_paged");
+    hipLaunchKernelGGL(paged_reduce, dim3((unsigned)Hq, D / 32, (unsigned)n_seq), dim3(256), 0, st, a, out,
+                       out_stride_seq, out_dtype);
+    IQ_CHECK_LAUNCH("paged_reduce");
+    return IQ_OK;
+}

@@ -1,0 +1,16 @@
+"""Paged InQuant cache in the vLLM plugin's page layout, on MI355X.
+
+Mirrors the reference's extensions/vllm/src/inquant_vllm modules that carry
+the packed-KV hot path: `layout` (PageLayout, pack_pages,
+unpack_pages_reference, pack_pages_into), `packing` (write_codec_pages) and
+`kernels` (paged_decode, plus paged_decode_batch for several sequences in
+one launch).  The vLLM platform, worker and attention-backend integration
+(backend.py, platform.py, worker.py) need vLLM itself and are not part of
+this package.
+"""
+from .layout import PageLayout, pack_pages, pack_pages_into, unpack_pages_reference
+from .packing import write_codec_pages
+from .kernels import paged_decode, paged_decode_batch
+
+__all__ = ["PageLayout", "pack_pages", "pack_pages_into", "unpack_pages_reference", "write_codec_pages",
+           "paged_decode", "paged_decode_batch"]

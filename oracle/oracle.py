@@ -181,3 +181,100 @@ def check_recip_division(n_max: int = 256, samples: int = 20000, seed: int = 1) 
     """Mismatches of the GPU tile encoder's reciprocal-and-remainder quotient
     against IEEE division (test support, see iqo_check_recip_division)."""
     return int(lib().iqo_check_recip_division(n_max, samples, seed))
+
+
+# ---------------------------------------------------------------- paged cache (vLLM page layout)
+
+def page_fields(H: int, B: int):
+    """Field order, dtypes and shapes of one page (layout.py:18-31)."""
+    return (("key_payload", np.uint8, (H, B, 64)), ("key_scales", np.float32, (H, 128)),
+            ("key_map", np.int16, (H, 128)), ("key_padding", np.float32, (H, 16)),
+            ("value_payload", np.uint8, (H, B, 32)), ("value_scales", np.float16, (H, B, 2)),
+            ("value_offsets", np.float16, (H, B, 2)))
+
+
+def page_offsets(H: int, B: int):
+    """Byte offset of every field and the page size (layout.py:33-45)."""
+    off, result = 0, {}
+    for name, dtype, shape in page_fields(H, B):
+        result[name] = off
+        off += int(np.prod(shape)) * np.dtype(dtype).itemsize
+    return result, off
+
+
+def page_views(pages: np.ndarray, H: int, B: int):
+    offsets, size = page_offsets(H, B)
+    assert pages.dtype == np.uint8 and pages.ndim == 2 and pages.shape[1] == size
+    out = {}
+    for name, dtype, shape in page_fields(H, B):
+        n = int(np.prod(shape)) * np.dtype(dtype).itemsize
+        out[name] = pages[:, offsets[name]:offsets[name] + n].view(dtype).reshape(-1, *shape)
+    return out
+
+
+def pack_pages(kq: dict, vq: dict, H: int, B: int) -> np.ndarray:
+    """Codec outputs of [P, H, B, 128] pages -> [P, page_bytes] (layout.py:56-81):
+    fields copied, role map -1 / donor channel for a source / -2 - j for donor j."""
+    P = kq["payload"].shape[0]
+    _, size = page_offsets(H, B)
+    pages = np.zeros((P, size), np.uint8)
+    f = page_views(pages, H, B)
+    f["key_payload"][...] = kq["payload"]
+    f["key_scales"][...] = kq["scales"]
+    f["key_padding"][...] = kq["padding"]
+    src = np.asarray(kq["salient_channels"], np.int64).reshape(P * H, -1)
+    don = np.asarray(kq["donor_channels"], np.int64).reshape(P * H, -1)
+    f["key_map"][...] = role_map(src, don).reshape(P, H, 128)
+    f["value_payload"][...] = vq["payload"]
+    f["value_scales"][...] = np.asarray(vq["scales"], np.float16)
+    f["value_offsets"][...] = np.asarray(vq["offsets"], np.float16)
+    return pages
+
+
+def unpack_pages(pages: np.ndarray, H: int, B: int, dtype: str = "bfloat16"):
+    """[P, page_bytes] -> K, V float32 [P, H, B, 128] rounded to dtype (layout.py:84-100)."""
+    f = page_views(np.ascontiguousarray(pages), H, B)
+    role = f["key_map"].astype(np.int64)                                    # [P, H, 128]
+    kp = f["key_payload"]
+    slots = np.stack((kp & 15, kp >> 4), -1).reshape(*kp.shape[:-1], 128).astype(np.int64)
+    partner = np.take_along_axis(slots, np.broadcast_to(np.maximum(role, 0)[:, :, None, :], slots.shape), -1)
+    code = np.where(role[:, :, None, :] >= 0, (slots << 4 | partner) - 128, slots - 8)
+    keys = code.astype(np.float32) * f["key_scales"][:, :, None, :]
+    pad = np.take_along_axis(f["key_padding"], np.maximum(-role - 2, 0), -1)  # [P, H, 128]
+    keys = np.where(role[:, :, None, :] <= -2, pad[:, :, None, :], keys).astype(np.float32)
+    vp = f["value_payload"]
+    codes = np.stack([(vp >> i) & 3 for i in (0, 2, 4, 6)], -1).reshape(*vp.shape[:-1], 128)
+    vals = codes.astype(np.float32).reshape(*codes.shape[:-1], 2, 64)
+    vals = (vals * f["value_scales"].astype(np.float32)[..., None]
+            + f["value_offsets"].astype(np.float32)[..., None]).reshape(*codes.shape[:-1], 128)
+    rnd = to_bf16 if dtype == "bfloat16" else (to_f16 if dtype == "float16" else (lambda a: a))
+    return rnd(keys), rnd(vals.astype(np.float32))
+
+
+def paged_tokens(pool: np.ndarray, ids, dense: np.ndarray, n_pages: int, tail_t: int, sink_t: int,
+                 H: int, B: int):
+    """The K/V tokens paged decode attends to, in any order (kernels.py:29-59): packed
+    tokens of the block table's pages whose global index is at least the sink
+    length, dense slots below the sink length, and dense tail slots 4 .. 4 + tail
+    whose global position n_pages * B + slot - 4 is at least the sink length.
+    dense: float32 [2, H, B + 4, 128]."""
+    ks, vs = [], []
+    if n_pages:
+        k, v = unpack_pages(pool[np.asarray(ids[:n_pages], np.int64)], H, B)     # [n, H, B, 128]
+        k = k.transpose(1, 0, 2, 3).reshape(H, n_pages * B, 128)
+        v = v.transpose(1, 0, 2, 3).reshape(H, n_pages * B, 128)
+        live = np.arange(n_pages * B) >= sink_t
+        ks.append(k[:, live])
+        vs.append(v[:, live])
+    slots = np.arange(B + 4)
+    live = (slots < sink_t) | ((slots >= 4) & (slots < 4 + tail_t) & (n_pages * B + slots - 4 >= sink_t))
+    ks.append(dense[0][:, live])
+    vs.append(dense[1][:, live])
+    return np.concatenate(ks, 1), np.concatenate(vs, 1)
+
+
+def paged_attend(q: np.ndarray, pool: np.ndarray, ids, dense: np.ndarray, n_pages: int, tail_t: int,
+                 sink_t: int, H: int, B: int, scale: float) -> np.ndarray:
+    """fp64 paged decode of one sequence: q [Hq, 128] -> [Hq, 128]."""
+    k, v = paged_tokens(pool, ids, dense, n_pages, tail_t, sink_t, H, B)
+    return attend(q, k, v, scale)

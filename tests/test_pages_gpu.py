@@ -1,0 +1,174 @@
+"""GPU parity of the paged cache: page bytes bit-exact against the oracle,
+paged decode within 2e-3 of the fp64 oracle (restates the reference's
+extensions/vllm/tests/test_pages.py and test_direct_packing.py)."""
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle
+
+pytestmark = pytest.mark.gpu
+ATOL = 2e-3
+
+
+def _np(t):
+    return t.detach().cpu().numpy()
+
+
+def _kv(seed, shape, device="cuda"):
+    g = torch.Generator(device=device).manual_seed(seed)
+    k = torch.randn(shape, generator=g, device=device)
+    v = torch.randn(shape, generator=g, device=device)
+    k[..., 17:19] *= 20
+    return k.to(torch.bfloat16), v.to(torch.bfloat16)
+
+
+@pytest.mark.parametrize("block", [16, 64, 128, 256])
+def test_page_layout_matches_existing_codecs(block):
+    # test_pages.py:9-19, plus the page bytes against the oracle
+    from inquant.codec import CodecConfig, quantize
+    from inquant.value_codec import quantize_values
+    from inquant_vllm import PageLayout, pack_pages, unpack_pages_reference
+    layout = PageLayout(block, 2)
+    k, v = _kv(7, (3, 2, block, 128))
+    pages = pack_pages(k, v, layout)
+    assert pages.shape == (3, layout.page_bytes)
+    kq = oracle.k4_quantize(_np(k.float()), 8, 0.125, "min_error")
+    vq = oracle.v_quantize(_np(v.float()), 2, 64)
+    np.testing.assert_array_equal(_np(pages), oracle.pack_pages(kq, vq, 2, block))
+    rk, rv = unpack_pages_reference(pages, layout)
+    assert torch.equal(rk, quantize(k, CodecConfig(donor_policy="min_error")).dequantize())
+    assert torch.equal(rv, quantize_values(v).dequantize())
+    for dtype, name in ((torch.float32, "float32"), (torch.float16, "float16")):
+        rk, rv = unpack_pages_reference(pages, layout, dtype)
+        ok, ov = oracle.unpack_pages(_np(pages), 2, block, name)
+        np.testing.assert_array_equal(_np(rk.float()).view(np.uint32), ok.view(np.uint32))
+        np.testing.assert_array_equal(_np(rv.float()).view(np.uint32), ov.view(np.uint32))
+
+
+@pytest.mark.parametrize("block", [16, 64, 128, 256])
+@pytest.mark.parametrize("backend", ["torch", "triton"])
+@pytest.mark.parametrize("heads", [4, 8])
+def test_direct_scattered_pages_match_reference_and_reuse(block, backend, heads):
+    # test_direct_packing.py:9-22
+    from inquant_vllm import PageLayout, pack_pages, pack_pages_into
+    layout = PageLayout(block, heads)
+    pool = torch.full((7, layout.page_bytes), 173, device="cuda", dtype=torch.uint8)
+    ids = torch.tensor([5, 0, 3], device="cuda", dtype=torch.int32)
+    for r in range(2):
+        k, v = _kv(915 + r, (3, heads, block, 128))
+        reference = pack_pages(k, v, layout)
+        pack_pages_into(k, v, layout, pool, ids, donor_backend=backend)
+        assert torch.equal(pool[ids.long()], reference)
+        assert (pool[torch.tensor([1, 2, 4, 6], device="cuda")] == 173).all()
+
+
+def _paged_case(seed, block, pages, tail, h=4, hq=28, spare=7):
+    from inquant_vllm import PageLayout, pack_pages
+    layout = PageLayout(block, h)
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    pool = torch.full((pages + spare, layout.page_bytes), 255, dtype=torch.uint8, device="cuda")
+    ids = torch.randperm(pages + spare, generator=g, device="cuda")[:pages].to(torch.int32)
+    dense = torch.full((2, h, block + 4, 128), float("nan"), dtype=torch.bfloat16, device="cuda")
+    k, v = _kv(seed + 1, (h, pages * block + tail, 128))
+    sink = min(4, k.shape[1])
+    dense[0, :, :sink], dense[1, :, :sink] = k[:, :sink], v[:, :sink]
+    if tail:
+        dense[0, :, 4:4 + tail], dense[1, :, 4:4 + tail] = k[:, -tail:], v[:, -tail:]
+    if pages:
+        kt = k[:, :pages * block].reshape(h, pages, block, 128).transpose(0, 1)
+        vt = v[:, :pages * block].reshape(h, pages, block, 128).transpose(0, 1)
+        pool.index_copy_(0, ids.long(), pack_pages(kt, vt, layout))
+    q = torch.randn(1, hq, 128, generator=g, device="cuda").to(torch.bfloat16)
+    return layout, pool, ids, dense, sink, q
+
+
+def _expected(layout, pool, ids, dense, pages, tail, sink, q):
+    d = _np(dense.float())
+    return oracle.paged_attend(_np(q.float())[0], _np(pool), _np(ids), d, pages, tail, sink,
+                               layout.heads, layout.block_size, 128 ** -0.5)
+
+
+@pytest.mark.parametrize("block,pages,tail", [(64, 0, 1), (64, 0, 63), (64, 1, 0), (64, 1, 64), (128, 3, 17),
+                                               (256, 128, 128), (256, 2, 256), (16, 1, 1), (16, 37, 9),
+                                               (32, 9, 31), (16, 0, 3)])
+def test_paged_decode_random_page_order_and_reuse(block, pages, tail):
+    # test_pages.py:22-58 (random physical order, unused pages full of 0xff,
+    # NaN in dead dense slots, the workspace reused), against the fp64 oracle
+    from inquant.triton_attention import SharedDecodeWorkspace
+    from inquant_vllm import paged_decode
+    workspace = SharedDecodeWorkspace()
+    for reuse in range(2):
+        layout, pool, ids, dense, sink, q = _paged_case(71 + reuse, block, pages, tail)
+        actual = paged_decode(q, pool, ids, dense, pages, tail, sink, layout, workspace, 128 ** -0.5)
+        assert actual.shape == q.shape and actual.dtype == torch.bfloat16
+        got = _np(actual.float())[0]
+        assert np.isfinite(got).all()
+        exp = _expected(layout, pool, ids, dense, pages, tail, sink, q)
+        assert np.abs(got - exp).max() <= ATOL + np.abs(exp).max() * 2 ** -8   # bf16 output rounding
+        out32 = torch.empty(q.shape, dtype=torch.float32, device="cuda")
+        paged_decode(q, pool, ids, dense, pages, tail, sink, layout, workspace, 128 ** -0.5, out32)
+        assert np.abs(_np(out32)[0] - exp).max() <= ATOL
+
+
+def test_paged_decode_batch_equals_single_sequences():
+    # sequences of different lengths and pools in one launch (16-token pages)
+    from inquant.triton_attention import SharedDecodeWorkspace
+    from inquant_vllm import paged_decode, paged_decode_batch
+    cases = [_paged_case(300 + i, 16, n, t) for i, (n, t) in enumerate([(5, 3), (0, 7), (40, 15), (13, 0)])]
+    layout = cases[0][0]
+    # one shared pool: append every case's pages, re-basing its ids
+    pools, bases, tables, infos, dense, qs = [], 0, [], [], [], []
+    max_pages = max(n for n, _ in [(5, 3), (0, 7), (40, 15), (13, 0)])
+    for (lay, pool, ids, d, sink, q), (n, t) in zip(cases, [(5, 3), (0, 7), (40, 15), (13, 0)]):
+        pools.append(pool)
+        row = torch.zeros(max_pages, dtype=torch.int32, device="cuda")
+        row[:n] = ids + bases
+        tables.append(row)
+        bases += pool.shape[0]
+        infos.append([n, t, sink])
+        dense.append(d)
+        qs.append(q[0])
+    pool = torch.cat(pools)
+    out = paged_decode_batch(torch.stack(qs), pool, torch.stack(tables),
+                             torch.tensor(infos, dtype=torch.int32, device="cuda"), torch.stack(dense),
+                             max_pages, layout, SharedDecodeWorkspace(), 128 ** -0.5)
+    for i, ((lay, p1, ids, d, sink, q), (n, t)) in enumerate(zip(cases, [(5, 3), (0, 7), (40, 15), (13, 0)])):
+        single = paged_decode(q, p1, ids, d, n, t, sink, lay, SharedDecodeWorkspace(), 128 ** -0.5)
+        assert torch.equal(out[i], single[0])
+
+
+def test_page_ids_outside_the_pool_contribute_nothing():
+    from inquant.triton_attention import SharedDecodeWorkspace
+    from inquant_vllm import paged_decode
+    layout, pool, ids, dense, sink, q = _paged_case(5, 64, 3, 10)
+    bad = ids.clone()
+    bad[1] = pool.shape[0] + 100
+    got = _np(paged_decode(q, pool, bad, dense, 3, 10, sink, layout, SharedDecodeWorkspace(), 128 ** -0.5)
+              .float())[0]
+    # expected: the same decode without page 1's tokens
+    k, v = oracle.paged_tokens(_np(pool), _np(ids), _np(dense.float()), 3, 10, sink, 4, 64)
+    live = np.ones(k.shape[1], bool)
+    live[64 - sink:128 - sink] = False          # the token list starts after the first `sink` packed tokens
+    exp = oracle.attend(_np(q.float())[0], k[:, live], v[:, live], 128 ** -0.5)
+    assert np.abs(got - exp).max() <= ATOL + np.abs(exp).max() * 2 ** -8
+
+
+def test_page_write_and_decode_beyond_signed_32bit_byte_offset():
+    # test_direct_packing.py:25-46
+    from inquant.triton_attention import SharedDecodeWorkspace
+    from inquant_vllm import PageLayout, pack_pages, pack_pages_into, paged_decode
+    layout = PageLayout(64, 4)
+    far = 2 ** 31 // layout.page_bytes + 1
+    pool = torch.empty((far + 1, layout.page_bytes), device="cuda", dtype=torch.uint8)
+    ids = torch.tensor([0, far], device="cuda", dtype=torch.int32)
+    k, v = _kv(811, (1, 4, 64, 128))
+    reference = pack_pages(k, v, layout)
+    pack_pages_into(k.expand(2, -1, -1, -1), v.expand(2, -1, -1, -1), layout, pool, ids, donor_backend="triton")
+    assert torch.equal(pool[ids.long()], reference.expand(2, -1))
+    query = torch.randn(1, 28, 128, device="cuda", dtype=torch.bfloat16)
+    tail = torch.randn(2, 4, 68, 128, device="cuda", dtype=torch.bfloat16)
+    workspace = SharedDecodeWorkspace()
+    near = paged_decode(query, pool, ids[:1], tail, 1, 1, 4, layout, workspace, 128 ** -0.5)
+    far_out = paged_decode(query, pool, ids[1:], tail, 1, 1, 4, layout, workspace, 128 ** -0.5)
+    assert torch.equal(near, far_out)
