@@ -38,6 +38,7 @@ def parse():
     ap.add_argument("--blocks", type=int, default=128)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-graph", action="store_true", help="launch layer by layer instead of a HIP graph")
+    ap.add_argument("--no-paged", action="store_true", help="skip the batched paged decode (config 4)")
     ap.add_argument("--copy-probe", action="store_true",
                     help="only run a 1 GiB device-to-device copy (calibrates rocprofv3 FETCH_SIZE / WRITE_SIZE)")
     return ap.parse_args()
@@ -227,6 +228,80 @@ def time_encode(device, reps=10):
             "encode_gbs": enc_bytes / (ms * 1e-3) / 1e9, "encode_bytes_per_layer": enc_bytes}
 
 
+def time_paged(device, layers=4, n_seq=16, block=16, H=4, G=7, seed=4, steps=20):
+    """Config 4: batched paged decode, 16 sequences with contexts ~ U{2048..32768}
+    in 16-token pages of the vLLM layout, random physical page order, per-sequence
+    BF16 sink (4) and partial-page tail.  `layers` independent pools (rotated, so
+    the working set exceeds the Infinity Cache) decoded back to back in a graph."""
+    import torch
+    from inquant.triton_attention import SharedDecodeWorkspace
+    from inquant_vllm import PageLayout, pack_pages_into, paged_decode_batch
+    gen = torch.Generator(device="cpu").manual_seed(seed)
+    ctx = torch.randint(2048, 32769, (n_seq,), generator=gen).tolist()
+    pages = [c // block for c in ctx]
+    tails = [c % block for c in ctx]
+    layout = PageLayout(block, H)
+    max_pages = max(pages)
+    total_pages = sum(pages)
+    work = []
+    g = torch.Generator(device=device).manual_seed(seed)
+    for _ in range(layers):
+        pool = torch.empty((total_pages, layout.page_bytes), dtype=torch.uint8, device=device)
+        perm = torch.randperm(total_pages, generator=g, device=device).to(torch.int32)
+        tables = torch.zeros((n_seq, max_pages), dtype=torch.int32, device=device)
+        dense = torch.zeros((n_seq, 2, H, block + 4, 128), dtype=torch.bfloat16, device=device)
+        first = 0
+        for i, n in enumerate(pages):
+            ids = perm[first:first + n]
+            first += n
+            tables[i, :n] = ids
+            k = kv_tensor(g, H, n * block + tails[i], device)[0]
+            v = kv_tensor(g, H, n * block + tails[i], device)[0]
+            kp = k[:, :n * block].reshape(H, n, block, 128).transpose(0, 1)
+            vp = v[:, :n * block].reshape(H, n, block, 128).transpose(0, 1)
+            pack_pages_into(kp, vp, layout, pool, ids)
+            dense[i, 0, :, :4], dense[i, 1, :, :4] = k[:, :4], v[:, :4]
+            if tails[i]:
+                dense[i, 0, :, 4:4 + tails[i]] = k[:, n * block:]
+                dense[i, 1, :, 4:4 + tails[i]] = v[:, n * block:]
+        info = torch.tensor([[n, t, 4] for n, t in zip(pages, tails)], dtype=torch.int32, device=device)
+        q = torch.randn((n_seq, H * G, 128), generator=g, device=device).to(torch.bfloat16)
+        work.append((q, pool, tables, info, dense, SharedDecodeWorkspace(), torch.empty_like(q)))
+    torch.cuda.synchronize()
+
+    def step():
+        for q, pool, tables, info, dense, ws, out in work:
+            paged_decode_batch(q, pool, tables, info, dense, max_pages, layout, ws, 128 ** -0.5, out)
+
+    graph = torch.cuda.CUDAGraph()
+    st = torch.cuda.Stream()            # the workspaces are pinned to the stream they first run on
+    st.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(st):
+        step()
+        torch.cuda.synchronize()
+        with torch.cuda.graph(graph, stream=st):
+            step()
+    torch.cuda.synchronize()
+    graph.replay()
+    torch.cuda.synchronize()
+    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(steps):
+        graph.replay()
+    stop.record()
+    torch.cuda.synchronize()
+    us = start.elapsed_time(stop) * 1e3 / steps / layers
+    # algorithmic bytes per layer: every page of every sequence, its block-table
+    # entry, the live dense sink/tail rows, Q and O
+    bytes_layer = total_pages * (layout.page_bytes + 4) + sum(4 + t for t in tails) * 2 * H * 128 * 2 \
+        + 2 * n_seq * H * G * 128 * 2
+    return {"sequences": n_seq, "page_tokens": block, "mean_ctx": round(sum(ctx) / n_seq, 1),
+            "us_per_layer": round(us, 3), "bytes_per_layer": bytes_layer,
+            "gbs": round(bytes_layer / (us * 1e-6) / 1e9, 2),
+            "hbm_frac": round(bytes_layer / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+            "tokens_per_s": round(n_seq / (us * 1e-6), 1), "layers_rotated": layers}
+
+
 def cpu_baseline(layer):
     """Time the CPU oracle (dequantize-then-attend, fp64) on a bounded sample of one layer."""
     import numpy as np
@@ -284,6 +359,7 @@ def main():
     layer_us = ms * 1e3 / args.layers
     achieved = per_layer / (layer_us * 1e-6) / 1e9
     enc = time_encode(device)
+    paged = None if args.no_paged else time_paged(device)
     result = {
         "metric": METRIC,
         "value": round(gbs, 2),
@@ -310,6 +386,8 @@ def main():
         "encode_mtok_s": round(enc["encode_mtok_s"], 2),
         "encode": {k: round(v, 3) for k, v in enc.items()},
     }
+    if paged is not None:
+        result["paged_cfg4"] = paged
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(layers[0])
     print(json.dumps(result))
