@@ -302,6 +302,66 @@ def time_paged(device, layers=4, n_seq=16, block=16, H=4, G=7, seed=4, steps=20)
             "tokens_per_s": round(n_seq / (us * 1e-6), 1), "layers_rotated": layers}
 
 
+def time_append(device, H=4, packed_tokens=32768):
+    """Config 2 append, through the cache API of one Qwen2.5-7B layer (32K packed
+    context): 128 single-token appends (dense tail 128 -> 256, no seal), then the
+    append that seals one 256-token block (K4 + V2 encode) starting from a
+    383-token tail, then the decode-state metadata append for that block."""
+    import torch
+    from inquant.cache import CacheConfig, InQuantCache
+    from inquant.codec import CodecConfig
+    from inquant.triton_attention import PackedDecodeState
+    g = torch.Generator(device=device).manual_seed(11)
+    cfg = CacheConfig(codec=CodecConfig(donor_policy="min_error"), value_bits=2, value_group_size=64)
+    cache = InQuantCache(cfg)
+    n0 = 4 + packed_tokens + 128
+    k = kv_tensor(g, H, n0 + 768, device)
+    v = kv_tensor(g, H, n0 + 768, device)
+    cache.update(k[:, :, :n0], v[:, :, :n0], 0)
+    layer = cache._layers[0]
+    state = PackedDecodeState(list(layer.key_blocks), list(layer.value_blocks))
+    pos = n0
+    # one full cycle first (tail 128 -> 384 -> seal -> 128), so that the timed
+    # window sees warm allocator blocks and loaded kernels
+    for _ in range(256):
+        cache.append_for_attention(k[:, :, pos:pos + 1], v[:, :, pos:pos + 1], 0,
+                                   {"cache_position": torch.tensor([pos], device=device)})
+        pos += 1
+    state.extend(list(layer.key_blocks), list(layer.value_blocks))
+    torch.cuda.synchronize()
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(6)]
+    ev[0].record()
+    t0 = time.perf_counter()
+    for _ in range(128):
+        cache.append_for_attention(k[:, :, pos:pos + 1], v[:, :, pos:pos + 1], 0,
+                                   {"cache_position": torch.tensor([pos], device=device)})
+        pos += 1
+    ev[1].record()
+    torch.cuda.synchronize()
+    host_us = (time.perf_counter() - t0) * 1e6 / 128
+    for _ in range(383 - 256):           # tail 256 -> 383 (no seal)
+        cache.append_for_attention(k[:, :, pos:pos + 1], v[:, :, pos:pos + 1], 0,
+                                   {"cache_position": torch.tensor([pos], device=device)})
+        pos += 1
+    torch.cuda.synchronize()
+    blocks_before = len(layer.key_blocks)
+    ev[2].record()
+    cache.append_for_attention(k[:, :, pos:pos + 1], v[:, :, pos:pos + 1], 0,
+                               {"cache_position": torch.tensor([pos], device=device)})
+    ev[3].record()
+    assert len(layer.key_blocks) == blocks_before + 1
+    ev[4].record()
+    state.extend(list(layer.key_blocks), list(layer.value_blocks))
+    ev[5].record()
+    torch.cuda.synchronize()
+    seal_bytes = 2 * H * 256 * 128 * 2 + (16384 + 512 + 32 + 64 + 8192 + 2048) * H + 64 + H * 128
+    return {"append_us_per_token": round(ev[0].elapsed_time(ev[1]) * 1e3 / 128, 2),
+            "append_host_us_per_token": round(host_us, 2),
+            "seal_us": round(ev[2].elapsed_time(ev[3]) * 1e3, 2),
+            "metadata_append_us": round(ev[4].elapsed_time(ev[5]) * 1e3, 2),
+            "seal_bytes": seal_bytes}
+
+
 def cpu_baseline(layer):
     """Time the CPU oracle (dequantize-then-attend, fp64) on a bounded sample of one layer."""
     import numpy as np
@@ -360,6 +420,7 @@ def main():
     achieved = per_layer / (layer_us * 1e-6) / 1e9
     enc = time_encode(device)
     paged = None if args.no_paged else time_paged(device)
+    append = time_append(device)
     result = {
         "metric": METRIC,
         "value": round(gbs, 2),
@@ -381,11 +442,12 @@ def main():
         "decode_tokens_per_s": round(1e3 / ms, 2),
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": measured_traffic(),
-                     "kernel": "decode_fast (matrix-core decode with in-kernel partition merge; one launch per layer)",
+                     "kernel": "decode_fast + decode_reduce (matrix-core decode, then the partition merge)",
                      "bytes_per_launch": per_layer},
         "encode_mtok_s": round(enc["encode_mtok_s"], 2),
         "encode": {k: round(v, 3) for k, v in enc.items()},
     }
+    result["append_cfg2"] = append
     if paged is not None:
         result["paged_cfg4"] = paged
     if not args.no_cpu_baseline:

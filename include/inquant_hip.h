@@ -133,22 +133,14 @@ int iq_decode_append(int64_t *tables, int8_t *key_map, int8_t *value_map, int64_
  *   value_bits in {0, 2, 4}, value_group in {32, 64, 128};
  *   sink/tail K/V of q_dtype with (head, token) element strides, lengths
  *   sink_t / tail_t (pointers may be NULL when the length is 0);
- *   workspace f32 with at least iq_decode_workspace_floats(...) elements;
- *   merge_counters (may be NULL) with iq_decode_merge_counter_ints(...) ints;
+ *   workspace f32 with at least iq_decode_workspace_floats(...) elements
+ *   (per-partition partials [Hq, P, 130], merged by a second kernel);
  *   out [Hq, 128] contiguous of out_dtype.
  * Keys/values are decoded and rounded to q_dtype exactly as the reference's
  * dequantize-then-attend path does; logits, softmax and P.V accumulate in
  * fp32.  Replaces PackedDecodeState.decode (triton_attention.py:377-448).
  */
 int64_t iq_decode_workspace_floats(int64_t Hq, int64_t n_blocks, int64_t sink_t, int64_t tail_t);
-
-/*
- * int32 merge counters needed by iq_decode_attention to merge partitions
- * in-kernel (last-arriving workgroups).  The caller allocates them zeroed
- * once; every launch leaves them zero again.  Calls that share counters must
- * be ordered on one stream.  Without counters a second kernel merges.
- */
-int64_t iq_decode_merge_counter_ints(int64_t H, int64_t n_blocks, int64_t sink_t, int64_t tail_t);
 
 int iq_decode_attention(const void *q, int q_dtype, int64_t q_stride_h, int64_t Hq,
                         const int64_t *tables, const int8_t *key_map, const int8_t *value_map,
@@ -159,7 +151,6 @@ int iq_decode_attention(const void *q, int q_dtype, int64_t q_stride_h, int64_t 
                         const void *tail_k, const void *tail_v, int64_t tail_k_sh, int64_t tail_k_st,
                         int64_t tail_v_sh, int64_t tail_v_st, int64_t tail_t,
                         float scale, float *workspace, int64_t workspace_floats,
-                        int *merge_counters, int64_t merge_counter_ints,
                         void *out, int out_dtype, void *stream);
 
 /*

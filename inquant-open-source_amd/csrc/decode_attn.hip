@@ -221,14 +221,15 @@ __global__ __launch_bounds__(DA_THREADS) void decode_partials_generic(DecodeArgs
 
 // Log-sum-exp merge of the partition partials (_reduce_partials, triton_attention.py:168-181).
 // grid (Hq, D / 32): each workgroup merges 32 output channels of one query
-// head; its 256 threads split the partitions 8 ways per channel.
-constexpr int RED_THREADS = 256;
+// head; its 512 threads split the partitions 16 ways per channel, so up to
+// 256 partitions (64K packed tokens) merge in one round of loads.
+constexpr int RED_THREADS = 512;
 constexpr int RED_COLS = 32;
 constexpr int RED_PARTS = RED_THREADS / RED_COLS;
 
-// Each thread merges every 8th partition of one channel: all loads of a
+// Each thread merges every 16th partition of one channel: all loads of a
 // round of 16 partitions are issued before any dependent arithmetic, then the
-// 8 running (max, weighted sum, normalizer) states merge through LDS.
+// 16 running (max, weighted sum, normalizer) states merge through LDS.
 constexpr int RED_BATCH = 16;
 
 __global__ __launch_bounds__(RED_THREADS) void decode_reduce(const float *ws, int64_t P, void *out, int odt)
@@ -240,16 +241,25 @@ __global__ __launch_bounds__(RED_THREADS) void decode_reduce(const float *ws, in
     const float *base = ws + hq * P * (D + 2);
     const float ninf = -__uint_as_float(0x7f800000u);
     float m = ninf, num = 0.0f, den = 0.0f;
-    for (int64_t p0 = part; p0 < P; p0 += RED_PARTS * RED_BATCH) {
+    for (int p0 = part; p0 < (int)P; p0 += RED_PARTS * RED_BATCH) {
+        // every load of the round first (clamped rows, 32-bit offsets), the
+        // masks after: a load consumed under a condition right away would be
+        // waited for one at a time
         float mv[RED_BATCH], lv[RED_BATCH], av[RED_BATCH];
 #pragma unroll
         for (int k = 0; k < RED_BATCH; ++k) {
-            const int64_t pp = p0 + (int64_t)RED_PARTS * k;
-            const bool ok = pp < P;
-            const float *r = base + (ok ? pp : 0) * (D + 2);
-            mv[k] = ok ? r[D] : ninf;
-            lv[k] = ok ? r[D + 1] : 0.0f;
-            av[k] = ok ? r[c0 + c] : 0.0f;
+            const int pp = min(p0 + RED_PARTS * k, (int)P - 1);
+            const float *r = base + pp * (D + 2);
+            mv[k] = r[D];
+            lv[k] = r[D + 1];
+            av[k] = r[c0 + c];
+        }
+#pragma unroll
+        for (int k = 0; k < RED_BATCH; ++k) {
+            const bool ok = p0 + RED_PARTS * k < (int)P;
+            mv[k] = ok ? mv[k] : ninf;
+            lv[k] = ok ? lv[k] : 0.0f;
+            av[k] = ok ? av[k] : 0.0f;
         }
         float mm = m;
 #pragma unroll
@@ -293,9 +303,7 @@ int iq_decode_fast_launch(const void *q, int q_dtype, int64_t q_stride_h, int64_
                           int64_t sink_k_st, int64_t sink_v_sh, int64_t sink_v_st, int64_t sink_t,
                           const void *tail_k, const void *tail_v, int64_t tail_k_sh, int64_t tail_k_st,
                           int64_t tail_v_sh, int64_t tail_v_st, int64_t tail_t, float scale, float *workspace,
-                          int64_t P, int *counters, int64_t counter_ints, void *out, int out_dtype,
-                          int *merged, hipStream_t stream);
-int64_t iq_decode_merge_ints(int64_t H, int64_t P);
+                          int64_t P, void *out, int out_dtype, int *merged, hipStream_t stream);
 
 namespace {
 
@@ -311,10 +319,6 @@ extern "C" int64_t iq_decode_workspace_floats(int64_t Hq, int64_t n_blocks, int6
     return Hq * partitions(n_blocks, sink_t, tail_t) * (D + 2);
 }
 
-extern "C" int64_t iq_decode_merge_counter_ints(int64_t H, int64_t n_blocks, int64_t sink_t, int64_t tail_t)
-{
-    return iq_decode_merge_ints(H, partitions(n_blocks, sink_t, tail_t));
-}
 
 extern "C" int iq_decode_attention(const void *q, int q_dtype, int64_t q_stride_h, int64_t Hq,
                                    const int64_t *tables, const int8_t *key_map, const int8_t *value_map,
@@ -323,8 +327,8 @@ extern "C" int iq_decode_attention(const void *q, int q_dtype, int64_t q_stride_
                                    int64_t sink_k_st, int64_t sink_v_sh, int64_t sink_v_st, int64_t sink_t,
                                    const void *tail_k, const void *tail_v, int64_t tail_k_sh, int64_t tail_k_st,
                                    int64_t tail_v_sh, int64_t tail_v_st, int64_t tail_t, float scale,
-                                   float *workspace, int64_t workspace_floats, int *merge_counters,
-                                   int64_t merge_counter_ints, void *out, int out_dtype, void *stream)
+                                   float *workspace, int64_t workspace_floats, void *out, int out_dtype,
+                                   void *stream)
 {
     IQ_CHECK_ARG(q && out && workspace, "iq_decode_attention: null pointer");
     IQ_CHECK_ARG(q_dtype >= IQ_F32 && q_dtype <= IQ_F16, "iq_decode_attention: bad query dtype");
@@ -351,8 +355,8 @@ extern "C" int iq_decode_attention(const void *q, int q_dtype, int64_t q_stride_
     const int fast = iq_decode_fast_launch(q, q_dtype, q_stride_h, Hq, tables, key_map, n_blocks, block_tokens, H,
                                            S, value_bits, value_group, sink_k, sink_v, sink_k_sh, sink_k_st,
                                            sink_v_sh, sink_v_st, sink_t, tail_k, tail_v, tail_k_sh, tail_k_st,
-                                           tail_v_sh, tail_v_st, tail_t, scale, workspace, P, merge_counters,
-                                           merge_counter_ints, out, out_dtype, &merged, (hipStream_t)stream);
+                                           tail_v_sh, tail_v_st, tail_t, scale, workspace, P, out, out_dtype, &merged,
+                                           (hipStream_t)stream);
     if (fast == IQ_OK) {
         IQ_CHECK_LAUNCH("decode_fast");
         if (merged) return IQ_OK;

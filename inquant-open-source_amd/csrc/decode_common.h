@@ -1,7 +1,6 @@
 // Device helpers shared by the fused decode kernels (gfx950): bf16/f16
 // packing, matrix-core wrappers, exact fp8 nibble conversion, 16-lane
-// reductions, global-address-space loads and the agent-coherent partial
-// exchange between workgroups.
+// reductions and global-address-space loads.
 #pragma once
 
 #include "iq_common.h"
@@ -92,46 +91,6 @@ __device__ __forceinline__ T ldg(const void *p)
 
 __device__ __forceinline__ u32x4 ld16(const void *p) { return ldg<u32x4>(p); }
 
-// Partials exchanged between workgroups use agent-coherent stores and loads
-// (sc1: written through / read past the per-XCD L2), so publishing them costs
-// a wait for store completion instead of an L2 write-back fence.
-__device__ __forceinline__ void st_agent(float *p, float v)
-{
-    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-__device__ __forceinline__ float ld_agent(const float *p)
-{
-    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-// Returns true in the workgroup whose arrival completes `expected` arrivals.
-// Every thread's agent-coherent stores have completed before the increment.
-__device__ __forceinline__ bool arrive_last(int *counter, int expected, int *flag)
-{
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
-    if (threadIdx.x == 0)
-        *flag = __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == expected - 1;
-    __syncthreads();
-    return *flag;
-}
-
 constexpr float NEG_INF = -__builtin_inff();
-
-// Reduction over the 16 consecutive lanes that share one query row.
-__device__ __forceinline__ float rowmax16(float v)
-{
-#pragma unroll
-    for (int o = 1; o < 16; o <<= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
-    return v;
-}
-
-__device__ __forceinline__ float rowsum16(float v)
-{
-#pragma unroll
-    for (int o = 1; o < 16; o <<= 1) v += __shfl_xor(v, o, 64);
-    return v;
-}
 
 }  // namespace

@@ -35,7 +35,6 @@ constexpr int KROW = 17;               // dwords per staged K row (16 + 1: confl
 constexpr int KC_STRIDE = 68;          // float2 slots per 32-channel group of K constants (+4: no bank overlap)
 constexpr int DENSE_SPLIT = 256;
 constexpr float LN2 = 0.693147180559945309f;
-constexpr int MERGE_GROUP = 16;        // partitions merged by the last-arriving workgroup of a group
 
 struct FastArgs {
     const uint16_t *q;
@@ -52,100 +51,9 @@ struct FastArgs {
     float c_log2;    // softmax scale * log2(e)
     float *ws;
     int64_t P;
-    int *cnt;        // merge counters [H][ngrp + 1] (zero between launches), or null
-    int ngrp;        // partition groups of MERGE_GROUP per KV head
-    void *out;       // final [Hq, 128] output when merged in this kernel
+    void *out;       // final [Hq, 128] output when there is one partition
     int odt;
 };
-
-// Log-sum-exp merge of `count` partials (partition p_first + k * stride) of
-// query rows g0 .. g0 + gn - 1 of kv head h (gn <= 8), in chunks of
-// MERGE_GROUP.  Every load of a chunk is issued before any of its arithmetic:
-// the accumulator values of this thread's output channels first, then the
-// (m, l) pair of partial k = tid % 16 of row g0 + tid / 16.  Row maxima and
-// denominators reduce over the 16 lanes of a row; the weights reach the
-// threads that own the channels through LDS (`sm`, 16 * MERGE_GROUP + 48
-// floats of the caller's free staging memory).  Writes the merged rows to
-// partition p_first, or the normalized output when final_out.
-template <int ITEMS>
-__device__ __forceinline__ void merge_rows(const FastArgs &a, float *sm, int h, int G, int g0, int gn,
-                                           int64_t p_first, int64_t stride, int count, bool final_out)
-{
-    float *s_w = sm, *s_alpha = sm + 16 * MERGE_GROUP, *s_den = s_alpha + 16, *s_mx = s_den + 16;
-    const int tid = threadIdx.x;
-    const int mg = tid >> 4, mk = tid & 15;
-    const int64_t pstride = stride * (D + 2);
-    const float *hbase = a.ws + ((int64_t)(h * G + g0) * a.P + p_first) * (D + 2);
-    float mx = NEG_INF, den = 0.0f;
-    float num[ITEMS];
-#pragma unroll
-    for (int it = 0; it < ITEMS; ++it) num[it] = 0.0f;
-
-    for (int k0 = 0; k0 < count; k0 += MERGE_GROUP) {
-        const int n = min(MERGE_GROUP, count - k0);
-        float v[ITEMS][MERGE_GROUP];
-#pragma unroll
-        for (int it = 0; it < ITEMS; ++it) {
-            const int i = min(tid + 256 * it, gn * D - 1);
-            const float *r = hbase + (int64_t)(i >> 7) * a.P * (D + 2) + k0 * pstride + (i & (D - 1));
-#pragma unroll
-            for (int k = 0; k < MERGE_GROUP; ++k) v[it][k] = ld_agent(r + min(k, n - 1) * pstride);
-        }
-        const bool mine = mg < gn && mk < n;
-        const float *rm = hbase + (int64_t)(mine ? mg : 0) * a.P * (D + 2) + (k0 + (mine ? mk : 0)) * pstride + D;
-        const float m0 = ld_agent(rm), l0 = ld_agent(rm + 1);
-        const float m = mine ? m0 : NEG_INF, l = mine ? l0 : 0.0f;
-        const float nm = fmaxf(mx, rowmax16(m));
-        const float alpha = mx == nm ? 1.0f : __expf(mx - nm);
-        const float w = m == NEG_INF ? 0.0f : __expf(m - nm);
-        den = fmaf(den, alpha, rowsum16(w * l));
-        mx = nm;
-        s_w[tid] = w;
-        if (mk == 0) s_alpha[mg] = alpha;
-        __syncthreads();
-#pragma unroll
-        for (int it = 0; it < ITEMS; ++it) {
-            const int g = min(tid + 256 * it, gn * D - 1) >> 7;
-            float acc = num[it] * s_alpha[g];
-#pragma unroll
-            for (int k = 0; k < MERGE_GROUP; ++k) acc = fmaf(v[it][k], s_w[g * MERGE_GROUP + k], acc);
-            num[it] = acc;
-        }
-        __syncthreads();
-    }
-    if (mk == 0 && mg < gn) {
-        s_den[mg] = den;
-        s_mx[mg] = mx;
-    }
-    __syncthreads();
-#pragma unroll
-    for (int it = 0; it < ITEMS; ++it) {
-        const int i = tid + 256 * it;
-        if (i >= gn * D) continue;
-        const int g = i >> 7, c = i & (D - 1);
-        if (final_out) {
-            iq_store_as(a.out, (int64_t)(h * G + g0 + g) * D + c, num[it] / s_den[g], a.odt);
-        } else {
-            float *row = a.ws + ((int64_t)(h * G + g0 + g) * a.P + p_first) * (D + 2);
-            st_agent(row + c, num[it]);
-            if (c == 0) {
-                st_agent(row + D, s_mx[g]);
-                st_agent(row + D + 1, s_den[g]);
-            }
-        }
-    }
-    __syncthreads();
-}
-
-__device__ __forceinline__ void merge_partials(const FastArgs &a, float *sm, int h, int G, int64_t p_first,
-                                               int64_t stride, int count, bool final_out)
-{
-    if (G <= 2) merge_rows<1>(a, sm, h, G, 0, G, p_first, stride, count, final_out);
-    else if (G <= 4) merge_rows<2>(a, sm, h, G, 0, G, p_first, stride, count, final_out);
-    else
-        for (int g0 = 0; g0 < G; g0 += 8)
-            merge_rows<4>(a, sm, h, G, g0, min(8, G - g0), p_first, stride, count, final_out);
-}
 
 template <bool F16, int VBITS>
 __global__ __launch_bounds__(256, 3) void decode_fast(FastArgs a)
@@ -573,47 +481,28 @@ __global__ __launch_bounds__(256, 3) void decode_fast(FastArgs a)
             continue;
         }
         float *out = a.ws + ((int64_t)(h * G + g) * a.P + p) * (D + 2);
-        st_agent(out + c, num);
+        out[c] = num;
         if (c == 0) {
-            st_agent(out + D, mx * LN2);
-            st_agent(out + D + 1, den);
+            out[D] = mx * LN2;
+            out[D + 1] = den;
         }
     }
-    if (a.P == 1 || a.cnt == nullptr) return;
-
-    // ---------------- last-arriving workgroups merge: first per group of
-    // MERGE_GROUP partitions (into the group's first slot), then per KV head
-    __shared__ int s_last;
-    float *sm = (float *)s_v[0];           // free once every wave is past its combine reads
-    const int grp = (int)(p / MERGE_GROUP);
-    const int gsize = (int)min((int64_t)MERGE_GROUP, a.P - (int64_t)grp * MERGE_GROUP);
-    int *cnt = a.cnt + h * (a.ngrp + 1);
-    if (!arrive_last(cnt + grp, gsize, &s_last)) return;
-    if (tid == 0) __hip_atomic_store(cnt + grp, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    merge_partials(a, sm, h, G, (int64_t)grp * MERGE_GROUP, 1, gsize, a.ngrp == 1);
-    if (a.ngrp == 1) return;
-    if (!arrive_last(cnt + a.ngrp, a.ngrp, &s_last)) return;
-    if (tid == 0) __hip_atomic_store(cnt + a.ngrp, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    merge_partials(a, sm, h, G, 0, MERGE_GROUP, a.ngrp, true);
 }
 
 }  // namespace
 
 #undef IQ_LOAD_CHUNK
 
-int64_t iq_decode_merge_ints(int64_t H, int64_t P) { return H * ((P + MERGE_GROUP - 1) / MERGE_GROUP + 1); }
-
 // Launches the matrix-core decode; returns IQ_ERR_UNSUPPORTED for layouts it
-// does not cover.  *merged = 1 when the output was written in-kernel,
-// 0 when the caller must run the separate partial reduction.
+// does not cover.  *merged = 1 when the output was written in-kernel (a single
+// partition), 0 when the caller must run the partial reduction.
 int iq_decode_fast_launch(const void *q, int q_dtype, int64_t q_stride_h, int64_t Hq, const int64_t *tables,
                           const int8_t *key_map, int64_t n_blocks, int64_t block_tokens, int64_t H, int64_t S,
                           int value_bits, int value_group, const void *sink_k, const void *sink_v, int64_t sink_k_sh,
                           int64_t sink_k_st, int64_t sink_v_sh, int64_t sink_v_st, int64_t sink_t,
                           const void *tail_k, const void *tail_v, int64_t tail_k_sh, int64_t tail_k_st,
                           int64_t tail_v_sh, int64_t tail_v_st, int64_t tail_t, float scale, float *workspace,
-                          int64_t P, int *counters, int64_t counter_ints, void *out, int out_dtype,
-                          int *merged, hipStream_t stream)
+                          int64_t P, void *out, int out_dtype, int *merged, hipStream_t stream)
 {
     if (q_dtype != IQ_BF16 && q_dtype != IQ_F16) return IQ_ERR_UNSUPPORTED;
     if (out_dtype != IQ_F32 && out_dtype != IQ_BF16 && out_dtype != IQ_F16) return IQ_ERR_UNSUPPORTED;
@@ -633,14 +522,8 @@ int iq_decode_fast_launch(const void *q, int q_dtype, int64_t q_stride_h, int64_
                value_group ? value_group : 64, (const uint16_t *)sink_k, (const uint16_t *)sink_v, sink_k_sh,
                sink_k_st, sink_v_sh, sink_v_st, sink_t, (const uint16_t *)tail_k, (const uint16_t *)tail_v,
                tail_k_sh, tail_k_st, tail_v_sh, tail_v_st, tail_t, scale * 1.44269504088896341f, workspace, P,
-               nullptr, 0, out, out_dtype};
-    const int64_t ngrp = (P + MERGE_GROUP - 1) / MERGE_GROUP;
+               out, out_dtype};
     *merged = P == 1;
-    if (P > 1 && counters && counter_ints >= H * (ngrp + 1)) {
-        a.cnt = counters;       // merged in-kernel by the last-arriving workgroups
-        a.ngrp = (int)ngrp;
-        *merged = 1;
-    }
     const dim3 grid((unsigned)H, (unsigned)P), block(256);
     const bool f16 = q_dtype == IQ_F16;
     const int vb = n_blocks > 0 ? value_bits : 2;

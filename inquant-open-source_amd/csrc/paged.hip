@@ -596,15 +596,21 @@ __global__ __launch_bounds__(256) void paged_reduce(PagedArgs a, void *out, int6
     const float *base = a.ws + ((int64_t)sq * a.H * a.G + hq) * a.max_parts * (D + 2);
     float m = NEG_INF, num = 0.0f, den = 0.0f;
     for (int p0 = part; p0 < P; p0 += 8 * 16) {
+        // every load of the round first, the masks after (see decode_reduce)
         float mv[16], lv[16], av[16];
 #pragma unroll
         for (int k = 0; k < 16; ++k) {
-            const int pp = p0 + 8 * k;
-            const bool ok = pp < P;
-            const float *r = base + (int64_t)(ok ? pp : 0) * (D + 2);
-            mv[k] = ok ? r[D] : NEG_INF;
-            lv[k] = ok ? r[D + 1] : 0.0f;
-            av[k] = ok ? r[c0 + c] : 0.0f;
+            const float *r = base + min(p0 + 8 * k, P - 1) * (D + 2);
+            mv[k] = r[D];
+            lv[k] = r[D + 1];
+            av[k] = r[c0 + c];
+        }
+#pragma unroll
+        for (int k = 0; k < 16; ++k) {
+            const bool ok = p0 + 8 * k < P;
+            mv[k] = ok ? mv[k] : NEG_INF;
+            lv[k] = ok ? lv[k] : 0.0f;
+            av[k] = ok ? av[k] : 0.0f;
         }
         float mm = m;
 #pragma unroll

@@ -42,11 +42,10 @@ _SIGNATURES = {
     "iq_v_dequantize": (_int, [_p, _p, _p, _i64, _i64, _int, _int, _p, _int, _p]),
     "iq_decode_append": (_int, [_p, _p, _p, _i64, _i64, ctypes.POINTER(BlockPtrs), _i64, _i64, _int, _p]),
     "iq_decode_workspace_floats": (_i64, [_i64, _i64, _i64, _i64]),
-    "iq_decode_merge_counter_ints": (_i64, [_i64, _i64, _i64, _i64]),
     "iq_decode_attention": (_int, [_p, _int, _i64, _i64, _p, _p, _p, _i64, _i64, _i64, _i64, _int, _int,
                                    _p, _p, _i64, _i64, _i64, _i64, _i64,
                                    _p, _p, _i64, _i64, _i64, _i64, _i64,
-                                   _f32, _p, _i64, _p, _i64, _p, _int, _p]),
+                                   _f32, _p, _i64, _p, _int, _p]),
     "iq_page_bytes": (_i64, [_i64, _i64]),
     "iq_write_pages": (_int, [_p, _p, _p, _p, _p, _int, _p, _p, _p, _i64, _i64, _i64, _p, _i64, _p, _int, _p]),
     "iq_unpack_pages": (_int, [_p, _i64, _i64, _i64, _p, _p, _int, _p]),

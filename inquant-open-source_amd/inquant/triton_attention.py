@@ -78,9 +78,6 @@ class PackedDecodeState:
         self._value_group = 64
         self._capacity = 0
         self._stream_identity = None
-        # int32 counters that let the last-arriving workgroups merge partitions
-        # inside the decode kernel; zero between calls (each launch resets them)
-        self._merge = None
         self.extend(key_blocks, value_blocks)
 
     def extend(self, key_blocks, value_blocks):
@@ -167,7 +164,7 @@ class PackedDecodeState:
     def nbytes(self) -> int:
         """Auxiliary GPU allocations of this state (tables, maps, private workspace)."""
         return sum(t.untyped_storage().nbytes() for t in
-                   (self._tables, self._key_map, self._value_map, self._workspace, self._merge) if t is not None)
+                   (self._tables, self._key_map, self._value_map, self._workspace) if t is not None)
 
     @torch.no_grad()
     def decode(self, query, *, sink_key=None, sink_value=None, residual_key=None, residual_value=None,
@@ -238,11 +235,6 @@ class PackedDecodeState:
         n_blocks = len(self.key_blocks)
         stream = nat.stream_handle(query.device)
         lib = nat.lib()
-        need = lib.iq_decode_merge_counter_ints(kv_heads, n_blocks, sink_t, tail_t)
-        if partitions > 1 and (self._merge is None or self._merge.numel() < need
-                               or self._merge.device != query.device):
-            self._merge = torch.zeros(-(-need // 64) * 64, dtype=torch.int32, device=query.device)
-        merge = self._merge if partitions > 1 else None
 
         def st(t, dim):
             return 0 if t is None else t.stride(dim)
@@ -254,8 +246,8 @@ class PackedDecodeState:
             n_blocks, self._packed_tokens, kv_heads, self._salient, self._value_bits, self._value_group,
             nat.ptr(sk), nat.ptr(sv), st(sk, 1), st(sk, 2), st(sv, 1), st(sv, 2), sink_t,
             nat.ptr(tk), nat.ptr(tv), st(tk, 1), st(tk, 2), st(tv, 1), st(tv, 2), tail_t,
-            float(scale), workspace.data_ptr(), workspace.numel(), nat.ptr(merge),
-            0 if merge is None else merge.numel(), output.data_ptr(), nat.dtype_code(output.dtype), stream))
+            float(scale), workspace.data_ptr(), workspace.numel(), output.data_ptr(),
+            nat.dtype_code(output.dtype), stream))
         return output
 
 

@@ -37,8 +37,7 @@ def test_k4_values_with_sink_and_unsealed_tail(dtype, fraction, policy):
     # the typed result is the fp32 result rounded once
     expect_typed = torch.from_numpy(got).to("cuda").to(dtype).view_as(typed)
     assert torch.equal(typed, expect_typed)
-    merge_bytes = 0 if state._merge is None else state._merge.numel() * 4
-    assert state.nbytes == descriptor_bytes + state._workspace.numel() * 4 + merge_bytes
+    assert state.nbytes == descriptor_bytes + state._workspace.numel() * 4
     pointer = state._workspace.data_ptr()
     state.decode(case.query, **case.kwargs())
     assert state._workspace.data_ptr() == pointer
@@ -138,8 +137,8 @@ def test_growing_state_matches_fresh_state_and_rejects_replacement():
         assert state._key_map.dtype == torch.int8
         assert torch.equal(state._key_map[:i + 1], fresh._key_map[:i + 1])
         assert state.nbytes == sum(x.untyped_storage().nbytes() for x in
-                                   (state._tables, state._key_map, state._value_map, state._workspace,
-                                    state._merge) if x is not None)
+                                   (state._tables, state._key_map, state._value_map, state._workspace)
+                                   if x is not None)
     with pytest.raises(ValueError, match="append-only"):
         state.extend(keys[:-1], values[:-1])
     with pytest.raises(ValueError, match="append-only"):
@@ -224,12 +223,11 @@ def test_matrix_core_path_peaked_attention_keeps_precision():
 
 def test_cfg2_full_context_matches_oracle_and_is_repeatable():
     # BASELINE config 2 layer: 128 packed blocks (32768 tokens) + 4 sink + 128 tail;
-    # 130 partitions merged in-kernel by the last-arriving workgroups
+    # 130 partitions merged by the reduction kernel
     from inquant.triton_attention import PackedDecodeState
     case = make_case(2, n_blocks=128, sink=4, tail=128)
     state = PackedDecodeState(case.key_blocks, case.value_blocks)
     outs = [_decode_f32(state, case) for _ in range(4)]
     for o in outs[1:]:
-        assert np.array_equal(o, outs[0])            # merge order is fixed, not arrival order
-    assert state._merge is not None and not state._merge.any()   # counters reset by every launch
+        assert np.array_equal(o, outs[0])            # the merge order is fixed
     np.testing.assert_allclose(outs[0], case.expected(), atol=ATOL, rtol=0)
