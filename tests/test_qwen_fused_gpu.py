@@ -1,0 +1,100 @@
+"""Qwen2 / Mistral adapters on the GPU: the patched single-token forward runs the
+fused HIP decode and matches the model's own forward over the materialized
+(dequantize-then-attend) cache (restates test_qwen_fused.py:112-146)."""
+import copy
+from unittest.mock import patch
+
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+
+
+def _qwen(head_dim=128, layers=1):
+    from transformers import Qwen2Config, Qwen2ForCausalLM
+    return Qwen2ForCausalLM(Qwen2Config(
+        vocab_size=97, hidden_size=4 * head_dim, intermediate_size=8 * head_dim, num_hidden_layers=layers,
+        num_attention_heads=4, num_key_value_heads=2, max_position_embeddings=65536, bos_token_id=1,
+        eos_token_id=96, pad_token_id=0, attn_implementation="sdpa")).eval()
+
+
+def _mistral(layers=1):
+    from transformers import MistralConfig, MistralForCausalLM
+    return MistralForCausalLM(MistralConfig(
+        vocab_size=97, hidden_size=512, intermediate_size=1024, num_hidden_layers=layers, num_attention_heads=8,
+        num_key_value_heads=2, head_dim=128, max_position_embeddings=65536, sliding_window=None,
+        bos_token_id=1, eos_token_id=96, pad_token_id=0, attn_implementation="sdpa")).eval()
+
+
+@pytest.mark.parametrize("family", ["qwen2", "mistral"])
+@pytest.mark.parametrize("prefill_tokens", [3, 98])
+def test_packed_kernel_logits_and_auxiliary_accounting(family, prefill_tokens):
+    from inquant.cache import CacheConfig, InQuantCache
+    from inquant.codec import CodecConfig
+    from inquant.qwen_fused import enable_fused_attention
+    torch.manual_seed(37)
+    model = (_qwen() if family == "qwen2" else _mistral()).to(device="cuda", dtype=torch.bfloat16)
+    reference_model = copy.deepcopy(model)
+    config = CacheConfig(CodecConfig(salient_fraction=.125), block_size=32, residual_length=4, sink_tokens=2)
+    with enable_fused_attention(model) as handle, torch.no_grad():
+        reference, packed = InQuantCache(config), InQuantCache(config)
+        tokens = torch.randint(2, 90, (1, prefill_tokens), device="cuda")
+        expected = reference_model(tokens, past_key_values=reference).logits
+        actual = model(tokens, past_key_values=packed).logits
+        assert torch.equal(actual, expected)
+        for step in range(7):
+            token = torch.tensor([[3 + step]], device="cuda")
+            expected = reference_model(token, past_key_values=reference).logits
+            with patch.object(packed, "materialize", side_effect=AssertionError("Unexpected full materialization")):
+                actual = model(token, past_key_values=packed).logits
+            torch.testing.assert_close(actual.float(), expected.float(), rtol=.035, atol=.012)
+            assert packed.get_seq_length() == reference.get_seq_length()
+        assert handle.fused_decode_calls == 7 and handle.cpu_reference_calls == 0
+        assert packed.auxiliary_nbytes > 0
+        stats = packed.memory_stats()
+        assert stats["nbytes"] == sum(stats[name] for name in (
+            "payload_nbytes", "metadata_nbytes", "residual_nbytes", "sink_nbytes", "auxiliary_nbytes"))
+        if prefill_tokens == 3:
+            assert stats["quantized_layer_tokens"] == 0
+        packed.release()
+        assert packed.auxiliary_nbytes == 0
+
+
+def test_generate_patch_restore_and_rejections():
+    from inquant.cache import CacheConfig, InQuantCache
+    from inquant.codec import CodecConfig
+    from inquant.qwen_fused import enable_fused_mistral, enable_fused_qwen2
+    torch.manual_seed(41)
+    model = _qwen(layers=2).to(device="cuda", dtype=torch.bfloat16)
+    original = model.model.layers[0].self_attn.forward
+    config = CacheConfig(CodecConfig(salient_fraction=.125), block_size=16, residual_length=4, sink_tokens=2)
+    handle = enable_fused_qwen2(model)
+    tokens = torch.randint(2, 90, (1, 40), device="cuda")
+    with torch.no_grad():
+        generated = model.generate(tokens, attention_mask=torch.ones_like(tokens), past_key_values=InQuantCache(config),
+                                   do_sample=False, num_beams=1, max_new_tokens=4, min_new_tokens=4)
+    assert tuple(generated.shape) == (1, 44)
+    with pytest.raises(ValueError, match="already"):
+        enable_fused_qwen2(model)
+    with pytest.raises(ValueError, match="Mistral"):
+        enable_fused_mistral(model)
+    handle.restore()
+    handle.restore()
+    assert model.model.layers[0].self_attn.forward == original
+    model.train()
+    with pytest.raises(ValueError, match="eval"):
+        enable_fused_qwen2(model)
+    with pytest.raises(ValueError, match="head_dim=128"):
+        enable_fused_qwen2(_qwen(head_dim=64).to("cuda"))
+
+
+def test_grad_mode_is_refused():
+    from inquant.cache import InQuantCache
+    from inquant.qwen_fused import enable_fused_qwen2
+    model = _qwen().to(device="cuda", dtype=torch.bfloat16)
+    cache = InQuantCache()
+    with enable_fused_qwen2(model):
+        with torch.no_grad():
+            model(torch.tensor([[2, 3, 4]], device="cuda"), past_key_values=cache)
+        with pytest.raises(RuntimeError, match="inference-only"):
+            model(torch.tensor([[5]], device="cuda"), past_key_values=cache)
