@@ -223,21 +223,24 @@ __global__ __launch_bounds__(DA_THREADS) void decode_partials_generic(DecodeArgs
 // grid (Hq, D / 32): each workgroup merges 32 output channels of one query
 // head; its 512 threads split the partitions 16 ways per channel, so up to
 // 256 partitions (64K packed tokens) merge in one round of loads.
-constexpr int RED_THREADS = 512;
-constexpr int RED_COLS = 32;
+constexpr int RED_THREADS = 256;
+constexpr int RED_COLS = 16;
 constexpr int RED_PARTS = RED_THREADS / RED_COLS;
 
 // Each thread merges every 16th partition of one channel: all loads of a
-// round of 16 partitions are issued before any dependent arithmetic, then the
-// 16 running (max, weighted sum, normalizer) states merge through LDS.
+// round of 16 partitions are issued before any dependent arithmetic.  The 16
+// running (max, weighted sum, normalizer) states of a channel then merge in
+// two steps: the workgroup max (lane shuffles, then LDS across the four
+// wavefronts), and a sum of the states rescaled to it.
 constexpr int RED_BATCH = 16;
 
 __global__ __launch_bounds__(RED_THREADS) void decode_reduce(const float *ws, int64_t P, void *out, int odt)
 {
-    __shared__ float s_m[RED_THREADS], s_n[RED_THREADS], s_l[RED_THREADS];
+    __shared__ float s_m[RED_THREADS / 64][RED_COLS], s_n[RED_THREADS / 64][RED_COLS],
+        s_l[RED_THREADS / 64][RED_COLS];
     const int64_t hq = blockIdx.x;
     const int c0 = blockIdx.y * RED_COLS;
-    const int tid = threadIdx.x, c = tid % RED_COLS, part = tid / RED_COLS;
+    const int tid = threadIdx.x, c = tid % RED_COLS, part = tid / RED_COLS, lane = tid & 63, wave = tid >> 6;
     const float *base = ws + hq * P * (D + 2);
     const float ninf = -__uint_as_float(0x7f800000u);
     float m = ninf, num = 0.0f, den = 0.0f;
@@ -276,22 +279,33 @@ __global__ __launch_bounds__(RED_THREADS) void decode_reduce(const float *ws, in
         }
         m = mm;
     }
-    s_m[tid] = m;
-    s_n[tid] = num;
-    s_l[tid] = den;
+    // lanes c, c + 16, c + 32, c + 48 of a wavefront hold four parts of channel c
+    float mw = fmaxf(m, __shfl_xor(m, 16, 64));
+    mw = fmaxf(mw, __shfl_xor(mw, 32, 64));
+    if (lane < RED_COLS) s_m[wave][c] = mw;
+    __syncthreads();
+    float mm = s_m[0][c];
+#pragma unroll
+    for (int w = 1; w < RED_THREADS / 64; ++w) mm = fmaxf(mm, s_m[w][c]);
+    const float wt = m == ninf ? 0.0f : __expf(m - mm);
+    float n = num * wt, d = den * wt;
+    n += __shfl_xor(n, 16, 64);
+    d += __shfl_xor(d, 16, 64);
+    n += __shfl_xor(n, 32, 64);
+    d += __shfl_xor(d, 32, 64);
+    if (lane < RED_COLS) {
+        s_n[wave][c] = n;
+        s_l[wave][c] = d;
+    }
     __syncthreads();
     if (tid < RED_COLS) {
-        float mm = ninf;
-        for (int k = 0; k < RED_PARTS; ++k) mm = fmaxf(mm, s_m[k * RED_COLS + tid]);
-        float nn = 0.0f, dd = 0.0f;
-        for (int k = 0; k < RED_PARTS; ++k) {
-            const float mk = s_m[k * RED_COLS + tid];
-            if (mk == ninf) continue;
-            const float w = __expf(mk - mm);
-            nn = fmaf(s_n[k * RED_COLS + tid], w, nn);
-            dd = fmaf(s_l[k * RED_COLS + tid], w, dd);
+        float nn = s_n[0][c], dd = s_l[0][c];
+#pragma unroll
+        for (int w = 1; w < RED_THREADS / 64; ++w) {
+            nn += s_n[w][c];
+            dd += s_l[w][c];
         }
-        iq_store_as(out, hq * D + c0 + tid, nn / dd, odt);
+        iq_store_as(out, hq * D + c0 + c, nn / dd, odt);
     }
 }
 
@@ -303,7 +317,7 @@ int iq_decode_fast_launch(const void *q, int q_dtype, int64_t q_stride_h, int64_
                           int64_t sink_k_st, int64_t sink_v_sh, int64_t sink_v_st, int64_t sink_t,
                           const void *tail_k, const void *tail_v, int64_t tail_k_sh, int64_t tail_k_st,
                           int64_t tail_v_sh, int64_t tail_v_st, int64_t tail_t, float scale, float *workspace,
-                          int64_t P, void *out, int out_dtype, int *merged, hipStream_t stream);
+                          void *out, int out_dtype, int64_t *parts, hipStream_t stream);
 
 namespace {
 
@@ -351,15 +365,15 @@ extern "C" int iq_decode_attention(const void *q, int q_dtype, int64_t q_stride_
     IQ_CHECK_ARG(workspace_floats >= Hq * P * (D + 2), "iq_decode_attention: workspace too small");
     // Matrix-core path for bf16/f16 queries with V2/V4 values; the general
     // kernel covers fp32 queries and K4-coded values.
-    int merged = 0;
+    int64_t parts = P;
     const int fast = iq_decode_fast_launch(q, q_dtype, q_stride_h, Hq, tables, key_map, n_blocks, block_tokens, H,
                                            S, value_bits, value_group, sink_k, sink_v, sink_k_sh, sink_k_st,
                                            sink_v_sh, sink_v_st, sink_t, tail_k, tail_v, tail_k_sh, tail_k_st,
-                                           tail_v_sh, tail_v_st, tail_t, scale, workspace, P, out, out_dtype, &merged,
+                                           tail_v_sh, tail_v_st, tail_t, scale, workspace, out, out_dtype, &parts,
                                            (hipStream_t)stream);
     if (fast == IQ_OK) {
         IQ_CHECK_LAUNCH("decode_fast");
-        if (merged) return IQ_OK;
+        if (parts == 1) return IQ_OK;
     } else {
         DecodeArgs a{q, q_dtype, q_stride_h, Hq, tables, key_map, value_map, n_blocks, block_tokens, H, S,
                      value_bits, value_group, sink_k, sink_v, sink_k_sh, sink_k_st, sink_v_sh, sink_v_st, sink_t,
@@ -370,7 +384,7 @@ extern "C" int iq_decode_attention(const void *q, int q_dtype, int64_t q_stride_
         IQ_CHECK_LAUNCH("decode_partials_generic");
     }
     hipLaunchKernelGGL(decode_reduce, dim3((unsigned)Hq, D / RED_COLS), dim3(RED_THREADS), 0, (hipStream_t)stream,
-                       workspace, P, out, out_dtype);
+                       workspace, parts, out, out_dtype);
     IQ_CHECK_LAUNCH("decode_reduce");
     return IQ_OK;
 }

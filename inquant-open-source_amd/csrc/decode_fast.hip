@@ -31,6 +31,7 @@ constexpr int D = 128;
 constexpr int WAVES = 4;
 constexpr int CHUNK = 64;              // tokens per wavefront per pass
 constexpr int VR = 136;                // dwords per staged token-pair row of decoded V (128 + 8: two passes per read)
+constexpr int OROW = 132;              // floats per staged output row in the combine (128 + 4: conflict-free 16-byte stores)
 constexpr int KROW = 17;               // dwords per staged K row (16 + 1: conflict-free byte gathers)
 constexpr int KC_STRIDE = 68;          // float2 slots per 32-channel group of K constants (+4: no bank overlap)
 constexpr int DENSE_SPLIT = 256;
@@ -55,30 +56,51 @@ struct FastArgs {
     int odt;
 };
 
-template <bool F16, int VBITS>
-__global__ __launch_bounds__(256, 3) void decode_fast(FastArgs a)
+// Workgroup LDS, shared by the packed and the dense instantiation of the body.
+struct __attribute__((aligned(16))) FastSmem {
+    // per wavefront: staged decoded V as [token pair][channel] dwords (two
+    // tokens of one channel per dword); also K staging and the final combine
+    uint32_t v[WAVES][16 * VR];
+    uint16_t q[16 * D];          // query rows (dtype bits), zero beyond G
+    uint16_t qm[16 * D];         // query rows masked at salient/donor channels
+    f32x2 kc[4 * KC_STRIDE];     // per channel (s * 2^9, -8 s)
+    int8_t role[D];
+    uint32_t sal[64];            // src | don << 8
+    uint32_t salw[64];           // gather offsets: src byte, shift, don byte, shift
+    f32x2 salf[64];              // (s_src, -128 s_src)
+    uint16_t qsal[16 * 64];      // Q[g][src_k], zero beyond S
+    float dpad[64];              // padding of donor k, rounded to the query dtype
+    float wm[WAVES][16], wl[WAVES][16];
+};
+
+// One partition.  PACKED and dense partitions are separate instantiations so
+// that neither has a branch between its loads and their first use: a branch
+// join there makes the compiler wait for every load in flight.
+template <bool F16, int VBITS, bool PACKED>
+__device__ __forceinline__ void fast_body(const FastArgs &a, FastSmem &sm)
 {
     constexpr int VROW = D * VBITS / 8;          // V payload bytes per token
     constexpr int VQ = VROW / 4;                 // bytes per 32-channel quarter row
     constexpr int VQW = VQ / 4;                  // dwords per quarter row
 
-    // per wavefront: staged decoded V as [token pair][channel] dwords (two
-    // tokens of one channel per dword); also K staging and the final combine
-    __shared__ __attribute__((aligned(16))) uint32_t s_v[WAVES][16 * VR];
-    __shared__ __attribute__((aligned(16))) uint16_t s_q[16 * D];     // query rows (dtype bits), zero beyond G
-    __shared__ __attribute__((aligned(16))) uint16_t s_qm[16 * D];    // query rows masked at salient/donor channels
-    __shared__ __attribute__((aligned(16))) f32x2 s_kc[4 * KC_STRIDE]; // per channel (s * 2^9, -8 s)
-    __shared__ __attribute__((aligned(16))) int8_t s_role[D];
-    __shared__ __attribute__((aligned(16))) uint32_t s_sal[64];       // src | don << 8
-    __shared__ __attribute__((aligned(16))) uint32_t s_salw[64];      // gather offsets: src byte, shift, don byte, shift
-    __shared__ __attribute__((aligned(16))) f32x2 s_salf[64];         // (s_src, -128 s_src)
-    __shared__ __attribute__((aligned(16))) uint16_t s_qsal[16 * 64]; // Q[g][src_k], zero beyond S
-    __shared__ float s_dpad[64];                                      // padding of donor k, rounded to the query dtype
-    __shared__ float s_wm[WAVES][16], s_wl[WAVES][16];
+    uint32_t (&s_v)[WAVES][16 * VR] = sm.v;
+    uint16_t *const s_q = sm.q;
+    uint16_t *const s_qm = sm.qm;
+    f32x2 *const s_kc = sm.kc;
+    int8_t *const s_role = sm.role;
+    uint32_t *const s_sal = sm.sal;
+    uint32_t *const s_salw = sm.salw;
+    f32x2 *const s_salf = sm.salf;
+    uint16_t *const s_qsal = sm.qsal;
+    float *const s_dpad = sm.dpad;
+    float (&s_wm)[WAVES][16] = sm.wm;
+    float (&s_wl)[WAVES][16] = sm.wl;
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int gl = lane & 15, ql = lane >> 4;     // MFMA column (query row / channel) and k-slot group
-    const int pl = lane >> 2, qq = lane & 3;      // V writer: token pair and 32-channel quarter
+    // V writer: token pair and 32-channel quarter; the 8 lanes of one LDS cycle
+    // take 8 different token pairs, so their 16-byte stores hit distinct banks
+    const int pl = lane & 15, qq = lane >> 4;
     const int h = blockIdx.x;
     const int64_t p = blockIdx.y;
     const int G = a.G;
@@ -87,87 +109,106 @@ __global__ __launch_bounds__(256, 3) void decode_fast(FastArgs a)
     const int ngroups = D / a.vgroup;
 
     // ---------------- geometry (wave-uniform) and every global load up front
-    const bool packed = p < a.nblk;
+    // All loads are unconditional (indices clamped into range) and issued
+    // before any of them is consumed: the query row, then the block's
+    // per-channel constants, then the payload, so one round trip after the
+    // pointer-table row covers all of them.  Rows past the end of a partition
+    // load a clamped valid row; their logits are masked to -inf, so they get
+    // weight exactly 0.
+    constexpr bool packed = PACKED;
     const uint8_t *kpay = nullptr, *vpay = nullptr;
     const uint16_t *vsc = nullptr, *voff = nullptr;
-    const uint16_t *dk = nullptr, *dv = nullptr;
-    int dk_st = 0, dv_st = 0, start = 0, stop = 0;
+    int start = 0, stop = 0;
     const int S = packed ? (int)a.S : 0;
     const int sal_groups = (S + 15) / 16;
+    const int qg = tid >> 4, qc = (tid & 15) * 8;  // this thread's 8 query elements
+    const u32x4 qraw = ld16(a.q + (int64_t)(h * G + (qg < G ? qg : G - 1)) * a.q_sh + qc);
+    float kscale = 0.0f, kpad = 0.0f;
+    uint32_t krole = 0u, ksrc = 0u, kdon = 0u;
+    int base = 0;
+    u32x4 kw[4];
+    uint32_t vw[2][2][VQW];                        // [half chunk][token of the pair][dword]
+    uint32_t vp[2][2][2];                          // [half chunk][token of the pair][scale, offset] (f16 bits)
+#define IQ_LOAD_CHUNK(b_)                                                                             \
+    do {                                                                                              \
+        const int b0 = (b_);                                                                          \
+        _Pragma("unroll") for (int j = 0; j < 4; ++j) {                                               \
+            const int t = min(b0 + 16 * j + gl, stop - 1);                                            \
+            kw[j] = ld16(kpay + t * (D / 2) + 16 * ql);                                               \
+        }                                                                                             \
+        const int gi = (32 * qq) / a.vgroup;                                                          \
+        _Pragma("unroll") for (int m = 0; m < 2; ++m) {                                               \
+            _Pragma("unroll") for (int u = 0; u < 2; ++u) {                                           \
+                const int t = min(b0 + 32 * m + 2 * pl + u, stop - 1);                                \
+                const uint8_t *src = vpay + (int64_t)t * VROW + VQ * qq;                              \
+                if constexpr (VQW == 2) {                                                             \
+                    const u32x2 r = ldg<u32x2>(src);                                                  \
+                    vw[m][u][0] = r[0];                                                               \
+                    vw[m][u][1] = r[1];                                                               \
+                } else {                                                                              \
+                    const u32x4 r = ld16(src);                                                        \
+                    _Pragma("unroll") for (int w = 0; w < VQW; ++w) vw[m][u][w] = r[w];               \
+                }                                                                                     \
+                vp[m][u][0] = ldg<uint16_t>(vsc + t * ngroups + gi);                                  \
+                vp[m][u][1] = ldg<uint16_t>(voff + t * ngroups + gi);                                 \
+            }                                                                                         \
+        }                                                                                             \
+    } while (0)
     if (packed) {
         const int64_t *row = a.tables + p * IQ_TABLE_COLS;
+        krole = (uint8_t)ldg<int8_t>(a.kmap + (p * a.H + h) * D + (tid & (D - 1)));
+        kscale = ldg<float>((const float *)row[1] + h * D + (tid & (D - 1)));
+        {   // no branch around these loads: with S == 0 they read valid
+            // addresses (the role map, the scales) whose values go unused
+            const int k = tid < S ? tid : (S > 0 ? S - 1 : 0);
+            const uint8_t *srcs = S > 0 ? (const uint8_t *)row[6] + h * S : (const uint8_t *)a.kmap;
+            const uint8_t *dons = S > 0 ? (const uint8_t *)row[7] + h * S : (const uint8_t *)a.kmap;
+            const float *pads = S > 0 ? (const float *)row[2] + h * S : (const float *)row[1];
+            ksrc = ldg<uint8_t>(srcs + k);
+            kdon = ldg<uint8_t>(dons + k);
+            kpad = ldg<float>(pads + k);
+        }
         kpay = (const uint8_t *)row[0] + (int64_t)h * a.BT * (D / 2);
         vpay = (const uint8_t *)row[3] + (int64_t)h * a.BT * VROW;
         vsc = (const uint16_t *)row[4] + (int64_t)h * a.BT * ngroups;
         voff = (const uint16_t *)row[5] + (int64_t)h * a.BT * ngroups;
         stop = (int)a.BT;
+        base = CHUNK * wave;
+        IQ_LOAD_CHUNK(base);                        // clamped: also for waves past the end
+        // keep every use of the small loads below the payload issue
+        asm volatile("" ::: "memory");
+    } else {
+        // dense partitions cover sink ++ tail as one token sequence
+        const int length = (int)(a.sink_t + a.tail_t);
+        start = (int)((p - a.nblk) * DENSE_SPLIT);
+        stop = start + DENSE_SPLIT < length ? start + DENSE_SPLIT : length;
+        base = start + CHUNK * wave;
+    }
+    // row t (already clamped into [0, stop)) of the dense key / value sequence
+    const int nsink = (int)a.sink_t;
+    auto dense_k = [&](int t) {
+        return t < nsink ? a.sk + h * a.sk_sh + (int64_t)t * a.sk_st : a.tk + h * a.tk_sh + (int64_t)(t - nsink) * a.tk_st;
+    };
+    auto dense_v = [&](int t) {
+        return t < nsink ? a.sv + h * a.sv_sh + (int64_t)t * a.sv_st : a.tv + h * a.tv_sh + (int64_t)(t - nsink) * a.tv_st;
+    };
+    // consume the small loads (the payload stays in flight)
+    *(u32x4 *)(s_q + qg * D + qc) = qg < G ? qraw : u32x4{0u, 0u, 0u, 0u};
+    if (packed) {
         if (tid < D) {
-            const float s = ldg<float>((const float *)row[1] + h * D + tid);
-            s_kc[(tid >> 5) * KC_STRIDE + (tid & 31)] = f32x2{s * inv_unit, -8.0f * s};
-            s_role[tid] = ldg<int8_t>(a.kmap + (p * a.H + h) * D + tid);
+            s_kc[(tid >> 5) * KC_STRIDE + (tid & 31)] = f32x2{kscale * inv_unit, -8.0f * kscale};
+            s_role[tid] = (int8_t)krole;
         }
         if (tid < S) {
-            const uint32_t src = ldg<uint8_t>((const uint8_t *)row[6] + h * S + tid);
-            const uint32_t don = ldg<uint8_t>((const uint8_t *)row[7] + h * S + tid);
-            s_sal[tid] = src | (don << 8);
-            s_dpad[tid] = round_q<F16>(ldg<float>((const float *)row[2] + h * S + tid));
+            s_sal[tid] = ksrc | (kdon << 8);
+            s_dpad[tid] = round_q<F16>(kpad);
         }
-    } else {
-        const int64_t dp = p - a.nblk;
-        const int64_t sink_parts = (a.sink_t + DENSE_SPLIT - 1) / DENSE_SPLIT;
-        int64_t length;
-        if (dp < sink_parts) {
-            dk = a.sk + h * a.sk_sh; dv = a.sv + h * a.sv_sh; dk_st = (int)a.sk_st; dv_st = (int)a.sv_st;
-            start = (int)(dp * DENSE_SPLIT);
-            length = a.sink_t;
-        } else {
-            dk = a.tk + h * a.tk_sh; dv = a.tv + h * a.tv_sh; dk_st = (int)a.tk_st; dv_st = (int)a.tv_st;
-            start = (int)((dp - sink_parts) * DENSE_SPLIT);
-            length = a.tail_t;
-        }
-        stop = (int)(start + DENSE_SPLIT < length ? start + DENSE_SPLIT : length);
     }
-    const int qg = tid >> 4, qc = (tid & 15) * 8;  // this thread's 8 query elements
-    const u32x4 qraw = qg < G ? ld16(a.q + (int64_t)(h * G + qg) * a.q_sh + qc) : u32x4{0u, 0u, 0u, 0u};
-    *(u32x4 *)(s_q + qg * D + qc) = qraw;
-
-    // first chunk of this wavefront: K rows (lane t = gl, channels 32 ql..), V quarter rows
-    int base = start + CHUNK * wave;
-    u32x4 kw[4];
-    uint32_t vw[2][2][VQW];                        // [half chunk][token of the pair][dword]
-    uint16_t vp[2][2][2];                          // [half chunk][token of the pair][scale, offset]
-#define IQ_LOAD_CHUNK(b_)                                                                             \
-    do {                                                                                              \
-        const int b0 = (b_);                                                                          \
-        _Pragma("unroll") for (int j = 0; j < 4; ++j) {                                               \
-            const int t = b0 + 16 * j + gl;                                                           \
-            kw[j] = t < stop ? ld16(kpay + t * (D / 2) + 16 * ql) : u32x4{0u, 0u, 0u, 0u};            \
-        }                                                                                             \
-        const int gi = (32 * qq) / a.vgroup;                                                          \
-        _Pragma("unroll") for (int m = 0; m < 2; ++m) {                                               \
-            _Pragma("unroll") for (int u = 0; u < 2; ++u) {                                           \
-                const int t = b0 + 32 * m + 2 * pl + u;                                               \
-                const bool ok = t < stop;                                                             \
-                const uint8_t *src = vpay + (int64_t)t * VROW + VQ * qq;                              \
-                if constexpr (VQW == 2) {                                                             \
-                    const u32x2 r = ok ? ldg<u32x2>(src) : u32x2{0u, 0u};                             \
-                    vw[m][u][0] = r[0];                                                               \
-                    vw[m][u][1] = r[1];                                                               \
-                } else {                                                                              \
-                    const u32x4 r = ok ? ld16(src) : u32x4{0u, 0u, 0u, 0u};                           \
-                    _Pragma("unroll") for (int w = 0; w < VQW; ++w) vw[m][u][w] = r[w];               \
-                }                                                                                     \
-                vp[m][u][0] = ok ? ldg<uint16_t>(vsc + t * ngroups + gi) : (uint16_t)0;               \
-                vp[m][u][1] = ok ? ldg<uint16_t>(voff + t * ngroups + gi) : (uint16_t)0;              \
-            }                                                                                         \
-        }                                                                                             \
-    } while (0)
-    if (packed && base < stop) IQ_LOAD_CHUNK(base);
     __syncthreads();
 
     // ---------------- cooperative per-workgroup constants
     {   // masked query rows: role != -1 (salient or donor) -> 0
-        u32x4 v = qraw;
+        u32x4 v = qg < G ? qraw : u32x4{0u, 0u, 0u, 0u};
         if (packed) {
             const uint32_t r0 = *(const uint32_t *)(s_role + qc), r1 = *(const uint32_t *)(s_role + qc + 4);
 #pragma unroll
@@ -187,9 +228,11 @@ __global__ __launch_bounds__(256, 3) void decode_fast(FastArgs a)
         s_salf[tid] = f32x2{-0.125f * m8, 16.0f * m8};                   // (s_src, -128 s_src), exact
         s_salw[tid] = (src >> 1) | (((src & 1) * 4) << 8) | ((don >> 1) << 16) | (((don & 1) * 4) << 24);
     }
-    for (int i = tid; i < 16 * 16 * sal_groups; i += 256) {
-        const int g = i / (16 * sal_groups), k = i % (16 * sal_groups);
-        s_qsal[g * 64 + k] = k < S ? s_q[g * D + (s_sal[k] & 0xffu)] : (uint16_t)0;
+    if constexpr (PACKED) {
+        for (int i = tid; i < 16 * 16 * sal_groups; i += 256) {
+            const int g = i / (16 * sal_groups), k = i % (16 * sal_groups);
+            s_qsal[g * 64 + k] = k < S ? s_q[g * D + (s_sal[k] & 0xffu)] : (uint16_t)0;
+        }
     }
     __syncthreads();
 
@@ -219,17 +262,18 @@ __global__ __launch_bounds__(256, 3) void decode_fast(FastArgs a)
         // ---------------- logits S^T[token, g] for four 16-token tiles
         f32x4 sc[4];
         if (packed) {
+            // channel group d outer: each lane's 8 constants of group d are read
+            // from LDS once and serve all four tiles; per tile the sum over d
+            // keeps its order, so the logits do not depend on the loop nest
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                // re-read the per-channel constants from LDS for every tile rather
-                // than keeping all 64 of them live in registers
-                asm volatile("" ::: "memory");
-                f32x4 s = {bias, bias, bias, bias};
+            for (int j = 0; j < 4; ++j) sc[j] = f32x4{bias, bias, bias, bias};
 #pragma unroll
-                for (int d = 0; d < 4; ++d) {
-                    const f32x2 *kc = s_kc + ql * KC_STRIDE + 8 * d;
-                    const u32x4 c01 = *(const u32x4 *)(kc + 0), c23 = *(const u32x4 *)(kc + 2);
-                    const u32x4 c45 = *(const u32x4 *)(kc + 4), c67 = *(const u32x4 *)(kc + 6);
+            for (int d = 0; d < 4; ++d) {
+                const f32x2 *kc = s_kc + ql * KC_STRIDE + 8 * d;
+                const u32x4 c01 = *(const u32x4 *)(kc + 0), c23 = *(const u32x4 *)(kc + 2);
+                const u32x4 c45 = *(const u32x4 *)(kc + 4), c67 = *(const u32x4 *)(kc + 6);
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
                     const uint32_t x = kw[j][d];
                     const uint32_t lo = x & 0x0f0f0f0fu, hi = (x >> 4) & 0x0f0f0f0fu;
                     const f32x2 e01 = fp8x2<false>(lo), e23 = fp8x2<true>(lo);
@@ -241,9 +285,8 @@ __global__ __launch_bounds__(256, 3) void decode_fast(FastArgs a)
                     kv[2] = pack2<F16>(fmaf(e23.x, KF(c45, 0), KF(c45, 1)), fmaf(o23.x, KF(c45, 2), KF(c45, 3)));
                     kv[3] = pack2<F16>(fmaf(e23.y, KF(c67, 0), KF(c67, 1)), fmaf(o23.y, KF(c67, 2), KF(c67, 3)));
 #undef KF
-                    s = mma32<F16>(kv, qb[d], s);
+                    sc[j] = mma32<F16>(kv, qb[d], sc[j]);
                 }
-                sc[j] = s;
             }
             if (sal_groups) {
                 // stage the four K tiles as [64 tokens][17 dwords] for the salient gathers
@@ -290,7 +333,7 @@ __global__ __launch_bounds__(256, 3) void decode_fast(FastArgs a)
                     const int t = base + 16 * (j2 + jj) + gl;
                     const int tc = t < stop ? t : stop - 1;
 #pragma unroll
-                    for (int d = 0; d < 4; ++d) kd[jj][d] = ld16(dk + (int64_t)tc * dk_st + 32 * ql + 8 * d);
+                    for (int d = 0; d < 4; ++d) kd[jj][d] = ld16(dense_k(tc) + 32 * ql + 8 * d);
                 }
 #pragma unroll
                 for (int jj = 0; jj < 2; ++jj) {
@@ -419,8 +462,8 @@ __global__ __launch_bounds__(256, 3) void decode_fast(FastArgs a)
                 u32x4 r0[4], r1[4];
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
-                    r0[i] = ld16(dv + (int64_t)ta * dv_st + 32 * qq + 8 * i);
-                    r1[i] = ld16(dv + (int64_t)tb * dv_st + 32 * qq + 8 * i);
+                    r0[i] = ld16(dense_v(ta) + 32 * qq + 8 * i);
+                    r1[i] = ld16(dense_v(tb) + 32 * qq + 8 * i);
                 }
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
@@ -452,41 +495,53 @@ __global__ __launch_bounds__(256, 3) void decode_fast(FastArgs a)
 #undef IQ_LOAD_CHUNK
 
     // ---------------- combine the four wavefronts, write this partition's partial
+    // Each wavefront rescales its O to the workgroup's running max in
+    // registers and stages it as O[g][c] rows; readers then only add.
     l_run = xsum16(l_run);
-    if (ql == 0) {
-        s_wm[wave][gl] = m_run;
-        s_wl[wave][gl] = l_run;
-    }
-    float *ot = (float *)vt;        // O^T[c][g] of this wavefront, row stride 17
-#pragma unroll
-    for (int n = 0; n < 8; ++n)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) ot[(16 * n + 4 * ql + r) * 17 + gl] = acc[n][r];
+    if (ql == 0) s_wm[wave][gl] = m_run;
     __syncthreads();
-    for (int i = tid; i < G * D; i += 256) {
-        const int g = i >> 7, c = i & (D - 1);
-        float mx = NEG_INF;
+    float mx = s_wm[0][gl];
 #pragma unroll
-        for (int w = 0; w < WAVES; ++w) mx = fmaxf(mx, s_wm[w][g]);
-        float num = 0.0f, den = 0.0f;
+    for (int w = 1; w < WAVES; ++w) mx = fmaxf(mx, s_wm[w][gl]);
+    const float wt = m_run == NEG_INF ? 0.0f : __builtin_amdgcn_exp2f(m_run - mx);
+    if (ql == 0) s_wl[wave][gl] = l_run * wt;
+    float *ot = (float *)vt;
 #pragma unroll
-        for (int w = 0; w < WAVES; ++w) {
-            const float mw = s_wm[w][g];
-            const float wt = mw == NEG_INF ? 0.0f : __builtin_amdgcn_exp2f(mw - mx);
-            num = fmaf(((const float *)s_v[w])[c * 17 + g], wt, num);
-            den = fmaf(s_wl[w][g], wt, den);
+    for (int n = 0; n < 8; ++n) *(f32x4 *)(ot + gl * OROW + 16 * n + 4 * ql) = acc[n] * wt;
+    __syncthreads();
+    for (int i = tid; i < G * (D / 4); i += 256) {
+        const int g = i >> 5, c = (i & 31) * 4;
+        f32x4 num = *(const f32x4 *)((const float *)s_v[0] + g * OROW + c);
+        float den = s_wl[0][g];
+#pragma unroll
+        for (int w = 1; w < WAVES; ++w) {
+            num += *(const f32x4 *)((const float *)s_v[w] + g * OROW + c);
+            den += s_wl[w][g];
         }
         if (a.P == 1) {
-            iq_store_as(a.out, (int64_t)(h * G + g) * D + c, num / den, a.odt);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) iq_store_as(a.out, (int64_t)(h * G + g) * D + c + e, num[e] / den, a.odt);
             continue;
         }
-        float *out = a.ws + ((int64_t)(h * G + g) * a.P + p) * (D + 2);
-        out[c] = num;
+        float *out = a.ws + ((int64_t)(h * G + g) * a.P + p) * (D + 2);   // rows of 130 floats: 8-byte aligned
+        *(f32x2 *)(out + c) = f32x2{num[0], num[1]};
+        *(f32x2 *)(out + c + 2) = f32x2{num[2], num[3]};
         if (c == 0) {
-            out[D] = mx * LN2;
+            float m = s_wm[0][g];
+#pragma unroll
+            for (int w = 1; w < WAVES; ++w) m = fmaxf(m, s_wm[w][g]);
+            out[D] = m * LN2;
             out[D + 1] = den;
         }
     }
+}
+
+template <bool F16, int VBITS>
+__global__ __launch_bounds__(256, 3) void decode_fast(FastArgs a)
+{
+    __shared__ FastSmem sm;
+    if ((int64_t)blockIdx.y < a.nblk) fast_body<F16, VBITS, true>(a, sm);
+    else fast_body<F16, VBITS, false>(a, sm);
 }
 
 }  // namespace
@@ -494,15 +549,16 @@ __global__ __launch_bounds__(256, 3) void decode_fast(FastArgs a)
 #undef IQ_LOAD_CHUNK
 
 // Launches the matrix-core decode; returns IQ_ERR_UNSUPPORTED for layouts it
-// does not cover.  *merged = 1 when the output was written in-kernel (a single
-// partition), 0 when the caller must run the partial reduction.
+// does not cover.  Partitions are the packed blocks, then 256-token slices of
+// sink ++ tail; *parts receives their count.  With one partition the output is
+// written in-kernel, otherwise the caller merges *parts partials.
 int iq_decode_fast_launch(const void *q, int q_dtype, int64_t q_stride_h, int64_t Hq, const int64_t *tables,
                           const int8_t *key_map, int64_t n_blocks, int64_t block_tokens, int64_t H, int64_t S,
                           int value_bits, int value_group, const void *sink_k, const void *sink_v, int64_t sink_k_sh,
                           int64_t sink_k_st, int64_t sink_v_sh, int64_t sink_v_st, int64_t sink_t,
                           const void *tail_k, const void *tail_v, int64_t tail_k_sh, int64_t tail_k_st,
                           int64_t tail_v_sh, int64_t tail_v_st, int64_t tail_t, float scale, float *workspace,
-                          int64_t P, void *out, int out_dtype, int *merged, hipStream_t stream)
+                          void *out, int out_dtype, int64_t *parts, hipStream_t stream)
 {
     if (q_dtype != IQ_BF16 && q_dtype != IQ_F16) return IQ_ERR_UNSUPPORTED;
     if (out_dtype != IQ_F32 && out_dtype != IQ_BF16 && out_dtype != IQ_F16) return IQ_ERR_UNSUPPORTED;
@@ -518,12 +574,14 @@ int iq_decode_fast_launch(const void *q, int q_dtype, int64_t q_stride_h, int64_
         return IQ_ERR_UNSUPPORTED;
     if (tail_t && !(aligned(tail_k, tail_k_sh, tail_k_st) && aligned(tail_v, tail_v_sh, tail_v_st)))
         return IQ_ERR_UNSUPPORTED;
+    const int64_t P = n_blocks + (sink_t + tail_t + DENSE_SPLIT - 1) / DENSE_SPLIT;
+    if (P < 1 || P > 65535) return IQ_ERR_UNSUPPORTED;
     FastArgs a{(const uint16_t *)q, q_stride_h, (int)(Hq / H), tables, key_map, n_blocks, block_tokens, H, S,
                value_group ? value_group : 64, (const uint16_t *)sink_k, (const uint16_t *)sink_v, sink_k_sh,
                sink_k_st, sink_v_sh, sink_v_st, sink_t, (const uint16_t *)tail_k, (const uint16_t *)tail_v,
                tail_k_sh, tail_k_st, tail_v_sh, tail_v_st, tail_t, scale * 1.44269504088896341f, workspace, P,
                out, out_dtype};
-    *merged = P == 1;
+    *parts = P;
     const dim3 grid((unsigned)H, (unsigned)P), block(256);
     const bool f16 = q_dtype == IQ_F16;
     const int vb = n_blocks > 0 ? value_bits : 2;

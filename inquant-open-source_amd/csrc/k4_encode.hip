@@ -199,6 +199,7 @@ __global__ __launch_bounds__(K4_THREADS) void k4_encode_kernel(K4Args a)
 // k4_encode_kernel.
 constexpr int TILE_D = 128;
 constexpr int TILE_T = 256;
+constexpr int XROW = TILE_D + 2;         // u16 per staged row: 65 dwords, so the 4 tokens a wave reads fall on distinct banks
 
 template <bool F16IN>
 __device__ __forceinline__ float tile_f32(uint32_t bits16)
@@ -210,7 +211,7 @@ __device__ __forceinline__ float tile_f32(uint32_t bits16)
 template <bool F16IN>
 __global__ __launch_bounds__(K4_THREADS) void k4_encode_tile(K4Args a)
 {
-    __shared__ __attribute__((aligned(16))) uint16_t s_x[TILE_T * TILE_D];
+    __shared__ __attribute__((aligned(16))) uint16_t s_x[TILE_T * XROW];
     __shared__ double s_rcp[TILE_T];    // RN(1 / n), n = 1 .. T
     __shared__ float s_sal[TILE_D], s_smean[TILE_D], s_err[TILE_D], s_amax[TILE_D], s_scale[TILE_D];
     __shared__ int16_t s_src_of[TILE_D];
@@ -236,7 +237,12 @@ __global__ __launch_bounds__(K4_THREADS) void k4_encode_tile(K4Args a)
         }
         // rows at and beyond T receive copies of the last segment and are never read
 #pragma unroll
-        for (int k = 0; k < TILE_T * 16 / K4_THREADS; ++k) *(u32x4_t *)(s_x + 8 * (tid + K4_THREADS * k)) = v[k];
+        for (int k = 0; k < TILE_T * 16 / K4_THREADS; ++k) {
+            const int i = tid + K4_THREADS * k;       // row i / 16, segment i % 16 (4-byte aligned)
+            uint32_t *d = (uint32_t *)(s_x + (i >> 4) * XROW + 8 * (i & 15));
+#pragma unroll
+            for (int w = 0; w < 4; ++w) d[w] = v[k][w];
+        }
     }
     if (tid < T) s_rcp[tid] = 1.0 / (double)(tid + 1);
     if (tid == 0) s_bad = 0;
@@ -262,14 +268,14 @@ __global__ __launch_bounds__(K4_THREADS) void k4_encode_tile(K4Args a)
             double ycur[8], ynxt[8];
 #pragma unroll
             for (int u = 0; u < 8; ++u) {
-                cur[u] = Tg ? tile_f32<F16IN>(s_x[u * TILE_D + c]) : 0.0f;
+                cur[u] = Tg ? tile_f32<F16IN>(s_x[u * XROW + c]) : 0.0f;
                 ycur[u] = s_rcp[u];
             }
             for (int t0 = 0; t0 < Tg; t0 += 8) {
                 const int tn = t0 + 8 < Tg ? t0 + 8 : t0;
 #pragma unroll
                 for (int u = 0; u < 8; ++u) {
-                    nxt[u] = tile_f32<F16IN>(s_x[(tn + u) * TILE_D + c]);
+                    nxt[u] = tile_f32<F16IN>(s_x[(tn + u) * XROW + c]);
                     ynxt[u] = s_rcp[tn + u];
                 }
 #pragma unroll
@@ -280,7 +286,7 @@ __global__ __launch_bounds__(K4_THREADS) void k4_encode_tile(K4Args a)
                     ycur[u] = ynxt[u];
                 }
             }
-            for (int t = Tg; t < T; ++t) step(tile_f32<F16IN>(s_x[t * TILE_D + c]), s_rcp[t], t);
+            for (int t = Tg; t < T; ++t) step(tile_f32<F16IN>(s_x[t * XROW + c]), s_rcp[t], t);
             s_err[c] = (float)(m2 / (double)T);     // var; the mean term is added below
             s_smean[c] = (float)mean;                                // full mean, replaced below
         }
@@ -291,7 +297,7 @@ __global__ __launch_bounds__(K4_THREADS) void k4_encode_tile(K4Args a)
         sm.init(ns);
 #pragma unroll 8
         for (int r = 0; r < ns; ++r) {
-            const float v = tile_f32<F16IN>(s_x[(int)(r * a.stride) * TILE_D + c]);
+            const float v = tile_f32<F16IN>(s_x[(int)(r * a.stride) * XROW + c]);
             sa.add(fabsf(v));
             sm.add(v);
         }
@@ -299,7 +305,7 @@ __global__ __launch_bounds__(K4_THREADS) void k4_encode_tile(K4Args a)
         bool bad = false;
 #pragma unroll 16
         for (int t = 0; t < T; ++t) {
-            const float v = tile_f32<F16IN>(s_x[t * TILE_D + c]);
+            const float v = tile_f32<F16IN>(s_x[t * XROW + c]);
             bad |= !iq_isfinite(v);
             amax = fmaxf(amax, fabsf(v));
         }
@@ -358,7 +364,7 @@ __global__ __launch_bounds__(K4_THREADS) void k4_encode_tile(K4Args a)
     }
     uint32_t *out = (uint32_t *)(a.payload + row * (int64_t)T * (TILE_D / 2));
     for (int t = tid >> 4; t < T; t += K4_THREADS / 16) {
-        const uint16_t *xt = s_x + t * TILE_D;
+        const uint16_t *xt = s_x + t * XROW;
         // branch-free: every channel reads the value it encodes (its own, or
         // for a donor slot its source's), the reciprocal quotient decides the
         // rounding, and only a token with a near-tie quotient divides exactly

@@ -232,7 +232,7 @@ __global__ __launch_bounds__(256, 2) void decode_paged(PagedArgs a)
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int gl = lane & 15, ql = lane >> 4;
-    const int pl = lane >> 2, qq = lane & 3;
+    const int pl = lane & 15, qq = lane >> 4;      // V writer: distinct token pairs per LDS cycle
     const int h = blockIdx.x, p = blockIdx.y, sq = blockIdx.z;
     const int G = a.G;
     const SeqGeom geo = seq_geom(a, sq);

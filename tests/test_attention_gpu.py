@@ -189,7 +189,8 @@ def test_workspace_pool_is_shared_once_and_rejects_other_stream():
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("fraction", [0.0, 0.125, 0.5])
-@pytest.mark.parametrize("block,sink,tail", [(256, 4, 128), (41, 0, 281), (32, 4, 0), (300, 3, 1)])
+@pytest.mark.parametrize("block,sink,tail", [(256, 4, 128), (41, 0, 281), (32, 4, 0), (300, 3, 1),
+                                              (64, 100, 300), (64, 300, 20)])
 def test_matrix_core_path_matches_oracle(dtype, fraction, block, sink, tail):
     # bf16/f16 queries with V2 values take the MFMA kernel: partial tiles,
     # 0..64 salient channels, blocks longer than one 256-token pass
