@@ -32,6 +32,7 @@ constexpr int WAVES = 4;
 constexpr int PART = 256;              // tokens per partition
 constexpr int VR = 136;                // dwords per staged token-pair row of decoded V
 constexpr int KROW = 17;               // dwords per staged K row (salient byte gathers)
+constexpr int OROW = 132;              // floats per staged output row in the combine (conflict-free 16-byte stores)
 constexpr int KG = 36;                 // floats per 32-channel group of page scales (+4: no bank overlap)
 constexpr int SPG = 16;                // salient channels per page (the layout's key_padding width)
 constexpr float LN2 = 0.693147180559945309f;
@@ -209,42 +210,50 @@ __device__ __forceinline__ SeqGeom seq_geom(const PagedArgs &a, int s)
     return g;
 }
 
-// One workgroup per (KV head, partition, sequence); NPG = pages per packed
-// partition (PART / B).
+// Workgroup LDS of decode_paged, shared by its packed and dense bodies.
 template <int NPG>
-__global__ __launch_bounds__(256, 2) void decode_paged(PagedArgs a)
+struct __attribute__((aligned(16))) PagedSmem {
+    uint32_t v[WAVES][16 * VR];        // decoded V tiles, K staging, the final combine
+    uint16_t q[16 * D];
+    float ka[NPG][4 * KG];             // s * 2^9, zero at salient/donor channels
+    int16_t role[NPG][D];              // key_map of each page
+    uint32_t salw[NPG][SPG];           // gather offsets per page
+    f32x2 salf[NPG][SPG];              // (s_src, -128 s_src)
+    uint16_t qsal[NPG][16 * SPG];
+    float bias[NPG][16];               // sum_k q[g][don_k] * round(pad_k)
+    int16_t src[NPG][SPG], don[NPG][SPG];
+    float ssc[NPG][SPG], pad[NPG][SPG], padraw[NPG][SPG];
+    uint64_t page[NPG];
+    int pok[NPG];
+    float wm[WAVES][16], wl[WAVES][16];
+};
+
+// One partition of one sequence.  The packed and the dense body are separate
+// instantiations so that neither has a branch between its loads and their
+// first use (a branch join there makes the compiler wait for every load in
+// flight).  `pid` is this thread's block-table entry (page tid % NPG of the
+// partition), loaded before the sequence lengths were known.
+template <int NPG, bool PACKED>
+__device__ __forceinline__ void paged_body(const PagedArgs &a, PagedSmem<NPG> &sm, const SeqGeom &geo, int pid)
 {
     constexpr int B = PART / NPG;
     constexpr int VQW = 2;                       // dwords per 32-channel quarter of a V2 row
-
-    __shared__ __attribute__((aligned(16))) uint32_t s_v[WAVES][16 * VR];
-    __shared__ __attribute__((aligned(16))) uint16_t s_q[16 * D];
-    __shared__ __attribute__((aligned(16))) float s_ka[NPG][4 * KG];      // s * 2^9, zero at salient/donor channels
-    __shared__ __attribute__((aligned(16))) uint32_t s_salw[NPG][SPG];   // gather offsets per page
-    __shared__ __attribute__((aligned(16))) f32x2 s_salf[NPG][SPG];      // (s_src, -128 s_src)
-    __shared__ __attribute__((aligned(16))) uint16_t s_qsal[NPG][16 * SPG];
-    __shared__ float s_bias[NPG][16];                                    // sum_k q[g][don_k] * round(pad_k)
-    __shared__ int16_t s_src[NPG][SPG], s_don[NPG][SPG];
-    __shared__ float s_ssc[NPG][SPG], s_pad[NPG][SPG];
-    __shared__ uint64_t s_page[NPG];
-    __shared__ int s_pok[NPG];
-    __shared__ float s_wm[WAVES][16], s_wl[WAVES][16];
+    constexpr int CPT = (NPG * D + 255) / 256;   // (page, channel) constants per thread
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int gl = lane & 15, ql = lane >> 4;
     const int pl = lane & 15, qq = lane >> 4;      // V writer: distinct token pairs per LDS cycle
     const int h = blockIdx.x, p = blockIdx.y, sq = blockIdx.z;
     const int G = a.G;
-    const SeqGeom geo = seq_geom(a, sq);
-    if (p >= geo.npp + geo.ndp) return;
-    const bool packed = p < geo.npp;
     const float unit = fp8x2<false>(1u).x;       // fp8 byte 1 == 2^-9
     const float inv_unit = 1.0f / unit;
+    uint32_t *const s_v = &sm.v[0][0];
+    uint16_t *const s_q = sm.q;
 
     // ---------------- geometry
     int ntok, tok0 = 0, slot0 = 0;
     const uint16_t *dk = nullptr, *dv = nullptr;
-    if (packed) {
+    if constexpr (PACKED) {
         tok0 = p * PART;
         ntok = min(PART, geo.npg * B - tok0);
     } else {
@@ -254,55 +263,40 @@ __global__ __launch_bounds__(256, 2) void decode_paged(PagedArgs a)
         dk = dn + ((int64_t)h * (B + 4) + slot0) * D;
         dv = dn + ((int64_t)(a.H + h) * (B + 4) + slot0) * D;
     }
-    const int npg_here = packed ? (ntok + B - 1) / B : 0;
-
-    // ---------------- query rows; page addresses and per-page constants
+    const int npg_here = PACKED ? (ntok + B - 1) / B : 0;
     const int qg = tid >> 4, qc = (tid & 15) * 8;
-    const u32x4 qraw = qg < G ? ld16(a.q + sq * a.q_ss + (int64_t)(h * G + qg) * a.q_sh + qc)
-                              : u32x4{0u, 0u, 0u, 0u};
-    *(u32x4 *)(s_q + qg * D + qc) = qraw;
-    if (tid < npg_here) {
-        const int64_t id = a.bt[sq * a.bt_ss + (int64_t)p * NPG + tid];
-        const bool ok = id >= 0 && id < a.pool_pages;
-        s_page[tid] = (uint64_t)(a.pool + (ok ? id : 0) * a.page_bytes);
-        s_pok[tid] = ok;
+    const u32x4 qraw = ld16(a.q + sq * a.q_ss + (int64_t)(h * G + (qg < G ? qg : G - 1)) * a.q_sh + qc);
+    if (PACKED && tid < NPG) {
+        // pages past the partition's end or outside the pool read page 0 and stay dead
+        const bool ok = tid < npg_here && pid >= 0 && pid < a.pool_pages;
+        sm.page[tid] = (uint64_t)(a.pool + (ok ? pid : 0) * a.page_bytes);
+        sm.pok[tid] = ok;
     }
-    if (tid < NPG * SPG) {
-        (&s_src[0][0])[tid] = 0;
-        (&s_don[0][0])[tid] = 0;
-        (&s_ssc[0][0])[tid] = 0.0f;
-        (&s_pad[0][0])[tid] = 0.0f;
-    }
-    __syncthreads();
-    for (int i = tid; i < npg_here * D; i += 256) {
-        const int lp = i >> 7, c = i & (D - 1);
-        const uint8_t *page = (const uint8_t *)s_page[lp];
-        const float sc = ldg<float>(page + a.off.ks + ((int64_t)h * D + c) * 4);
-        const int role = ldg<int16_t>(page + a.off.km + ((int64_t)h * D + c) * 2);
-        s_ka[lp][(c >> 5) * KG + (c & 31)] = role == -1 ? sc * inv_unit : 0.0f;
-        if (role >= 0 && role < D) {                    // source: its donor's descriptor index
-            const int j = -2 - (int)ldg<int16_t>(page + a.off.km + ((int64_t)h * D + role) * 2);
-            if (j >= 0 && j < SPG) {
-                s_src[lp][j] = (int16_t)c;
-                s_ssc[lp][j] = sc;
-            }
-        } else if (role <= -2 && role >= -2 - (SPG - 1)) {  // donor j
-            const int j = -2 - role;
-            s_don[lp][j] = (int16_t)c;
-            s_pad[lp][j] = round_q<false>(ldg<float>(page + a.off.kp + ((int64_t)h * SPG + j) * 4));
-        }
-    }
+    if constexpr (PACKED) __syncthreads();
 
-    // ---------------- every global load of this wavefront's 64 tokens
+    // ---------------- every global load of the partition, unconditional (clamped)
     const int base = 64 * wave;
+    float ksc[CPT], kpad = 0.0f;
+    int krl[CPT];
     u32x4 kw[4];
     uint32_t vw[2][2][VQW];
-    uint16_t vp[2][2][2];
-    if (packed && base < ntok) {
+    uint32_t vp[2][2][2];                          // f16 bits of the V scale / offset
+    if constexpr (PACKED) {
+#pragma unroll
+        for (int k = 0; k < CPT; ++k) {
+            const int i = min(tid + 256 * k, NPG * D - 1), lp = i >> 7, c = i & (D - 1);
+            const uint8_t *page = (const uint8_t *)sm.page[lp];
+            ksc[k] = ldg<float>(page + a.off.ks + ((int64_t)h * D + c) * 4);
+            krl[k] = ldg<int16_t>(page + a.off.km + ((int64_t)h * D + c) * 2);
+        }
+        {
+            const int i = min(tid, NPG * SPG - 1), lp = i / SPG, j = i % SPG;
+            kpad = ldg<float>((const uint8_t *)sm.page[lp] + a.off.kp + ((int64_t)h * SPG + j) * 4);
+        }
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             const int t = min(base + 16 * j + gl, ntok - 1);
-            const uint8_t *page = (const uint8_t *)s_page[t / B];
+            const uint8_t *page = (const uint8_t *)sm.page[t / B];
             kw[j] = ld16(page + ((int64_t)h * B + t % B) * 64 + 16 * ql);
         }
 #pragma unroll
@@ -310,7 +304,7 @@ __global__ __launch_bounds__(256, 2) void decode_paged(PagedArgs a)
 #pragma unroll
             for (int u = 0; u < 2; ++u) {
                 const int t = min(base + 32 * m + 2 * pl + u, ntok - 1);
-                const uint8_t *page = (const uint8_t *)s_page[t / B];
+                const uint8_t *page = (const uint8_t *)sm.page[t / B];
                 const int64_t r = (int64_t)h * B + t % B;
                 const u32x2 w = ldg<u32x2>(page + a.off.vp + r * 32 + 8 * qq);
                 vw[m][u][0] = w[0];
@@ -318,26 +312,69 @@ __global__ __launch_bounds__(256, 2) void decode_paged(PagedArgs a)
                 vp[m][u][0] = ldg<uint16_t>(page + a.off.vs + (r * 2 + (qq >> 1)) * 2);
                 vp[m][u][1] = ldg<uint16_t>(page + a.off.vo + (r * 2 + (qq >> 1)) * 2);
             }
+        // keep every use of the constants below the payload issue
+        asm volatile("" ::: "memory");
     }
-    __syncthreads();
 
-    // ---------------- per-page salient tables and donor bias
-    for (int i = tid; i < npg_here * SPG; i += 256) {
-        const int lp = i / SPG, k = i % SPG;
-        const uint32_t src = (uint32_t)s_src[lp][k], don = (uint32_t)s_don[lp][k];
-        s_salw[lp][k] = (src >> 1) | (((src & 1) * 4) << 8) | ((don >> 1) << 16) | (((don & 1) * 4) << 24);
-        const float ssc = s_ssc[lp][k];
-        s_salf[lp][k] = f32x2{ssc, -128.0f * ssc};
-    }
-    for (int i = tid; i < npg_here * 16; i += 256) {
-        const int lp = i >> 4, g = i & 15;
-        float b = 0.0f;
-        for (int k = 0; k < SPG; ++k) b = fmaf(to_f32<false>(s_q[g * D + s_don[lp][k]]), s_pad[lp][k], b);
-        s_bias[lp][g] = b;
-    }
-    for (int i = tid; i < npg_here * 16 * SPG; i += 256) {
-        const int lp = i / (16 * SPG), r = i % (16 * SPG), g = r / SPG, k = r % SPG;
-        s_qsal[lp][g * SPG + k] = s_q[g * D + s_src[lp][k]];
+    // ---------------- query rows; per-page constants and roles
+    *(u32x4 *)(s_q + qg * D + qc) = qg < G ? qraw : u32x4{0u, 0u, 0u, 0u};
+    if constexpr (PACKED) {
+#pragma unroll
+        for (int k = 0; k < CPT; ++k) {
+            const int i = tid + 256 * k;
+            if (i < NPG * D) {
+                const int lp = i >> 7, c = i & (D - 1);
+                sm.ka[lp][(c >> 5) * KG + (c & 31)] = krl[k] == -1 ? ksc[k] * inv_unit : 0.0f;
+                sm.role[lp][c] = (int16_t)krl[k];
+            }
+        }
+        if (tid < NPG * SPG) {
+            const int lp = tid / SPG, j = tid % SPG;
+            sm.padraw[lp][j] = kpad;
+            sm.src[lp][j] = 0;
+            sm.don[lp][j] = 0;
+            sm.ssc[lp][j] = 0.0f;
+            sm.pad[lp][j] = 0.0f;
+        }
+        __syncthreads();
+        // a source's descriptor index is -2 - key_map[its donor]; a donor's is -2 - key_map
+#pragma unroll
+        for (int k = 0; k < CPT; ++k) {
+            const int i = tid + 256 * k;
+            if (i < NPG * D) {
+                const int lp = i >> 7, c = i & (D - 1), role = krl[k];
+                if (role >= 0 && role < D) {
+                    const int j = -2 - (int)sm.role[lp][role];
+                    if (j >= 0 && j < SPG) {
+                        sm.src[lp][j] = (int16_t)c;
+                        sm.ssc[lp][j] = ksc[k];
+                    }
+                } else if (role <= -2 && role >= -2 - (SPG - 1)) {
+                    const int j = -2 - role;
+                    sm.don[lp][j] = (int16_t)c;
+                    sm.pad[lp][j] = round_q<false>(sm.padraw[lp][j]);
+                }
+            }
+        }
+        __syncthreads();
+        // per-page salient tables and donor bias
+        for (int i = tid; i < NPG * SPG; i += 256) {
+            const int lp = i / SPG, k = i % SPG;
+            const uint32_t src = (uint32_t)sm.src[lp][k], don = (uint32_t)sm.don[lp][k];
+            sm.salw[lp][k] = (src >> 1) | (((src & 1) * 4) << 8) | ((don >> 1) << 16) | (((don & 1) * 4) << 24);
+            const float ssc = sm.ssc[lp][k];
+            sm.salf[lp][k] = f32x2{ssc, -128.0f * ssc};
+        }
+        for (int i = tid; i < NPG * 16; i += 256) {
+            const int lp = i >> 4, g = i & 15;
+            float b = 0.0f;
+            for (int k = 0; k < SPG; ++k) b = fmaf(to_f32<false>(s_q[g * D + sm.don[lp][k]]), sm.pad[lp][k], b);
+            sm.bias[lp][g] = b;
+        }
+        for (int i = tid; i < NPG * 16 * SPG; i += 256) {
+            const int lp = i / (16 * SPG), r = i % (16 * SPG), g = r / SPG, k = r % SPG;
+            sm.qsal[lp][g * SPG + k] = s_q[g * D + sm.src[lp][k]];
+        }
     }
     __syncthreads();
 
@@ -349,7 +386,7 @@ __global__ __launch_bounds__(256, 2) void decode_paged(PagedArgs a)
     f32x4 acc[8];
 #pragma unroll
     for (int n = 0; n < 8; ++n) acc[n] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-    uint32_t *vt = s_v[wave];
+    uint32_t *vt = s_v + wave * (16 * VR);
 
     if (base < ntok) {
         // a token is live when it exists in this partition and (packed) lies
@@ -357,21 +394,21 @@ __global__ __launch_bounds__(256, 2) void decode_paged(PagedArgs a)
         // position is past the sink (kernels.py:37,48)
         auto live = [&](int t) -> bool {
             if (t >= ntok) return false;
-            if (packed) return s_pok[t / B] && tok0 + t >= geo.sink;
+            if constexpr (PACKED) return sm.pok[t / B] && tok0 + t >= geo.sink;
             const int slot = slot0 + t;
             return slot < geo.sink || (slot >= 4 && slot < 4 + geo.tail && geo.npg * B + slot - 4 >= geo.sink);
         };
         f32x4 sc[4];
-        if (packed) {
+        if constexpr (PACKED) {
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
                 const int lp = (base + 16 * j) / B;
                 asm volatile("" ::: "memory");
-                const float bias = s_bias[lp][gl];
+                const float bias = sm.bias[lp][gl];
                 f32x4 s = {bias, bias, bias, bias};
 #pragma unroll
                 for (int d = 0; d < 4; ++d) {
-                    const float *ka = &s_ka[lp][ql * KG + 8 * d];
+                    const float *ka = &sm.ka[lp][ql * KG + 8 * d];
                     const u32x4 a03 = *(const u32x4 *)ka, a47 = *(const u32x4 *)(ka + 4);
                     float A[8], Bc[8];
 #pragma unroll
@@ -404,12 +441,12 @@ __global__ __launch_bounds__(256, 2) void decode_paged(PagedArgs a)
             for (int j = 0; j < 4; ++j) {
                 const int lp = (base + 16 * j) / B;
                 const uint8_t *rowp = kt + (16 * j + gl) * (4 * KROW);
-                const u32x2 qs = *(const u32x2 *)(&s_qsal[lp][gl * SPG + 4 * ql]);
+                const u32x2 qs = *(const u32x2 *)(&sm.qsal[lp][gl * SPG + 4 * ql]);
                 float v[4];
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
-                    const uint32_t w = s_salw[lp][4 * ql + e];
-                    const f32x2 sf = s_salf[lp][4 * ql + e];
+                    const uint32_t w = sm.salw[lp][4 * ql + e];
+                    const f32x2 sf = sm.salf[lp][4 * ql + e];
                     const uint32_t hi = (rowp[w & 0xffu] >> ((w >> 8) & 0xffu)) & 15u;
                     const uint32_t lo = (rowp[(w >> 16) & 0xffu] >> (w >> 24)) & 15u;
                     v[e] = fmaf((float)((hi << 4) | lo), sf.x, sf.y);
@@ -478,15 +515,15 @@ __global__ __launch_bounds__(256, 2) void decode_paged(PagedArgs a)
 #pragma unroll
         for (int m = 0; m < 2; ++m) {
             uint32_t *dst = vt + pl * VR + 32 * qq;    // token pair pl, channels 32 qq .. 32 qq + 31
-            if (packed) {
+            if constexpr (PACKED) {
                 // dead tokens decode to zero: a zero weight times a non-finite
-                // value (a page id outside the pool) would still poison P.V
+                // value (a page outside the pool) would still poison P.V
                 float s9[2], of[2];
 #pragma unroll
                 for (int u = 0; u < 2; ++u) {
                     const bool ok = live(base + 32 * m + 2 * pl + u);
-                    s9[u] = ok ? iq_f16_to_f32(vp[m][u][0]) * inv_unit : 0.0f;
-                    of[u] = ok ? iq_f16_to_f32(vp[m][u][1]) : 0.0f;
+                    s9[u] = ok ? iq_f16_to_f32((uint16_t)vp[m][u][0]) * inv_unit : 0.0f;
+                    of[u] = ok ? iq_f16_to_f32((uint16_t)vp[m][u][1]) : 0.0f;
                 }
 #pragma unroll
                 for (int w = 0; w < 2; ++w) {          // 16 channels 32 qq + 16 w + (4 b + k)
@@ -551,63 +588,84 @@ __global__ __launch_bounds__(256, 2) void decode_paged(PagedArgs a)
     }
 
     // ---------------- combine the four wavefronts, write this partition's partial
+    // Each wavefront rescales its O to the workgroup's running max in
+    // registers and stages it as O[g][c] rows; readers then only add.
     l_run = xsum16(l_run);
-    if (ql == 0) {
-        s_wm[wave][gl] = m_run;
-        s_wl[wave][gl] = l_run;
-    }
+    if (ql == 0) sm.wm[wave][gl] = m_run;
     __syncthreads();
-    float *ot = (float *)vt;        // O^T[c][g] of this wavefront, row stride 17
+    float mx = sm.wm[0][gl];
 #pragma unroll
-    for (int n = 0; n < 8; ++n)
+    for (int w = 1; w < WAVES; ++w) mx = fmaxf(mx, sm.wm[w][gl]);
+    const float wt = m_run == NEG_INF ? 0.0f : __builtin_amdgcn_exp2f(m_run - mx);
+    if (ql == 0) sm.wl[wave][gl] = l_run * wt;
+    float *ot = (float *)vt;
 #pragma unroll
-        for (int r = 0; r < 4; ++r) ot[(16 * n + 4 * ql + r) * 17 + gl] = acc[n][r];
+    for (int n = 0; n < 8; ++n) *(f32x4 *)(ot + gl * OROW + 16 * n + 4 * ql) = acc[n] * wt;
     __syncthreads();
-    for (int i = tid; i < G * D; i += 256) {
-        const int g = i >> 7, c = i & (D - 1);
-        float mx = NEG_INF;
+    for (int i = tid; i < G * (D / 4); i += 256) {
+        const int g = i >> 5, c = (i & 31) * 4;
+        f32x4 num = *(const f32x4 *)((const float *)sm.v[0] + g * OROW + c);
+        float den = sm.wl[0][g];
 #pragma unroll
-        for (int w = 0; w < WAVES; ++w) mx = fmaxf(mx, s_wm[w][g]);
-        float num = 0.0f, den = 0.0f;
-#pragma unroll
-        for (int w = 0; w < WAVES; ++w) {
-            const float mw = s_wm[w][g];
-            const float wt = mw == NEG_INF ? 0.0f : __builtin_amdgcn_exp2f(mw - mx);
-            num = fmaf(((const float *)s_v[w])[c * 17 + g], wt, num);
-            den = fmaf(s_wl[w][g], wt, den);
+        for (int w = 1; w < WAVES; ++w) {
+            num += *(const f32x4 *)((const float *)sm.v[w] + g * OROW + c);
+            den += sm.wl[w][g];
         }
+        // rows of 130 floats: 8-byte aligned
         float *out = a.ws + (((int64_t)sq * a.H * G + h * G + g) * a.max_parts + p) * (D + 2);
-        out[c] = num;
+        *(f32x2 *)(out + c) = f32x2{num[0], num[1]};
+        *(f32x2 *)(out + c + 2) = f32x2{num[2], num[3]};
         if (c == 0) {
-            out[D] = mx == NEG_INF ? NEG_INF : mx * LN2;
+            float m = sm.wm[0][g];
+#pragma unroll
+            for (int w = 1; w < WAVES; ++w) m = fmaxf(m, sm.wm[w][g]);
+            out[D] = m == NEG_INF ? NEG_INF : m * LN2;
             out[D + 1] = den;
         }
     }
 }
 
-// grid (Hq, D / 32, seq): merges the partitions of one sequence.
+// One workgroup per (KV head, partition, sequence); NPG = pages per packed
+// partition (PART / B).
+template <int NPG>
+__global__ __launch_bounds__(256, 2) void decode_paged(PagedArgs a)
+{
+    __shared__ PagedSmem<NPG> sm;
+    const int p = blockIdx.y, sq = blockIdx.z;
+    // this thread's block-table entry, requested before the lengths arrive
+    int pid = 0;
+    if (a.max_pages > 0) pid = a.bt[sq * a.bt_ss + min((int64_t)p * NPG + (int)(threadIdx.x % NPG), a.max_pages - 1)];
+    const SeqGeom geo = seq_geom(a, sq);
+    if (p >= geo.npp + geo.ndp) return;
+    if (p < geo.npp) paged_body<NPG, true>(a, sm, geo, pid);
+    else paged_body<NPG, false>(a, sm, geo, pid);
+}
+
+// grid (Hq, D / 16, seq): merges the partitions of one sequence; thread
+// (part, c) merges every 16th partition of channel c, then the 16 states of a
+// channel merge through lane shuffles and LDS (as decode_reduce).
 __global__ __launch_bounds__(256) void paged_reduce(PagedArgs a, void *out, int64_t out_ss, int odt)
 {
-    __shared__ float s_m[256], s_n[256], s_l[256];
-    const int hq = blockIdx.x, c0 = blockIdx.y * 32, sq = blockIdx.z;
-    const int tid = threadIdx.x, c = tid & 31, part = tid >> 5;
+    __shared__ float s_m[4][16], s_n[4][16], s_l[4][16];
+    const int hq = blockIdx.x, c0 = blockIdx.y * 16, sq = blockIdx.z;
+    const int tid = threadIdx.x, c = tid & 15, part = tid >> 4, lane = tid & 63, wave = tid >> 6;
     const SeqGeom geo = seq_geom(a, sq);
     const int P = geo.npp + geo.ndp;
     const float *base = a.ws + ((int64_t)sq * a.H * a.G + hq) * a.max_parts * (D + 2);
     float m = NEG_INF, num = 0.0f, den = 0.0f;
-    for (int p0 = part; p0 < P; p0 += 8 * 16) {
+    for (int p0 = part; p0 < P; p0 += 16 * 16) {
         // every load of the round first, the masks after (see decode_reduce)
         float mv[16], lv[16], av[16];
 #pragma unroll
         for (int k = 0; k < 16; ++k) {
-            const float *r = base + min(p0 + 8 * k, P - 1) * (D + 2);
+            const float *r = base + min(p0 + 16 * k, P - 1) * (D + 2);
             mv[k] = r[D];
             lv[k] = r[D + 1];
             av[k] = r[c0 + c];
         }
 #pragma unroll
         for (int k = 0; k < 16; ++k) {
-            const bool ok = p0 + 8 * k < P;
+            const bool ok = p0 + 16 * k < P;
             mv[k] = ok ? mv[k] : NEG_INF;
             lv[k] = ok ? lv[k] : 0.0f;
             av[k] = ok ? av[k] : 0.0f;
@@ -627,22 +685,26 @@ __global__ __launch_bounds__(256) void paged_reduce(PagedArgs a, void *out, int6
         }
         m = mm;
     }
-    s_m[tid] = m;
-    s_n[tid] = num;
-    s_l[tid] = den;
+    float mw = fmaxf(m, __shfl_xor(m, 16, 64));
+    mw = fmaxf(mw, __shfl_xor(mw, 32, 64));
+    if (lane < 16) s_m[wave][c] = mw;
     __syncthreads();
-    if (tid < 32) {
-        float mm = NEG_INF;
-        for (int k = 0; k < 8; ++k) mm = fmaxf(mm, s_m[k * 32 + tid]);
-        float nn = 0.0f, dd = 0.0f;
-        for (int k = 0; k < 8; ++k) {
-            const float mk = s_m[k * 32 + tid];
-            if (mk == NEG_INF) continue;
-            const float w = __expf(mk - mm);
-            nn = fmaf(s_n[k * 32 + tid], w, nn);
-            dd = fmaf(s_l[k * 32 + tid], w, dd);
-        }
-        iq_store_as(out, sq * out_ss + (int64_t)hq * D + c0 + tid, nn / dd, odt);
+    const float mm = fmaxf(fmaxf(s_m[0][c], s_m[1][c]), fmaxf(s_m[2][c], s_m[3][c]));
+    const float wt = m == NEG_INF ? 0.0f : __expf(m - mm);
+    float n = num * wt, d = den * wt;
+    n += __shfl_xor(n, 16, 64);
+    d += __shfl_xor(d, 16, 64);
+    n += __shfl_xor(n, 32, 64);
+    d += __shfl_xor(d, 32, 64);
+    if (lane < 16) {
+        s_n[wave][c] = n;
+        s_l[wave][c] = d;
+    }
+    __syncthreads();
+    if (tid < 16) {
+        const float nn = s_n[0][c] + s_n[1][c] + s_n[2][c] + s_n[3][c];
+        const float dd = s_l[0][c] + s_l[1][c] + s_l[2][c] + s_l[3][c];
+        iq_store_as(out, sq * out_ss + (int64_t)hq * D + c0 + c, nn / dd, odt);
     }
 }
 
@@ -762,7 +824,7 @@ extern "C" int iq_paged_decode(const void *q, int64_t q_stride_seq, int64_t q_st
     default: hipLaunchKernelGGL(decode_paged<1>, grid, dim3(256), 0, st, a); break;
     }
     IQ_CHECK_LAUNCH("decode_paged");
-    hipLaunchKernelGGL(paged_reduce, dim3((unsigned)Hq, D / 32, (unsigned)n_seq), dim3(256), 0, st, a, out,
+    hipLaunchKernelGGL(paged_reduce, dim3((unsigned)Hq, D / 16, (unsigned)n_seq), dim3(256), 0, st, a, out,
                        out_stride_seq, out_dtype);
     IQ_CHECK_LAUNCH("paged_reduce");
     return IQ_OK;
