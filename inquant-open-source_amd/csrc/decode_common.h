@@ -91,6 +91,15 @@ __device__ __forceinline__ T ldg(const void *p)
 
 __device__ __forceinline__ u32x4 ld16(const void *p) { return ldg<u32x4>(p); }
 
+// Streaming loads of packed payload, read once per call: the non-temporal hint
+// keeps them from displacing small, re-read data (pointer tables, scales,
+// queries, partials) in the caches.
+template <class T>
+__device__ __forceinline__ T ldnt(const void *p)
+{
+    return __builtin_nontemporal_load((const __attribute__((address_space(1))) T *)p);
+}
+
 constexpr float NEG_INF = -__builtin_inff();
 
 }  // namespace

@@ -297,7 +297,7 @@ __device__ __forceinline__ void paged_body(const PagedArgs &a, PagedSmem<NPG> &s
         for (int j = 0; j < 4; ++j) {
             const int t = min(base + 16 * j + gl, ntok - 1);
             const uint8_t *page = (const uint8_t *)sm.page[t / B];
-            kw[j] = ld16(page + ((int64_t)h * B + t % B) * 64 + 16 * ql);
+            kw[j] = ldnt<u32x4>(page + ((int64_t)h * B + t % B) * 64 + 16 * ql);
         }
 #pragma unroll
         for (int m = 0; m < 2; ++m)
@@ -306,7 +306,7 @@ __device__ __forceinline__ void paged_body(const PagedArgs &a, PagedSmem<NPG> &s
                 const int t = min(base + 32 * m + 2 * pl + u, ntok - 1);
                 const uint8_t *page = (const uint8_t *)sm.page[t / B];
                 const int64_t r = (int64_t)h * B + t % B;
-                const u32x2 w = ldg<u32x2>(page + a.off.vp + r * 32 + 8 * qq);
+                const u32x2 w = ldnt<u32x2>(page + a.off.vp + r * 32 + 8 * qq);
                 vw[m][u][0] = w[0];
                 vw[m][u][1] = w[1];
                 vp[m][u][0] = ldg<uint16_t>(page + a.off.vs + (r * 2 + (qq >> 1)) * 2);
