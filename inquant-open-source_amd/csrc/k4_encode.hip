@@ -188,18 +188,23 @@ __global__ __launch_bounds__(K4_THREADS) void k4_encode_kernel(K4Args a)
 
 // ---------------------------------------------------------------------------
 // Tile encoder for the cache shapes: D = 128, 16-bit input, T <= 256 tokens,
-// channel-contiguous rows.  The whole [T, 128] block is staged in LDS with
-// 16-byte loads (64 KiB at T = 256), then
-//   waves 0-1  the fp64 Welford var_mean of channel tid (min_error only);
-//              delta / n uses a table of RN(1/n) and one remainder fma,
-//              which is the correctly rounded quotient for n <= 256;
-//   waves 2-3  sampled sums (torch cascade order), amax, finiteness;
-// wave 0 selects donors, and every thread quantizes 8 channels of a token
-// per step from LDS, writing 4 payload bytes.  Bit-identical to
-// k4_encode_kernel.
+// channel-contiguous rows.  The block streams through LDS in 32-token chunks
+// (double-buffered, 16-byte loads, three chunks in flight while the current
+// one is consumed), twice:
+//   pass 1  waves 0-1: the fp64 Welford var_mean of channel tid (min_error
+//           only); delta / n uses a table of RN(1/n) and one remainder fma,
+//           which is the correctly rounded quotient for n <= 256;
+//           waves 2-3: sampled sums (torch cascade order), amax, finiteness;
+//   then    donor selection by the whole workgroup (iq_select_tile128);
+//   pass 2  every thread quantizes 8 channels of a token per step, writing
+//           4 payload bytes.
+// LDS stays near 24 KiB, so several blocks share a compute unit and their
+// latency-bound phases (the Welford chains, the donor picks) overlap.
+// Bit-identical to k4_encode_kernel.
 constexpr int TILE_D = 128;
 constexpr int TILE_T = 256;
-constexpr int XROW = TILE_D + 2;         // u16 per staged row: 65 dwords, so the 4 tokens a wave reads fall on distinct banks
+constexpr int CH = 32;                   // tokens per staged chunk
+constexpr int XROW = TILE_D + 8;         // u16 per staged row: 68 dwords (16-byte aligned rows, distinct banks)
 
 template <bool F16IN>
 __device__ __forceinline__ float tile_f32(uint32_t bits16)
@@ -211,110 +216,156 @@ __device__ __forceinline__ float tile_f32(uint32_t bits16)
 template <bool F16IN>
 __global__ __launch_bounds__(K4_THREADS) void k4_encode_tile(K4Args a)
 {
-    __shared__ __attribute__((aligned(16))) uint16_t s_x[TILE_T * XROW];
+    __shared__ __attribute__((aligned(16))) uint16_t s_x[2][CH * XROW];
     __shared__ double s_rcp[TILE_T];    // RN(1 / n), n = 1 .. T
-    __shared__ float s_sal[TILE_D], s_smean[TILE_D], s_err[TILE_D], s_amax[TILE_D], s_scale[TILE_D];
+    __shared__ __attribute__((aligned(16))) float s_sal[TILE_D], s_smean[TILE_D], s_err[TILE_D], s_amax[TILE_D],
+        s_scale[TILE_D];
     __shared__ int16_t s_src_of[TILE_D];
     __shared__ uint8_t s_is_src[TILE_D];
     __shared__ int16_t s_src[TILE_D / 2], s_don[TILE_D / 2];
+    __shared__ __attribute__((aligned(16))) uint64_t s_key[TILE_D];
+    __shared__ __attribute__((aligned(16))) int s_part[K4_THREADS];
+    __shared__ __attribute__((aligned(16))) uint8_t s_flag[TILE_D];
+    __shared__ int16_t s_list[TILE_D / 2];
     __shared__ int s_bad;
 
-    const int tid = threadIdx.x;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int64_t row = blockIdx.x;
     const int64_t b = row / a.H, h = row % a.H;
     const uint16_t *xr = (const uint16_t *)a.x + b * a.sb + h * a.sh;
     const int T = (int)a.T;
     const int ns = (int)((T + a.stride - 1) / a.stride);
+    const int nch = (T + CH - 1) / CH;
 
-    // ---- stage the block: T rows x 16 segments of 8 channels
-    {
-        u32x4_t v[TILE_T * 16 / K4_THREADS];
-        // unconditional (clamped) loads so that all of them are in flight at once
+    // chunk staging: thread tid moves segments tid and tid + 256 (row i / 16,
+    // 8 channels at 8 (i % 16)); rows past T are clamped copies, never read.
+    // Three chunks stay in flight in registers (about 24 KiB per block), which
+    // is what covers the load latency while every block streams at once.
+    u32x4_t seg[3][2];
+    auto load_chunk = [&](int ch, u32x4_t (&sg)[2]) {
 #pragma unroll
-        for (int k = 0; k < TILE_T * 16 / K4_THREADS; ++k) {
-            const int i = min(tid + K4_THREADS * k, T * 16 - 1);
-            v[k] = *(const u32x4_t *)(xr + (int64_t)(i >> 4) * a.st + 8 * (i & 15));
+        for (int k = 0; k < 2; ++k) {
+            const int i = tid + K4_THREADS * k;
+            const int t = min(ch * CH + (i >> 4), T - 1);
+            sg[k] = *(const u32x4_t *)(xr + (int64_t)t * a.st + 8 * (i & 15));
         }
-        // rows at and beyond T receive copies of the last segment and are never read
+    };
+    auto store_chunk = [&](const u32x4_t (&sg)[2], int buf) {
 #pragma unroll
-        for (int k = 0; k < TILE_T * 16 / K4_THREADS; ++k) {
-            const int i = tid + K4_THREADS * k;       // row i / 16, segment i % 16 (4-byte aligned)
-            uint32_t *d = (uint32_t *)(s_x + (i >> 4) * XROW + 8 * (i & 15));
-#pragma unroll
-            for (int w = 0; w < 4; ++w) d[w] = v[k][w];
+        for (int k = 0; k < 2; ++k) {
+            const int i = tid + K4_THREADS * k;
+            *(u32x4_t *)(s_x[buf] + (i >> 4) * XROW + 8 * (i & 15)) = sg[k];
         }
-    }
+    };
+    // chunks 0..2 are loaded and chunk 0 is in LDS buffer 0; visits chunks in
+    // order, with chunk ch in buffer ch & 1 during body(ch)
+    auto start_stream = [&]() {
+#pragma unroll
+        for (int r = 0; r < 3; ++r)
+            if (r < nch) load_chunk(r, seg[r]);
+    };
+    auto stream = [&](auto &&body) {
+        for (int c0 = 0; c0 < nch; c0 += 3) {
+#pragma unroll
+            for (int r = 0; r < 3; ++r) {
+                const int ch = c0 + r;
+                if (ch < nch) {
+                    if (ch + 3 < nch) load_chunk(ch + 3, seg[r]);   // seg[r] already sits in LDS
+                    body(ch);
+                    if (ch + 1 < nch) store_chunk(seg[(r + 1) % 3], (ch + 1) & 1);
+                    __syncthreads();
+                }
+            }
+        }
+    };
+
+    start_stream();
     if (tid < T) s_rcp[tid] = 1.0 / (double)(tid + 1);
     if (tid == 0) s_bad = 0;
+    store_chunk(seg[0], 0);
     __syncthreads();
 
+    // ---- pass 1: statistics
+    double mean = 0.0, m2 = 0.0;                  // waves 0-1, channel tid
+    IqCascade sa, sm;                             // waves 2-3, channel tid - 128
+    sa.init(ns);
+    sm.init(ns);
+    float amax = 0.0f;
+    bool bad = false;
+    int next_sample = 0;
+    const int c1 = tid & (TILE_D - 1);
+    stream([&](int ch) {
+        const uint16_t *xs = s_x[ch & 1] + c1;
+        const int t0 = ch * CH, nt = min(CH, T - t0);
+        if (tid < TILE_D) {
+            if (a.min_error) {
+                auto step = [&](float xf, double y, int t) {
+                    const double dv = (double)xf;
+                    const double delta = __dsub_rn(dv, mean);
+                    const double q0 = __dmul_rn(delta, y);
+                    const double r = __builtin_fma(-q0, (double)(t + 1), delta);
+                    mean = __dadd_rn(mean, __builtin_fma(r, y, q0));
+                    const double nd = __dsub_rn(dv, mean);
+                    m2 = __dadd_rn(m2, __dmul_rn(delta, nd));
+                };
+                if (nt == CH) {
+                    // LDS reads of the next eight tokens in flight while the
+                    // current eight dependent steps run
+                    float cur[8], nxt[8];
+                    double ycur[8], ynxt[8];
+#pragma unroll
+                    for (int u = 0; u < 8; ++u) {
+                        cur[u] = tile_f32<F16IN>(xs[u * XROW]);
+                        ycur[u] = s_rcp[t0 + u];
+                    }
+#pragma unroll
+                    for (int g = 0; g < CH; g += 8) {
+                        const int gn = g + 8 < CH ? g + 8 : g;
+#pragma unroll
+                        for (int u = 0; u < 8; ++u) {
+                            nxt[u] = tile_f32<F16IN>(xs[(gn + u) * XROW]);
+                            ynxt[u] = s_rcp[t0 + gn + u];
+                        }
+#pragma unroll
+                        for (int u = 0; u < 8; ++u) step(cur[u], ycur[u], t0 + g + u);
+#pragma unroll
+                        for (int u = 0; u < 8; ++u) {
+                            cur[u] = nxt[u];
+                            ycur[u] = ynxt[u];
+                        }
+                    }
+                } else {
+                    for (int u = 0; u < nt; ++u) step(tile_f32<F16IN>(xs[u * XROW]), s_rcp[t0 + u], t0 + u);
+                }
+            }
+        } else {
+            for (int u = 0; u < nt; ++u) {
+                const float v = tile_f32<F16IN>(xs[u * XROW]);
+                bad |= !iq_isfinite(v);
+                amax = fmaxf(amax, fabsf(v));
+            }
+            // the samples r * stride that fall in this chunk, in order
+            for (; next_sample < t0 + nt; next_sample += (int)a.stride) {
+                const float v = tile_f32<F16IN>(xs[(next_sample - t0) * XROW]);
+                sa.add(fabsf(v));
+                sm.add(v);
+            }
+        }
+    });
     if (tid < TILE_D) {
         if (a.min_error) {
-            const int c = tid;
-            double mean = 0.0, m2 = 0.0;
-            auto step = [&](float xf, double y, int t) {
-                const double dv = (double)xf;
-                const double delta = __dsub_rn(dv, mean);
-                const double q0 = __dmul_rn(delta, y);
-                const double r = __builtin_fma(-q0, (double)(t + 1), delta);
-                mean = __dadd_rn(mean, __builtin_fma(r, y, q0));
-                const double nd = __dsub_rn(dv, mean);
-                m2 = __dadd_rn(m2, __dmul_rn(delta, nd));
-            };
-            // groups of eight tokens, the next group's LDS reads in flight
-            // while the current group's dependent steps run
-            const int Tg = T & ~7;
-            float cur[8], nxt[8];
-            double ycur[8], ynxt[8];
-#pragma unroll
-            for (int u = 0; u < 8; ++u) {
-                cur[u] = Tg ? tile_f32<F16IN>(s_x[u * XROW + c]) : 0.0f;
-                ycur[u] = s_rcp[u];
-            }
-            for (int t0 = 0; t0 < Tg; t0 += 8) {
-                const int tn = t0 + 8 < Tg ? t0 + 8 : t0;
-#pragma unroll
-                for (int u = 0; u < 8; ++u) {
-                    nxt[u] = tile_f32<F16IN>(s_x[(tn + u) * XROW + c]);
-                    ynxt[u] = s_rcp[tn + u];
-                }
-#pragma unroll
-                for (int u = 0; u < 8; ++u) step(cur[u], ycur[u], t0 + u);
-#pragma unroll
-                for (int u = 0; u < 8; ++u) {
-                    cur[u] = nxt[u];
-                    ycur[u] = ynxt[u];
-                }
-            }
-            for (int t = Tg; t < T; ++t) step(tile_f32<F16IN>(s_x[t * XROW + c]), s_rcp[t], t);
-            s_err[c] = (float)(m2 / (double)T);     // var; the mean term is added below
-            s_smean[c] = (float)mean;                                // full mean, replaced below
+            s_err[c1] = (float)(m2 / (double)T);      // var; the mean term is added below
+            s_smean[c1] = (float)mean;                // full mean, replaced below
         }
     } else {
-        const int c = tid - TILE_D;
-        IqCascade sa, sm;
-        sa.init(ns);
-        sm.init(ns);
-#pragma unroll 8
-        for (int r = 0; r < ns; ++r) {
-            const float v = tile_f32<F16IN>(s_x[(int)(r * a.stride) * XROW + c]);
-            sa.add(fabsf(v));
-            sm.add(v);
-        }
-        float amax = 0.0f;
-        bool bad = false;
-#pragma unroll 16
-        for (int t = 0; t < T; ++t) {
-            const float v = tile_f32<F16IN>(s_x[t * XROW + c]);
-            bad |= !iq_isfinite(v);
-            amax = fmaxf(amax, fabsf(v));
-        }
-        s_amax[c] = amax;
-        s_sal[c] = sa.finish() / (float)ns;
+        s_amax[c1] = amax;
+        s_sal[c1] = sa.finish() / (float)ns;
         if (bad) s_bad = 1;
         // stash the sampled mean until the Welford waves are done with s_smean
-        s_scale[c] = sm.finish() / (float)ns;
+        s_scale[c1] = sm.finish() / (float)ns;
     }
+    // the first chunks of pass 2 load during the selection
+    start_stream();
     __syncthreads();
     if (tid < TILE_D) {
         const float smean = s_scale[tid];
@@ -326,9 +377,8 @@ __global__ __launch_bounds__(K4_THREADS) void k4_encode_tile(K4Args a)
     }
     __syncthreads();
 
-    if (tid < 64)
-        iq_select_wave_t<2>(s_sal, a.min_error ? s_err : nullptr, TILE_D, (int)a.count, s_src, s_don, s_is_src,
-                       s_src_of);
+    iq_select_tile128(s_sal, a.min_error ? s_err : nullptr, (int)a.count, s_src, s_don, s_is_src, s_src_of,
+                      s_key, s_part, s_flag, s_list);
     __syncthreads();
 
     const float flt_min = 1.17549435e-38f;
@@ -344,11 +394,13 @@ __global__ __launch_bounds__(K4_THREADS) void k4_encode_tile(K4Args a)
         a.padding[row * a.count + tid] = s_smean[s_don[tid]];
     }
     if (tid == 0 && s_bad) atomicOr(a.bad, 1);
+    store_chunk(seg[0], 0);
     __syncthreads();
 
-    // ---- quantize: thread owns channels 8 j .. 8 j + 7 of tokens t0, t0 + 16, ...
-    const int j = tid & 15;
-    float scl[8], rscl[8], lim[8];
+    // ---- pass 2: quantize; thread owns channels 8 j .. 8 j + 7 of tokens
+    // t0 + 8 wave + tq and t0 + 8 wave + tq + 4 of every chunk
+    const int j = lane & 15, tq = lane >> 4;
+    float scl[8], rscl[8], lim[8], bias[8];
     int shift[8], srcc[8];
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
@@ -360,37 +412,49 @@ __global__ __launch_bounds__(K4_THREADS) void k4_encode_tile(K4Args a)
         scl[e] = s_scale[srcc[e]];
         rscl[e] = __builtin_amdgcn_rcpf(scl[e]);
         lim[e] = (hi || lo) ? 127.0f : 7.0f;
+        // q + lim + 1 lands in the low mantissa bits of 1.5 * 2^23 + (lim + 1)
+        bias[e] = 12582912.0f + lim[e] + 1.0f;
         shift[e] = hi ? 4 : 0;
     }
     uint32_t *out = (uint32_t *)(a.payload + row * (int64_t)T * (TILE_D / 2));
-    for (int t = tid >> 4; t < T; t += K4_THREADS / 16) {
-        const uint16_t *xt = s_x + t * XROW;
-        // branch-free: every channel reads the value it encodes (its own, or
-        // for a donor slot its source's), the reciprocal quotient decides the
-        // rounding, and only a token with a near-tie quotient divides exactly
-        float v[8], q[8];
-        bool near = false;
+    stream([&](int ch) {
+        const int t0 = ch * CH;
 #pragma unroll
-        for (int e = 0; e < 8; ++e) v[e] = tile_f32<F16IN>(xt[srcc[e]]);
+        for (int it = 0; it < 2; ++it) {
+            const int tl = 8 * wave + 4 * it + tq, t = t0 + tl;
+            if (t < T) {
+                const uint16_t *xt = s_x[ch & 1] + tl * XROW;
+                // branch-free: every channel reads the value it encodes (its
+                // own, or for a donor slot its source's); the reciprocal
+                // quotient decides the rounding unless it is within 2^-12 of
+                // a half-integer, where the exact quotient decides.  Below
+                // |q| = 256 the reciprocal's error is under 2^-14; beyond
+                // it every code clamps to +-lim either way.
+                float v[8], q[8];
+                bool near = false;
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-            const float f = __fmul_rn(v[e], rscl[e]);
-            q[e] = rintf(f);
-            near |= !(0.5f - fabsf(__fsub_rn(f, q[e])) > fabsf(f) * 0x1p-20f);
+                for (int e = 0; e < 8; ++e) v[e] = tile_f32<F16IN>(xt[srcc[e]]);
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    const float f = __fmul_rn(v[e], rscl[e]);
+                    q[e] = rintf(f);
+                    near |= fabsf(__fsub_rn(f, q[e])) >= 0.5f - 0x1p-12f;
+                }
+                if (near) {
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) q[e] = iq_rint_div(v[e], scl[e], rscl[e]);
+                }
+                uint32_t word = 0;
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    const float qc = __builtin_amdgcn_fmed3f(q[e], -lim[e], lim[e]);
+                    const uint32_t code = __float_as_uint(__fadd_rn(qc, bias[e]));
+                    word |= ((code >> shift[e]) & 15u) << (4 * e);
+                }
+                out[t * (TILE_D / 8) + j] = word;
+            }
         }
-        if (near) {
-#pragma unroll
-            for (int e = 0; e < 8; ++e) q[e] = iq_rint_div(v[e], scl[e], rscl[e]);
-        }
-        uint32_t word = 0;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-            const float qc = fminf(fmaxf(q[e], -lim[e]), lim[e]);
-            const uint32_t code = (uint32_t)(int)(qc + lim[e] + 1.0f);
-            word |= ((code >> shift[e]) & 15u) << (4 * e);
-        }
-        out[t * (TILE_D / 8) + j] = word;
-    }
+    });
 }
 
 struct SelectArgs {

@@ -188,6 +188,136 @@ __device__ __forceinline__ void iq_select_wave_t(const float *sal, const float *
     }
 }
 
+// Lanes' versions of iq_bit_below / iq_bit_above for D = 128 (two mask words,
+// per-lane position).
+__device__ __forceinline__ int iq_lane_bit_below(uint64_t m0, uint64_t m1, int pos)
+{
+    const uint64_t w1 = pos <= 64 ? 0ull : pos >= 128 ? m1 : m1 & ((1ull << (pos - 64)) - 1);
+    const uint64_t w0 = pos <= 0 ? 0ull : pos >= 64 ? m0 : m0 & ((1ull << pos) - 1);
+    return w1 ? 127 - __builtin_clzll(w1) : w0 ? 63 - __builtin_clzll(w0) : -1;
+}
+
+__device__ __forceinline__ int iq_lane_bit_above(uint64_t m0, uint64_t m1, int pos)
+{
+    const uint64_t w0 = pos >= 63 ? 0ull : pos < 0 ? m0 : m0 & ~((2ull << pos) - 1);
+    const uint64_t w1 = pos >= 127 ? 0ull : pos < 64 ? m1 : m1 & ~((2ull << (pos - 64)) - 1);
+    return w0 ? __builtin_ctzll(w0) : w1 ? 64 + __builtin_ctzll(w1) : 128;
+}
+
+// The selection of iq_select_wave_t<2> for one D = 128 row, computed by a
+// whole 256-thread workgroup (every thread calls it: it holds barriers).
+// Sources and the min_error pool come from ranks over all channel pairs:
+// each channel gets a 64-bit key that orders it exactly as the stable sort
+// does (the value's bits, then the channel as tie-break), and its rank is the
+// number of keys ordered before it, each thread comparing against 64 of
+// them.  The sequential donor picks then run on wave 0 from the neighbour
+// order and run boundaries precomputed one source per lane, so a pick with a
+// free neighbour is a handful of scalar operations.  LDS scratch: key[128],
+// part[256], flag[128], list[64].
+__device__ __forceinline__ void iq_select_tile128(const float *sal, const float *err, int count,
+                                                  int16_t *src_out, int16_t *don_out, uint8_t *is_src,
+                                                  int16_t *src_of, uint64_t *key, int *part, uint8_t *flag,
+                                                  int16_t *list)
+{
+    typedef __attribute__((ext_vector_type(2))) uint64_t v2u64;
+    const int tid = threadIdx.x, c = tid & 127, half = tid >> 7, lane = tid & 63;
+    // 1. sources: the `count` channels first in descending saliency, ties to
+    //    the lower channel; as one ascending key: ~bits, then the channel
+    if (tid < 128) key[c] = ((uint64_t)~iq_nonneg_bits(sal[c]) << 7) | (uint64_t)c;
+    __syncthreads();
+    {
+        const uint64_t mine = key[c];
+        int r = 0;
+#pragma unroll 8
+        for (int k = 0; k < 64; k += 2) {
+            const v2u64 kk = *(const v2u64 *)(key + 64 * half + k);
+            r += kk[0] < mine;
+            r += kk[1] < mine;
+        }
+        part[tid] = r;
+    }
+    __syncthreads();
+    const bool sel = part[c] + part[c + 128] < count;
+    bool avail = !sel;
+    if (err) {  // 2. pool: the `count` non-sources first in ascending error, ties to the lower channel
+        if (tid < 128) key[c] = sel ? ~0ull : ((uint64_t)iq_nonneg_bits(err[c]) << 7) | (uint64_t)c;
+        __syncthreads();
+        const uint64_t mine = key[c];
+        int r = 0;
+#pragma unroll 8
+        for (int k = 0; k < 64; k += 2) {
+            const v2u64 kk = *(const v2u64 *)(key + 64 * half + k);
+            r += kk[0] < mine;
+            r += kk[1] < mine;
+        }
+        __syncthreads();            // every thread has read part[] for sel
+        part[tid] = r;
+        __syncthreads();
+        avail = !sel && part[c] + part[c + 128] < count;
+    }
+    if (tid < 128) flag[c] = (sel ? 1 : 0) | (avail ? 2 : 0);
+    __syncthreads();
+    if (tid >= 64) return;
+
+    // 3. sequential donor picks on wave 0; sources in ascending channel order
+    const uint32_t f0 = flag[lane], f1 = flag[64 + lane];
+    const uint64_t sel0 = __ballot(f0 & 1u), sel1 = __ballot(f1 & 1u);
+    uint64_t av0 = __ballot(f0 & 2u), av1 = __ballot(f1 & 2u);
+    const uint64_t below = (1ull << lane) - 1;
+    if (f0 & 1u) list[__popcll(sel0 & below)] = (int16_t)lane;
+    if (f1 & 1u) list[__popcll(sel0) + __popcll(sel1 & below)] = (int16_t)(64 + lane);
+    is_src[lane] = (uint8_t)(f0 & 1u);
+    is_src[64 + lane] = (uint8_t)(f1 & 1u);
+    src_of[lane] = -1;
+    src_of[64 + lane] = -1;
+    const uint32_t sk0 = iq_nonneg_bits(sal[lane]), sk1 = iq_nonneg_bits(sal[64 + lane]);
+    // lane i: the i-th source s, whether its left neighbour wins a saliency
+    // comparison with the right one, and its selected run [lb, rb], packed
+    // into one word so that a pick reads them with a single readlane
+    const int s = lane < count ? list[lane] : 0;
+    const uint32_t kl = s >= 1 ? iq_nonneg_bits(sal[s - 1]) : ~0u;
+    const uint32_t kr = s + 1 < 128 ? iq_nonneg_bits(sal[s + 1]) : ~0u;
+    const int lb = iq_lane_bit_below(~sel0, ~sel1, s) + 1;
+    const int rb = iq_lane_bit_above(~sel0, ~sel1, s) - 1;
+    const uint32_t wv = (uint32_t)s | ((kl <= kr ? 1u : 0u) << 8) | ((uint32_t)lb << 9) | ((uint32_t)(rb + 1) << 17);
+    int don_v = 0;
+    for (int i = 0; i < count; ++i) {
+        const uint32_t w = __builtin_amdgcn_readlane(wv, i);
+        const int si = (int)(w & 255u), l1 = si - 1, r1 = si + 1;
+        const bool lo = l1 >= 0 && (((l1 < 64 ? av0 : av1) >> (l1 & 63)) & 1ull);
+        const bool ro = r1 < 128 && (((r1 < 64 ? av0 : av1) >> (r1 & 63)) & 1ull);
+        int donor;
+        if (lo || ro) {
+            donor = (lo && (!ro || ((w >> 8) & 1u))) ? l1 : r1;
+        } else {
+            // the nearest available channel below the run or above it; less
+            // saliency, then the lower channel, on a distance tie
+            const int lbi = (int)((w >> 9) & 255u), rbi = (int)((w >> 17) & 255u) - 1;
+            const uint64_t m[2] = {av0, av1};
+            const int pl = iq_bit_below<2>(m, lbi);
+            const int pr = iq_bit_above<2>(m, rbi, 128);
+            const int dl = pl >= 0 ? lbi - pl : 0x7fffffff;
+            const int dr = pr < 128 ? pr - rbi : 0x7fffffff;
+            donor = 0;            // an empty pool only arises from non-finite statistics
+            if (dl < dr) donor = pl;
+            else if (dr < dl) donor = pr;
+            else if (dl != 0x7fffffff) {
+                const uint32_t ka = __builtin_amdgcn_readlane(pl < 64 ? sk0 : sk1, pl & 63);
+                const uint32_t kb = __builtin_amdgcn_readlane(pr < 64 ? sk0 : sk1, pr & 63);
+                donor = ka <= kb ? pl : pr;
+            }
+        }
+        if (donor < 64) av0 &= ~(1ull << donor);
+        else av1 &= ~(1ull << (donor - 64));
+        don_v = lane == i ? donor : don_v;
+    }
+    if (lane < count) {
+        src_out[lane] = (int16_t)s;
+        don_out[lane] = (int16_t)don_v;
+        src_of[don_v] = (int16_t)s;
+    }
+}
+
 __device__ __forceinline__ void iq_select_wave(const float *sal, const float *err, int D, int count,
                                                int16_t *src_out, int16_t *don_out, uint8_t *is_src,
                                                int16_t *src_of)
