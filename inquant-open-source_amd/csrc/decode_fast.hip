@@ -155,23 +155,33 @@ __device__ __forceinline__ void fast_body(const FastArgs &a, FastSmem &sm)
         }                                                                                             \
     } while (0)
     if (packed) {
-        const int64_t *row = a.tables + p * IQ_TABLE_COLS;
+        // the whole pointer-table row in one round trip (64 bytes, the same
+        // for every lane), its pointers moved to scalar registers
+        const u32x4 *rv = (const u32x4 *)(a.tables + p * IQ_TABLE_COLS);
+        u32x4 tr[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) tr[k] = ldg<u32x4>(rv + k);
+        auto row = [&](int k) -> uintptr_t {
+            const uint32_t lo = __builtin_amdgcn_readfirstlane(tr[k >> 1][2 * (k & 1)]);
+            const uint32_t hi = __builtin_amdgcn_readfirstlane(tr[k >> 1][2 * (k & 1) + 1]);
+            return (uintptr_t)lo | ((uintptr_t)hi << 32);
+        };
         krole = (uint8_t)ldg<int8_t>(a.kmap + (p * a.H + h) * D + (tid & (D - 1)));
-        kscale = ldg<float>((const float *)row[1] + h * D + (tid & (D - 1)));
+        kscale = ldg<float>((const float *)row(1) + h * D + (tid & (D - 1)));
         {   // no branch around these loads: with S == 0 they read valid
             // addresses (the role map, the scales) whose values go unused
             const int k = tid < S ? tid : (S > 0 ? S - 1 : 0);
-            const uint8_t *srcs = S > 0 ? (const uint8_t *)row[6] + h * S : (const uint8_t *)a.kmap;
-            const uint8_t *dons = S > 0 ? (const uint8_t *)row[7] + h * S : (const uint8_t *)a.kmap;
-            const float *pads = S > 0 ? (const float *)row[2] + h * S : (const float *)row[1];
+            const uint8_t *srcs = S > 0 ? (const uint8_t *)row(6) + h * S : (const uint8_t *)a.kmap;
+            const uint8_t *dons = S > 0 ? (const uint8_t *)row(7) + h * S : (const uint8_t *)a.kmap;
+            const float *pads = S > 0 ? (const float *)row(2) + h * S : (const float *)row(1);
             ksrc = ldg<uint8_t>(srcs + k);
             kdon = ldg<uint8_t>(dons + k);
             kpad = ldg<float>(pads + k);
         }
-        kpay = (const uint8_t *)row[0] + (int64_t)h * a.BT * (D / 2);
-        vpay = (const uint8_t *)row[3] + (int64_t)h * a.BT * VROW;
-        vsc = (const uint16_t *)row[4] + (int64_t)h * a.BT * ngroups;
-        voff = (const uint16_t *)row[5] + (int64_t)h * a.BT * ngroups;
+        kpay = (const uint8_t *)row(0) + (int64_t)h * a.BT * (D / 2);
+        vpay = (const uint8_t *)row(3) + (int64_t)h * a.BT * VROW;
+        vsc = (const uint16_t *)row(4) + (int64_t)h * a.BT * ngroups;
+        voff = (const uint16_t *)row(5) + (int64_t)h * a.BT * ngroups;
         stop = (int)a.BT;
         base = CHUNK * wave;
         IQ_LOAD_CHUNK(base);                        // clamped: also for waves past the end
