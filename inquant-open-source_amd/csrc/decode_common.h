@@ -91,6 +91,20 @@ __device__ __forceinline__ T ldg(const void *p)
 
 __device__ __forceinline__ u32x4 ld16(const void *p) { return ldg<u32x4>(p); }
 
+// base + a 32-bit byte offset: with `base` uniform this is the scalar-base
+// form of the load (no 64-bit address arithmetic per lane)
+template <class T>
+__device__ __forceinline__ T ldg_at(const void *base, uint32_t off)
+{
+    return *(const __attribute__((address_space(1))) T *)((const char *)base + off);
+}
+
+template <class T>
+__device__ __forceinline__ T ldnt_at(const void *base, uint32_t off)
+{
+    return __builtin_nontemporal_load((const __attribute__((address_space(1))) T *)((const char *)base + off));
+}
+
 // Streaming loads of packed payload, read once per call: the non-temporal hint
 // keeps them from displacing small, re-read data (pointer tables, scales,
 // queries, partials) in the caches.

@@ -134,23 +134,23 @@ __device__ __forceinline__ void fast_body(const FastArgs &a, FastSmem &sm)
         const int b0 = (b_);                                                                          \
         _Pragma("unroll") for (int j = 0; j < 4; ++j) {                                               \
             const int t = min(b0 + 16 * j + gl, stop - 1);                                            \
-            kw[j] = ldnt<u32x4>(kpay + t * (D / 2) + 16 * ql);                                        \
+            kw[j] = ldnt_at<u32x4>(kpay, (uint32_t)(t * (D / 2) + 16 * ql));                          \
         }                                                                                             \
         const int gi = (32 * qq) / a.vgroup;                                                          \
         _Pragma("unroll") for (int m = 0; m < 2; ++m) {                                               \
             _Pragma("unroll") for (int u = 0; u < 2; ++u) {                                           \
                 const int t = min(b0 + 32 * m + 2 * pl + u, stop - 1);                                \
-                const uint8_t *src = vpay + (int64_t)t * VROW + VQ * qq;                              \
+                const uint32_t vo = (uint32_t)(t * VROW + VQ * qq);                                   \
                 if constexpr (VQW == 2) {                                                             \
-                    const u32x2 r = ldnt<u32x2>(src);                                                 \
+                    const u32x2 r = ldnt_at<u32x2>(vpay, vo);                                         \
                     vw[m][u][0] = r[0];                                                               \
                     vw[m][u][1] = r[1];                                                               \
                 } else {                                                                              \
-                    const u32x4 r = ldnt<u32x4>(src);                                                 \
+                    const u32x4 r = ldnt_at<u32x4>(vpay, vo);                                         \
                     _Pragma("unroll") for (int w = 0; w < VQW; ++w) vw[m][u][w] = r[w];               \
                 }                                                                                     \
-                vp[m][u][0] = ldg<uint16_t>(vsc + t * ngroups + gi);                                  \
-                vp[m][u][1] = ldg<uint16_t>(voff + t * ngroups + gi);                                 \
+                vp[m][u][0] = ldg_at<uint16_t>(vsc, (uint32_t)(2 * (t * ngroups + gi)));              \
+                vp[m][u][1] = ldg_at<uint16_t>(voff, (uint32_t)(2 * (t * ngroups + gi)));             \
             }                                                                                         \
         }                                                                                             \
     } while (0)
