@@ -97,6 +97,10 @@ __device__ __forceinline__ void fast_body(const FastArgs &a, FastSmem &sm)
     float (&s_wl)[WAVES][16] = sm.wl;
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    // Issue priority falls as a wavefront advances through its phases, so
+    // the workgroups sharing a compute unit progress together instead of the
+    // oldest finishing first and leaving the last one alone to run latency-bound.
+    __builtin_amdgcn_s_setprio(3);
     const int gl = lane & 15, ql = lane >> 4;     // MFMA column (query row / channel) and k-slot group
     // V writer: token pair and 32-channel quarter; the 8 lanes of one LDS cycle
     // take 8 different token pairs, so their 16-byte stores hit distinct banks
@@ -356,6 +360,7 @@ __device__ __forceinline__ void fast_body(const FastArgs &a, FastSmem &sm)
             }
         }
 
+        __builtin_amdgcn_s_setprio(2);
         // ---------------- online softmax (log2 domain); lane holds g = gl, tokens 16 j + 4 ql + r
         float cmax = NEG_INF;
         if (full) {
@@ -504,6 +509,7 @@ __device__ __forceinline__ void fast_body(const FastArgs &a, FastSmem &sm)
     }
 #undef IQ_LOAD_CHUNK
 
+    __builtin_amdgcn_s_setprio(1);
     // ---------------- combine the four wavefronts, write this partition's partial
     // Each wavefront rescales its O to the workgroup's running max in
     // registers and stages it as O[g][c] rows; readers then only add.
