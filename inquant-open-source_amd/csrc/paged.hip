@@ -33,7 +33,7 @@ constexpr int PART = 256;              // tokens per partition
 constexpr int VR = 136;                // dwords per staged token-pair row of decoded V
 constexpr int KROW = 17;               // dwords per staged K row (salient byte gathers)
 constexpr int OROW = 132;              // floats per staged output row in the combine (conflict-free 16-byte stores)
-constexpr int KG = 36;                 // floats per 32-channel group of page scales (+4: no bank overlap)
+constexpr int KG = 36;                 // (A, B) pairs per 32-channel group of page constants (+4: no bank overlap)
 constexpr int SPG = 16;                // salient channels per page (the layout's key_padding width)
 constexpr float LN2 = 0.693147180559945309f;
 
@@ -210,12 +210,21 @@ __device__ __forceinline__ SeqGeom seq_geom(const PagedArgs &a, int s)
     return g;
 }
 
+// A wave-uniform 64-bit value (a page address read from LDS) moved to scalar
+// registers, so loads from it take the scalar-base form.
+__device__ __forceinline__ uint64_t uniform_ptr(uint64_t v)
+{
+    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
+    const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+    return (uint64_t)lo | ((uint64_t)hi << 32);
+}
+
 // Workgroup LDS of decode_paged, shared by its packed and dense bodies.
 template <int NPG>
 struct __attribute__((aligned(16))) PagedSmem {
     uint32_t v[WAVES][16 * VR];        // decoded V tiles, K staging, the final combine
     uint16_t q[16 * D];
-    float ka[NPG][4 * KG];             // s * 2^9, zero at salient/donor channels
+    f32x2 kc[NPG][4 * KG];             // (s * 2^9, -8 s), zero at salient/donor channels
     int16_t role[NPG][D];              // key_map of each page
     uint32_t salw[NPG][SPG];           // gather offsets per page
     f32x2 salf[NPG][SPG];              // (s_src, -128 s_src)
@@ -284,10 +293,12 @@ __device__ __forceinline__ void paged_body(const PagedArgs &a, PagedSmem<NPG> &s
     if constexpr (PACKED) {
 #pragma unroll
         for (int k = 0; k < CPT; ++k) {
+            // the page is the same for a whole wavefront: its base goes to
+            // scalar registers and each lane adds a 32-bit offset
             const int i = min(tid + 256 * k, NPG * D - 1), lp = i >> 7, c = i & (D - 1);
-            const uint8_t *page = (const uint8_t *)sm.page[lp];
-            ksc[k] = ldg<float>(page + a.off.ks + ((int64_t)h * D + c) * 4);
-            krl[k] = ldg<int16_t>(page + a.off.km + ((int64_t)h * D + c) * 2);
+            const uint8_t *page = (const uint8_t *)uniform_ptr(sm.page[__builtin_amdgcn_readfirstlane(lp)]);
+            ksc[k] = ldg_at<float>(page, (uint32_t)(a.off.ks + (h * D + c) * 4));
+            krl[k] = ldg_at<int16_t>(page, (uint32_t)(a.off.km + (h * D + c) * 2));
         }
         {
             const int i = min(tid, NPG * SPG - 1), lp = i / SPG, j = i % SPG;
@@ -295,23 +306,28 @@ __device__ __forceinline__ void paged_body(const PagedArgs &a, PagedSmem<NPG> &s
         }
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
+            // a 16-token tile lies in one page (B is a multiple of 16); rows
+            // past the end read a clamped row of that page and stay dead
+            const int lp = (base + 16 * j) / B;
+            const uint8_t *page = (const uint8_t *)uniform_ptr(sm.page[lp]);
             const int t = min(base + 16 * j + gl, ntok - 1);
-            const uint8_t *page = (const uint8_t *)sm.page[t / B];
-            kw[j] = ldnt<u32x4>(page + ((int64_t)h * B + t % B) * 64 + 16 * ql);
+            kw[j] = ldnt_at<u32x4>(page, (uint32_t)((h * B + t % B) * 64 + 16 * ql));
         }
 #pragma unroll
-        for (int m = 0; m < 2; ++m)
+        for (int m = 0; m < 2; ++m) {
+            // both tokens of a lane's pair (clamped ones too) lie in one page
+            const uint8_t *page = (const uint8_t *)sm.page[min(base + 32 * m + 2 * pl, ntok - 1) / B];
 #pragma unroll
             for (int u = 0; u < 2; ++u) {
                 const int t = min(base + 32 * m + 2 * pl + u, ntok - 1);
-                const uint8_t *page = (const uint8_t *)sm.page[t / B];
-                const int64_t r = (int64_t)h * B + t % B;
-                const u32x2 w = ldnt<u32x2>(page + a.off.vp + r * 32 + 8 * qq);
+                const uint32_t r = (uint32_t)(h * B + t % B);
+                const u32x2 w = ldnt_at<u32x2>(page, (uint32_t)a.off.vp + r * 32 + 8 * qq);
                 vw[m][u][0] = w[0];
                 vw[m][u][1] = w[1];
-                vp[m][u][0] = ldg<uint16_t>(page + a.off.vs + (r * 2 + (qq >> 1)) * 2);
-                vp[m][u][1] = ldg<uint16_t>(page + a.off.vo + (r * 2 + (qq >> 1)) * 2);
+                vp[m][u][0] = ldg_at<uint16_t>(page, (uint32_t)a.off.vs + (r * 2 + (qq >> 1)) * 2);
+                vp[m][u][1] = ldg_at<uint16_t>(page, (uint32_t)a.off.vo + (r * 2 + (qq >> 1)) * 2);
             }
+        }
         // keep every use of the constants below the payload issue
         asm volatile("" ::: "memory");
     }
@@ -324,7 +340,8 @@ __device__ __forceinline__ void paged_body(const PagedArgs &a, PagedSmem<NPG> &s
             const int i = tid + 256 * k;
             if (i < NPG * D) {
                 const int lp = i >> 7, c = i & (D - 1);
-                sm.ka[lp][(c >> 5) * KG + (c & 31)] = krl[k] == -1 ? ksc[k] * inv_unit : 0.0f;
+                sm.kc[lp][(c >> 5) * KG + (c & 31)] =
+                    krl[k] == -1 ? f32x2{ksc[k] * inv_unit, -8.0f * ksc[k]} : f32x2{0.0f, 0.0f};
                 sm.role[lp][c] = (int16_t)krl[k];
             }
         }
@@ -408,25 +425,20 @@ __device__ __forceinline__ void paged_body(const PagedArgs &a, PagedSmem<NPG> &s
                 f32x4 s = {bias, bias, bias, bias};
 #pragma unroll
                 for (int d = 0; d < 4; ++d) {
-                    const float *ka = &sm.ka[lp][ql * KG + 8 * d];
-                    const u32x4 a03 = *(const u32x4 *)ka, a47 = *(const u32x4 *)(ka + 4);
-                    float A[8], Bc[8];
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) {
-                        A[e] = __uint_as_float(a03[e]);
-                        A[4 + e] = __uint_as_float(a47[e]);
-                    }
-#pragma unroll
-                    for (int e = 0; e < 8; ++e) Bc[e] = A[e] * -0.015625f;   // -8 s, exact
+                    const f32x2 *kc = &sm.kc[lp][ql * KG + 8 * d];
+                    const u32x4 c01 = *(const u32x4 *)(kc + 0), c23 = *(const u32x4 *)(kc + 2);
+                    const u32x4 c45 = *(const u32x4 *)(kc + 4), c67 = *(const u32x4 *)(kc + 6);
                     const uint32_t x = kw[j][d];
                     const uint32_t lo = x & 0x0f0f0f0fu, hi = (x >> 4) & 0x0f0f0f0fu;
                     const f32x2 e01 = fp8x2<false>(lo), e23 = fp8x2<true>(lo);
                     const f32x2 o01 = fp8x2<false>(hi), o23 = fp8x2<true>(hi);
+#define KF(cv, i) __uint_as_float(cv[i])
                     u32x4 kv;
-                    kv[0] = pack2<false>(fmaf(e01.x, A[0], Bc[0]), fmaf(o01.x, A[1], Bc[1]));
-                    kv[1] = pack2<false>(fmaf(e01.y, A[2], Bc[2]), fmaf(o01.y, A[3], Bc[3]));
-                    kv[2] = pack2<false>(fmaf(e23.x, A[4], Bc[4]), fmaf(o23.x, A[5], Bc[5]));
-                    kv[3] = pack2<false>(fmaf(e23.y, A[6], Bc[6]), fmaf(o23.y, A[7], Bc[7]));
+                    kv[0] = pack2<false>(fmaf(e01.x, KF(c01, 0), KF(c01, 1)), fmaf(o01.x, KF(c01, 2), KF(c01, 3)));
+                    kv[1] = pack2<false>(fmaf(e01.y, KF(c23, 0), KF(c23, 1)), fmaf(o01.y, KF(c23, 2), KF(c23, 3)));
+                    kv[2] = pack2<false>(fmaf(e23.x, KF(c45, 0), KF(c45, 1)), fmaf(o23.x, KF(c45, 2), KF(c45, 3)));
+                    kv[3] = pack2<false>(fmaf(e23.y, KF(c67, 0), KF(c67, 1)), fmaf(o23.y, KF(c67, 2), KF(c67, 3)));
+#undef KF
                     s = mma32<false>(kv, qb[d], s);
                 }
                 sc[j] = s;
