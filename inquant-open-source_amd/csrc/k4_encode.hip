@@ -194,7 +194,8 @@ __global__ __launch_bounds__(K4_THREADS) void k4_encode_kernel(K4Args a)
 //   pass 1  waves 0-1: the fp64 Welford var_mean of channel tid (min_error
 //           only); delta / n uses a table of RN(1/n) and one remainder fma,
 //           which is the correctly rounded quotient for n <= 256;
-//           waves 2-3: sampled sums (torch cascade order), amax, finiteness;
+//           waves 2-3: sampled sums (torch cascade order), amax and
+//           finiteness as an integer max of the 16-bit magnitudes;
 //   then    donor selection by the whole workgroup (iq_select_tile128);
 //   pass 2  every thread quantizes 8 channels of a token per step, writing
 //           4 payload bytes.
@@ -290,8 +291,7 @@ __global__ __launch_bounds__(K4_THREADS) void k4_encode_tile(K4Args a)
     IqCascade sa, sm;                             // waves 2-3, channel tid - 128
     sa.init(ns);
     sm.init(ns);
-    float amax = 0.0f;
-    bool bad = false;
+    uint32_t amax_bits = 0;
     int next_sample = 0;
     const int c1 = tid & (TILE_D - 1);
     stream([&](int ch) {
@@ -339,10 +339,13 @@ __global__ __launch_bounds__(K4_THREADS) void k4_encode_tile(K4Args a)
                 }
             }
         } else {
-            for (int u = 0; u < nt; ++u) {
-                const float v = tile_f32<F16IN>(xs[u * XROW]);
-                bad |= !iq_isfinite(v);
-                amax = fmaxf(amax, fabsf(v));
+            // |x| as 16-bit integers: for finite values their order is the
+            // order of the magnitudes, and inf / NaN sort above every finite one
+            if (nt == CH) {
+#pragma unroll
+                for (int u = 0; u < CH; ++u) amax_bits = max(amax_bits, (uint32_t)xs[u * XROW] & 0x7fffu);
+            } else {
+                for (int u = 0; u < nt; ++u) amax_bits = max(amax_bits, (uint32_t)xs[u * XROW] & 0x7fffu);
             }
             // the samples r * stride that fall in this chunk, in order
             for (; next_sample < t0 + nt; next_sample += (int)a.stride) {
@@ -358,9 +361,9 @@ __global__ __launch_bounds__(K4_THREADS) void k4_encode_tile(K4Args a)
             s_smean[c1] = (float)mean;                // full mean, replaced below
         }
     } else {
-        s_amax[c1] = amax;
+        s_amax[c1] = tile_f32<F16IN>(amax_bits);
         s_sal[c1] = sa.finish() / (float)ns;
-        if (bad) s_bad = 1;
+        if (amax_bits >= (F16IN ? 0x7c00u : 0x7f80u)) s_bad = 1;     // an inf or NaN in the channel
         // stash the sampled mean until the Welford waves are done with s_smean
         s_scale[c1] = sm.finish() / (float)ns;
     }
