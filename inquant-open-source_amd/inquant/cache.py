@@ -205,9 +205,9 @@ class InQuantCache(_HFCache):
                     or position.numel() != key_states.shape[2] or position.dtype not in (torch.int32, torch.int64)):
                 raise ValueError("cache_position must be a 1D integer tensor with one position per new token")
             if self.config.validate_positions:
-                expected = torch.arange(old_length, old_length + key_states.shape[2], device=position.device,
-                                        dtype=position.dtype)
-                if not torch.equal(position, expected):
+                # compared on the host: one copy instead of two kernels and a reduction
+                expected = torch.arange(old_length, old_length + key_states.shape[2], dtype=position.dtype)
+                if not torch.equal(position.cpu(), expected):
                     raise ValueError("Only contiguous append positions are supported; reset before a new request")
         return layer
 
@@ -217,13 +217,20 @@ class InQuantCache(_HFCache):
         layer = self._validate_update(key_states, value_states, layer_idx, cache_kwargs)
         if key_states.shape[2] != 1 or layer is None:
             raise ValueError("append_for_attention requires one new token after an existing prefill")
-        tail_key, tail_value = key_states, value_states
-        if layer.residual_key is not None:
-            tail_key = torch.cat((layer.residual_key, tail_key), dim=2)
-            tail_value = torch.cat((layer.residual_value, tail_value), dim=2)
-        view = PackedAttentionView(tuple(layer.key_blocks), tuple(layer.value_blocks), layer.sink_key,
-                                   layer.sink_value, tail_key, tail_value, layer.seq_length + 1)
-        self._append(layer, key_states, value_states)
+        blocks = (tuple(layer.key_blocks), tuple(layer.value_blocks))
+        sink = (layer.sink_key, layer.sink_value)
+        length = layer.seq_length + 1
+        sink_full = (0 if sink[0] is None else sink[0].shape[2]) >= self.config.sink_tokens
+        if sink_full and layer.residual_key is not None:
+            # the pre-seal tail is exactly the concatenation the append builds
+            tail_key, tail_value = self._append(layer, key_states, value_states)
+        else:
+            tail_key, tail_value = key_states, value_states
+            if layer.residual_key is not None:
+                tail_key = torch.cat((layer.residual_key, tail_key), dim=2)
+                tail_value = torch.cat((layer.residual_value, tail_value), dim=2)
+            self._append(layer, key_states, value_states)
+        view = PackedAttentionView(blocks[0], blocks[1], sink[0], sink[1], tail_key, tail_value, length)
         self.record_peak(layer_idx)
         if layer_idx == 0:
             self._seen_tokens = layer.seq_length
@@ -241,7 +248,8 @@ class InQuantCache(_HFCache):
                 nv = torch.cat((sink_value, nv), dim=2)
             sink_key, sink_value = nk.clone(), nv.clone()
         pending_key, pending_value = keys[:, :, take:], values[:, :, take:]
-        if layer.residual_key is not None:
+        fresh = layer.residual_key is not None      # pending is a new tensor, not a view of the input
+        if fresh:
             pending_key = torch.cat((layer.residual_key, pending_key), dim=2)
             pending_value = torch.cat((layer.residual_value, pending_value), dim=2)
         blocks = max(0, (pending_key.shape[2] - cfg.residual_length) // cfg.block_size)
@@ -253,8 +261,12 @@ class InQuantCache(_HFCache):
             new_values = quantize_value_blocks(pending_value, blocks, cfg.block_size, cfg.value_bits,
                                                cfg.value_group_size)
         offset = blocks * cfg.block_size
-        residual_key = pending_key[:, :, offset:].clone()
-        residual_value = pending_value[:, :, offset:].clone()
+        if fresh and offset == 0:
+            # nothing sealed: the concatenation is already an owned tensor
+            residual_key, residual_value = pending_key, pending_value
+        else:
+            residual_key = pending_key[:, :, offset:].clone()
+            residual_value = pending_value[:, :, offset:].clone()
         layer.sink_key, layer.sink_value = sink_key, sink_value
         layer.residual_key, layer.residual_value = residual_key, residual_value
         layer.key_blocks.extend(new_keys)
@@ -262,6 +274,7 @@ class InQuantCache(_HFCache):
         if cfg.track_peak_bytes:
             layer.packed_nbytes += sum(block.nbytes for block in new_keys + new_values)
         layer.seq_length += keys.shape[2]
+        return pending_key, pending_value
 
     def record_peak(self, layer_idx) -> None:
         if not self.config.track_peak_bytes:
