@@ -33,7 +33,7 @@ constexpr int PART = 256;              // tokens per partition
 constexpr int VR = 136;                // dwords per staged token-pair row of decoded V
 constexpr int KROW = 17;               // dwords per staged K row (salient byte gathers)
 constexpr int OROW = 132;              // floats per staged output row in the combine (conflict-free 16-byte stores)
-constexpr int KG = 36;                 // (A, B) pairs per 32-channel group of page constants (+4: no bank overlap)
+constexpr int KG = 36;                 // floats per 32-channel group of page scales (+4: no bank overlap)
 constexpr int SPG = 16;                // salient channels per page (the layout's key_padding width)
 constexpr float LN2 = 0.693147180559945309f;
 
@@ -222,16 +222,24 @@ __device__ __forceinline__ uint64_t uniform_ptr(uint64_t v)
 // Workgroup LDS of decode_paged, shared by its packed and dense bodies.
 template <int NPG>
 struct __attribute__((aligned(16))) PagedSmem {
-    uint32_t v[WAVES][16 * VR];        // decoded V tiles, K staging, the final combine
+    // The V / K staging space of the waves is free until the per-page tables
+    // are built, so the role-resolution arrays live in it: at 16-token pages
+    // this keeps a workgroup under 53 KiB, three per compute unit.
+    struct Setup {
+        int16_t role[NPG][D];          // key_map of each page
+        float padraw[NPG][SPG];
+        int16_t src[NPG][SPG], don[NPG][SPG];
+        float ssc[NPG][SPG], pad[NPG][SPG];
+    };
+    union {
+        uint32_t v[WAVES][16 * VR];    // decoded V tiles, K staging, the final combine
+        Setup setup;
+    };
     uint16_t q[16 * D];
-    f32x2 kc[NPG][4 * KG];             // (s * 2^9, -8 s), zero at salient/donor channels
-    int16_t role[NPG][D];              // key_map of each page
+    float ka[NPG][4 * KG];             // s * 2^9, zero at salient/donor channels
     uint32_t salw[NPG][SPG];           // gather offsets per page
     f32x2 salf[NPG][SPG];              // (s_src, -128 s_src)
-    uint16_t qsal[NPG][16 * SPG];
     float bias[NPG][16];               // sum_k q[g][don_k] * round(pad_k)
-    int16_t src[NPG][SPG], don[NPG][SPG];
-    float ssc[NPG][SPG], pad[NPG][SPG], padraw[NPG][SPG];
     uint64_t page[NPG];
     int pok[NPG];
     float wm[WAVES][16], wl[WAVES][16];
@@ -340,18 +348,17 @@ __device__ __forceinline__ void paged_body(const PagedArgs &a, PagedSmem<NPG> &s
             const int i = tid + 256 * k;
             if (i < NPG * D) {
                 const int lp = i >> 7, c = i & (D - 1);
-                sm.kc[lp][(c >> 5) * KG + (c & 31)] =
-                    krl[k] == -1 ? f32x2{ksc[k] * inv_unit, -8.0f * ksc[k]} : f32x2{0.0f, 0.0f};
-                sm.role[lp][c] = (int16_t)krl[k];
+                sm.ka[lp][(c >> 5) * KG + (c & 31)] = krl[k] == -1 ? ksc[k] * inv_unit : 0.0f;
+                sm.setup.role[lp][c] = (int16_t)krl[k];
             }
         }
         if (tid < NPG * SPG) {
             const int lp = tid / SPG, j = tid % SPG;
-            sm.padraw[lp][j] = kpad;
-            sm.src[lp][j] = 0;
-            sm.don[lp][j] = 0;
-            sm.ssc[lp][j] = 0.0f;
-            sm.pad[lp][j] = 0.0f;
+            sm.setup.padraw[lp][j] = kpad;
+            sm.setup.src[lp][j] = 0;
+            sm.setup.don[lp][j] = 0;
+            sm.setup.ssc[lp][j] = 0.0f;
+            sm.setup.pad[lp][j] = 0.0f;
         }
         __syncthreads();
         // a source's descriptor index is -2 - key_map[its donor]; a donor's is -2 - key_map
@@ -361,15 +368,15 @@ __device__ __forceinline__ void paged_body(const PagedArgs &a, PagedSmem<NPG> &s
             if (i < NPG * D) {
                 const int lp = i >> 7, c = i & (D - 1), role = krl[k];
                 if (role >= 0 && role < D) {
-                    const int j = -2 - (int)sm.role[lp][role];
+                    const int j = -2 - (int)sm.setup.role[lp][role];
                     if (j >= 0 && j < SPG) {
-                        sm.src[lp][j] = (int16_t)c;
-                        sm.ssc[lp][j] = ksc[k];
+                        sm.setup.src[lp][j] = (int16_t)c;
+                        sm.setup.ssc[lp][j] = ksc[k];
                     }
                 } else if (role <= -2 && role >= -2 - (SPG - 1)) {
                     const int j = -2 - role;
-                    sm.don[lp][j] = (int16_t)c;
-                    sm.pad[lp][j] = round_q<false>(sm.padraw[lp][j]);
+                    sm.setup.don[lp][j] = (int16_t)c;
+                    sm.setup.pad[lp][j] = round_q<false>(sm.setup.padraw[lp][j]);
                 }
             }
         }
@@ -377,20 +384,16 @@ __device__ __forceinline__ void paged_body(const PagedArgs &a, PagedSmem<NPG> &s
         // per-page salient tables and donor bias
         for (int i = tid; i < NPG * SPG; i += 256) {
             const int lp = i / SPG, k = i % SPG;
-            const uint32_t src = (uint32_t)sm.src[lp][k], don = (uint32_t)sm.don[lp][k];
+            const uint32_t src = (uint32_t)sm.setup.src[lp][k], don = (uint32_t)sm.setup.don[lp][k];
             sm.salw[lp][k] = (src >> 1) | (((src & 1) * 4) << 8) | ((don >> 1) << 16) | (((don & 1) * 4) << 24);
-            const float ssc = sm.ssc[lp][k];
+            const float ssc = sm.setup.ssc[lp][k];
             sm.salf[lp][k] = f32x2{ssc, -128.0f * ssc};
         }
         for (int i = tid; i < NPG * 16; i += 256) {
             const int lp = i >> 4, g = i & 15;
             float b = 0.0f;
-            for (int k = 0; k < SPG; ++k) b = fmaf(to_f32<false>(s_q[g * D + sm.don[lp][k]]), sm.pad[lp][k], b);
+            for (int k = 0; k < SPG; ++k) b = fmaf(to_f32<false>(s_q[g * D + sm.setup.don[lp][k]]), sm.setup.pad[lp][k], b);
             sm.bias[lp][g] = b;
-        }
-        for (int i = tid; i < NPG * 16 * SPG; i += 256) {
-            const int lp = i / (16 * SPG), r = i % (16 * SPG), g = r / SPG, k = r % SPG;
-            sm.qsal[lp][g * SPG + k] = s_q[g * D + sm.src[lp][k]];
         }
     }
     __syncthreads();
@@ -425,20 +428,25 @@ __device__ __forceinline__ void paged_body(const PagedArgs &a, PagedSmem<NPG> &s
                 f32x4 s = {bias, bias, bias, bias};
 #pragma unroll
                 for (int d = 0; d < 4; ++d) {
-                    const f32x2 *kc = &sm.kc[lp][ql * KG + 8 * d];
-                    const u32x4 c01 = *(const u32x4 *)(kc + 0), c23 = *(const u32x4 *)(kc + 2);
-                    const u32x4 c45 = *(const u32x4 *)(kc + 4), c67 = *(const u32x4 *)(kc + 6);
+                    const float *ka = &sm.ka[lp][ql * KG + 8 * d];
+                    const u32x4 a03 = *(const u32x4 *)ka, a47 = *(const u32x4 *)(ka + 4);
+                    float A[8], Bc[8];
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        A[e] = __uint_as_float(a03[e]);
+                        A[4 + e] = __uint_as_float(a47[e]);
+                    }
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) Bc[e] = A[e] * -0.015625f;   // -8 s, exact
                     const uint32_t x = kw[j][d];
                     const uint32_t lo = x & 0x0f0f0f0fu, hi = (x >> 4) & 0x0f0f0f0fu;
                     const f32x2 e01 = fp8x2<false>(lo), e23 = fp8x2<true>(lo);
                     const f32x2 o01 = fp8x2<false>(hi), o23 = fp8x2<true>(hi);
-#define KF(cv, i) __uint_as_float(cv[i])
                     u32x4 kv;
-                    kv[0] = pack2<false>(fmaf(e01.x, KF(c01, 0), KF(c01, 1)), fmaf(o01.x, KF(c01, 2), KF(c01, 3)));
-                    kv[1] = pack2<false>(fmaf(e01.y, KF(c23, 0), KF(c23, 1)), fmaf(o01.y, KF(c23, 2), KF(c23, 3)));
-                    kv[2] = pack2<false>(fmaf(e23.x, KF(c45, 0), KF(c45, 1)), fmaf(o23.x, KF(c45, 2), KF(c45, 3)));
-                    kv[3] = pack2<false>(fmaf(e23.y, KF(c67, 0), KF(c67, 1)), fmaf(o23.y, KF(c67, 2), KF(c67, 3)));
-#undef KF
+                    kv[0] = pack2<false>(fmaf(e01.x, A[0], Bc[0]), fmaf(o01.x, A[1], Bc[1]));
+                    kv[1] = pack2<false>(fmaf(e01.y, A[2], Bc[2]), fmaf(o01.y, A[3], Bc[3]));
+                    kv[2] = pack2<false>(fmaf(e23.x, A[4], Bc[4]), fmaf(o23.x, A[5], Bc[5]));
+                    kv[3] = pack2<false>(fmaf(e23.y, A[6], Bc[6]), fmaf(o23.y, A[7], Bc[7]));
                     s = mma32<false>(kv, qb[d], s);
                 }
                 sc[j] = s;
@@ -453,17 +461,20 @@ __device__ __forceinline__ void paged_body(const PagedArgs &a, PagedSmem<NPG> &s
             for (int j = 0; j < 4; ++j) {
                 const int lp = (base + 16 * j) / B;
                 const uint8_t *rowp = kt + (16 * j + gl) * (4 * KROW);
-                const u32x2 qs = *(const u32x2 *)(&sm.qsal[lp][gl * SPG + 4 * ql]);
                 float v[4];
+                uint32_t qv[4];
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
                     const uint32_t w = sm.salw[lp][4 * ql + e];
+                    // Q[g][source channel]; the source is 2 (w & 255) + ((w >> 8) & 255) / 4
+                    qv[e] = s_q[gl * D + 2 * (w & 0xffu) + (((w >> 8) & 0xffu) >> 2)];
                     const f32x2 sf = sm.salf[lp][4 * ql + e];
                     const uint32_t hi = (rowp[w & 0xffu] >> ((w >> 8) & 0xffu)) & 15u;
                     const uint32_t lo = (rowp[(w >> 16) & 0xffu] >> (w >> 24)) & 15u;
                     v[e] = fmaf((float)((hi << 4) | lo), sf.x, sf.y);
                 }
                 const u32x2 ka = {pack2<false>(v[0], v[1]), pack2<false>(v[2], v[3])};
+                const u32x2 qs = {qv[0] | (qv[1] << 16), qv[2] | (qv[3] << 16)};
                 sc[j] = mma16<false>(ka, qs, sc[j]);
             }
         } else {
@@ -640,7 +651,7 @@ __device__ __forceinline__ void paged_body(const PagedArgs &a, PagedSmem<NPG> &s
 // One workgroup per (KV head, partition, sequence); NPG = pages per packed
 // partition (PART / B).
 template <int NPG>
-__global__ __launch_bounds__(256, 2) void decode_paged(PagedArgs a)
+__global__ __launch_bounds__(256, 3) void decode_paged(PagedArgs a)
 {
     __shared__ PagedSmem<NPG> sm;
     const int p = blockIdx.y, sq = blockIdx.z;
