@@ -214,8 +214,12 @@ __device__ __forceinline__ float tile_f32(uint32_t bits16)
     else return __uint_as_float(bits16 << 16);
 }
 
-template <bool F16IN>
-__global__ __launch_bounds__(K4_THREADS) void k4_encode_tile(K4Args a)
+// NCH > 0: the block length is NCH chunks (a sealed cache block), known at
+// compile time, so the chunk loops unroll without branches and each load is
+// waited for exactly when its chunk is stored (a branch around loads makes
+// the compiler wait for all of them).  NCH = 0: any T <= 256.
+template <bool F16IN, int NCH>
+__global__ __launch_bounds__(K4_THREADS, 4) void k4_encode_tile(K4Args a)
 {
     __shared__ __attribute__((aligned(16))) uint16_t s_x[2][CH * XROW];
     __shared__ double s_rcp[TILE_T];    // RN(1 / n), n = 1 .. T
@@ -231,11 +235,13 @@ __global__ __launch_bounds__(K4_THREADS) void k4_encode_tile(K4Args a)
     __shared__ int s_bad;
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int64_t row = blockIdx.x;
-    const int64_t b = row / a.H, h = row % a.H;
+    // grid (blocks, heads): no 64-bit division for the row's coordinates
+    const int64_t b = blockIdx.x, h = blockIdx.y;
+    const int64_t row = b * a.H + h;
     const uint16_t *xr = (const uint16_t *)a.x + b * a.sb + h * a.sh;
-    const int T = (int)a.T;
-    const int ns = (int)((T + a.stride - 1) / a.stride);
+    const int T = NCH > 0 ? NCH * CH : (int)a.T;
+    const int stride = (int)min(a.stride, (int64_t)TILE_T);   // a larger stride samples token 0 only
+    const int ns = (T + stride - 1) / stride;
     const int nch = (T + CH - 1) / CH;
 
     // chunk staging: thread tid moves segments tid and tid + 256 (row i / 16,
@@ -266,6 +272,7 @@ __global__ __launch_bounds__(K4_THREADS) void k4_encode_tile(K4Args a)
             if (r < nch) load_chunk(r, seg[r]);
     };
     auto stream = [&](auto &&body) {
+#pragma unroll
         for (int c0 = 0; c0 < nch; c0 += 3) {
 #pragma unroll
             for (int r = 0; r < 3; ++r) {
@@ -286,9 +293,13 @@ __global__ __launch_bounds__(K4_THREADS) void k4_encode_tile(K4Args a)
     store_chunk(seg[0], 0);
     __syncthreads();
 
-    // ---- pass 1: statistics
-    double mean = 0.0, m2 = 0.0;                  // waves 0-1, channel tid
-    IqCascade sa, sm;                             // waves 2-3, channel tid - 128
+    // ---- pass 1: statistics.  Two waves run the Welford chains (channel
+    // tid & 127) and two the sums; which pair does which alternates between
+    // neighbouring blocks, so that the blocks sharing a compute unit spread
+    // the fp64 chains over all four SIMDs instead of stacking them on two.
+    const bool welford = ((tid >> 7) ^ (int)(((blockIdx.x + gridDim.x * blockIdx.y) >> 8) & 1)) == 0;
+    double mean = 0.0, m2 = 0.0;                  // Welford waves
+    IqCascade sa, sm;                             // sums waves
     sa.init(ns);
     sm.init(ns);
     uint32_t amax_bits = 0;
@@ -297,7 +308,7 @@ __global__ __launch_bounds__(K4_THREADS) void k4_encode_tile(K4Args a)
     stream([&](int ch) {
         const uint16_t *xs = s_x[ch & 1] + c1;
         const int t0 = ch * CH, nt = min(CH, T - t0);
-        if (tid < TILE_D) {
+        if (welford) {
             if (a.min_error) {
                 auto step = [&](float xf, double y, int t) {
                     const double dv = (double)xf;
@@ -348,14 +359,14 @@ __global__ __launch_bounds__(K4_THREADS) void k4_encode_tile(K4Args a)
                 for (int u = 0; u < nt; ++u) amax_bits = max(amax_bits, (uint32_t)xs[u * XROW] & 0x7fffu);
             }
             // the samples r * stride that fall in this chunk, in order
-            for (; next_sample < t0 + nt; next_sample += (int)a.stride) {
+            for (; next_sample < t0 + nt; next_sample += stride) {
                 const float v = tile_f32<F16IN>(xs[(next_sample - t0) * XROW]);
                 sa.add(fabsf(v));
                 sm.add(v);
             }
         }
     });
-    if (tid < TILE_D) {
+    if (welford) {
         if (a.min_error) {
             s_err[c1] = (float)(m2 / (double)T);      // var; the mean term is added below
             s_smean[c1] = (float)mean;                // full mean, replaced below
@@ -507,16 +518,19 @@ extern "C" int iq_k4_quantize(const void *x, int x_dtype, const int64_t *x_strid
     IQ_CHECK_ARG(B * H <= 0x7fffffffLL, "iq_k4_quantize: too many rows");
     K4Args a{x, x_dtype, x_strides[0], x_strides[1], x_strides[2], x_strides[3], H, T, D, count, sample_stride,
              min_error ? 1 : 0, payload, scales, src, don, desc_bytes, padding, bad_flag};
-    const bool tile = (x_dtype == IQ_BF16 || x_dtype == IQ_F16) && D == TILE_D && T <= TILE_T &&
+    const bool tile = (x_dtype == IQ_BF16 || x_dtype == IQ_F16) && D == TILE_D && T <= TILE_T && H <= 65535 &&
                       x_strides[3] == 1 && x_strides[2] % 8 == 0 && x_strides[1] % 8 == 0 &&
                       x_strides[0] % 8 == 0 && ((uintptr_t)x & 15) == 0;
     if (tile) {
-        if (x_dtype == IQ_F16)
-            hipLaunchKernelGGL(k4_encode_tile<true>, dim3((unsigned)(B * H)), dim3(K4_THREADS), 0,
-                               (hipStream_t)stream, a);
-        else
-            hipLaunchKernelGGL(k4_encode_tile<false>, dim3((unsigned)(B * H)), dim3(K4_THREADS), 0,
-                               (hipStream_t)stream, a);
+        const dim3 grid((unsigned)B, (unsigned)H), block(K4_THREADS);
+        const hipStream_t st = (hipStream_t)stream;
+        if (x_dtype == IQ_F16) {
+            if (T == TILE_T) hipLaunchKernelGGL((k4_encode_tile<true, TILE_T / CH>), grid, block, 0, st, a);
+            else hipLaunchKernelGGL((k4_encode_tile<true, 0>), grid, block, 0, st, a);
+        } else {
+            if (T == TILE_T) hipLaunchKernelGGL((k4_encode_tile<false, TILE_T / CH>), grid, block, 0, st, a);
+            else hipLaunchKernelGGL((k4_encode_tile<false, 0>), grid, block, 0, st, a);
+        }
         IQ_CHECK_LAUNCH("k4_encode_tile");
         return IQ_OK;
     }
