@@ -205,6 +205,10 @@ __global__ __launch_bounds__(K4_THREADS) void k4_encode_kernel(K4Args a)
 constexpr int TILE_D = 128;
 constexpr int TILE_T = 256;
 constexpr int CH = 32;                   // tokens per staged chunk
+#ifndef IQ_K4_KPF
+#define IQ_K4_KPF 1
+#endif
+constexpr int KPF = IQ_K4_KPF;           // chunks in flight
 constexpr int XROW = TILE_D + 8;         // u16 per staged row: 68 dwords (16-byte aligned rows, distinct banks)
 
 template <bool F16IN>
@@ -248,7 +252,7 @@ __global__ __launch_bounds__(K4_THREADS, 4) void k4_encode_tile(K4Args a)
     // 8 channels at 8 (i % 16)); rows past T are clamped copies, never read.
     // Three chunks stay in flight in registers (about 24 KiB per block), which
     // is what covers the load latency while every block streams at once.
-    u32x4_t seg[3][2];
+    u32x4_t seg[KPF][2];
     auto load_chunk = [&](int ch, u32x4_t (&sg)[2]) {
 #pragma unroll
         for (int k = 0; k < 2; ++k) {
@@ -268,19 +272,19 @@ __global__ __launch_bounds__(K4_THREADS, 4) void k4_encode_tile(K4Args a)
     // order, with chunk ch in buffer ch & 1 during body(ch)
     auto start_stream = [&]() {
 #pragma unroll
-        for (int r = 0; r < 3; ++r)
+        for (int r = 0; r < KPF; ++r)
             if (r < nch) load_chunk(r, seg[r]);
     };
     auto stream = [&](auto &&body) {
 #pragma unroll
-        for (int c0 = 0; c0 < nch; c0 += 3) {
+        for (int c0 = 0; c0 < nch; c0 += KPF) {
 #pragma unroll
-            for (int r = 0; r < 3; ++r) {
+            for (int r = 0; r < KPF; ++r) {
                 const int ch = c0 + r;
                 if (ch < nch) {
-                    if (ch + 3 < nch) load_chunk(ch + 3, seg[r]);   // seg[r] already sits in LDS
+                    if (ch + KPF < nch) load_chunk(ch + KPF, seg[r]);   // seg[r] already sits in LDS
                     body(ch);
-                    if (ch + 1 < nch) store_chunk(seg[(r + 1) % 3], (ch + 1) & 1);
+                    if (ch + 1 < nch) store_chunk(seg[(r + 1) % KPF], (ch + 1) & 1);
                     __syncthreads();
                 }
             }
