@@ -122,6 +122,160 @@ __global__ __launch_bounds__(V_THREADS) void v_encode_kernel(VEncArgs a)
     if (__ballot(live && bad) != 0 && (threadIdx.x & 63) == 0) atomicOr(a.bad, 1);
 }
 
+// Rows of 16-bit values with unit channel stride and 16-byte aligned rows,
+// D = 16 * PR channels.  Grid (token blocks, B*H); each thread encodes 16
+// consecutive channels of NT tokens, GL = group / 16 adjacent lanes forming
+// one group.  Same arithmetic as v_encode_kernel with fewer instructions:
+//  * min / max use the NaN-propagating v_minimum3 / v_maximum3, so a NaN or
+//    infinity anywhere in a group makes its offset or scale non-finite and
+//    that single check replaces the per-value finiteness test;
+//  * the quotient is clamped to [0, levels] before rounding (rint and an
+//    integer clamp commute), so every value that can decide a code lies in
+//    [0, levels] and the near-half test uses the fixed band 2^-16 >=
+//    levels * 2^-20 instead of one relative to |quotient|;
+//  * the codes of 8 values are packed with exact fp32 multiply-adds
+//    (sum of c_e * 2^(BITS*e) <= 2^16 - 1 for BITS=2; 4 values for BITS=4).
+struct VRowArgs {
+    const uint16_t *x;
+    int64_t sb, sh, st;      // element strides of batch, head, token
+    int H, T;
+    uint8_t *payload;
+    uint16_t *scales, *offsets;
+    int *bad;
+};
+
+template <bool F16IN, int BITS, int GL, int PR, int NT>
+__global__ __launch_bounds__(V_THREADS) void v_encode_rows(VRowArgs a)
+{
+    constexpr int TPB = V_THREADS / PR;                   // tokens per pass of the block
+    constexpr int L = (1 << BITS) - 1;
+    constexpr int D = 16 * PR, GROUPS = PR / GL;          // groups per token
+    constexpr int PB = D * BITS / 8;                      // payload bytes per token
+    const int tid = threadIdx.x;
+    const int j = tid % PR, tl = tid / PR;
+    const int bh = blockIdx.y, b = bh / a.H, h = bh - b * a.H;
+    const int t0 = blockIdx.x * (TPB * NT);
+    const uint16_t *xb = a.x + b * a.sb + h * a.sh + (int64_t)t0 * a.st + 16 * j;
+    const int64_t r0 = (int64_t)bh * a.T + t0;            // first row of the block
+
+    u32x4_t raw[NT][2];
+#pragma unroll
+    for (int k = 0; k < NT; ++k) {
+        const int tk = min(tl + k * TPB, a.T - 1 - t0);   // clamp the tail to the last token
+        const u32x4_t *p = (const u32x4_t *)(xb + (uint32_t)tk * (uint32_t)a.st);
+        raw[k][0] = __builtin_nontemporal_load(p);
+        raw[k][1] = __builtin_nontemporal_load(p + 1);
+    }
+    bool bad = false;
+#pragma unroll
+    for (int k = 0; k < NT; ++k) {
+        const int tk = tl + k * TPB;
+        const bool live = t0 + tk < a.T;
+        float v[16];
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+            const uint32_t w = raw[k][e >> 3][(e >> 1) & 3];
+            const uint16_t hbits = (uint16_t)(e & 1 ? w >> 16 : w);
+            v[e] = F16IN ? iq_f16_to_f32(hbits) : __uint_as_float(e & 1 ? w & 0xffff0000u : w << 16);
+        }
+        float lo = v[0], hi = v[0];
+#pragma unroll
+        for (int e = 1; e < 15; e += 2) {
+            lo = __builtin_elementwise_minimum(__builtin_elementwise_minimum(lo, v[e]), v[e + 1]);
+            hi = __builtin_elementwise_maximum(__builtin_elementwise_maximum(hi, v[e]), v[e + 1]);
+        }
+        lo = __builtin_elementwise_minimum(lo, v[15]);
+        hi = __builtin_elementwise_maximum(hi, v[15]);
+#pragma unroll
+        for (int o = 1; o < GL; o <<= 1) {
+            lo = __builtin_elementwise_minimum(lo, __shfl_xor(lo, o, 64));
+            hi = __builtin_elementwise_maximum(hi, __shfl_xor(hi, o, 64));
+        }
+        const uint16_t off_h = iq_f32_to_f16(lo);
+        float s = __fsub_rn(hi, lo) / (float)L;
+        s = s < 6.103515625e-05f ? 6.103515625e-05f : s;
+        const uint16_t sc_h = iq_f32_to_f16(s);
+        const float off = iq_f16_to_f32(off_h), sc = iq_f16_to_f32(sc_h);
+        bad |= live && !(iq_isfinite(off) && iq_isfinite(sc));
+
+        const float rsc = __builtin_amdgcn_rcpf(sc);
+        float q[16], dev = 0.0f;
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+            const float c = __builtin_amdgcn_fmed3f(__fmul_rn(__fsub_rn(v[e], off), rsc), 0.0f, (float)L);
+            q[e] = __builtin_rintf(c);
+            dev = fmaxf(dev, fabsf(__fsub_rn(q[e], c)));
+        }
+        if (dev >= 0.5f - 0x1p-16f) {     // a quotient near a half-integer: the IEEE division decides
+#pragma unroll
+            for (int e = 0; e < 16; ++e)
+                q[e] = fminf(fmaxf(rintf(__fsub_rn(v[e], off) / sc), 0.0f), (float)L);
+        }
+        const int row = tk;   // row offset within the block
+        if (live) {
+            if (BITS == 2) {
+                float p0 = q[0], p1 = q[8];
+#pragma unroll
+                for (int e = 1; e < 8; ++e) {
+                    p0 = __builtin_fmaf(q[e], (float)(1 << (2 * e)), p0);
+                    p1 = __builtin_fmaf(q[8 + e], (float)(1 << (2 * e)), p1);
+                }
+                const uint32_t word = (uint32_t)p0 | ((uint32_t)p1 << 16);
+                *(uint32_t *)(a.payload + r0 * PB + (uint32_t)(row * PB + 4 * j)) = word;
+            } else {
+                uint32_t w[4];
+#pragma unroll
+                for (int g = 0; g < 4; ++g) {
+                    float p = q[4 * g];
+#pragma unroll
+                    for (int e = 1; e < 4; ++e) p = __builtin_fmaf(q[4 * g + e], (float)(1 << (4 * e)), p);
+                    w[g] = (uint32_t)p;
+                }
+                typedef __attribute__((ext_vector_type(2))) uint32_t u32x2_t;
+                u32x2_t o;
+                o[0] = w[0] | (w[1] << 16);
+                o[1] = w[2] | (w[3] << 16);
+                *(u32x2_t *)(a.payload + r0 * PB + (uint32_t)(row * PB + 8 * j)) = o;
+            }
+            const int64_t gi = r0 * GROUPS + (uint32_t)(row * GROUPS + j / GL);
+            if (j % GL == 0) a.offsets[gi] = off_h;
+            if (j % GL == GL - 1) a.scales[gi] = sc_h;
+        }
+    }
+    if (__ballot(bad) != 0 && (tid & 63) == 0) atomicOr(a.bad, 1);
+}
+
+template <bool F16IN, int BITS, int GL>
+bool v_rows_dispatch_pr(int PR, dim3 grid, hipStream_t st, const VRowArgs &a)
+{
+    switch (PR) {
+#define IQ_V_CASE(P)                                                                              \
+    case P:                                                                                       \
+        if constexpr (GL <= P) {                                                                  \
+            hipLaunchKernelGGL((v_encode_rows<F16IN, BITS, GL, P, 2>), grid, dim3(V_THREADS), 0, st, a); \
+            return true;                                                                          \
+        }                                                                                         \
+        return false;
+    IQ_V_CASE(2)
+    IQ_V_CASE(4)
+    IQ_V_CASE(8)
+    IQ_V_CASE(16)
+#undef IQ_V_CASE
+    default: return false;
+    }
+}
+
+template <bool F16IN, int BITS>
+bool v_rows_dispatch_gl(int GL, int PR, dim3 grid, hipStream_t st, const VRowArgs &a)
+{
+    switch (GL) {
+    case 2: return v_rows_dispatch_pr<F16IN, BITS, 2>(PR, grid, st, a);
+    case 4: return v_rows_dispatch_pr<F16IN, BITS, 4>(PR, grid, st, a);
+    case 8: return v_rows_dispatch_pr<F16IN, BITS, 8>(PR, grid, st, a);
+    default: return false;
+    }
+}
+
 struct VDecArgs {
     const uint8_t *payload;
     const uint16_t *scales, *offsets;
@@ -211,6 +365,25 @@ extern "C" int iq_v_quantize(const void *x, int x_dtype, const int64_t *x_stride
     const int64_t vmul = 16 / elt;         // elements per 16 bytes
     const int vec = x_dtype != IQ_F64 && x_strides[3] == 1 && x_strides[0] % vmul == 0 &&
                     x_strides[1] % vmul == 0 && x_strides[2] % vmul == 0 && ((uintptr_t)x & 15) == 0;
+    const int64_t PR = D / 16;
+    if (vec && (x_dtype == IQ_BF16 || x_dtype == IQ_F16) && D % 16 == 0 && (PR == 2 || PR == 4 || PR == 8 || PR == 16) &&
+        B * H <= 65535 && T <= 0x7fffffffLL - 512 && x_strides[2] >= 0 && x_strides[2] <= (1 << 23)) {
+        const int64_t span = (V_THREADS / PR) * 2;          // tokens per block
+        const dim3 grid((unsigned)((T + span - 1) / span), (unsigned)(B * H));
+        const VRowArgs ra{(const uint16_t *)x, x_strides[0], x_strides[1], x_strides[2], (int)H, (int)T,
+                          payload, scales, offsets, bad_flag};
+        const int GL = group / 16;
+        const hipStream_t st = (hipStream_t)stream;
+        const bool ok = x_dtype == IQ_F16
+                            ? (bits == 2 ? v_rows_dispatch_gl<true, 2>(GL, (int)PR, grid, st, ra)
+                                         : v_rows_dispatch_gl<true, 4>(GL, (int)PR, grid, st, ra))
+                            : (bits == 2 ? v_rows_dispatch_gl<false, 2>(GL, (int)PR, grid, st, ra)
+                                         : v_rows_dispatch_gl<false, 4>(GL, (int)PR, grid, st, ra));
+        if (ok) {
+            IQ_CHECK_LAUNCH("v_encode_rows");
+            return IQ_OK;
+        }
+    }
     VEncArgs a{x, x_dtype, x_strides[0], x_strides[1], x_strides[2], x_strides[3], H, T, D, bits, group, units,
                vec, payload, scales, offsets, bad_flag};
     hipLaunchKernelGGL(v_encode_kernel, dim3((unsigned)((units + V_THREADS - 1) / V_THREADS)), dim3(V_THREADS), 0,

@@ -129,20 +129,62 @@ def test_reuse_map_with_ties_and_adjacent_outliers(count, policy):
             np.testing.assert_array_equal(_np(a), b)
 
 
-@pytest.mark.parametrize("bits,group", [(2, 32), (2, 64), (2, 128), (4, 64), (4, 32)])
-@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def _check_values(got, ref):
+    np.testing.assert_array_equal(_np(got.payload), ref["payload"])
+    np.testing.assert_array_equal(_np(got.scales).view(np.uint16), ref["scales"].view(np.uint16))
+    np.testing.assert_array_equal(_np(got.offsets).view(np.uint16), ref["offsets"].view(np.uint16))
+
+
+@pytest.mark.parametrize("bits,group", [(2, 32), (2, 64), (2, 128), (4, 64), (4, 32), (4, 128)])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
 def test_value_codec_matches_oracle(bits, group, dtype):
     from inquant.value_codec import quantize_values
     x = synth.kv_like(11 + bits, 4, 300, groups=(2, 2, 1))
     xt = _dev(x).to(dtype)
     ref = oracle.v_quantize(_np(xt.float()), bits, group)
     got = quantize_values(xt, bits, group)
-    np.testing.assert_array_equal(_np(got.payload), ref["payload"])
-    np.testing.assert_array_equal(_np(got.scales).view(np.uint16), ref["scales"].view(np.uint16))
-    np.testing.assert_array_equal(_np(got.offsets).view(np.uint16), ref["offsets"].view(np.uint16))
+    _check_values(got, ref)
     for out in ("float32", "bfloat16", "float16"):
         dec = got.dequantize(TORCH_DTYPES[out])
         _same_bits(_np(dec.float()), oracle.v_dequantize(ref, bits, group, out), out)
+
+
+@pytest.mark.parametrize("D,group", [(32, 32), (64, 32), (64, 64), (96, 32), (256, 64), (256, 128), (512, 128)])
+@pytest.mark.parametrize("bits", [2, 4])
+def test_value_codec_head_dims(D, group, bits):
+    # D = 32..256 take the row kernel (16 channels per lane), 96 and 512 the
+    # per-8-channel kernel; T = 1, 255 and 1000 end inside a token block
+    from inquant.value_codec import quantize_values
+    for T in (1, 255, 1000):
+        x = synth.kv_like(40 + D + T, 3, T, D=D, groups=(1,))
+        for dtype in (torch.bfloat16, torch.float16):
+            xt = _dev(x).to(dtype)
+            _check_values(quantize_values(xt, bits, group), oracle.v_quantize(_np(xt.float()), bits, group))
+
+
+def test_value_codec_strided_blocks_and_many_rows():
+    # the [blocks, H, B, D] view of a cache tensor (quantize_value_blocks) and
+    # a batch*heads count above the row kernel's 65535 grid rows
+    from inquant.value_codec import quantize_value_blocks, quantize_values
+    x = _dev(synth.kv_like(77, 4, 1024), torch.bfloat16)
+    blocks = quantize_value_blocks(x, 3, 256, 2, 64)
+    for i, packed in enumerate(blocks):
+        _check_values(packed, oracle.v_quantize(_np(x[:, :, 256 * i:256 * (i + 1)].float()), 2, 64))
+    many = _dev(synth.normal(78, (256, 257, 1, 32)), torch.bfloat16)
+    _check_values(quantize_values(many, 2, 32), oracle.v_quantize(_np(many.float()), 2, 32))
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+def test_value_codec_rejects_one_nonfinite_value(dtype):
+    from inquant.value_codec import quantize_values
+    x = _dev(synth.kv_like(79, 2, 300), dtype)
+    quantize_values(x, 2, 64)
+    for value, where in ((float("nan"), (0, 1, 299, 127)), (float("inf"), (0, 0, 0, 5)),
+                         (float("-inf"), (0, 1, 130, 64)), (float("nan"), (0, 0, 17, 0))):
+        bad = x.clone()
+        bad[where] = value
+        with pytest.raises(ValueError, match="finite"):
+            quantize_values(bad, 2, 64)
 
 
 def test_value_codec_known_answers_and_rejections():
