@@ -35,6 +35,7 @@ constexpr int OROW = 132;              // floats per staged output row in the co
 constexpr int KROW = 17;               // dwords per staged K row (16 + 1: conflict-free byte gathers)
 constexpr int KC_STRIDE = 68;          // float2 slots per 32-channel group of K constants (+4: no bank overlap)
 constexpr int DENSE_SPLIT = 256;
+constexpr int QROW = D + 8;            // u16 per staged query row (+8: the 16 rows of a B-operand read hit distinct banks)
 constexpr float LN2 = 0.693147180559945309f;
 
 struct FastArgs {
@@ -61,14 +62,14 @@ struct __attribute__((aligned(16))) FastSmem {
     // per wavefront: staged decoded V as [token pair][channel] dwords (two
     // tokens of one channel per dword); also K staging and the final combine
     uint32_t v[WAVES][16 * VR];
-    uint16_t q[16 * D];          // query rows (dtype bits), zero beyond G
-    uint16_t qm[16 * D];         // query rows masked at salient/donor channels
+    uint16_t q[16 * QROW];          // query rows (dtype bits), zero beyond G
+    uint16_t qm[16 * QROW];         // query rows masked at salient/donor channels
     f32x2 kc[4 * KC_STRIDE];     // per channel (s * 2^9, -8 s)
     int8_t role[D];
     uint32_t sal[64];            // src | don << 8
     uint32_t salw[64];           // gather offsets: src byte, shift, don byte, shift
     f32x2 salf[64];              // (s_src, -128 s_src)
-    uint16_t qsal[16 * 64];      // Q[g][src_k], zero beyond S
+    uint16_t qsal[16 * 68];      // Q[g][src_k], zero beyond S (68: fewer bank collisions than 64)
     float dpad[64];              // padding of donor k, rounded to the query dtype
     float wm[WAVES][16], wl[WAVES][16];
 };
@@ -161,15 +162,11 @@ __device__ __forceinline__ void fast_body(const FastArgs &a, FastSmem &sm)
     if (packed) {
         // the whole pointer-table row in one round trip (64 bytes, the same
         // for every lane), its pointers moved to scalar registers
-        const u32x4 *rv = (const u32x4 *)(a.tables + p * IQ_TABLE_COLS);
-        u32x4 tr[4];
+        const int64_t *rv = a.tables + p * IQ_TABLE_COLS;
+        int64_t tr[8];
 #pragma unroll
-        for (int k = 0; k < 4; ++k) tr[k] = ldg<u32x4>(rv + k);
-        auto row = [&](int k) -> uintptr_t {
-            const uint32_t lo = __builtin_amdgcn_readfirstlane(tr[k >> 1][2 * (k & 1)]);
-            const uint32_t hi = __builtin_amdgcn_readfirstlane(tr[k >> 1][2 * (k & 1) + 1]);
-            return (uintptr_t)lo | ((uintptr_t)hi << 32);
-        };
+        for (int k = 0; k < 8; ++k) tr[k] = rv[k];
+        auto row = [&](int k) -> uintptr_t { return (uintptr_t)tr[k]; };
         krole = (uint8_t)ldg<int8_t>(a.kmap + (p * a.H + h) * D + (tid & (D - 1)));
         kscale = ldg<float>((const float *)row(1) + h * D + (tid & (D - 1)));
         {   // no branch around these loads: with S == 0 they read valid
@@ -207,7 +204,7 @@ __device__ __forceinline__ void fast_body(const FastArgs &a, FastSmem &sm)
         return t < nsink ? a.sv + h * a.sv_sh + (int64_t)t * a.sv_st : a.tv + h * a.tv_sh + (int64_t)(t - nsink) * a.tv_st;
     };
     // consume the small loads (the payload stays in flight)
-    *(u32x4 *)(s_q + qg * D + qc) = qg < G ? qraw : u32x4{0u, 0u, 0u, 0u};
+    *(u32x4 *)(s_q + qg * QROW + qc) = qg < G ? qraw : u32x4{0u, 0u, 0u, 0u};
     if (packed) {
         if (tid < D) {
             s_kc[(tid >> 5) * KC_STRIDE + (tid & 31)] = f32x2{kscale * inv_unit, -8.0f * kscale};
@@ -233,7 +230,7 @@ __device__ __forceinline__ void fast_body(const FastArgs &a, FastSmem &sm)
                 v[w] &= keep;
             }
         }
-        *(u32x4 *)(s_qm + qg * D + qc) = v;
+        *(u32x4 *)(s_qm + qg * QROW + qc) = v;
     }
     if (tid < S) {
         const uint32_t sd = s_sal[tid];
@@ -245,7 +242,7 @@ __device__ __forceinline__ void fast_body(const FastArgs &a, FastSmem &sm)
     if constexpr (PACKED) {
         for (int i = tid; i < 16 * 16 * sal_groups; i += 256) {
             const int g = i / (16 * sal_groups), k = i % (16 * sal_groups);
-            s_qsal[g * 64 + k] = k < S ? s_q[g * D + (s_sal[k] & 0xffu)] : (uint16_t)0;
+            s_qsal[g * 68 + k] = k < S ? s_q[g * QROW + (s_sal[k] & 0xffu)] : (uint16_t)0;
         }
     }
     __syncthreads();
@@ -253,13 +250,13 @@ __device__ __forceinline__ void fast_body(const FastArgs &a, FastSmem &sm)
     // ---------------- per-lane constants
     u32x4 qb[4];                                   // B operand: Q[g = gl][32 ql + 8 d + e], masked
 #pragma unroll
-    for (int d = 0; d < 4; ++d) qb[d] = *(const u32x4 *)(s_qm + gl * D + 32 * ql + 8 * d);
+    for (int d = 0; d < 4; ++d) qb[d] = *(const u32x4 *)(s_qm + gl * QROW + 32 * ql + 8 * d);
     float bias = 0.0f;                             // sum_k q[gl][don_k] * round(pad_k)
     for (int grp = 0; grp < sal_groups; ++grp)
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
             const int k = 16 * grp + 4 * ql + e;
-            if (k < S) bias = fmaf(to_f32<F16>(s_q[gl * D + (s_sal[k] >> 8)]), s_dpad[k], bias);
+            if (k < S) bias = fmaf(to_f32<F16>(s_q[gl * QROW + (s_sal[k] >> 8)]), s_dpad[k], bias);
         }
     bias = xsum16(bias);
 
@@ -318,7 +315,7 @@ __device__ __forceinline__ void fast_body(const FastArgs &a, FastSmem &sm)
                         sw[e] = k < S ? s_salw[k] : 0u;
                         sf[e] = k < S ? s_salf[k] : f32x2{0.0f, 0.0f};
                     }
-                    const u32x2 qs = *(const u32x2 *)(s_qsal + gl * 64 + 16 * grp + 4 * ql);
+                    const u32x2 qs = *(const u32x2 *)(s_qsal + gl * 68 + 16 * grp + 4 * ql);
 #pragma unroll
                     for (int j = 0; j < 4; ++j) {
                         const uint8_t *rowp = kt + (16 * j + gl) * (4 * KROW);

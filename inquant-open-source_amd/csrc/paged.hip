@@ -34,6 +34,7 @@ constexpr int VR = 136;                // dwords per staged token-pair row of de
 constexpr int KROW = 17;               // dwords per staged K row (salient byte gathers)
 constexpr int OROW = 132;              // floats per staged output row in the combine (conflict-free 16-byte stores)
 constexpr int KG = 36;                 // floats per 32-channel group of page scales (+4: no bank overlap)
+constexpr int QROW = D + 8;            // u16 per staged query row (+8: rows of one column spread over the banks)
 constexpr int SPG = 16;                // salient channels per page (the layout's key_padding width)
 constexpr float LN2 = 0.693147180559945309f;
 
@@ -235,7 +236,7 @@ struct __attribute__((aligned(16))) PagedSmem {
         uint32_t v[WAVES][16 * VR];    // decoded V tiles, K staging, the final combine
         Setup setup;
     };
-    uint16_t q[16 * D];
+    uint16_t q[16 * QROW];
     float ka[NPG][4 * KG];             // s * 2^9, zero at salient/donor channels
     uint32_t salw[NPG][SPG];           // gather offsets per page
     f32x2 salf[NPG][SPG];              // (s_src, -128 s_src)
@@ -341,7 +342,7 @@ __device__ __forceinline__ void paged_body(const PagedArgs &a, PagedSmem<NPG> &s
     }
 
     // ---------------- query rows; per-page constants and roles
-    *(u32x4 *)(s_q + qg * D + qc) = qg < G ? qraw : u32x4{0u, 0u, 0u, 0u};
+    *(u32x4 *)(s_q + qg * QROW + qc) = qg < G ? qraw : u32x4{0u, 0u, 0u, 0u};
     if constexpr (PACKED) {
 #pragma unroll
         for (int k = 0; k < CPT; ++k) {
@@ -392,7 +393,7 @@ __device__ __forceinline__ void paged_body(const PagedArgs &a, PagedSmem<NPG> &s
         for (int i = tid; i < NPG * 16; i += 256) {
             const int lp = i >> 4, g = i & 15;
             float b = 0.0f;
-            for (int k = 0; k < SPG; ++k) b = fmaf(to_f32<false>(s_q[g * D + sm.setup.don[lp][k]]), sm.setup.pad[lp][k], b);
+            for (int k = 0; k < SPG; ++k) b = fmaf(to_f32<false>(s_q[g * QROW + sm.setup.don[lp][k]]), sm.setup.pad[lp][k], b);
             sm.bias[lp][g] = b;
         }
     }
@@ -400,7 +401,7 @@ __device__ __forceinline__ void paged_body(const PagedArgs &a, PagedSmem<NPG> &s
 
     u32x4 qb[4];                                   // B operand: Q[g = gl][32 ql + 8 d + e]
 #pragma unroll
-    for (int d = 0; d < 4; ++d) qb[d] = *(const u32x4 *)(s_q + gl * D + 32 * ql + 8 * d);
+    for (int d = 0; d < 4; ++d) qb[d] = *(const u32x4 *)(s_q + gl * QROW + 32 * ql + 8 * d);
 
     float m_run = NEG_INF, l_run = 0.0f;
     f32x4 acc[8];
@@ -467,7 +468,7 @@ __device__ __forceinline__ void paged_body(const PagedArgs &a, PagedSmem<NPG> &s
                 for (int e = 0; e < 4; ++e) {
                     const uint32_t w = sm.salw[lp][4 * ql + e];
                     // Q[g][source channel]; the source is 2 (w & 255) + ((w >> 8) & 255) / 4
-                    qv[e] = s_q[gl * D + 2 * (w & 0xffu) + (((w >> 8) & 0xffu) >> 2)];
+                    qv[e] = s_q[gl * QROW + 2 * (w & 0xffu) + (((w >> 8) & 0xffu) >> 2)];
                     const f32x2 sf = sm.salf[lp][4 * ql + e];
                     const uint32_t hi = (rowp[w & 0xffu] >> ((w >> 8) & 0xffu)) & 15u;
                     const uint32_t lo = (rowp[(w >> 16) & 0xffu] >> (w >> 24)) & 15u;
