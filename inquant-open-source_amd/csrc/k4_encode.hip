@@ -210,6 +210,44 @@ constexpr int CH = 32;                   // tokens per staged chunk
 #endif
 constexpr int KPF = IQ_K4_KPF;           // chunks in flight
 constexpr int XROW = TILE_D + 8;         // u16 per staged row: 68 dwords (16-byte aligned rows, distinct banks)
+#ifndef IQ_K4_NBUF
+#define IQ_K4_NBUF 4
+#endif
+// sealed blocks stream by direct global -> LDS loads into NBUF chunk buffers
+// (unpadded rows), NBUF - 1 chunks in flight while one is processed
+constexpr int NBUF_DMA = IQ_K4_NBUF;
+
+// s_waitcnt vmcnt(2 * ahead) lgkmcnt(0), then s_barrier: this wave's loads
+// of every chunk but the `ahead` newest have landed in LDS and its LDS reads
+// are done; after the barrier the same holds for every wave.  (A plain
+// __syncthreads would wait for all loads in flight.)
+// One 16-byte-per-lane direct load: lane l's 16 bytes at base + voff land
+// at LDS byte lds_base + 16 l (base and lds_base wave-uniform).  Issued from
+// inline assembly so that the compiler does not treat every later LDS read
+// as possibly dependent on it (it would wait for all loads in flight); the
+// waits are explicit (wait_chunk_barrier).
+__device__ __forceinline__ void lds_load16(const void *base, uint32_t voff, uint32_t lds_base)
+{
+    // the operands are wave-uniform: make them scalar registers explicitly
+    // (readfirstlane returns int: widen through uint32_t, not by sign extension)
+    const uint64_t b = (uint64_t)(uintptr_t)base;
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)b);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(b >> 32));
+    const uint64_t sb = (uint64_t)lo | ((uint64_t)hi << 32);
+    asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sb),
+                 "s"(__builtin_amdgcn_readfirstlane(lds_base))
+                 : "memory", "m0");
+}
+
+__device__ __forceinline__ void wait_chunk_barrier(int ahead)
+{
+    switch (ahead) {
+    case 0: asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory"); break;
+    case 1: asm volatile("s_waitcnt vmcnt(2) lgkmcnt(0)\n\ts_barrier" ::: "memory"); break;
+    case 2: asm volatile("s_waitcnt vmcnt(4) lgkmcnt(0)\n\ts_barrier" ::: "memory"); break;
+    default: asm volatile("s_waitcnt vmcnt(6) lgkmcnt(0)\n\ts_barrier" ::: "memory"); break;
+    }
+}
 
 template <bool F16IN>
 __device__ __forceinline__ float tile_f32(uint32_t bits16)
@@ -225,7 +263,11 @@ __device__ __forceinline__ float tile_f32(uint32_t bits16)
 template <bool F16IN, int NCH>
 __global__ __launch_bounds__(K4_THREADS, 4) void k4_encode_tile(K4Args a)
 {
-    __shared__ __attribute__((aligned(16))) uint16_t s_x[2][CH * XROW];
+    constexpr bool DMA = NCH > 0;
+    constexpr int NBUF = DMA ? NBUF_DMA : 2;
+    constexpr int ROWLEN = DMA ? TILE_D : XROW;       // u16 per staged row
+    static_assert(!DMA || (NBUF >= 2 && NBUF <= 4), "chunk buffers");
+    __shared__ __attribute__((aligned(16))) uint16_t s_x[NBUF][CH * ROWLEN];
     __shared__ double s_rcp[TILE_T];    // RN(1 / n), n = 1 .. T
     __shared__ __attribute__((aligned(16))) float s_sal[TILE_D], s_smean[TILE_D], s_err[TILE_D], s_amax[TILE_D],
         s_scale[TILE_D];
@@ -265,27 +307,62 @@ __global__ __launch_bounds__(K4_THREADS, 4) void k4_encode_tile(K4Args a)
 #pragma unroll
         for (int k = 0; k < 2; ++k) {
             const int i = tid + K4_THREADS * k;
-            *(u32x4_t *)(s_x[buf] + (i >> 4) * XROW + 8 * (i & 15)) = sg[k];
+            *(u32x4_t *)(s_x[buf] + (i >> 4) * ROWLEN + 8 * (i & 15)) = sg[k];
         }
     };
-    // chunks 0..2 are loaded and chunk 0 is in LDS buffer 0; visits chunks in
-    // order, with chunk ch in buffer ch & 1 during body(ch)
-    auto start_stream = [&]() {
+    // direct loads of chunk ch into buffer ch % NBUF: each wave fills its two
+    // 1 KiB quarters (64 lanes x 16 bytes, 4 rows each); every row is a whole
+    // block row, so no clamping
+    // LDS byte address of the staging buffers
+    const uint32_t s_x_lds = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint16_t *)&s_x[0][0];
+    // lane byte offset of segment 128 wave + lane within a chunk (rows 4 on
+    // for the second load); the chunk base is wave-uniform
+    const uint32_t dma_off = (uint32_t)(((8 * wave + (lane >> 4)) * (int)a.st + 8 * (lane & 15)) * 2);
+    auto dma_chunk = [&](int ch) {
+        const char *cb = (const char *)xr + (int64_t)ch * CH * a.st * 2;
 #pragma unroll
-        for (int r = 0; r < KPF; ++r)
-            if (r < nch) load_chunk(r, seg[r]);
+        for (int k = 0; k < 2; ++k) {
+            const uint32_t dst = s_x_lds + (uint32_t)((ch % NBUF) * CH * ROWLEN * 2 + 16 * (128 * wave + 64 * k));
+            lds_load16(cb, dma_off + (uint32_t)(k * 4 * (int)a.st * 2), dst);
+        }
     };
+    auto buf_of = [&](int ch) -> const uint16_t * { return s_x[DMA ? ch % NBUF : ch & 1]; };
+    // registers: chunks 0..KPF-1 are loaded and chunk 0 is in LDS buffer 0;
+    // direct loads: chunks 0..NBUF-2 are requested
+    auto start_stream = [&]() {
+        if constexpr (DMA) {
+#pragma unroll
+            for (int r = 0; r < NBUF - 1; ++r)
+                if (r < NCH) dma_chunk(r);
+        } else {
+#pragma unroll
+            for (int r = 0; r < KPF; ++r)
+                if (r < nch) load_chunk(r, seg[r]);
+        }
+    };
+    // visits chunks in order, chunk ch in buf_of(ch) during body(ch)
     auto stream = [&](auto &&body) {
+        if constexpr (DMA) {
 #pragma unroll
-        for (int c0 = 0; c0 < nch; c0 += KPF) {
+            for (int ch = 0; ch < NCH; ++ch) {
+                // requested so far: chunks 0 .. ch + NBUF - 2
+                wait_chunk_barrier(min(NBUF - 2, NCH - 1 - ch));
+                // every wave is past body(ch - 1): its buffer takes chunk ch + NBUF - 1
+                if (ch + NBUF - 1 < NCH) dma_chunk(ch + NBUF - 1);
+                body(ch);
+            }
+        } else {
 #pragma unroll
-            for (int r = 0; r < KPF; ++r) {
-                const int ch = c0 + r;
-                if (ch < nch) {
-                    if (ch + KPF < nch) load_chunk(ch + KPF, seg[r]);   // seg[r] already sits in LDS
-                    body(ch);
-                    if (ch + 1 < nch) store_chunk(seg[(r + 1) % KPF], (ch + 1) & 1);
-                    __syncthreads();
+            for (int c0 = 0; c0 < nch; c0 += KPF) {
+#pragma unroll
+                for (int r = 0; r < KPF; ++r) {
+                    const int ch = c0 + r;
+                    if (ch < nch) {
+                        if (ch + KPF < nch) load_chunk(ch + KPF, seg[r]);   // seg[r] already sits in LDS
+                        body(ch);
+                        if (ch + 1 < nch) store_chunk(seg[(r + 1) % KPF], (ch + 1) & 1);
+                        __syncthreads();
+                    }
                 }
             }
         }
@@ -294,7 +371,7 @@ __global__ __launch_bounds__(K4_THREADS, 4) void k4_encode_tile(K4Args a)
     start_stream();
     if (tid < T) s_rcp[tid] = 1.0 / (double)(tid + 1);
     if (tid == 0) s_bad = 0;
-    store_chunk(seg[0], 0);
+    if constexpr (!DMA) store_chunk(seg[0], 0);
     __syncthreads();
 
     // ---- pass 1: statistics.  Two waves run the Welford chains (channel
@@ -310,7 +387,7 @@ __global__ __launch_bounds__(K4_THREADS, 4) void k4_encode_tile(K4Args a)
     int next_sample = 0;
     const int c1 = tid & (TILE_D - 1);
     stream([&](int ch) {
-        const uint16_t *xs = s_x[ch & 1] + c1;
+        const uint16_t *xs = buf_of(ch) + c1;
         const int t0 = ch * CH, nt = min(CH, T - t0);
         if (welford) {
             if (a.min_error) {
@@ -330,7 +407,7 @@ __global__ __launch_bounds__(K4_THREADS, 4) void k4_encode_tile(K4Args a)
                     double ycur[8], ynxt[8];
 #pragma unroll
                     for (int u = 0; u < 8; ++u) {
-                        cur[u] = tile_f32<F16IN>(xs[u * XROW]);
+                        cur[u] = tile_f32<F16IN>(xs[u * ROWLEN]);
                         ycur[u] = s_rcp[t0 + u];
                     }
 #pragma unroll
@@ -338,7 +415,7 @@ __global__ __launch_bounds__(K4_THREADS, 4) void k4_encode_tile(K4Args a)
                         const int gn = g + 8 < CH ? g + 8 : g;
 #pragma unroll
                         for (int u = 0; u < 8; ++u) {
-                            nxt[u] = tile_f32<F16IN>(xs[(gn + u) * XROW]);
+                            nxt[u] = tile_f32<F16IN>(xs[(gn + u) * ROWLEN]);
                             ynxt[u] = s_rcp[t0 + gn + u];
                         }
 #pragma unroll
@@ -350,7 +427,7 @@ __global__ __launch_bounds__(K4_THREADS, 4) void k4_encode_tile(K4Args a)
                         }
                     }
                 } else {
-                    for (int u = 0; u < nt; ++u) step(tile_f32<F16IN>(xs[u * XROW]), s_rcp[t0 + u], t0 + u);
+                    for (int u = 0; u < nt; ++u) step(tile_f32<F16IN>(xs[u * ROWLEN]), s_rcp[t0 + u], t0 + u);
                 }
             }
         } else {
@@ -358,13 +435,13 @@ __global__ __launch_bounds__(K4_THREADS, 4) void k4_encode_tile(K4Args a)
             // order of the magnitudes, and inf / NaN sort above every finite one
             if (nt == CH) {
 #pragma unroll
-                for (int u = 0; u < CH; ++u) amax_bits = max(amax_bits, (uint32_t)xs[u * XROW] & 0x7fffu);
+                for (int u = 0; u < CH; ++u) amax_bits = max(amax_bits, (uint32_t)xs[u * ROWLEN] & 0x7fffu);
             } else {
-                for (int u = 0; u < nt; ++u) amax_bits = max(amax_bits, (uint32_t)xs[u * XROW] & 0x7fffu);
+                for (int u = 0; u < nt; ++u) amax_bits = max(amax_bits, (uint32_t)xs[u * ROWLEN] & 0x7fffu);
             }
             // the samples r * stride that fall in this chunk, in order
             for (; next_sample < t0 + nt; next_sample += stride) {
-                const float v = tile_f32<F16IN>(xs[(next_sample - t0) * XROW]);
+                const float v = tile_f32<F16IN>(xs[(next_sample - t0) * ROWLEN]);
                 sa.add(fabsf(v));
                 sm.add(v);
             }
@@ -382,9 +459,10 @@ __global__ __launch_bounds__(K4_THREADS, 4) void k4_encode_tile(K4Args a)
         // stash the sampled mean until the Welford waves are done with s_smean
         s_scale[c1] = sm.finish() / (float)ns;
     }
-    // the first chunks of pass 2 load during the selection
-    start_stream();
+    // the first chunks of pass 2 load during the selection (once every wave
+    // is done with pass 1's buffers)
     __syncthreads();
+    start_stream();
     if (tid < TILE_D) {
         const float smean = s_scale[tid];
         if (a.min_error) {
@@ -412,7 +490,7 @@ __global__ __launch_bounds__(K4_THREADS, 4) void k4_encode_tile(K4Args a)
         a.padding[row * a.count + tid] = s_smean[s_don[tid]];
     }
     if (tid == 0 && s_bad) atomicOr(a.bad, 1);
-    store_chunk(seg[0], 0);
+    if constexpr (!DMA) store_chunk(seg[0], 0);
     __syncthreads();
 
     // ---- pass 2: quantize; thread owns channels 8 j .. 8 j + 7 of tokens
@@ -441,7 +519,7 @@ __global__ __launch_bounds__(K4_THREADS, 4) void k4_encode_tile(K4Args a)
         for (int it = 0; it < 2; ++it) {
             const int tl = 8 * wave + 4 * it + tq, t = t0 + tl;
             if (t < T) {
-                const uint16_t *xt = s_x[ch & 1] + tl * XROW;
+                const uint16_t *xt = buf_of(ch) + tl * ROWLEN;
                 // branch-free: every channel reads the value it encodes (its
                 // own, or for a donor slot its source's); the reciprocal
                 // quotient decides the rounding unless it is within 2^-12 of
@@ -524,7 +602,8 @@ extern "C" int iq_k4_quantize(const void *x, int x_dtype, const int64_t *x_strid
              min_error ? 1 : 0, payload, scales, src, don, desc_bytes, padding, bad_flag};
     const bool tile = (x_dtype == IQ_BF16 || x_dtype == IQ_F16) && D == TILE_D && T <= TILE_T && H <= 65535 &&
                       x_strides[3] == 1 && x_strides[2] % 8 == 0 && x_strides[1] % 8 == 0 &&
-                      x_strides[0] % 8 == 0 && ((uintptr_t)x & 15) == 0;
+                      x_strides[0] % 8 == 0 && ((uintptr_t)x & 15) == 0 && x_strides[2] >= 0 &&
+                      x_strides[2] <= (1 << 24);   // 32-bit lane offsets within a chunk
     if (tile) {
         const dim3 grid((unsigned)B, (unsigned)H), block(K4_THREADS);
         const hipStream_t st = (hipStream_t)stream;
