@@ -219,8 +219,11 @@ constexpr int NBUF_DMA = IQ_K4_NBUF;
 
 // s_waitcnt vmcnt(2 * ahead) lgkmcnt(0), then s_barrier: this wave's loads
 // of every chunk but the `ahead` newest have landed in LDS and its LDS reads
-// are done; after the barrier the same holds for every wave.  (A plain
-// __syncthreads would wait for all loads in flight.)
+// are done; after the barrier the same holds for every wave.  Vector memory
+// operations retire in issue order, so at most 2 * ahead outstanding means
+// every older load is done; stores issued after a chunk's loads only make
+// the wait longer.  (A plain __syncthreads would wait for all loads in
+// flight.)
 // One 16-byte-per-lane direct load: lane l's 16 bytes at base + voff land
 // at LDS byte lds_base + 16 l (base and lds_base wave-uniform).  Issued from
 // inline assembly so that the compiler does not treat every later LDS read
