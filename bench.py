@@ -10,8 +10,10 @@ replayed as one HIP graph).  Inputs are resident in HBM; the 28 layers
 value  = algorithmic bytes (packed K/V, scales, role maps, padding, V params,
          pointer table, sink, tail, Q, O) per step / step time  [GB/s]
 extras = codec encode Mtok/s (Mistral-7B layer, 32768
-         tokens x 8 KV heads, K4 min_error + V2 g64), roofline and the CPU
-         oracle baseline on a bounded sample.
+         tokens x 8 KV heads, K4 min_error + V2 g64), the config 3 decode
+         (32 Mistral-7B layers), the config 2 append, the config 4 batched
+         paged decode, roofline and the CPU oracle baseline on a bounded
+         sample.
 """
 from __future__ import annotations
 
@@ -39,6 +41,7 @@ def parse():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-graph", action="store_true", help="launch layer by layer instead of a HIP graph")
     ap.add_argument("--no-paged", action="store_true", help="skip the batched paged decode (config 4)")
+    ap.add_argument("--no-cfg3", action="store_true", help="skip the Mistral-7B decode (config 3)")
     ap.add_argument("--copy-probe", action="store_true",
                     help="only run a 1 GiB device-to-device copy (calibrates rocprofv3 FETCH_SIZE / WRITE_SIZE)")
     return ap.parse_args()
@@ -87,15 +90,15 @@ def kv_tensor(gen, heads, tokens, device, frac_groups=(2, 2, 1), scale=20.0):
     return x.to(torch.bfloat16)
 
 
-def build_layer(seed, device, H=4, G=7, n_blocks=128, block=256, sink=4, tail=128):
+def build_layer(seed, device, H=4, G=7, n_blocks=128, block=256, sink=4, tail=128, frac_groups=(2, 2, 1)):
     import torch
     from inquant.cache import _quantize_temporal_blocks
     from inquant.codec import CodecConfig
     from inquant.triton_attention import PackedDecodeState, SharedDecodeWorkspace
     from inquant.value_codec import quantize_value_blocks
     gen = torch.Generator(device=device).manual_seed(seed)
-    k = kv_tensor(gen, H, n_blocks * block, device)
-    v = kv_tensor(gen, H, n_blocks * block, device)
+    k = kv_tensor(gen, H, n_blocks * block, device, frac_groups=frac_groups)
+    v = kv_tensor(gen, H, n_blocks * block, device, frac_groups=frac_groups)
     cfg = CodecConfig(donor_policy="min_error")
     kb = _quantize_temporal_blocks(k, n_blocks, block, cfg)
     vb = quantize_value_blocks(v, n_blocks, block, 2, 64)
@@ -164,6 +167,24 @@ def time_decode(layers, steps, warmup, use_graph):
     torch.cuda.synchronize()
     ms = start.elapsed_time(stop) / steps
     return ms, outs
+
+
+def time_decode_cfg3(device, layers=32, steps=20, warmup=3):
+    """Config 3 decode: Mistral-7B shape, 32 query heads over 8 KV heads, 32768
+    packed tokens (outliers at 8% of channels in 3-wide runs) + 4 sink + 128
+    tail per layer, 32 layers replayed as one HIP graph."""
+    import torch
+    lay = [build_layer(3000 + i, device, H=8, G=4, frac_groups=(3, 3, 3, 1)) for i in range(layers)]
+    torch.cuda.synchronize()
+    per_layer = algorithmic_bytes(lay[0])
+    ms, _ = time_decode(lay, steps, warmup, True)
+    us = ms * 1e3 / layers
+    out = {"layers": layers, "us_per_layer": round(us, 3), "bytes_per_layer": per_layer,
+           "gbs": round(per_layer / (us * 1e-6) / 1e9, 2),
+           "hbm_frac": round(per_layer / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
+    del lay
+    torch.cuda.empty_cache()
+    return out
 
 
 def time_encode(device, reps=10):
@@ -302,7 +323,7 @@ def time_paged(device, layers=4, n_seq=16, block=16, H=4, G=7, seed=4, steps=20)
             "tokens_per_s": round(n_seq / (us * 1e-6), 1), "layers_rotated": layers}
 
 
-def time_append(device, H=4, packed_tokens=32768):
+def time_append(device, H=4, packed_tokens=32768, validate_positions=True):
     """Config 2 append, through the cache API of one Qwen2.5-7B layer (32K packed
     context): 128 single-token appends (dense tail 128 -> 256, no seal), then the
     append that seals one 256-token block (K4 + V2 encode) starting from a
@@ -312,7 +333,8 @@ def time_append(device, H=4, packed_tokens=32768):
     from inquant.codec import CodecConfig
     from inquant.triton_attention import PackedDecodeState
     g = torch.Generator(device=device).manual_seed(11)
-    cfg = CacheConfig(codec=CodecConfig(donor_policy="min_error"), value_bits=2, value_group_size=64)
+    cfg = CacheConfig(codec=CodecConfig(donor_policy="min_error"), value_bits=2, value_group_size=64,
+                      validate_positions=validate_positions)
     cache = InQuantCache(cfg)
     n0 = 4 + packed_tokens + 128
     k = kv_tensor(g, H, n0 + 768, device)
@@ -421,6 +443,10 @@ def main():
     enc = time_encode(device)
     paged = None if args.no_paged else time_paged(device)
     append = time_append(device)
+    # a controlled runner may skip the position check and its device-to-host
+    # copy per token (cache.py:30-32)
+    append["append_us_per_token_unvalidated"] = time_append(device, validate_positions=False)["append_us_per_token"]
+    cfg3 = None if args.no_cfg3 else time_decode_cfg3(device)
     result = {
         "metric": METRIC,
         "value": round(gbs, 2),
@@ -448,6 +474,8 @@ def main():
         "encode": {k: round(v, 3) for k, v in enc.items()},
     }
     result["append_cfg2"] = append
+    if cfg3 is not None:
+        result["decode_cfg3"] = cfg3
     if paged is not None:
         result["paged_cfg4"] = paged
     if not args.no_cpu_baseline:
