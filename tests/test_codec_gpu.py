@@ -102,6 +102,24 @@ def test_k4_quantize_matches_oracle(D, T, stride, policy, frac, dtype):
         _same_bits(_np(got.tensors[field]).astype(ref[field].dtype), ref[field], field)
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_k4_sealed_blocks_with_padded_rows(dtype):
+    # sealed 256-token blocks whose rows are 192 elements apart (a view of
+    # wider rows) and whose heads are not adjacent: the direct-to-LDS chunk
+    # loads take the strides from the view
+    from inquant.codec import CodecConfig, quantize
+    x = synth.normal(91, (2, 3, 256, 192)) * np.exp(synth.normal(92, (2, 3, 256, 1)))
+    x[..., 5:8] *= 30
+    wide = _dev(x, torch.float64).to(dtype)
+    view = wide[:, :, :, 32:160]
+    assert view.stride(2) == 192 and not view.is_contiguous()
+    for policy in ("neighbors", "min_error"):
+        ref = oracle.k4_quantize(_np(view.float()), 8, 0.125, policy)
+        got = quantize(view, CodecConfig(donor_policy=policy))
+        for field in ("payload", "scales", "salient_channels", "donor_channels", "padding"):
+            _same_bits(_np(got.tensors[field]).astype(ref[field].dtype), ref[field], field)
+
+
 def test_k4_rejects_nonfinite_values():
     from inquant.codec import quantize
     for bad in (float("nan"), float("inf")):
