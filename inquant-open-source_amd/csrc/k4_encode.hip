@@ -228,7 +228,9 @@ constexpr int NBUF_DMA = IQ_K4_NBUF;
 // at LDS byte lds_base + 16 l (base and lds_base wave-uniform).  Issued from
 // inline assembly so that the compiler does not treat every later LDS read
 // as possibly dependent on it (it would wait for all loads in flight); the
-// waits are explicit (wait_chunk_barrier).
+// waits are explicit (wait_chunk_barrier).  The assembly sets M0 itself;
+// nothing the compiler generates for this kernel reads M0 (M0 is a reserved
+// register, so it cannot be listed as clobbered).
 __device__ __forceinline__ void lds_load16(const void *base, uint32_t voff, uint32_t lds_base)
 {
     // the operands are wave-uniform: make them scalar registers explicitly
@@ -239,7 +241,7 @@ __device__ __forceinline__ void lds_load16(const void *base, uint32_t voff, uint
     const uint64_t sb = (uint64_t)lo | ((uint64_t)hi << 32);
     asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sb),
                  "s"(__builtin_amdgcn_readfirstlane(lds_base))
-                 : "memory", "m0");
+                 : "memory");
 }
 
 __device__ __forceinline__ void wait_chunk_barrier(int ahead)
@@ -355,7 +357,6 @@ __global__ __launch_bounds__(K4_THREADS, 4) void k4_encode_tile(K4Args a)
                 body(ch);
             }
         } else {
-#pragma unroll
             for (int c0 = 0; c0 < nch; c0 += KPF) {
 #pragma unroll
                 for (int r = 0; r < KPF; ++r) {
