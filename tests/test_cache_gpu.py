@@ -1,0 +1,201 @@
+"""InQuantCache behaviour on the GPU, restating the reference's cache tests
+(tests/test_cache.py:15-158) with ROCm tensors: storage ownership and
+accounting, append chunking over seal boundaries, immutable sealed blocks,
+sink accumulation, batched prefill equal to serial per-block encodes, position
+checks, reset, and a 32K-token layer.  Serial encodes are additionally pinned
+to the CPU oracle, so the comparison is not only self-consistency."""
+from unittest.mock import patch
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle
+
+pytestmark = pytest.mark.gpu
+
+
+def _cfg(**kw):
+    from inquant.cache import CacheConfig
+    from inquant.codec import CodecConfig
+    base = dict(block_size=8, residual_length=3, sink_tokens=2)
+    base.update(kw)
+    codec = base.pop("codec", CodecConfig(salient_fraction=0))
+    return CacheConfig(codec, **base)
+
+
+def _randn(*shape, seed, dtype=torch.float32):
+    g = torch.Generator().manual_seed(seed)
+    return torch.randn(*shape, generator=g).to(dtype).cuda()
+
+
+def test_prefill_exact_small_tail_storage_and_accounting():
+    # test_cache.py:15-31
+    from inquant.cache import InQuantCache
+    cache = InQuantCache(_cfg())
+    key, value = _randn(1, 2, 37, 8, seed=1), _randn(1, 2, 37, 8, seed=2)
+    returned_key, returned_value = cache.update(key, value, 0)
+    assert returned_key is key and returned_value is value
+    layer = cache._layers[0]
+    for item in (layer.sink_key, layer.sink_value, layer.residual_key, layer.residual_value):
+        assert item.untyped_storage().nbytes() == item.numel() * item.element_size()
+        assert item.untyped_storage().data_ptr() != key.untyped_storage().data_ptr()
+    packed_bytes = sum(block.nbytes for block in layer.key_blocks + layer.value_blocks)
+    assert cache.nbytes == packed_bytes + cache.sink_nbytes + cache.residual_nbytes
+    assert cache.bf16_nbytes == 2 * key.numel() * 2
+    assert cache.memory_stats()["quantized_layer_tokens"] == 32
+    assert cache.get_seq_length() == 37 and cache.get_usable_length(2) == 37
+    assert cache.get_max_cache_shape() is None
+
+
+def test_multihead_append_chunking_and_old_blocks_immutable():
+    # test_cache.py:33-59, with the serial blocks also checked against the oracle
+    from inquant.cache import InQuantCache
+    from inquant.codec import quantize
+    cfg = _cfg()
+    cache = InQuantCache(cfg)
+    key, value = _randn(1, 3, 61, 8, seed=3), _randn(1, 3, 61, 8, seed=4)
+    cache.update(key[:, :, :21], value[:, :, :21], 0)
+    old_block = cache._layers[0].key_blocks[0]
+    old_decoded = old_block.dequantize().clone()
+    seen = 21
+    for count in (1, 7, 12, 20):
+        prior_key, prior_value = cache.materialize()
+        out_key, out_value = cache.update(key[:, :, seen:seen + count], value[:, :, seen:seen + count], 0)
+        torch.testing.assert_close(out_key, torch.cat((prior_key, key[:, :, seen:seen + count]), dim=2))
+        torch.testing.assert_close(out_value, torch.cat((prior_value, value[:, :, seen:seen + count]), dim=2))
+        seen += count
+    layer = cache._layers[0]
+    assert layer.key_blocks[0] is old_block
+    torch.testing.assert_close(old_block.dequantize(), old_decoded, rtol=0, atol=0)
+    blocks = (seen - cfg.sink_tokens - cfg.residual_length) // cfg.block_size
+    for original, actual, sealed in ((key, cache.materialize()[0], layer.key_blocks),
+                                     (value, cache.materialize()[1], layer.value_blocks)):
+        pieces = [original[:, :, :2]]
+        for index in range(blocks):
+            start = 2 + index * 8
+            serial = quantize(original[:, :, start:start + 8], cfg.codec)
+            pieces.append(serial.dequantize(dtype=original.dtype))
+            ref = oracle.k4_quantize(original[:, :, start:start + 8].cpu().numpy(), cfg.codec.sample_stride,
+                                     cfg.codec.salient_fraction, cfg.codec.donor_policy)
+            np.testing.assert_array_equal(sealed[index].payload.cpu().numpy(), ref["payload"])
+            np.testing.assert_array_equal(sealed[index].scales.cpu().numpy().view(np.uint32),
+                                          ref["scales"].view(np.uint32))
+        pieces.append(original[:, :, 2 + blocks * 8:])
+        torch.testing.assert_close(actual, torch.cat(pieces, dim=2), rtol=0, atol=0)
+    assert seen == 61 and cache.get_seq_length() == 61
+    assert layer.residual_key.shape[2] < cfg.residual_length + cfg.block_size
+
+
+def test_sink_accumulates_across_short_prefills():
+    # test_cache.py:61-67
+    from inquant.cache import InQuantCache
+    cache = InQuantCache(_cfg())
+    x = _randn(1, 2, 7, 8, seed=5)
+    for pos in range(7):
+        result, _ = cache.update(x[:, :, pos:pos + 1], x[:, :, pos:pos + 1], 0)
+        torch.testing.assert_close(result, x[:, :, :pos + 1], rtol=0, atol=0)
+    torch.testing.assert_close(cache.materialize()[0], x, rtol=0, atol=0)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_batched_prefill_matches_serial_blocks_and_owns_compact_storage(dtype):
+    # test_cache.py:69-108: heads and temporal blocks keep independent
+    # statistics after the block axis moves into the batch; one encode call
+    # per tensor, every field an owned compact tensor
+    import inquant.cache as cache_mod
+    from inquant.cache import InQuantCache
+    from inquant.codec import CodecConfig, quantize
+    cfg = _cfg(codec=CodecConfig(sample_stride=3, salient_fraction=.25))
+    key = _randn(1, 3, 16, 55, seed=6, dtype=dtype).transpose(2, 3)
+    value = _randn(1, 3, 16, 55, seed=7, dtype=dtype).transpose(2, 3)
+    assert not key.is_contiguous()
+    for index in range(6):
+        key[:, index % 3, 2 + index * 8:10 + index * 8, index] *= 20
+        value[:, (index + 1) % 3, 2 + index * 8:10 + index * 8, 15 - index] *= 17
+    cache = InQuantCache(cfg)
+    with patch.object(cache_mod, "quantize", wraps=quantize) as observed:
+        cache.update(key, value, 0)
+    assert observed.call_count == 2
+    assert tuple(observed.call_args_list[0].args[0].shape) == (6, 3, 8, 16)
+    layer = cache._layers[0]
+    expected_bytes = 0
+    owned = set()
+    for original, blocks in ((key, layer.key_blocks), (value, layer.value_blocks)):
+        assert len(blocks) == 6
+        for index, actual in enumerate(blocks):
+            start = 2 + index * 8
+            serial = quantize(original[:, :, start:start + 8], cfg.codec)
+            assert actual.shape == serial.shape and actual.original_dtype == dtype
+            assert actual.nbytes == serial.nbytes
+            expected_bytes += serial.nbytes
+            for name, tensor in actual.tensors.items():
+                torch.testing.assert_close(tensor, serial.tensors[name], rtol=0, atol=0)
+                assert tensor.untyped_storage().nbytes() == tensor.numel() * tensor.element_size()
+                assert tensor.is_contiguous()
+                if tensor.numel():
+                    address = tensor.untyped_storage().data_ptr()
+                    assert address not in owned
+                    owned.add(address)
+            torch.testing.assert_close(actual.dequantize(), serial.dequantize(), rtol=0, atol=0)
+    assert cache.nbytes == expected_bytes + cache.sink_nbytes + cache.residual_nbytes
+
+
+def test_positions_layers_reset_and_unsupported_operations():
+    # test_cache.py:110-134
+    from inquant.cache import InQuantCache
+    cache = InQuantCache(_cfg())
+    x = _randn(1, 2, 7, 8, seed=8)
+    pos = torch.arange(7, device="cuda")
+    cache.update(x, x, 0, {"cache_position": pos})
+    cache.update(x, x, 1, {"cache_position": pos})
+    assert len(cache) == 2 and cache.seen_tokens == 7
+    assert cache.get_seq_length(5) == 0
+    assert cache.get_mask_sizes(torch.arange(7, 9, device="cuda"), 1) == (9, 0)
+    with pytest.raises(ValueError):
+        cache.update(x, x, 0, {"cache_position": pos})
+    assert cache.get_seq_length() == 7
+    with pytest.raises(NotImplementedError):
+        cache.update(x.expand(2, -1, -1, -1), x.expand(2, -1, -1, -1), 0)
+    with pytest.raises(NotImplementedError):
+        cache.reorder_cache(torch.tensor([0]))
+    with pytest.raises(NotImplementedError):
+        cache.crop(3)
+    with pytest.raises(ValueError):
+        cache.update(x[:, :, :, :7], x[:, :, :, :7], 2)
+    assert len(cache) == 2
+    cache.release()
+    assert cache.nbytes == 0 and cache.get_seq_length() == 0 and len(cache) == 0
+
+
+def test_controlled_position_validation_opt_out_keeps_shape_checks():
+    # test_cache.py:136-148
+    from inquant.cache import CacheConfig, InQuantCache
+    cache = InQuantCache(CacheConfig(validate_positions=False))
+    x = _randn(1, 2, 3, 8, seed=9)
+    with patch("inquant.cache.torch.equal", side_effect=AssertionError("Unexpected value synchronization")):
+        cache.update(x, x, 0, {"cache_position": torch.arange(3, device="cuda")})
+        cache.append_for_attention(x[:, :, :1], x[:, :, :1], 0, {"cache_position": torch.tensor([3], device="cuda")})
+    assert cache.get_seq_length() == 4
+    for bad in (torch.tensor([[4]]), torch.tensor([4, 5]), torch.tensor([4.0]), [4]):
+        with pytest.raises(ValueError):
+            cache.append_for_attention(x[:, :, :1], x[:, :, :1], 0, {"cache_position": bad})
+        assert cache.get_seq_length() == 4
+    with pytest.raises(ValueError):
+        CacheConfig(validate_positions="false")
+
+
+def test_over_32k_cache_shape_and_persistent_bytes():
+    # test_cache.py:150-158
+    from inquant.cache import CacheConfig, InQuantCache
+    from inquant.codec import CodecConfig
+    cache = InQuantCache(CacheConfig(CodecConfig(salient_fraction=0), block_size=256, residual_length=128,
+                                     sink_tokens=4))
+    x = _randn(1, 2, 32768, 8, seed=10, dtype=torch.bfloat16)
+    cache.update(x, x, 0)
+    tail = _randn(1, 2, 3, 8, seed=11, dtype=torch.bfloat16)
+    out, _ = cache.update(tail, tail, 0)
+    assert tuple(out.shape) == (1, 2, 32771, 8)
+    assert cache.get_seq_length() == 32771
+    assert cache.nbytes < cache.bf16_nbytes * 0.8
+    assert cache.metadata_nbytes > 0
