@@ -1,8 +1,9 @@
 """InQuantCache behaviour on the GPU, restating the reference's cache tests
-(tests/test_cache.py:15-158) with ROCm tensors: storage ownership and
-accounting, append chunking over seal boundaries, immutable sealed blocks,
-sink accumulation, batched prefill equal to serial per-block encodes, position
-checks, reset, and a 32K-token layer.  Serial encodes are additionally pinned
+(tests/test_cache.py:15-158, test_value_codec.py:52-76) with ROCm tensors:
+storage ownership and accounting, append chunking over seal boundaries,
+immutable sealed blocks, sink accumulation, batched prefill equal to serial
+per-block encodes, position checks, reset, a 32K-token layer, and the append
+view against update() across seals.  Serial encodes are additionally pinned
 to the CPU oracle, so the comparison is not only self-consistency."""
 from unittest.mock import patch
 
@@ -199,3 +200,32 @@ def test_over_32k_cache_shape_and_persistent_bytes():
     assert cache.get_seq_length() == 32771
     assert cache.nbytes < cache.bf16_nbytes * 0.8
     assert cache.metadata_nbytes > 0
+
+
+def test_k4v2_append_semantics_and_owned_bytes_across_seal_boundary():
+    # test_value_codec.py:52-76: the append view (sink, sealed blocks, tail)
+    # equals what update() returns, token by token across seals, with the
+    # same owned bytes and peak
+    from inquant.cache import CacheConfig, InQuantCache
+    from inquant.codec import CodecConfig
+    cfg = CacheConfig(CodecConfig(donor_policy="min_error"), block_size=8, residual_length=3, sink_tokens=2,
+                      value_bits=2, track_peak_bytes=True)
+    a, b = InQuantCache(cfg), InQuantCache(cfg)
+    k, v = _randn(1, 2, 51, 128, seed=12), _randn(1, 2, 51, 128, seed=13)
+    for cache in (a, b):
+        cache.update(k[:, :, :27], v[:, :, :27], 0)
+    expected_peak = a.nbytes
+    for step in range(27, 51):
+        expected = a.update(k[:, :, step:step + 1], v[:, :, step:step + 1], 0)
+        view = b.append_for_attention(k[:, :, step:step + 1], v[:, :, step:step + 1], 0)
+        for wanted, sink, blocks, tail in zip(expected, (view.sink_key, view.sink_value),
+                                              (view.key_blocks, view.value_blocks),
+                                              (view.residual_key, view.residual_value)):
+            actual = torch.cat([sink] + [block.dequantize() for block in blocks] + [tail], dim=2)
+            torch.testing.assert_close(actual, wanted, rtol=0, atol=0)
+        assert a.nbytes == b.nbytes
+        expected_peak = max(expected_peak, a.nbytes)
+        assert a.peak_nbytes == b.peak_nbytes == expected_peak
+    stats = a.memory_stats()
+    assert stats["nbytes"] == sum(stats[key] for key in ("payload_nbytes", "metadata_nbytes", "sink_nbytes",
+                                                         "residual_nbytes", "auxiliary_nbytes"))
