@@ -98,3 +98,45 @@ def test_grad_mode_is_refused():
             model(torch.tensor([[2, 3, 4]], device="cuda"), past_key_values=cache)
         with pytest.raises(RuntimeError, match="inference-only"):
             model(torch.tensor([[5]], device="cuda"), past_key_values=cache)
+
+
+@pytest.mark.parametrize("value_bits", [None, 2])
+def test_qwen_three_layers_shared_workspace_and_cache_reset(value_bits):
+    # test_value_codec.py:124-159: three layers share one decode workspace
+    # with bit-identical logits to per-layer workspaces, the byte accounting
+    # differs by exactly the two saved workspaces, and reset drops the pool
+    from dataclasses import replace
+    from inquant.cache import CacheConfig, InQuantCache
+    from inquant.codec import CodecConfig
+    from inquant.qwen_fused import enable_fused_qwen2
+    torch.manual_seed(87)
+    model = _qwen(layers=3).to(device="cuda", dtype=torch.bfloat16)
+    original_model = copy.deepcopy(model)
+    cfg = CacheConfig(CodecConfig(donor_policy="min_error"), block_size=32, residual_length=4, sink_tokens=2,
+                      value_bits=value_bits, shared_workspace=True, track_peak_bytes=True)
+    packed = InQuantCache(cfg)
+    independent = InQuantCache(replace(cfg, shared_workspace=False))
+    dense_ref = InQuantCache(cfg)
+    tokens = torch.randint(0, 97, (1, 99), device="cuda")
+    with enable_fused_qwen2(model), torch.inference_mode():
+        for cache in (packed, independent):
+            model(tokens, past_key_values=cache)
+        original_model(tokens, past_key_values=dense_ref)
+        for step in range(10):
+            token = torch.tensor([[step + 3]], device="cuda")
+            expected = model(token, past_key_values=independent).logits
+            dense = original_model(token, past_key_values=dense_ref).logits
+            with patch.object(packed, "materialize", side_effect=AssertionError("dense history not allowed")):
+                actual = model(token, past_key_values=packed).logits
+            torch.testing.assert_close(actual, expected, rtol=0, atol=0)
+            torch.testing.assert_close(actual.float(), dense.float(), rtol=.035, atol=.015)
+    per_layer = next(iter(independent._attention_states.values())).kernel._workspace.untyped_storage().nbytes()
+    assert independent.nbytes - packed.nbytes == 2 * per_layer
+    for cache in (packed, independent):
+        shared = cache._shared_decode_workspace.nbytes if cache._shared_decode_workspace else 0
+        assert cache._tracked_live_bytes + cache._tracked_aux_bytes + shared == cache.nbytes
+        assert cache.peak_nbytes >= cache.nbytes
+    old_pool = packed._shared_decode_workspace
+    packed.reset()
+    assert packed.nbytes == 0 and packed._shared_decode_workspace is None
+    assert old_pool is not InQuantCache(cfg)._shared_decode_workspace
