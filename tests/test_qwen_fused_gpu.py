@@ -140,3 +140,36 @@ def test_qwen_three_layers_shared_workspace_and_cache_reset(value_bits):
     packed.reset()
     assert packed.nbytes == 0 and packed._shared_decode_workspace is None
     assert old_pool is not InQuantCache(cfg)._shared_decode_workspace
+
+
+def test_mistral_v2_cache_logits_across_sealing_boundaries():
+    # test_mistral_fused.py:12-40 (GPU case): two layers, K4 keys with V2
+    # values, a 66-token prompt in 32-token blocks, eight decode steps that
+    # cross a seal, restored attention forward afterwards
+    from transformers import MistralConfig, MistralForCausalLM
+    from inquant.cache import CacheConfig, InQuantCache
+    from inquant.codec import CodecConfig
+    from inquant.qwen_fused import enable_fused_mistral
+    torch.manual_seed(673)
+    cfg = MistralConfig(vocab_size=97, hidden_size=512, intermediate_size=1024, num_hidden_layers=2,
+                        num_attention_heads=4, num_key_value_heads=2, max_position_embeddings=32768,
+                        sliding_window=None, rope_theta=1e6, bos_token_id=1, eos_token_id=96, pad_token_id=0,
+                        attn_implementation="sdpa")
+    model = MistralForCausalLM(cfg).to(device="cuda", dtype=torch.bfloat16).eval()
+    ref = copy.deepcopy(model)
+    cache_cfg = CacheConfig(CodecConfig(donor_policy="min_error"), block_size=32, residual_length=4, sink_tokens=4,
+                            value_bits=2, value_group_size=64)
+    original = model.model.layers[0].self_attn.forward
+    with enable_fused_mistral(model) as handle, torch.no_grad():
+        a, b = InQuantCache(cache_cfg), InQuantCache(cache_cfg)
+        prompt = torch.randint(2, 90, (1, 66), device="cuda")
+        torch.testing.assert_close(model(prompt, past_key_values=a).logits, ref(prompt, past_key_values=b).logits,
+                                   atol=0, rtol=0)
+        for i in range(8):
+            token = torch.tensor([[i + 5]], device="cuda")
+            expected = ref(token, past_key_values=b).logits
+            with patch.object(a, "materialize", side_effect=AssertionError("dense fallback")):
+                actual = model(token, past_key_values=a).logits
+            torch.testing.assert_close(actual.float(), expected.float(), atol=.012, rtol=.035)
+        assert handle.fused_decode_calls == 16 and handle.cpu_reference_calls == 0
+    assert model.model.layers[0].self_attn.forward == original
