@@ -120,6 +120,54 @@ def test_k4_sealed_blocks_with_padded_rows(dtype):
             _same_bits(_np(got.tensors[field]).astype(ref[field].dtype), ref[field], field)
 
 
+@pytest.mark.parametrize("fraction", [0.0, 0.125, 0.5])
+def test_k4_all_zero_is_finite_and_exact(fraction):
+    # test_codec.py:73-81; T = 256 takes the tile encoder, 17 the generic one
+    from inquant.codec import CodecConfig, quantize
+    for T, D in ((17, 16), (256, 128)):
+        x = torch.zeros(1, 2, T, D, dtype=torch.bfloat16, device="cuda")
+        packed = quantize(x, CodecConfig(salient_fraction=fraction))
+        restored = packed.dequantize()
+        assert restored.dtype == x.dtype and torch.isfinite(restored).all()
+        assert torch.count_nonzero(restored) == 0
+        assert packed.dequantize(torch.float32).dtype == torch.float32
+
+
+def test_k4_zero_fraction_is_uniform_int4_and_nibble_patterns_stay_codes():
+    # test_codec.py:84-99
+    from inquant.codec import CodecConfig, quantize
+    x = synth.normal(93, (1, 4, 256, 128)).astype(np.float32)
+    xt = _dev(x)
+    packed = quantize(xt, CodecConfig(salient_fraction=0))
+    s = packed.scales.unsqueeze(-2)
+    torch.testing.assert_close(packed.dequantize(), (xt / s).round().clamp(-7, 7) * s, rtol=0, atol=0)
+    assert packed.salient_channels.numel() == packed.donor_channels.numel() == packed.padding.numel() == 0
+    assert packed.metadata_nbytes == packed.scales.numel() * 4
+    codes = torch.arange(-7, 8, dtype=torch.float32, device="cuda").view(1, 1, 15, 1).expand(1, 1, 15, 16)
+    torch.testing.assert_close(quantize(codes, CodecConfig(salient_fraction=0)).dequantize(), codes, rtol=0, atol=0)
+
+
+def test_k4_noncontiguous_input_and_detached_output():
+    # test_codec.py:109-115
+    from inquant.codec import quantize
+    x = _dev(synth.normal(94, (1, 2, 16, 12))).requires_grad_(True).transpose(-2, -1)
+    packed = quantize(x)
+    assert packed.dequantize().shape == x.shape
+    assert all(not t.requires_grad for t in packed.tensors.values())
+    assert torch.isfinite(packed.dequantize()).all()
+
+
+@pytest.mark.parametrize("channels", [2, 128, 258])
+def test_k4_half_salient_fraction_always_has_enough_donors(channels):
+    # test_codec.py:118-124
+    from inquant.codec import CodecConfig, quantize
+    packed = quantize(_dev(synth.normal(95 + channels, (1, 1, 3, channels))), CodecConfig(salient_fraction=0.5))
+    assert packed.donor_channels.unique().numel() == channels // 2
+    assert torch.isfinite(packed.dequantize()).all()
+    if channels > 256:
+        assert packed.donor_channels.dtype == torch.int32
+
+
 def test_k4_rejects_nonfinite_values():
     from inquant.codec import quantize
     for bad in (float("nan"), float("inf")):
