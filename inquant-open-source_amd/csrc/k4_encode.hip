@@ -399,7 +399,12 @@ __global__ __launch_bounds__(K4_THREADS, 4) void k4_encode_tile(K4Args a)
                     const double dv = (double)xf;
                     const double delta = __dsub_rn(dv, mean);
                     const double q0 = __dmul_rn(delta, y);
-                    const double r = __builtin_fma(-q0, (double)(t + 1), delta);
+                    double n = (double)(t + 1);
+                    // a sealed block's counts are compile-time constants: held in
+                    // scalar registers they feed a three-address fma; as a literal
+                    // operand they force the two-address form and a copy of delta
+                    if constexpr (NCH > 0) asm("" : "+s"(n));
+                    const double r = __builtin_fma(-q0, n, delta);
                     mean = __dadd_rn(mean, __builtin_fma(r, y, q0));
                     const double nd = __dsub_rn(dv, mean);
                     m2 = __dadd_rn(m2, __dmul_rn(delta, nd));
@@ -500,21 +505,30 @@ __global__ __launch_bounds__(K4_THREADS, 4) void k4_encode_tile(K4Args a)
     // ---- pass 2: quantize; thread owns channels 8 j .. 8 j + 7 of tokens
     // t0 + 8 wave + tq and t0 + 8 wave + tq + 4 of every chunk
     const int j = lane & 15, tq = lane >> 4;
+    // Per-slot constants, computed once and pinned in registers (opaque to
+    // the compiler, which would otherwise rebuild them from the role masks at
+    // every token: four extra instructions per element).  xe[e] is the LDS
+    // address of the value slot e encodes (its own channel, or for a donor
+    // slot its source's) in row 8 wave + tq of buffer 0; every other row and
+    // buffer is a constant offset from it.
     float scl[8], rscl[8], lim[8], bias[8];
-    int shift[8], srcc[8];
+    uint32_t shift[8];
+    const uint16_t *xe[8];
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
         const int c = 8 * j + e;
         const bool hi = s_is_src[c];
         const int owner = s_src_of[c];
         const bool lo = !hi && owner >= 0;
-        srcc[e] = lo ? owner : c;
-        scl[e] = s_scale[srcc[e]];
+        const int srcc = lo ? owner : c;
+        scl[e] = s_scale[srcc];
         rscl[e] = __builtin_amdgcn_rcpf(scl[e]);
         lim[e] = (hi || lo) ? 127.0f : 7.0f;
         // q + lim + 1 lands in the low mantissa bits of 1.5 * 2^23 + (lim + 1)
         bias[e] = 12582912.0f + lim[e] + 1.0f;
-        shift[e] = hi ? 4 : 0;
+        shift[e] = hi ? 4u : 0u;
+        xe[e] = &s_x[0][0] + (8 * wave + tq) * ROWLEN + srcc;
+        asm volatile("" : "+v"(scl[e]), "+v"(rscl[e]), "+v"(lim[e]), "+v"(bias[e]), "+v"(shift[e]));
     }
     uint32_t *out = (uint32_t *)(a.payload + row * (int64_t)T * (TILE_D / 2));
     stream([&](int ch) {
@@ -523,33 +537,38 @@ __global__ __launch_bounds__(K4_THREADS, 4) void k4_encode_tile(K4Args a)
         for (int it = 0; it < 2; ++it) {
             const int tl = 8 * wave + 4 * it + tq, t = t0 + tl;
             if (t < T) {
-                const uint16_t *xt = buf_of(ch) + tl * ROWLEN;
-                // branch-free: every channel reads the value it encodes (its
-                // own, or for a donor slot its source's); the reciprocal
-                // quotient decides the rounding unless it is within 2^-12 of
-                // a half-integer, where the exact quotient decides.  Below
-                // |q| = 256 the reciprocal's error is under 2^-14; beyond
-                // it every code clamps to +-lim either way.
-                float v[8], q[8];
-                bool near = false;
+                const int off = (DMA ? ch % NBUF : ch & 1) * CH * ROWLEN + 4 * it * ROWLEN;
+                // The reciprocal quotient f decides the rounding unless it is
+                // within 2^-13 of a half-integer, where the IEEE quotient
+                // decides.  Below |f| = 256, f is within 2^-14 of the IEEE
+                // quotient (v_rcp_f32 is within 1 ulp, plus the product's
+                // rounding, plus the quotient's own half ulp), so no rounding
+                // can differ outside that band; beyond it every code clamps to
+                // +-lim either way.  The band test is one max over the lane's
+                // eight distances; the rare lanes inside it redo only the
+                // slots that are.
+                float v[8], f[8], q[8];
 #pragma unroll
-                for (int e = 0; e < 8; ++e) v[e] = tile_f32<F16IN>(xt[srcc[e]]);
+                for (int e = 0; e < 8; ++e) v[e] = tile_f32<F16IN>(xe[e][off]);
+                float dmax = 0.0f;
 #pragma unroll
                 for (int e = 0; e < 8; ++e) {
-                    const float f = __fmul_rn(v[e], rscl[e]);
-                    q[e] = rintf(f);
-                    near |= fabsf(__fsub_rn(f, q[e])) >= 0.5f - 0x1p-12f;
+                    f[e] = __fmul_rn(v[e], rscl[e]);
+                    q[e] = rintf(f[e]);
+                    dmax = fmaxf(dmax, fabsf(__fsub_rn(f[e], q[e])));
                 }
-                if (near) {
+                constexpr float band = 0.5f - 0x1p-13f;
+                if (__builtin_expect(dmax >= band, 0)) {
 #pragma unroll
-                    for (int e = 0; e < 8; ++e) q[e] = iq_rint_div(v[e], scl[e], rscl[e]);
+                    for (int e = 0; e < 8; ++e)
+                        if (fabsf(__fsub_rn(f[e], q[e])) >= band) q[e] = rintf(v[e] / scl[e]);
                 }
                 uint32_t word = 0;
 #pragma unroll
                 for (int e = 0; e < 8; ++e) {
                     const float qc = __builtin_amdgcn_fmed3f(q[e], -lim[e], lim[e]);
                     const uint32_t code = __float_as_uint(__fadd_rn(qc, bias[e]));
-                    word |= ((code >> shift[e]) & 15u) << (4 * e);
+                    word |= __builtin_amdgcn_ubfe(code, shift[e], 4) << (4 * e);
                 }
                 out[t * (TILE_D / 8) + j] = word;
             }

@@ -22,7 +22,7 @@ except ImportError:  # codec/cache use does not need transformers
     class _HFCache:
         pass
 
-from .codec import CodecConfig, PackedTensor, quantize
+from .codec import _BAD_K, CodecConfig, PackedTensor, quantize
 
 
 @dataclass(frozen=True)
@@ -86,19 +86,20 @@ def _tensor_bytes(t: torch.Tensor | None) -> int:
 
 
 def _quantize_temporal_blocks(tensor: torch.Tensor, block_count: int, block_size: int,
-                              config: CodecConfig) -> list[PackedTensor]:
+                              config: CodecConfig, bad: torch.Tensor | None = None) -> list[PackedTensor]:
     """Encode `block_count` leading blocks of [1, H, T, D] in one launch, one owned PackedTensor each.
 
     The blocked [nb, H, B, D] view is read in place by the kernel (no copy);
-    statistics stay per (block, head).
+    statistics stay per (block, head).  With `bad` given, the non-finite flag
+    goes to bad[0] and is left for the caller to check.
     """
     if block_count == 0:
         return []
     if block_count == 1:
-        return [quantize(tensor[:, :, :block_size], config)]
+        return [quantize(tensor[:, :, :block_size], config, _flag=bad)]
     _, heads, _, channels = tensor.shape
     blocked = tensor[0, :, :block_count * block_size].reshape(heads, block_count, block_size, channels).permute(1, 0, 2, 3)
-    packed = quantize(blocked, config)
+    packed = quantize(blocked, config, _flag=bad)
     shape = (1, heads, block_size, channels)
     return [PackedTensor(**{name: t[i:i + 1].clone(memory_format=torch.contiguous_format)
                             for name, t in packed.tensors.items()},
@@ -206,8 +207,13 @@ class InQuantCache(_HFCache):
                 raise ValueError("cache_position must be a 1D integer tensor with one position per new token")
             if self.config.validate_positions:
                 # compared on the host: one copy instead of two kernels and a reduction
-                expected = torch.arange(old_length, old_length + key_states.shape[2], dtype=position.dtype)
-                if not torch.equal(position.cpu(), expected):
+                host = position.cpu()
+                if host.numel() == 1:
+                    ok = int(host[0]) == old_length
+                else:
+                    ok = torch.equal(host, torch.arange(old_length, old_length + key_states.shape[2],
+                                                        dtype=position.dtype))
+                if not ok:
                     raise ValueError("Only contiguous append positions are supported; reset before a new request")
         return layer
 
@@ -253,13 +259,28 @@ class InQuantCache(_HFCache):
             pending_key = torch.cat((layer.residual_key, pending_key), dim=2)
             pending_value = torch.cat((layer.residual_value, pending_value), dim=2)
         blocks = max(0, (pending_key.shape[2] - cfg.residual_length) // cfg.block_size)
-        new_keys = _quantize_temporal_blocks(pending_key, blocks, cfg.block_size, cfg.codec)
+        # Both encoders raise their non-finite flag into one buffer that is
+        # read with a single device sync; the reference syncs once per
+        # encoder (codec.py:197, value_codec.py:64).  The key error wins, as
+        # the reference raises it before encoding the values.
+        flags = torch.zeros(2, dtype=torch.int32, device=keys.device) if blocks else None
+        new_keys = _quantize_temporal_blocks(pending_key, blocks, cfg.block_size, cfg.codec,
+                                             flags[0:1] if blocks else None)
         if cfg.value_bits is None:
-            new_values = _quantize_temporal_blocks(pending_value, blocks, cfg.block_size, cfg.codec)
+            new_values = _quantize_temporal_blocks(pending_value, blocks, cfg.block_size, cfg.codec,
+                                                   flags[1:2] if blocks else None)
+            bad_v = _BAD_K
         else:
-            from .value_codec import quantize_value_blocks
-            new_values = quantize_value_blocks(pending_value, blocks, cfg.block_size, cfg.value_bits,
-                                               cfg.value_group_size)
+            from .value_codec import _BAD_V, _value_blocks
+            new_values = _value_blocks(pending_value, blocks, cfg.block_size, cfg.value_bits,
+                                       cfg.value_group_size, flags[1:2] if blocks else None)
+            bad_v = _BAD_V
+        if blocks:
+            bad_k_set, bad_v_set = flags.tolist()
+            if bad_k_set:
+                raise ValueError(_BAD_K)
+            if bad_v_set:
+                raise ValueError(bad_v)
         offset = blocks * cfg.block_size
         if fresh and offset == 0:
             # nothing sealed: the concatenation is already an owned tensor

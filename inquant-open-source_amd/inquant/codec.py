@@ -144,14 +144,23 @@ def _check_bad_flag(flag: torch.Tensor, message: str) -> None:
         raise ValueError(message)
 
 
+_BAD_K = "x must contain finite values representable in float32"
+
+
 @torch.no_grad()
-def quantize(x: torch.Tensor, config: CodecConfig = CodecConfig()) -> PackedTensor:
+def quantize(x: torch.Tensor, config: CodecConfig = CodecConfig(), *,
+             _flag: torch.Tensor | None = None) -> PackedTensor:
     """Pack one [batch, heads, tokens, even_head_dim] tensor (codec.py:181-243).
 
     floor(head_dim * salient_fraction) channels get 8-bit codes; as many
     low-saliency channels donate their slot and decode to their sampled mean.
-    Raises ValueError for empty, non-floating, odd-width or non-finite input.
+    Raises ValueError for empty, non-floating, odd-width or non-finite input;
+    the non-finite check costs one device sync (as the reference's finite
+    check at codec.py:197).  With the private `_flag` (a one-element int32
+    device tensor) the kernel raises the flag there instead and the caller
+    checks it, so that a caller encoding several tensors syncs once.
     """
+    bad = _flag
     if x.ndim != 4 or any(size < 1 for size in x.shape):
         raise ValueError("x must have nonempty [batch, heads, tokens, channels] dimensions")
     if not x.is_floating_point():
@@ -173,11 +182,14 @@ def quantize(x: torch.Tensor, config: CodecConfig = CodecConfig()) -> PackedTens
     src = torch.empty((B, H, count), dtype=desc_dtype, device=device)
     don = torch.empty((B, H, count), dtype=desc_dtype, device=device)
     padding = torch.empty((B, H, count), dtype=torch.float32, device=device)
-    bad = torch.zeros(1, dtype=torch.int32, device=device)
+    own_flag = bad is None
+    if own_flag:
+        bad = torch.zeros(1, dtype=torch.int32, device=device)
     nat.check(nat.lib().iq_k4_quantize(
         x.data_ptr(), nat.dtype_code(x.dtype), nat.strides4(x), B, H, T, D, count, config.sample_stride,
         int(config.donor_policy == "min_error"), payload.data_ptr(), scales.data_ptr(),
         src.data_ptr() if count else None, don.data_ptr() if count else None, src.element_size(),
         padding.data_ptr() if count else None, bad.data_ptr(), nat.stream_handle(device)))
-    _check_bad_flag(bad, "x must contain finite values representable in float32")
+    if own_flag:
+        _check_bad_flag(bad, _BAD_K)
     return PackedTensor(payload, scales, src, don, padding, tuple(x.shape), original_dtype)

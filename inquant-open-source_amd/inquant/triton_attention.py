@@ -106,14 +106,18 @@ class PackedDecodeState:
         self._kv_heads = first.shape[1]
         self._packed_tokens = first.shape[2]
         self._salient = first.salient_channels.shape[-1]
-        for block in key_blocks:
+        # The prefix was validated against the same first block by an earlier
+        # call and is identical (checked above), so only the new suffix is
+        # checked; the reference re-checks every block on every append
+        # (triton_attention.py:257-269), which costs O(blocks) host time per seal.
+        for block in key_blocks[old:]:
             if (not isinstance(block, PackedTensor) or block.shape != first.shape
                     or block.salient_channels.shape[-1] != self._salient):
                 raise ValueError("All packed K/V blocks must share shape and salient-channel count")
         v0 = value_blocks[0]
         self._value_bits = v0.bits if isinstance(v0, PackedValues) else 0
         self._value_group = v0.group_size if self._value_bits else 64
-        for block in value_blocks:
+        for block in value_blocks[old:]:
             if block.shape != first.shape:
                 raise ValueError("All packed blocks must share shape")
             if self._value_bits:
@@ -122,7 +126,7 @@ class PackedDecodeState:
                     raise ValueError("All V blocks must share the same quantizer")
             elif not isinstance(block, PackedTensor) or block.salient_channels.shape[-1] != self._salient:
                 raise ValueError("All InQuant V blocks must share the salient-channel count")
-        for block in (*key_blocks, *value_blocks):
+        for block in (*key_blocks[old:], *value_blocks[old:]):
             if any(t.device != self._device for t in block.tensors.values()):
                 raise ValueError("All packed tensors must share the same CUDA device")
         if self._salient > 64:

@@ -57,8 +57,16 @@ class PackedValues:
         return out if out_dtype == dtype else out.to(dtype)
 
 
+_BAD_V = "Values and stored FP16 quantization parameters must be finite"
+
+
 @torch.no_grad()
-def quantize_values(x: torch.Tensor, bits: int = 2, group_size: int = 64) -> PackedValues:
+def quantize_values(x: torch.Tensor, bits: int = 2, group_size: int = 64, *,
+                    _flag: torch.Tensor | None = None) -> PackedValues:
+    """Group-wise V2/V4 codes (value_codec.py:51-72); ValueError for non-finite
+    data or parameters, checked with one device sync (value_codec.py:64)
+    unless the private `_flag` hands the check to the caller."""
+    bad = _flag
     if type(bits) is not int or bits not in (2, 4):
         raise ValueError("Value bits must be 2 or 4")
     if type(group_size) is not int or group_size not in (32, 64, 128):
@@ -74,25 +82,32 @@ def quantize_values(x: torch.Tensor, bits: int = 2, group_size: int = 64) -> Pac
     payload = torch.empty((B, H, T, D * bits // 8), dtype=torch.uint8, device=device)
     scales = torch.empty((B, H, T, D // group_size), dtype=torch.float16, device=device)
     offsets = torch.empty_like(scales)
-    bad = torch.zeros(1, dtype=torch.int32, device=device)
+    own_flag = bad is None
+    if own_flag:
+        bad = torch.zeros(1, dtype=torch.int32, device=device)
     nat.check(nat.lib().iq_v_quantize(
         x.data_ptr(), nat.dtype_code(x.dtype), nat.strides4(x), B, H, T, D, bits, group_size,
         payload.data_ptr(), scales.data_ptr(), offsets.data_ptr(), bad.data_ptr(), nat.stream_handle(device)))
-    if int(bad.item()):
-        raise ValueError("Values and stored FP16 quantization parameters must be finite")
+    if own_flag and int(bad.item()):
+        raise ValueError(_BAD_V)
     return PackedValues(payload, scales, offsets, tuple(x.shape), original_dtype, bits, group_size)
 
 
 def quantize_value_blocks(tensor: torch.Tensor, block_count: int, block_size: int, bits: int, group_size: int):
     """Encode `block_count` leading temporal blocks of [1, H, T, D] as separately owned PackedValues."""
+    return _value_blocks(tensor, block_count, block_size, bits, group_size, None)
+
+
+def _value_blocks(tensor, block_count, block_size, bits, group_size, bad):
+    """quantize_value_blocks with the private flag of quantize_values."""
     if not block_count:
         return []
     if block_count == 1:
-        return [quantize_values(tensor[:, :, :block_size], bits, group_size)]
+        return [quantize_values(tensor[:, :, :block_size], bits, group_size, _flag=bad)]
     _, heads, _, channels = tensor.shape
     # [nb, H, B, D] view of the first nb*B tokens; the kernel reads it in place
     blocked = tensor[0, :, :block_count * block_size].reshape(heads, block_count, block_size, channels).permute(1, 0, 2, 3)
-    packed = quantize_values(blocked, bits, group_size)
+    packed = quantize_values(blocked, bits, group_size, _flag=bad)
     out = []
     for i in range(block_count):
         fields = {name: t[i:i + 1].clone(memory_format=torch.contiguous_format)
