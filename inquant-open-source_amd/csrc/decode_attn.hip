@@ -11,7 +11,7 @@
 //
 // This file holds the general kernel (any query dtype, K4- or V2/V4-coded
 // values, G <= 16 query heads per KV head, VALU arithmetic).
-#include "iq_common.h"
+#include "decode_common.h"
 
 namespace {
 
@@ -220,92 +220,91 @@ __global__ __launch_bounds__(DA_THREADS) void decode_partials_generic(DecodeArgs
 }
 
 // Log-sum-exp merge of the partition partials (_reduce_partials, triton_attention.py:168-181).
-// grid (Hq, D / 32): each workgroup merges 32 output channels of one query
-// head; its 512 threads split the partitions 16 ways per channel, so up to
-// 256 partitions (64K packed tokens) merge in one round of loads.
+// grid (Hq, D / 16): each workgroup merges 16 output channels of one query
+// head.  Thread (column c4 = tid % 4, lane of partitions part = tid / 4)
+// owns channels 4 c4 .. 4 c4 + 3 and every 64th partition from `part`; a
+// partition costs it three 8-byte loads (two for its four channels, one for
+// (m, l)), all of a round issued before any arithmetic.  Partial rows are
+// 130 floats, so only 8-byte alignment holds.  The 64 running states of a
+// column then merge: the maximum and the rescaled sums over the 16 lanes of
+// a wavefront by shuffles, then over the four wavefronts through LDS.
 constexpr int RED_THREADS = 256;
-constexpr int RED_COLS = 16;
-constexpr int RED_PARTS = RED_THREADS / RED_COLS;
-
-// Each thread merges every 16th partition of one channel: all loads of a
-// round of 16 partitions are issued before any dependent arithmetic.  The 16
-// running (max, weighted sum, normalizer) states of a channel then merge in
-// two steps: the workgroup max (lane shuffles, then LDS across the four
-// wavefronts), and a sum of the states rescaled to it.
-constexpr int RED_BATCH = 16;
+constexpr int RED_C4 = 4;                          // four-channel columns per workgroup
+constexpr int RED_PARTS = RED_THREADS / RED_C4;    // partition lanes
+constexpr int RED_BATCH = 4;                       // partitions per thread per round (256 partitions)
 
 __global__ __launch_bounds__(RED_THREADS) void decode_reduce(const float *ws, int64_t P, void *out, int odt)
 {
-    __shared__ float s_m[RED_THREADS / 64][RED_COLS], s_n[RED_THREADS / 64][RED_COLS],
-        s_l[RED_THREADS / 64][RED_COLS];
+    __shared__ float s_m[RED_THREADS / 64][RED_C4], s_l[RED_THREADS / 64][RED_C4];
+    __shared__ f32x4 s_n[RED_THREADS / 64][RED_C4];
     const int64_t hq = blockIdx.x;
-    const int c0 = blockIdx.y * RED_COLS;
-    const int tid = threadIdx.x, c = tid % RED_COLS, part = tid / RED_COLS, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x, c4 = tid % RED_C4, part = tid / RED_C4, wave = tid >> 6;
+    const int c0 = blockIdx.y * (4 * RED_C4) + 4 * c4;
     const float *base = ws + hq * P * (D + 2);
     const float ninf = -__uint_as_float(0x7f800000u);
-    float m = ninf, num = 0.0f, den = 0.0f;
+    float m = ninf, den = 0.0f;
+    f32x4 num = {0.0f, 0.0f, 0.0f, 0.0f};
     for (int p0 = part; p0 < (int)P; p0 += RED_PARTS * RED_BATCH) {
-        // every load of the round first (clamped rows, 32-bit offsets), the
-        // masks after: a load consumed under a condition right away would be
-        // waited for one at a time
-        float mv[RED_BATCH], lv[RED_BATCH], av[RED_BATCH];
+        f32x2 a0[RED_BATCH], a1[RED_BATCH], ml[RED_BATCH];
 #pragma unroll
         for (int k = 0; k < RED_BATCH; ++k) {
             const int pp = min(p0 + RED_PARTS * k, (int)P - 1);
-            const float *r = base + pp * (D + 2);
-            mv[k] = r[D];
-            lv[k] = r[D + 1];
-            av[k] = r[c0 + c];
-        }
-#pragma unroll
-        for (int k = 0; k < RED_BATCH; ++k) {
-            const bool ok = p0 + RED_PARTS * k < (int)P;
-            mv[k] = ok ? mv[k] : ninf;
-            lv[k] = ok ? lv[k] : 0.0f;
-            av[k] = ok ? av[k] : 0.0f;
+            const float *r = base + (int64_t)pp * (D + 2);
+            a0[k] = *(const f32x2 *)(r + c0);
+            a1[k] = *(const f32x2 *)(r + c0 + 2);
+            ml[k] = *(const f32x2 *)(r + D);
         }
         float mm = m;
 #pragma unroll
-        for (int k = 0; k < RED_BATCH; ++k) mm = fmaxf(mm, mv[k]);
+        for (int k = 0; k < RED_BATCH; ++k) {
+            if (p0 + RED_PARTS * k >= (int)P) ml[k] = f32x2{ninf, 0.0f};
+            mm = fmaxf(mm, ml[k].x);
+        }
         if (mm == ninf) continue;
         const float wo = m == ninf ? 0.0f : __expf(m - mm);
         num *= wo;
         den *= wo;
 #pragma unroll
         for (int k = 0; k < RED_BATCH; ++k) {
-            const float w = mv[k] == ninf ? 0.0f : __expf(mv[k] - mm);
-            num = fmaf(av[k], w, num);
-            den = fmaf(lv[k], w, den);
+            const float w = ml[k].x == ninf ? 0.0f : __expf(ml[k].x - mm);
+            num += f32x4{a0[k].x, a0[k].y, a1[k].x, a1[k].y} * w;
+            den = fmaf(ml[k].y, w, den);
         }
         m = mm;
     }
-    // lanes c, c + 16, c + 32, c + 48 of a wavefront hold four parts of channel c
-    float mw = fmaxf(m, __shfl_xor(m, 16, 64));
-    mw = fmaxf(mw, __shfl_xor(mw, 32, 64));
-    if (lane < RED_COLS) s_m[wave][c] = mw;
-    __syncthreads();
-    float mm = s_m[0][c];
+    // lanes with equal tid % 4 of a wavefront hold 16 partition lanes of one column
+    float mw = m;
 #pragma unroll
-    for (int w = 1; w < RED_THREADS / 64; ++w) mm = fmaxf(mm, s_m[w][c]);
-    const float wt = m == ninf ? 0.0f : __expf(m - mm);
-    float n = num * wt, d = den * wt;
-    n += __shfl_xor(n, 16, 64);
-    d += __shfl_xor(d, 16, 64);
-    n += __shfl_xor(n, 32, 64);
-    d += __shfl_xor(d, 32, 64);
-    if (lane < RED_COLS) {
-        s_n[wave][c] = n;
-        s_l[wave][c] = d;
+    for (int sh = RED_C4; sh < 64; sh <<= 1) mw = fmaxf(mw, __shfl_xor(mw, sh, 64));
+    const float wt = m == ninf ? 0.0f : __expf(m - mw);
+    num *= wt;
+    den *= wt;
+#pragma unroll
+    for (int sh = RED_C4; sh < 64; sh <<= 1) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) num[e] += __shfl_xor(num[e], sh, 64);
+        den += __shfl_xor(den, sh, 64);
+    }
+    if ((tid & 63) < RED_C4) {
+        s_m[wave][c4] = mw;
+        s_l[wave][c4] = den;
+        s_n[wave][c4] = num;
     }
     __syncthreads();
-    if (tid < RED_COLS) {
-        float nn = s_n[0][c], dd = s_l[0][c];
+    if (tid < RED_C4) {
+        float M = s_m[0][c4];
 #pragma unroll
-        for (int w = 1; w < RED_THREADS / 64; ++w) {
-            nn += s_n[w][c];
-            dd += s_l[w][c];
+        for (int w = 1; w < RED_THREADS / 64; ++w) M = fmaxf(M, s_m[w][c4]);
+        f32x4 nn = {0.0f, 0.0f, 0.0f, 0.0f};
+        float dd = 0.0f;
+#pragma unroll
+        for (int w = 0; w < RED_THREADS / 64; ++w) {
+            const float x = s_m[w][c4] == ninf ? 0.0f : __expf(s_m[w][c4] - M);
+            nn += s_n[w][c4] * x;
+            dd = fmaf(s_l[w][c4], x, dd);
         }
-        iq_store_as(out, hq * D + c0 + c, nn / dd, odt);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) iq_store_as(out, hq * D + c0 + e, nn[e] / dd, odt);
     }
 }
 
@@ -383,7 +382,7 @@ extern "C" int iq_decode_attention(const void *q, int q_dtype, int64_t q_stride_
                            (hipStream_t)stream, a);
         IQ_CHECK_LAUNCH("decode_partials_generic");
     }
-    hipLaunchKernelGGL(decode_reduce, dim3((unsigned)Hq, D / RED_COLS), dim3(RED_THREADS), 0, (hipStream_t)stream,
+    hipLaunchKernelGGL(decode_reduce, dim3((unsigned)Hq, D / (4 * RED_C4)), dim3(RED_THREADS), 0, (hipStream_t)stream,
                        workspace, parts, out, out_dtype);
     IQ_CHECK_LAUNCH("decode_reduce");
     return IQ_OK;

@@ -162,7 +162,11 @@ __device__ __forceinline__ void fast_body(const FastArgs &a, FastSmem &sm)
     if (packed) {
         // the whole pointer-table row in one round trip (64 bytes, the same
         // for every lane), its pointers moved to scalar registers
-        const int64_t *rv = a.tables + p * IQ_TABLE_COLS;
+        // scalar loads (the row is the same for every lane): one 64-byte
+        // s_load through the scalar cache; the table was written by an
+        // earlier launch, so the kernel-start cache invalidation covers it
+        const __attribute__((address_space(4))) int64_t *rv =
+            (const __attribute__((address_space(4))) int64_t *)(a.tables + p * IQ_TABLE_COLS);
         int64_t tr[8];
 #pragma unroll
         for (int k = 0; k < 8; ++k) tr[k] = rv[k];
