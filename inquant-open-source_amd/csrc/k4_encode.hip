@@ -383,6 +383,9 @@ __global__ __launch_bounds__(K4_THREADS, 4) void k4_encode_tile(K4Args a)
     // neighbouring blocks, so that the blocks sharing a compute unit spread
     // the fp64 chains over all four SIMDs instead of stacking them on two.
     const bool welford = ((tid >> 7) ^ (int)(((blockIdx.x + gridDim.x * blockIdx.y) >> 8) & 1)) == 0;
+    // The Welford chains are the critical path of pass 1 (the sums waves
+    // then wait at every chunk barrier), so their waves issue first.
+    if (welford && a.min_error) __builtin_amdgcn_s_setprio(2);
     double mean = 0.0, m2 = 0.0;                  // Welford waves
     IqCascade sa, sm;                             // sums waves
     sa.init(ns);
@@ -482,8 +485,12 @@ __global__ __launch_bounds__(K4_THREADS, 4) void k4_encode_tile(K4Args a)
     }
     __syncthreads();
 
+    // the sequential donor picks on wave 0 hold up the whole block: top priority
+    if (wave == 0) __builtin_amdgcn_s_setprio(3);
+    else __builtin_amdgcn_s_setprio(0);
     iq_select_tile128(s_sal, a.min_error ? s_err : nullptr, (int)a.count, s_src, s_don, s_is_src, s_src_of,
                       s_key, s_part, s_flag, s_list);
+    __builtin_amdgcn_s_setprio(1);
     __syncthreads();
 
     const float flt_min = 1.17549435e-38f;
