@@ -232,3 +232,33 @@ def test_cfg2_full_context_matches_oracle_and_is_repeatable():
     for o in outs[1:]:
         assert np.array_equal(o, outs[0])            # the merge order is fixed
     np.testing.assert_allclose(outs[0], case.expected(), atol=ATOL, rtol=0)
+
+
+def test_extend_checks_every_appended_block_and_keeps_the_state_on_error():
+    # triton_attention.py:257-269: every appended block must match the first
+    # block's shape, salient count and value quantizer; a rejected extend
+    # leaves the state as it was
+    from inquant.codec import CodecConfig, quantize
+    from inquant.value_codec import quantize_values
+    from inquant.triton_attention import PackedDecodeState
+    torch.manual_seed(832)
+    mk = lambda t=32: torch.randn(1, 2, t, 128, device="cuda", dtype=torch.bfloat16)
+    keys = [quantize(mk()) for _ in range(3)]
+    values = [quantize_values(mk()) for _ in range(3)]
+    q = torch.randn(1, 8, 1, 128, device="cuda", dtype=torch.bfloat16)
+    state = PackedDecodeState(keys[:2], values[:2])
+    ref = state.decode(q).clone()
+    cases = [
+        (keys[:2] + [quantize(mk(16))], values, "shape"),
+        (keys[:2] + [quantize(mk(), CodecConfig(salient_fraction=0.25))], values, "salient-channel"),
+        (keys, values[:2] + [quantize_values(mk(), bits=4)], "same quantizer"),
+        (keys, values[:2] + [quantize(mk())], "same quantizer"),
+        (keys[:2] + [values[2]], values, "shape and salient-channel"),
+    ]
+    for ks, vs, msg in cases:
+        with pytest.raises(ValueError, match=msg):
+            state.extend(ks, vs)
+        assert state.key_blocks == tuple(keys[:2]) and state.value_blocks == tuple(values[:2])
+        assert torch.equal(state.decode(q), ref)
+    state.extend(keys, values)
+    assert torch.equal(state.decode(q), PackedDecodeState(keys, values).decode(q))

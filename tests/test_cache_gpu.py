@@ -229,3 +229,44 @@ def test_k4v2_append_semantics_and_owned_bytes_across_seal_boundary():
     stats = a.memory_stats()
     assert stats["nbytes"] == sum(stats[key] for key in ("payload_nbytes", "metadata_nbytes", "sink_nbytes",
                                                          "residual_nbytes", "auxiliary_nbytes"))
+
+
+@pytest.mark.parametrize("value_bits", [None, 2])
+def test_seal_nonfinite_raises_the_encoders_error_and_leaves_the_layer(value_bits):
+    # codec.py:197 and value_codec.py:64 raise before anything is stored; the
+    # cache reads both encoders' flags with one sync, the key error first
+    from inquant.cache import InQuantCache
+    cfg = _cfg(value_bits=value_bits, value_group_size=32) if value_bits else _cfg()
+    cache = InQuantCache(cfg)
+    key, value = _randn(1, 2, 5, 64, seed=30), _randn(1, 2, 5, 64, seed=31)
+    cache.update(key, value, 0)
+    before = (cache.get_seq_length(), len(cache._layers[0].key_blocks), cache.nbytes)
+    v_msg = "FP16 quantization parameters" if value_bits else "finite values"
+    for bad_k, bad_v, msg in ((True, False, "finite values"), (False, True, v_msg), (True, True, "finite values")):
+        k, v = _randn(1, 2, 16, 64, seed=32), _randn(1, 2, 16, 64, seed=33)
+        if bad_k:
+            k[0, 1, 3, 7] = float("nan")
+        if bad_v:
+            v[0, 0, 9, 40] = float("inf")
+        with pytest.raises(ValueError, match=msg):
+            cache.update(k, v, 0)
+        assert (cache.get_seq_length(), len(cache._layers[0].key_blocks), cache.nbytes) == before
+    # a clean append after the failures seals normally
+    cache.update(_randn(1, 2, 16, 64, seed=34), _randn(1, 2, 16, 64, seed=35), 0)
+    assert len(cache._layers[0].key_blocks) == 2 and cache.get_seq_length() == 21
+
+
+def test_single_token_position_check():
+    # test_cache.py:110-134: a wrong one-token position raises and changes nothing
+    from inquant.cache import InQuantCache
+    cache = InQuantCache(_cfg())
+    x = _randn(1, 2, 6, 8, seed=36)
+    cache.update(x, x, 0, {"cache_position": torch.arange(6, device="cuda")})
+    t = x[:, :, :1]
+    for wrong in (5, 7, 0):
+        for dtype in (torch.int64, torch.int32):
+            with pytest.raises(ValueError, match="contiguous append positions"):
+                cache.append_for_attention(t, t, 0, {"cache_position": torch.tensor([wrong], dtype=dtype, device="cuda")})
+    assert cache.get_seq_length() == 6
+    cache.append_for_attention(t, t, 0, {"cache_position": torch.tensor([6], dtype=torch.int32, device="cuda")})
+    assert cache.get_seq_length() == 7
