@@ -160,8 +160,6 @@ __device__ __forceinline__ void fast_body(const FastArgs &a, FastSmem &sm)
         }                                                                                             \
     } while (0)
     if (packed) {
-        // the whole pointer-table row in one round trip (64 bytes, the same
-        // for every lane), its pointers moved to scalar registers
         // scalar loads (the row is the same for every lane): one 64-byte
         // s_load through the scalar cache; the table was written by an
         // earlier launch, so the kernel-start cache invalidation covers it
