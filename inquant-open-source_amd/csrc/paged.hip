@@ -665,70 +665,83 @@ __global__ __launch_bounds__(256, 3) void decode_paged(PagedArgs a)
     else paged_body<NPG, false>(a, sm, geo, pid);
 }
 
-// grid (Hq, D / 16, seq): merges the partitions of one sequence; thread
-// (part, c) merges every 16th partition of channel c, then the 16 states of a
-// channel merge through lane shuffles and LDS (as decode_reduce).
+// grid (Hq, D / 16, seq): merges the partitions of one sequence for 16
+// channels of one query head; the 64 per-thread states of a four-channel
+// column then merge through lane shuffles and LDS (as decode_reduce).
 __global__ __launch_bounds__(256) void paged_reduce(PagedArgs a, void *out, int64_t out_ss, int odt)
 {
-    __shared__ float s_m[4][16], s_n[4][16], s_l[4][16];
-    const int hq = blockIdx.x, c0 = blockIdx.y * 16, sq = blockIdx.z;
-    const int tid = threadIdx.x, c = tid & 15, part = tid >> 4, lane = tid & 63, wave = tid >> 6;
+    // thread (column c4 of four channels, partition lane part): every 64th
+    // partition from `part`, three 8-byte loads each (partial rows are 130
+    // floats, so only 8-byte alignment holds), all of a round in flight
+    __shared__ float s_m[4][4], s_l[4][4];
+    __shared__ f32x4 s_n[4][4];
+    const int hq = blockIdx.x, sq = blockIdx.z;
+    const int tid = threadIdx.x, c4 = tid & 3, part = tid >> 2, wave = tid >> 6;
+    const int c0 = blockIdx.y * 16 + 4 * c4;
     const SeqGeom geo = seq_geom(a, sq);
     const int P = geo.npp + geo.ndp;
     const float *base = a.ws + ((int64_t)sq * a.H * a.G + hq) * a.max_parts * (D + 2);
-    float m = NEG_INF, num = 0.0f, den = 0.0f;
-    for (int p0 = part; p0 < P; p0 += 16 * 16) {
+    float m = NEG_INF, den = 0.0f;
+    f32x4 num = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int p0 = part; p0 < P; p0 += 64 * 4) {
         // every load of the round first, the masks after (see decode_reduce)
-        float mv[16], lv[16], av[16];
+        f32x2 a0[4], a1[4], ml[4];
 #pragma unroll
-        for (int k = 0; k < 16; ++k) {
-            const float *r = base + min(p0 + 16 * k, P - 1) * (D + 2);
-            mv[k] = r[D];
-            lv[k] = r[D + 1];
-            av[k] = r[c0 + c];
-        }
-#pragma unroll
-        for (int k = 0; k < 16; ++k) {
-            const bool ok = p0 + 16 * k < P;
-            mv[k] = ok ? mv[k] : NEG_INF;
-            lv[k] = ok ? lv[k] : 0.0f;
-            av[k] = ok ? av[k] : 0.0f;
+        for (int k = 0; k < 4; ++k) {
+            const float *r = base + min(p0 + 64 * k, P - 1) * (D + 2);
+            a0[k] = *(const f32x2 *)(r + c0);
+            a1[k] = *(const f32x2 *)(r + c0 + 2);
+            ml[k] = *(const f32x2 *)(r + D);
         }
         float mm = m;
 #pragma unroll
-        for (int k = 0; k < 16; ++k) mm = fmaxf(mm, mv[k]);
+        for (int k = 0; k < 4; ++k) {
+            if (p0 + 64 * k >= P) ml[k] = f32x2{NEG_INF, 0.0f};
+            mm = fmaxf(mm, ml[k].x);
+        }
         if (mm == NEG_INF) continue;
         const float wo = m == NEG_INF ? 0.0f : __expf(m - mm);
         num *= wo;
         den *= wo;
 #pragma unroll
-        for (int k = 0; k < 16; ++k) {
-            const float w = mv[k] == NEG_INF ? 0.0f : __expf(mv[k] - mm);
-            num = fmaf(av[k], w, num);
-            den = fmaf(lv[k], w, den);
+        for (int k = 0; k < 4; ++k) {
+            const float w = ml[k].x == NEG_INF ? 0.0f : __expf(ml[k].x - mm);
+            num += f32x4{a0[k].x, a0[k].y, a1[k].x, a1[k].y} * w;
+            den = fmaf(ml[k].y, w, den);
         }
         m = mm;
     }
-    float mw = fmaxf(m, __shfl_xor(m, 16, 64));
-    mw = fmaxf(mw, __shfl_xor(mw, 32, 64));
-    if (lane < 16) s_m[wave][c] = mw;
-    __syncthreads();
-    const float mm = fmaxf(fmaxf(s_m[0][c], s_m[1][c]), fmaxf(s_m[2][c], s_m[3][c]));
-    const float wt = m == NEG_INF ? 0.0f : __expf(m - mm);
-    float n = num * wt, d = den * wt;
-    n += __shfl_xor(n, 16, 64);
-    d += __shfl_xor(d, 16, 64);
-    n += __shfl_xor(n, 32, 64);
-    d += __shfl_xor(d, 32, 64);
-    if (lane < 16) {
-        s_n[wave][c] = n;
-        s_l[wave][c] = d;
+    // lanes with equal tid % 4 of a wavefront hold 16 partition lanes of one column
+    float mw = m;
+#pragma unroll
+    for (int sh = 4; sh < 64; sh <<= 1) mw = fmaxf(mw, __shfl_xor(mw, sh, 64));
+    const float wt = m == NEG_INF ? 0.0f : __expf(m - mw);
+    num *= wt;
+    den *= wt;
+#pragma unroll
+    for (int sh = 4; sh < 64; sh <<= 1) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) num[e] += __shfl_xor(num[e], sh, 64);
+        den += __shfl_xor(den, sh, 64);
+    }
+    if ((tid & 63) < 4) {
+        s_m[wave][c4] = mw;
+        s_l[wave][c4] = den;
+        s_n[wave][c4] = num;
     }
     __syncthreads();
-    if (tid < 16) {
-        const float nn = s_n[0][c] + s_n[1][c] + s_n[2][c] + s_n[3][c];
-        const float dd = s_l[0][c] + s_l[1][c] + s_l[2][c] + s_l[3][c];
-        iq_store_as(out, sq * out_ss + (int64_t)hq * D + c0 + c, nn / dd, odt);
+    if (tid < 4) {
+        float M = fmaxf(fmaxf(s_m[0][c4], s_m[1][c4]), fmaxf(s_m[2][c4], s_m[3][c4]));
+        f32x4 nn = {0.0f, 0.0f, 0.0f, 0.0f};
+        float dd = 0.0f;
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+            const float x = s_m[w][c4] == NEG_INF ? 0.0f : __expf(s_m[w][c4] - M);
+            nn += s_n[w][c4] * x;
+            dd = fmaf(s_l[w][c4], x, dd);
+        }
+#pragma unroll
+        for (int e = 0; e < 4; ++e) iq_store_as(out, sq * out_ss + (int64_t)hq * D + c0 + e, nn[e] / dd, odt);
     }
 }
 
