@@ -220,8 +220,8 @@ __global__ __launch_bounds__(DA_THREADS) void decode_partials_generic(DecodeArgs
 }
 
 // Log-sum-exp merge of the partition partials (_reduce_partials, triton_attention.py:168-181).
-// grid (Hq, D / 16): each workgroup merges 16 output channels of one query
-// head.  Thread (column c4 = tid % 4, lane of partitions part = tid / 4)
+// 1-D grid of 64 * ceil(Hq / 8): each workgroup merges 16 output channels
+// of one query head, the eight channel slices of a head on one XCD.  Thread (column c4 = tid % 4, lane of partitions part = tid / 4)
 // owns channels 4 c4 .. 4 c4 + 3 and every 64th partition from `part`; a
 // partition costs it three 8-byte loads (two for its four channels, one for
 // (m, l)), all of a round issued before any arithmetic.  Partial rows are
@@ -233,13 +233,16 @@ constexpr int RED_C4 = 4;                          // four-channel columns per w
 constexpr int RED_PARTS = RED_THREADS / RED_C4;    // partition lanes
 constexpr int RED_BATCH = 4;                       // partitions per thread per round (256 partitions)
 
-__global__ __launch_bounds__(RED_THREADS) void decode_reduce(const float *ws, int64_t P, void *out, int odt)
+__global__ __launch_bounds__(RED_THREADS) void decode_reduce(const float *ws, int64_t P, int Hq, void *out, int odt)
 {
     __shared__ float s_m[RED_THREADS / 64][RED_C4], s_l[RED_THREADS / 64][RED_C4];
     __shared__ f32x4 s_n[RED_THREADS / 64][RED_C4];
-    const int64_t hq = blockIdx.x;
+    int item, slice;
+    iq_xcd_item_slice((int)blockIdx.x, item, slice);    // the 8 channel slices of a head on one XCD
+    if (item >= Hq) return;
+    const int64_t hq = item;
     const int tid = threadIdx.x, c4 = tid % RED_C4, part = tid / RED_C4, wave = tid >> 6;
-    const int c0 = blockIdx.y * (4 * RED_C4) + 4 * c4;
+    const int c0 = slice * (4 * RED_C4) + 4 * c4;
     const float *base = ws + hq * P * (D + 2);
     const float ninf = -__uint_as_float(0x7f800000u);
     float m = ninf, den = 0.0f;
@@ -382,8 +385,9 @@ extern "C" int iq_decode_attention(const void *q, int q_dtype, int64_t q_stride_
                            (hipStream_t)stream, a);
         IQ_CHECK_LAUNCH("decode_partials_generic");
     }
-    hipLaunchKernelGGL(decode_reduce, dim3((unsigned)Hq, D / (4 * RED_C4)), dim3(RED_THREADS), 0, (hipStream_t)stream,
-                       workspace, parts, out, out_dtype);
+    static_assert(D / (4 * RED_C4) == 8, "eight channel slices per head");
+    hipLaunchKernelGGL(decode_reduce, dim3((unsigned)(64 * ((Hq + 7) / 8))), dim3(RED_THREADS), 0,
+                       (hipStream_t)stream, workspace, parts, (int)Hq, out, out_dtype);
     IQ_CHECK_LAUNCH("decode_reduce");
     return IQ_OK;
 }

@@ -116,4 +116,16 @@ __device__ __forceinline__ T ldnt(const void *p)
 
 constexpr float NEG_INF = -__builtin_inff();
 
+// Workgroups go to the eight XCDs round-robin by linear id, and each XCD has
+// its own L2.  For a 1-D grid of 64 * ceil(n / 8) workgroups this maps the
+// linear id i to (item, slice) so that the eight slices of an item run on one
+// XCD: a row the eight slices all read then misses one L2, not several.
+// Items >= n are surplus workgroups that return at once.
+__device__ __forceinline__ void iq_xcd_item_slice(int i, int &item, int &slice)
+{
+    const int r = i & 7, k = i >> 3;
+    slice = k & 7;
+    item = ((k >> 3) << 3) | r;
+}
+
 }  // namespace

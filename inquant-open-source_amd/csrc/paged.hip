@@ -665,8 +665,9 @@ __global__ __launch_bounds__(256, 3) void decode_paged(PagedArgs a)
     else paged_body<NPG, false>(a, sm, geo, pid);
 }
 
-// grid (Hq, D / 16, seq): merges the partitions of one sequence for 16
-// channels of one query head; the 64 per-thread states of a four-channel
+// grid (64 * ceil(Hq / 8), 1, seq): merges the partitions of one sequence
+// for 16 channels of one query head (the eight channel slices of a head on
+// one XCD); the 64 per-thread states of a four-channel
 // column then merge through lane shuffles and LDS (as decode_reduce).
 __global__ __launch_bounds__(256) void paged_reduce(PagedArgs a, void *out, int64_t out_ss, int odt)
 {
@@ -675,9 +676,12 @@ __global__ __launch_bounds__(256) void paged_reduce(PagedArgs a, void *out, int6
     // floats, so only 8-byte alignment holds), all of a round in flight
     __shared__ float s_m[4][4], s_l[4][4];
     __shared__ f32x4 s_n[4][4];
-    const int hq = blockIdx.x, sq = blockIdx.z;
+    int hq, slice;
+    iq_xcd_item_slice((int)blockIdx.x, hq, slice);       // the 8 channel slices of a head on one XCD
+    if (hq >= a.H * a.G) return;
+    const int sq = blockIdx.z;
     const int tid = threadIdx.x, c4 = tid & 3, part = tid >> 2, wave = tid >> 6;
-    const int c0 = blockIdx.y * 16 + 4 * c4;
+    const int c0 = slice * 16 + 4 * c4;
     const SeqGeom geo = seq_geom(a, sq);
     const int P = geo.npp + geo.ndp;
     const float *base = a.ws + ((int64_t)sq * a.H * a.G + hq) * a.max_parts * (D + 2);
@@ -861,7 +865,7 @@ extern "C" int iq_paged_decode(const void *q, int64_t q_stride_seq, int64_t q_st
     default: hipLaunchKernelGGL(decode_paged<1>, grid, dim3(256), 0, st, a); break;
     }
     IQ_CHECK_LAUNCH("decode_paged");
-    hipLaunchKernelGGL(paged_reduce, dim3((unsigned)Hq, D / 16, (unsigned)n_seq), dim3(256), 0, st, a, out,
+    hipLaunchKernelGGL(paged_reduce, dim3((unsigned)(64 * ((Hq + 7) / 8)), 1, (unsigned)n_seq), dim3(256), 0, st, a, out,
                        out_stride_seq, out_dtype);
     IQ_CHECK_LAUNCH("paged_reduce");
     return IQ_OK;
