@@ -16,9 +16,12 @@
 //   * Normal channels decode with one fma per element: the fp8 converter maps
 //     a nibble byte n to n * 2^-9 exactly, so fma(v, s * 2^9, -8 s) is the
 //     single rounding of (n - 8) * s, as the reference's fp32 multiply.
-//   * Salient and donor channels are masked out of Q; an extra
-//     v_mfma_f32_16x16x16 over the gathered 8-bit codes adds the salient
-//     terms, and a per-block constant adds q . round(padding) for donors.
+//   * Salient and donor channels decode to zero in the 4-bit pass (zero
+//     constants); an extra v_mfma_f32_16x16x16 over the gathered 8-bit codes
+//     adds the salient terms, and a per-block constant adds
+//     q . round(padding) for donors.
+//   * LDS stays within 40 KiB (the query rows live in a V tile until every
+//     lane holds its operands), so four workgroups share a compute unit.
 //   * Online softmax in the log2 domain; P = hi + lo (two bf16/f16 terms) so
 //     the P.V product keeps ~16 significant bits of the weights.
 //   * V half-rows decode with the same fp8 trick into a 32-row LDS tile that
@@ -58,21 +61,23 @@ struct FastArgs {
 };
 
 // Workgroup LDS, shared by the packed and the dense instantiation of the body.
+// At most 40 KiB, so that four workgroups share a compute unit.
 struct __attribute__((aligned(16))) FastSmem {
     // per wavefront: staged decoded V as [token pair][channel] dwords (two
-    // tokens of one channel per dword); also K staging and the final combine
+    // tokens of one channel per dword); also K staging and the final combine.
+    // Until every lane holds its query operands, wave 0's tile holds the
+    // query rows (dtype bits, QROW halves per row, zero beyond G).
     uint32_t v[WAVES][16 * VR];
-    uint16_t q[16 * QROW];          // query rows (dtype bits), zero beyond G
-    uint16_t qm[16 * QROW];         // query rows masked at salient/donor channels
-    f32x2 kc[4 * KC_STRIDE];     // per channel (s * 2^9, -8 s)
+    f32x2 kc[4 * KC_STRIDE];     // per channel (s * 2^9, -8 s); (0, 0) at salient and donor channels
     int8_t role[D];
-    uint32_t sal[64];            // src | don << 8
     uint32_t salw[64];           // gather offsets: src byte, shift, don byte, shift
     f32x2 salf[64];              // (s_src, -128 s_src)
     uint16_t qsal[16 * 68];      // Q[g][src_k], zero beyond S (68: fewer bank collisions than 64)
     float dpad[64];              // padding of donor k, rounded to the query dtype
     float wm[WAVES][16], wl[WAVES][16];
 };
+static_assert(sizeof(FastSmem) <= 40 * 1024, "four workgroups per compute unit");
+static_assert(16 * QROW / 2 <= 16 * VR, "the query rows fit in one wave's tile");
 
 // One partition.  PACKED and dense partitions are separate instantiations so
 // that neither has a branch between its loads and their first use: a branch
@@ -85,11 +90,9 @@ __device__ __forceinline__ void fast_body(const FastArgs &a, FastSmem &sm)
     constexpr int VQW = VQ / 4;                  // dwords per quarter row
 
     uint32_t (&s_v)[WAVES][16 * VR] = sm.v;
-    uint16_t *const s_q = sm.q;
-    uint16_t *const s_qm = sm.qm;
+    uint16_t *const s_q = (uint16_t *)&sm.v[0][0];
     f32x2 *const s_kc = sm.kc;
     int8_t *const s_role = sm.role;
-    uint32_t *const s_sal = sm.sal;
     uint32_t *const s_salw = sm.salw;
     f32x2 *const s_salf = sm.salf;
     uint16_t *const s_qsal = sm.qsal;
@@ -209,58 +212,50 @@ __device__ __forceinline__ void fast_body(const FastArgs &a, FastSmem &sm)
     *(u32x4 *)(s_q + qg * QROW + qc) = qg < G ? qraw : u32x4{0u, 0u, 0u, 0u};
     if (packed) {
         if (tid < D) {
-            s_kc[(tid >> 5) * KC_STRIDE + (tid & 31)] = f32x2{kscale * inv_unit, -8.0f * kscale};
+            // salient and donor channels decode to zero in the 4-bit pass:
+            // their terms come from the 8-bit codes and the donor padding
+            s_kc[(tid >> 5) * KC_STRIDE + (tid & 31)] =
+                krole == 0xffu ? f32x2{kscale * inv_unit, -8.0f * kscale} : f32x2{0.0f, 0.0f};
             s_role[tid] = (int8_t)krole;
         }
         if (tid < S) {
-            s_sal[tid] = ksrc | (kdon << 8);
+            s_salw[tid] = (ksrc >> 1) | (((ksrc & 1) * 4) << 8) | ((kdon >> 1) << 16) | (((kdon & 1) * 4) << 24);
             s_dpad[tid] = round_q<F16>(kpad);
         }
     }
     __syncthreads();
 
     // ---------------- cooperative per-workgroup constants
-    {   // masked query rows: role != -1 (salient or donor) -> 0
-        u32x4 v = qg < G ? qraw : u32x4{0u, 0u, 0u, 0u};
-        if (packed) {
-            const uint32_t r0 = *(const uint32_t *)(s_role + qc), r1 = *(const uint32_t *)(s_role + qc + 4);
-#pragma unroll
-            for (int w = 0; w < 4; ++w) {
-                const uint32_t r2 = (w < 2 ? r0 : r1) >> (16 * (w & 1));
-                const uint32_t keep = ((r2 & 0xffu) == 0xffu ? 0x0000ffffu : 0u) |
-                                      (((r2 >> 8) & 0xffu) == 0xffu ? 0xffff0000u : 0u);
-                v[w] &= keep;
-            }
-        }
-        *(u32x4 *)(s_qm + qg * QROW + qc) = v;
-    }
-    if (tid < S) {
-        const uint32_t sd = s_sal[tid];
-        const uint32_t src = sd & 0xffu, don = sd >> 8;
-        const float m8 = s_kc[(src >> 5) * KC_STRIDE + (src & 31)].y;   // -8 s_src
-        s_salf[tid] = f32x2{-0.125f * m8, 16.0f * m8};                   // (s_src, -128 s_src), exact
-        s_salw[tid] = (src >> 1) | (((src & 1) * 4) << 8) | ((don >> 1) << 16) | (((don & 1) * 4) << 24);
-    }
+    // channel and descriptor index of salient slot k, from its gather word
+    auto sal_src = [&](uint32_t w) { return 2u * (w & 0xffu) + ((w >> 8) & 0xffu) / 4u; };
+    auto sal_don = [&](uint32_t w) { return 2u * ((w >> 16) & 0xffu) + (w >> 24) / 4u; };
     if constexpr (PACKED) {
+        // a source channel's descriptor index is -2 - role[its donor]
+        if (tid < D && krole < (uint32_t)D) {
+            const int k = -2 - (int)s_role[krole];
+            if (k >= 0 && k < S) s_salf[k] = f32x2{kscale, -128.0f * kscale};   // exact
+        }
         for (int i = tid; i < 16 * 16 * sal_groups; i += 256) {
             const int g = i / (16 * sal_groups), k = i % (16 * sal_groups);
-            s_qsal[g * 68 + k] = k < S ? s_q[g * QROW + (s_sal[k] & 0xffu)] : (uint16_t)0;
+            s_qsal[g * 68 + k] = k < S ? s_q[g * QROW + sal_src(s_salw[k])] : (uint16_t)0;
         }
     }
     __syncthreads();
 
     // ---------------- per-lane constants
-    u32x4 qb[4];                                   // B operand: Q[g = gl][32 ql + 8 d + e], masked
+    u32x4 qb[4];                                   // B operand: Q[g = gl][32 ql + 8 d + e]
 #pragma unroll
-    for (int d = 0; d < 4; ++d) qb[d] = *(const u32x4 *)(s_qm + gl * QROW + 32 * ql + 8 * d);
+    for (int d = 0; d < 4; ++d) qb[d] = *(const u32x4 *)(s_q + gl * QROW + 32 * ql + 8 * d);
     float bias = 0.0f;                             // sum_k q[gl][don_k] * round(pad_k)
     for (int grp = 0; grp < sal_groups; ++grp)
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
             const int k = 16 * grp + 4 * ql + e;
-            if (k < S) bias = fmaf(to_f32<F16>(s_q[gl * QROW + (s_sal[k] >> 8)]), s_dpad[k], bias);
+            if (k < S) bias = fmaf(to_f32<F16>(s_q[gl * QROW + sal_don(s_salw[k])]), s_dpad[k], bias);
         }
     bias = xsum16(bias);
+    // every lane holds its query operands: wave 0's tile may now be overwritten
+    __syncthreads();
 
     float m_run = NEG_INF, l_run = 0.0f;
     f32x4 acc[8];
@@ -552,7 +547,7 @@ __device__ __forceinline__ void fast_body(const FastArgs &a, FastSmem &sm)
 }
 
 template <bool F16, int VBITS>
-__global__ __launch_bounds__(256, 3) void decode_fast(FastArgs a)
+__global__ __launch_bounds__(256, 4) void decode_fast(FastArgs a)
 {
     __shared__ FastSmem sm;
     if ((int64_t)blockIdx.y < a.nblk) fast_body<F16, VBITS, true>(a, sm);
