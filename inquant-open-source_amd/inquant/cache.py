@@ -127,6 +127,9 @@ class InQuantCache(_HFCache):
         self._tracked_aux_bytes = 0
         self.peak_nbytes = 0
         self._seen_tokens = 0
+        # (tensor, its in-place version, expected first position) of the last
+        # cache_position that passed the check
+        self._checked_position = None
 
     # ---- Hugging Face cache protocol
     def __len__(self) -> int:
@@ -205,8 +208,20 @@ class InQuantCache(_HFCache):
             if (not isinstance(position, torch.Tensor) or position.ndim != 1
                     or position.numel() != key_states.shape[2] or position.dtype not in (torch.int32, torch.int64)):
                 raise ValueError("cache_position must be a 1D integer tensor with one position per new token")
-            if self.config.validate_positions:
-                # compared on the host: one copy instead of two kernels and a reduction
+            # Inference-mode tensors keep no in-place version counter, so they
+            # are checked every time.
+            version = None if position.is_inference() else position._version
+            checked = self._checked_position
+            if self.config.validate_positions and not (
+                    version is not None and checked is not None and checked[0] is position
+                    and checked[1] == version and checked[2] == old_length):
+                # Compared on the host: one copy instead of two kernels and a
+                # reduction.  The layers of one decode step share the step's
+                # cache_position tensor and expect the same first position,
+                # so a tensor that already passed, unmodified since (its
+                # in-place version counter is unchanged), for the same
+                # expected start is not copied again; the device-to-host copy
+                # waits for all queued GPU work.
                 host = position.cpu()
                 if host.numel() == 1:
                     ok = int(host[0]) == old_length
@@ -215,6 +230,7 @@ class InQuantCache(_HFCache):
                                                         dtype=position.dtype))
                 if not ok:
                     raise ValueError("Only contiguous append positions are supported; reset before a new request")
+                self._checked_position = None if version is None else (position, version, old_length)
         return layer
 
     @torch.no_grad()
@@ -384,6 +400,7 @@ class InQuantCache(_HFCache):
         self._tracked_auxiliary.clear()
         self._tracked_live_bytes = self._tracked_aux_bytes = self.peak_nbytes = 0
         self._seen_tokens = 0
+        self._checked_position = None
 
     def release(self) -> None:
         self.reset()

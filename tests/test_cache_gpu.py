@@ -270,3 +270,44 @@ def test_single_token_position_check():
     assert cache.get_seq_length() == 6
     cache.append_for_attention(t, t, 0, {"cache_position": torch.tensor([6], dtype=torch.int32, device="cuda")})
     assert cache.get_seq_length() == 7
+
+
+def _count_host_copies(position):
+    calls = []
+    original = position.cpu
+
+    def counted(*args, **kwargs):
+        calls.append(1)
+        return original(*args, **kwargs)
+    position.cpu = counted
+    return calls
+
+
+@pytest.mark.parametrize("inference", [False, True])
+def test_shared_cache_position_checked_once_per_step(inference):
+    # The layers of one step share one cache_position tensor: it is copied to
+    # the host for the first layer only, again after an in-place change, and
+    # again for a layer that expects another first position.  Inference-mode
+    # tensors keep no version counter and are copied for every layer.
+    from inquant.cache import InQuantCache
+    cache = InQuantCache(_cfg())
+    x = _randn(1, 2, 6, 8, seed=37)
+    for layer in (0, 1):
+        cache.update(x, x, layer, {"cache_position": torch.arange(6, device="cuda")})
+    cache.update(x[:, :, :5], x[:, :, :5], 2, {"cache_position": torch.arange(5, device="cuda")})
+    t = x[:, :, :1]
+    with torch.inference_mode(inference):
+        p = torch.tensor([6], device="cuda")
+        calls = _count_host_copies(p)
+        for layer in (0, 1):
+            cache.append_for_attention(t, t, layer, {"cache_position": p})
+        assert len(calls) == (2 if inference else 1)
+        with pytest.raises(ValueError, match="contiguous append positions"):
+            cache.append_for_attention(t, t, 2, {"cache_position": p})
+        assert cache.get_seq_length(2) == 5
+        p += 1
+        cache.append_for_attention(t, t, 0, {"cache_position": p})
+        p.fill_(3)
+        with pytest.raises(ValueError, match="contiguous append positions"):
+            cache.append_for_attention(t, t, 1, {"cache_position": p})
+        assert [cache.get_seq_length(i) for i in range(3)] == [8, 7, 5]
