@@ -388,6 +388,41 @@ def time_append(device, H=4, packed_tokens=32768, validate_positions=True):
             "seal_bytes": seal_bytes}
 
 
+def time_append_step(device, H=4, packed_tokens=32768, layers=28, steps=128):
+    """Config 2 append as a model makes it: each decode step appends one token
+    to every layer of a 28-layer cache (32K packed context each, tail 128 ->
+    256, no seal), the layers sharing the step's cache_position tensor."""
+    import torch
+    from inquant.cache import CacheConfig, InQuantCache
+    from inquant.codec import CodecConfig
+    g = torch.Generator(device=device).manual_seed(12)
+    cfg = CacheConfig(codec=CodecConfig(donor_policy="min_error"), value_bits=2, value_group_size=64)
+    cache = InQuantCache(cfg)
+    n0 = 4 + packed_tokens + 128
+    k = kv_tensor(g, H, n0 + steps, device)
+    v = kv_tensor(g, H, n0 + steps, device)
+    for i in range(layers):
+        cache.update(k[:, :, :n0], v[:, :, :n0], i)
+    positions = torch.arange(n0 + steps, device=device)
+
+    def run(pos):
+        for _ in range(steps // 2):
+            p = positions[pos:pos + 1]
+            for i in range(layers):
+                cache.append_for_attention(k[:, :, pos:pos + 1], v[:, :, pos:pos + 1], i, {"cache_position": p})
+            pos += 1
+        return pos
+    pos = run(n0)                        # warm allocator blocks (tail 128 -> 192)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    pos = run(pos)                       # tail 192 -> 256
+    torch.cuda.synchronize()
+    step_us = (time.perf_counter() - t0) * 1e6 / (steps // 2)
+    assert cache.get_seq_length(layers - 1) == n0 + steps
+    return {"layers": layers, "append_step_us": round(step_us, 1),
+            "append_us_per_layer_token": round(step_us / layers, 2)}
+
+
 def cpu_baseline(layer):
     """Time the CPU oracle (dequantize-then-attend, fp64) on a bounded sample of one layer."""
     import numpy as np
@@ -450,6 +485,7 @@ def main():
     # a controlled runner may skip the position check and its device-to-host
     # copy per token (cache.py:30-32)
     append["append_us_per_token_unvalidated"] = time_append(device, validate_positions=False)["append_us_per_token"]
+    append["step"] = time_append_step(device)
     cfg3 = None if args.no_cfg3 else time_decode_cfg3(device)
     result = {
         "metric": METRIC,
