@@ -23,6 +23,7 @@ except ImportError:  # codec/cache use does not need transformers
         pass
 
 from .codec import _BAD_K, CodecConfig, PackedTensor, quantize
+from .value_codec import _BAD_V, _value_blocks
 
 
 @dataclass(frozen=True)
@@ -287,7 +288,6 @@ class InQuantCache(_HFCache):
                                                    flags[1:2] if blocks else None)
             bad_v = _BAD_K
         else:
-            from .value_codec import _BAD_V, _value_blocks
             new_values = _value_blocks(pending_value, blocks, cfg.block_size, cfg.value_bits,
                                        cfg.value_group_size, flags[1:2] if blocks else None)
             bad_v = _BAD_V
