@@ -118,6 +118,34 @@ def test_cache_update_validation_runs_on_host():
     assert cache.get_seq_length() == 0 and cache.nbytes == 0
 
 
+def test_shared_position_tensor_is_read_once_per_expected_start():
+    # Host logic only: no block is sealed, so no codec call is made.  One
+    # cache_position shared by two layers is read for the first; an in-place
+    # change, another expected start or reset() makes it read again.
+    from inquant.cache import CacheConfig, InQuantCache
+    cache = InQuantCache(CacheConfig())
+    x = torch.zeros(1, 1, 6, 8)
+    for layer in (0, 1):
+        cache.update(x, x, layer, {"cache_position": torch.arange(6)})
+    cache.update(x[:, :, :5], x[:, :, :5], 2, {"cache_position": torch.arange(5)})
+    t = x[:, :, :1]
+    p = torch.tensor([6])
+    reads = []
+    original = p.cpu
+    p.cpu = lambda *a, **k: reads.append(1) or original(*a, **k)
+    for layer in (0, 1):
+        cache.append_for_attention(t, t, layer, {"cache_position": p})
+    assert len(reads) == 1
+    with pytest.raises(ValueError, match="contiguous append positions"):
+        cache.append_for_attention(t, t, 2, {"cache_position": p})
+    assert len(reads) == 2 and cache.get_seq_length(2) == 5
+    p += 1
+    cache.append_for_attention(t, t, 0, {"cache_position": p})
+    assert len(reads) == 3
+    cache.reset()
+    assert cache._checked_position is None
+
+
 def test_decode_state_validation_without_gpu():
     from inquant.triton_attention import PackedDecodeState
     state = PackedDecodeState([], [])
