@@ -323,3 +323,48 @@ def test_codecs_round_half_to_even_on_exact_ties(dtype):
         ref = oracle.v_quantize(_np(vt.float()), bits, 64)
         got = quantize_values(vt, bits, 64)
         np.testing.assert_array_equal(_np(got.payload), ref["payload"])
+
+
+@pytest.mark.parametrize("bits", [2, 4])
+@pytest.mark.parametrize("dtype", ["bfloat16", "float32"])
+def test_value_codes_match_ieee_division_known_answers(bits, dtype):
+    # value_codec.py:66-67 pinned by literal codes (tests/vknown.py): exact
+    # ties go to the even code; quotients one ulp from k + 1/2 follow the
+    # IEEE division (fp32 rows: the generic encoder; bf16 rows: the row encoder)
+    import vknown
+    from inquant.value_codec import quantize_values
+    x, codes = vknown.build(bits, dtype)
+    got = quantize_values(_dev(x, TORCH_DTYPES[dtype]), bits, vknown.GROUP)
+    np.testing.assert_array_equal(vknown.unpack_codes(_np(got.payload)[0, 0], bits), codes)
+    ref = oracle.v_quantize(x, bits, vknown.GROUP)
+    np.testing.assert_array_equal(_np(got.scales).view(np.uint16), ref["scales"].view(np.uint16))
+    np.testing.assert_array_equal(_np(got.offsets).view(np.uint16), ref["offsets"].view(np.uint16))
+
+
+def test_cfg3_full_layer_encode_matches_oracle():
+    # config 3 at its real size: one Mistral-7B layer of 32768 tokens x 8 KV
+    # heads in 256-token blocks (the cache's strided view of the prefill),
+    # 8% outlier channels as three 3-wide runs plus one, K4 min_error and V2
+    # g64, bit-exact against the oracle (codec.py:181-243, value_codec.py:51-72)
+    from inquant.codec import CodecConfig, quantize
+    from inquant.value_codec import quantize_values
+    H, T, B = 8, 32768, 256
+    print("cfg3 full-layer encode", flush=True)
+    g = torch.Generator(device="cuda").manual_seed(3003)
+    kv = []
+    for which in range(2):
+        x = torch.randn((1, H, T, 128), generator=g, device="cuda")
+        for h, chans in enumerate(synth.outlier_channels(3003 + which, H, 128, [3, 3, 3, 1])):
+            x[0, h, :, chans] *= 20
+        kv.append(x.to(torch.bfloat16))
+    k, v = kv
+    view = lambda t: t[0].reshape(H, T // B, B, 128).permute(1, 0, 2, 3)
+    got_k = quantize(view(k), CodecConfig(donor_policy="min_error"))
+    got_v = quantize_values(view(v), 2, 64)
+    ref_k = oracle.k4_quantize(_np(view(k).float()), 8, 0.125, "min_error")
+    for field in ("payload", "scales", "salient_channels", "donor_channels", "padding"):
+        _same_bits(_np(got_k.tensors[field]).astype(ref_k[field].dtype), ref_k[field], field)
+    ref_v = oracle.v_quantize(_np(view(v).float()), 2, 64)
+    np.testing.assert_array_equal(_np(got_v.payload), ref_v["payload"])
+    np.testing.assert_array_equal(_np(got_v.scales).view(np.uint16), ref_v["scales"].view(np.uint16))
+    np.testing.assert_array_equal(_np(got_v.offsets).view(np.uint16), ref_v["offsets"].view(np.uint16))

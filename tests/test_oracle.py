@@ -162,6 +162,18 @@ def test_value_codec_parameters_and_nearest_level(bits, group):
     assert (chosen <= dist.min(-1) * (1 + 1e-6) + 1e-6).all()
 
 
+@pytest.mark.parametrize("bits", [2, 4])
+def test_value_codec_rounds_like_ieee_division_and_half_to_even(bits):
+    # value_codec.py:66-67: torch.round (half to even) of the IEEE fp32
+    # quotient.  Literal known answers: exact ties, and quotients one ulp
+    # from k + 1/2 where a reciprocal product would round the other way.
+    import vknown
+    vknown.quotients_hold()
+    x, codes = vknown.build(bits, "float32")
+    q = oracle.v_quantize(x, bits, vknown.GROUP)
+    np.testing.assert_array_equal(vknown.unpack_codes(q["payload"][0, 0], bits), codes)
+
+
 def test_value_codec_rejects_unrepresentable_parameters():
     for value in (float("nan"), float("inf"), 1e6):
         with pytest.raises(ValueError, match="finite"):

@@ -172,3 +172,50 @@ def test_page_write_and_decode_beyond_signed_32bit_byte_offset():
     near = paged_decode(query, pool, ids[:1], tail, 1, 1, 4, layout, workspace, 128 ** -0.5)
     far_out = paged_decode(query, pool, ids[1:], tail, 1, 1, 4, layout, workspace, 128 ** -0.5)
     assert torch.equal(near, far_out)
+
+
+def test_paged_decode_batch_sixteen_sequences_against_oracle():
+    # config 4 at its real shape: 16 sequences, contexts drawn from 2K..32K,
+    # 16-token pages at random physical ids in one pool, per-sequence sink and
+    # partial-page tail; every sequence within 2e-3 of the fp64 oracle
+    # (kernels.py:8-88 semantics, batched over sequences in one launch)
+    from inquant.triton_attention import SharedDecodeWorkspace
+    from inquant_vllm import PageLayout, pack_pages, paged_decode_batch
+    B, H, HQ, S = 16, 4, 28, 16
+    layout = PageLayout(B, H)
+    ctx = np.random.default_rng(404).integers(2048, 32769, S)
+    pages = ctx // B
+    tails = ctx % B
+    total = int(pages.sum())
+    print(f"cfg4 batch: contexts {ctx.tolist()}, {total} pages", flush=True)
+    g = torch.Generator(device="cuda").manual_seed(404)
+    perm = torch.randperm(total + 9, generator=g, device="cuda")[:total].to(torch.int32)
+    pool = torch.full((total + 9, layout.page_bytes), 255, dtype=torch.uint8, device="cuda")
+    max_pages = int(pages.max())
+    tables = torch.zeros((S, max_pages), dtype=torch.int32, device="cuda")
+    dense = torch.full((S, 2, H, B + 4, 128), float("nan"), dtype=torch.bfloat16, device="cuda")
+    first = 0
+    for i in range(S):
+        n, t = int(pages[i]), int(tails[i])
+        k, v = _kv(4040 + i, (H, int(ctx[i]), 128))
+        ids = perm[first:first + n]
+        first += n
+        tables[i, :n] = ids
+        kt = k[:, :n * B].reshape(H, n, B, 128).transpose(0, 1)
+        vt = v[:, :n * B].reshape(H, n, B, 128).transpose(0, 1)
+        pool.index_copy_(0, ids.long(), pack_pages(kt, vt, layout))
+        dense[i, 0, :, :4], dense[i, 1, :, :4] = k[:, :4], v[:, :4]
+        if t:
+            dense[i, 0, :, 4:4 + t], dense[i, 1, :, 4:4 + t] = k[:, -t:], v[:, -t:]
+    infos = torch.tensor([[int(pages[i]), int(tails[i]), 4] for i in range(S)], dtype=torch.int32, device="cuda")
+    q = torch.randn(S, HQ, 128, generator=g, device="cuda").to(torch.bfloat16)
+    out = torch.empty((S, HQ, 128), dtype=torch.float32, device="cuda")
+    paged_decode_batch(q, pool, tables, infos, dense, max_pages, layout, SharedDecodeWorkspace(), 128 ** -0.5,
+                       out)
+    got = _np(out)
+    pool_np, tables_np, dense_np, q_np = _np(pool), _np(tables), _np(dense.float()), _np(q.float())
+    for i in range(S):
+        exp = oracle.paged_attend(q_np[i], pool_np, tables_np[i], dense_np[i], int(pages[i]), int(tails[i]), 4,
+                                  H, B, 128 ** -0.5)
+        err = float(np.abs(got[i] - exp).max())
+        assert err <= ATOL, (i, int(ctx[i]), err)
