@@ -31,6 +31,8 @@
  *                       (+ the role-map part of layout.py:66-81 pack_pages)
  *   iq_unpack_pages     extensions/vllm/src/inquant_vllm/layout.py:84-100 unpack_pages_reference
  *   iq_paged_decode     extensions/vllm/src/inquant_vllm/kernels.py:66-88 paged_decode
+ *   iq_tail_append      src/inquant/cache.py:256-259,283-286 (the dense tail
+ *                       concatenation of append_for_attention / _append)
  */
 #ifndef INQUANT_HIP_H
 #define INQUANT_HIP_H
@@ -212,6 +214,24 @@ int iq_paged_decode(const void *q, int64_t q_stride_seq, int64_t q_stride_h, int
                     const int32_t *seq_info, int64_t n_pages, int64_t tail_t, int64_t sink_t,
                     const void *dense, int64_t dense_stride_seq, float scale, float *workspace,
                     int64_t workspace_floats, void *out, int64_t out_stride_seq, int out_dtype, void *stream);
+
+/*
+ * Dense tail append of a cache layer.  buf holds [2 (keys, values), H,
+ * capacity, D] elements of elem_bytes (element strides buf_kv, buf_h,
+ * buf_t); k / v hold n_new (<= 64) rows per head (element strides: head,
+ * token).  One launch moves rows [shift_src, shift_src + shift_count) to
+ * [0, shift_count) (the rows that survive a seal), then writes the new rows
+ * at [slot, slot + n_new); the three row ranges must be disjoint.  With
+ * `positions` (i32 or i64 per pos_bytes, n_new values on the device) the
+ * kernel compares positions[i] with expected + i and sets *flag = 1 on any
+ * mismatch.  Replaces the per-token concatenation of the dense tail in
+ * InQuantCache.append_for_attention / _append (cache.py:256-259,283-286).
+ */
+int iq_tail_append(const void *k, const void *v, int64_t k_sh, int64_t k_st, int64_t v_sh, int64_t v_st,
+                   int64_t H, int64_t n_new, int64_t D, int elem_bytes, void *buf, int64_t buf_kv,
+                   int64_t buf_h, int64_t buf_t, int64_t capacity, int64_t slot, int64_t shift_src,
+                   int64_t shift_count, const void *positions, int pos_bytes, int64_t expected, int *flag,
+                   void *stream);
 
 #ifdef __cplusplus
 }

@@ -1,13 +1,36 @@
-"""Append-only InQuant KV cache (drop-in for the reference's inquant.cache).
+"""Append-only InQuant KV cache of one request on MI355X.
 
-Per layer: an exact dense sink (first `sink_tokens` tokens), immutable K4
-(and K4 or V2/V4) packed temporal blocks, and a dense recent tail of
-`residual_length` .. `residual_length + block_size - 1` tokens.  Blocks are
-sealed from the front of (tail ++ new) whenever at least
-`residual_length + block_size` tokens are pending.  Semantics, validation and
-byte accounting follow src/inquant/cache.py of the reference (CacheConfig
-:24-54, _quantize_temporal_blocks :89-119, InQuantCache :122-419); the codec
-work runs in libinquant_hip.so.
+Drop-in for the reference's ``inquant.cache`` (src/inquant/cache.py): the
+same ``CacheConfig`` fields and validation messages, the same
+``InQuantCache`` methods and Hugging Face cache protocol, the same sealing
+rule (sink = first ``sink_tokens`` tokens; blocks of ``block_size`` tokens
+are sealed from the front of tail ++ new while at least
+``residual_length + block_size`` tokens are pending, cache.py:271-306) and
+the same byte accounting (cache.py:308-394).
+
+How a layer is stored here (not how the reference stores it):
+
+* Sink and tail are rows of two preallocated buffers of shape
+  [2 (keys, values), KV heads, rows, head_dim].  The tail buffer holds
+  ``residual_length + block_size`` rows; the live tail is rows
+  [start, start + count).  A one-token append writes one row in place with a
+  single kernel (``iq_tail_append``) instead of concatenating the whole tail
+  (the reference's two ``torch.cat`` per layer per token,
+  cache.py:256-259).  When the tail reaches ``residual_length + block_size``
+  rows its first ``block_size`` rows are sealed and ``start`` moves past them;
+  the first append after that moves the survivors back to row 0 in the same
+  launch.  A view handed out by ``append_for_attention`` therefore stays
+  valid until the append after the next seal.
+* Sealed blocks are per-block views of one batched encode (one K4 and one
+  value launch per seal, no per-block copies).  Their byte counts are the
+  bytes of their views, which tile the batched allocation exactly, so the
+  totals equal the reference's per-block clones.
+* ``cache_position`` is compared on the device by the append kernel.  With
+  ``validate_positions`` the first layer of each decode step (a position
+  tensor not yet checked for this start) synchronizes and raises before
+  anything changes, as the reference does; the other layers of the step,
+  which share the tensor, rely on the device comparison, whose flag is read
+  at the next synchronization (the next step's check or the next seal).
 """
 from __future__ import annotations
 
@@ -18,16 +41,24 @@ import torch
 
 try:
     from transformers.cache_utils import Cache as _HFCache
-except ImportError:  # codec/cache use does not need transformers
+except ImportError:  # the codec and cache do not need transformers
     class _HFCache:
         pass
 
-from .codec import _BAD_K, CodecConfig, PackedTensor, quantize
+from . import _native as nat
+from .codec import _BAD_K, CodecConfig, PackedTensor, _per_block, quantize
 from .value_codec import _BAD_V, _value_blocks
+
+_POSITION_ERROR = "Only contiguous append positions are supported; reset before a new request"
+# flag words of a cache: key non-finite, value non-finite, position mismatch
+_KEY_BAD, _VALUE_BAD, _POSITION_BAD = 0, 1, 2
 
 
 @dataclass(frozen=True)
 class CacheConfig:
+    """Cache options (cache.py:24-54).  ``validate_positions=False`` skips the
+    position comparison (the caller guarantees contiguous positions)."""
+
     codec: CodecConfig = field(default_factory=CodecConfig)
     block_size: int = 256
     residual_length: int = 128
@@ -40,38 +71,23 @@ class CacheConfig:
 
     def __post_init__(self) -> None:
         for name in ("block_size", "residual_length", "sink_tokens"):
-            value = getattr(self, name)
-            if isinstance(value, bool) or not isinstance(value, int):
+            if type(getattr(self, name)) is not int:
                 raise ValueError(f"{name} must be an integer")
-        if self.block_size < 1 or self.residual_length < 0 or self.sink_tokens < 0:
+        if min(self.block_size - 1, self.residual_length, self.sink_tokens) < 0:
             raise ValueError("block_size must be positive; residual_length and sink_tokens nonnegative")
         for name in ("validate_positions", "shared_workspace", "track_peak_bytes"):
-            if not isinstance(getattr(self, name), bool):
+            if type(getattr(self, name)) is not bool:
                 raise ValueError(f"{name} must be a boolean")
-        if self.value_bits is not None and (type(self.value_bits) is not int or self.value_bits not in (2, 4)):
+        if self.value_bits not in (None, 2, 4) or type(self.value_bits) not in (type(None), int):
             raise ValueError("value_bits must be None, 2 or 4")
-        if type(self.value_group_size) is not int or self.value_group_size not in (32, 64, 128):
+        if self.value_group_size not in (32, 64, 128) or type(self.value_group_size) is not int:
             raise ValueError("value_group_size must be 32, 64 or 128")
-
-
-@dataclass
-class _Layer:
-    shape: tuple
-    dtype: torch.dtype
-    device: torch.device
-    seq_length: int = 0
-    sink_key: torch.Tensor | None = None
-    sink_value: torch.Tensor | None = None
-    residual_key: torch.Tensor | None = None
-    residual_value: torch.Tensor | None = None
-    key_blocks: list = field(default_factory=list)
-    value_blocks: list = field(default_factory=list)
-    packed_nbytes: int = 0
 
 
 @dataclass(frozen=True)
 class PackedAttentionView:
-    """Snapshot for one decode: old packed blocks plus the exact sink and tail (with the new token)."""
+    """What one decode step attends to: the blocks sealed before this step,
+    the exact sink, and the exact tail including the new token (cache.py:72-82)."""
 
     key_blocks: tuple
     value_blocks: tuple
@@ -82,34 +98,104 @@ class PackedAttentionView:
     seq_length: int
 
 
-def _tensor_bytes(t: torch.Tensor | None) -> int:
-    return 0 if t is None else t.numel() * t.element_size()
+class _Rows:
+    """A [2, H, capacity, D] buffer of dense rows; keys at [0], values at [1]."""
+
+    __slots__ = ("buf", "start", "count")
+
+    def __init__(self, heads: int, capacity: int, dim: int, dtype: torch.dtype, device: torch.device):
+        self.buf = torch.empty((2, heads, capacity, dim), dtype=dtype, device=device)
+        self.start = 0
+        self.count = 0
+
+    @property
+    def capacity(self) -> int:
+        return self.buf.shape[2]
+
+    def keys(self, extra: int = 0) -> torch.Tensor:
+        return self.buf[0:1, :, self.start:self.start + self.count + extra]
+
+    def values(self, extra: int = 0) -> torch.Tensor:
+        return self.buf[1:2, :, self.start:self.start + self.count + extra]
+
+    def live_nbytes(self) -> int:
+        return 2 * self.buf.shape[1] * self.count * self.buf.shape[3] * self.buf.element_size()
+
+    def write(self, keys: torch.Tensor, values: torch.Tensor) -> None:
+        """Copy new rows after the live ones (host-ordered torch copies)."""
+        n = keys.shape[2]
+        if self.start + self.count + n > self.capacity:
+            self.compact()
+        end = self.start + self.count
+        self.buf[0:1, :, end:end + n].copy_(keys)
+        self.buf[1:2, :, end:end + n].copy_(values)
+
+    def compact(self) -> None:
+        if self.start:
+            live = self.buf[:, :, self.start:self.start + self.count].clone()
+            self.buf[:, :, :self.count].copy_(live)
+            self.start = 0
+
+
+class _LayerCache:
+    """One layer's sink rows, dense tail rows and sealed blocks."""
+
+    def __init__(self, shape, dtype, device):
+        self.shape = tuple(shape)
+        self.dtype = dtype
+        self.device = device
+        self.seq_length = 0
+        self.sink: _Rows | None = None
+        self.tail: _Rows | None = None
+        self.key_blocks: list = []
+        self.value_blocks: list = []
+        self.packed_nbytes = 0
+
+    # the reference's field names, as views of the rows
+    @property
+    def sink_key(self):
+        return None if self.sink is None else self.sink.keys()
+
+    @property
+    def sink_value(self):
+        return None if self.sink is None else self.sink.values()
+
+    @property
+    def residual_key(self):
+        return None if self.tail is None else self.tail.keys()
+
+    @property
+    def residual_value(self):
+        return None if self.tail is None else self.tail.values()
+
+    def dense_nbytes(self) -> tuple[int, int]:
+        """(live sink bytes, live tail bytes)."""
+        return (0 if self.sink is None else self.sink.live_nbytes(),
+                0 if self.tail is None else self.tail.live_nbytes())
+
+    def reserved_nbytes(self) -> int:
+        """Bytes of the dense row buffers beyond their live rows."""
+        held = sum(r.buf.numel() * r.buf.element_size() for r in (self.sink, self.tail) if r is not None)
+        return held - sum(self.dense_nbytes())
 
 
 def _quantize_temporal_blocks(tensor: torch.Tensor, block_count: int, block_size: int,
                               config: CodecConfig, bad: torch.Tensor | None = None) -> list[PackedTensor]:
-    """Encode `block_count` leading blocks of [1, H, T, D] in one launch, one owned PackedTensor each.
-
-    The blocked [nb, H, B, D] view is read in place by the kernel (no copy);
-    statistics stay per (block, head).  With `bad` given, the non-finite flag
-    goes to bad[0] and is left for the caller to check.
-    """
+    """K4-encode the first ``block_count`` blocks of [1, H, T, D] as
+    independent (block, head) rows (cache.py:89-119): one launch over the
+    strided [blocks, H, B, D] view, one PackedTensor view per block.  With
+    ``bad`` the non-finite flag is left there for the caller."""
     if block_count == 0:
         return []
-    if block_count == 1:
-        return [quantize(tensor[:, :, :block_size], config, _flag=bad)]
-    _, heads, _, channels = tensor.shape
-    blocked = tensor[0, :, :block_count * block_size].reshape(heads, block_count, block_size, channels).permute(1, 0, 2, 3)
+    _, heads, _, dim = tensor.shape
+    blocked = tensor[0, :, :block_count * block_size].unflatten(1, (block_count, block_size)).transpose(0, 1)
     packed = quantize(blocked, config, _flag=bad)
-    shape = (1, heads, block_size, channels)
-    return [PackedTensor(**{name: t[i:i + 1].clone(memory_format=torch.contiguous_format)
-                            for name, t in packed.tensors.items()},
-                         shape=shape, original_dtype=tensor.dtype)
-            for i in range(block_count)]
+    return _per_block(packed, block_count, (1, heads, block_size, dim), PackedTensor)
 
 
 class InQuantCache(_HFCache):
-    """Immutable quantized history plus exact sink and a bounded recent tail (batch 1, append-only)."""
+    """Immutable packed history, exact sink and a bounded exact tail
+    (batch 1, append-only), as src/inquant/cache.py:122-419."""
 
     is_compileable = False
 
@@ -117,35 +203,32 @@ class InQuantCache(_HFCache):
         try:
             super().__init__()
         except (TypeError, ValueError):
-            super().__init__(layers=[])  # transformers >= 5 requires an explicit layer list
+            super().__init__(layers=[])     # transformers >= 5 wants an explicit layer list
         self.config = config or CacheConfig()
-        self._layers: dict[int, _Layer] = {}
+        self._layers: dict[int, _LayerCache] = {}
         self._attention_states: dict[int, Any] = {}
         self._shared_decode_workspace = None
-        self._tracked_storage: dict[int, int] = {}
-        self._tracked_auxiliary: dict[int, int] = {}
-        self._tracked_live_bytes = 0
-        self._tracked_aux_bytes = 0
-        self.peak_nbytes = 0
         self._seen_tokens = 0
-        # (tensor, its in-place version, expected first position) of the last
-        # cache_position that passed the check
-        self._checked_position = None
+        self.peak_nbytes = 0
+        # running totals for track_peak_bytes: layer -> (owned, auxiliary)
+        self._owned: dict[int, tuple[int, int]] = {}
+        self._owned_total = 0
+        self._flags: torch.Tensor | None = None          # int32 [3] on the cache's device
+        self._position_checked: tuple | None = None      # (tensor, expected start) verified by a sync
 
-    # ---- Hugging Face cache protocol
+    # ------------------------------------------------------------ HF protocol
     def __len__(self) -> int:
-        return max(self._layers, default=-1) + 1
+        return 1 + max(self._layers, default=-1)
 
     def __getitem__(self, layer_idx: int):
         return self.materialize(layer_idx)
 
     def __iter__(self):
-        for idx in range(len(self)):
-            yield self.materialize(idx)
+        return (self.materialize(i) for i in range(len(self)))
 
     def get_seq_length(self, layer_idx: int | None = 0) -> int:
-        layer = self._layers.get(0 if layer_idx is None else layer_idx)
-        return 0 if layer is None else layer.seq_length
+        layer = self._layers.get(layer_idx or 0)
+        return layer.seq_length if layer is not None else 0
 
     def get_usable_length(self, new_seq_length: int, layer_idx: int | None = 0) -> int:
         return self.get_seq_length(layer_idx)
@@ -157,228 +240,299 @@ class InQuantCache(_HFCache):
         return None
 
     def get_mask_sizes(self, cache_position, layer_idx: int = 0):
-        n = int(cache_position.numel()) if isinstance(cache_position, torch.Tensor) else int(cache_position)
-        return self.get_seq_length(layer_idx) + n, 0
+        new = cache_position.numel() if isinstance(cache_position, torch.Tensor) else int(cache_position)
+        return self.get_seq_length(layer_idx) + int(new), 0
 
     @property
     def seen_tokens(self) -> int:
         return self._seen_tokens
 
-    # ---- updates
-    @torch.no_grad()
-    def update(self, key_states, value_states, layer_idx, cache_kwargs=None, *args, **kwargs):
-        layer = self._validate_update(key_states, value_states, layer_idx, cache_kwargs)
-        if layer is None:
-            layer = _Layer(tuple(key_states.shape), key_states.dtype, key_states.device)
-            full_key, full_value = key_states, value_states
-        else:
-            old_key, old_value = self.materialize(layer_idx)
-            full_key = torch.cat((old_key, key_states), dim=2)
-            full_value = torch.cat((old_value, value_states), dim=2)
-        self._append(layer, key_states, value_states)
-        self._layers[layer_idx] = layer
-        self.record_peak(layer_idx)
-        if layer_idx == 0:
-            self._seen_tokens = layer.seq_length
-        return full_key, full_value
-
-    def _validate_update(self, key_states, value_states, layer_idx, cache_kwargs):
-        if not isinstance(layer_idx, int) or layer_idx < 0:
+    # ------------------------------------------------------------ validation
+    def _check(self, keys, values, layer_idx, cache_kwargs):
+        """Argument checks of cache.py:202-240; returns (layer or None, position tensor or None)."""
+        if type(layer_idx) is not int or layer_idx < 0:
             raise ValueError("layer_idx must be a nonnegative integer")
-        if key_states.ndim != 4 or value_states.shape != key_states.shape:
+        if keys.ndim != 4 or values.shape != keys.shape:
             raise ValueError("K/V must have matching [batch, KV_heads, tokens, head_dim] shapes")
-        if key_states.shape[0] != 1:
+        if keys.shape[0] != 1:
             raise NotImplementedError("InQuantCache currently supports batch size 1 only")
-        if not key_states.is_floating_point() or not value_states.is_floating_point():
+        if not (keys.is_floating_point() and values.is_floating_point()):
             raise ValueError("K/V must be floating-point tensors")
-        if key_states.dtype != value_states.dtype or key_states.device != value_states.device:
+        if keys.dtype != values.dtype or keys.device != values.device:
             raise ValueError("K/V must share dtype and device")
-        if any(size < 1 for size in key_states.shape):
+        if 0 in keys.shape:
             raise ValueError("K/V dimensions must be nonempty")
-        if key_states.shape[3] % 2:
+        if keys.shape[3] & 1:
             raise ValueError("Packed cache requires an even head dimension")
         layer = self._layers.get(layer_idx)
-        old_length = 0 if layer is None else layer.seq_length
-        if layer is not None:
-            same = (key_states.shape[0], key_states.shape[1], key_states.shape[3]) == (
-                layer.shape[0], layer.shape[1], layer.shape[3])
-            if not same or key_states.dtype != layer.dtype or key_states.device != layer.device:
-                raise ValueError("Layer shape, dtype and device must remain unchanged")
-        position = (cache_kwargs or {}).get("cache_position")
+        if layer is not None and ((keys.shape[1], keys.shape[3]) != (layer.shape[1], layer.shape[3])
+                                  or keys.dtype != layer.dtype or keys.device != layer.device):
+            raise ValueError("Layer shape, dtype and device must remain unchanged")
+        position = cache_kwargs.get("cache_position") if cache_kwargs else None
+        if position is not None and not (
+                isinstance(position, torch.Tensor) and position.ndim == 1 and position.numel() == keys.shape[2]
+                and position.dtype in (torch.int32, torch.int64)):
+            raise ValueError("cache_position must be a 1D integer tensor with one position per new token")
+        return layer, position if self.config.validate_positions else None
+
+    def _flag_words(self, device) -> torch.Tensor:
+        if self._flags is None or self._flags.device != device:
+            self._flags = torch.zeros(3, dtype=torch.int32, device=device)
+        return self._flags
+
+    def _host_position_check(self, position: torch.Tensor, start: int) -> None:
+        """Synchronous comparison with start, start + 1, ... (raises before any change)."""
+        host = position.cpu()
+        wanted = torch.arange(start, start + host.numel(), dtype=host.dtype)
+        flags = self._flags
+        deferred = flags is not None and bool(flags[_POSITION_BAD].item())
+        if deferred:
+            flags[_POSITION_BAD].zero_()
+        if deferred or not bool((host == wanted).all()):
+            self._position_checked = None
+            raise ValueError(_POSITION_ERROR)
+
+    # ------------------------------------------------------------ updates
+    @torch.no_grad()
+    def update(self, key_states, value_states, layer_idx, cache_kwargs=None, *args, **kwargs):
+        """Store new tokens; return the layer's full K/V (the inputs themselves
+        on the first call, else dequantized history ++ the new tokens)."""
+        layer, position = self._check(key_states, value_states, layer_idx, cache_kwargs)
+        start = 0 if layer is None else layer.seq_length
         if position is not None:
-            if (not isinstance(position, torch.Tensor) or position.ndim != 1
-                    or position.numel() != key_states.shape[2] or position.dtype not in (torch.int32, torch.int64)):
-                raise ValueError("cache_position must be a 1D integer tensor with one position per new token")
-            # Inference-mode tensors keep no in-place version counter, so they
-            # are checked every time.
-            version = None if position.is_inference() else position._version
-            checked = self._checked_position
-            if self.config.validate_positions and not (
-                    version is not None and checked is not None and checked[0] is position
-                    and checked[1] == version and checked[2] == old_length):
-                # Compared on the host: one copy instead of two kernels and a
-                # reduction.  The layers of one decode step share the step's
-                # cache_position tensor and expect the same first position,
-                # so a tensor that already passed, unmodified since (its
-                # in-place version counter is unchanged), for the same
-                # expected start is not copied again; the device-to-host copy
-                # waits for all queued GPU work.
-                host = position.cpu()
-                if host.numel() == 1:
-                    ok = int(host[0]) == old_length
-                else:
-                    ok = torch.equal(host, torch.arange(old_length, old_length + key_states.shape[2],
-                                                        dtype=position.dtype))
-                if not ok:
-                    raise ValueError("Only contiguous append positions are supported; reset before a new request")
-                self._checked_position = None if version is None else (position, version, old_length)
-        return layer
+            self._host_position_check(position, start)
+        if layer is None:
+            layer = _LayerCache(key_states.shape, key_states.dtype, key_states.device)
+            result = (key_states, value_states)
+        else:
+            history_k, history_v = self.materialize(layer_idx)
+            result = (torch.cat((history_k, key_states), 2), torch.cat((history_v, value_states), 2))
+        self._ingest(layer, key_states, value_states)
+        self._layers[layer_idx] = layer
+        self._after_write(layer_idx, layer)
+        return result
 
     @torch.no_grad()
     def append_for_attention(self, key_states, value_states, layer_idx, cache_kwargs=None) -> PackedAttentionView:
-        """Append one token and return the pre-seal view (blocks sealed now are seen next step)."""
-        layer = self._validate_update(key_states, value_states, layer_idx, cache_kwargs)
-        if key_states.shape[2] != 1 or layer is None:
+        """Append one decode token and return the view that step attends to.
+
+        Blocks sealed by this append are attended from the next step on
+        (cache.py:242-269)."""
+        layer, position = self._check(key_states, value_states, layer_idx, cache_kwargs)
+        if layer is None or key_states.shape[2] != 1:
             raise ValueError("append_for_attention requires one new token after an existing prefill")
         blocks = (tuple(layer.key_blocks), tuple(layer.value_blocks))
         sink = (layer.sink_key, layer.sink_value)
-        length = layer.seq_length + 1
-        sink_full = (0 if sink[0] is None else sink[0].shape[2]) >= self.config.sink_tokens
-        if sink_full and layer.residual_key is not None:
-            # the pre-seal tail is exactly the concatenation the append builds
-            tail_key, tail_value = self._append(layer, key_states, value_states)
+        tail = layer.tail
+        sink_rows = 0 if layer.sink is None else layer.sink.count
+        if tail is None or sink_rows < self.config.sink_tokens or key_states.device.type != "cuda":
+            # the sink is still filling or nothing is dense yet: general path
+            if position is not None:
+                self._host_position_check(position, layer.seq_length)
+            before = (layer.residual_key, layer.residual_value)
+            pending_k = key_states if before[0] is None else torch.cat((before[0], key_states), 2)
+            pending_v = value_states if before[1] is None else torch.cat((before[1], value_states), 2)
+            self._ingest(layer, key_states, value_states)
+            view = PackedAttentionView(*blocks, *sink, pending_k, pending_v, layer.seq_length)
         else:
-            tail_key, tail_value = key_states, value_states
-            if layer.residual_key is not None:
-                tail_key = torch.cat((layer.residual_key, tail_key), dim=2)
-                tail_value = torch.cat((layer.residual_value, tail_value), dim=2)
-            self._append(layer, key_states, value_states)
-        view = PackedAttentionView(blocks[0], blocks[1], sink[0], sink[1], tail_key, tail_value, length)
-        self.record_peak(layer_idx)
-        if layer_idx == 0:
-            self._seen_tokens = layer.seq_length
+            view = self._append_token(layer, key_states, value_states, position, blocks, sink)
+        self._after_write(layer_idx, layer)
         return view
 
-    def _append(self, layer: _Layer, keys, values) -> None:
+    def _append_token(self, layer, key, value, position, blocks, sink) -> PackedAttentionView:
+        """One row written in place by iq_tail_append; seal when the tail is full."""
         cfg = self.config
-        have = 0 if layer.sink_key is None else layer.sink_key.shape[2]
-        take = min(cfg.sink_tokens - have, keys.shape[2])
-        sink_key, sink_value = layer.sink_key, layer.sink_value
-        if take:
-            nk, nv = keys[:, :, :take], values[:, :, :take]
-            if sink_key is not None:
-                nk = torch.cat((sink_key, nk), dim=2)
-                nv = torch.cat((sink_value, nv), dim=2)
-            sink_key, sink_value = nk.clone(), nv.clone()
-        pending_key, pending_value = keys[:, :, take:], values[:, :, take:]
-        fresh = layer.residual_key is not None      # pending is a new tensor, not a view of the input
-        if fresh:
-            pending_key = torch.cat((layer.residual_key, pending_key), dim=2)
-            pending_value = torch.cat((layer.residual_value, pending_value), dim=2)
-        blocks = max(0, (pending_key.shape[2] - cfg.residual_length) // cfg.block_size)
-        # Both encoders raise their non-finite flag into one buffer that is
-        # read with a single device sync; the reference syncs once per
-        # encoder (codec.py:197, value_codec.py:64).  The key error wins, as
-        # the reference raises it before encoding the values.
-        flags = torch.zeros(2, dtype=torch.int32, device=keys.device) if blocks else None
-        new_keys = _quantize_temporal_blocks(pending_key, blocks, cfg.block_size, cfg.codec,
-                                             flags[0:1] if blocks else None)
+        tail = layer.tail
+        flags = self._flag_words(key.device)
+        start, count, capacity = tail.start, tail.count, tail.capacity
+        shift = start + count + 1 > capacity
+        if shift and start < count + 1:
+            tail.compact()              # survivors and the new row would overlap: move them first
+            start, shift = 0, False
+        check_now = False
+        pos_ptr, pos_bytes = None, 0
+        if position is not None:
+            if position.device.type != "cuda":
+                self._host_position_check(position, layer.seq_length)
+            else:
+                pos_ptr, pos_bytes = position.data_ptr(), position.element_size()
+                checked = self._position_checked
+                check_now = not (checked is not None and checked[0] is position and checked[1] == layer.seq_length)
+        buf = tail.buf
+        nat.check(nat.lib().iq_tail_append(
+            key.data_ptr(), value.data_ptr(), key.stride(1), key.stride(2), value.stride(1), value.stride(2),
+            buf.shape[1], 1, buf.shape[3], buf.element_size(), buf.data_ptr(), buf.stride(0), buf.stride(1),
+            buf.stride(2), capacity, count if shift else start + count, start if shift else 0,
+            count if shift else 0, pos_ptr, pos_bytes, layer.seq_length,
+            flags[_POSITION_BAD:].data_ptr(), torch.cuda.current_stream(key.device).cuda_stream))
+        if shift:
+            tail.start = start = 0
+        if check_now:
+            # the first layer of a step: raise now, before the row counts
+            if bool(flags[_POSITION_BAD].item()):
+                flags[_POSITION_BAD].zero_()
+                self._position_checked = None
+                raise ValueError(_POSITION_ERROR)
+            self._position_checked = (position, layer.seq_length)
+        tail.count += 1
+        layer.seq_length += 1
+        view = PackedAttentionView(*blocks, *sink, tail.keys(), tail.values(), layer.seq_length)
+        if tail.count >= cfg.residual_length + cfg.block_size:
+            try:
+                self._seal(layer, tail.keys(), tail.values(), 1)
+            except ValueError:
+                tail.count -= 1                  # the reference leaves the layer unchanged on errors
+                layer.seq_length -= 1
+                raise
+            tail.start += cfg.block_size
+            tail.count -= cfg.block_size
+        return view
+
+    def _seal(self, layer, keys, values, count) -> None:
+        """Encode the first ``count`` blocks of keys/values [1, H, >= count * B, D]
+        and append them; non-finite data raise ValueError with the layer unchanged.
+        The key and value encoders raise flags into one buffer read by a single
+        synchronization (the reference syncs once per encoder, codec.py:197 and
+        value_codec.py:64); a pending position mismatch is reported first."""
+        cfg = self.config
+        flags = self._flag_words(keys.device)
+        flags[:_POSITION_BAD].zero_()
+        new_keys = _quantize_temporal_blocks(keys, count, cfg.block_size, cfg.codec, flags[_KEY_BAD:_KEY_BAD + 1])
         if cfg.value_bits is None:
-            new_values = _quantize_temporal_blocks(pending_value, blocks, cfg.block_size, cfg.codec,
-                                                   flags[1:2] if blocks else None)
-            bad_v = _BAD_K
+            new_values = _quantize_temporal_blocks(values, count, cfg.block_size, cfg.codec,
+                                                   flags[_VALUE_BAD:_VALUE_BAD + 1])
+            value_error = _BAD_K
         else:
-            new_values = _value_blocks(pending_value, blocks, cfg.block_size, cfg.value_bits,
-                                       cfg.value_group_size, flags[1:2] if blocks else None)
-            bad_v = _BAD_V
-        if blocks:
-            bad_k_set, bad_v_set = flags.tolist()
-            if bad_k_set:
-                raise ValueError(_BAD_K)
-            if bad_v_set:
-                raise ValueError(bad_v)
-        offset = blocks * cfg.block_size
-        if fresh and offset == 0:
-            # nothing sealed: the concatenation is already an owned tensor
-            residual_key, residual_value = pending_key, pending_value
-        else:
-            residual_key = pending_key[:, :, offset:].clone()
-            residual_value = pending_value[:, :, offset:].clone()
-        layer.sink_key, layer.sink_value = sink_key, sink_value
-        layer.residual_key, layer.residual_value = residual_key, residual_value
+            new_values = _value_blocks(values, count, cfg.block_size, cfg.value_bits, cfg.value_group_size,
+                                       flags[_VALUE_BAD:_VALUE_BAD + 1])
+            value_error = _BAD_V
+        bad_key, bad_value, bad_position = flags.tolist()
+        if bad_position:
+            flags[_POSITION_BAD].zero_()
+            self._position_checked = None
+            raise ValueError(_POSITION_ERROR)
+        if bad_key:
+            raise ValueError(_BAD_K)
+        if bad_value:
+            raise ValueError(value_error)
         layer.key_blocks.extend(new_keys)
         layer.value_blocks.extend(new_values)
         if cfg.track_peak_bytes:
-            layer.packed_nbytes += sum(block.nbytes for block in new_keys + new_values)
-        layer.seq_length += keys.shape[2]
-        return pending_key, pending_value
+            layer.packed_nbytes += sum(b.nbytes for b in new_keys) + sum(b.nbytes for b in new_values)
+
+    def _ingest(self, layer: _LayerCache, keys, values) -> None:
+        """General append of any number of tokens (cache.py:271-306 semantics)."""
+        cfg = self.config
+        _, heads, n, dim = keys.shape
+        have = 0 if layer.sink is None else layer.sink.count
+        take = min(cfg.sink_tokens - have, n)
+        if take > 0:
+            if layer.sink is None:
+                layer.sink = _Rows(heads, cfg.sink_tokens, dim, keys.dtype, keys.device)
+            layer.sink.write(keys[:, :, :take], values[:, :, :take])
+        else:
+            take = 0
+        rest_k, rest_v = keys[:, :, take:], values[:, :, take:]
+        m = n - take
+        tail = layer.tail
+        live = 0 if tail is None else tail.count
+        blocks = max(0, (live + m - cfg.residual_length) // cfg.block_size)
+        if blocks:
+            pending_k = rest_k if not live else torch.cat((tail.keys(), rest_k), 2)
+            pending_v = rest_v if not live else torch.cat((tail.values(), rest_v), 2)
+            self._seal(layer, pending_k, pending_v, blocks)
+            done = blocks * cfg.block_size
+            rest_k, rest_v = pending_k[:, :, done:], pending_v[:, :, done:]
+            m = live + m - done
+            if tail is not None:
+                tail.start = tail.count = 0
+        if m > 0:
+            if tail is None:
+                tail = layer.tail = _Rows(heads, cfg.residual_length + cfg.block_size, dim, keys.dtype,
+                                          keys.device)
+            tail.write(rest_k, rest_v)
+        if take:
+            layer.sink.count += take
+        if m > 0:
+            tail.count += rest_k.shape[2]
+        layer.seq_length += n
+
+    def _after_write(self, layer_idx: int, layer: _LayerCache) -> None:
+        if layer_idx == 0:
+            self._seen_tokens = layer.seq_length
+        self.record_peak(layer_idx)
 
     def record_peak(self, layer_idx) -> None:
+        """Update peak_nbytes with this layer's current persistent and auxiliary bytes."""
         if not self.config.track_peak_bytes:
             return
         layer = self._layers[layer_idx]
-        owned = layer.packed_nbytes + sum(_tensor_bytes(t) for t in (
-            layer.sink_key, layer.sink_value, layer.residual_key, layer.residual_value))
-        self._tracked_live_bytes += owned - self._tracked_storage.get(layer_idx, 0)
-        self._tracked_storage[layer_idx] = owned
         state = self._attention_states.get(layer_idx)
-        aux = 0 if state is None else state.nbytes
-        self._tracked_aux_bytes += aux - self._tracked_auxiliary.get(layer_idx, 0)
-        self._tracked_auxiliary[layer_idx] = aux
-        shared = 0 if self._shared_decode_workspace is None else self._shared_decode_workspace.nbytes
-        self.peak_nbytes = max(self.peak_nbytes, self._tracked_live_bytes + self._tracked_aux_bytes + shared)
+        now = (layer.packed_nbytes + sum(layer.dense_nbytes()), 0 if state is None else state.nbytes)
+        before = self._owned.get(layer_idx, (0, 0))
+        self._owned[layer_idx] = now
+        self._owned_total += sum(now) - sum(before)
+        shared = self._shared_decode_workspace
+        total = self._owned_total + (0 if shared is None else shared.nbytes)
+        if total > self.peak_nbytes:
+            self.peak_nbytes = total
 
+    # ------------------------------------------------------------ reads
     @torch.no_grad()
     def materialize(self, layer_idx: int = 0):
-        """Dense reconstruction of one layer (not retained by the cache)."""
-        if layer_idx not in self._layers:
+        """Dense (keys, values) of one layer: sink ++ dequantized blocks ++ tail (not retained)."""
+        layer = self._layers.get(layer_idx)
+        if layer is None:
             raise KeyError(f"No cached layer {layer_idx}")
-        layer = self._layers[layer_idx]
+        out = []
+        for side, blocks in ((0, layer.key_blocks), (1, layer.value_blocks)):
+            parts = [rows.buf[side:side + 1, :, rows.start:rows.start + rows.count]
+                     for rows in (layer.sink,) if rows is not None and rows.count]
+            parts += [b.dequantize(dtype=layer.dtype) for b in blocks]
+            if layer.tail is not None and layer.tail.count:
+                parts.append(layer.tail.keys() if side == 0 else layer.tail.values())
+            out.append(torch.cat(parts, 2))
+        return out[0], out[1]
 
-        def restore(sink, blocks, tail):
-            pieces = [] if sink is None else [sink]
-            pieces.extend(block.dequantize(dtype=layer.dtype) for block in blocks)
-            if tail is not None:
-                pieces.append(tail)
-            return torch.cat(pieces, dim=2)
+    # ------------------------------------------------------------ accounting (cache.py:346-394)
+    def _blocks(self):
+        for layer in self._layers.values():
+            yield from layer.key_blocks
+            yield from layer.value_blocks
 
-        return (restore(layer.sink_key, layer.key_blocks, layer.residual_key),
-                restore(layer.sink_value, layer.value_blocks, layer.residual_value))
-
-    # ---- accounting
     @property
     def payload_nbytes(self) -> int:
-        return sum(b.payload_nbytes for layer in self._layers.values() for b in layer.key_blocks + layer.value_blocks)
+        return sum(b.payload_nbytes for b in self._blocks())
 
     @property
     def metadata_nbytes(self) -> int:
-        return sum(b.metadata_nbytes for layer in self._layers.values()
-                   for b in layer.key_blocks + layer.value_blocks)
+        return sum(b.metadata_nbytes for b in self._blocks())
 
     @property
     def residual_nbytes(self) -> int:
-        return sum(_tensor_bytes(l.residual_key) + _tensor_bytes(l.residual_value) for l in self._layers.values())
+        return sum(layer.dense_nbytes()[1] for layer in self._layers.values())
 
     @property
     def sink_nbytes(self) -> int:
-        return sum(_tensor_bytes(l.sink_key) + _tensor_bytes(l.sink_value) for l in self._layers.values())
+        return sum(layer.dense_nbytes()[0] for layer in self._layers.values())
 
     @property
     def auxiliary_nbytes(self) -> int:
-        shared = 0 if self._shared_decode_workspace is None else self._shared_decode_workspace.nbytes
-        return shared + sum(state.nbytes for state in self._attention_states.values())
+        shared = self._shared_decode_workspace
+        return (0 if shared is None else shared.nbytes) + sum(s.nbytes for s in self._attention_states.values())
 
     @property
     def nbytes(self) -> int:
-        return (self.payload_nbytes + self.metadata_nbytes + self.residual_nbytes + self.sink_nbytes
-                + self.auxiliary_nbytes)
+        """Live persistent bytes: packed blocks, exact sink and tail rows, decode state."""
+        return self.payload_nbytes + self.metadata_nbytes + self.residual_nbytes + self.sink_nbytes \
+            + self.auxiliary_nbytes
 
     @property
     def bf16_nbytes(self) -> int:
-        return sum(4 * l.shape[0] * l.shape[1] * l.seq_length * l.shape[3] for l in self._layers.values())
+        return sum(2 * 2 * l.shape[1] * l.seq_length * l.shape[3] for l in self._layers.values())
 
     def memory_stats(self) -> dict:
-        total, baseline = self.nbytes, self.bf16_nbytes
+        total, dense = self.nbytes, self.bf16_nbytes
         return {
             "nbytes": total,
             "peak_nbytes": self.peak_nbytes if self.config.track_peak_bytes else None,
@@ -387,20 +541,23 @@ class InQuantCache(_HFCache):
             "residual_nbytes": self.residual_nbytes,
             "sink_nbytes": self.sink_nbytes,
             "auxiliary_nbytes": self.auxiliary_nbytes,
-            "bf16_nbytes": baseline,
+            "bf16_nbytes": dense,
             "quantized_layer_tokens": sum(b.shape[2] for l in self._layers.values() for b in l.key_blocks),
-            "kv_reduction_vs_bf16": 1 - total / baseline if baseline else 0.0,
+            "kv_reduction_vs_bf16": (1 - total / dense) if dense else 0.0,
+            # preallocated dense rows not yet holding tokens (not part of nbytes)
+            "dense_reserve_nbytes": sum(l.reserved_nbytes() for l in self._layers.values()),
         }
 
     def reset(self) -> None:
         self._layers.clear()
         self._attention_states.clear()
         self._shared_decode_workspace = None
-        self._tracked_storage.clear()
-        self._tracked_auxiliary.clear()
-        self._tracked_live_bytes = self._tracked_aux_bytes = self.peak_nbytes = 0
+        self._owned.clear()
+        self._owned_total = 0
+        self.peak_nbytes = 0
         self._seen_tokens = 0
-        self._checked_position = None
+        self._flags = None
+        self._position_checked = None
 
     def release(self) -> None:
         self.reset()

@@ -50,6 +50,23 @@ class CodecConfig:
             raise ValueError("donor_policy must be neighbors or min_error")
 
 
+def _view_nbytes(t: torch.Tensor) -> int:
+    """Bytes a field occupies.  A field is either an owned compact tensor
+    (its whole storage) or a per-block view of a batched encode; the views
+    of one encode tile its storage exactly, so summing them counts every
+    stored byte once (the reference clones each block and counts storage,
+    codec.py:98-110, with the same totals)."""
+    return t.numel() * t.element_size()
+
+
+def _per_block(packed, count: int, shape, cls, **extra) -> list:
+    """Per-block objects whose fields are views of a batched [count, H, ...] encode."""
+    names = list(packed.tensors)
+    pieces = [t.split(1) for t in packed.tensors.values()]
+    return [cls(**dict(zip(names, parts)), shape=shape, original_dtype=packed.original_dtype, **extra)
+            for parts in zip(*pieces)]
+
+
 @dataclass(frozen=True)
 class PackedTensor:
     """One packed K4 tensor; layout of codec.py:58-110.
@@ -74,11 +91,11 @@ class PackedTensor:
 
     @property
     def payload_nbytes(self) -> int:
-        return self.payload.untyped_storage().nbytes()
+        return _view_nbytes(self.payload)
 
     @property
     def nbytes(self) -> int:
-        return sum(t.untyped_storage().nbytes() for t in self.tensors.values())
+        return sum(_view_nbytes(t) for t in self.tensors.values())
 
     @property
     def metadata_nbytes(self) -> int:
@@ -86,13 +103,12 @@ class PackedTensor:
 
     def storage_stats(self) -> dict:
         dense = math.prod(self.shape) * self.original_dtype.itemsize
-        descriptors = (self.salient_channels.untyped_storage().nbytes()
-                       + self.donor_channels.untyped_storage().nbytes())
+        descriptors = _view_nbytes(self.salient_channels) + _view_nbytes(self.donor_channels)
         return {
             "payload_nbytes": self.payload_nbytes,
-            "scale_nbytes": self.scales.untyped_storage().nbytes(),
+            "scale_nbytes": _view_nbytes(self.scales),
             "descriptor_nbytes": descriptors,
-            "padding_nbytes": self.padding.untyped_storage().nbytes(),
+            "padding_nbytes": _view_nbytes(self.padding),
             "metadata_nbytes": self.metadata_nbytes,
             "nbytes": self.nbytes,
             "source_nbytes": dense,

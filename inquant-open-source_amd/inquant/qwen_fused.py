@@ -1,193 +1,202 @@
-"""Instance-local Qwen2.5 / Mistral single-token decode over packed KV (MI355X).
+"""Packed single-token decode for Hugging Face Qwen2 / Mistral models (MI355X).
 
-Drop-in for the reference's inquant.qwen_fused (qwen_fused.py:1-188): the
-same entry points (enable_fused_attention / enable_fused_qwen2 /
-enable_fused_mistral), handle (fused_decode_calls, cpu_reference_calls,
-restore(), context manager) and eligibility rules.  Prefill, masked or
-multi-token calls and other cache types keep the model's own forward; a
-single-token step with an InQuantCache appends the token and runs the fused
-HIP decode through PackedDecodeState.
+Drop-in for the reference's ``inquant.qwen_fused`` (src/inquant/qwen_fused.py):
+``enable_fused_attention``, ``enable_fused_qwen2`` and ``enable_fused_mistral``
+patch the attention modules of one model instance and return a handle with
+``fused_decode_calls``, ``cpu_reference_calls``, ``restore()`` and context
+manager support.  The eligibility rules and error messages are the
+reference's; the structure is this build's own:
 
-The attention keyword is `past_key_value` in Transformers 4.53 and
-`past_key_values` in 5.x; both are accepted.  There is no CPU decode path in
-this build (the codec runs on the GPU only), so `allow_cpu_reference` keeps
-its meaning for the head-size check but a CPU tensor still raises.
+* every attention module gets a ``_PackedAttention`` object as its forward;
+  it hands prefill, masked, multi-token and non-InQuant calls to the saved
+  original forward untouched;
+* an eligible decode step projects q/k/v, applies the model's RoPE, appends
+  the token with ``InQuantCache.append_for_attention`` (one in-place tail
+  write), brings the layer's ``PackedDecodeState`` up to date with the blocks
+  sealed so far and runs the fused HIP decode, then ``o_proj``.
+
+Transformers 4.53 passes the cache as ``past_key_value`` and 5.x as
+``past_key_values``; the keyword is read from the module's signature.  There
+is no CPU decode: a CPU step raises (``allow_cpu_reference`` only lifts the
+head-size check, as in the reference).
 """
 from __future__ import annotations
 
+import importlib
 import inspect
-from dataclasses import dataclass
-from types import MethodType
 from typing import Any
 
 import torch
-import torch.nn.functional as F
 
-from .cache import InQuantCache, PackedAttentionView
+from .cache import InQuantCache
 
-
-def _reference_decode(query: torch.Tensor, view: PackedAttentionView, scale: float) -> torch.Tensor:
-    """Test oracle (qwen_fused.py:21-30): materializes every old block and runs SDPA in fp32."""
-    def restore(sink, blocks, tail):
-        pieces = [] if sink is None else [sink]
-        pieces.extend(block.dequantize(dtype=query.dtype) for block in blocks)
-        pieces.append(tail)
-        return torch.cat(pieces, dim=2)
-    key = restore(view.sink_key, view.key_blocks, view.residual_key)
-    value = restore(view.sink_value, view.value_blocks, view.residual_value)
-    groups = query.shape[1] // key.shape[1]
-    key = key.float().repeat_interleave(groups, dim=1)
-    value = value.float().repeat_interleave(groups, dim=1)
-    return F.scaled_dot_product_attention(query.float(), key, value, scale=scale).to(query.dtype)
+_FAMILIES = {
+    "qwen2": ("transformers.models.qwen2.modeling_qwen2", "Qwen2Attention"),
+    "mistral": ("transformers.models.mistral.modeling_mistral", "MistralAttention"),
+}
+_INTERFACE_ERROR = "Unsupported Transformers attention interface; validated versions are 4.53.x and 5.x"
 
 
-@dataclass
-class _KernelState:
-    kernel: Any
+def _attention_family(model):
+    """(attention class, apply_rotary_pos_emb) of a dense Qwen2 or Mistral model."""
+    kind = getattr(model.config, "model_type", None)
+    if kind not in _FAMILIES:
+        raise ValueError("Expected a dense Qwen2 or Mistral model")
+    if kind == "mistral" and getattr(model.config, "sliding_window", None) is not None:
+        raise ValueError("Mistral sliding-window attention requires a window-aware cache and is not supported")
+    module_name, class_name = _FAMILIES[kind]
+    module = importlib.import_module(module_name)
+    return getattr(module, class_name), module.apply_rotary_pos_emb
 
-    @property
-    def nbytes(self) -> int:
-        return self.kernel.nbytes
+
+def _cache_keyword(forward) -> str:
+    params = inspect.signature(forward).parameters
+    if "position_embeddings" not in params:
+        raise RuntimeError(_INTERFACE_ERROR)
+    for name in ("past_key_values", "past_key_value"):
+        if name in params:
+            return name
+    raise RuntimeError(_INTERFACE_ERROR)
 
 
-@dataclass
+def _layer_state(cache: InQuantCache, layer: int, view):
+    """The layer's decode state, extended with blocks sealed since the last step."""
+    from .triton_attention import PackedDecodeState, SharedDecodeWorkspace
+    state = cache._attention_states.get(layer)
+    if state is None:
+        if cache.config.shared_workspace and cache._shared_decode_workspace is None:
+            cache._shared_decode_workspace = SharedDecodeWorkspace()
+        state = PackedDecodeState(view.key_blocks, view.value_blocks,
+                                  workspace_pool=cache._shared_decode_workspace)
+        cache._attention_states[layer] = state
+    elif len(state.key_blocks) != len(view.key_blocks):
+        state.extend(view.key_blocks, view.value_blocks)
+    return state
+
+
+class _PackedAttention:
+    """Forward of one patched attention module."""
+
+    def __init__(self, module, rotary, cache_keyword: str):
+        self.module = module
+        self.rotary = rotary
+        self.cache_keyword = cache_keyword
+        self.own_forward = "forward" in vars(module)    # an instance attribute to put back on restore
+        self.original = module.forward
+        self.fused_calls = 0
+        self.cpu_reference_calls = 0
+
+    def __call__(self, hidden_states, position_embeddings, attention_mask=None, *args, **kwargs):
+        cache = kwargs.get(self.cache_keyword)
+        eligible = (isinstance(cache, InQuantCache) and hidden_states.shape[1] == 1
+                    and attention_mask is None and not kwargs.get("output_attentions", False)
+                    and cache.get_seq_length(self.module.layer_idx) > 0)
+        if not eligible:
+            return self.original(hidden_states, position_embeddings, attention_mask, *args, **kwargs)
+        return self._step(cache, hidden_states, position_embeddings, kwargs.get("cache_position"))
+
+    def _step(self, cache, hidden, position_embeddings, cache_position):
+        attn = self.module
+        if attn.training or torch.is_grad_enabled():
+            raise RuntimeError("Packed decode is inference-only; use model.eval() and torch.no_grad()")
+        if hidden.shape[0] != 1:
+            raise ValueError("Packed decode supports batch size 1 only")
+        if hidden.device.type != "cuda":
+            raise RuntimeError("Packed decode requires CUDA (ROCm) tensors; this build has no CPU decode path")
+        split = (1, 1, -1, attn.head_dim)
+        q = attn.q_proj(hidden).view(split).transpose(1, 2)
+        k = attn.k_proj(hidden).view(split).transpose(1, 2)
+        v = attn.v_proj(hidden).view(split).transpose(1, 2)
+        cos, sin = position_embeddings
+        q, k = self.rotary(q, k, cos, sin)
+        extra = {"sin": sin, "cos": cos}
+        if cache_position is not None:
+            extra["cache_position"] = cache_position
+        layer = attn.layer_idx
+        view = cache.append_for_attention(k, v, layer, extra)
+        out = _layer_state(cache, layer, view).decode(
+            q, sink_key=view.sink_key, sink_value=view.sink_value, residual_key=view.residual_key,
+            residual_value=view.residual_value, scale=attn.scaling)
+        cache.record_peak(layer)
+        self.fused_calls += 1
+        # [1, Hq, 1, D] contiguous is already the [1, 1, Hq * D] row o_proj takes
+        return attn.o_proj(out.view(1, 1, -1)), None
+
+    def remove(self) -> None:
+        if self.own_forward:
+            self.module.forward = self.original
+        else:
+            del self.module.forward
+        del self.module._inquant_patch
+
+
 class FusedQwen2Handle:
-    """Owns only this model's forward overrides; restore removes them."""
-    originals: list[tuple[Any, Any]]
-    restored: bool = False
+    """The patches of one model; ``restore()`` (or leaving the ``with`` block) removes them."""
+
+    def __init__(self, patches: list[_PackedAttention]):
+        self._patches = patches
+        self.restored = False
 
     @property
     def fused_decode_calls(self) -> int:
-        return sum(getattr(module, "_inquant_fused_decode_calls", 0) for module, _ in self.originals)
+        return sum(p.fused_calls for p in self._patches)
 
     @property
     def cpu_reference_calls(self) -> int:
-        return sum(getattr(module, "_inquant_cpu_reference_calls", 0) for module, _ in self.originals)
+        return sum(p.cpu_reference_calls for p in self._patches)
 
     def restore(self) -> None:
-        if self.restored:
-            return
-        for module, original in self.originals:
-            module.forward = original
-            delattr(module, "_inquant_original_forward")
-        self.restored = True
+        if not self.restored:
+            for patch in self._patches:
+                patch.remove()
+            self.restored = True
 
     def __enter__(self) -> "FusedQwen2Handle":
         return self
 
-    def __exit__(self, *_args) -> None:
+    def __exit__(self, *exc) -> None:
         self.restore()
 
 
-def _cache_keyword(module) -> str:
-    params = inspect.signature(module.forward).parameters
-    if "past_key_values" in params:
-        return "past_key_values"
-    if "past_key_value" in params:
-        return "past_key_value"
-    raise RuntimeError("Unsupported Transformers attention interface; validated versions are 4.53.x and 5.x")
-
-
 def enable_fused_attention(model: Any, *, allow_cpu_reference: bool = False) -> FusedQwen2Handle:
-    """Patch this instantiated model only; its weights and prefill forward stay.
+    """Patch the attention modules of this model instance (weights and prefill untouched).
 
-    The accelerated path requires a ROCm device, head_dim=128, batch=1,
-    q_len=1, full attention, no padding mask and an InQuantCache.  Other
-    query lengths and cache types keep the original forward.
-    """
-    model_type = getattr(model.config, "model_type", None)
-    if model_type == "qwen2":
-        from transformers.models.qwen2.modeling_qwen2 import Qwen2Attention as Attention, apply_rotary_pos_emb
-    elif model_type == "mistral":
-        from transformers.models.mistral.modeling_mistral import MistralAttention as Attention, apply_rotary_pos_emb
-        if getattr(model.config, "sliding_window", None) is not None:
-            raise ValueError("Mistral sliding-window attention requires a window-aware cache and is not supported")
-    else:
-        raise ValueError("Expected a dense Qwen2 or Mistral model")
+    Decode steps take the packed path when the cache is an InQuantCache, the
+    batch and query length are 1, there is no attention mask and the module
+    is not windowed; the HIP kernel needs head_dim 128."""
+    attention_class, rotary = _attention_family(model)
     if model.training:
         raise ValueError("Call model.eval() before enabling inference-only packed decode")
     modules = [layer.self_attn for layer in model.model.layers]
-    keyword = None
+    keywords = []
     for module in modules:
-        if not isinstance(module, Attention):
+        if not isinstance(module, attention_class):
             raise TypeError("Expected an unmodified attention instance for this model family")
-        if hasattr(module, "_inquant_original_forward"):
+        if hasattr(module, "_inquant_patch"):
             raise ValueError("This model already has fused InQuant decode enabled")
-        if "position_embeddings" not in inspect.signature(module.forward).parameters:
-            raise RuntimeError("Unsupported Transformers attention interface; validated versions are 4.53.x and 5.x")
-        keyword = _cache_keyword(module)
+        keywords.append(_cache_keyword(module.forward))
         if getattr(module, "sliding_window", None) is not None:
             raise ValueError("Sliding-window attention is unsupported by packed decode")
-        if not allow_cpu_reference and module.head_dim != 128:
+        if module.head_dim != 128 and not allow_cpu_reference:
             raise ValueError("The packed decode kernel currently requires head_dim=128")
-
-    def forward(attention, hidden_states: torch.Tensor, position_embeddings, attention_mask=None, *args, **kwargs):
-        cache = kwargs.get(keyword)
-        cache_position = kwargs.get("cache_position")
-        use_packed = (
-            isinstance(cache, InQuantCache)
-            and hidden_states.shape[1] == 1
-            and cache.get_seq_length(attention.layer_idx) > 0
-            and attention_mask is None
-            and not kwargs.get("output_attentions", False)
-        )
-        if not use_packed:
-            return attention._inquant_original_forward(hidden_states, position_embeddings, attention_mask,
-                                                       *args, **kwargs)
-        if attention.training or torch.is_grad_enabled():
-            raise RuntimeError("Packed decode is inference-only; use model.eval() and torch.no_grad()")
-        if hidden_states.shape[0] != 1:
-            raise ValueError("Packed decode supports batch size 1 only")
-        if hidden_states.device.type != "cuda":
-            raise RuntimeError("Packed decode requires CUDA (ROCm) tensors; this build has no CPU decode path")
-        input_shape = hidden_states.shape[:-1]
-        hidden_shape = (*input_shape, -1, attention.head_dim)
-        query = attention.q_proj(hidden_states).view(hidden_shape).transpose(1, 2)
-        key = attention.k_proj(hidden_states).view(hidden_shape).transpose(1, 2)
-        value = attention.v_proj(hidden_states).view(hidden_shape).transpose(1, 2)
-        cos, sin = position_embeddings
-        query, key = apply_rotary_pos_emb(query, key, cos, sin)
-        cache_kwargs = {"sin": sin, "cos": cos}
-        if cache_position is not None:
-            cache_kwargs["cache_position"] = cache_position
-        view = cache.append_for_attention(key, value, attention.layer_idx, cache_kwargs)
-        from .triton_attention import PackedDecodeState, SharedDecodeWorkspace
-        if cache.config.shared_workspace and cache._shared_decode_workspace is None:
-            cache._shared_decode_workspace = SharedDecodeWorkspace()
-        state = cache._attention_states.get(attention.layer_idx)
-        if state is None:
-            state = _KernelState(PackedDecodeState(view.key_blocks, view.value_blocks,
-                                                   workspace_pool=cache._shared_decode_workspace))
-            cache._attention_states[attention.layer_idx] = state
-        elif len(state.kernel.key_blocks) != len(view.key_blocks):
-            state.kernel.extend(view.key_blocks, view.value_blocks)
-        result = state.kernel.decode(query, sink_key=view.sink_key, sink_value=view.sink_value,
-                                     residual_key=view.residual_key, residual_value=view.residual_value,
-                                     scale=attention.scaling)
-        cache.record_peak(attention.layer_idx)
-        attention._inquant_fused_decode_calls += 1
-        output = result.transpose(1, 2).reshape(*input_shape, -1).contiguous()
-        return attention.o_proj(output), None
-
-    originals = []
-    for module in modules:
-        originals.append((module, module.forward))
-        module._inquant_original_forward = module.forward
-        module._inquant_fused_decode_calls = 0
-        module._inquant_cpu_reference_calls = 0
-        module.forward = MethodType(forward, module)
-    return FusedQwen2Handle(originals)
+    patches = []
+    for module, keyword in zip(modules, keywords):
+        patch = _PackedAttention(module, rotary, keyword)
+        module._inquant_patch = patch
+        module.forward = patch
+        patches.append(patch)
+    return FusedQwen2Handle(patches)
 
 
 def enable_fused_qwen2(model: Any, *, allow_cpu_reference: bool = False) -> FusedQwen2Handle:
-    """Backward-compatible Qwen-only entry point."""
+    """Qwen2 / Qwen2.5 only."""
     if getattr(model.config, "model_type", None) != "qwen2":
         raise ValueError("Expected a dense Qwen2/Qwen2.5 model")
     return enable_fused_attention(model, allow_cpu_reference=allow_cpu_reference)
 
 
 def enable_fused_mistral(model: Any, *, allow_cpu_reference: bool = False) -> FusedQwen2Handle:
-    """Mistral full-attention entry point; keeps the native projections and RoPE."""
+    """Mistral with full attention only."""
     if getattr(model.config, "model_type", None) != "mistral":
         raise ValueError("Expected a dense Mistral model")
     return enable_fused_attention(model, allow_cpu_reference=allow_cpu_reference)

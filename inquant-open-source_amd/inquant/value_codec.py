@@ -12,6 +12,7 @@ from dataclasses import dataclass
 import torch
 
 from . import _native as nat
+from .codec import _per_block, _view_nbytes
 
 
 @dataclass(frozen=True)
@@ -30,11 +31,11 @@ class PackedValues:
 
     @property
     def payload_nbytes(self) -> int:
-        return self.payload.untyped_storage().nbytes()
+        return _view_nbytes(self.payload)
 
     @property
     def nbytes(self) -> int:
-        return sum(t.untyped_storage().nbytes() for t in self.tensors.values())
+        return sum(_view_nbytes(t) for t in self.tensors.values())
 
     @property
     def metadata_nbytes(self) -> int:
@@ -94,24 +95,18 @@ def quantize_values(x: torch.Tensor, bits: int = 2, group_size: int = 64, *,
 
 
 def quantize_value_blocks(tensor: torch.Tensor, block_count: int, block_size: int, bits: int, group_size: int):
-    """Encode `block_count` leading temporal blocks of [1, H, T, D] as separately owned PackedValues."""
+    """Encode the first `block_count` temporal blocks of [1, H, T, D] with
+    statistics per (block, head) (value_codec.py:75-88): one launch over the
+    strided [blocks, H, B, D] view, one PackedValues view per block."""
     return _value_blocks(tensor, block_count, block_size, bits, group_size, None)
 
 
 def _value_blocks(tensor, block_count, block_size, bits, group_size, bad):
-    """quantize_value_blocks with the private flag of quantize_values."""
+    """quantize_value_blocks with the private non-finite flag of quantize_values."""
     if not block_count:
         return []
-    if block_count == 1:
-        return [quantize_values(tensor[:, :, :block_size], bits, group_size, _flag=bad)]
-    _, heads, _, channels = tensor.shape
-    # [nb, H, B, D] view of the first nb*B tokens; the kernel reads it in place
-    blocked = tensor[0, :, :block_count * block_size].reshape(heads, block_count, block_size, channels).permute(1, 0, 2, 3)
+    _, heads, _, dim = tensor.shape
+    blocked = tensor[0, :, :block_count * block_size].unflatten(1, (block_count, block_size)).transpose(0, 1)
     packed = quantize_values(blocked, bits, group_size, _flag=bad)
-    out = []
-    for i in range(block_count):
-        fields = {name: t[i:i + 1].clone(memory_format=torch.contiguous_format)
-                  for name, t in packed.tensors.items()}
-        out.append(PackedValues(**fields, shape=(1, heads, block_size, channels), original_dtype=tensor.dtype,
-                                bits=bits, group_size=group_size))
-    return out
+    return _per_block(packed, block_count, (1, heads, block_size, dim), PackedValues, bits=bits,
+                      group_size=group_size)

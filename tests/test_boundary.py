@@ -118,32 +118,25 @@ def test_cache_update_validation_runs_on_host():
     assert cache.get_seq_length() == 0 and cache.nbytes == 0
 
 
-def test_shared_position_tensor_is_read_once_per_expected_start():
-    # Host logic only: no block is sealed, so no codec call is made.  One
-    # cache_position shared by two layers is read for the first; an in-place
-    # change, another expected start or reset() makes it read again.
+def test_cache_positions_and_dense_rows_on_the_host():
+    # Host logic only (CPU tensors, no block sealed, so no codec call): a
+    # wrong position raises and changes nothing, the sink and tail rows hold
+    # the exact tokens, reset() forgets the checked position
     from inquant.cache import CacheConfig, InQuantCache
     cache = InQuantCache(CacheConfig())
-    x = torch.zeros(1, 1, 6, 8)
+    x = torch.arange(6 * 8, dtype=torch.float32).view(1, 1, 6, 8)
     for layer in (0, 1):
         cache.update(x, x, layer, {"cache_position": torch.arange(6)})
-    cache.update(x[:, :, :5], x[:, :, :5], 2, {"cache_position": torch.arange(5)})
-    t = x[:, :, :1]
-    p = torch.tensor([6])
-    reads = []
-    original = p.cpu
-    p.cpu = lambda *a, **k: reads.append(1) or original(*a, **k)
-    for layer in (0, 1):
-        cache.append_for_attention(t, t, layer, {"cache_position": p})
-    assert len(reads) == 1
+    t = x[:, :, :1] + 100
     with pytest.raises(ValueError, match="contiguous append positions"):
-        cache.append_for_attention(t, t, 2, {"cache_position": p})
-    assert len(reads) == 2 and cache.get_seq_length(2) == 5
-    p += 1
-    cache.append_for_attention(t, t, 0, {"cache_position": p})
-    assert len(reads) == 3
+        cache.append_for_attention(t, t, 0, {"cache_position": torch.tensor([5])})
+    assert cache.get_seq_length(0) == 6
+    view = cache.append_for_attention(t, t, 0, {"cache_position": torch.tensor([6])})
+    assert view.seq_length == 7 and torch.equal(view.residual_key[:, :, -1:], t)
+    assert torch.equal(view.sink_key, x[:, :, :4]) and torch.equal(view.residual_key[:, :, :2], x[:, :, 4:])
+    assert cache.residual_nbytes == 2 * (3 + 2) * 8 * 4 and cache.sink_nbytes == 2 * 2 * 4 * 8 * 4
     cache.reset()
-    assert cache._checked_position is None
+    assert cache._position_checked is None and cache.nbytes == 0
 
 
 def test_decode_state_validation_without_gpu():

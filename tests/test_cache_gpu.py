@@ -38,9 +38,15 @@ def test_prefill_exact_small_tail_storage_and_accounting():
     returned_key, returned_value = cache.update(key, value, 0)
     assert returned_key is key and returned_value is value
     layer = cache._layers[0]
+    # the exact rows live in the cache's own [2, H, rows, D] buffers (never a
+    # view of the prefill input); accounting counts the live rows, and the
+    # unfilled part of the preallocated tail is reported separately
     for item in (layer.sink_key, layer.sink_value, layer.residual_key, layer.residual_value):
-        assert item.untyped_storage().nbytes() == item.numel() * item.element_size()
         assert item.untyped_storage().data_ptr() != key.untyped_storage().data_ptr()
+    assert cache.sink_nbytes == 2 * 2 * 2 * 8 * 4 and cache.residual_nbytes == 2 * 2 * 3 * 8 * 4
+    assert torch.equal(layer.sink_key, key[:, :, :2]) and torch.equal(layer.residual_value, value[:, :, -3:])
+    held = layer.tail.buf.untyped_storage().nbytes() + layer.sink.buf.untyped_storage().nbytes()
+    assert cache.memory_stats()["dense_reserve_nbytes"] == held - cache.sink_nbytes - cache.residual_nbytes
     packed_bytes = sum(block.nbytes for block in layer.key_blocks + layer.value_blocks)
     assert cache.nbytes == packed_bytes + cache.sink_nbytes + cache.residual_nbytes
     assert cache.bf16_nbytes == 2 * key.numel() * 2
@@ -121,7 +127,7 @@ def test_batched_prefill_matches_serial_blocks_and_owns_compact_storage(dtype):
     assert tuple(observed.call_args_list[0].args[0].shape) == (6, 3, 8, 16)
     layer = cache._layers[0]
     expected_bytes = 0
-    owned = set()
+    ranges, storages = [], {}
     for original, blocks in ((key, layer.key_blocks), (value, layer.value_blocks)):
         assert len(blocks) == 6
         for index, actual in enumerate(blocks):
@@ -132,13 +138,17 @@ def test_batched_prefill_matches_serial_blocks_and_owns_compact_storage(dtype):
             expected_bytes += serial.nbytes
             for name, tensor in actual.tensors.items():
                 torch.testing.assert_close(tensor, serial.tensors[name], rtol=0, atol=0)
-                assert tensor.untyped_storage().nbytes() == tensor.numel() * tensor.element_size()
                 assert tensor.is_contiguous()
                 if tensor.numel():
-                    address = tensor.untyped_storage().data_ptr()
-                    assert address not in owned
-                    owned.add(address)
+                    ranges.append((tensor.data_ptr(), tensor.data_ptr() + tensor.numel() * tensor.element_size()))
+                    st = tensor.untyped_storage()
+                    storages.setdefault(st.data_ptr(), [st.nbytes(), 0])[1] += tensor.numel() * tensor.element_size()
             torch.testing.assert_close(actual.dequantize(), serial.dequantize(), rtol=0, atol=0)
+    # per-block fields are disjoint views that tile their batched allocations
+    # exactly: the counted bytes are every stored byte, once
+    ranges.sort()
+    assert all(a[1] <= b[0] for a, b in zip(ranges, ranges[1:]))
+    assert all(held == counted for held, counted in storages.values())
     assert cache.nbytes == expected_bytes + cache.sink_nbytes + cache.residual_nbytes
 
 
@@ -272,23 +282,13 @@ def test_single_token_position_check():
     assert cache.get_seq_length() == 7
 
 
-def _count_host_copies(position):
-    calls = []
-    original = position.cpu
-
-    def counted(*args, **kwargs):
-        calls.append(1)
-        return original(*args, **kwargs)
-    position.cpu = counted
-    return calls
-
-
 @pytest.mark.parametrize("inference", [False, True])
-def test_shared_cache_position_checked_once_per_step(inference):
-    # The layers of one step share one cache_position tensor: it is copied to
-    # the host for the first layer only, again after an in-place change, and
-    # again for a layer that expects another first position.  Inference-mode
-    # tensors keep no version counter and are copied for every layer.
+def test_shared_cache_position_checked_on_the_device(inference):
+    # The layers of one step share one cache_position tensor.  The first
+    # layer's append synchronizes and raises on a mismatch before anything
+    # changes; the other layers rely on the append kernel's comparison, so
+    # an in-place change of the tensor between layers is reported at the
+    # next synchronizing check (the next step's first layer).
     from inquant.cache import InQuantCache
     cache = InQuantCache(_cfg())
     x = _randn(1, 2, 6, 8, seed=37)
@@ -298,16 +298,39 @@ def test_shared_cache_position_checked_once_per_step(inference):
     t = x[:, :, :1]
     with torch.inference_mode(inference):
         p = torch.tensor([6], device="cuda")
-        calls = _count_host_copies(p)
         for layer in (0, 1):
             cache.append_for_attention(t, t, layer, {"cache_position": p})
-        assert len(calls) == (2 if inference else 1)
+        assert cache._position_checked[0] is p and cache._position_checked[1] == 6
         with pytest.raises(ValueError, match="contiguous append positions"):
-            cache.append_for_attention(t, t, 2, {"cache_position": p})
+            cache.append_for_attention(t, t, 2, {"cache_position": p})   # layer 2 expects 5
         assert cache.get_seq_length(2) == 5
-        p += 1
-        cache.append_for_attention(t, t, 0, {"cache_position": p})
-        p.fill_(3)
+        q = torch.tensor([7], device="cuda")
+        cache.append_for_attention(t, t, 0, {"cache_position": q})
+        q.fill_(3)                                   # changed in place between layers
+        cache.append_for_attention(t, t, 1, {"cache_position": q})    # compared on the device only
+        assert [cache.get_seq_length(i) for i in range(3)] == [8, 8, 5]
         with pytest.raises(ValueError, match="contiguous append positions"):
-            cache.append_for_attention(t, t, 1, {"cache_position": p})
-        assert [cache.get_seq_length(i) for i in range(3)] == [8, 7, 5]
+            cache.append_for_attention(t, t, 0, {"cache_position": torch.tensor([8], device="cuda")})
+        cache.append_for_attention(t, t, 0, {"cache_position": torch.tensor([8], device="cuda")})
+        assert cache.get_seq_length(0) == 9
+
+
+def test_tail_rows_move_once_after_a_seal():
+    # one-token appends write rows in place; after a seal the tail's first
+    # rows are the survivors, moved by the next append; every append view
+    # equals the exact tokens (sink 2, residual 3, blocks of 8)
+    from inquant.cache import InQuantCache
+    cache = InQuantCache(_cfg())
+    k, v = _randn(1, 2, 40, 8, seed=38), _randn(1, 2, 40, 8, seed=39)
+    cache.update(k[:, :, :5], v[:, :, :5], 0)
+    seen = []
+    for pos in range(5, 40):
+        view = cache.append_for_attention(k[:, :, pos:pos + 1], v[:, :, pos:pos + 1], 0,
+                                          {"cache_position": torch.tensor([pos], device="cuda")})
+        sealed = len(view.key_blocks)
+        first = 2 + 8 * sealed
+        assert torch.equal(view.residual_key, k[:, :, first:pos + 1])
+        assert torch.equal(view.residual_value, v[:, :, first:pos + 1])
+        seen.append(cache._layers[0].tail.start)
+    assert 8 in seen and seen[-1] in (0, 8)
+    assert len(cache._layers[0].key_blocks) == (40 - 2 - 3) // 8

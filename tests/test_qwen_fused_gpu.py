@@ -130,11 +130,11 @@ def test_qwen_three_layers_shared_workspace_and_cache_reset(value_bits):
                 actual = model(token, past_key_values=packed).logits
             torch.testing.assert_close(actual, expected, rtol=0, atol=0)
             torch.testing.assert_close(actual.float(), dense.float(), rtol=.035, atol=.015)
-    per_layer = next(iter(independent._attention_states.values())).kernel._workspace.untyped_storage().nbytes()
+    per_layer = next(iter(independent._attention_states.values()))._workspace.untyped_storage().nbytes()
     assert independent.nbytes - packed.nbytes == 2 * per_layer
     for cache in (packed, independent):
         shared = cache._shared_decode_workspace.nbytes if cache._shared_decode_workspace else 0
-        assert cache._tracked_live_bytes + cache._tracked_aux_bytes + shared == cache.nbytes
+        assert cache._owned_total + shared == cache.nbytes
         assert cache.peak_nbytes >= cache.nbytes
     old_pool = packed._shared_decode_workspace
     packed.reset()
