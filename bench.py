@@ -37,6 +37,9 @@ def parse():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--layers", type=int, default=28)
+    ap.add_argument("--rotate", type=int, default=2,
+                    help="independent sets of `layers` layers replayed in turn (2 x 28 layers = 800 MB, "
+                         "above the 512 MiB flush rule), so no step finds its layers in the Infinity Cache")
     ap.add_argument("--blocks", type=int, default=128)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-graph", action="store_true", help="launch layer by layer instead of a HIP graph")
@@ -388,10 +391,13 @@ def time_append(device, H=4, packed_tokens=32768, validate_positions=True):
             "seal_bytes": seal_bytes}
 
 
-def time_append_step(device, H=4, packed_tokens=32768, layers=28, steps=128):
-    """Config 2 append as a model makes it: each decode step appends one token
-    to every layer of a 28-layer cache (32K packed context each, tail 128 ->
-    256, no seal), the layers sharing the step's cache_position tensor."""
+def time_append_step(device, H=4, packed_tokens=32768, layers=28):
+    """Config 2 append as a model makes it: every decode step appends one
+    token to each layer of a 28-layer cache (32K packed context per layer),
+    the layers sharing the step's cache_position tensor.  One full cycle of
+    256 steps is timed (tail 128 -> 383, then the step on which all 28
+    layers seal a 256-token block back to 128): the mean step, the mean of
+    the steps that seal nothing, and the sealing step."""
     import torch
     from inquant.cache import CacheConfig, InQuantCache
     from inquant.codec import CodecConfig
@@ -399,61 +405,122 @@ def time_append_step(device, H=4, packed_tokens=32768, layers=28, steps=128):
     cfg = CacheConfig(codec=CodecConfig(donor_policy="min_error"), value_bits=2, value_group_size=64)
     cache = InQuantCache(cfg)
     n0 = 4 + packed_tokens + 128
-    k = kv_tensor(g, H, n0 + steps, device)
-    v = kv_tensor(g, H, n0 + steps, device)
+    steps = 256
+    k = kv_tensor(g, H, n0 + 2 * steps, device)
+    v = kv_tensor(g, H, n0 + 2 * steps, device)
     for i in range(layers):
         cache.update(k[:, :, :n0], v[:, :, :n0], i)
-    positions = torch.arange(n0 + steps, device=device)
+    positions = torch.arange(n0 + 2 * steps, device=device)
+    times = []
 
-    def run(pos):
-        for _ in range(steps // 2):
-            p = positions[pos:pos + 1]
-            for i in range(layers):
-                cache.append_for_attention(k[:, :, pos:pos + 1], v[:, :, pos:pos + 1], i, {"cache_position": p})
-            pos += 1
-        return pos
-    pos = run(n0)                        # warm allocator blocks (tail 128 -> 192)
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    pos = run(pos)                       # tail 192 -> 256
-    torch.cuda.synchronize()
-    step_us = (time.perf_counter() - t0) * 1e6 / (steps // 2)
-    assert cache.get_seq_length(layers - 1) == n0 + steps
-    return {"layers": layers, "append_step_us": round(step_us, 1),
-            "append_us_per_layer_token": round(step_us / layers, 2)}
+    def step(pos):
+        p = positions[pos:pos + 1]
+        kk, vv = k[:, :, pos:pos + 1], v[:, :, pos:pos + 1]
+        t0 = time.perf_counter()
+        for i in range(layers):
+            cache.append_for_attention(kk, vv, i, {"cache_position": p})
+        torch.cuda.synchronize()
+        return time.perf_counter() - t0
+
+    pos = n0
+    for _ in range(steps):               # one warm cycle (allocator blocks, kernels, views)
+        step(pos)
+        pos += 1
+    for _ in range(steps):
+        times.append(step(pos))
+        pos += 1
+    blocks = len(cache._layers[0].key_blocks)
+    seal_at = max(range(steps), key=lambda i: times[i])
+    plain = [t for i, t in enumerate(times) if i != seal_at]
+    assert cache.get_seq_length(layers - 1) == n0 + 2 * steps and blocks == packed_tokens // 256 + 2
+    return {"layers": layers, "cycle_steps": steps,
+            "append_step_us": round(sum(plain) / len(plain) * 1e6, 1),
+            "append_us_per_layer_token": round(sum(plain) / len(plain) * 1e6 / layers, 2),
+            "sealing_step_us": round(times[seal_at] * 1e6, 1),
+            "cycle_mean_step_us": round(sum(times) / steps * 1e6, 1)}
 
 
-def cpu_baseline(layer):
-    """Time the CPU oracle (dequantize-then-attend, fp64) on a bounded sample of one layer."""
+def _cpu_model() -> str:
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def _timed(fn, budget_s: float, max_reps: int = 200) -> tuple[float, int]:
+    """Seconds per call of fn, repeated until `budget_s` has passed (at least once)."""
+    reps, t0 = 0, time.perf_counter()
+    while True:
+        fn()
+        reps += 1
+        dt = time.perf_counter() - t0
+        if dt >= budget_s or reps >= max_reps:
+            return dt / reps, reps
+
+
+def cpu_baseline(layer, device):
+    """The C oracle (the CPU restatement of the reference's codec and of its
+    dequantize-then-attend decode) timed on this host, on all cores and on
+    one thread, on bounded samples of the benchmark's workloads:
+      decode: one config-2 layer restricted to 16 of its 128 packed blocks
+              (+ sink and tail): K4/V2 dequantize to bf16, fp64 attention;
+      encode: K4 min_error + V2 g64 of 8 blocks x 8 heads of a config-3 layer
+              (2048 tokens of the 32768)."""
     import numpy as np
+    import torch
     sys.path.insert(0, ROOT)
     sys.path.insert(0, os.path.join(ROOT, "tests"))
     from oracle import oracle
     from kvcase import oracle_dequant_k4, oracle_dequant_v, to_np
+    from dataclasses import replace
     cores = len(os.sched_getaffinity(0))
-    n = min(16, len(layer["kb"]))          # sample: 16 of the 128 blocks + sink + tail
+    n = min(16, len(layer["kb"]))
     kb, vb = layer["kb"][:n], layer["vb"][:n]
     q = to_np(layer["q"])[0, :, 0]
     sink_k, sink_v = to_np(layer["sink_k"])[0], to_np(layer["sink_v"])[0]
     tail_k, tail_v = to_np(layer["tail_k"])[0], to_np(layer["tail_v"])[0]
-    from dataclasses import replace
-    # host copies of the packed blocks (the oracle reads numpy arrays)
     blocks = [(replace(k, **{f: t.cpu() for f, t in k.tensors.items()}),
                replace(v, **{f: t.cpu() for f, t in v.tensors.items()})) for k, v in zip(kb, vb)]
-    reps, t0 = 0, time.perf_counter()
-    while True:
+
+    def decode():
         ks = [sink_k] + [oracle_dequant_k4(k, "bfloat16") for k, _ in blocks] + [tail_k]
         vs = [sink_v] + [oracle_dequant_v(v, "bfloat16") for _, v in blocks] + [tail_v]
         oracle.attend(q, np.concatenate(ks, 1), np.concatenate(vs, 1), 128 ** -0.5)
-        reps += 1
-        if time.perf_counter() - t0 > 10.0 or reps >= 50:
-            break
-    dt = (time.perf_counter() - t0) / reps
-    frac = n / len(layer["kb"])
-    sample_bytes = algorithmic_bytes(layer) * frac   # packed part scales with the block sample
-    return {"value": sample_bytes / dt / 1e9, "unit": "GB/s", "cores": cores, "kind": "port",
-            "sample": f"1 layer, {n} of {len(layer['kb'])} packed blocks (+sink, tail): oracle K4/V2 dequantize "
-                      f"to bf16 then fp64 attention, {reps} reps, {dt * 1e3:.1f} ms each, OpenMP {cores} threads"}
+
+    g = torch.Generator(device=device).manual_seed(33)
+    enc_blocks, H, B = 8, 8, 256
+    kx = kv_tensor(g, H, enc_blocks * B, device, frac_groups=(3, 3, 3, 1))
+    vx = kv_tensor(g, H, enc_blocks * B, device, frac_groups=(3, 3, 3, 1))
+    kx = np.ascontiguousarray(kx[0].float().reshape(H, enc_blocks, B, 128).transpose(0, 1).cpu().numpy())
+    vx = np.ascontiguousarray(vx[0].float().reshape(H, enc_blocks, B, 128).transpose(0, 1).cpu().numpy())
+
+    def encode():
+        oracle.k4_quantize(kx, 8, 0.125, "min_error")
+        oracle.v_quantize(vx, 2, 64)
+
+    sample_bytes = algorithmic_bytes(layer) * n / len(layer["kb"])
+    enc_tokens = enc_blocks * B
+    result = {}
+    for threads, tag in ((cores, ""), (1, "_1t")):
+        oracle.set_threads(threads)
+        dec_s, dec_reps = _timed(decode, 4.0)
+        enc_s, enc_reps = _timed(encode, 4.0)
+        result["decode_gbs" + tag] = sample_bytes / dec_s / 1e9
+        result["encode_mtok_s" + tag] = enc_tokens / enc_s / 1e6
+        result["reps" + tag] = [dec_reps, enc_reps]
+    oracle.set_threads(cores)
+    return {"value": round(result["decode_gbs"], 4), "unit": "GB/s", "cores": cores, "kind": "port",
+            "sample": f"decode: 1 config-2 layer, {n} of {len(layer['kb'])} packed blocks + sink + tail, oracle "
+                      f"K4/V2 dequantize to bf16 then fp64 attention; encode: K4 min_error + V2 g64 of "
+                      f"{enc_blocks} blocks x {H} heads (config 3); ~4 s per leg per thread count",
+            "cpu_model": _cpu_model(),
+            "decode_gbs_1thread": round(result["decode_gbs_1t"], 4),
+            "encode_mtok_s": round(result["encode_mtok_s"], 4),
+            "encode_mtok_s_1thread": round(result["encode_mtok_s_1t"], 4),
+            "reps": {"all_cores": result["reps"], "one_thread": result["reps_1t"]}}
 
 
 def main():
@@ -471,11 +538,14 @@ def main():
         sys.exit(2)
     device = "cuda:0"
     torch.cuda.set_device(0)
-    layers = [build_layer(1000 + i, device, n_blocks=args.blocks) for i in range(args.layers)]
+    rotate = max(1, args.rotate)
+    layers = [build_layer(1000 + i, device, n_blocks=args.blocks) for i in range(args.layers * rotate)]
     torch.cuda.synchronize()
     per_layer = algorithmic_bytes(layers[0])
-    step_bytes = sum(algorithmic_bytes(l) for l in layers)
-    ms, _ = time_decode(layers, args.steps, args.warmup, not args.no_graph)
+    step_bytes = sum(algorithmic_bytes(l) for l in layers) / rotate
+    # one replay runs `rotate` steps, each over its own set of layers
+    ms_replay, _ = time_decode(layers, args.steps, args.warmup, not args.no_graph)
+    ms = ms_replay / rotate
     gbs = step_bytes / (ms * 1e-3) / 1e9
     layer_us = ms * 1e3 / args.layers
     achieved = per_layer / (layer_us * 1e-6) / 1e9
@@ -502,7 +572,8 @@ def main():
         "data": "synthetic (N(0,1) bf16 KV with 4% x20 outlier channel runs, seeded per layer)",
         "config": {"workload": "cfg2: Qwen2.5-7B decode, 28 layers x (32768 packed K4/V2 tokens in 256-token "
                                "blocks + 4 BF16 sink + 128 BF16 tail), Hq=28, H_kv=4, D=128, batch 1",
-                   "layers": args.layers, "packed_tokens": args.blocks * 256, "graph": not args.no_graph},
+                   "layers": args.layers, "packed_tokens": args.blocks * 256, "graph": not args.no_graph,
+                   "rotated_sets": rotate, "rotated_bytes": int(step_bytes * rotate)},
         "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
         "decode_us_per_layer": round(layer_us, 3),
         "decode_tokens_per_s": round(1e3 / ms, 2),
@@ -519,7 +590,7 @@ def main():
     if paged is not None:
         result["paged_cfg4"] = paged
     if not args.no_cpu_baseline:
-        result["cpu_baseline"] = cpu_baseline(layers[0])
+        result["cpu_baseline"] = cpu_baseline(layers[0], device)
     print(json.dumps(result))
 
 

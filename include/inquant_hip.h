@@ -233,6 +233,29 @@ int iq_tail_append(const void *k, const void *v, int64_t k_sh, int64_t k_st, int
                    int64_t shift_count, const void *positions, int pos_bytes, int64_t expected, int *flag,
                    void *stream);
 
+/*
+ * The same append of one row with the parts that stay fixed across a
+ * layer's decode steps in a descriptor (built once per layer, the row
+ * strides refreshed when they change), for the per-token host path: buf with
+ * element strides buf_kv, buf_h, buf_t; heads; row length dim; capacity
+ * rows; elem_bytes per element; flag = the int the position check sets;
+ * pos_bytes = 4 or 8; k_sh, k_st, v_sh, v_st = element strides (head,
+ * token) of the new key and value rows.  Equivalent to iq_tail_append(k, v,
+ * k_sh, k_st, v_sh, v_st, heads, 1, dim, elem_bytes, buf, buf_kv, buf_h,
+ * buf_t, capacity, slot, shift_src, shift_count, positions, pos_bytes,
+ * expected, flag, stream).
+ */
+typedef struct iq_tail_desc {
+    uint64_t buf;
+    int64_t buf_kv, buf_h, buf_t, heads, dim, capacity;
+    int elem_bytes, pos_bytes;
+    uint64_t flag;
+    int64_t k_sh, k_st, v_sh, v_st;
+} iq_tail_desc;
+
+int iq_tail_append_row(const iq_tail_desc *desc, const void *k, const void *v, int64_t slot, int64_t shift_src,
+                       int64_t shift_count, const void *positions, int64_t expected, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -112,3 +112,13 @@ extern "C" int iq_tail_append(const void *k, const void *v, int64_t k_sh, int64_
     IQ_CHECK_LAUNCH("tail_append_kernel");
     return IQ_OK;
 }
+
+extern "C" int iq_tail_append_row(const iq_tail_desc *d, const void *k, const void *v, int64_t slot,
+                                  int64_t shift_src, int64_t shift_count, const void *positions, int64_t expected,
+                                  void *stream)
+{
+    IQ_CHECK_ARG(d, "iq_tail_append_row: null descriptor");
+    return iq_tail_append(k, v, d->k_sh, d->k_st, d->v_sh, d->v_st, d->heads, 1, d->dim, d->elem_bytes,
+                          (void *)d->buf, d->buf_kv, d->buf_h, d->buf_t, d->capacity, slot, shift_src, shift_count,
+                          positions, d->pos_bytes, expected, (int *)d->flag, stream);
+}

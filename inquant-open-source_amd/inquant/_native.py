@@ -30,6 +30,15 @@ class BlockPtrs(ctypes.Structure):
         "k_src", "k_don", "v_src", "v_don")]
 
 
+class TailDesc(ctypes.Structure):
+    """Mirror of iq_tail_desc in include/inquant_hip.h: the fixed part of a
+    cache layer's tail append (its [2, H, capacity, D] row buffer and the
+    position flag word)."""
+    _fields_ = [("buf", ctypes.c_uint64), ("buf_kv", _i64), ("buf_h", _i64), ("buf_t", _i64),
+                ("heads", _i64), ("dim", _i64), ("capacity", _i64), ("elem_bytes", _int), ("pos_bytes", _int),
+                ("flag", ctypes.c_uint64), ("k_sh", _i64), ("k_st", _i64), ("v_sh", _i64), ("v_st", _i64)]
+
+
 _SIGNATURES = {
     "iq_abi_version": (_int, []),
     "iq_last_error": (ctypes.c_char_p, []),
@@ -54,9 +63,20 @@ _SIGNATURES = {
                                _p, _i64, _i64, _i64, _p, _i64, _f32, _p, _i64, _p, _i64, _int, _p]),
     "iq_tail_append": (_int, [_p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _int, _p, _i64, _i64, _i64,
                               _i64, _i64, _i64, _i64, _p, _int, _i64, _p, _p]),
+    "iq_tail_append_row": (_int, [ctypes.POINTER(TailDesc), _p, _p, _i64, _i64, _i64, _p, _i64, _p]),
 }
 
 _lib = None
+_tail_row = None
+
+
+def tail_append_row(desc, *args) -> int:
+    """iq_tail_append_row(desc, ...); kept as a module-level function bound once."""
+    global _tail_row
+    if _tail_row is None:
+        lib()
+        _tail_row = _lib.iq_tail_append_row
+    return _tail_row(ctypes.byref(desc), *args)
 
 
 class NativeError(RuntimeError):

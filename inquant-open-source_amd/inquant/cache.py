@@ -35,7 +35,7 @@ How a layer is stored here (not how the reference stores it):
 from __future__ import annotations
 
 from dataclasses import dataclass, field
-from typing import Any
+from typing import Any, NamedTuple
 
 import torch
 
@@ -84,10 +84,10 @@ class CacheConfig:
             raise ValueError("value_group_size must be 32, 64 or 128")
 
 
-@dataclass(frozen=True)
-class PackedAttentionView:
+class PackedAttentionView(NamedTuple):
     """What one decode step attends to: the blocks sealed before this step,
-    the exact sink, and the exact tail including the new token (cache.py:72-82)."""
+    the exact sink, and the exact tail including the new token (cache.py:72-82).
+    Immutable, with the reference's field names."""
 
     key_blocks: tuple
     value_blocks: tuple
@@ -101,22 +101,34 @@ class PackedAttentionView:
 class _Rows:
     """A [2, H, capacity, D] buffer of dense rows; keys at [0], values at [1]."""
 
-    __slots__ = ("buf", "start", "count")
+    __slots__ = ("buf", "kbuf", "vbuf", "start", "count", "desc", "row_strides", "_views")
 
     def __init__(self, heads: int, capacity: int, dim: int, dtype: torch.dtype, device: torch.device):
         self.buf = torch.empty((2, heads, capacity, dim), dtype=dtype, device=device)
+        self.kbuf, self.vbuf = self.buf[0:1], self.buf[1:2]      # [1, H, capacity, D] each
         self.start = 0
         self.count = 0
+        self.desc = None            # ctypes descriptor of the append kernel
+        self.row_strides = None     # (key strides, value strides) the descriptor holds
+        self._views = {}            # (start, count) -> (keys, values): the buffer never moves
 
     @property
     def capacity(self) -> int:
         return self.buf.shape[2]
 
-    def keys(self, extra: int = 0) -> torch.Tensor:
-        return self.buf[0:1, :, self.start:self.start + self.count + extra]
+    def views(self) -> tuple:
+        key = (self.start, self.count)
+        pair = self._views.get(key)
+        if pair is None:
+            pair = self._views[key] = (self.kbuf.narrow(2, self.start, self.count),
+                                       self.vbuf.narrow(2, self.start, self.count))
+        return pair
 
-    def values(self, extra: int = 0) -> torch.Tensor:
-        return self.buf[1:2, :, self.start:self.start + self.count + extra]
+    def keys(self) -> torch.Tensor:
+        return self.views()[0]
+
+    def values(self) -> torch.Tensor:
+        return self.views()[1]
 
     def live_nbytes(self) -> int:
         return 2 * self.buf.shape[1] * self.count * self.buf.shape[3] * self.buf.element_size()
@@ -150,6 +162,8 @@ class _LayerCache:
         self.key_blocks: list = []
         self.value_blocks: list = []
         self.packed_nbytes = 0
+        self.full_sink = None          # (keys, values) views once the sink holds all its rows
+        self.block_tuples = None       # (key blocks, value blocks) as tuples, rebuilt after a seal
 
     # the reference's field names, as views of the rows
     @property
@@ -252,25 +266,27 @@ class InQuantCache(_HFCache):
         """Argument checks of cache.py:202-240; returns (layer or None, position tensor or None)."""
         if type(layer_idx) is not int or layer_idx < 0:
             raise ValueError("layer_idx must be a nonnegative integer")
-        if keys.ndim != 4 or values.shape != keys.shape:
+        shape = keys.shape
+        if len(shape) != 4 or values.shape != shape:
             raise ValueError("K/V must have matching [batch, KV_heads, tokens, head_dim] shapes")
-        if keys.shape[0] != 1:
+        if shape[0] != 1:
             raise NotImplementedError("InQuantCache currently supports batch size 1 only")
         if not (keys.is_floating_point() and values.is_floating_point()):
             raise ValueError("K/V must be floating-point tensors")
-        if keys.dtype != values.dtype or keys.device != values.device:
+        dtype, device = keys.dtype, keys.device
+        if values.dtype != dtype or values.device != device:
             raise ValueError("K/V must share dtype and device")
-        if 0 in keys.shape:
+        if 0 in shape:
             raise ValueError("K/V dimensions must be nonempty")
-        if keys.shape[3] & 1:
+        if shape[3] & 1:
             raise ValueError("Packed cache requires an even head dimension")
         layer = self._layers.get(layer_idx)
-        if layer is not None and ((keys.shape[1], keys.shape[3]) != (layer.shape[1], layer.shape[3])
-                                  or keys.dtype != layer.dtype or keys.device != layer.device):
+        if layer is not None and (shape[1] != layer.shape[1] or shape[3] != layer.shape[3]
+                                  or dtype != layer.dtype or device != layer.device):
             raise ValueError("Layer shape, dtype and device must remain unchanged")
         position = cache_kwargs.get("cache_position") if cache_kwargs else None
         if position is not None and not (
-                isinstance(position, torch.Tensor) and position.ndim == 1 and position.numel() == keys.shape[2]
+                isinstance(position, torch.Tensor) and position.ndim == 1 and position.numel() == shape[2]
                 and position.dtype in (torch.int32, torch.int64)):
             raise ValueError("cache_position must be a 1D integer tensor with one position per new token")
         return layer, position if self.config.validate_positions else None
@@ -312,7 +328,6 @@ class InQuantCache(_HFCache):
         self._after_write(layer_idx, layer)
         return result
 
-    @torch.no_grad()
     def append_for_attention(self, key_states, value_states, layer_idx, cache_kwargs=None) -> PackedAttentionView:
         """Append one decode token and return the view that step attends to.
 
@@ -321,23 +336,29 @@ class InQuantCache(_HFCache):
         layer, position = self._check(key_states, value_states, layer_idx, cache_kwargs)
         if layer is None or key_states.shape[2] != 1:
             raise ValueError("append_for_attention requires one new token after an existing prefill")
-        blocks = (tuple(layer.key_blocks), tuple(layer.value_blocks))
-        sink = (layer.sink_key, layer.sink_value)
-        tail = layer.tail
-        sink_rows = 0 if layer.sink is None else layer.sink.count
-        if tail is None or sink_rows < self.config.sink_tokens or key_states.device.type != "cuda":
-            # the sink is still filling or nothing is dense yet: general path
-            if position is not None:
-                self._host_position_check(position, layer.seq_length)
-            before = (layer.residual_key, layer.residual_value)
-            pending_k = key_states if before[0] is None else torch.cat((before[0], key_states), 2)
-            pending_v = value_states if before[1] is None else torch.cat((before[1], value_states), 2)
-            self._ingest(layer, key_states, value_states)
-            view = PackedAttentionView(*blocks, *sink, pending_k, pending_v, layer.seq_length)
+        blocks = layer.block_tuples
+        if blocks is None:
+            blocks = layer.block_tuples = (tuple(layer.key_blocks), tuple(layer.value_blocks))
+        if layer.full_sink is not None and layer.tail is not None and key_states.is_cuda:
+            view = self._append_token(layer, key_states, value_states, position, blocks, layer.full_sink)
         else:
-            view = self._append_token(layer, key_states, value_states, position, blocks, sink)
-        self._after_write(layer_idx, layer)
+            with torch.no_grad():      # the sink is still filling or nothing is dense yet
+                view = self._append_general(layer, key_states, value_states, position, blocks)
+        if layer_idx == 0:
+            self._seen_tokens = layer.seq_length
+        if self.config.track_peak_bytes:
+            self.record_peak(layer_idx)
         return view
+
+    def _append_general(self, layer, key_states, value_states, position, blocks) -> PackedAttentionView:
+        if position is not None:
+            self._host_position_check(position, layer.seq_length)
+        sink = (layer.sink_key, layer.sink_value)
+        before = (layer.residual_key, layer.residual_value)
+        pending_k = key_states if before[0] is None else torch.cat((before[0], key_states), 2)
+        pending_v = value_states if before[1] is None else torch.cat((before[1], value_states), 2)
+        self._ingest(layer, key_states, value_states)
+        return PackedAttentionView(*blocks, *sink, pending_k, pending_v, layer.seq_length)
 
     def _append_token(self, layer, key, value, position, blocks, sink) -> PackedAttentionView:
         """One row written in place by iq_tail_append; seal when the tail is full."""
@@ -358,13 +379,23 @@ class InQuantCache(_HFCache):
                 pos_ptr, pos_bytes = position.data_ptr(), position.element_size()
                 checked = self._position_checked
                 check_now = not (checked is not None and checked[0] is position and checked[1] == layer.seq_length)
-        buf = tail.buf
-        nat.check(nat.lib().iq_tail_append(
-            key.data_ptr(), value.data_ptr(), key.stride(1), key.stride(2), value.stride(1), value.stride(2),
-            buf.shape[1], 1, buf.shape[3], buf.element_size(), buf.data_ptr(), buf.stride(0), buf.stride(1),
-            buf.stride(2), capacity, count if shift else start + count, start if shift else 0,
-            count if shift else 0, pos_ptr, pos_bytes, layer.seq_length,
-            flags[_POSITION_BAD:].data_ptr(), torch.cuda.current_stream(key.device).cuda_stream))
+        desc = tail.desc
+        if desc is None:
+            buf = tail.buf
+            desc = tail.desc = nat.TailDesc(buf.data_ptr(), buf.stride(0), buf.stride(1), buf.stride(2),
+                                            buf.shape[1], buf.shape[3], capacity, buf.element_size(), 8,
+                                            flags[_POSITION_BAD:].data_ptr())
+        strides = (key.stride(), value.stride())
+        if strides != tail.row_strides:
+            desc.k_sh, desc.k_st, desc.v_sh, desc.v_st = strides[0][1], strides[0][2], strides[1][1], strides[1][2]
+            tail.row_strides = strides
+        if pos_bytes and pos_bytes != desc.pos_bytes:
+            desc.pos_bytes = pos_bytes
+        status = nat.tail_append_row(
+            desc, key.data_ptr(), value.data_ptr(), count if shift else start + count, start if shift else 0,
+            count if shift else 0, pos_ptr, layer.seq_length, torch._C._cuda_getCurrentRawStream(key.device.index))
+        if status:
+            nat.check(status)
         if shift:
             tail.start = start = 0
         if check_now:
@@ -376,10 +407,12 @@ class InQuantCache(_HFCache):
             self._position_checked = (position, layer.seq_length)
         tail.count += 1
         layer.seq_length += 1
-        view = PackedAttentionView(*blocks, *sink, tail.keys(), tail.values(), layer.seq_length)
+        tail_k, tail_v = tail.views()
+        view = PackedAttentionView(*blocks, *sink, tail_k, tail_v, layer.seq_length)
         if tail.count >= cfg.residual_length + cfg.block_size:
             try:
-                self._seal(layer, tail.keys(), tail.values(), 1)
+                with torch.no_grad():
+                    self._seal(layer, tail_k, tail_v, 1)
             except ValueError:
                 tail.count -= 1                  # the reference leaves the layer unchanged on errors
                 layer.seq_length -= 1
@@ -417,6 +450,7 @@ class InQuantCache(_HFCache):
             raise ValueError(value_error)
         layer.key_blocks.extend(new_keys)
         layer.value_blocks.extend(new_values)
+        layer.block_tuples = None
         if cfg.track_peak_bytes:
             layer.packed_nbytes += sum(b.nbytes for b in new_keys) + sum(b.nbytes for b in new_values)
 
@@ -453,6 +487,10 @@ class InQuantCache(_HFCache):
             tail.write(rest_k, rest_v)
         if take:
             layer.sink.count += take
+            if layer.sink.count == cfg.sink_tokens:
+                layer.full_sink = (layer.sink.keys(), layer.sink.values())
+        elif cfg.sink_tokens == 0 and layer.full_sink is None:
+            layer.full_sink = (None, None)
         if m > 0:
             tail.count += rest_k.shape[2]
         layer.seq_length += n

@@ -20,6 +20,7 @@
  *                        mean and m2/n are each rounded to fp32.
  */
 #include <math.h>
+#include <omp.h>
 #include <stdint.h>
 #include <stdlib.h>
 #include <string.h>
@@ -285,6 +286,9 @@ IQO_EXPORT void iqo_reuse_map_row(const float *sal, const float *err, int64_t D,
         available[best] = 0;
     }
 }
+
+/* OpenMP thread count of the oracle's parallel loops (CPU-baseline timing). */
+IQO_EXPORT void iqo_set_threads(int n) { omp_set_num_threads(n > 0 ? n : 1); }
 
 IQO_EXPORT void iqo_reuse_map(const float *sal, const float *err, int64_t rows, int64_t D,
                               int64_t count, int64_t *src, int64_t *don)

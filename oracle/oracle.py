@@ -50,7 +50,13 @@ def lib():
         _lib.iqo_check_recip_division.argtypes = [c_i64, c_i64, ctypes.c_uint64]
         _lib.iqo_check_recip_division.restype = c_i64
         _lib.iqo_attend.argtypes = [c_p, c_p, c_p, c_i64, c_i64, c_i64, c_i64, ctypes.c_double, c_p]
+        _lib.iqo_set_threads.argtypes = [ctypes.c_int]
     return _lib
+
+
+def set_threads(n: int) -> None:
+    """Thread count of the oracle's OpenMP loops."""
+    lib().iqo_set_threads(int(n))
 
 
 def _ptr(a: np.ndarray):
