@@ -156,6 +156,28 @@ int iq_decode_attention(const void *q, int q_dtype, int64_t q_stride_h, int64_t 
                         void *out, int out_dtype, void *stream);
 
 /*
+ * iq_decode_attention without a workspace argument, for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).  No counterpart in the reference.  The
+ * partials live in a file-scope device array of IQ_NOALLOC_SCRATCH_FLOATS
+ * floats (16 MiB) that each GPU holds until the process ends; a call needing
+ * more (Hq * partitions * 130 floats) returns IQ_ERR_ARG.  Allocates and
+ * frees nothing.  Calls that overlap on one GPU share the array and race:
+ * serialize them (one stream, or events).
+ */
+#define IQ_NOALLOC_SCRATCH_FLOATS (4LL << 20)
+
+int iq_decode_attention_noalloc(const void *q, int q_dtype, int64_t q_stride_h, int64_t Hq,
+                                const int64_t *tables, const int8_t *key_map, const int8_t *value_map,
+                                int64_t n_blocks, int64_t block_tokens, int64_t H, int64_t S,
+                                int value_bits, int value_group,
+                                const void *sink_k, const void *sink_v, int64_t sink_k_sh, int64_t sink_k_st,
+                                int64_t sink_v_sh, int64_t sink_v_st, int64_t sink_t,
+                                const void *tail_k, const void *tail_v, int64_t tail_k_sh, int64_t tail_k_st,
+                                int64_t tail_v_sh, int64_t tail_v_st, int64_t tail_t,
+                                float scale, void *out, int out_dtype, void *stream);
+
+/*
  * ---------------------------------------------------------------- paged cache
  * Page layout of the vLLM plugin (extensions/vllm/src/inquant_vllm/layout.py:8-53),
  * field-major per page, B tokens per page, H KV heads, D = 128, 16 salient channels:

@@ -11,6 +11,8 @@
 //
 // This file holds the general kernel (any query dtype, K4- or V2/V4-coded
 // values, G <= 16 query heads per KV head, VALU arithmetic).
+#include <mutex>
+
 #include "decode_common.h"
 
 namespace {
@@ -390,4 +392,70 @@ extern "C" int iq_decode_attention(const void *q, int q_dtype, int64_t q_stride_
                        (hipStream_t)stream, workspace, parts, (int)Hq, out, out_dtype);
     IQ_CHECK_LAUNCH("decode_reduce");
     return IQ_OK;
+}
+
+// ---------------------------------------------------------------- allocation-free variant
+//
+// Scratch of iq_decode_attention_noalloc: the partition partials live in this
+// file-scope device array instead of a caller workspace.  Each GPU the library
+// runs on holds its own copy (IQ_NOALLOC_SCRATCH_FLOATS floats) until the
+// process ends.  Host code never passes `scratch` itself to a kernel: its
+// per-device address comes from hipGetSymbolAddress, taken once per device
+// with that device current.  The partials are fully written by the first
+// kernel before the merge kernel reads them, so nothing needs clearing
+// between calls; calls that overlap on one GPU share the array and race.
+static __device__ __align__(256) float scratch[IQ_NOALLOC_SCRATCH_FLOATS];
+
+namespace {
+
+constexpr int SCRATCH_DEVICES = 64;
+std::mutex g_scratch_mu;
+float *g_scratch_ptr[SCRATCH_DEVICES] = {};
+
+// Address of this device's copy of `scratch`, or nullptr after recording an error.
+float *device_scratch()
+{
+    int dev = -1;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= SCRATCH_DEVICES) {
+        iq_fail(IQ_ERR_DEVICE, "iq_decode_attention_noalloc: no current device below %d", SCRATCH_DEVICES);
+        return nullptr;
+    }
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+        void *p = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !p) {
+            iq_fail(IQ_ERR_DEVICE, "iq_decode_attention_noalloc: hipGetSymbolAddress: %s", hipGetErrorString(e));
+            return nullptr;
+        }
+        g_scratch_ptr[dev] = (float *)p;
+    }
+    return g_scratch_ptr[dev];
+}
+
+}  // namespace
+
+extern "C" int iq_decode_attention_noalloc(const void *q, int q_dtype, int64_t q_stride_h, int64_t Hq,
+                                           const int64_t *tables, const int8_t *key_map, const int8_t *value_map,
+                                           int64_t n_blocks, int64_t block_tokens, int64_t H, int64_t S,
+                                           int value_bits, int value_group, const void *sink_k, const void *sink_v,
+                                           int64_t sink_k_sh, int64_t sink_k_st, int64_t sink_v_sh,
+                                           int64_t sink_v_st, int64_t sink_t, const void *tail_k,
+                                           const void *tail_v, int64_t tail_k_sh, int64_t tail_k_st,
+                                           int64_t tail_v_sh, int64_t tail_v_st, int64_t tail_t, float scale,
+                                           void *out, int out_dtype, void *stream)
+{
+    IQ_CHECK_ARG(Hq >= 1 && n_blocks >= 0 && sink_t >= 0 && tail_t >= 0, "iq_decode_attention_noalloc: bad sizes");
+    const int64_t need = Hq * partitions(n_blocks, sink_t, tail_t) * (D + 2);
+    IQ_CHECK_ARG(need <= IQ_NOALLOC_SCRATCH_FLOATS,
+                 "iq_decode_attention_noalloc: %lld query heads x %lld partitions need %lld scratch floats; the "
+                 "static scratch holds %lld (use iq_decode_attention with a workspace)",
+                 (long long)Hq, (long long)partitions(n_blocks, sink_t, tail_t), (long long)need,
+                 (long long)IQ_NOALLOC_SCRATCH_FLOATS);
+    float *ws = device_scratch();
+    if (!ws) return IQ_ERR_DEVICE;
+    return iq_decode_attention(q, q_dtype, q_stride_h, Hq, tables, key_map, value_map, n_blocks, block_tokens, H, S,
+                               value_bits, value_group, sink_k, sink_v, sink_k_sh, sink_k_st, sink_v_sh, sink_v_st,
+                               sink_t, tail_k, tail_v, tail_k_sh, tail_k_st, tail_v_sh, tail_v_st, tail_t, scale,
+                               ws, IQ_NOALLOC_SCRATCH_FLOATS, out, out_dtype, stream);
 }

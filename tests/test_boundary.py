@@ -37,6 +37,12 @@ def test_invalid_arguments_return_errors_without_a_gpu():
     assert b"D=2000" in lib.iq_last_error()
     assert lib.iq_v_dequantize(None, None, None, 1, 128, 3, 64, None, 0, None) == -1
     assert lib.iq_decode_workspace_floats(28, 128, 4, 128) == 28 * 130 * 130
+    # the allocation-free decode refuses, on the host and before touching a
+    # device, inputs whose partials exceed its static scratch (4 Mi floats)
+    assert lib.iq_decode_attention_noalloc(
+        None, 1, 128, 28, None, None, None, 1, 256, 4, 16, 2, 64, None, None, 0, 0, 0, 0, 0,
+        None, None, 0, 0, 0, 0, 4700 * 256, 0.088, None, 0, None) == -1
+    assert b"static scratch" in lib.iq_last_error()
 
 
 @pytest.mark.parametrize("bad", [-0.1, 0.51, float("nan")])
