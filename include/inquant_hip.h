@@ -31,6 +31,8 @@
  *                       (+ the role-map part of layout.py:66-81 pack_pages)
  *   iq_unpack_pages     extensions/vllm/src/inquant_vllm/layout.py:84-100 unpack_pages_reference
  *   iq_paged_decode     extensions/vllm/src/inquant_vllm/kernels.py:66-88 paged_decode
+ *   iq_prefill_attention extensions/vllm/src/inquant_vllm/backend.py:139-144
+ *                       (flash_attn_varlen_func, causal prefill on exact K/V)
  *   iq_tail_append      src/inquant/cache.py:256-259,283-286 (the dense tail
  *                       concatenation of append_for_attention / _append)
  */
@@ -236,6 +238,22 @@ int iq_paged_decode(const void *q, int64_t q_stride_seq, int64_t q_stride_h, int
                     const int32_t *seq_info, int64_t n_pages, int64_t tail_t, int64_t sink_t,
                     const void *dense, int64_t dense_stride_seq, float scale, float *workspace,
                     int64_t workspace_floats, void *out, int64_t out_stride_seq, int out_dtype, void *stream);
+
+/*
+ * Causal self-attention over exact K/V for prefill, vLLM token-major layout:
+ * q [tokens, Hq, 128], k/v [tokens, H, 128] of dtype (bf16 or f16) with
+ * element strides (token, head), 16-byte aligned rows; sequences
+ * [cu_seqlens[i], cu_seqlens[i + 1]) (i32, on the device, n_seq + 1 values),
+ * none longer than max_seqlen; query i of a sequence attends to its keys
+ * 0..i; out [tokens, Hq, 128] of out_dtype with strides (o_st, o_sh).  fp32
+ * logits, softmax and accumulation; softmax weights rounded to the K/V dtype
+ * before P.V.  Replaces flash_attn_varlen_func(..., causal=True) in the
+ * plugin's prefill (extensions/vllm/src/inquant_vllm/backend.py:139-144).
+ */
+int iq_prefill_attention(const void *q, const void *k, const void *v, int dtype, int64_t q_st, int64_t q_sh,
+                         int64_t k_st, int64_t k_sh, int64_t v_st, int64_t v_sh, const int32_t *cu_seqlens,
+                         int64_t n_seq, int64_t max_seqlen, int64_t Hq, int64_t H, int64_t head_dim, float scale,
+                         void *out, int64_t o_st, int64_t o_sh, int out_dtype, void *stream);
 
 /*
  * Dense tail append of a cache layer.  buf holds [2 (keys, values), H,

@@ -1,0 +1,180 @@
+// Causal prefill attention over exact K/V on matrix cores (gfx950).
+//
+// Replaces the vLLM plugin's prefill call
+//   flash_attn_varlen_func(q, k, v, out, cu_seqlens_q=cu, cu_seqlens_k=cu,
+//                          max_seqlen_q=n, max_seqlen_k=n, causal=True, softmax_scale)
+// (extensions/vllm/src/inquant_vllm/backend.py:139-144): every query attends to
+// the keys at or before its position in its own sequence, in the K/V dtype
+// with fp32 logits, softmax and accumulation.  Layout is vLLM's token-major
+// [tokens, heads, 128] with runtime (token, head) strides; sequences are
+// delimited by cu_seqlens.
+//
+// One workgroup = 64 queries of one query head (16 per wavefront); key tiles
+// of 64 stream through LDS (K row-major, V transposed into key pairs).  Keys
+// are the rows of S^T = K Q^T (v_mfma_f32_16x16x32, queries as columns), so
+// the softmax weights land in exactly the lanes and k-slots of the B operand
+// of O^T = V^T P^T and no transpose of P is needed.  Query tiles are
+// dispatched longest-first (the causal work grows with the tile index).
+#include "decode_common.h"
+
+namespace {
+
+constexpr int D = 128;
+constexpr int QT = 64;              // queries per workgroup, 16 per wavefront
+constexpr int KT = 64;              // keys per tile
+constexpr int KROW = D + 8;         // halves per staged key row
+constexpr int VROW = KT / 2 + 4;    // key-pair dwords per staged V^T row
+
+struct PrefillArgs {
+    const uint16_t *q, *k, *v;
+    void *out;
+    int64_t q_st, q_sh, k_st, k_sh, v_st, v_sh, o_st, o_sh;   // element strides (token, head)
+    const int32_t *cu;                                        // [n_seq + 1] token offsets
+    int G;
+    float c_log2;                                             // softmax scale * log2(e)
+    int odt;
+};
+
+struct __attribute__((aligned(16))) PrefillSmem {
+    uint16_t k[KT * KROW];
+    uint32_t vt[D * VROW];           // V^T[d][key pair]: (V[2p][d], V[2p+1][d])
+};
+
+template <bool F16>
+__global__ __launch_bounds__(256) void prefill_attn(PrefillArgs a)
+{
+    __shared__ PrefillSmem sm;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int col = lane & 15, g = lane >> 4;
+    const int hq = blockIdx.y, seq = blockIdx.z, h = hq / a.G;
+    const int start = a.cu[seq], len = a.cu[seq + 1] - start;
+    const int q0 = (int)(gridDim.x - 1 - blockIdx.x) * QT;
+    if (q0 >= len) return;                       // uniform: no barrier is skipped by part of the group
+    const int qw = q0 + 16 * wave;               // this wavefront's first query
+    const int my_q = qw + col;                   // the query of this lane's column
+    u32x4 qb[4];                                 // B operand: Q[my_q][32 ks + 8 g .. + 7]
+    {
+        const int qq = my_q < len ? my_q : len - 1;
+        const uint16_t *qp = a.q + (int64_t)(start + qq) * a.q_st + (int64_t)hq * a.q_sh + 8 * g;
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) qb[ks] = ld16(qp + 32 * ks);
+    }
+    const uint16_t *kbase = a.k + (int64_t)start * a.k_st + (int64_t)h * a.k_sh;
+    const uint16_t *vbase = a.v + (int64_t)start * a.v_st + (int64_t)h * a.v_sh;
+    float m_run = NEG_INF, l_run = 0.0f;
+    f32x4 acc[8];
+#pragma unroll
+    for (int rb = 0; rb < 8; ++rb) acc[rb] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    const int kend = q0 + QT < len ? q0 + QT : len;
+    for (int k0 = 0; k0 < kend; k0 += KT) {
+        __syncthreads();                         // the previous tile's reads are done
+        // keys [k0, k0 + 64) (rows past the sequence read its last row and are masked)
+#pragma unroll
+        for (int it = 0; it < 4; ++it) {
+            const int i = tid + 256 * it;
+            const int r = i >> 4, c = (i & 15) * 8;
+            const int kk = k0 + r < len ? k0 + r : len - 1;
+            *(u32x4 *)(sm.k + r * KROW + c) = ld16(kbase + (int64_t)kk * a.k_st + c);
+        }
+#pragma unroll
+        for (int it = 0; it < 2; ++it) {
+            const int i = tid + 256 * it;
+            const int p = i >> 4, c = (i & 15) * 8;
+            const int ka = k0 + 2 * p < len ? k0 + 2 * p : len - 1;
+            const int kb = k0 + 2 * p + 1 < len ? k0 + 2 * p + 1 : len - 1;
+            const u32x4 r0 = ld16(vbase + (int64_t)ka * a.v_st + c);
+            const u32x4 r1 = ld16(vbase + (int64_t)kb * a.v_st + c);
+#pragma unroll
+            for (int w = 0; w < 4; ++w) {
+                sm.vt[(c + 2 * w) * VROW + p] = __builtin_amdgcn_perm(r1[w], r0[w], 0x05040100u);
+                sm.vt[(c + 2 * w + 1) * VROW + p] = __builtin_amdgcn_perm(r1[w], r0[w], 0x07060302u);
+            }
+        }
+        __syncthreads();
+        if (k0 > qw + 15) continue;              // every key of this tile is after this wavefront's queries
+        // S^T (keys x queries) for four 16-key subtiles; lane holds keys 16 j + 4 g + r of column my_q
+        f32x4 sc[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            sc[j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int ks = 0; ks < 4; ++ks)
+                sc[j] = mma32<F16>(*(const u32x4 *)(sm.k + (16 * j + col) * KROW + 32 * ks + 8 * g), qb[ks], sc[j]);
+        }
+        float cmax = NEG_INF;
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int key = k0 + 16 * j + 4 * g + r;
+                const float s = (key <= my_q && key < len) ? sc[j][r] * a.c_log2 : NEG_INF;
+                sc[j][r] = s;
+                cmax = fmaxf(cmax, s);
+            }
+        cmax = xmax16(cmax);
+        const float m_new = fmaxf(m_run, cmax);  // finite: key 0 is visible to every query
+        const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
+        float lsum = 0.0f;
+        u32x4 pb[2];                             // B operand of O^T: slots 0-3 subtile 2ks, 4-7 subtile 2ks+1
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            float pr[4];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                pr[r] = __builtin_amdgcn_exp2f(sc[j][r] - m_new);
+                lsum += pr[r];
+            }
+            pb[j >> 1][2 * (j & 1)] = pack2<F16>(pr[0], pr[1]);
+            pb[j >> 1][2 * (j & 1) + 1] = pack2<F16>(pr[2], pr[3]);
+        }
+        l_run = l_run * alpha + xsum16(lsum);
+        m_run = m_new;
+#pragma unroll
+        for (int rb = 0; rb < 8; ++rb) {
+            acc[rb] *= alpha;
+            const uint32_t *vr = sm.vt + (16 * rb + col) * VROW + 2 * g;
+#pragma unroll
+            for (int ks = 0; ks < 2; ++ks) {
+                const u32x2 lo = *(const u32x2 *)(vr + 16 * ks), hi = *(const u32x2 *)(vr + 16 * ks + 8);
+                acc[rb] = mma32<F16>(u32x4{lo[0], lo[1], hi[0], hi[1]}, pb[ks], acc[rb]);
+            }
+        }
+    }
+    if (my_q < len) {
+        const float inv = 1.0f / l_run;
+        const int64_t o = (int64_t)(start + my_q) * a.o_st + (int64_t)hq * a.o_sh + 4 * g;
+#pragma unroll
+        for (int rb = 0; rb < 8; ++rb)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) iq_store_as(a.out, o + 16 * rb + r, acc[rb][r] * inv, a.odt);
+    }
+}
+
+}  // namespace
+
+extern "C" int iq_prefill_attention(const void *q, const void *k, const void *v, int dtype, int64_t q_st,
+                                    int64_t q_sh, int64_t k_st, int64_t k_sh, int64_t v_st, int64_t v_sh,
+                                    const int32_t *cu_seqlens, int64_t n_seq, int64_t max_seqlen, int64_t Hq,
+                                    int64_t H, int64_t head_dim, float scale, void *out, int64_t o_st,
+                                    int64_t o_sh, int out_dtype, void *stream)
+{
+    IQ_CHECK_ARG(q && k && v && out && cu_seqlens, "iq_prefill_attention: null pointer");
+    IQ_CHECK_ARG(dtype == IQ_BF16 || dtype == IQ_F16, "iq_prefill_attention: q/k/v must be bf16 or f16");
+    IQ_CHECK_ARG(out_dtype >= IQ_F32 && out_dtype <= IQ_F16, "iq_prefill_attention: bad output dtype");
+    IQ_CHECK_ARG(head_dim == D, "iq_prefill_attention: head_dim %lld (128 required)", (long long)head_dim);
+    IQ_CHECK_ARG(H >= 1 && Hq >= 1 && Hq % H == 0 && Hq <= 65535, "iq_prefill_attention: heads %lld / %lld",
+                 (long long)Hq, (long long)H);
+    IQ_CHECK_ARG(n_seq >= 1 && n_seq <= 65535 && max_seqlen >= 1 && max_seqlen <= 0x7fffffffLL - QT,
+                 "iq_prefill_attention: bad sequence count or length");
+    // rows are read as 16-byte vectors
+    const uintptr_t bases = (uintptr_t)q | (uintptr_t)k | (uintptr_t)v;
+    IQ_CHECK_ARG(bases % 16 == 0 && (q_st | q_sh | k_st | k_sh | v_st | v_sh) % 8 == 0,
+                 "iq_prefill_attention: q/k/v rows must be 16-byte aligned");
+    PrefillArgs a{(const uint16_t *)q, (const uint16_t *)k, (const uint16_t *)v, out, q_st, q_sh, k_st, k_sh,
+                  v_st, v_sh, o_st, o_sh, cu_seqlens, (int)(Hq / H), scale * 1.44269504088896341f, out_dtype};
+    const dim3 grid((unsigned)((max_seqlen + QT - 1) / QT), (unsigned)Hq, (unsigned)n_seq), block(256);
+    if (dtype == IQ_F16) hipLaunchKernelGGL(prefill_attn<true>, grid, block, 0, (hipStream_t)stream, a);
+    else hipLaunchKernelGGL(prefill_attn<false>, grid, block, 0, (hipStream_t)stream, a);
+    IQ_CHECK_LAUNCH("prefill_attn");
+    return IQ_OK;
+}

@@ -59,6 +59,8 @@ _SIGNATURES = {
                                            _p, _p, _i64, _i64, _i64, _i64, _i64,
                                            _p, _p, _i64, _i64, _i64, _i64, _i64,
                                            _f32, _p, _int, _p]),
+    "iq_prefill_attention": (_int, [_p, _p, _p, _int, _i64, _i64, _i64, _i64, _i64, _i64, _p, _i64, _i64, _i64,
+                                    _i64, _i64, _f32, _p, _i64, _i64, _int, _p]),
     "iq_page_bytes": (_i64, [_i64, _i64]),
     "iq_write_pages": (_int, [_p, _p, _p, _p, _p, _int, _p, _p, _p, _i64, _i64, _i64, _p, _i64, _p, _int, _p]),
     "iq_unpack_pages": (_int, [_p, _i64, _i64, _i64, _p, _p, _int, _p]),

@@ -10,7 +10,7 @@ this package.
 """
 from .layout import PageLayout, pack_pages, pack_pages_into, unpack_pages_reference
 from .packing import write_codec_pages
-from .kernels import paged_decode, paged_decode_batch
+from .kernels import paged_decode, paged_decode_batch, prefill_attention
 
 __all__ = ["PageLayout", "pack_pages", "pack_pages_into", "unpack_pages_reference", "write_codec_pages",
-           "paged_decode", "paged_decode_batch"]
+           "paged_decode", "paged_decode_batch", "prefill_attention"]

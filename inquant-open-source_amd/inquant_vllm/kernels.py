@@ -83,3 +83,38 @@ def paged_decode_batch(query, cache, block_tables, seq_info, dense, max_pages, l
         dense.data_ptr(), dense[0].numel(), float(scale), scratch.data_ptr(), need,
         output.data_ptr(), hq * 128, nat.dtype_code(output.dtype), nat.stream_handle(query.device)))
     return output
+
+
+def prefill_attention(query, key, value, cu_seqlens, max_seqlen, scale, output=None):
+    """Causal self-attention of a prefill over its exact K/V (replaces the
+    plugin's flash_attn_varlen_func(..., causal=True) call, backend.py:139-144).
+
+    query [tokens, Hq, 128], key/value [tokens, H, 128] (bf16 or f16, rows
+    16-byte aligned), cu_seqlens int32 [sequences + 1] on the device,
+    max_seqlen >= every sequence length.  Returns (or fills) output
+    [tokens, Hq, 128] of the query dtype or float32."""
+    if query.ndim != 3 or key.ndim != 3 or key.shape != value.shape or query.shape[-1] != 128 \
+            or key.shape[-1] != 128 or query.shape[0] != key.shape[0]:
+        raise ValueError("Expected query [tokens, Hq, 128] and key/value [tokens, H, 128]")
+    if query.dtype not in (torch.bfloat16, torch.float16) or key.dtype != query.dtype or value.dtype != query.dtype:
+        raise ValueError("Prefill attention expects BF16 or FP16 query, key and value")
+    hq, h = query.shape[1], key.shape[1]
+    if hq % h:
+        raise ValueError("query heads must be a multiple of KV heads")
+    if cu_seqlens.dtype != torch.int32 or cu_seqlens.ndim != 1 or cu_seqlens.numel() < 2:
+        raise ValueError("cu_seqlens must be an int32 [sequences + 1] tensor")
+    nat.require_gpu(query, key, value, cu_seqlens, what="prefill_attention")
+    if any(t.stride(-1) != 1 for t in (query, key, value)):
+        raise ValueError("head dimension must be contiguous")
+    if output is None:
+        output = torch.empty_like(query)
+    elif tuple(output.shape) != tuple(query.shape) or output.stride(-1) != 1 \
+            or output.dtype not in (query.dtype, torch.float32):
+        raise ValueError("output must be [tokens, Hq, 128] of the query dtype or float32")
+    cu = cu_seqlens.contiguous()
+    nat.check(nat.lib().iq_prefill_attention(
+        query.data_ptr(), key.data_ptr(), value.data_ptr(), nat.dtype_code(query.dtype),
+        query.stride(0), query.stride(1), key.stride(0), key.stride(1), value.stride(0), value.stride(1),
+        cu.data_ptr(), cu.numel() - 1, int(max_seqlen), hq, h, 128, float(scale), output.data_ptr(),
+        output.stride(0), output.stride(1), nat.dtype_code(output.dtype), nat.stream_handle(query.device)))
+    return output

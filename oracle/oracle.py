@@ -284,3 +284,22 @@ def paged_attend(q: np.ndarray, pool: np.ndarray, ids, dense: np.ndarray, n_page
     """fp64 paged decode of one sequence: q [Hq, 128] -> [Hq, 128]."""
     k, v = paged_tokens(pool, ids, dense, n_pages, tail_t, sink_t, H, B)
     return attend(q, k, v, scale)
+
+
+def causal_attend(q: np.ndarray, k: np.ndarray, v: np.ndarray, scale: float) -> np.ndarray:
+    """fp64 causal self-attention of one sequence: q [n, Hq, D], k/v [n, H, D]
+    -> [n, Hq, D]; query i sees keys 0..i of its KV head (query head h reads
+    KV head h // (Hq / H)).  The semantics of the plugin's prefill call
+    flash_attn_varlen_func(..., causal=True) (backend.py:139-144)."""
+    q64, k64, v64 = (np.asarray(a, np.float64) for a in (q, k, v))
+    n, hq, _ = q64.shape
+    group = hq // k64.shape[1]
+    out = np.empty_like(q64)
+    future = np.triu(np.ones((n, n), bool), 1)
+    for h in range(hq):
+        s = q64[:, h] @ k64[:, h // group].T * scale
+        s[future] = -np.inf
+        s -= s.max(1, keepdims=True)
+        p = np.exp(s)
+        out[:, h] = (p @ v64[:, h // group]) / p.sum(1, keepdims=True)
+    return out

@@ -260,3 +260,20 @@ def test_tile_encoder_quotient_identity():
     # the GPU tile encoder's Welford step replaces delta / n by a reciprocal
     # product with one remainder correction; it must be the IEEE quotient
     assert oracle.check_recip_division(256, 20000, 11) == 0
+
+
+def test_causal_attention_oracle_against_torch_sdpa():
+    # the prefill oracle against torch's scaled_dot_product_attention in fp64
+    # (is_causal, GQA expanded by repeat), and the first query's closed form
+    # (it sees only key 0: its output is v[0])
+    n, hq, h = 37, 6, 2
+    q = synth.normal(501, (n, hq, 128))
+    k = synth.normal(502, (n, h, 128))
+    v = synth.normal(503, (n, h, 128))
+    got = oracle.causal_attend(q, k, v, 0.1)
+    qt = torch.from_numpy(q).double().transpose(0, 1)
+    kt = torch.from_numpy(k).double().transpose(0, 1).repeat_interleave(hq // h, 0)
+    vt = torch.from_numpy(v).double().transpose(0, 1).repeat_interleave(hq // h, 0)
+    ref = torch.nn.functional.scaled_dot_product_attention(qt, kt, vt, is_causal=True, scale=0.1).transpose(0, 1)
+    np.testing.assert_allclose(got, ref.numpy(), rtol=1e-10, atol=1e-12)
+    np.testing.assert_allclose(got[0], np.repeat(v[0], hq // h, 0), rtol=0, atol=1e-15)

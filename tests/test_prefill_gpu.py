@@ -1,0 +1,74 @@
+"""GPU parity of the causal prefill attention (the plugin's
+flash_attn_varlen_func call, backend.py:139-144) against the fp64 oracle.
+
+Tolerance: the reference's own prefill bound against SDPA (atol 0.02,
+rtol 0.02, extensions/vllm/tests/test_backend.py:73), since the kernel, like
+flash attention, rounds the softmax weights to the K/V dtype before P.V; the
+fp32 output of bf16 inputs is additionally held to 1e-2 max-abs."""
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle
+
+pytestmark = pytest.mark.gpu
+
+
+def _qkv(seed, n, hq, h, dtype):
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    q = torch.randn((n, hq, 128), generator=g, device="cuda").to(dtype)
+    k = torch.randn((n, h, 128), generator=g, device="cuda")
+    k[..., 17:19] *= 8
+    v = torch.randn((n, h, 128), generator=g, device="cuda")
+    return q, k.to(dtype), v.to(dtype)
+
+
+def _np(t):
+    return t.detach().float().cpu().numpy()
+
+
+@pytest.mark.parametrize("n", [1, 2, 63, 64, 65, 130, 257, 1000])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_prefill_matches_causal_oracle(n, dtype):
+    from inquant_vllm import prefill_attention
+    print(f"prefill n={n} {dtype}", flush=True)
+    hq, h = 28, 4
+    q, k, v = _qkv(n + 7, n, hq, h, dtype)
+    cu = torch.tensor([0, n], dtype=torch.int32, device="cuda")
+    out = prefill_attention(q, k, v, cu, n, 128 ** -0.5)
+    out32 = prefill_attention(q, k, v, cu, n, 128 ** -0.5, torch.empty(q.shape, device="cuda"))
+    exp = oracle.causal_attend(_np(q), _np(k), _np(v), 128 ** -0.5)
+    got = _np(out)
+    assert out.dtype == dtype and np.isfinite(got).all()
+    assert (np.abs(got - exp) <= 0.02 + 0.02 * np.abs(exp)).all()
+    assert np.abs(_np(out32) - exp).max() <= 1e-2
+    assert torch.equal(out, out32.to(dtype))
+
+
+def test_prefill_varlen_sequences_and_strided_views():
+    # three sequences in one launch, q/k/v as views of a fused [tokens, heads, 128] projection
+    from inquant_vllm import prefill_attention
+    lens = [5, 300, 77]
+    n, hq, h = sum(lens), 32, 8
+    g = torch.Generator(device="cuda").manual_seed(9)
+    qkv = torch.randn((n, hq + 2 * h, 128), generator=g, device="cuda").to(torch.bfloat16)
+    q, k, v = qkv[:, :hq], qkv[:, hq:hq + h], qkv[:, hq + h:]
+    cu = torch.tensor(np.cumsum([0] + lens), dtype=torch.int32, device="cuda")
+    out = torch.full((n, hq, 128), float("nan"), device="cuda")
+    prefill_attention(q, k, v, cu, max(lens), 0.1, out)
+    got = _np(out)
+    for a, b in zip(np.cumsum([0] + lens)[:-1], np.cumsum(lens)):
+        exp = oracle.causal_attend(_np(q[a:b]), _np(k[a:b]), _np(v[a:b]), 0.1)
+        assert np.abs(got[a:b] - exp).max() <= 1e-2
+
+
+def test_prefill_rejects_bad_arguments():
+    from inquant_vllm import prefill_attention
+    q, k, v = _qkv(1, 8, 4, 2, torch.bfloat16)
+    cu = torch.tensor([0, 8], dtype=torch.int32, device="cuda")
+    with pytest.raises(ValueError, match="multiple"):
+        prefill_attention(q[:, :3], k, v, cu, 8, 0.1)
+    with pytest.raises(ValueError, match="int32"):
+        prefill_attention(q, k, v, cu.long(), 8, 0.1)
+    with pytest.raises(ValueError, match="BF16 or FP16"):
+        prefill_attention(q.float(), k.float(), v.float(), cu, 8, 0.1)
