@@ -29,6 +29,8 @@
  *                       (_attention_partials :67-165 + _reduce_partials :168-181)
  *   iq_write_pages      extensions/vllm/src/inquant_vllm/packing.py:41-55 write_codec_pages
  *                       (+ the role-map part of layout.py:66-81 pack_pages)
+ *   iq_encode_pages     extensions/vllm/src/inquant_vllm/layout.py:103-115 pack_pages_into
+ *                       (quantize + quantize_values + write_codec_pages, one launch)
  *   iq_unpack_pages     extensions/vllm/src/inquant_vllm/layout.py:84-100 unpack_pages_reference
  *   iq_paged_decode     extensions/vllm/src/inquant_vllm/kernels.py:66-88 paged_decode
  *   iq_prefill_attention extensions/vllm/src/inquant_vllm/backend.py:139-144
@@ -205,6 +207,24 @@ int iq_write_pages(const uint8_t *k_payload, const float *k_scales, const float 
                    const uint16_t *v_scales, const uint16_t *v_offsets, int64_t n_pages, int64_t H,
                    int64_t block_tokens, uint8_t *pool, int64_t pool_pages, const void *page_ids,
                    int id_bytes, void *stream);
+
+/*
+ * Encode n_pages full pages straight into the pool, one launch: keys/values
+ * [n, H, B, 128] of dtype (bf16 or f16) with element strides k_strides /
+ * v_strides (unit channel stride, 16-byte aligned rows), B in {16, 32, 64,
+ * 128, 256}.  Page n goes to physical id page_ids[n] (i32 or i64 per
+ * id_bytes; ids outside [0, pool_pages) are skipped): K4 min_error with
+ * stride 8 and 16 salient channels (payload, scales, padding and the i16
+ * role map) and V2 with 64-channel groups.  flags[0] / flags[1] are set for
+ * non-finite keys / values; the launch zeroes next_flags[0..1] (the pair the
+ * caller passes as flags to its next call, so no clearing launch is needed).
+ * Replaces pack_pages_into (layout.py:103-115: quantize, quantize_values,
+ * write_codec_pages) and the encode of pack_pages (layout.py:56-81).
+ */
+int iq_encode_pages(const void *keys, const void *values, int dtype, const int64_t *k_strides,
+                    const int64_t *v_strides, int64_t n_pages, int64_t H, int64_t block_tokens, uint8_t *pool,
+                    int64_t pool_pages, const void *page_ids, int id_bytes, int *flags, int *next_flags,
+                    void *stream);
 
 /*
  * Decode n_pages contiguous pages to keys/values [n, H, B, 128] of out_dtype.

@@ -9,6 +9,7 @@
 //            source and donor slots, nibble packing, padding (codec.py:218-233).
 // Results are bit-identical to the reference CPU implementation.
 #include "select_dev.h"
+#include "v_rows_dev.h"
 
 #include <cstdarg>
 #include <cstdio>
@@ -16,7 +17,6 @@
 namespace {
 
 constexpr int K4_THREADS = 256;
-typedef __attribute__((ext_vector_type(4))) uint32_t u32x4_t;
 
 struct K4Args {
     const void *x;
@@ -30,6 +30,18 @@ struct K4Args {
     int desc_bytes;
     float *padding;
     int *bad;
+    // page mode (k4_encode_tile<..., true>): row (b, h) is written into the
+    // physical page ids[b] of `pool` (byte offsets of the page fields), with
+    // an int16 role map instead of descriptors, and the value rows of v
+    // (element strides vsb, vsh, vst) are V2-encoded into the same page
+    uint8_t *pool;
+    int64_t pool_pages, page_bytes;
+    const void *ids;
+    int id_bytes;
+    int64_t off_kpay, off_kscale, off_kmap, off_kpad, off_vpay, off_vscale, off_voff;
+    const uint16_t *v;
+    int64_t vsb, vsh, vst;
+    int *vbad, *clear;          // value flag; flag pair the next page launch uses, zeroed here
 };
 
 __device__ __forceinline__ void store_desc(void *p, int64_t i, int v, int bytes)
@@ -265,7 +277,7 @@ __device__ __forceinline__ float tile_f32(uint32_t bits16)
 // compile time, so the chunk loops unroll without branches and each load is
 // waited for exactly when its chunk is stored (a branch around loads makes
 // the compiler wait for all of them).  NCH = 0: any T <= 256.
-template <bool F16IN, int NCH>
+template <bool F16IN, int NCH, bool PAGES = false>
 __global__ __launch_bounds__(K4_THREADS, 4) void k4_encode_tile(K4Args a)
 {
     constexpr bool DMA = NCH > 0;
@@ -289,6 +301,15 @@ __global__ __launch_bounds__(K4_THREADS, 4) void k4_encode_tile(K4Args a)
     // grid (blocks, heads): no 64-bit division for the row's coordinates
     const int64_t b = blockIdx.x, h = blockIdx.y;
     const int64_t row = b * a.H + h;
+    uint8_t *page = nullptr;
+    __shared__ int16_t s_role[TILE_D];
+    if constexpr (PAGES) {
+        if (b == 0 && h == 0 && threadIdx.x < 2) a.clear[threadIdx.x] = 0;
+        const int64_t id = a.id_bytes == 8 ? ((const int64_t *)a.ids)[b] : (int64_t)((const int32_t *)a.ids)[b];
+        if (id < 0 || id >= a.pool_pages) return;       // uniform: before any barrier or load
+        page = a.pool + id * a.page_bytes;
+        if (threadIdx.x < TILE_D) s_role[threadIdx.x] = -1;
+    }
     const uint16_t *xr = (const uint16_t *)a.x + b * a.sb + h * a.sh;
     const int T = NCH > 0 ? NCH * CH : (int)a.T;
     const int stride = (int)min(a.stride, (int64_t)TILE_T);   // a larger stride samples token 0 only
@@ -498,12 +519,20 @@ __global__ __launch_bounds__(K4_THREADS, 4) void k4_encode_tile(K4Args a)
         const float s = s_amax[tid] / (s_is_src[tid] ? 127.0f : 7.0f);
         const float sc = s < flt_min ? flt_min : s;
         s_scale[tid] = sc;
-        a.scales[row * TILE_D + tid] = sc;
+        if constexpr (PAGES) ((float *)(page + a.off_kscale))[h * TILE_D + tid] = sc;
+        else a.scales[row * TILE_D + tid] = sc;
     }
     if (tid < a.count) {
-        store_desc(a.src, row * a.count + tid, s_src[tid], a.desc_bytes);
-        store_desc(a.don, row * a.count + tid, s_don[tid], a.desc_bytes);
-        a.padding[row * a.count + tid] = s_smean[s_don[tid]];
+        if constexpr (PAGES) {
+            // page role map: the donor channel for a source, -2 - k for donor k
+            s_role[s_src[tid]] = (int16_t)s_don[tid];
+            s_role[s_don[tid]] = (int16_t)(-2 - tid);
+            ((float *)(page + a.off_kpad))[h * a.count + tid] = s_smean[s_don[tid]];
+        } else {
+            store_desc(a.src, row * a.count + tid, s_src[tid], a.desc_bytes);
+            store_desc(a.don, row * a.count + tid, s_don[tid], a.desc_bytes);
+            a.padding[row * a.count + tid] = s_smean[s_don[tid]];
+        }
     }
     if (tid == 0 && s_bad) atomicOr(a.bad, 1);
     if constexpr (!DMA) store_chunk(seg[0], 0);
@@ -537,7 +566,11 @@ __global__ __launch_bounds__(K4_THREADS, 4) void k4_encode_tile(K4Args a)
         xe[e] = &s_x[0][0] + (8 * wave + tq) * ROWLEN + srcc;
         asm volatile("" : "+v"(scl[e]), "+v"(rscl[e]), "+v"(lim[e]), "+v"(bias[e]), "+v"(shift[e]));
     }
-    uint32_t *out = (uint32_t *)(a.payload + row * (int64_t)T * (TILE_D / 2));
+    if constexpr (PAGES) {
+        if (tid < TILE_D) ((int16_t *)(page + a.off_kmap))[h * TILE_D + tid] = s_role[tid];
+    }
+    uint32_t *out = PAGES ? (uint32_t *)(page + a.off_kpay + h * (int64_t)T * (TILE_D / 2))
+                          : (uint32_t *)(a.payload + row * (int64_t)T * (TILE_D / 2));
     stream([&](int ch) {
         const int t0 = ch * CH;
 #pragma unroll
@@ -581,6 +614,40 @@ __global__ __launch_bounds__(K4_THREADS, 4) void k4_encode_tile(K4Args a)
             }
         }
     });
+    if constexpr (PAGES) {
+        // the row's values, V2 with 64-channel groups (value_codec.py:51-72):
+        // 8 lanes per token (16 channels each, 4 lanes per group), 32 tokens
+        // per pass, four passes' loads in flight
+        const int j8 = tid & 7, tl = tid >> 3;
+        const uint16_t *vr = a.v + b * a.vsb + h * a.vsh + 16 * j8;
+        uint8_t *vpay = page + a.off_vpay + h * (int64_t)T * (TILE_D / 4);
+        uint16_t *vscale = (uint16_t *)(page + a.off_vscale) + h * (int64_t)T * 2;
+        uint16_t *voff = (uint16_t *)(page + a.off_voff) + h * (int64_t)T * 2;
+        bool vbad = false;
+        for (int t0 = 0; t0 < T; t0 += 4 * 32) {
+            u32x4_t raw[4][2];
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const int t = min(t0 + 32 * k + tl, T - 1);
+                raw[k][0] = *(const u32x4_t *)(vr + (int64_t)t * a.vst);
+                raw[k][1] = *(const u32x4_t *)(vr + (int64_t)t * a.vst + 8);
+            }
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const int t = t0 + 32 * k + tl;
+                const bool live = t < T;
+                uint32_t code[1];
+                uint16_t off_h, sc_h;
+                v_encode16<F16IN, 2, 4>(raw[k], live, code, off_h, sc_h, vbad);
+                if (live) {
+                    ((uint32_t *)(vpay + t * (TILE_D / 4)))[j8] = code[0];
+                    if ((j8 & 3) == 0) voff[2 * t + (j8 >> 2)] = off_h;
+                    if ((j8 & 3) == 3) vscale[2 * t + (j8 >> 2)] = sc_h;
+                }
+            }
+        }
+        if (__ballot(vbad) != 0 && lane == 0) atomicOr(a.vbad, 1);
+    }
 }
 
 struct SelectArgs {
@@ -663,5 +730,72 @@ extern "C" int iq_reuse_map(const float *saliency, const float *donor_error, int
     SelectArgs a{saliency, donor_error, D, count, src, don};
     hipLaunchKernelGGL(reuse_map_kernel, dim3((unsigned)rows), dim3(64), 0, (hipStream_t)stream, a);
     IQ_CHECK_LAUNCH("reuse_map_kernel");
+    return IQ_OK;
+}
+
+extern "C" int iq_encode_pages(const void *keys, const void *values, int dtype, const int64_t *k_strides,
+                               const int64_t *v_strides, int64_t n_pages, int64_t H, int64_t block_tokens,
+                               uint8_t *pool, int64_t pool_pages, const void *page_ids, int id_bytes, int *flags,
+                               int *next_flags, void *stream)
+{
+    IQ_CHECK_ARG(keys && values && k_strides && v_strides && pool && page_ids && flags && next_flags,
+                 "iq_encode_pages: null pointer");
+    IQ_CHECK_ARG(dtype == IQ_BF16 || dtype == IQ_F16, "iq_encode_pages: keys/values must be bf16 or f16");
+    IQ_CHECK_ARG(id_bytes == 4 || id_bytes == 8, "iq_encode_pages: id_bytes");
+    const int64_t B = block_tokens;
+    IQ_CHECK_ARG(B == 16 || B == 32 || B == 64 || B == 128 || B == 256, "iq_encode_pages: %lld-token pages",
+                 (long long)B);
+    IQ_CHECK_ARG(n_pages >= 0 && n_pages <= 0x7fffffffLL && H >= 1 && H <= 65535, "iq_encode_pages: shape");
+    // rows read as 16-byte vectors (keys through direct-to-LDS chunk loads)
+    auto rows_ok = [](const void *p, const int64_t *st) {
+        return ((uintptr_t)p & 15) == 0 && st[3] == 1 && st[0] % 8 == 0 && st[1] % 8 == 0 && st[2] % 8 == 0 &&
+               st[2] >= 0 && st[2] <= (1 << 24);
+    };
+    IQ_CHECK_ARG(rows_ok(keys, k_strides) && rows_ok(values, v_strides),
+                 "iq_encode_pages: key/value rows must be contiguous and 16-byte aligned");
+    const int64_t page_bytes = H * (104 * B + 832);
+    K4Args a{};
+    a.x = keys;
+    a.dt = dtype;
+    a.sb = k_strides[0];
+    a.sh = k_strides[1];
+    a.st = k_strides[2];
+    a.sc = 1;
+    a.H = H;
+    a.T = B;
+    a.D = TILE_D;
+    a.count = 16;
+    a.stride = 8;
+    a.min_error = 1;
+    a.bad = flags;
+    a.pool = pool;
+    a.pool_pages = pool_pages;
+    a.page_bytes = page_bytes;
+    a.ids = page_ids;
+    a.id_bytes = id_bytes;
+    a.off_kpay = 0;
+    a.off_kscale = H * B * 64;
+    a.off_kmap = a.off_kscale + H * 128 * 4;
+    a.off_kpad = a.off_kmap + H * 128 * 2;
+    a.off_vpay = a.off_kpad + H * 16 * 4;
+    a.off_vscale = a.off_vpay + H * B * 32;
+    a.off_voff = a.off_vscale + H * B * 2 * 2;
+    a.v = (const uint16_t *)values;
+    a.vsb = v_strides[0];
+    a.vsh = v_strides[1];
+    a.vst = v_strides[2];
+    a.vbad = flags + 1;
+    a.clear = next_flags;
+    if (n_pages == 0) return IQ_OK;
+    const dim3 grid((unsigned)n_pages, (unsigned)H), block(K4_THREADS);
+    const hipStream_t st = (hipStream_t)stream;
+    if (dtype == IQ_F16) {
+        if (B == TILE_T) hipLaunchKernelGGL((k4_encode_tile<true, TILE_T / CH, true>), grid, block, 0, st, a);
+        else hipLaunchKernelGGL((k4_encode_tile<true, 0, true>), grid, block, 0, st, a);
+    } else {
+        if (B == TILE_T) hipLaunchKernelGGL((k4_encode_tile<false, TILE_T / CH, true>), grid, block, 0, st, a);
+        else hipLaunchKernelGGL((k4_encode_tile<false, 0, true>), grid, block, 0, st, a);
+    }
+    IQ_CHECK_LAUNCH("k4_encode_tile (pages)");
     return IQ_OK;
 }

@@ -8,7 +8,7 @@
 // Decode (value_codec.py:38-48): code * f32(scale) + f32(offset).  The
 // product of a <=4-bit code and an f16 scale is exact in fp32, so the
 // reference's separate multiply and add round exactly once.
-#include "iq_common.h"
+#include "v_rows_dev.h"
 
 namespace {
 
@@ -26,8 +26,6 @@ struct VEncArgs {
     uint16_t *scales, *offsets;
     int *bad;
 };
-
-typedef __attribute__((ext_vector_type(4))) uint32_t u32x4_t;
 
 // Eight consecutive channels of x as fp32.
 __device__ __forceinline__ void v_load8(const VEncArgs &a, int64_t base, float v[8])
@@ -124,17 +122,9 @@ __global__ __launch_bounds__(V_THREADS) void v_encode_kernel(VEncArgs a)
 
 // Rows of 16-bit values with unit channel stride and 16-byte aligned rows,
 // D = 16 * PR channels.  Grid (token blocks, B*H); each thread encodes 16
-// consecutive channels of NT tokens, GL = group / 16 adjacent lanes forming
-// one group.  Same arithmetic as v_encode_kernel with fewer instructions:
-//  * min / max use the NaN-propagating v_minimum3 / v_maximum3, so a NaN or
-//    infinity anywhere in a group makes its offset or scale non-finite and
-//    that single check replaces the per-value finiteness test;
-//  * the quotient is clamped to [0, levels] before rounding (rint and an
-//    integer clamp commute), so every value that can decide a code lies in
-//    [0, levels] and the near-half test uses the fixed band 2^-16 >=
-//    levels * 2^-20 instead of one relative to |quotient|;
-//  * the codes of 8 values are packed with exact fp32 multiply-adds
-//    (sum of c_e * 2^(BITS*e) <= 2^16 - 1 for BITS=2; 4 values for BITS=4).
+// consecutive channels of NT tokens with v_encode16 (v_rows_dev.h), GL =
+// group / 16 adjacent lanes forming one group: the same codes as
+// v_encode_kernel with fewer instructions.
 struct VRowArgs {
     const uint16_t *x;
     int64_t sb, sh, st;      // element strides of batch, head, token
@@ -148,7 +138,6 @@ template <bool F16IN, int BITS, int GL, int PR, int NT>
 __global__ __launch_bounds__(V_THREADS) void v_encode_rows(VRowArgs a)
 {
     constexpr int TPB = V_THREADS / PR;                   // tokens per pass of the block
-    constexpr int L = (1 << BITS) - 1;
     constexpr int D = 16 * PR, GROUPS = PR / GL;          // groups per token
     constexpr int PB = D * BITS / 8;                      // payload bytes per token
     const int tid = threadIdx.x;
@@ -171,71 +160,16 @@ __global__ __launch_bounds__(V_THREADS) void v_encode_rows(VRowArgs a)
     for (int k = 0; k < NT; ++k) {
         const int tk = tl + k * TPB;
         const bool live = t0 + tk < a.T;
-        float v[16];
-#pragma unroll
-        for (int e = 0; e < 16; ++e) {
-            const uint32_t w = raw[k][e >> 3][(e >> 1) & 3];
-            const uint16_t hbits = (uint16_t)(e & 1 ? w >> 16 : w);
-            v[e] = F16IN ? iq_f16_to_f32(hbits) : __uint_as_float(e & 1 ? w & 0xffff0000u : w << 16);
-        }
-        float lo = v[0], hi = v[0];
-#pragma unroll
-        for (int e = 1; e < 15; e += 2) {
-            lo = __builtin_elementwise_minimum(__builtin_elementwise_minimum(lo, v[e]), v[e + 1]);
-            hi = __builtin_elementwise_maximum(__builtin_elementwise_maximum(hi, v[e]), v[e + 1]);
-        }
-        lo = __builtin_elementwise_minimum(lo, v[15]);
-        hi = __builtin_elementwise_maximum(hi, v[15]);
-#pragma unroll
-        for (int o = 1; o < GL; o <<= 1) {
-            lo = __builtin_elementwise_minimum(lo, __shfl_xor(lo, o, 64));
-            hi = __builtin_elementwise_maximum(hi, __shfl_xor(hi, o, 64));
-        }
-        const uint16_t off_h = iq_f32_to_f16(lo);
-        float s = __fsub_rn(hi, lo) / (float)L;
-        s = s < 6.103515625e-05f ? 6.103515625e-05f : s;
-        const uint16_t sc_h = iq_f32_to_f16(s);
-        const float off = iq_f16_to_f32(off_h), sc = iq_f16_to_f32(sc_h);
-        bad |= live && !(iq_isfinite(off) && iq_isfinite(sc));
-
-        const float rsc = __builtin_amdgcn_rcpf(sc);
-        float q[16], dev = 0.0f;
-#pragma unroll
-        for (int e = 0; e < 16; ++e) {
-            const float c = __builtin_amdgcn_fmed3f(__fmul_rn(__fsub_rn(v[e], off), rsc), 0.0f, (float)L);
-            q[e] = __builtin_rintf(c);
-            dev = fmaxf(dev, fabsf(__fsub_rn(q[e], c)));
-        }
-        if (dev >= 0.5f - 0x1p-16f) {     // a quotient near a half-integer: the IEEE division decides
-#pragma unroll
-            for (int e = 0; e < 16; ++e)
-                q[e] = fminf(fmaxf(rintf(__fsub_rn(v[e], off) / sc), 0.0f), (float)L);
-        }
+        uint32_t word[BITS / 2];
+        uint16_t off_h, sc_h;
+        v_encode16<F16IN, BITS, GL>(raw[k], live, word, off_h, sc_h, bad);
         const int row = tk;   // row offset within the block
         if (live) {
             if (BITS == 2) {
-                float p0 = q[0], p1 = q[8];
-#pragma unroll
-                for (int e = 1; e < 8; ++e) {
-                    p0 = __builtin_fmaf(q[e], (float)(1 << (2 * e)), p0);
-                    p1 = __builtin_fmaf(q[8 + e], (float)(1 << (2 * e)), p1);
-                }
-                const uint32_t word = (uint32_t)p0 | ((uint32_t)p1 << 16);
-                *(uint32_t *)(a.payload + r0 * PB + (uint32_t)(row * PB + 4 * j)) = word;
+                *(uint32_t *)(a.payload + r0 * PB + (uint32_t)(row * PB + 4 * j)) = word[0];
             } else {
-                uint32_t w[4];
-#pragma unroll
-                for (int g = 0; g < 4; ++g) {
-                    float p = q[4 * g];
-#pragma unroll
-                    for (int e = 1; e < 4; ++e) p = __builtin_fmaf(q[4 * g + e], (float)(1 << (4 * e)), p);
-                    w[g] = (uint32_t)p;
-                }
                 typedef __attribute__((ext_vector_type(2))) uint32_t u32x2_t;
-                u32x2_t o;
-                o[0] = w[0] | (w[1] << 16);
-                o[1] = w[2] | (w[3] << 16);
-                *(u32x2_t *)(a.payload + r0 * PB + (uint32_t)(row * PB + 8 * j)) = o;
+                *(u32x2_t *)(a.payload + r0 * PB + (uint32_t)(row * PB + 8 * j)) = u32x2_t{word[0], word[BITS / 2 - 1]};
             }
             const int64_t gi = r0 * GROUPS + (uint32_t)(row * GROUPS + j / GL);
             if (j % GL == 0) a.offsets[gi] = off_h;

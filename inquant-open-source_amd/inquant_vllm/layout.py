@@ -5,8 +5,9 @@ Same fields, order and sizes as the reference (layout.py:8-53): per page of
 key_payload u8 [H,B,64] | key_scales f32 [H,128] | key_map i16 [H,128] |
 key_padding f32 [H,16] | value_payload u8 [H,B,32] | value_scales f16 [H,B,2] |
 value_offsets f16 [H,B,2], so `page_bytes = H * (104 B + 832)`.  Block sizes
-64/128/256 as in the reference, plus 16 and 32 for small-page pools.  Encoding
-runs in libinquant_hip.so (K4 min_error + V2 group 64, then one page writer).
+64/128/256 as in the reference, plus 16 and 32 for small-page pools.  Pages
+are encoded by one launch of libinquant_hip.so (iq_encode_pages: K4
+min_error, the role map and V2 group 64 written straight into the page).
 """
 from __future__ import annotations
 
@@ -16,8 +17,6 @@ from dataclasses import dataclass
 import torch
 
 from inquant import _native as nat
-from inquant.codec import CodecConfig, quantize
-from inquant.value_codec import quantize_values
 
 BLOCK_SIZES = (16, 32, 64, 128, 256)
 
@@ -73,17 +72,62 @@ def _check_pages(keys, values, layout):
         raise ValueError("Invalid full-page K/V shape")
 
 
+class _Flags:
+    """Two pairs of device ints per (device, stream): a page launch raises
+    (key, value) non-finite flags in one pair and zeroes the other, which the
+    next launch on that stream uses, so no separate clearing launch is needed."""
+
+    def __init__(self, device):
+        self.words = torch.zeros((2, 2), dtype=torch.int32, device=device)
+        self.turn = 0
+
+
+_FLAGS: dict = {}
+
+
+def _encode_into(keys, values, layout, pool, page_ids):
+    """One launch: K4 min_error (stride 8, 16 salient channels), the i16 role
+    map and V2 g64 of every (page, head) written straight into pool[page_ids]."""
+    nat.require_gpu(keys, values, pool, page_ids, what="pack_pages_into")
+    if keys.dtype not in (torch.bfloat16, torch.float16) or values.dtype != keys.dtype:
+        raise ValueError("Pages are encoded from BF16 or FP16 keys and values")
+    keys = keys if _rows_ok(keys) else keys.contiguous()
+    values = values if _rows_ok(values) else values.contiguous()
+    ids = page_ids.contiguous()
+    stream = nat.stream_handle(keys.device)
+    flags = _FLAGS.get((keys.device, stream))
+    if flags is None:
+        flags = _FLAGS[(keys.device, stream)] = _Flags(keys.device)
+    mine, other = flags.words[flags.turn], flags.words[1 - flags.turn]
+    nat.check(nat.lib().iq_encode_pages(
+        keys.data_ptr(), values.data_ptr(), nat.dtype_code(keys.dtype), nat.strides4(keys), nat.strides4(values),
+        keys.shape[0], layout.heads, layout.block_size, pool.data_ptr(), pool.shape[0], ids.data_ptr(),
+        ids.element_size(), mine.data_ptr(), other.data_ptr(), stream))
+    if keys.shape[0] == 0:
+        return
+    flags.turn = 1 - flags.turn
+    bad_key, bad_value = mine.tolist()          # the one synchronization, as the codec's finite check
+    if bad_key:
+        raise ValueError("x must contain finite values representable in float32")
+    if bad_value:
+        raise ValueError("Values and stored FP16 quantization parameters must be finite")
+
+
+def _rows_ok(t) -> bool:
+    """Rows the page encoder reads in place: unit channel stride, 16-byte aligned."""
+    return (t.stride(-1) == 1 and all(st % 8 == 0 for st in t.stride()[:-1])
+            and t.data_ptr() % 16 == 0)
+
+
 @torch.no_grad()
 def pack_pages(keys, values, layout):
-    """Encode full temporal pages [P, H, B, 128] into fresh [P, page_bytes] storage
-    (layout.py:56-81): K4 min_error and V2 group 64, written by the page writer."""
-    from .packing import write_codec_pages
+    """Encode full temporal pages [P, H, B, 128] into fresh [P, page_bytes]
+    storage (layout.py:56-81): K4 min_error, the role map and V2 group 64, in
+    one launch."""
     _check_pages(keys, values, layout)
-    k = quantize(keys, CodecConfig(donor_policy="min_error"))
-    v = quantize_values(values, bits=2, group_size=64)
     result = torch.empty((keys.shape[0], layout.page_bytes), dtype=torch.uint8, device=keys.device)
     ids = torch.arange(keys.shape[0], dtype=torch.int32, device=keys.device)
-    write_codec_pages(k, v, layout, result, ids)
+    _encode_into(keys, values, layout, result, ids)
     return result
 
 
@@ -104,12 +148,17 @@ def unpack_pages_reference(pages, layout, dtype=torch.bfloat16):
 
 @torch.no_grad()
 def pack_pages_into(keys, values, layout, destination, page_ids, *, donor_backend="torch"):
-    """Seal fresh pages directly into their physical slots (layout.py:103-115).
+    """Seal fresh pages straight into their physical slots (layout.py:103-115)
+    with one launch and one flag read; no codec temporaries.
 
-    The page allocator owns unique in-range ids; no staging page pool is
-    created (codec temporaries are separately owned)."""
-    from .packing import write_codec_pages
+    The page allocator owns unique in-range ids (ids outside the pool are
+    skipped).  ``donor_backend`` is accepted for compatibility: every backend
+    runs the same selector.  A non-finite input raises ValueError after the
+    pages were written (they belong to the caller's fresh allocation)."""
     _check_pages(keys, values, layout)
-    k = quantize(keys, CodecConfig(donor_policy="min_error", donor_backend=donor_backend))
-    v = quantize_values(values, bits=2, group_size=64)
-    write_codec_pages(k, v, layout, destination, page_ids)
+    if destination.dtype != torch.uint8 or destination.ndim != 2 or destination.shape[1] != layout.page_bytes \
+            or not destination.is_contiguous():
+        raise ValueError("Expected contiguous uint8 destination page pool")
+    if page_ids.ndim != 1 or page_ids.numel() != keys.shape[0] or page_ids.dtype not in (torch.int32, torch.int64):
+        raise ValueError("One integer physical page ID is required per input page")
+    _encode_into(keys, values, layout, destination, page_ids)

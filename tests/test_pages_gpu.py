@@ -219,3 +219,36 @@ def test_paged_decode_batch_sixteen_sequences_against_oracle():
                                   H, B, 128 ** -0.5)
         err = float(np.abs(got[i] - exp).max())
         assert err <= ATOL, (i, int(ctx[i]), err)
+
+
+@pytest.mark.parametrize("block", [16, 64, 256])
+def test_pack_pages_into_is_one_launch_and_reports_non_finite_inputs(block):
+    # the fused page encoder: K4 min_error, role map and V2 written straight
+    # into the physical pages by one kernel, bit-exact with the oracle's
+    # pages; a non-finite key or value raises the codec's message
+    from inquant_vllm import PageLayout, pack_pages_into
+    layout = PageLayout(block, 4)
+    pool = torch.full((9, layout.page_bytes), 7, device="cuda", dtype=torch.uint8)
+    ids = torch.tensor([8, 1, 4], device="cuda", dtype=torch.int64)
+    k, v = _kv(977, (3, 4, block, 128))
+    pack_pages_into(k, v, layout, pool, ids)           # warm (first-use allocations)
+    torch.cuda.synchronize()
+    with torch.profiler.profile(activities=[torch.profiler.ProfilerActivity.CUDA]) as prof:
+        pack_pages_into(k, v, layout, pool, ids)
+        torch.cuda.synchronize()
+    kernels = [e.name for e in prof.events() if e.device_type == torch.autograd.DeviceType.CUDA
+               and "memcpy" not in e.name.lower() and "memset" not in e.name.lower()]
+    assert len(kernels) == 1 and "k4_encode_tile" in kernels[0], kernels
+    kq = oracle.k4_quantize(_np(k.float()), 8, 0.125, "min_error")
+    vq = oracle.v_quantize(_np(v.float()), 2, 64)
+    np.testing.assert_array_equal(_np(pool[ids]), oracle.pack_pages(kq, vq, 4, block))
+    assert (pool[torch.tensor([0, 2, 3, 5, 6, 7], device="cuda")] == 7).all()
+    bad_k, bad_v = k.clone(), v.clone()
+    bad_k[1, 2, 3, 4] = float("nan")
+    bad_v[2, 0, 5, 6] = float("inf")
+    with pytest.raises(ValueError, match="finite values"):
+        pack_pages_into(bad_k, v, layout, pool, ids)
+    with pytest.raises(ValueError, match="FP16 quantization parameters"):
+        pack_pages_into(k, bad_v, layout, pool, ids)
+    pack_pages_into(k, v, layout, pool, ids)           # flags cleared for the next call
+    np.testing.assert_array_equal(_np(pool[ids]), oracle.pack_pages(kq, vq, 4, block))
