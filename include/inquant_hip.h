@@ -125,7 +125,7 @@ typedef struct iq_block_ptrs {
  * NULL for V2/V4 values).  Roles: -1 normal, donor channel for a source,
  * -2 - i for donor i.  `blocks` is a HOST array; its contents travel as
  * kernel arguments (no host-to-device copy).  Replaces
- * PackedDecodeState.extend / _write_maps (triton_attention.py:294-369).
+ * PackedDecodeState.extend / _write_maps (triton_attention.py:234-309).
  */
 int iq_decode_append(int64_t *tables, int8_t *key_map, int8_t *value_map, int64_t first, int64_t count,
                      const iq_block_ptrs *blocks, int64_t H, int64_t S, int desc_bytes, void *stream);
@@ -144,7 +144,7 @@ int iq_decode_append(int64_t *tables, int8_t *key_map, int8_t *value_map, int64_
  *   out [Hq, 128] contiguous of out_dtype.
  * Keys/values are decoded and rounded to q_dtype exactly as the reference's
  * dequantize-then-attend path does; logits, softmax and P.V accumulate in
- * fp32.  Replaces PackedDecodeState.decode (triton_attention.py:377-448).
+ * fp32.  Replaces PackedDecodeState.decode (triton_attention.py:317-388).
  */
 int64_t iq_decode_workspace_floats(int64_t Hq, int64_t n_blocks, int64_t sink_t, int64_t tail_t);
 

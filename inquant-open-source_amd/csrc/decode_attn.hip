@@ -1,6 +1,6 @@
 // Fused single-query GQA decode attention over [sink | packed blocks | tail].
 //
-// Semantics follow PackedDecodeState.decode (triton_attention.py:377-448):
+// Semantics follow PackedDecodeState.decode (triton_attention.py:317-388):
 // one partition per packed block and per 256-token slice of the dense
 // sink and tail; keys and values are decoded from the K4 / V2 / V4 formats
 // (_decode_tile :33-50, _decode_value_tile :53-64), rounded to the query

@@ -1,6 +1,6 @@
 // Incremental decode-metadata append (gfx950).
 //
-// Restates PackedDecodeState.extend / _write_maps (triton_attention.py:294-369):
+// Restates PackedDecodeState.extend / _write_maps (triton_attention.py:234-309):
 // for each newly sealed block, one row of the i64 pointer table
 // (K payload, K scales, K padding, V payload, V scales-or-K4-scales,
 // V offsets-or-padding, then the K source and donor descriptor addresses

@@ -461,7 +461,7 @@ IQO_EXPORT void iqo_v_dequantize(const uint8_t *payload, const uint16_t *scales,
 }
 
 /* ------------------------------------------------------------------ */
-/* role maps (triton_attention.py:361-369; layout.py:73-77)            */
+/* role maps (triton_attention.py:301-309; layout.py:73-77)            */
 /* ------------------------------------------------------------------ */
 
 /* out: [heads, D] int16 roles: -1 normal, donor index for a source, -2-i for donor i. */

@@ -149,7 +149,7 @@ def v_dequantize(packed: dict, bits: int, group_size: int, dtype: str = "float32
 
 
 def role_map(src: np.ndarray, don: np.ndarray, D: int = 128) -> np.ndarray:
-    """src/don int64 [heads, count] -> int16 [heads, D] roles (triton_attention.py:361-369)."""
+    """src/don int64 [heads, count] -> int16 [heads, D] roles (triton_attention.py:301-309)."""
     src = np.ascontiguousarray(src, np.int64)
     don = np.ascontiguousarray(don, np.int64)
     heads, count = src.shape
