@@ -45,6 +45,8 @@ def parse():
     ap.add_argument("--no-graph", action="store_true", help="launch layer by layer instead of a HIP graph")
     ap.add_argument("--no-paged", action="store_true", help="skip the batched paged decode (config 4)")
     ap.add_argument("--no-cfg3", action="store_true", help="skip the Mistral-7B decode (config 3)")
+    ap.add_argument("--no-encode", action="store_true", help="skip the config 3 encode")
+    ap.add_argument("--no-append", action="store_true", help="skip the config 2 append measurements")
     ap.add_argument("--copy-probe", action="store_true",
                     help="only run a 1 GiB device-to-device copy (calibrates rocprofv3 FETCH_SIZE / WRITE_SIZE)")
     return ap.parse_args()
@@ -549,13 +551,15 @@ def main():
     gbs = step_bytes / (ms * 1e-3) / 1e9
     layer_us = ms * 1e3 / args.layers
     achieved = per_layer / (layer_us * 1e-6) / 1e9
-    enc = time_encode(device)
+    enc = None if args.no_encode else time_encode(device)
     paged = None if args.no_paged else time_paged(device)
-    append = time_append(device)
-    # a controlled runner may skip the position check and its device-to-host
-    # copy per token (cache.py:30-32)
-    append["append_us_per_token_unvalidated"] = time_append(device, validate_positions=False)["append_us_per_token"]
-    append["step"] = time_append_step(device)
+    append = None
+    if not args.no_append:
+        append = time_append(device)
+        # a controlled runner may skip the position check and its synchronization (cache.py:30-32)
+        append["append_us_per_token_unvalidated"] = time_append(device, validate_positions=False)[
+            "append_us_per_token"]
+        append["step"] = time_append_step(device)
     cfg3 = None if args.no_cfg3 else time_decode_cfg3(device)
     result = {
         "metric": METRIC,
@@ -581,10 +585,12 @@ def main():
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": measured_traffic(),
                      "kernel": "decode_fast + decode_reduce (matrix-core decode, then the partition merge)",
                      "bytes_per_launch": per_layer},
-        "encode_mtok_s": round(enc["encode_mtok_s"], 2),
-        "encode": {k: round(v, 3) for k, v in enc.items()},
     }
-    result["append_cfg2"] = append
+    if enc is not None:
+        result["encode_mtok_s"] = round(enc["encode_mtok_s"], 2)
+        result["encode"] = {k: round(v, 3) for k, v in enc.items()}
+    if append is not None:
+        result["append_cfg2"] = append
     if cfg3 is not None:
         result["decode_cfg3"] = cfg3
     if paged is not None:

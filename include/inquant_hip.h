@@ -131,10 +131,26 @@ int iq_decode_append(int64_t *tables, int8_t *key_map, int8_t *value_map, int64_
                      const iq_block_ptrs *blocks, int64_t H, int64_t S, int desc_bytes, void *stream);
 
 /*
+ * The leading blocks of a decode state that sit at a fixed stride from each
+ * other (the per-block views of one batched encode): block i < blocks has
+ * field f (pointer-table column order: K payload, K scales, K padding,
+ * V payload, V scales, V offsets, K sources, K donors) at base[f] + i * that
+ * field's bytes per block (H*B*64, H*512, H*S*4, H*B*D*bits/8, H*B*(D/group)*2
+ * twice, H*S, H*S).  The decode reads these blocks' addresses from the
+ * kernel arguments instead of the pointer table; the table stays valid for
+ * every block.
+ */
+typedef struct iq_block_run {
+    uint64_t base[IQ_TABLE_COLS];
+    int64_t blocks;
+} iq_block_run;
+
+/*
  * Fused single-query GQA decode over [sink | packed blocks | tail].
  *   q [Hq, 128] (row stride q_stride_h) of q_dtype (f32, bf16, f16);
  *   tables i64 [n_blocks, IQ_TABLE_COLS], key_map/value_map int8 [n_blocks, H, 128]
  *   (value_map used only when value_bits == 0, i.e. K4-coded V);
+ *   run: optional (NULL) fixed-stride run of the leading blocks;
  *   block_tokens tokens per packed block, S salient channels per block;
  *   value_bits in {0, 2, 4}, value_group in {32, 64, 128};
  *   sink/tail K/V of q_dtype with (head, token) element strides, lengths
@@ -150,7 +166,7 @@ int64_t iq_decode_workspace_floats(int64_t Hq, int64_t n_blocks, int64_t sink_t,
 
 int iq_decode_attention(const void *q, int q_dtype, int64_t q_stride_h, int64_t Hq,
                         const int64_t *tables, const int8_t *key_map, const int8_t *value_map,
-                        int64_t n_blocks, int64_t block_tokens, int64_t H, int64_t S,
+                        const iq_block_run *run, int64_t n_blocks, int64_t block_tokens, int64_t H, int64_t S,
                         int value_bits, int value_group,
                         const void *sink_k, const void *sink_v, int64_t sink_k_sh, int64_t sink_k_st,
                         int64_t sink_v_sh, int64_t sink_v_st, int64_t sink_t,
@@ -173,7 +189,7 @@ int iq_decode_attention(const void *q, int q_dtype, int64_t q_stride_h, int64_t 
 
 int iq_decode_attention_noalloc(const void *q, int q_dtype, int64_t q_stride_h, int64_t Hq,
                                 const int64_t *tables, const int8_t *key_map, const int8_t *value_map,
-                                int64_t n_blocks, int64_t block_tokens, int64_t H, int64_t S,
+                                const iq_block_run *run, int64_t n_blocks, int64_t block_tokens, int64_t H, int64_t S,
                                 int value_bits, int value_group,
                                 const void *sink_k, const void *sink_v, int64_t sink_k_sh, int64_t sink_k_st,
                                 int64_t sink_v_sh, int64_t sink_v_st, int64_t sink_t,

@@ -321,7 +321,7 @@ int iq_decode_fast_launch(const void *q, int q_dtype, int64_t q_stride_h, int64_
                           int64_t sink_k_st, int64_t sink_v_sh, int64_t sink_v_st, int64_t sink_t,
                           const void *tail_k, const void *tail_v, int64_t tail_k_sh, int64_t tail_k_st,
                           int64_t tail_v_sh, int64_t tail_v_st, int64_t tail_t, float scale, float *workspace,
-                          void *out, int out_dtype, int64_t *parts, hipStream_t stream);
+                          void *out, int out_dtype, const iq_block_run *run, int64_t *parts, hipStream_t stream);
 
 namespace {
 
@@ -340,7 +340,7 @@ extern "C" int64_t iq_decode_workspace_floats(int64_t Hq, int64_t n_blocks, int6
 
 extern "C" int iq_decode_attention(const void *q, int q_dtype, int64_t q_stride_h, int64_t Hq,
                                    const int64_t *tables, const int8_t *key_map, const int8_t *value_map,
-                                   int64_t n_blocks, int64_t block_tokens, int64_t H, int64_t S, int value_bits,
+                                   const iq_block_run *run, int64_t n_blocks, int64_t block_tokens, int64_t H, int64_t S, int value_bits,
                                    int value_group, const void *sink_k, const void *sink_v, int64_t sink_k_sh,
                                    int64_t sink_k_st, int64_t sink_v_sh, int64_t sink_v_st, int64_t sink_t,
                                    const void *tail_k, const void *tail_v, int64_t tail_k_sh, int64_t tail_k_st,
@@ -373,8 +373,8 @@ extern "C" int iq_decode_attention(const void *q, int q_dtype, int64_t q_stride_
     const int fast = iq_decode_fast_launch(q, q_dtype, q_stride_h, Hq, tables, key_map, n_blocks, block_tokens, H,
                                            S, value_bits, value_group, sink_k, sink_v, sink_k_sh, sink_k_st,
                                            sink_v_sh, sink_v_st, sink_t, tail_k, tail_v, tail_k_sh, tail_k_st,
-                                           tail_v_sh, tail_v_st, tail_t, scale, workspace, out, out_dtype, &parts,
-                                           (hipStream_t)stream);
+                                           tail_v_sh, tail_v_st, tail_t, scale, workspace, out, out_dtype, run,
+                                           &parts, (hipStream_t)stream);
     if (fast == IQ_OK) {
         IQ_CHECK_LAUNCH("decode_fast");
         if (parts == 1) return IQ_OK;
@@ -437,7 +437,7 @@ float *device_scratch()
 
 extern "C" int iq_decode_attention_noalloc(const void *q, int q_dtype, int64_t q_stride_h, int64_t Hq,
                                            const int64_t *tables, const int8_t *key_map, const int8_t *value_map,
-                                           int64_t n_blocks, int64_t block_tokens, int64_t H, int64_t S,
+                                           const iq_block_run *run, int64_t n_blocks, int64_t block_tokens, int64_t H, int64_t S,
                                            int value_bits, int value_group, const void *sink_k, const void *sink_v,
                                            int64_t sink_k_sh, int64_t sink_k_st, int64_t sink_v_sh,
                                            int64_t sink_v_st, int64_t sink_t, const void *tail_k,
@@ -454,7 +454,7 @@ extern "C" int iq_decode_attention_noalloc(const void *q, int q_dtype, int64_t q
                  (long long)IQ_NOALLOC_SCRATCH_FLOATS);
     float *ws = device_scratch();
     if (!ws) return IQ_ERR_DEVICE;
-    return iq_decode_attention(q, q_dtype, q_stride_h, Hq, tables, key_map, value_map, n_blocks, block_tokens, H, S,
+    return iq_decode_attention(q, q_dtype, q_stride_h, Hq, tables, key_map, value_map, run, n_blocks, block_tokens, H, S,
                                value_bits, value_group, sink_k, sink_v, sink_k_sh, sink_k_st, sink_v_sh, sink_v_st,
                                sink_t, tail_k, tail_v, tail_k_sh, tail_k_st, tail_v_sh, tail_v_st, tail_t, scale,
                                ws, IQ_NOALLOC_SCRATCH_FLOATS, out, out_dtype, stream);

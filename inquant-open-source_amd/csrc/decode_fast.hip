@@ -17,9 +17,15 @@
 //     a nibble byte n to n * 2^-9 exactly, so fma(v, s * 2^9, -8 s) is the
 //     single rounding of (n - 8) * s, as the reference's fp32 multiply.
 //   * Salient and donor channels decode to zero in the 4-bit pass (zero
-//     constants); an extra v_mfma_f32_16x16x16 over the gathered 8-bit codes
-//     adds the salient terms, and a per-block constant adds
-//     q . round(padding) for donors.
+//     constants).  Their 8-bit codes come from the matrix cores: an int8
+//     v_mfma_i32_16x16x64 of a selection matrix (16 at a source's channel,
+//     1 at its donor's) with the raw nibble bytes gives 16 hi + lo exactly,
+//     already in the A-operand layout of the v_mfma_f32_16x16x16 that adds
+//     the salient terms; a per-block constant adds q . round(padding) for
+//     donors.
+//   * Blocks of one batched encode sit at a fixed stride from each other;
+//     for that leading run of blocks the addresses come from the kernel
+//     arguments, so the payload loads do not wait for a pointer-table row.
 //   * LDS stays within 40 KiB (the query rows live in a V tile until every
 //     lane holds its operands), so four workgroups share a compute unit.
 //   * Online softmax in the log2 domain; P = hi + lo (two bf16/f16 terms) so
@@ -35,13 +41,19 @@ constexpr int WAVES = 4;
 constexpr int CHUNK = 64;              // tokens per wavefront per pass
 constexpr int VR = 136;                // dwords per staged token-pair row of decoded V (128 + 8: two passes per read)
 constexpr int OROW = 132;              // floats per staged output row in the combine (128 + 4: conflict-free 16-byte stores)
-constexpr int KROW = 17;               // dwords per staged K row (16 + 1: conflict-free byte gathers)
 constexpr int KC_STRIDE = 68;          // float2 slots per 32-channel group of K constants (+4: no bank overlap)
 constexpr int DENSE_SPLIT = 256;
 constexpr int QROW = D + 8;            // u16 per staged query row (+8: the 16 rows of a B-operand read hit distinct banks)
 constexpr float LN2 = 0.693147180559945309f;
 
+typedef __attribute__((ext_vector_type(4))) int i32x4;
+
 struct FastArgs {
+    // the leading run of blocks laid out at a fixed stride (a batched encode):
+    // block p < run_blocks has field f (pointer-table column order) at
+    // run[f] + p * (that field's bytes per block)
+    const uint8_t *run[IQ_TABLE_COLS];
+    int64_t run_blocks;
     const uint16_t *q;
     int64_t q_sh;
     int G;
@@ -70,14 +82,15 @@ struct __attribute__((aligned(16))) FastSmem {
     uint32_t v[WAVES][16 * VR];
     f32x2 kc[4 * KC_STRIDE];     // per channel (s * 2^9, -8 s); (0, 0) at salient and donor channels
     int8_t role[D];
-    uint32_t salw[64];           // gather offsets: src byte, shift, don byte, shift
-    f32x2 salf[64];              // (s_src, -128 s_src)
-    uint16_t qsal[16 * 68];      // Q[g][src_k], zero beyond S (68: fewer bank collisions than 64)
-    float dpad[64];              // padding of donor k, rounded to the query dtype
+    uint32_t salw[16];           // source k: its channel | donor channel << 8
+    f32x2 salf[16];              // (s_src, -128 s_src)
+    uint16_t qsal[16 * 20];      // Q[g][src_k], zero beyond S
+    float dpad[16];              // padding of donor k, rounded to the query dtype
     float wm[WAVES][16], wl[WAVES][16];
 };
 static_assert(sizeof(FastSmem) <= 40 * 1024, "four workgroups per compute unit");
 static_assert(16 * QROW / 2 <= 16 * VR, "the query rows fit in one wave's tile");
+static_assert(16 * D <= 16 * VR * 4, "the salient selection matrix fits in one wave's tile");
 
 // One partition.  PACKED and dense partitions are separate instantiations so
 // that neither has a branch between its loads and their first use: a branch
@@ -127,8 +140,7 @@ __device__ __forceinline__ void fast_body(const FastArgs &a, FastSmem &sm)
     const uint8_t *kpay = nullptr, *vpay = nullptr;
     const uint16_t *vsc = nullptr, *voff = nullptr;
     int start = 0, stop = 0;
-    const int S = packed ? (int)a.S : 0;
-    const int sal_groups = (S + 15) / 16;
+    const int S = packed ? (int)a.S : 0;         // at most 16 (one group of salient channels)
     const int qg = tid >> 4, qc = (tid & 15) * 8;  // this thread's 8 query elements
     const u32x4 qraw = ld16(a.q + (int64_t)(h * G + (qg < G ? qg : G - 1)) * a.q_sh + qc);
     float kscale = 0.0f, kpad = 0.0f;
@@ -163,15 +175,26 @@ __device__ __forceinline__ void fast_body(const FastArgs &a, FastSmem &sm)
         }                                                                                             \
     } while (0)
     if (packed) {
-        // scalar loads (the row is the same for every lane): one 64-byte
-        // s_load through the scalar cache; the table was written by an
-        // earlier launch, so the kernel-start cache invalidation covers it
-        const __attribute__((address_space(4))) int64_t *rv =
-            (const __attribute__((address_space(4))) int64_t *)(a.tables + p * IQ_TABLE_COLS);
-        int64_t tr[8];
+        // block addresses: from the kernel arguments for the run of
+        // fixed-stride blocks, else one 64-byte scalar load of the pointer-table
+        // row (written by an earlier launch, so the kernel-start cache
+        // invalidation covers it)
+        uintptr_t tr[IQ_TABLE_COLS];
+        if (p < a.run_blocks) {
+            // bytes per block of each field: K payload, K scales, K padding,
+            // V payload, V scales, V offsets, K sources, K donors
+            const int64_t HB = a.H * a.BT;
+            const int64_t per[IQ_TABLE_COLS] = {HB * (D / 2), a.H * D * 4, a.H * a.S * 4, HB * VROW,
+                                                HB * ngroups * 2, HB * ngroups * 2, a.H * a.S, a.H * a.S};
 #pragma unroll
-        for (int k = 0; k < 8; ++k) tr[k] = rv[k];
-        auto row = [&](int k) -> uintptr_t { return (uintptr_t)tr[k]; };
+            for (int k = 0; k < IQ_TABLE_COLS; ++k) tr[k] = (uintptr_t)(a.run[k] + p * per[k]);
+        } else {
+            const __attribute__((address_space(4))) int64_t *rv =
+                (const __attribute__((address_space(4))) int64_t *)(a.tables + p * IQ_TABLE_COLS);
+#pragma unroll
+            for (int k = 0; k < IQ_TABLE_COLS; ++k) tr[k] = (uintptr_t)rv[k];
+        }
+        auto row = [&](int k) -> uintptr_t { return tr[k]; };
         krole = (uint8_t)ldg<int8_t>(a.kmap + (p * a.H + h) * D + (tid & (D - 1)));
         kscale = ldg<float>((const float *)row(1) + h * D + (tid & (D - 1)));
         {   // no branch around these loads: with S == 0 they read valid
@@ -210,6 +233,11 @@ __device__ __forceinline__ void fast_body(const FastArgs &a, FastSmem &sm)
     };
     // consume the small loads (the payload stays in flight)
     *(u32x4 *)(s_q + qg * QROW + qc) = qg < G ? qraw : u32x4{0u, 0u, 0u, 0u};
+    // selection matrix of the salient codes, [source k][channel] bytes with the
+    // even channels of a row first (channel c at byte (c & 1) * 64 + c / 2),
+    // staged in wave 1's V tile, which is free until the operands are loaded
+    uint8_t *const s_sel = (uint8_t *)&sm.v[1][0];
+    if (packed) *(u32x2 *)(s_sel + 8 * tid) = u32x2{0u, 0u};
     if (packed) {
         if (tid < D) {
             // salient and donor channels decode to zero in the 4-bit pass:
@@ -219,26 +247,30 @@ __device__ __forceinline__ void fast_body(const FastArgs &a, FastSmem &sm)
             s_role[tid] = (int8_t)krole;
         }
         if (tid < S) {
-            s_salw[tid] = (ksrc >> 1) | (((ksrc & 1) * 4) << 8) | ((kdon >> 1) << 16) | (((kdon & 1) * 4) << 24);
+            s_salw[tid] = ksrc | (kdon << 8);
             s_dpad[tid] = round_q<F16>(kpad);
         }
     }
     __syncthreads();
 
     // ---------------- cooperative per-workgroup constants
-    // channel and descriptor index of salient slot k, from its gather word
-    auto sal_src = [&](uint32_t w) { return 2u * (w & 0xffu) + ((w >> 8) & 0xffu) / 4u; };
-    auto sal_don = [&](uint32_t w) { return 2u * ((w >> 16) & 0xffu) + (w >> 24) / 4u; };
     if constexpr (PACKED) {
-        // a source channel's descriptor index is -2 - role[its donor]
-        if (tid < D && krole < (uint32_t)D) {
-            const int k = -2 - (int)s_role[krole];
-            if (k >= 0 && k < S) s_salf[k] = f32x2{kscale, -128.0f * kscale};   // exact
+        // a source channel's descriptor index is -2 - role[its donor]; a
+        // donor's is -2 - its role.  Each marks its byte of the selection
+        // matrix: 16 for the source (high nibble), 1 for the donor.
+        if (tid < D) {
+            const int r = (int)(int8_t)krole;
+            const int k = r >= 0 ? -2 - (int)s_role[r] : -2 - r;
+            if (k >= 0 && k < S) {
+                s_sel[k * D + (tid & 1) * (D / 2) + (tid >> 1)] = r >= 0 ? 16 : 1;
+                if (r >= 0) s_salf[k] = f32x2{kscale, -128.0f * kscale};   // exact
+            }
         }
-        for (int i = tid; i < 16 * 16 * sal_groups; i += 256) {
-            const int g = i / (16 * sal_groups), k = i % (16 * sal_groups);
-            s_qsal[g * 68 + k] = k < S ? s_q[g * QROW + sal_src(s_salw[k])] : (uint16_t)0;
+        if (tid < 16 * 16) {
+            const int g = tid >> 4, k = tid & 15;
+            s_qsal[g * 20 + k] = k < S ? s_q[g * QROW + (s_salw[k] & 0xffu)] : (uint16_t)0;
         }
+        if (tid >= S && tid < 16) s_salf[tid] = f32x2{0.0f, 0.0f};
     }
     __syncthreads();
 
@@ -247,12 +279,27 @@ __device__ __forceinline__ void fast_body(const FastArgs &a, FastSmem &sm)
 #pragma unroll
     for (int d = 0; d < 4; ++d) qb[d] = *(const u32x4 *)(s_q + gl * QROW + 32 * ql + 8 * d);
     float bias = 0.0f;                             // sum_k q[gl][don_k] * round(pad_k)
-    for (int grp = 0; grp < sal_groups; ++grp)
+    // salient operands: the selection matrix rows (source k = gl; byte i of
+    // sel_e / sel_o is channel 32 ql + 2 i / 32 ql + 2 i + 1: 16 at the
+    // source's channel, 1 at its donor's), the query values of the sources
+    // (B operand, k = 4 ql + e) and the codes' (scale, -128 scale)
+    i32x4 sel_e = {0, 0, 0, 0}, sel_o = {0, 0, 0, 0};
+    u32x2 qs = {0u, 0u};
+    f32x2 sf[4];
+    if (PACKED && S > 0) {
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-            const int k = 16 * grp + 4 * ql + e;
-            if (k < S) bias = fmaf(to_f32<F16>(s_q[gl * QROW + sal_don(s_salw[k])]), s_dpad[k], bias);
+            const int k = 4 * ql + e;
+            if (k < S) bias = fmaf(to_f32<F16>(s_q[gl * QROW + (s_salw[k] >> 8)]), s_dpad[k], bias);
+            sf[e] = s_salf[k];
         }
+        qs = *(const u32x2 *)(s_qsal + gl * 20 + 4 * ql);
+        sel_e = *(const i32x4 *)(s_sel + gl * D + 16 * ql);
+        sel_o = *(const i32x4 *)(s_sel + gl * D + D / 2 + 16 * ql);
+    } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) sf[e] = f32x2{0.0f, 0.0f};
+    }
     bias = xsum16(bias);
     // every lane holds its query operands: wave 0's tile may now be overwritten
     __syncthreads();
@@ -270,20 +317,26 @@ __device__ __forceinline__ void fast_body(const FastArgs &a, FastSmem &sm)
         // ---------------- logits S^T[token, g] for four 16-token tiles
         f32x4 sc[4];
         if (packed) {
-            // channel group d outer: each lane's 8 constants of group d are read
-            // from LDS once and serve all four tiles; per tile the sum over d
-            // keeps its order, so the logits do not depend on the loop nest
+            // tile outer: tile j is decoded and multiplied as soon as its payload
+            // has landed; each lane's 8 constants of group d are re-read from
+            // LDS per tile (four distinct addresses per read: broadcasts).
+            // Within a tile the sum over d keeps its order.
 #pragma unroll
-            for (int j = 0; j < 4; ++j) sc[j] = f32x4{bias, bias, bias, bias};
+            for (int j = 0; j < 4; ++j) {
+                f32x4 s = {bias, bias, bias, bias};
+                i32x4 lo4, hi4;                      // raw nibbles of the tile: even / odd channels
 #pragma unroll
-            for (int d = 0; d < 4; ++d) {
-                const f32x2 *kc = s_kc + ql * KC_STRIDE + 8 * d;
-                const u32x4 c01 = *(const u32x4 *)(kc + 0), c23 = *(const u32x4 *)(kc + 2);
-                const u32x4 c45 = *(const u32x4 *)(kc + 4), c67 = *(const u32x4 *)(kc + 6);
-#pragma unroll
-                for (int j = 0; j < 4; ++j) {
+                for (int d = 0; d < 4; ++d) {
+                    // keeps the constant reads inside the tile: hoisted out of the
+                    // tile loop, all 64 constants would stay live and spill
+                    asm volatile("" ::: "memory");
+                    const f32x2 *kc = s_kc + ql * KC_STRIDE + 8 * d;
+                    const u32x4 c01 = *(const u32x4 *)(kc + 0), c23 = *(const u32x4 *)(kc + 2);
+                    const u32x4 c45 = *(const u32x4 *)(kc + 4), c67 = *(const u32x4 *)(kc + 6);
                     const uint32_t x = kw[j][d];
                     const uint32_t lo = x & 0x0f0f0f0fu, hi = (x >> 4) & 0x0f0f0f0fu;
+                    lo4[d] = (int)lo;
+                    hi4[d] = (int)hi;
                     const f32x2 e01 = fp8x2<false>(lo), e23 = fp8x2<true>(lo);
                     const f32x2 o01 = fp8x2<false>(hi), o23 = fp8x2<true>(hi);
 #define KF(cv, i) __uint_as_float(cv[i])
@@ -293,41 +346,18 @@ __device__ __forceinline__ void fast_body(const FastArgs &a, FastSmem &sm)
                     kv[2] = pack2<F16>(fmaf(e23.x, KF(c45, 0), KF(c45, 1)), fmaf(o23.x, KF(c45, 2), KF(c45, 3)));
                     kv[3] = pack2<F16>(fmaf(e23.y, KF(c67, 0), KF(c67, 1)), fmaf(o23.y, KF(c67, 2), KF(c67, 3)));
 #undef KF
-                    sc[j] = mma32<F16>(kv, qb[d], sc[j]);
+                    s = mma32<F16>(kv, qb[d], s);
                 }
-            }
-            if (sal_groups) {
-                // stage the four K tiles as [64 tokens][17 dwords] for the salient gathers
+                if (S > 0) {
+                    // codes 16 hi + lo of sources 4 ql .. 4 ql + 3 for token 16 j + gl
+                    i32x4 code = __builtin_amdgcn_mfma_i32_16x16x64_i8(sel_e, lo4, i32x4{0, 0, 0, 0}, 0, 0, 0);
+                    code = __builtin_amdgcn_mfma_i32_16x16x64_i8(sel_o, hi4, code, 0, 0, 0);
+                    float v[4];
 #pragma unroll
-                for (int j = 0; j < 4; ++j)
-#pragma unroll
-                    for (int w = 0; w < 4; ++w) vt[(16 * j + gl) * KROW + 4 * ql + w] = kw[j][w];
-                const uint8_t *kt = (const uint8_t *)vt;
-                for (int grp = 0; grp < sal_groups; ++grp) {
-                    uint32_t sw[4];
-                    f32x2 sf[4];
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) {
-                        const int k = 16 * grp + 4 * ql + e;
-                        sw[e] = k < S ? s_salw[k] : 0u;
-                        sf[e] = k < S ? s_salf[k] : f32x2{0.0f, 0.0f};
-                    }
-                    const u32x2 qs = *(const u32x2 *)(s_qsal + gl * 68 + 16 * grp + 4 * ql);
-#pragma unroll
-                    for (int j = 0; j < 4; ++j) {
-                        const uint8_t *rowp = kt + (16 * j + gl) * (4 * KROW);
-                        float v[4];
-#pragma unroll
-                        for (int e = 0; e < 4; ++e) {
-                            const uint32_t w = sw[e];
-                            const uint32_t hi = (rowp[w & 0xffu] >> ((w >> 8) & 0xffu)) & 15u;
-                            const uint32_t lo = (rowp[(w >> 16) & 0xffu] >> (w >> 24)) & 15u;
-                            v[e] = fmaf((float)((hi << 4) | lo), sf[e].x, sf[e].y);
-                        }
-                        const u32x2 ka = {pack2<F16>(v[0], v[1]), pack2<F16>(v[2], v[3])};
-                        sc[j] = mma16<F16>(ka, qs, sc[j]);
-                    }
+                    for (int e = 0; e < 4; ++e) v[e] = fmaf((float)code[e], sf[e].x, sf[e].y);
+                    s = mma16<F16>(u32x2{pack2<F16>(v[0], v[1]), pack2<F16>(v[2], v[3])}, qs, s);
                 }
+                sc[j] = s;
             }
         } else {
             // dense sink / tail: K rows of the query dtype are the A operand
@@ -376,8 +406,7 @@ __device__ __forceinline__ void fast_body(const FastArgs &a, FastSmem &sm)
                 }
         }
         cmax = xmax16(cmax);
-        const float m_new = fmaxf(m_run, cmax);
-        const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
+        const float m_new = cmax;                  // one pass per wavefront: nothing to rescale
         float lsum = 0.0f;
         u32x4 phi[2], plo[2];
 #pragma unroll
@@ -396,10 +425,8 @@ __device__ __forceinline__ void fast_body(const FastArgs &a, FastSmem &sm)
             plo[j >> 1][2 * (j & 1) + 1] =
                 pack2<F16>(pr[2] - to_f32<F16>(h23 & 0xffffu), pr[3] - to_f32<F16>(h23 >> 16));
         }
-        l_run = l_run * alpha + lsum;
+        l_run = lsum;
         m_run = m_new;
-#pragma unroll
-        for (int n = 0; n < 8; ++n) acc[n] *= alpha;
 
         // ---------------- two half chunks: decode 32 V rows to LDS, then O^T += V^T P^T
 #pragma unroll
@@ -568,12 +595,12 @@ int iq_decode_fast_launch(const void *q, int q_dtype, int64_t q_stride_h, int64_
                           int64_t sink_k_st, int64_t sink_v_sh, int64_t sink_v_st, int64_t sink_t,
                           const void *tail_k, const void *tail_v, int64_t tail_k_sh, int64_t tail_k_st,
                           int64_t tail_v_sh, int64_t tail_v_st, int64_t tail_t, float scale, float *workspace,
-                          void *out, int out_dtype, int64_t *parts, hipStream_t stream)
+                          void *out, int out_dtype, const iq_block_run *run, int64_t *parts, hipStream_t stream)
 {
     if (q_dtype != IQ_BF16 && q_dtype != IQ_F16) return IQ_ERR_UNSUPPORTED;
     if (out_dtype != IQ_F32 && out_dtype != IQ_BF16 && out_dtype != IQ_F16) return IQ_ERR_UNSUPPORTED;
     if (n_blocks > 0 && value_bits != 2 && value_bits != 4) return IQ_ERR_UNSUPPORTED;
-    if (Hq / H > 16 || S > 64) return IQ_ERR_UNSUPPORTED;
+    if (Hq / H > 16 || S > 16) return IQ_ERR_UNSUPPORTED;
     if (n_blocks > 0 && block_tokens > CHUNK * WAVES) return IQ_ERR_UNSUPPORTED;   // one pass per workgroup
     // query, dense rows and packed rows are read as 16-byte vectors
     auto aligned = [](const void *ptr, int64_t sh, int64_t st) {
@@ -586,11 +613,15 @@ int iq_decode_fast_launch(const void *q, int q_dtype, int64_t q_stride_h, int64_
         return IQ_ERR_UNSUPPORTED;
     const int64_t P = n_blocks + (sink_t + tail_t + DENSE_SPLIT - 1) / DENSE_SPLIT;
     if (P < 1 || P > 65535) return IQ_ERR_UNSUPPORTED;
-    FastArgs a{(const uint16_t *)q, q_stride_h, (int)(Hq / H), tables, key_map, n_blocks, block_tokens, H, S,
+    FastArgs a{{}, 0, (const uint16_t *)q, q_stride_h, (int)(Hq / H), tables, key_map, n_blocks, block_tokens, H, S,
                value_group ? value_group : 64, (const uint16_t *)sink_k, (const uint16_t *)sink_v, sink_k_sh,
                sink_k_st, sink_v_sh, sink_v_st, sink_t, (const uint16_t *)tail_k, (const uint16_t *)tail_v,
                tail_k_sh, tail_k_st, tail_v_sh, tail_v_st, tail_t, scale * 1.44269504088896341f, workspace, P,
                out, out_dtype};
+    if (run && run->blocks > 0 && n_blocks > 0) {
+        for (int k = 0; k < IQ_TABLE_COLS; ++k) a.run[k] = (const uint8_t *)run->base[k];
+        a.run_blocks = run->blocks < n_blocks ? run->blocks : n_blocks;
+    }
     *parts = P;
     const dim3 grid((unsigned)H, (unsigned)P), block(256);
     const bool f16 = q_dtype == IQ_F16;

@@ -30,6 +30,12 @@ class BlockPtrs(ctypes.Structure):
         "k_src", "k_don", "v_src", "v_don")]
 
 
+class BlockRun(ctypes.Structure):
+    """Mirror of iq_block_run: field addresses of the first block of the
+    fixed-stride run of a decode state's leading blocks, and their count."""
+    _fields_ = [("base", ctypes.c_uint64 * 8), ("blocks", _i64)]
+
+
 class TailDesc(ctypes.Structure):
     """Mirror of iq_tail_desc in include/inquant_hip.h: the fixed part of a
     cache layer's tail append (its [2, H, capacity, D] row buffer and the
@@ -51,11 +57,13 @@ _SIGNATURES = {
     "iq_v_dequantize": (_int, [_p, _p, _p, _i64, _i64, _int, _int, _p, _int, _p]),
     "iq_decode_append": (_int, [_p, _p, _p, _i64, _i64, ctypes.POINTER(BlockPtrs), _i64, _i64, _int, _p]),
     "iq_decode_workspace_floats": (_i64, [_i64, _i64, _i64, _i64]),
-    "iq_decode_attention": (_int, [_p, _int, _i64, _i64, _p, _p, _p, _i64, _i64, _i64, _i64, _int, _int,
+    "iq_decode_attention": (_int, [_p, _int, _i64, _i64, _p, _p, _p, ctypes.POINTER(BlockRun), _i64, _i64, _i64,
+                                   _i64, _int, _int,
                                    _p, _p, _i64, _i64, _i64, _i64, _i64,
                                    _p, _p, _i64, _i64, _i64, _i64, _i64,
                                    _f32, _p, _i64, _p, _int, _p]),
-    "iq_decode_attention_noalloc": (_int, [_p, _int, _i64, _i64, _p, _p, _p, _i64, _i64, _i64, _i64, _int, _int,
+    "iq_decode_attention_noalloc": (_int, [_p, _int, _i64, _i64, _p, _p, _p, ctypes.POINTER(BlockRun), _i64, _i64,
+                                           _i64, _i64, _int, _int,
                                            _p, _p, _i64, _i64, _i64, _i64, _i64,
                                            _p, _p, _i64, _i64, _i64, _i64, _i64,
                                            _f32, _p, _int, _p]),

@@ -127,11 +127,29 @@ class _BlockFormat:
             raise ValueError("Packed decode supports at most 64 salient channels (int8 roles)")
 
 
+def _field_addresses(k, v, k4_values):
+    """A block's addresses in pointer-table column order."""
+    return (k.payload.data_ptr(), k.scales.data_ptr(), k.padding.data_ptr(), v.payload.data_ptr(),
+            v.scales.data_ptr(), (v.padding if k4_values else v.offsets).data_ptr(),
+            k.salient_channels.data_ptr(), k.donor_channels.data_ptr())
+
+
+def _field_bytes(fmt: "_BlockFormat") -> tuple:
+    """Bytes per block of each field, when blocks come from one batched encode."""
+    h, t, s = fmt.heads, fmt.tokens, fmt.salient
+    vbytes = 128 * fmt.value_bits // 8
+    groups = 128 // fmt.value_group
+    return (h * t * 64, h * 512, h * s * 4, h * t * vbytes, h * t * groups * 2, h * t * groups * 2,
+            h * s * fmt.desc_bytes, h * s * fmt.desc_bytes)
+
+
 class _Descriptors:
     """Pointer table and role maps, grown on demand: exact at first, then
     max(n, min(2 * capacity, n + 7)) blocks (triton_attention.py:282-283)."""
 
     def __init__(self, device, heads: int, k4_values: bool):
+        self.run = nat.BlockRun()          # leading blocks at a fixed stride (one batched encode)
+        self.run_open = True               # the run may still grow
         self.tables = torch.empty((0, _COLUMNS), dtype=torch.int64, device=device)
         self.key_map = torch.empty((0, heads, 128), dtype=torch.int8, device=device)
         self.value_map = torch.empty((0, heads, 128) if k4_values else (0,), dtype=torch.int8, device=device)
@@ -154,7 +172,26 @@ class _Descriptors:
         if self.k4_values:
             self.value_map = regrow(self.value_map, (grown, *self.value_map.shape[1:]))
 
+    def grow_run(self, first: int, keys, values, fmt: _BlockFormat) -> None:
+        """Extend the fixed-stride run over the new blocks while they continue it."""
+        if not self.run_open or fmt.value_bits == 0:
+            self.run_open = False
+            return
+        step = _field_bytes(fmt)
+        run = self.run
+        for i, (k, v) in enumerate(zip(keys, values)):
+            addr = _field_addresses(k, v, False)
+            if run.blocks == 0 and first + i == 0:
+                for f in range(_COLUMNS):
+                    run.base[f] = addr[f]
+            elif run.blocks != first + i or any(addr[f] != run.base[f] + run.blocks * step[f]
+                                                for f in range(_COLUMNS)):
+                self.run_open = False
+                return
+            run.blocks += 1
+
     def write(self, first: int, keys, values, fmt: _BlockFormat, stream: int) -> None:
+        self.grow_run(first, keys, values, fmt)
         rows = (nat.BlockPtrs * len(keys))()
         for row, k, v in zip(rows, keys, values):
             row.k_payload, row.k_scales, row.k_padding = k.payload.data_ptr(), k.scales.data_ptr(), k.padding.data_ptr()
@@ -313,7 +350,7 @@ class PackedDecodeState:
         nat.check(nat.lib().iq_decode_attention(
             query.data_ptr(), nat.dtype_code(query.dtype), query.stride(1), hq,
             desc.tables.data_ptr() if n_blocks else None, desc.key_map.data_ptr() if n_blocks else None,
-            desc.value_map.data_ptr() if k4_values else None, n_blocks,
+            desc.value_map.data_ptr() if k4_values else None, desc.run if desc.run.blocks else None, n_blocks,
             256 if fmt is None else fmt.tokens, heads, 0 if fmt is None else fmt.salient, bits,
             64 if fmt is None else fmt.value_group,
             nat.ptr(sk), nat.ptr(sv), *strides(sk), *strides(sv), sink_t,

@@ -40,7 +40,7 @@ def test_invalid_arguments_return_errors_without_a_gpu():
     # the allocation-free decode refuses, on the host and before touching a
     # device, inputs whose partials exceed its static scratch (4 Mi floats)
     assert lib.iq_decode_attention_noalloc(
-        None, 1, 128, 28, None, None, None, 1, 256, 4, 16, 2, 64, None, None, 0, 0, 0, 0, 0,
+        None, 1, 128, 28, None, None, None, None, 1, 256, 4, 16, 2, 64, None, None, 0, 0, 0, 0, 0,
         None, None, 0, 0, 0, 0, 4700 * 256, 0.088, None, 0, None) == -1
     assert b"static scratch" in lib.iq_last_error()
 

@@ -18,7 +18,8 @@ def _call(entry, case, state, out, workspace=None):
     fmt = state._format
     sk, sv, tk, tv = case.sink_k, case.sink_v, case.tail_k, case.tail_v
     args = [q.data_ptr(), nat.dtype_code(q.dtype), q.stride(1), q.shape[1],
-            state._tables.data_ptr() if n else None, state._key_map.data_ptr() if n else None, None, n,
+            state._tables.data_ptr() if n else None, state._key_map.data_ptr() if n else None, None,
+            state._desc.run if n and state._desc.run.blocks else None, n,
             fmt.tokens if n else 256, sk.shape[1], fmt.salient if n else 0, 2, 64,
             sk.data_ptr(), sv.data_ptr(), sk.stride(1), sk.stride(2), sv.stride(1), sv.stride(2), sk.shape[2],
             tk.data_ptr(), tv.data_ptr(), tk.stride(1), tk.stride(2), tv.stride(1), tv.stride(2), tk.shape[2],
