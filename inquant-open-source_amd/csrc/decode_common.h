@@ -68,16 +68,40 @@ __device__ __forceinline__ f32x4 mma16(u32x2 a, u32x2 b, f32x4 c)
 template <bool HI>
 __device__ __forceinline__ f32x2 fp8x2(uint32_t bytes) { return __builtin_amdgcn_cvt_pk_f32_fp8(bytes, HI); }
 
+// Reductions over the four 16-lane rows of a wavefront (lanes l, l ^ 16,
+// l ^ 32, l ^ 48), result in every lane.  v_permlane16_swap with both operands
+// equal to v yields rows (0, 0, 2, 2) and (1, 1, 3, 3); v_permlane32_swap
+// yields the low and the high half.  No LDS traffic and no lane-index math.
 __device__ __forceinline__ float xmax16(float v)
 {
-    v = fmaxf(v, __shfl_xor(v, 16, 64));
-    return fmaxf(v, __shfl_xor(v, 32, 64));
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+    const auto h = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return fmaxf(__uint_as_float(h[0]), __uint_as_float(h[1]));
 }
 
 __device__ __forceinline__ float xsum16(float v)
 {
-    v += __shfl_xor(v, 16, 64);
-    return v + __shfl_xor(v, 32, 64);
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+    const auto h = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(h[0]) + __uint_as_float(h[1]);
+}
+
+// Sum over the 16 lanes of each row, result in every lane of the row
+// (DPP: swap neighbours, swap pairs, mirror the quads, mirror the halves).
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v)
+{
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, false));
+}
+
+__device__ __forceinline__ float row_sum16(float v)
+{
+    v += dpp_f<0xb1>(v);     // quad_perm [1, 0, 3, 2]
+    v += dpp_f<0x4e>(v);     // quad_perm [2, 3, 0, 1]
+    v += dpp_f<0x141>(v);    // row_half_mirror
+    return v + dpp_f<0x140>(v);   // row_mirror
 }
 
 // Loads through global-address-space pointers: the pointer table holds plain

@@ -60,7 +60,7 @@ struct FastArgs {
     const int64_t *tables;
     const int8_t *kmap;
     int64_t nblk, BT, H, S;
-    int vgroup;
+    int vshift;      // log2 of the value group (32, 64 or 128 channels)
     const uint16_t *sk, *sv;
     int64_t sk_sh, sk_st, sv_sh, sv_st, sink_t;
     const uint16_t *tk, *tv;
@@ -86,6 +86,7 @@ struct __attribute__((aligned(16))) FastSmem {
     f32x2 salf[16];              // (s_src, -128 s_src)
     uint16_t qsal[16 * 20];      // Q[g][src_k], zero beyond S
     float dpad[16];              // padding of donor k, rounded to the query dtype
+    float bias[16];              // per query row: sum_k q[g][donor k] * dpad[k]
     float wm[WAVES][16], wl[WAVES][16];
 };
 static_assert(sizeof(FastSmem) <= 40 * 1024, "four workgroups per compute unit");
@@ -110,6 +111,7 @@ __device__ __forceinline__ void fast_body(const FastArgs &a, FastSmem &sm)
     f32x2 *const s_salf = sm.salf;
     uint16_t *const s_qsal = sm.qsal;
     float *const s_dpad = sm.dpad;
+    float *const s_bias = sm.bias;
     float (&s_wm)[WAVES][16] = sm.wm;
     float (&s_wl)[WAVES][16] = sm.wl;
 
@@ -127,7 +129,7 @@ __device__ __forceinline__ void fast_body(const FastArgs &a, FastSmem &sm)
     const int G = a.G;
     const float unit = fp8x2<false>(1u).x;        // fp8 byte 1 == 2^-9 (exact power of two)
     const float inv_unit = 1.0f / unit;
-    const int ngroups = D / a.vgroup;
+    const int ngroups = D >> a.vshift;
 
     // ---------------- geometry (wave-uniform) and every global load up front
     // All loads are unconditional (indices clamped into range) and issued
@@ -156,7 +158,7 @@ __device__ __forceinline__ void fast_body(const FastArgs &a, FastSmem &sm)
             const int t = min(b0 + 16 * j + gl, stop - 1);                                            \
             kw[j] = ldnt_at<u32x4>(kpay, (uint32_t)(t * (D / 2) + 16 * ql));                          \
         }                                                                                             \
-        const int gi = (32 * qq) / a.vgroup;                                                          \
+        const int gi = (32 * qq) >> a.vshift;                                                         \
         _Pragma("unroll") for (int m = 0; m < 2; ++m) {                                               \
             _Pragma("unroll") for (int u = 0; u < 2; ++u) {                                           \
                 const int t = min(b0 + 32 * m + 2 * pl + u, stop - 1);                                \
@@ -266,9 +268,14 @@ __device__ __forceinline__ void fast_body(const FastArgs &a, FastSmem &sm)
                 if (r >= 0) s_salf[k] = f32x2{kscale, -128.0f * kscale};   // exact
             }
         }
-        if (tid < 16 * 16) {
+        {   // thread (query row g, descriptor k): the source's query value, and
+            // the donor term q[g][donor k] * round(pad k) summed over the row's 16 lanes
             const int g = tid >> 4, k = tid & 15;
-            s_qsal[g * 20 + k] = k < S ? s_q[g * QROW + (s_salw[k] & 0xffu)] : (uint16_t)0;
+            const bool live = k < S;
+            const uint32_t sw = live ? s_salw[k] : 0u;
+            s_qsal[g * 20 + k] = live ? s_q[g * QROW + (sw & 0xffu)] : (uint16_t)0;
+            const float t = row_sum16(live ? to_f32<F16>(s_q[g * QROW + (sw >> 8)]) * s_dpad[k] : 0.0f);
+            if (k == 0) s_bias[g] = t;
         }
         if (tid >= S && tid < 16) s_salf[tid] = f32x2{0.0f, 0.0f};
     }
@@ -278,7 +285,7 @@ __device__ __forceinline__ void fast_body(const FastArgs &a, FastSmem &sm)
     u32x4 qb[4];                                   // B operand: Q[g = gl][32 ql + 8 d + e]
 #pragma unroll
     for (int d = 0; d < 4; ++d) qb[d] = *(const u32x4 *)(s_q + gl * QROW + 32 * ql + 8 * d);
-    float bias = 0.0f;                             // sum_k q[gl][don_k] * round(pad_k)
+    const float bias = PACKED ? s_bias[gl] : 0.0f;  // sum_k q[gl][don_k] * round(pad_k)
     // salient operands: the selection matrix rows (source k = gl; byte i of
     // sel_e / sel_o is channel 32 ql + 2 i / 32 ql + 2 i + 1: 16 at the
     // source's channel, 1 at its donor's), the query values of the sources
@@ -288,11 +295,7 @@ __device__ __forceinline__ void fast_body(const FastArgs &a, FastSmem &sm)
     f32x2 sf[4];
     if (PACKED && S > 0) {
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            const int k = 4 * ql + e;
-            if (k < S) bias = fmaf(to_f32<F16>(s_q[gl * QROW + (s_salw[k] >> 8)]), s_dpad[k], bias);
-            sf[e] = s_salf[k];
-        }
+        for (int e = 0; e < 4; ++e) sf[e] = s_salf[4 * ql + e];
         qs = *(const u32x2 *)(s_qsal + gl * 20 + 4 * ql);
         sel_e = *(const i32x4 *)(s_sel + gl * D + 16 * ql);
         sel_o = *(const i32x4 *)(s_sel + gl * D + D / 2 + 16 * ql);
@@ -300,14 +303,11 @@ __device__ __forceinline__ void fast_body(const FastArgs &a, FastSmem &sm)
 #pragma unroll
         for (int e = 0; e < 4; ++e) sf[e] = f32x2{0.0f, 0.0f};
     }
-    bias = xsum16(bias);
     // every lane holds its query operands: wave 0's tile may now be overwritten
     __syncthreads();
 
     float m_run = NEG_INF, l_run = 0.0f;
-    f32x4 acc[8];
-#pragma unroll
-    for (int n = 0; n < 8; ++n) acc[n] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    f32x4 acc[8];                                  // O^T rows 16 n + 4 ql + r, column gl (unscaled)
 
     uint32_t *vt = s_v[wave];
 
@@ -386,27 +386,21 @@ __device__ __forceinline__ void fast_body(const FastArgs &a, FastSmem &sm)
 
         __builtin_amdgcn_s_setprio(2);
         // ---------------- online softmax (log2 domain); lane holds g = gl, tokens 16 j + 4 ql + r
+        // raw logits: the scale is positive, so the maximum commutes with it
+        // and is applied once; p = 2^(s c - m) with one fma per logit
         float cmax = NEG_INF;
-        if (full) {
+        if (!full) {
 #pragma unroll
             for (int j = 0; j < 4; ++j)
 #pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    sc[j][r] *= a.c_log2;
-                    cmax = fmaxf(cmax, sc[j][r]);
-                }
-        } else {
-#pragma unroll
-            for (int j = 0; j < 4; ++j)
-#pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    const float v = base + 16 * j + 4 * ql + r < stop ? sc[j][r] * a.c_log2 : NEG_INF;
-                    sc[j][r] = v;
-                    cmax = fmaxf(cmax, v);
-                }
+                for (int r = 0; r < 4; ++r)
+                    if (base + 16 * j + 4 * ql + r >= stop) sc[j][r] = NEG_INF;
         }
-        cmax = xmax16(cmax);
-        const float m_new = cmax;                  // one pass per wavefront: nothing to rescale
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) cmax = fmaxf(cmax, sc[j][r]);
+        const float m_new = xmax16(cmax) * a.c_log2;   // one pass per wavefront: nothing to rescale
         float lsum = 0.0f;
         u32x4 phi[2], plo[2];
 #pragma unroll
@@ -414,7 +408,7 @@ __device__ __forceinline__ void fast_body(const FastArgs &a, FastSmem &sm)
             float pr[4];
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                pr[r] = __builtin_amdgcn_exp2f(sc[j][r] - m_new);
+                pr[r] = __builtin_amdgcn_exp2f(fmaf(sc[j][r], a.c_log2, -m_new));
                 lsum += pr[r];
             }
             const uint32_t h01 = pack2<F16>(pr[0], pr[1]), h23 = pack2<F16>(pr[2], pr[3]);
@@ -523,37 +517,46 @@ __device__ __forceinline__ void fast_body(const FastArgs &a, FastSmem &sm)
                     const int pp = e < 2 ? 2 * ql + e : 8 + 2 * ql + (e - 2);
                     va[e] = vt[pp * VR + 16 * n + gl];
                 }
-                acc[n] = mma32<F16>(va, phi[m], acc[n]);
+                acc[n] = mma32<F16>(va, phi[m], m == 0 ? f32x4{0.0f, 0.0f, 0.0f, 0.0f} : acc[n]);
                 acc[n] = mma32<F16>(va, plo[m], acc[n]);
             }
         }
+    } else {
+#pragma unroll
+        for (int n = 0; n < 8; ++n) acc[n] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
     }
 #undef IQ_LOAD_CHUNK
 
     __builtin_amdgcn_s_setprio(1);
     // ---------------- combine the four wavefronts, write this partition's partial
-    // Each wavefront rescales its O to the workgroup's running max in
-    // registers and stages it as O[g][c] rows; readers then only add.
+    // Each wavefront stages its unnormalized O as O[g][c] rows next to its
+    // (m, l); a reader weights the four rows by 2^(m_w - max m) and adds.
     l_run = xsum16(l_run);
-    if (ql == 0) s_wm[wave][gl] = m_run;
-    __syncthreads();
-    float mx = s_wm[0][gl];
-#pragma unroll
-    for (int w = 1; w < WAVES; ++w) mx = fmaxf(mx, s_wm[w][gl]);
-    const float wt = m_run == NEG_INF ? 0.0f : __builtin_amdgcn_exp2f(m_run - mx);
-    if (ql == 0) s_wl[wave][gl] = l_run * wt;
+    if (ql == 0) {
+        s_wm[wave][gl] = m_run;
+        s_wl[wave][gl] = l_run;
+    }
     float *ot = (float *)vt;
 #pragma unroll
-    for (int n = 0; n < 8; ++n) *(f32x4 *)(ot + gl * OROW + 16 * n + 4 * ql) = acc[n] * wt;
+    for (int n = 0; n < 8; ++n) *(f32x4 *)(ot + gl * OROW + 16 * n + 4 * ql) = acc[n];
     __syncthreads();
     for (int i = tid; i < G * (D / 4); i += 256) {
         const int g = i >> 5, c = (i & 31) * 4;
-        f32x4 num = *(const f32x4 *)((const float *)s_v[0] + g * OROW + c);
-        float den = s_wl[0][g];
+        float mw[WAVES], mx = NEG_INF;
 #pragma unroll
-        for (int w = 1; w < WAVES; ++w) {
-            num += *(const f32x4 *)((const float *)s_v[w] + g * OROW + c);
-            den += s_wl[w][g];
+        for (int w = 0; w < WAVES; ++w) {
+            mw[w] = s_wm[w][g];
+            mx = fmaxf(mx, mw[w]);
+        }
+        f32x4 num = {0.0f, 0.0f, 0.0f, 0.0f};
+        float den = 0.0f;
+#pragma unroll
+        for (int w = 0; w < WAVES; ++w) {
+            const float wt = mw[w] == NEG_INF ? 0.0f : __builtin_amdgcn_exp2f(mw[w] - mx);
+            const f32x4 o = *(const f32x4 *)((const float *)s_v[w] + g * OROW + c);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) num[e] = fmaf(o[e], wt, num[e]);
+            den = fmaf(s_wl[w][g], wt, den);
         }
         if (a.P == 1) {
 #pragma unroll
@@ -564,10 +567,7 @@ __device__ __forceinline__ void fast_body(const FastArgs &a, FastSmem &sm)
         *(f32x2 *)(out + c) = f32x2{num[0], num[1]};
         *(f32x2 *)(out + c + 2) = f32x2{num[2], num[3]};
         if (c == 0) {
-            float m = s_wm[0][g];
-#pragma unroll
-            for (int w = 1; w < WAVES; ++w) m = fmaxf(m, s_wm[w][g]);
-            out[D] = m * LN2;
+            out[D] = mx * LN2;
             out[D + 1] = den;
         }
     }
@@ -600,6 +600,7 @@ int iq_decode_fast_launch(const void *q, int q_dtype, int64_t q_stride_h, int64_
     if (q_dtype != IQ_BF16 && q_dtype != IQ_F16) return IQ_ERR_UNSUPPORTED;
     if (out_dtype != IQ_F32 && out_dtype != IQ_BF16 && out_dtype != IQ_F16) return IQ_ERR_UNSUPPORTED;
     if (n_blocks > 0 && value_bits != 2 && value_bits != 4) return IQ_ERR_UNSUPPORTED;
+    if (n_blocks > 0 && value_group != 32 && value_group != 64 && value_group != 128) return IQ_ERR_UNSUPPORTED;
     if (Hq / H > 16 || S > 16) return IQ_ERR_UNSUPPORTED;
     if (n_blocks > 0 && block_tokens > CHUNK * WAVES) return IQ_ERR_UNSUPPORTED;   // one pass per workgroup
     // query, dense rows and packed rows are read as 16-byte vectors
@@ -614,7 +615,7 @@ int iq_decode_fast_launch(const void *q, int q_dtype, int64_t q_stride_h, int64_
     const int64_t P = n_blocks + (sink_t + tail_t + DENSE_SPLIT - 1) / DENSE_SPLIT;
     if (P < 1 || P > 65535) return IQ_ERR_UNSUPPORTED;
     FastArgs a{{}, 0, (const uint16_t *)q, q_stride_h, (int)(Hq / H), tables, key_map, n_blocks, block_tokens, H, S,
-               value_group ? value_group : 64, (const uint16_t *)sink_k, (const uint16_t *)sink_v, sink_k_sh,
+               value_group == 32 ? 5 : value_group == 128 ? 7 : 6, (const uint16_t *)sink_k, (const uint16_t *)sink_v, sink_k_sh,
                sink_k_st, sink_v_sh, sink_v_st, sink_t, (const uint16_t *)tail_k, (const uint16_t *)tail_v,
                tail_k_sh, tail_k_st, tail_v_sh, tail_v_st, tail_t, scale * 1.44269504088896341f, workspace, P,
                out, out_dtype};
