@@ -277,19 +277,22 @@ __global__ __launch_bounds__(RED_THREADS) void decode_reduce(const float *ws, in
         }
         m = mm;
     }
-    // lanes with equal tid % 4 of a wavefront hold 16 partition lanes of one column
-    float mw = m;
-#pragma unroll
-    for (int sh = RED_C4; sh < 64; sh <<= 1) mw = fmaxf(mw, __shfl_xor(mw, sh, 64));
+    // lanes with equal tid % 4 of a wavefront hold 16 partition lanes of one
+    // column: rotate by 4 and 8 within each 16-lane row (DPP), then across rows
+    static_assert(RED_C4 == 4, "the DPP rotations assume four columns");
+    float mw = fmaxf(m, dpp_f<0x124>(m));          // row_ror:4
+    mw = fmaxf(mw, dpp_f<0x128>(mw));              // row_ror:8
+    mw = xmax16(mw);
     const float wt = m == ninf ? 0.0f : __expf(m - mw);
     num *= wt;
     den *= wt;
 #pragma unroll
-    for (int sh = RED_C4; sh < 64; sh <<= 1) {
-#pragma unroll
-        for (int e = 0; e < 4; ++e) num[e] += __shfl_xor(num[e], sh, 64);
-        den += __shfl_xor(den, sh, 64);
+    for (int e = 0; e < 4; ++e) {
+        num[e] += dpp_f<0x124>(num[e]);
+        num[e] = xsum16(num[e] + dpp_f<0x128>(num[e]));
     }
+    den += dpp_f<0x124>(den);
+    den = xsum16(den + dpp_f<0x128>(den));
     if ((tid & 63) < RED_C4) {
         s_m[wave][c4] = mw;
         s_l[wave][c4] = den;

@@ -39,7 +39,8 @@ namespace {
 constexpr int D = 128;
 constexpr int WAVES = 4;
 constexpr int CHUNK = 64;              // tokens per wavefront per pass
-constexpr int VR = 136;                // dwords per staged token-pair row of decoded V (128 + 8: two passes per read)
+constexpr int VR = 136;                // dwords per staged token-pair row of decoded V (128 + 8)
+constexpr int SELROW = D + 16;         // bytes per selection-matrix row (+16: the 16 rows of a read hit distinct banks)
 constexpr int OROW = 132;              // floats per staged output row in the combine (128 + 4: conflict-free 16-byte stores)
 constexpr int KC_STRIDE = 68;          // float2 slots per 32-channel group of K constants (+4: no bank overlap)
 constexpr int DENSE_SPLIT = 256;
@@ -91,7 +92,8 @@ struct __attribute__((aligned(16))) FastSmem {
 };
 static_assert(sizeof(FastSmem) <= 40 * 1024, "four workgroups per compute unit");
 static_assert(16 * QROW / 2 <= 16 * VR, "the query rows fit in one wave's tile");
-static_assert(16 * D <= 16 * VR * 4, "the salient selection matrix fits in one wave's tile");
+static_assert(16 * SELROW <= 16 * VR * 4, "the salient selection matrix fits in one wave's tile");
+
 
 // One partition.  PACKED and dense partitions are separate instantiations so
 // that neither has a branch between its loads and their first use: a branch
@@ -121,14 +123,16 @@ __device__ __forceinline__ void fast_body(const FastArgs &a, FastSmem &sm)
     // oldest finishing first and leaving the last one alone to run latency-bound.
     __builtin_amdgcn_s_setprio(3);
     const int gl = lane & 15, ql = lane >> 4;     // MFMA column (query row / channel) and k-slot group
-    // V writer: token pair and 32-channel quarter; the 8 lanes of one LDS cycle
-    // take 8 different token pairs, so their 16-byte stores hit distinct banks
+    // V writer: token pair pl and 32-channel quarter qq.  (A bank-spreading
+    // remap of these lanes with shifted quarters removed the store conflicts
+    // but measured slower end to end, so rows stay plain.)
     const int pl = lane & 15, qq = lane >> 4;
     const int h = blockIdx.x;
     const int64_t p = blockIdx.y;
     const int G = a.G;
-    const float unit = fp8x2<false>(1u).x;        // fp8 byte 1 == 2^-9 (exact power of two)
-    const float inv_unit = 1.0f / unit;
+    // the fp8 converter maps byte n < 16 to n * 2^-9 exactly (e4m3 subnormals
+    // and the first binade), so scales are pre-multiplied by 2^9
+    constexpr float inv_unit = 512.0f;
     const int ngroups = D >> a.vshift;
 
     // ---------------- geometry (wave-uniform) and every global load up front
@@ -239,7 +243,7 @@ __device__ __forceinline__ void fast_body(const FastArgs &a, FastSmem &sm)
     // even channels of a row first (channel c at byte (c & 1) * 64 + c / 2),
     // staged in wave 1's V tile, which is free until the operands are loaded
     uint8_t *const s_sel = (uint8_t *)&sm.v[1][0];
-    if (packed) *(u32x2 *)(s_sel + 8 * tid) = u32x2{0u, 0u};
+    if (packed && tid < 16 * SELROW / 16) *(u32x4 *)(s_sel + 16 * tid) = u32x4{0u, 0u, 0u, 0u};
     if (packed) {
         if (tid < D) {
             // salient and donor channels decode to zero in the 4-bit pass:
@@ -264,7 +268,7 @@ __device__ __forceinline__ void fast_body(const FastArgs &a, FastSmem &sm)
             const int r = (int)(int8_t)krole;
             const int k = r >= 0 ? -2 - (int)s_role[r] : -2 - r;
             if (k >= 0 && k < S) {
-                s_sel[k * D + (tid & 1) * (D / 2) + (tid >> 1)] = r >= 0 ? 16 : 1;
+                s_sel[k * SELROW + (tid & 1) * (D / 2) + (tid >> 1)] = r >= 0 ? 16 : 1;
                 if (r >= 0) s_salf[k] = f32x2{kscale, -128.0f * kscale};   // exact
             }
         }
@@ -297,8 +301,8 @@ __device__ __forceinline__ void fast_body(const FastArgs &a, FastSmem &sm)
 #pragma unroll
         for (int e = 0; e < 4; ++e) sf[e] = s_salf[4 * ql + e];
         qs = *(const u32x2 *)(s_qsal + gl * 20 + 4 * ql);
-        sel_e = *(const i32x4 *)(s_sel + gl * D + 16 * ql);
-        sel_o = *(const i32x4 *)(s_sel + gl * D + D / 2 + 16 * ql);
+        sel_e = *(const i32x4 *)(s_sel + gl * SELROW + 16 * ql);
+        sel_o = *(const i32x4 *)(s_sel + gl * SELROW + D / 2 + 16 * ql);
     } else {
 #pragma unroll
         for (int e = 0; e < 4; ++e) sf[e] = f32x2{0.0f, 0.0f};
@@ -317,47 +321,70 @@ __device__ __forceinline__ void fast_body(const FastArgs &a, FastSmem &sm)
         // ---------------- logits S^T[token, g] for four 16-token tiles
         f32x4 sc[4];
         if (packed) {
-            // tile outer: tile j is decoded and multiplied as soon as its payload
-            // has landed; each lane's 8 constants of group d are re-read from
-            // LDS per tile (four distinct addresses per read: broadcasts).
-            // Within a tile the sum over d keeps its order.
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                f32x4 s = {bias, bias, bias, bias};
-                i32x4 lo4, hi4;                      // raw nibbles of the tile: even / odd channels
+            // Per 16-token tile j and 32-channel group d: kv = K rows of the tile,
+            // channels 32 ql + 8 d .. + 7, rounded to the query dtype.
+            auto k_operand = [&](uint32_t x, const f32x2 *kc) {
+                const u32x4 c01 = *(const u32x4 *)(kc + 0), c23 = *(const u32x4 *)(kc + 2);
+                const u32x4 c45 = *(const u32x4 *)(kc + 4), c67 = *(const u32x4 *)(kc + 6);
+                const uint32_t lo = x & 0x0f0f0f0fu, hi = (x >> 4) & 0x0f0f0f0fu;
+                const f32x2 e01 = fp8x2<false>(lo), e23 = fp8x2<true>(lo);
+                const f32x2 o01 = fp8x2<false>(hi), o23 = fp8x2<true>(hi);
+#define KF(cv, i) __uint_as_float(cv[i])
+                u32x4 kv;
+                kv[0] = pack2<F16>(fmaf(e01.x, KF(c01, 0), KF(c01, 1)), fmaf(o01.x, KF(c01, 2), KF(c01, 3)));
+                kv[1] = pack2<F16>(fmaf(e01.y, KF(c23, 0), KF(c23, 1)), fmaf(o01.y, KF(c23, 2), KF(c23, 3)));
+                kv[2] = pack2<F16>(fmaf(e23.x, KF(c45, 0), KF(c45, 1)), fmaf(o23.x, KF(c45, 2), KF(c45, 3)));
+                kv[3] = pack2<F16>(fmaf(e23.y, KF(c67, 0), KF(c67, 1)), fmaf(o23.y, KF(c67, 2), KF(c67, 3)));
+#undef KF
+                return kv;
+            };
+            // salient terms of tile j: codes 16 hi + lo of sources 4 ql .. 4 ql + 3
+            // for token 16 j + gl from the raw nibbles (even / odd channels)
+            auto salient = [&](int j, f32x4 acc_j) {
+                i32x4 lo4, hi4;
 #pragma unroll
                 for (int d = 0; d < 4; ++d) {
-                    // keeps the constant reads inside the tile: hoisted out of the
-                    // tile loop, all 64 constants would stay live and spill
+                    lo4[d] = (int)(kw[j][d] & 0x0f0f0f0fu);
+                    hi4[d] = (int)((kw[j][d] >> 4) & 0x0f0f0f0fu);
+                }
+                i32x4 code = __builtin_amdgcn_mfma_i32_16x16x64_i8(sel_e, lo4, i32x4{0, 0, 0, 0}, 0, 0, 0);
+                code = __builtin_amdgcn_mfma_i32_16x16x64_i8(sel_o, hi4, code, 0, 0, 0);
+                float v[4];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) v[e] = fmaf((float)code[e], sf[e].x, sf[e].y);
+                return mma16<F16>(u32x2{pack2<F16>(v[0], v[1]), pack2<F16>(v[2], v[3])}, qs, acc_j);
+            };
+            // Per tile the sum keeps one order: bias, groups 0..3, salient terms.
+#pragma unroll
+            for (int j = 0; j < 4; ++j) sc[j] = f32x4{bias, bias, bias, bias};
+            if constexpr (VBITS == 2) {
+                // group outer: the 8 constants of group d (four distinct LDS
+                // addresses per read: broadcasts) are read once and serve the
+                // four tiles, whose accumulations are independent matrix-core chains
+#pragma unroll
+                for (int d = 0; d < 4; ++d) {
+                    // keeps this group's constant reads here: hoisted, all 64 would stay live
                     asm volatile("" ::: "memory");
-                    const f32x2 *kc = s_kc + ql * KC_STRIDE + 8 * d;
-                    const u32x4 c01 = *(const u32x4 *)(kc + 0), c23 = *(const u32x4 *)(kc + 2);
-                    const u32x4 c45 = *(const u32x4 *)(kc + 4), c67 = *(const u32x4 *)(kc + 6);
-                    const uint32_t x = kw[j][d];
-                    const uint32_t lo = x & 0x0f0f0f0fu, hi = (x >> 4) & 0x0f0f0f0fu;
-                    lo4[d] = (int)lo;
-                    hi4[d] = (int)hi;
-                    const f32x2 e01 = fp8x2<false>(lo), e23 = fp8x2<true>(lo);
-                    const f32x2 o01 = fp8x2<false>(hi), o23 = fp8x2<true>(hi);
-#define KF(cv, i) __uint_as_float(cv[i])
-                    u32x4 kv;
-                    kv[0] = pack2<F16>(fmaf(e01.x, KF(c01, 0), KF(c01, 1)), fmaf(o01.x, KF(c01, 2), KF(c01, 3)));
-                    kv[1] = pack2<F16>(fmaf(e01.y, KF(c23, 0), KF(c23, 1)), fmaf(o01.y, KF(c23, 2), KF(c23, 3)));
-                    kv[2] = pack2<F16>(fmaf(e23.x, KF(c45, 0), KF(c45, 1)), fmaf(o23.x, KF(c45, 2), KF(c45, 3)));
-                    kv[3] = pack2<F16>(fmaf(e23.y, KF(c67, 0), KF(c67, 1)), fmaf(o23.y, KF(c67, 2), KF(c67, 3)));
-#undef KF
-                    s = mma32<F16>(kv, qb[d], s);
+#pragma unroll
+                    for (int j = 0; j < 4; ++j)
+                        sc[j] = mma32<F16>(k_operand(kw[j][d], s_kc + ql * KC_STRIDE + 8 * d), qb[d], sc[j]);
                 }
                 if (S > 0) {
-                    // codes 16 hi + lo of sources 4 ql .. 4 ql + 3 for token 16 j + gl
-                    i32x4 code = __builtin_amdgcn_mfma_i32_16x16x64_i8(sel_e, lo4, i32x4{0, 0, 0, 0}, 0, 0, 0);
-                    code = __builtin_amdgcn_mfma_i32_16x16x64_i8(sel_o, hi4, code, 0, 0, 0);
-                    float v[4];
 #pragma unroll
-                    for (int e = 0; e < 4; ++e) v[e] = fmaf((float)code[e], sf[e].x, sf[e].y);
-                    s = mma16<F16>(u32x2{pack2<F16>(v[0], v[1]), pack2<F16>(v[2], v[3])}, qs, s);
+                    for (int j = 0; j < 4; ++j) sc[j] = salient(j, sc[j]);
                 }
-                sc[j] = s;
+            } else {
+                // 4-bit values hold twice the V payload in registers: tile outer
+                // keeps one tile's constants live at a time (re-read per tile)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+#pragma unroll
+                    for (int d = 0; d < 4; ++d) {
+                        asm volatile("" ::: "memory");
+                        sc[j] = mma32<F16>(k_operand(kw[j][d], s_kc + ql * KC_STRIDE + 8 * d), qb[d], sc[j]);
+                    }
+                    if (S > 0) sc[j] = salient(j, sc[j]);
+                }
             }
         } else {
             // dense sink / tail: K rows of the query dtype are the A operand
