@@ -46,6 +46,7 @@ def parse():
     ap.add_argument("--no-paged", action="store_true", help="skip the batched paged decode (config 4)")
     ap.add_argument("--no-cfg3", action="store_true", help="skip the Mistral-7B decode (config 3)")
     ap.add_argument("--no-encode", action="store_true", help="skip the config 3 encode")
+    ap.add_argument("--no-k4-values", action="store_true", help="skip the config 2 decode with K4-coded values")
     ap.add_argument("--no-append", action="store_true", help="skip the config 2 append measurements")
     ap.add_argument("--copy-probe", action="store_true",
                     help="only run a 1 GiB device-to-device copy (calibrates rocprofv3 FETCH_SIZE / WRITE_SIZE)")
@@ -95,7 +96,8 @@ def kv_tensor(gen, heads, tokens, device, frac_groups=(2, 2, 1), scale=20.0):
     return x.to(torch.bfloat16)
 
 
-def build_layer(seed, device, H=4, G=7, n_blocks=128, block=256, sink=4, tail=128, frac_groups=(2, 2, 1)):
+def build_layer(seed, device, H=4, G=7, n_blocks=128, block=256, sink=4, tail=128, frac_groups=(2, 2, 1),
+                k4_values=False):
     import torch
     from inquant.cache import _quantize_temporal_blocks
     from inquant.codec import CodecConfig
@@ -106,7 +108,8 @@ def build_layer(seed, device, H=4, G=7, n_blocks=128, block=256, sink=4, tail=12
     v = kv_tensor(gen, H, n_blocks * block, device, frac_groups=frac_groups)
     cfg = CodecConfig(donor_policy="min_error")
     kb = _quantize_temporal_blocks(k, n_blocks, block, cfg)
-    vb = quantize_value_blocks(v, n_blocks, block, 2, 64)
+    # K4-coded values (CacheConfig's default value_bits=None) or V2 with 64-channel groups
+    vb = _quantize_temporal_blocks(v, n_blocks, block, cfg) if k4_values else quantize_value_blocks(v, n_blocks, block, 2, 64)
     del k, v
     layer = {
         "q": torch.randn((1, H * G, 1, 128), generator=gen, device=device).to(torch.bfloat16),
@@ -122,10 +125,14 @@ def algorithmic_bytes(layer) -> int:
     H = layer["kb"][0].shape[1]
     n = len(layer["kb"])
     b = 0
+    k4_values = not hasattr(layer["vb"][0], "offsets")
     for k, v in zip(layer["kb"], layer["vb"]):
         b += k.payload.numel() + k.scales.numel() * 4 + k.padding.numel() * 4
-        b += v.payload.numel() + (v.scales.numel() + v.offsets.numel()) * 2
-    b += n * H * 128          # int8 role map read per (block, head)
+        if k4_values:
+            b += v.payload.numel() + v.scales.numel() * 4 + v.padding.numel() * 4
+        else:
+            b += v.payload.numel() + (v.scales.numel() + v.offsets.numel()) * 2
+    b += n * H * 128 * (2 if k4_values else 1)   # int8 role maps read per (block, head)
     b += n * 6 * 8            # pointer table
     for name in ("sink_k", "sink_v", "tail_k", "tail_v"):
         b += layer[name].numel() * 2
@@ -172,6 +179,23 @@ def time_decode(layers, steps, warmup, use_graph):
     torch.cuda.synchronize()
     ms = start.elapsed_time(stop) / steps
     return ms, outs
+
+
+def time_decode_k4_values(device, layers=28, steps=20, warmup=3):
+    """Config 2 shape with K4-coded values (the reference CacheConfig default,
+    value_bits=None): 28 layers of 32768 packed tokens + 4 sink + 128 tail."""
+    import torch
+    lay = [build_layer(5000 + i, device, k4_values=True) for i in range(layers)]
+    torch.cuda.synchronize()
+    per_layer = algorithmic_bytes(lay[0])
+    ms, _ = time_decode(lay, steps, warmup, True)
+    us = ms * 1e3 / layers
+    out = {"layers": layers, "us_per_layer": round(us, 3), "bytes_per_layer": per_layer,
+           "gbs": round(per_layer / (us * 1e-6) / 1e9, 2),
+           "hbm_frac": round(per_layer / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
+    del lay
+    torch.cuda.empty_cache()
+    return out
 
 
 def time_decode_cfg3(device, layers=32, steps=20, warmup=3):
@@ -561,6 +585,7 @@ def main():
             "append_us_per_token"]
         append["step"] = time_append_step(device)
     cfg3 = None if args.no_cfg3 else time_decode_cfg3(device)
+    k4v = None if args.no_k4_values else time_decode_k4_values(device)
     result = {
         "metric": METRIC,
         "value": round(gbs, 2),
@@ -593,6 +618,8 @@ def main():
         result["append_cfg2"] = append
     if cfg3 is not None:
         result["decode_cfg3"] = cfg3
+    if k4v is not None:
+        result["decode_cfg2_k4_values"] = k4v
     if paged is not None:
         result["paged_cfg4"] = paged
     if not args.no_cpu_baseline:

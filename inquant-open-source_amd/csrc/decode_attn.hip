@@ -319,7 +319,8 @@ __global__ __launch_bounds__(RED_THREADS) void decode_reduce(const float *ws, in
 }  // namespace
 
 int iq_decode_fast_launch(const void *q, int q_dtype, int64_t q_stride_h, int64_t Hq, const int64_t *tables,
-                          const int8_t *key_map, int64_t n_blocks, int64_t block_tokens, int64_t H, int64_t S,
+                          const int8_t *key_map, const int8_t *value_map, int64_t n_blocks, int64_t block_tokens,
+                          int64_t H, int64_t S,
                           int value_bits, int value_group, const void *sink_k, const void *sink_v, int64_t sink_k_sh,
                           int64_t sink_k_st, int64_t sink_v_sh, int64_t sink_v_st, int64_t sink_t,
                           const void *tail_k, const void *tail_v, int64_t tail_k_sh, int64_t tail_k_st,
@@ -370,10 +371,11 @@ extern "C" int iq_decode_attention(const void *q, int q_dtype, int64_t q_stride_
     IQ_CHECK_ARG(P >= 1, "iq_decode_attention: attention requires at least one key/value token");
     IQ_CHECK_ARG(P <= 65535, "iq_decode_attention: too many partitions");
     IQ_CHECK_ARG(workspace_floats >= Hq * P * (D + 2), "iq_decode_attention: workspace too small");
-    // Matrix-core path for bf16/f16 queries with V2/V4 values; the general
-    // kernel covers fp32 queries and K4-coded values.
+    // Matrix-core path for bf16/f16 queries (at most 16 salient channels, 16
+    // query heads per KV head); the general kernel covers the rest.
     int64_t parts = P;
-    const int fast = iq_decode_fast_launch(q, q_dtype, q_stride_h, Hq, tables, key_map, n_blocks, block_tokens, H,
+    const int fast = iq_decode_fast_launch(q, q_dtype, q_stride_h, Hq, tables, key_map, value_map, n_blocks,
+                                           block_tokens, H,
                                            S, value_bits, value_group, sink_k, sink_v, sink_k_sh, sink_k_st,
                                            sink_v_sh, sink_v_st, sink_t, tail_k, tail_v, tail_k_sh, tail_k_st,
                                            tail_v_sh, tail_v_st, tail_t, scale, workspace, out, out_dtype, run,

@@ -30,8 +30,15 @@
 //     lane holds its operands), so four workgroups share a compute unit.
 //   * Online softmax in the log2 domain; P = hi + lo (two bf16/f16 terms) so
 //     the P.V product keeps ~16 significant bits of the weights.
-//   * V half-rows decode with the same fp8 trick into a 32-row LDS tile that
-//     is read back transposed as the A operand of O^T = V^T P^T.
+//   * Values decode with the same fp8 trick into a 16-row LDS tile per half
+//     chunk (row q pairs tokens q and q + 16, rows 132 dwords apart: 16-byte
+//     stores and 32-lane reads are free of bank conflicts), read back
+//     transposed as the A operand of O^T = V^T P^T.  Group-wise values
+//     (V2/V4) take a per-token scale and offset; K4-coded values (the codec
+//     of the keys) take per-channel constants, their salient channels come
+//     from the int8 selection product with the payload as A operand (which
+//     leaves the codes in the k-slot layout of P^T, no LDS), and a donor
+//     channel's column is round(pad) * sum(p).
 #include "decode_common.h"
 
 namespace {
@@ -39,7 +46,7 @@ namespace {
 constexpr int D = 128;
 constexpr int WAVES = 4;
 constexpr int CHUNK = 64;              // tokens per wavefront per pass
-constexpr int VR = 136;                // dwords per staged token-pair row of decoded V (128 + 8)
+constexpr int VR = 132;                // dwords per staged token-pair row of decoded V (128 + 4: rows 4 banks apart)
 constexpr int SELROW = D + 16;         // bytes per selection-matrix row (+16: the 16 rows of a read hit distinct banks)
 constexpr int OROW = 132;              // floats per staged output row in the combine (128 + 4: conflict-free 16-byte stores)
 constexpr int KC_STRIDE = 68;          // float2 slots per 32-channel group of K constants (+4: no bank overlap)
@@ -59,7 +66,7 @@ struct FastArgs {
     int64_t q_sh;
     int G;
     const int64_t *tables;
-    const int8_t *kmap;
+    const int8_t *kmap, *vmap;   // role maps of keys and (K4-coded) values
     int64_t nblk, BT, H, S;
     int vshift;      // log2 of the value group (32, 64 or 128 channels)
     const uint16_t *sk, *sv;
@@ -77,9 +84,11 @@ struct FastArgs {
 // At most 40 KiB, so that four workgroups share a compute unit.
 struct __attribute__((aligned(16))) FastSmem {
     // per wavefront: staged decoded V as [token pair][channel] dwords (two
-    // tokens of one channel per dword); also K staging and the final combine.
-    // Until every lane holds its query operands, wave 0's tile holds the
-    // query rows (dtype bits, QROW halves per row, zero beyond G).
+    // tokens of one channel per dword: pair row q of half chunk m holds
+    // tokens 32 m + q and 32 m + 16 + q); also the final combine.  Until
+    // every lane holds its operands, wave 0's tile holds the query rows
+    // (dtype bits, QROW halves per row, zero beyond G) and waves 1 and 2's
+    // tiles the selection matrices of the key and the value salient codes.
     uint32_t v[WAVES][16 * VR];
     f32x2 kc[4 * KC_STRIDE];     // per channel (s * 2^9, -8 s); (0, 0) at salient and donor channels
     int8_t role[D];
@@ -88,20 +97,33 @@ struct __attribute__((aligned(16))) FastSmem {
     uint16_t qsal[16 * 20];      // Q[g][src_k], zero beyond S
     float dpad[16];              // padding of donor k, rounded to the query dtype
     float bias[16];              // per query row: sum_k q[g][donor k] * dpad[k]
+    // K4-coded values: per-channel constants as for keys, the value role map,
+    // and per descriptor k the source's (s, -128 s), the donor's rounded
+    // padding and both channels
+    f32x2 vc[4 * KC_STRIDE];
+    int8_t vrole[D];
+    f32x2 vsalf[16];
+    float vdpad[16];
+    int vsrc[16], vdon[16];
     float wm[WAVES][16], wl[WAVES][16];
 };
 static_assert(sizeof(FastSmem) <= 40 * 1024, "four workgroups per compute unit");
 static_assert(16 * QROW / 2 <= 16 * VR, "the query rows fit in one wave's tile");
 static_assert(16 * SELROW <= 16 * VR * 4, "the salient selection matrix fits in one wave's tile");
+static_assert(16 * OROW <= 16 * VR, "the combine's output rows fit in one wave's tile");
 
 
 // One partition.  PACKED and dense partitions are separate instantiations so
 // that neither has a branch between its loads and their first use: a branch
 // join there makes the compiler wait for every load in flight.
+//
+// VBITS 2 or 4: group-wise values (value_codec.py); VBITS 0: K4-coded values
+// (codec.py), decoded like the keys (triton_attention.py:33-51).
 template <bool F16, int VBITS, bool PACKED>
 __device__ __forceinline__ void fast_body(const FastArgs &a, FastSmem &sm)
 {
-    constexpr int VROW = D * VBITS / 8;          // V payload bytes per token
+    constexpr bool K4V = VBITS == 0;
+    constexpr int VROW = K4V ? D / 2 : D * VBITS / 8;   // V payload bytes per token
     constexpr int VQ = VROW / 4;                 // bytes per 32-channel quarter row
     constexpr int VQW = VQ / 4;                  // dwords per quarter row
 
@@ -114,6 +136,7 @@ __device__ __forceinline__ void fast_body(const FastArgs &a, FastSmem &sm)
     uint16_t *const s_qsal = sm.qsal;
     float *const s_dpad = sm.dpad;
     float *const s_bias = sm.bias;
+    f32x2 *const s_vc = sm.vc;
     float (&s_wm)[WAVES][16] = sm.wm;
     float (&s_wl)[WAVES][16] = sm.wl;
 
@@ -123,9 +146,8 @@ __device__ __forceinline__ void fast_body(const FastArgs &a, FastSmem &sm)
     // oldest finishing first and leaving the last one alone to run latency-bound.
     __builtin_amdgcn_s_setprio(3);
     const int gl = lane & 15, ql = lane >> 4;     // MFMA column (query row / channel) and k-slot group
-    // V writer: token pair pl and 32-channel quarter qq.  (A bank-spreading
-    // remap of these lanes with shifted quarters removed the store conflicts
-    // but measured slower end to end, so rows stay plain.)
+    // V writer of group-wise values and dense rows: pair row pl (tokens
+    // 32 m + pl and 32 m + 16 + pl) and 32-channel quarter qq
     const int pl = lane & 15, qq = lane >> 4;
     const int h = blockIdx.x;
     const int64_t p = blockIdx.y;
@@ -149,10 +171,11 @@ __device__ __forceinline__ void fast_body(const FastArgs &a, FastSmem &sm)
     const int S = packed ? (int)a.S : 0;         // at most 16 (one group of salient channels)
     const int qg = tid >> 4, qc = (tid & 15) * 8;  // this thread's 8 query elements
     const u32x4 qraw = ld16(a.q + (int64_t)(h * G + (qg < G ? qg : G - 1)) * a.q_sh + qc);
-    float kscale = 0.0f, kpad = 0.0f;
-    uint32_t krole = 0u, ksrc = 0u, kdon = 0u;
+    float kscale = 0.0f, kpad = 0.0f, vscale = 0.0f, vpad = 0.0f;
+    uint32_t krole = 0u, ksrc = 0u, kdon = 0u, vrole = 0u;
     int base = 0;
     u32x4 kw[4];
+    u32x4 vk[4];                                   // K4-coded values: laid out as kw
     uint32_t vw[2][2][VQW];                        // [half chunk][token of the pair][dword]
     uint32_t vp[2][2][2];                          // [half chunk][token of the pair][scale, offset] (f16 bits)
 #define IQ_LOAD_CHUNK(b_)                                                                             \
@@ -161,11 +184,12 @@ __device__ __forceinline__ void fast_body(const FastArgs &a, FastSmem &sm)
         _Pragma("unroll") for (int j = 0; j < 4; ++j) {                                               \
             const int t = min(b0 + 16 * j + gl, stop - 1);                                            \
             kw[j] = ldnt_at<u32x4>(kpay, (uint32_t)(t * (D / 2) + 16 * ql));                          \
+            if constexpr (K4V) vk[j] = ldnt_at<u32x4>(vpay, (uint32_t)(t * (D / 2) + 16 * ql));       \
         }                                                                                             \
         const int gi = (32 * qq) >> a.vshift;                                                         \
-        _Pragma("unroll") for (int m = 0; m < 2; ++m) {                                               \
+        _Pragma("unroll") for (int m = 0; m < (K4V ? 0 : 2); ++m) {                                   \
             _Pragma("unroll") for (int u = 0; u < 2; ++u) {                                           \
-                const int t = min(b0 + 32 * m + 2 * pl + u, stop - 1);                                \
+                const int t = min(b0 + 32 * m + 16 * u + pl, stop - 1);                               \
                 const uint32_t vo = (uint32_t)(t * VROW + VQ * qq);                                   \
                 if constexpr (VQW == 2) {                                                             \
                     const u32x2 r = ldnt_at<u32x2>(vpay, vo);                                         \
@@ -188,10 +212,11 @@ __device__ __forceinline__ void fast_body(const FastArgs &a, FastSmem &sm)
         uintptr_t tr[IQ_TABLE_COLS];
         if (p < a.run_blocks) {
             // bytes per block of each field: K payload, K scales, K padding,
-            // V payload, V scales, V offsets, K sources, K donors
+            // V payload, V scales, V offsets (K4 values: V padding), K sources, K donors
             const int64_t HB = a.H * a.BT;
             const int64_t per[IQ_TABLE_COLS] = {HB * (D / 2), a.H * D * 4, a.H * a.S * 4, HB * VROW,
-                                                HB * ngroups * 2, HB * ngroups * 2, a.H * a.S, a.H * a.S};
+                                                K4V ? a.H * D * 4 : HB * ngroups * 2,
+                                                K4V ? a.H * a.S * 4 : HB * ngroups * 2, a.H * a.S, a.H * a.S};
 #pragma unroll
             for (int k = 0; k < IQ_TABLE_COLS; ++k) tr[k] = (uintptr_t)(a.run[k] + p * per[k]);
         } else {
@@ -212,6 +237,11 @@ __device__ __forceinline__ void fast_body(const FastArgs &a, FastSmem &sm)
             ksrc = ldg<uint8_t>(srcs + k);
             kdon = ldg<uint8_t>(dons + k);
             kpad = ldg<float>(pads + k);
+            if constexpr (K4V) {
+                vrole = (uint8_t)ldg<int8_t>(a.vmap + (p * a.H + h) * D + (tid & (D - 1)));
+                vscale = ldg<float>((const float *)row(4) + h * D + (tid & (D - 1)));
+                vpad = ldg<float>(S > 0 ? (const float *)row(5) + h * S + k : (const float *)row(4));
+            }
         }
         kpay = (const uint8_t *)row(0) + (int64_t)h * a.BT * (D / 2);
         vpay = (const uint8_t *)row(3) + (int64_t)h * a.BT * VROW;
@@ -243,7 +273,9 @@ __device__ __forceinline__ void fast_body(const FastArgs &a, FastSmem &sm)
     // even channels of a row first (channel c at byte (c & 1) * 64 + c / 2),
     // staged in wave 1's V tile, which is free until the operands are loaded
     uint8_t *const s_sel = (uint8_t *)&sm.v[1][0];
+    uint8_t *const s_vsel = (uint8_t *)&sm.v[2][0];  // the same for K4-coded values
     if (packed && tid < 16 * SELROW / 16) *(u32x4 *)(s_sel + 16 * tid) = u32x4{0u, 0u, 0u, 0u};
+    if (packed && K4V && tid < 16 * SELROW / 16) *(u32x4 *)(s_vsel + 16 * tid) = u32x4{0u, 0u, 0u, 0u};
     if (packed) {
         if (tid < D) {
             // salient and donor channels decode to zero in the 4-bit pass:
@@ -255,6 +287,14 @@ __device__ __forceinline__ void fast_body(const FastArgs &a, FastSmem &sm)
         if (tid < S) {
             s_salw[tid] = ksrc | (kdon << 8);
             s_dpad[tid] = round_q<F16>(kpad);
+        }
+        if constexpr (K4V) {
+            if (tid < D) {
+                s_vc[(tid >> 5) * KC_STRIDE + (tid & 31)] =
+                    vrole == 0xffu ? f32x2{vscale * inv_unit, -8.0f * vscale} : f32x2{0.0f, 0.0f};
+                sm.vrole[tid] = (int8_t)vrole;
+            }
+            if (tid < S) sm.vdpad[tid] = round_q<F16>(vpad);
         }
     }
     __syncthreads();
@@ -282,6 +322,24 @@ __device__ __forceinline__ void fast_body(const FastArgs &a, FastSmem &sm)
             if (k == 0) s_bias[g] = t;
         }
         if (tid >= S && tid < 16) s_salf[tid] = f32x2{0.0f, 0.0f};
+        if constexpr (K4V) {
+            // the value role map marks the value selection matrix the same way;
+            // each descriptor also records its source and donor channel
+            if (tid < D) {
+                const int r = (int)(int8_t)vrole;
+                const int k = r >= 0 ? -2 - (int)sm.vrole[r] : -2 - r;
+                if (k >= 0 && k < S) {
+                    s_vsel[k * SELROW + (tid & 1) * (D / 2) + (tid >> 1)] = r >= 0 ? 16 : 1;
+                    if (r >= 0) {
+                        sm.vsalf[k] = f32x2{vscale, -128.0f * vscale};
+                        sm.vsrc[k] = tid;
+                    } else {
+                        sm.vdon[k] = tid;
+                    }
+                }
+            }
+            if (tid >= S && tid < 16) sm.vsalf[tid] = f32x2{0.0f, 0.0f};
+        }
     }
     __syncthreads();
 
@@ -307,11 +365,21 @@ __device__ __forceinline__ void fast_body(const FastArgs &a, FastSmem &sm)
 #pragma unroll
         for (int e = 0; e < 4; ++e) sf[e] = f32x2{0.0f, 0.0f};
     }
-    // every lane holds its query operands: wave 0's tile may now be overwritten
+    // K4-coded values: the value selection rows (as B operand: source gl) and
+    // the (s, -128 s) of source gl
+    i32x4 vsel_e = {0, 0, 0, 0}, vsel_o = {0, 0, 0, 0};
+    f32x2 vsf = {0.0f, 0.0f};
+    if (PACKED && K4V && S > 0) {
+        vsel_e = *(const i32x4 *)(s_vsel + gl * SELROW + 16 * ql);
+        vsel_o = *(const i32x4 *)(s_vsel + gl * SELROW + D / 2 + 16 * ql);
+        vsf = sm.vsalf[gl];
+    }
+    // every lane holds its operands: the tiles of waves 0-2 may now be overwritten
     __syncthreads();
 
     float m_run = NEG_INF, l_run = 0.0f;
     f32x4 acc[8];                                  // O^T rows 16 n + 4 ql + r, column gl (unscaled)
+    f32x4 acc_sal = {0.0f, 0.0f, 0.0f, 0.0f};      // K4 values: O^T rows = sources 4 ql + r, column gl
 
     uint32_t *vt = s_v[wave];
 
@@ -429,31 +497,95 @@ __device__ __forceinline__ void fast_body(const FastArgs &a, FastSmem &sm)
             for (int r = 0; r < 4; ++r) cmax = fmaxf(cmax, sc[j][r]);
         const float m_new = xmax16(cmax) * a.c_log2;   // one pass per wavefront: nothing to rescale
         float lsum = 0.0f;
-        u32x4 phi[2], plo[2];
+        float pr[4][4];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            float pr[4];
+        for (int j = 0; j < 4; ++j)
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                pr[r] = __builtin_amdgcn_exp2f(fmaf(sc[j][r], a.c_log2, -m_new));
-                lsum += pr[r];
+                pr[j][r] = __builtin_amdgcn_exp2f(fmaf(sc[j][r], a.c_log2, -m_new));
+                lsum += pr[j][r];
             }
-            const uint32_t h01 = pack2<F16>(pr[0], pr[1]), h23 = pack2<F16>(pr[2], pr[3]);
-            phi[j >> 1][2 * (j & 1)] = h01;
-            phi[j >> 1][2 * (j & 1) + 1] = h23;
-            plo[j >> 1][2 * (j & 1)] =
-                pack2<F16>(pr[0] - to_f32<F16>(h01 & 0xffffu), pr[1] - to_f32<F16>(h01 >> 16));
-            plo[j >> 1][2 * (j & 1) + 1] =
-                pack2<F16>(pr[2] - to_f32<F16>(h23 & 0xffffu), pr[3] - to_f32<F16>(h23 >> 16));
-        }
+        // B operand of half chunk m: k-slot pair r = tokens 32 m + 4 ql + r and
+        // 32 m + 16 + 4 ql + r (tiles 2 m and 2 m + 1)
+        u32x4 phi[2], plo[2];
+#pragma unroll
+        for (int m = 0; m < 2; ++m)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const uint32_t hh = pack2<F16>(pr[2 * m][r], pr[2 * m + 1][r]);
+                phi[m][r] = hh;
+                plo[m][r] = pack2<F16>(pr[2 * m][r] - to_f32<F16>(hh & 0xffffu),
+                                       pr[2 * m + 1][r] - to_f32<F16>(hh >> 16));
+            }
         l_run = lsum;
         m_run = m_new;
 
         // ---------------- two half chunks: decode 32 V rows to LDS, then O^T += V^T P^T
 #pragma unroll
         for (int m = 0; m < 2; ++m) {
-            uint32_t *dst = vt + pl * VR + 32 * qq;    // token pair pl, channels 32 qq .. 32 qq + 31
-            if (packed) {
+            uint32_t *dst = vt + pl * VR + 32 * qq;    // pair row pl, channels 32 qq .. 32 qq + 31
+            if (packed && K4V) {
+                // pair row gl (tokens 16 (2 m) + gl and 16 (2 m + 1) + gl: this
+                // lane's rows of tiles 2 m and 2 m + 1), channels 32 ql + 8 d + i,
+                // normal channels only (salient and donor channels decode to 0)
+                uint32_t *drow = vt + gl * VR + 32 * ql;
+#pragma unroll
+                for (int d = 0; d < 4; ++d) {
+                    asm volatile("" ::: "memory");
+                    const f32x2 *vcp = s_vc + ql * KC_STRIDE + 8 * d;
+                    const u32x4 c01 = *(const u32x4 *)(vcp + 0), c23 = *(const u32x4 *)(vcp + 2);
+                    const u32x4 c45 = *(const u32x4 *)(vcp + 4), c67 = *(const u32x4 *)(vcp + 6);
+                    float val[2][8];
+#pragma unroll
+                    for (int u = 0; u < 2; ++u) {
+                        const uint32_t x = vk[2 * m + u][d];
+                        const uint32_t lo = x & 0x0f0f0f0fu, hi = (x >> 4) & 0x0f0f0f0fu;
+                        const f32x2 e01 = fp8x2<false>(lo), e23 = fp8x2<true>(lo);
+                        const f32x2 o01 = fp8x2<false>(hi), o23 = fp8x2<true>(hi);
+#define KF(cv, i) __uint_as_float(cv[i])
+                        val[u][0] = fmaf(e01.x, KF(c01, 0), KF(c01, 1));
+                        val[u][1] = fmaf(o01.x, KF(c01, 2), KF(c01, 3));
+                        val[u][2] = fmaf(e01.y, KF(c23, 0), KF(c23, 1));
+                        val[u][3] = fmaf(o01.y, KF(c23, 2), KF(c23, 3));
+                        val[u][4] = fmaf(e23.x, KF(c45, 0), KF(c45, 1));
+                        val[u][5] = fmaf(o23.x, KF(c45, 2), KF(c45, 3));
+                        val[u][6] = fmaf(e23.y, KF(c67, 0), KF(c67, 1));
+                        val[u][7] = fmaf(o23.y, KF(c67, 2), KF(c67, 3));
+#undef KF
+                    }
+#pragma unroll
+                    for (int c4 = 0; c4 < 2; ++c4) {
+                        u32x4 o;
+#pragma unroll
+                        for (int i = 0; i < 4; ++i) o[i] = pack2<F16>(val[0][4 * c4 + i], val[1][4 * c4 + i]);
+                        *(u32x4 *)(drow + 8 * d + 4 * c4) = o;
+                    }
+                }
+                if (S > 0) {
+                    // salient values of tiles 2 m, 2 m + 1: codes 16 hi + lo with the
+                    // payload as A operand, so lane (source gl, ql) gets tokens
+                    // 4 ql + r, exactly the k-slot pairs of the P^T operand
+                    float sv[2][4];
+#pragma unroll
+                    for (int u = 0; u < 2; ++u) {
+                        i32x4 lo4, hi4;
+#pragma unroll
+                        for (int d = 0; d < 4; ++d) {
+                            lo4[d] = (int)(vk[2 * m + u][d] & 0x0f0f0f0fu);
+                            hi4[d] = (int)((vk[2 * m + u][d] >> 4) & 0x0f0f0f0fu);
+                        }
+                        i32x4 code = __builtin_amdgcn_mfma_i32_16x16x64_i8(lo4, vsel_e, i32x4{0, 0, 0, 0}, 0, 0, 0);
+                        code = __builtin_amdgcn_mfma_i32_16x16x64_i8(hi4, vsel_o, code, 0, 0, 0);
+#pragma unroll
+                        for (int r = 0; r < 4; ++r) sv[u][r] = fmaf((float)code[r], vsf.x, vsf.y);
+                    }
+                    u32x4 sa;
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) sa[r] = pack2<F16>(sv[0][r], sv[1][r]);
+                    acc_sal = mma32<F16>(sa, phi[m], acc_sal);
+                    acc_sal = mma32<F16>(sa, plo[m], acc_sal);
+                }
+            } else if (packed) {
                 float s9[2], of[2];
 #pragma unroll
                 for (int u = 0; u < 2; ++u) {
@@ -514,8 +646,8 @@ __device__ __forceinline__ void fast_body(const FastArgs &a, FastSmem &sm)
                     }
                 }
             } else {
-                const int t0 = base + 32 * m + 2 * pl;
-                const int ta = t0 < stop ? t0 : stop - 1, tb = t0 + 1 < stop ? t0 + 1 : stop - 1;
+                const int t0 = base + 32 * m + pl, t1 = t0 + 16;
+                const int ta = t0 < stop ? t0 : stop - 1, tb = t1 < stop ? t1 : stop - 1;
                 u32x4 r0[4], r1[4];
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
@@ -525,7 +657,7 @@ __device__ __forceinline__ void fast_body(const FastArgs &a, FastSmem &sm)
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
                     if (t0 >= stop) r0[i] = u32x4{0u, 0u, 0u, 0u};
-                    if (t0 + 1 >= stop) r1[i] = u32x4{0u, 0u, 0u, 0u};
+                    if (t1 >= stop) r1[i] = u32x4{0u, 0u, 0u, 0u};
                     u32x4 lo, hi;
 #pragma unroll
                     for (int w = 0; w < 4; ++w) {
@@ -538,12 +670,9 @@ __device__ __forceinline__ void fast_body(const FastArgs &a, FastSmem &sm)
             }
 #pragma unroll
             for (int n = 0; n < 8; ++n) {
-                u32x4 va;
+                u32x4 va;                              // k-slot pair r: pair row 4 ql + r
 #pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    const int pp = e < 2 ? 2 * ql + e : 8 + 2 * ql + (e - 2);
-                    va[e] = vt[pp * VR + 16 * n + gl];
-                }
+                for (int r = 0; r < 4; ++r) va[r] = vt[(4 * ql + r) * VR + 16 * n + gl];
                 acc[n] = mma32<F16>(va, phi[m], m == 0 ? f32x4{0.0f, 0.0f, 0.0f, 0.0f} : acc[n]);
                 acc[n] = mma32<F16>(va, plo[m], acc[n]);
             }
@@ -566,6 +695,20 @@ __device__ __forceinline__ void fast_body(const FastArgs &a, FastSmem &sm)
     float *ot = (float *)vt;
 #pragma unroll
     for (int n = 0; n < 8; ++n) *(f32x4 *)(ot + gl * OROW + 16 * n + 4 * ql) = acc[n];
+    if constexpr (PACKED && K4V) {
+        // the value columns that decoded to 0: a source's column takes its
+        // 8-bit-code product, a donor's round(pad) * sum(p)
+        if (S > 0) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int k = 4 * ql + e;
+                if (k < S) {
+                    ot[gl * OROW + sm.vsrc[k]] = acc_sal[e];
+                    ot[gl * OROW + sm.vdon[k]] = sm.vdpad[k] * l_run;
+                }
+            }
+        }
+    }
     __syncthreads();
     for (int i = tid; i < G * (D / 4); i += 256) {
         const int g = i >> 5, c = (i & 31) * 4;
@@ -600,8 +743,10 @@ __device__ __forceinline__ void fast_body(const FastArgs &a, FastSmem &sm)
     }
 }
 
+// K4-coded values keep twice the value payload and their own selection
+// operands in registers: three workgroups per compute unit instead of four.
 template <bool F16, int VBITS>
-__global__ __launch_bounds__(256, 4) void decode_fast(FastArgs a)
+__global__ __launch_bounds__(256, VBITS == 0 ? 3 : 4) void decode_fast(FastArgs a)
 {
     __shared__ FastSmem sm;
     if ((int64_t)blockIdx.y < a.nblk) fast_body<F16, VBITS, true>(a, sm);
@@ -617,7 +762,8 @@ __global__ __launch_bounds__(256, 4) void decode_fast(FastArgs a)
 // sink ++ tail; *parts receives their count.  With one partition the output is
 // written in-kernel, otherwise the caller merges *parts partials.
 int iq_decode_fast_launch(const void *q, int q_dtype, int64_t q_stride_h, int64_t Hq, const int64_t *tables,
-                          const int8_t *key_map, int64_t n_blocks, int64_t block_tokens, int64_t H, int64_t S,
+                          const int8_t *key_map, const int8_t *value_map, int64_t n_blocks, int64_t block_tokens,
+                          int64_t H, int64_t S,
                           int value_bits, int value_group, const void *sink_k, const void *sink_v, int64_t sink_k_sh,
                           int64_t sink_k_st, int64_t sink_v_sh, int64_t sink_v_st, int64_t sink_t,
                           const void *tail_k, const void *tail_v, int64_t tail_k_sh, int64_t tail_k_st,
@@ -626,8 +772,10 @@ int iq_decode_fast_launch(const void *q, int q_dtype, int64_t q_stride_h, int64_
 {
     if (q_dtype != IQ_BF16 && q_dtype != IQ_F16) return IQ_ERR_UNSUPPORTED;
     if (out_dtype != IQ_F32 && out_dtype != IQ_BF16 && out_dtype != IQ_F16) return IQ_ERR_UNSUPPORTED;
-    if (n_blocks > 0 && value_bits != 2 && value_bits != 4) return IQ_ERR_UNSUPPORTED;
-    if (n_blocks > 0 && value_group != 32 && value_group != 64 && value_group != 128) return IQ_ERR_UNSUPPORTED;
+    if (n_blocks > 0 && value_bits != 0 && value_bits != 2 && value_bits != 4) return IQ_ERR_UNSUPPORTED;
+    if (n_blocks > 0 && value_bits == 0 && !value_map) return IQ_ERR_UNSUPPORTED;
+    if (n_blocks > 0 && value_bits != 0 && value_group != 32 && value_group != 64 && value_group != 128)
+        return IQ_ERR_UNSUPPORTED;
     if (Hq / H > 16 || S > 16) return IQ_ERR_UNSUPPORTED;
     if (n_blocks > 0 && block_tokens > CHUNK * WAVES) return IQ_ERR_UNSUPPORTED;   // one pass per workgroup
     // query, dense rows and packed rows are read as 16-byte vectors
@@ -641,7 +789,8 @@ int iq_decode_fast_launch(const void *q, int q_dtype, int64_t q_stride_h, int64_
         return IQ_ERR_UNSUPPORTED;
     const int64_t P = n_blocks + (sink_t + tail_t + DENSE_SPLIT - 1) / DENSE_SPLIT;
     if (P < 1 || P > 65535) return IQ_ERR_UNSUPPORTED;
-    FastArgs a{{}, 0, (const uint16_t *)q, q_stride_h, (int)(Hq / H), tables, key_map, n_blocks, block_tokens, H, S,
+    FastArgs a{{}, 0, (const uint16_t *)q, q_stride_h, (int)(Hq / H), tables, key_map, value_map, n_blocks,
+               block_tokens, H, S,
                value_group == 32 ? 5 : value_group == 128 ? 7 : 6, (const uint16_t *)sink_k, (const uint16_t *)sink_v, sink_k_sh,
                sink_k_st, sink_v_sh, sink_v_st, sink_t, (const uint16_t *)tail_k, (const uint16_t *)tail_v,
                tail_k_sh, tail_k_st, tail_v_sh, tail_v_st, tail_t, scale * 1.44269504088896341f, workspace, P,
@@ -655,8 +804,10 @@ int iq_decode_fast_launch(const void *q, int q_dtype, int64_t q_stride_h, int64_
     const bool f16 = q_dtype == IQ_F16;
     const int vb = n_blocks > 0 ? value_bits : 2;
     if (f16 && vb == 2) hipLaunchKernelGGL((decode_fast<true, 2>), grid, block, 0, stream, a);
-    else if (f16) hipLaunchKernelGGL((decode_fast<true, 4>), grid, block, 0, stream, a);
+    else if (f16 && vb == 4) hipLaunchKernelGGL((decode_fast<true, 4>), grid, block, 0, stream, a);
+    else if (f16) hipLaunchKernelGGL((decode_fast<true, 0>), grid, block, 0, stream, a);
     else if (vb == 2) hipLaunchKernelGGL((decode_fast<false, 2>), grid, block, 0, stream, a);
-    else hipLaunchKernelGGL((decode_fast<false, 4>), grid, block, 0, stream, a);
+    else if (vb == 4) hipLaunchKernelGGL((decode_fast<false, 4>), grid, block, 0, stream, a);
+    else hipLaunchKernelGGL((decode_fast<false, 0>), grid, block, 0, stream, a);
     return IQ_OK;
 }

@@ -203,6 +203,60 @@ def test_matrix_core_path_matches_oracle(dtype, fraction, block, sink, tail):
     assert torch.equal(typed, torch.from_numpy(got).to("cuda").to(dtype).view_as(typed))
 
 
+def _kernels_run(fn):
+    """Names of the GPU kernels launched by fn()."""
+    from torch.profiler import ProfilerActivity, profile
+    torch.cuda.synchronize()
+    with profile(activities=[ProfilerActivity.CUDA]) as prof:
+        fn()
+        torch.cuda.synchronize()
+    return [e.name for e in prof.events() if e.device_type.name == "CUDA"]
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("fraction,policy", [(0.0, "min_error"), (0.0625, "neighbors"), (0.125, "min_error"),
+                                             (0.125, "neighbors")])
+@pytest.mark.parametrize("block,sink,tail", [(256, 4, 128), (41, 0, 281), (32, 4, 0), (64, 300, 20)])
+def test_k4_values_take_the_matrix_core_path(dtype, fraction, policy, block, sink, tail):
+    # K4-coded values (CacheConfig's default, value_bits=None) with at most 16
+    # salient channels decode on the matrix-core kernel: the value role map,
+    # the 8-bit codes split across source and donor slots and the donor
+    # padding, against the fp64 dequantize-then-attend oracle
+    from inquant.triton_attention import PackedDecodeState
+    case = make_case(31 + block, n_blocks=3, block=block, sink=sink, tail=tail, dtype=dtype, fraction=fraction,
+                     policy=policy, value_bits=0)
+    state = PackedDecodeState(case.key_blocks, case.value_blocks)
+    names = _kernels_run(lambda: _decode_f32(state, case))
+    assert any("decode_fast" in n for n in names) and not any("decode_partials_generic" in n for n in names)
+    np.testing.assert_allclose(_decode_f32(state, case), case.expected(), atol=ATOL, rtol=0)
+
+
+def test_k4_values_peaked_attention_with_salient_value_outliers():
+    # one dominant token whose value outlier channels (x40) are salient: their
+    # 8-bit codes and the donor padding carry the output
+    from inquant.codec import CodecConfig, quantize
+    from inquant.triton_attention import PackedDecodeState
+    from kvcase import oracle_decode
+    import synth
+    cfg = CodecConfig(salient_fraction=0.125, donor_policy="neighbors")
+    k = torch.from_numpy(synth.kv_like(15, 4, 256)).cuda().to(torch.bfloat16)
+    v = torch.from_numpy(synth.kv_like(16, 4, 256, scale=40.0)).cuda().to(torch.bfloat16)
+    q = (k[:, :, 200:201, :].repeat_interleave(7, dim=1) * 0.5).contiguous()
+    kp, vp = quantize(k, cfg), quantize(v, cfg)
+    state = PackedDecodeState([kp], [vp])
+    out = torch.empty(q.shape, dtype=torch.float32, device="cuda")
+    state.decode(q, output=out)
+    np.testing.assert_allclose(to_np(out)[0, :, 0], oracle_decode(q, [kp], [vp]), atol=ATOL, rtol=0)
+
+
+def test_cfg2_full_context_with_k4_values_matches_oracle():
+    # config 2 layer with the reference's default value codec (K4-coded values)
+    from inquant.triton_attention import PackedDecodeState
+    case = make_case(4, n_blocks=128, sink=4, tail=128, value_bits=0)
+    state = PackedDecodeState(case.key_blocks, case.value_blocks)
+    np.testing.assert_allclose(_decode_f32(state, case), case.expected(), atol=ATOL, rtol=0)
+
+
 def test_matrix_core_path_peaked_attention_keeps_precision():
     # one dominant token with large outlier values: P must keep more than
     # bf16 precision for the 2e-3 bound to hold
