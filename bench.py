@@ -556,7 +556,8 @@ def main():
         return
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported on this single-GPU build "
-              "(the decode shards over KV heads with no exchange; see DESIGN.md)", file=sys.stderr)
+              "(the decode shards over KV heads with no exchange: each GPU runs the same kernel on "
+              "its share of heads)", file=sys.stderr)
         sys.exit(2)
     import torch
     if not torch.cuda.is_available():
