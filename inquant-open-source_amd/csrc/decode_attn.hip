@@ -222,28 +222,28 @@ __global__ __launch_bounds__(DA_THREADS) void decode_partials_generic(DecodeArgs
 }
 
 // Log-sum-exp merge of the partition partials (_reduce_partials, triton_attention.py:168-181).
-// 1-D grid of 64 * ceil(Hq / 8): each workgroup merges 16 output channels
-// of one query head, the eight channel slices of a head on one XCD.  Thread (column c4 = tid % 4, lane of partitions part = tid / 4)
-// owns channels 4 c4 .. 4 c4 + 3 and every 64th partition from `part`; a
-// partition costs it three 8-byte loads (two for its four channels, one for
-// (m, l)), all of a round issued before any arithmetic.  Partial rows are
-// 130 floats, so only 8-byte alignment holds.  The 64 running states of a
-// column then merge: the maximum and the rescaled sums over the 16 lanes of
-// a wavefront by shuffles, then over the four wavefronts through LDS.
-constexpr int RED_THREADS = 256;
+// 1-D grid of 64 * ceil(Hq / 8) single-wave workgroups: each merges 16 output
+// channels of one query head, the eight channel slices of a head on one XCD.
+// Lane (column c4 = lane % 4, partition lane part = lane / 4) owns channels
+// 4 c4 .. 4 c4 + 3 and every 16th partition from `part`; a partition costs
+// it three 8-byte loads (two for its four channels, one for (m, l)), nine
+// partitions per round, all issued before any arithmetic.  Partial rows are
+// 130 floats, so only 8-byte alignment holds.  The 16 running states of a
+// column then merge inside the wave (two DPP row rotations, two permlane
+// swaps): no LDS, no barrier (a four-wave form with an LDS exchange measured
+// 0.1 us per layer slower).
+constexpr int RED_THREADS = 64;
 constexpr int RED_C4 = 4;                          // four-channel columns per workgroup
 constexpr int RED_PARTS = RED_THREADS / RED_C4;    // partition lanes
-constexpr int RED_BATCH = 4;                       // partitions per thread per round (256 partitions)
+constexpr int RED_BATCH = 9;                       // partitions per lane per round (144 partitions)
 
 __global__ __launch_bounds__(RED_THREADS) void decode_reduce(const float *ws, int64_t P, int Hq, void *out, int odt)
 {
-    __shared__ float s_m[RED_THREADS / 64][RED_C4], s_l[RED_THREADS / 64][RED_C4];
-    __shared__ f32x4 s_n[RED_THREADS / 64][RED_C4];
     int item, slice;
     iq_xcd_item_slice((int)blockIdx.x, item, slice);    // the 8 channel slices of a head on one XCD
     if (item >= Hq) return;
     const int64_t hq = item;
-    const int tid = threadIdx.x, c4 = tid % RED_C4, part = tid / RED_C4, wave = tid >> 6;
+    const int lane = threadIdx.x, c4 = lane % RED_C4, part = lane / RED_C4;
     const int c0 = slice * (4 * RED_C4) + 4 * c4;
     const float *base = ws + hq * P * (D + 2);
     const float ninf = -__uint_as_float(0x7f800000u);
@@ -277,9 +277,9 @@ __global__ __launch_bounds__(RED_THREADS) void decode_reduce(const float *ws, in
         }
         m = mm;
     }
-    // lanes with equal tid % 4 of a wavefront hold 16 partition lanes of one
-    // column: rotate by 4 and 8 within each 16-lane row (DPP), then across rows
-    static_assert(RED_C4 == 4, "the DPP rotations assume four columns");
+    // lanes with equal lane % 4 hold the 16 partition lanes of one column:
+    // rotate by 4 and 8 within each 16-lane row (DPP), then across the rows
+    static_assert(RED_C4 == 4 && RED_THREADS == 64, "the DPP rotations assume four columns in one wave");
     float mw = fmaxf(m, dpp_f<0x124>(m));          // row_ror:4
     mw = fmaxf(mw, dpp_f<0x128>(mw));              // row_ror:8
     mw = xmax16(mw);
@@ -293,26 +293,9 @@ __global__ __launch_bounds__(RED_THREADS) void decode_reduce(const float *ws, in
     }
     den += dpp_f<0x124>(den);
     den = xsum16(den + dpp_f<0x128>(den));
-    if ((tid & 63) < RED_C4) {
-        s_m[wave][c4] = mw;
-        s_l[wave][c4] = den;
-        s_n[wave][c4] = num;
-    }
-    __syncthreads();
-    if (tid < RED_C4) {
-        float M = s_m[0][c4];
+    if (lane < RED_C4) {
 #pragma unroll
-        for (int w = 1; w < RED_THREADS / 64; ++w) M = fmaxf(M, s_m[w][c4]);
-        f32x4 nn = {0.0f, 0.0f, 0.0f, 0.0f};
-        float dd = 0.0f;
-#pragma unroll
-        for (int w = 0; w < RED_THREADS / 64; ++w) {
-            const float x = s_m[w][c4] == ninf ? 0.0f : __expf(s_m[w][c4] - M);
-            nn += s_n[w][c4] * x;
-            dd = fmaf(s_l[w][c4], x, dd);
-        }
-#pragma unroll
-        for (int e = 0; e < 4; ++e) iq_store_as(out, hq * D + c0 + e, nn[e] / dd, odt);
+        for (int e = 0; e < 4; ++e) iq_store_as(out, hq * D + c0 + e, num[e] / den, odt);
     }
 }
 

@@ -665,42 +665,42 @@ __global__ __launch_bounds__(256, 3) void decode_paged(PagedArgs a)
     else paged_body<NPG, false>(a, sm, geo, pid);
 }
 
-// grid (64 * ceil(Hq / 8), 1, seq): merges the partitions of one sequence
-// for 16 channels of one query head (the eight channel slices of a head on
-// one XCD); the 64 per-thread states of a four-channel
-// column then merge through lane shuffles and LDS (as decode_reduce).
-__global__ __launch_bounds__(256) void paged_reduce(PagedArgs a, void *out, int64_t out_ss, int odt)
+// grid (64 * ceil(Hq / 8), 1, seq) of single-wave workgroups: merges the
+// partitions of one sequence for 16 channels of one query head (the eight
+// channel slices of a head on one XCD), as decode_reduce: lane (column c4 of
+// four channels, partition lane part) takes every 16th partition from
+// `part`, three 8-byte loads each (partial rows are 130 floats, so only
+// 8-byte alignment holds), nine partitions per round all in flight; the 16
+// states of a column then merge inside the wave (DPP row rotations and
+// permlane swaps), with no LDS and no barrier.
+__global__ __launch_bounds__(64) void paged_reduce(PagedArgs a, void *out, int64_t out_ss, int odt)
 {
-    // thread (column c4 of four channels, partition lane part): every 64th
-    // partition from `part`, three 8-byte loads each (partial rows are 130
-    // floats, so only 8-byte alignment holds), all of a round in flight
-    __shared__ float s_m[4][4], s_l[4][4];
-    __shared__ f32x4 s_n[4][4];
+    constexpr int BATCH = 9;
     int hq, slice;
     iq_xcd_item_slice((int)blockIdx.x, hq, slice);       // the 8 channel slices of a head on one XCD
     if (hq >= a.H * a.G) return;
     const int sq = blockIdx.z;
-    const int tid = threadIdx.x, c4 = tid & 3, part = tid >> 2, wave = tid >> 6;
+    const int lane = threadIdx.x, c4 = lane & 3, part = lane >> 2;
     const int c0 = slice * 16 + 4 * c4;
     const SeqGeom geo = seq_geom(a, sq);
     const int P = geo.npp + geo.ndp;
     const float *base = a.ws + ((int64_t)sq * a.H * a.G + hq) * a.max_parts * (D + 2);
     float m = NEG_INF, den = 0.0f;
     f32x4 num = {0.0f, 0.0f, 0.0f, 0.0f};
-    for (int p0 = part; p0 < P; p0 += 64 * 4) {
+    for (int p0 = part; p0 < P; p0 += 16 * BATCH) {
         // every load of the round first, the masks after (see decode_reduce)
-        f32x2 a0[4], a1[4], ml[4];
+        f32x2 a0[BATCH], a1[BATCH], ml[BATCH];
 #pragma unroll
-        for (int k = 0; k < 4; ++k) {
-            const float *r = base + min(p0 + 64 * k, P - 1) * (D + 2);
+        for (int k = 0; k < BATCH; ++k) {
+            const float *r = base + min(p0 + 16 * k, P - 1) * (D + 2);
             a0[k] = *(const f32x2 *)(r + c0);
             a1[k] = *(const f32x2 *)(r + c0 + 2);
             ml[k] = *(const f32x2 *)(r + D);
         }
         float mm = m;
 #pragma unroll
-        for (int k = 0; k < 4; ++k) {
-            if (p0 + 64 * k >= P) ml[k] = f32x2{NEG_INF, 0.0f};
+        for (int k = 0; k < BATCH; ++k) {
+            if (p0 + 16 * k >= P) ml[k] = f32x2{NEG_INF, 0.0f};
             mm = fmaxf(mm, ml[k].x);
         }
         if (mm == NEG_INF) continue;
@@ -708,44 +708,30 @@ __global__ __launch_bounds__(256) void paged_reduce(PagedArgs a, void *out, int6
         num *= wo;
         den *= wo;
 #pragma unroll
-        for (int k = 0; k < 4; ++k) {
+        for (int k = 0; k < BATCH; ++k) {
             const float w = ml[k].x == NEG_INF ? 0.0f : __expf(ml[k].x - mm);
             num += f32x4{a0[k].x, a0[k].y, a1[k].x, a1[k].y} * w;
             den = fmaf(ml[k].y, w, den);
         }
         m = mm;
     }
-    // lanes with equal tid % 4 of a wavefront hold 16 partition lanes of one column
-    float mw = m;
-#pragma unroll
-    for (int sh = 4; sh < 64; sh <<= 1) mw = fmaxf(mw, __shfl_xor(mw, sh, 64));
+    // lanes with equal lane % 4 hold the 16 partition lanes of one column
+    float mw = fmaxf(m, dpp_f<0x124>(m));          // row_ror:4
+    mw = fmaxf(mw, dpp_f<0x128>(mw));              // row_ror:8
+    mw = xmax16(mw);
     const float wt = m == NEG_INF ? 0.0f : __expf(m - mw);
     num *= wt;
     den *= wt;
 #pragma unroll
-    for (int sh = 4; sh < 64; sh <<= 1) {
-#pragma unroll
-        for (int e = 0; e < 4; ++e) num[e] += __shfl_xor(num[e], sh, 64);
-        den += __shfl_xor(den, sh, 64);
+    for (int e = 0; e < 4; ++e) {
+        num[e] += dpp_f<0x124>(num[e]);
+        num[e] = xsum16(num[e] + dpp_f<0x128>(num[e]));
     }
-    if ((tid & 63) < 4) {
-        s_m[wave][c4] = mw;
-        s_l[wave][c4] = den;
-        s_n[wave][c4] = num;
-    }
-    __syncthreads();
-    if (tid < 4) {
-        float M = fmaxf(fmaxf(s_m[0][c4], s_m[1][c4]), fmaxf(s_m[2][c4], s_m[3][c4]));
-        f32x4 nn = {0.0f, 0.0f, 0.0f, 0.0f};
-        float dd = 0.0f;
+    den += dpp_f<0x124>(den);
+    den = xsum16(den + dpp_f<0x128>(den));
+    if (lane < 4) {
 #pragma unroll
-        for (int w = 0; w < 4; ++w) {
-            const float x = s_m[w][c4] == NEG_INF ? 0.0f : __expf(s_m[w][c4] - M);
-            nn += s_n[w][c4] * x;
-            dd = fmaf(s_l[w][c4], x, dd);
-        }
-#pragma unroll
-        for (int e = 0; e < 4; ++e) iq_store_as(out, sq * out_ss + (int64_t)hq * D + c0 + e, nn[e] / dd, odt);
+        for (int e = 0; e < 4; ++e) iq_store_as(out, sq * out_ss + (int64_t)hq * D + c0 + e, num[e] / den, odt);
     }
 }
 
@@ -865,7 +851,7 @@ extern "C" int iq_paged_decode(const void *q, int64_t q_stride_seq, int64_t q_st
     default: hipLaunchKernelGGL(decode_paged<1>, grid, dim3(256), 0, st, a); break;
     }
     IQ_CHECK_LAUNCH("decode_paged");
-    hipLaunchKernelGGL(paged_reduce, dim3((unsigned)(64 * ((Hq + 7) / 8)), 1, (unsigned)n_seq), dim3(256), 0, st, a, out,
+    hipLaunchKernelGGL(paged_reduce, dim3((unsigned)(64 * ((Hq + 7) / 8)), 1, (unsigned)n_seq), dim3(64), 0, st, a, out,
                        out_stride_seq, out_dtype);
     IQ_CHECK_LAUNCH("paged_reduce");
     return IQ_OK;
