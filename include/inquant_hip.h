@@ -24,6 +24,8 @@
  *   iq_k4_dequantize    src/inquant/codec.py:112-134         PackedTensor.dequantize()
  *   iq_v_quantize       src/inquant/value_codec.py:51-72     quantize_values()
  *   iq_v_dequantize     src/inquant/value_codec.py:38-48     PackedValues.dequantize()
+ *   iq_kv_quantize      src/inquant/cache.py:288-295 (the paired key / value block
+ *                       encodes of an append: iq_k4_quantize + iq_v_quantize)
  *   iq_decode_append    src/inquant/triton_attention.py:234-309 PackedDecodeState.extend/_write_maps
  *   iq_decode_attention src/inquant/triton_attention.py:317-388 PackedDecodeState.decode
  *                       (_attention_partials :67-165 + _reduce_partials :168-181)
@@ -102,6 +104,23 @@ int iq_k4_dequantize(const uint8_t *payload, const float *scales, const void *sr
 int iq_v_quantize(const void *x, int x_dtype, const int64_t *x_strides,
                   int64_t B, int64_t H, int64_t T, int64_t D, int bits, int group,
                   uint8_t *payload, uint16_t *scales, uint16_t *offsets, int *bad_flag, void *stream);
+
+/*
+ * Keys and values of the same blocks in one call: iq_k4_quantize of
+ * keys[B, H, T, D] plus iq_v_quantize of values[B, H, T, D] (value_bits 2 or
+ * 4), with the same arguments, outputs and flags as those two.  Sealed
+ * blocks (T = 256, D = 128, 16-bit rows) take one launch whose workgroups
+ * encode a block's values while their first wavefront makes the donor
+ * picks; other shapes run the two encoders back to back.  Replaces the
+ * paired block encodes of a cache append (cache.py:288-295: keys through
+ * _quantize_temporal_blocks, values through quantize_value_blocks).
+ */
+int iq_kv_quantize(const void *keys, const void *values, int dtype, const int64_t *k_strides,
+                   const int64_t *v_strides, int64_t B, int64_t H, int64_t T, int64_t D,
+                   int64_t count, int64_t sample_stride, int min_error, uint8_t *k_payload,
+                   float *k_scales, void *src, void *don, int desc_bytes, float *padding,
+                   int value_bits, int value_group, uint8_t *v_payload, uint16_t *v_scales,
+                   uint16_t *v_offsets, int *key_bad, int *value_bad, void *stream);
 
 /* Value decode: out [rows, D] of out_dtype (rows = B*H*T); value_codec.py:38-48. */
 int iq_v_dequantize(const uint8_t *payload, const uint16_t *scales, const uint16_t *offsets,

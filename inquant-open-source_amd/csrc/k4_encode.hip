@@ -42,6 +42,10 @@ struct K4Args {
     const uint16_t *v;
     int64_t vsb, vsh, vst;
     int *vbad, *clear;          // value flag; flag pair the next page launch uses, zeroed here
+    // fused key/value mode (k4_encode_tile<..., VB = 2 or 4>): the value rows
+    // of v are encoded group-wise into the outputs of iq_v_quantize
+    uint8_t *vpayload;
+    uint16_t *vscales, *voffsets;
 };
 
 __device__ __forceinline__ void store_desc(void *p, int64_t i, int v, int bytes)
@@ -209,9 +213,13 @@ __global__ __launch_bounds__(K4_THREADS) void k4_encode_kernel(K4Args a)
 //           waves 2-3: sampled sums (torch cascade order), amax and
 //           finiteness as an integer max of the 16-bit magnitudes;
 //   then    donor selection by the whole workgroup (iq_select_tile128);
+//           the sequential donor picks run on wave 0 alone, and with a
+//           value row to encode (page mode, or VB = 2 / 4) waves 1-3
+//           group-encode the values meanwhile (v_encode16, the same bits as
+//           v_encode_rows), reading them from HBM while it is otherwise idle;
 //   pass 2  every thread quantizes 8 channels of a token per step, writing
 //           4 payload bytes.
-// LDS stays near 24 KiB, so several blocks share a compute unit and their
+// LDS stays under 40 KiB, so four blocks share a compute unit and their
 // latency-bound phases (the Welford chains, the donor picks) overlap.
 // Bit-identical to k4_encode_kernel.
 constexpr int TILE_D = 128;
@@ -277,9 +285,16 @@ __device__ __forceinline__ float tile_f32(uint32_t bits16)
 // compile time, so the chunk loops unroll without branches and each load is
 // waited for exactly when its chunk is stored (a branch around loads makes
 // the compiler wait for all of them).  NCH = 0: any T <= 256.
-template <bool F16IN, int NCH, bool PAGES = false>
+// PAGES: the row goes into a physical page, values V2 with 64-channel groups.
+// VB = 2 / 4 (not PAGES): the row's values are encoded too, VB bits with
+// 16 * VGL-channel groups, into the outputs of iq_v_quantize.
+template <bool F16IN, int NCH, bool PAGES = false, int VB = 0, int VGL = 4>
 __global__ __launch_bounds__(K4_THREADS, 4) void k4_encode_tile(K4Args a)
 {
+    constexpr int VBITS = PAGES ? 2 : VB;
+    constexpr int GLV = PAGES ? 4 : VGL;
+    static_assert(VBITS == 0 || VBITS == 2 || VBITS == 4, "value bits");
+    static_assert(GLV == 2 || GLV == 4 || GLV == 8, "value group");
     constexpr bool DMA = NCH > 0;
     constexpr int NBUF = DMA ? NBUF_DMA : 2;
     constexpr int ROWLEN = DMA ? TILE_D : XROW;       // u16 per staged row
@@ -496,6 +511,58 @@ __global__ __launch_bounds__(K4_THREADS, 4) void k4_encode_tile(K4Args a)
     // is done with pass 1's buffers)
     __syncthreads();
     start_stream();
+
+    // ---- values (VBITS > 0), encoded by waves 1-3 while wave 0 makes the
+    // sequential donor picks, with the row's HBM reads in that otherwise
+    // idle stretch.  Thread vt of waves 1-3 takes channels 16 vj .. 16 vj + 15
+    // of token vtok0 + 24 it in iteration it (192 threads = 24 tokens), so a
+    // group's GLV lanes are adjacent lanes of one wavefront.  A sealed block
+    // (11 iterations) issues its first VPF iterations' loads here, before
+    // the ranks; the rest run VPF iterations ahead.
+    constexpr int VT = K4_THREADS - 64;
+    constexpr int VIT = NCH > 0 ? (NCH * CH * 8 + VT - 1) / VT : 1;
+    constexpr int VPF = 4;
+    const int vt = tid - 64, vj = vt & 7, vtok0 = vt >> 3;
+    u32x4_t vraw[NCH > 0 ? VIT : 1][2];
+    auto vload = [&](int it, u32x4_t(&r)[2]) {
+        const int t = min(vtok0 + 24 * it, T - 1);
+        const u32x4_t *p = (const u32x4_t *)(a.v + b * a.vsb + h * a.vsh + (int64_t)t * a.vst + 16 * vj);
+        r[0] = __builtin_nontemporal_load(p);
+        r[1] = __builtin_nontemporal_load(p + 1);
+    };
+    auto vencode = [&](int it, const u32x4_t(&r)[2], bool &vbad) {
+        const int t = vtok0 + 24 * it;
+        const bool live = t < T;
+        uint32_t code[VBITS > 0 ? VBITS / 2 : 1];
+        uint16_t off_h, sc_h;
+        if constexpr (VBITS > 0) v_encode16<F16IN, VBITS, GLV>(r, live, code, off_h, sc_h, vbad);
+        if (VBITS > 0 && live) {
+            if constexpr (PAGES) {
+                ((uint32_t *)(page + a.off_vpay + (h * T + t) * (TILE_D / 4)))[vj] = code[0];
+                if ((vj & 3) == 0) ((uint16_t *)(page + a.off_voff))[(h * T + t) * 2 + (vj >> 2)] = off_h;
+                if ((vj & 3) == 3) ((uint16_t *)(page + a.off_vscale))[(h * T + t) * 2 + (vj >> 2)] = sc_h;
+            } else {
+                constexpr int PB = TILE_D * (VBITS > 0 ? VBITS : 2) / 8;   // payload bytes per token
+                constexpr int GROUPS = 8 / GLV;
+                const int64_t vr = row * T + t;
+                if constexpr (VBITS == 2) {
+                    ((uint32_t *)(a.vpayload + vr * PB))[vj] = code[0];
+                } else {
+                    typedef __attribute__((ext_vector_type(2))) uint32_t u32x2_t;
+                    ((u32x2_t *)(a.vpayload + vr * PB))[vj] = u32x2_t{code[0], code[VBITS / 2 - 1]};
+                }
+                if (vj % GLV == 0) a.voffsets[vr * GROUPS + vj / GLV] = off_h;
+                if (vj % GLV == GLV - 1) a.vscales[vr * GROUPS + vj / GLV] = sc_h;
+            }
+        }
+    };
+    if constexpr (VBITS > 0 && NCH > 0) {
+        if (wave > 0) {
+#pragma unroll
+            for (int it = 0; it < VPF; ++it) vload(it, vraw[it]);
+        }
+    }
+
     if (tid < TILE_D) {
         const float smean = s_scale[tid];
         if (a.min_error) {
@@ -511,6 +578,25 @@ __global__ __launch_bounds__(K4_THREADS, 4) void k4_encode_tile(K4Args a)
     else __builtin_amdgcn_s_setprio(0);
     iq_select_tile128(s_sal, a.min_error ? s_err : nullptr, (int)a.count, s_src, s_don, s_is_src, s_src_of,
                       s_key, s_part, s_flag, s_list);
+    if constexpr (VBITS > 0) {
+        if (wave > 0) {
+            bool vbad = false;
+            if constexpr (NCH > 0) {
+#pragma unroll
+                for (int it = 0; it < VIT; ++it) {
+                    if (it + VPF < VIT) vload(it + VPF, vraw[it + VPF]);
+                    vencode(it, vraw[it], vbad);
+                }
+            } else {
+                const int nit = (T * 8 + VT - 1) / VT;
+                for (int it = 0; it < nit; ++it) {
+                    vload(it, vraw[0]);
+                    vencode(it, vraw[0], vbad);
+                }
+            }
+            if (__ballot(vbad) != 0 && lane == 0) atomicOr(a.vbad, 1);
+        }
+    }
     __builtin_amdgcn_s_setprio(1);
     __syncthreads();
 
@@ -614,40 +700,6 @@ __global__ __launch_bounds__(K4_THREADS, 4) void k4_encode_tile(K4Args a)
             }
         }
     });
-    if constexpr (PAGES) {
-        // the row's values, V2 with 64-channel groups (value_codec.py:51-72):
-        // 8 lanes per token (16 channels each, 4 lanes per group), 32 tokens
-        // per pass, four passes' loads in flight
-        const int j8 = tid & 7, tl = tid >> 3;
-        const uint16_t *vr = a.v + b * a.vsb + h * a.vsh + 16 * j8;
-        uint8_t *vpay = page + a.off_vpay + h * (int64_t)T * (TILE_D / 4);
-        uint16_t *vscale = (uint16_t *)(page + a.off_vscale) + h * (int64_t)T * 2;
-        uint16_t *voff = (uint16_t *)(page + a.off_voff) + h * (int64_t)T * 2;
-        bool vbad = false;
-        for (int t0 = 0; t0 < T; t0 += 4 * 32) {
-            u32x4_t raw[4][2];
-#pragma unroll
-            for (int k = 0; k < 4; ++k) {
-                const int t = min(t0 + 32 * k + tl, T - 1);
-                raw[k][0] = *(const u32x4_t *)(vr + (int64_t)t * a.vst);
-                raw[k][1] = *(const u32x4_t *)(vr + (int64_t)t * a.vst + 8);
-            }
-#pragma unroll
-            for (int k = 0; k < 4; ++k) {
-                const int t = t0 + 32 * k + tl;
-                const bool live = t < T;
-                uint32_t code[1];
-                uint16_t off_h, sc_h;
-                v_encode16<F16IN, 2, 4>(raw[k], live, code, off_h, sc_h, vbad);
-                if (live) {
-                    ((uint32_t *)(vpay + t * (TILE_D / 4)))[j8] = code[0];
-                    if ((j8 & 3) == 0) voff[2 * t + (j8 >> 2)] = off_h;
-                    if ((j8 & 3) == 3) vscale[2 * t + (j8 >> 2)] = sc_h;
-                }
-            }
-        }
-        if (__ballot(vbad) != 0 && lane == 0) atomicOr(a.vbad, 1);
-    }
 }
 
 struct SelectArgs {
@@ -716,6 +768,93 @@ extern "C" int iq_k4_quantize(const void *x, int x_dtype, const int64_t *x_strid
     }
     hipLaunchKernelGGL(k4_encode_kernel, dim3((unsigned)(B * H)), dim3(K4_THREADS), 0, (hipStream_t)stream, a);
     IQ_CHECK_LAUNCH("k4_encode_kernel");
+    return IQ_OK;
+}
+
+namespace {
+
+template <bool F16IN, int VB>
+void launch_kv_tile(int VGL, dim3 grid, hipStream_t st, const K4Args &a)
+{
+    constexpr int N = TILE_T / CH;
+    switch (VGL) {
+    case 2: hipLaunchKernelGGL((k4_encode_tile<F16IN, N, false, VB, 2>), grid, dim3(K4_THREADS), 0, st, a); break;
+    case 4: hipLaunchKernelGGL((k4_encode_tile<F16IN, N, false, VB, 4>), grid, dim3(K4_THREADS), 0, st, a); break;
+    default: hipLaunchKernelGGL((k4_encode_tile<F16IN, N, false, VB, 8>), grid, dim3(K4_THREADS), 0, st, a); break;
+    }
+}
+
+}  // namespace
+
+extern "C" int iq_kv_quantize(const void *keys, const void *values, int dtype, const int64_t *k_strides,
+                              const int64_t *v_strides, int64_t B, int64_t H, int64_t T, int64_t D,
+                              int64_t count, int64_t sample_stride, int min_error, uint8_t *k_payload,
+                              float *k_scales, void *src, void *don, int desc_bytes, float *padding,
+                              int value_bits, int value_group, uint8_t *v_payload, uint16_t *v_scales,
+                              uint16_t *v_offsets, int *key_bad, int *value_bad, void *stream)
+{
+    IQ_CHECK_ARG(keys && values && k_strides && v_strides && k_payload && k_scales && v_payload && v_scales &&
+                     v_offsets && key_bad && value_bad,
+                 "iq_kv_quantize: null pointer");
+    IQ_CHECK_ARG(value_bits == 2 || value_bits == 4, "iq_kv_quantize: value_bits must be 2 or 4");
+    IQ_CHECK_ARG(value_group == 32 || value_group == 64 || value_group == 128,
+                 "iq_kv_quantize: value_group must be 32, 64 or 128");
+    auto rows16 = [](const void *p, const int64_t *s) {
+        return ((uintptr_t)p & 15) == 0 && s[3] == 1 && s[0] % 8 == 0 && s[1] % 8 == 0 && s[2] % 8 == 0 &&
+               s[2] >= 0 && s[2] <= (1 << 23);
+    };
+    const bool fused = (dtype == IQ_BF16 || dtype == IQ_F16) && D == TILE_D && T == TILE_T && B >= 1 &&
+                       B <= 0x7fffffffLL && H >= 1 && H <= 65535 && B * H <= 0x7fffffffLL && count >= 0 &&
+                       2 * count <= D && (count == 0 || (src && don && padding)) && sample_stride >= 1 &&
+                       (desc_bytes == 1 || desc_bytes == 4 || desc_bytes == 8) && rows16(keys, k_strides) &&
+                       rows16(values, v_strides);
+    if (!fused) {
+        // any other shape: the two encoders back to back on the stream
+        const int rk = iq_k4_quantize(keys, dtype, k_strides, B, H, T, D, count, sample_stride, min_error,
+                                      k_payload, k_scales, src, don, desc_bytes, padding, key_bad, stream);
+        if (rk != IQ_OK) return rk;
+        return iq_v_quantize(values, dtype, v_strides, B, H, T, D, value_bits, value_group, v_payload, v_scales,
+                             v_offsets, value_bad, stream);
+    }
+    K4Args a{};
+    a.x = keys;
+    a.dt = dtype;
+    a.sb = k_strides[0];
+    a.sh = k_strides[1];
+    a.st = k_strides[2];
+    a.sc = 1;
+    a.H = H;
+    a.T = T;
+    a.D = D;
+    a.count = count;
+    a.stride = sample_stride;
+    a.min_error = min_error ? 1 : 0;
+    a.payload = k_payload;
+    a.scales = k_scales;
+    a.src = src;
+    a.don = don;
+    a.desc_bytes = desc_bytes;
+    a.padding = padding;
+    a.bad = key_bad;
+    a.v = (const uint16_t *)values;
+    a.vsb = v_strides[0];
+    a.vsh = v_strides[1];
+    a.vst = v_strides[2];
+    a.vbad = value_bad;
+    a.vpayload = v_payload;
+    a.vscales = v_scales;
+    a.voffsets = v_offsets;
+    const dim3 grid((unsigned)B, (unsigned)H);
+    const hipStream_t st = (hipStream_t)stream;
+    const int VGL = value_group / 16;
+    if (dtype == IQ_F16) {
+        if (value_bits == 2) launch_kv_tile<true, 2>(VGL, grid, st, a);
+        else launch_kv_tile<true, 4>(VGL, grid, st, a);
+    } else {
+        if (value_bits == 2) launch_kv_tile<false, 2>(VGL, grid, st, a);
+        else launch_kv_tile<false, 4>(VGL, grid, st, a);
+    }
+    IQ_CHECK_LAUNCH("k4_encode_tile (keys and values)");
     return IQ_OK;
 }
 

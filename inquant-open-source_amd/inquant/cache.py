@@ -34,6 +34,7 @@ How a layer is stored here (not how the reference stores it):
 """
 from __future__ import annotations
 
+import math
 from dataclasses import dataclass, field
 from typing import Any, NamedTuple
 
@@ -47,7 +48,7 @@ except ImportError:  # the codec and cache do not need transformers
 
 from . import _native as nat
 from .codec import _BAD_K, CodecConfig, PackedTensor, _per_block, quantize
-from .value_codec import _BAD_V, _value_blocks
+from .value_codec import _BAD_V, PackedValues, _value_blocks
 
 _POSITION_ERROR = "Only contiguous append positions are supported; reset before a new request"
 # flag words of a cache: key non-finite, value non-finite, position mismatch
@@ -205,6 +206,52 @@ def _quantize_temporal_blocks(tensor: torch.Tensor, block_count: int, block_size
     blocked = tensor[0, :, :block_count * block_size].unflatten(1, (block_count, block_size)).transpose(0, 1)
     packed = quantize(blocked, config, _flag=bad)
     return _per_block(packed, block_count, (1, heads, block_size, dim), PackedTensor)
+
+
+def _kv_blocks(keys: torch.Tensor, values: torch.Tensor, block_count: int, block_size: int, config: CodecConfig,
+               bits: int, group_size: int, key_flag: torch.Tensor, value_flag: torch.Tensor):
+    """K4 keys and group-wise values of the first ``block_count`` blocks of
+    [1, H, T, D] in one library call (iq_kv_quantize: one launch for sealed
+    256-token blocks of 128 16-bit channels, the two encoders back to back
+    otherwise), with the per-block objects and flags of
+    _quantize_temporal_blocks + _value_blocks (cache.py:288-295)."""
+    if block_count == 0:
+        return [], []
+    _, heads, _, dim = keys.shape
+
+    def blocked(t):
+        return t[0, :, :block_count * block_size].unflatten(1, (block_count, block_size)).transpose(0, 1)
+
+    kb, vb = blocked(keys), blocked(values)
+    native = (keys.dtype == values.dtype and keys.dtype in (torch.float32, torch.bfloat16, torch.float16)
+              and keys.shape == values.shape and dim % 2 == 0 and dim <= 1024 and dim % group_size == 0)
+    if not native:      # the separate encoders, with their own argument errors
+        return (_quantize_temporal_blocks(keys, block_count, block_size, config, key_flag),
+                _value_blocks(values, block_count, block_size, bits, group_size, value_flag))
+    device = nat.require_gpu(keys, what="quantize")
+    B, H, T, D = kb.shape
+    count = math.floor(D * config.salient_fraction)
+    desc_dtype = torch.uint8 if D <= 256 else torch.int32
+    payload = torch.empty((B, H, T, D // 2), dtype=torch.uint8, device=device)
+    scales = torch.empty((B, H, D), dtype=torch.float32, device=device)
+    src = torch.empty((B, H, count), dtype=desc_dtype, device=device)
+    don = torch.empty((B, H, count), dtype=desc_dtype, device=device)
+    padding = torch.empty((B, H, count), dtype=torch.float32, device=device)
+    v_payload = torch.empty((B, H, T, D * bits // 8), dtype=torch.uint8, device=device)
+    v_scales = torch.empty((B, H, T, D // group_size), dtype=torch.float16, device=device)
+    v_offsets = torch.empty_like(v_scales)
+    nat.check(nat.lib().iq_kv_quantize(
+        kb.data_ptr(), vb.data_ptr(), nat.dtype_code(kb.dtype), nat.strides4(kb), nat.strides4(vb), B, H, T, D,
+        count, config.sample_stride, int(config.donor_policy == "min_error"), payload.data_ptr(),
+        scales.data_ptr(), src.data_ptr() if count else None, don.data_ptr() if count else None,
+        src.element_size(), padding.data_ptr() if count else None, bits, group_size, v_payload.data_ptr(),
+        v_scales.data_ptr(), v_offsets.data_ptr(), key_flag.data_ptr(), value_flag.data_ptr(),
+        nat.stream_handle(device)))
+    shape = (1, heads, block_size, dim)
+    packed_k = PackedTensor(payload, scales, src, don, padding, tuple(kb.shape), keys.dtype)
+    packed_v = PackedValues(v_payload, v_scales, v_offsets, tuple(vb.shape), values.dtype, bits, group_size)
+    return (_per_block(packed_k, block_count, shape, PackedTensor),
+            _per_block(packed_v, block_count, shape, PackedValues, bits=bits, group_size=group_size))
 
 
 class InQuantCache(_HFCache):
@@ -430,14 +477,16 @@ class InQuantCache(_HFCache):
         cfg = self.config
         flags = self._flag_words(keys.device)
         flags[:_POSITION_BAD].zero_()
-        new_keys = _quantize_temporal_blocks(keys, count, cfg.block_size, cfg.codec, flags[_KEY_BAD:_KEY_BAD + 1])
         if cfg.value_bits is None:
+            new_keys = _quantize_temporal_blocks(keys, count, cfg.block_size, cfg.codec,
+                                                 flags[_KEY_BAD:_KEY_BAD + 1])
             new_values = _quantize_temporal_blocks(values, count, cfg.block_size, cfg.codec,
                                                    flags[_VALUE_BAD:_VALUE_BAD + 1])
             value_error = _BAD_K
         else:
-            new_values = _value_blocks(values, count, cfg.block_size, cfg.value_bits, cfg.value_group_size,
-                                       flags[_VALUE_BAD:_VALUE_BAD + 1])
+            new_keys, new_values = _kv_blocks(keys, values, count, cfg.block_size, cfg.codec, cfg.value_bits,
+                                              cfg.value_group_size, flags[_KEY_BAD:_KEY_BAD + 1],
+                                              flags[_VALUE_BAD:_VALUE_BAD + 1])
             value_error = _BAD_V
         bad_key, bad_value, bad_position = flags.tolist()
         if bad_position:
