@@ -30,7 +30,7 @@ namespace {
 constexpr int D = 128;
 constexpr int WAVES = 4;
 constexpr int PART = 256;              // tokens per partition
-constexpr int VR = 136;                // dwords per staged token-pair row of decoded V
+constexpr int VR = 132;                // dwords per staged token-pair row of decoded V (pairs t, t + 16)
 constexpr int KROW = 17;               // dwords per staged K row (salient byte gathers)
 constexpr int OROW = 132;              // floats per staged output row in the combine (conflict-free 16-byte stores)
 constexpr int KG = 36;                 // floats per 32-channel group of page scales (+4: no bank overlap)
@@ -211,13 +211,11 @@ __device__ __forceinline__ SeqGeom seq_geom(const PagedArgs &a, int s)
     return g;
 }
 
-// A wave-uniform 64-bit value (a page address read from LDS) moved to scalar
-// registers, so loads from it take the scalar-base form.
-__device__ __forceinline__ uint64_t uniform_ptr(uint64_t v)
+// Pages a wavefront's 64 tokens touch, and the first of them.
+__host__ __device__ constexpr int pages_per_wave(int npg) { return npg >= WAVES ? npg / WAVES : 1; }
+__device__ __forceinline__ int page_of_wave(int npg, int wave)
 {
-    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
-    const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
-    return (uint64_t)lo | ((uint64_t)hi << 32);
+    return npg >= WAVES ? wave * (npg / WAVES) : wave * npg / WAVES;
 }
 
 // Workgroup LDS of decode_paged, shared by its packed and dense bodies.
@@ -225,7 +223,7 @@ template <int NPG>
 struct __attribute__((aligned(16))) PagedSmem {
     // The V / K staging space of the waves is free until the per-page tables
     // are built, so the role-resolution arrays live in it: at 16-token pages
-    // this keeps a workgroup under 53 KiB, three per compute unit.
+    // this keeps a workgroup under 52 KiB, three per compute unit.
     struct Setup {
         int16_t role[NPG][D];          // key_map of each page
         float padraw[NPG][SPG];
@@ -241,32 +239,34 @@ struct __attribute__((aligned(16))) PagedSmem {
     uint32_t salw[NPG][SPG];           // gather offsets per page
     f32x2 salf[NPG][SPG];              // (s_src, -128 s_src)
     float bias[NPG][16];               // sum_k q[g][don_k] * round(pad_k)
-    uint64_t page[NPG];
-    int pok[NPG];
     float wm[WAVES][16], wl[WAVES][16];
 };
 
 // One partition of one sequence.  The packed and the dense body are separate
 // instantiations so that neither has a branch between its loads and their
 // first use (a branch join there makes the compiler wait for every load in
-// flight).  `pid` is this thread's block-table entry (page tid % NPG of the
-// partition), loaded before the sequence lengths were known.
+// flight).  `pid` holds the block-table entries of this wavefront's pages
+// (page_of_wave), read with scalar loads before the sequence lengths were
+// known.
 template <int NPG, bool PACKED>
-__device__ __forceinline__ void paged_body(const PagedArgs &a, PagedSmem<NPG> &sm, const SeqGeom &geo, int pid)
+__device__ __forceinline__ void paged_body(const PagedArgs &a, PagedSmem<NPG> &sm, const SeqGeom &geo, int wave,
+                                           const int (&pid)[pages_per_wave(NPG)])
 {
     constexpr int B = PART / NPG;
     constexpr int VQW = 2;                       // dwords per 32-channel quarter of a V2 row
     constexpr int CPT = (NPG * D + 255) / 256;   // (page, channel) constants per thread
+    constexpr int PPW = pages_per_wave(NPG);
 
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63;
     const int gl = lane & 15, ql = lane >> 4;
-    const int pl = lane & 15, qq = lane >> 4;      // V writer: distinct token pairs per LDS cycle
+    const int pl = lane & 15, qq = lane >> 4;      // V writer: pair row pl, channels 32 qq .. 32 qq + 31
     const int h = blockIdx.x, p = blockIdx.y, sq = blockIdx.z;
     const int G = a.G;
     const float unit = fp8x2<false>(1u).x;       // fp8 byte 1 == 2^-9
     const float inv_unit = 1.0f / unit;
     uint32_t *const s_v = &sm.v[0][0];
     uint16_t *const s_q = sm.q;
+    const int base = 64 * wave;
 
     // ---------------- geometry
     int ntok, tok0 = 0, slot0 = 0;
@@ -281,19 +281,34 @@ __device__ __forceinline__ void paged_body(const PagedArgs &a, PagedSmem<NPG> &s
         dk = dn + ((int64_t)h * (B + 4) + slot0) * D;
         dv = dn + ((int64_t)(a.H + h) * (B + 4) + slot0) * D;
     }
-    const int npg_here = PACKED ? (ntok + B - 1) / B : 0;
     const int qg = tid >> 4, qc = (tid & 15) * 8;
     const u32x4 qraw = ld16(a.q + sq * a.q_ss + (int64_t)(h * G + (qg < G ? qg : G - 1)) * a.q_sh + qc);
-    if (PACKED && tid < NPG) {
-        // pages past the partition's end or outside the pool read page 0 and stay dead
-        const bool ok = tid < npg_here && pid >= 0 && pid < a.pool_pages;
-        sm.page[tid] = (uint64_t)(a.pool + (ok ? pid : 0) * a.page_bytes);
-        sm.pok[tid] = ok;
+
+    // ---------------- this wavefront's page addresses, in scalar registers:
+    // wpg[i] is page page_of_wave(wave) + i of the partition.  Pages past the
+    // partition's end or outside the pool read page 0 and stay dead (bit i of
+    // okmask clear).
+    const uint8_t *wpg[PPW];
+    uint32_t okmask = 0;
+    if constexpr (PACKED) {
+        const int npg_here = (ntok + B - 1) / B;
+#pragma unroll
+        for (int i = 0; i < PPW; ++i) {
+            const bool ok = page_of_wave(NPG, wave) + i < npg_here && pid[i] >= 0 && pid[i] < a.pool_pages;
+            // page_bytes < 2^32 (checked at launch): one 32 x 32 -> 64-bit product
+            wpg[i] = a.pool + (uint64_t)(uint32_t)(ok ? pid[i] : 0) * (uint32_t)a.page_bytes;
+            okmask |= (ok ? 1u : 0u) << i;
+        }
     }
-    if constexpr (PACKED) __syncthreads();
+    // (page, channel) of this thread's k-th per-channel constant: each
+    // wavefront takes its own pages (NPG >= 4), or half a page (NPG = 2), or
+    // waves 0-1 the one page (NPG = 1)
+    auto cpage = [&](int k) -> int { return NPG >= WAVES ? k >> 1 : 0; };            // index into wpg
+    auto cpart = [&](int k) -> int { return NPG >= WAVES ? wave * PPW + (k >> 1) : (NPG == 2 ? wave >> 1 : 0); };
+    auto cchan = [&](int k) -> int { return NPG >= WAVES ? ((k & 1) << 6) + lane : (tid & (D - 1)); };
+    const bool cvalid = NPG > 1 || tid < D;
 
     // ---------------- every global load of the partition, unconditional (clamped)
-    const int base = 64 * wave;
     float ksc[CPT], kpad = 0.0f;
     int krl[CPT];
     u32x4 kw[4];
@@ -302,41 +317,42 @@ __device__ __forceinline__ void paged_body(const PagedArgs &a, PagedSmem<NPG> &s
     if constexpr (PACKED) {
 #pragma unroll
         for (int k = 0; k < CPT; ++k) {
-            // the page is the same for a whole wavefront: its base goes to
-            // scalar registers and each lane adds a 32-bit offset
-            const int i = min(tid + 256 * k, NPG * D - 1), lp = i >> 7, c = i & (D - 1);
-            const uint8_t *page = (const uint8_t *)uniform_ptr(sm.page[__builtin_amdgcn_readfirstlane(lp)]);
+            // the page is wave-uniform: scalar base, 32-bit lane offset
+            const uint8_t *page = wpg[cpage(k)];
+            const int c = cchan(k);
             ksc[k] = ldg_at<float>(page, (uint32_t)(a.off.ks + (h * D + c) * 4));
             krl[k] = ldg_at<int16_t>(page, (uint32_t)(a.off.km + (h * D + c) * 2));
         }
         {
-            const int i = min(tid, NPG * SPG - 1), lp = i / SPG, j = i % SPG;
-            kpad = ldg<float>((const uint8_t *)sm.page[lp] + a.off.kp + ((int64_t)h * SPG + j) * 4);
+            // lane l of a wavefront: padding j = l % 16 of its page l / 16
+            const int lpl = NPG >= WAVES ? min(lane >> 4, PPW - 1) : 0;
+            const uint8_t *page = wpg[0];
+#pragma unroll
+            for (int i = 1; i < PPW; ++i) page = lpl == i ? wpg[i] : page;
+            kpad = ldg_at<float>(page, (uint32_t)(a.off.kp + (h * SPG + (lane & 15)) * 4));
         }
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             // a 16-token tile lies in one page (B is a multiple of 16); rows
             // past the end read a clamped row of that page and stay dead
-            const int lp = (base + 16 * j) / B;
-            const uint8_t *page = (const uint8_t *)uniform_ptr(sm.page[lp]);
-            const int t = min(base + 16 * j + gl, ntok - 1);
-            kw[j] = ldnt_at<u32x4>(page, (uint32_t)((h * B + t % B) * 64 + 16 * ql));
+            const uint8_t *page = wpg[NPG >= WAVES ? (16 * j) / B : 0];
+            const uint32_t t = (uint32_t)min(base + 16 * j + gl, ntok - 1) & (B - 1);
+            kw[j] = ldnt_at<u32x4>(page, (uint32_t)((h * B + t) * 64 + 16 * ql));
         }
 #pragma unroll
-        for (int m = 0; m < 2; ++m) {
-            // both tokens of a lane's pair (clamped ones too) lie in one page
-            const uint8_t *page = (const uint8_t *)sm.page[min(base + 32 * m + 2 * pl, ntok - 1) / B];
+        for (int m = 0; m < 2; ++m)
 #pragma unroll
             for (int u = 0; u < 2; ++u) {
-                const int t = min(base + 32 * m + 2 * pl + u, ntok - 1);
-                const uint32_t r = (uint32_t)(h * B + t % B);
+                // pair row pl of half m: tokens 32 m + pl (u = 0) and + 16 (u = 1),
+                // each run of 16 tokens inside one page
+                const uint8_t *page = wpg[NPG >= WAVES ? (32 * m + 16 * u) / B : 0];
+                const uint32_t r = (uint32_t)(h * B) + ((uint32_t)min(base + 32 * m + 16 * u + pl, ntok - 1) & (B - 1));
                 const u32x2 w = ldnt_at<u32x2>(page, (uint32_t)a.off.vp + r * 32 + 8 * qq);
                 vw[m][u][0] = w[0];
                 vw[m][u][1] = w[1];
                 vp[m][u][0] = ldg_at<uint16_t>(page, (uint32_t)a.off.vs + (r * 2 + (qq >> 1)) * 2);
                 vp[m][u][1] = ldg_at<uint16_t>(page, (uint32_t)a.off.vo + (r * 2 + (qq >> 1)) * 2);
             }
-        }
         // keep every use of the constants below the payload issue
         asm volatile("" ::: "memory");
     }
@@ -344,17 +360,16 @@ __device__ __forceinline__ void paged_body(const PagedArgs &a, PagedSmem<NPG> &s
     // ---------------- query rows; per-page constants and roles
     *(u32x4 *)(s_q + qg * QROW + qc) = qg < G ? qraw : u32x4{0u, 0u, 0u, 0u};
     if constexpr (PACKED) {
+        if (cvalid) {
 #pragma unroll
-        for (int k = 0; k < CPT; ++k) {
-            const int i = tid + 256 * k;
-            if (i < NPG * D) {
-                const int lp = i >> 7, c = i & (D - 1);
+            for (int k = 0; k < CPT; ++k) {
+                const int lp = cpart(k), c = cchan(k);
                 sm.ka[lp][(c >> 5) * KG + (c & 31)] = krl[k] == -1 ? ksc[k] * inv_unit : 0.0f;
                 sm.setup.role[lp][c] = (int16_t)krl[k];
             }
         }
-        if (tid < NPG * SPG) {
-            const int lp = tid / SPG, j = tid % SPG;
+        if (NPG >= WAVES ? lane < 16 * PPW : lane < 16) {
+            const int lp = NPG >= WAVES ? wave * PPW + (lane >> 4) : wave * NPG / WAVES, j = lane & 15;
             sm.setup.padraw[lp][j] = kpad;
             sm.setup.src[lp][j] = 0;
             sm.setup.don[lp][j] = 0;
@@ -363,11 +378,10 @@ __device__ __forceinline__ void paged_body(const PagedArgs &a, PagedSmem<NPG> &s
         }
         __syncthreads();
         // a source's descriptor index is -2 - key_map[its donor]; a donor's is -2 - key_map
+        if (cvalid) {
 #pragma unroll
-        for (int k = 0; k < CPT; ++k) {
-            const int i = tid + 256 * k;
-            if (i < NPG * D) {
-                const int lp = i >> 7, c = i & (D - 1), role = krl[k];
+            for (int k = 0; k < CPT; ++k) {
+                const int lp = cpart(k), c = cchan(k), role = krl[k];
                 if (role >= 0 && role < D) {
                     const int j = -2 - (int)sm.setup.role[lp][role];
                     if (j >= 0 && j < SPG) {
@@ -411,11 +425,11 @@ __device__ __forceinline__ void paged_body(const PagedArgs &a, PagedSmem<NPG> &s
 
     if (base < ntok) {
         // a token is live when it exists in this partition and (packed) lies
-        // past the sink, or (dense) is a sink slot or a tail slot whose
-        // position is past the sink (kernels.py:37,48)
+        // in a live page past the sink, or (dense) is a sink slot or a tail
+        // slot whose position is past the sink (kernels.py:37,48)
         auto live = [&](int t) -> bool {
             if (t >= ntok) return false;
-            if constexpr (PACKED) return sm.pok[t / B] && tok0 + t >= geo.sink;
+            if constexpr (PACKED) return ((okmask >> ((uint32_t)(t - base) / B)) & 1u) && tok0 + t >= geo.sink;
             const int slot = slot0 + t;
             return slot < geo.sink || (slot >= 4 && slot < 4 + geo.tail && geo.npg * B + slot - 4 >= geo.sink);
         };
@@ -501,51 +515,54 @@ __device__ __forceinline__ void paged_body(const PagedArgs &a, PagedSmem<NPG> &s
             }
         }
 
-        // ---------------- online softmax (log2 domain); lane holds g = gl, tokens 16 j + 4 ql + r
+        // ---------------- softmax (log2 domain); lane holds g = gl, tokens 16 j + 4 ql + r.
+        // Raw logits: the scale is positive, so the maximum commutes with it
+        // and p = 2^(s c - m) takes one fma per logit.
         float cmax = NEG_INF;
 #pragma unroll
         for (int j = 0; j < 4; ++j)
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                const float v = live(base + 16 * j + 4 * ql + r) ? sc[j][r] * a.c_log2 : NEG_INF;
-                sc[j][r] = v;
-                cmax = fmaxf(cmax, v);
+                if (!live(base + 16 * j + 4 * ql + r)) sc[j][r] = NEG_INF;
+                cmax = fmaxf(cmax, sc[j][r]);
             }
-        cmax = xmax16(cmax);
-        const float m_new = fmaxf(m_run, cmax);
+        const float m_new = xmax16(cmax) * a.c_log2;
         const float m_use = m_new == NEG_INF ? 0.0f : m_new;
         float lsum = 0.0f;
-        u32x4 phi[2], plo[2];
+        float pr[4][4];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            float pr[4];
+        for (int j = 0; j < 4; ++j)
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                pr[r] = __builtin_amdgcn_exp2f(sc[j][r] - m_use);
-                lsum += pr[r];
+                pr[j][r] = __builtin_amdgcn_exp2f(fmaf(sc[j][r], a.c_log2, -m_use));
+                lsum += pr[j][r];
             }
-            const uint32_t h01 = pack2<false>(pr[0], pr[1]), h23 = pack2<false>(pr[2], pr[3]);
-            phi[j >> 1][2 * (j & 1)] = h01;
-            phi[j >> 1][2 * (j & 1) + 1] = h23;
-            plo[j >> 1][2 * (j & 1)] =
-                pack2<false>(pr[0] - to_f32<false>(h01 & 0xffffu), pr[1] - to_f32<false>(h01 >> 16));
-            plo[j >> 1][2 * (j & 1) + 1] =
-                pack2<false>(pr[2] - to_f32<false>(h23 & 0xffffu), pr[3] - to_f32<false>(h23 >> 16));
-        }
+        // B operand of half chunk m: k-slot pair r = tokens 32 m + 4 ql + r and
+        // 32 m + 16 + 4 ql + r (tiles 2 m and 2 m + 1)
+        u32x4 phi[2], plo[2];
+#pragma unroll
+        for (int m = 0; m < 2; ++m)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const uint32_t hh = pack2<false>(pr[2 * m][r], pr[2 * m + 1][r]);
+                phi[m][r] = hh;
+                plo[m][r] = pack2<false>(pr[2 * m][r] - to_f32<false>(hh & 0xffffu),
+                                         pr[2 * m + 1][r] - to_f32<false>(hh >> 16));
+            }
         l_run = lsum;
         m_run = m_new;
 
         // ---------------- two half chunks: decode 32 V rows to LDS, then O^T += V^T P^T
 #pragma unroll
         for (int m = 0; m < 2; ++m) {
-            uint32_t *dst = vt + pl * VR + 32 * qq;    // token pair pl, channels 32 qq .. 32 qq + 31
+            uint32_t *dst = vt + pl * VR + 32 * qq;    // pair row pl, channels 32 qq .. 32 qq + 31
             if constexpr (PACKED) {
                 // dead tokens decode to zero: a zero weight times a non-finite
                 // value (a page outside the pool) would still poison P.V
                 float s9[2], of[2];
 #pragma unroll
                 for (int u = 0; u < 2; ++u) {
-                    const bool ok = live(base + 32 * m + 2 * pl + u);
+                    const bool ok = live(base + 32 * m + 16 * u + pl);
                     s9[u] = ok ? iq_f16_to_f32((uint16_t)vp[m][u][0]) * inv_unit : 0.0f;
                     of[u] = ok ? iq_f16_to_f32((uint16_t)vp[m][u][1]) : 0.0f;
                 }
@@ -574,9 +591,9 @@ __device__ __forceinline__ void paged_body(const PagedArgs &a, PagedSmem<NPG> &s
                     }
                 }
             } else {
-                const int t0 = base + 32 * m + 2 * pl;
-                const int ta = min(t0, ntok - 1), tb = min(t0 + 1, ntok - 1);
-                const bool oka = live(t0), okb = live(t0 + 1);
+                const int t0 = base + 32 * m + pl, t1 = t0 + 16;
+                const int ta = min(t0, ntok - 1), tb = min(t1, ntok - 1);
+                const bool oka = live(t0), okb = live(t1);
                 u32x4 r0[4], r1[4];
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
@@ -590,8 +607,8 @@ __device__ __forceinline__ void paged_body(const PagedArgs &a, PagedSmem<NPG> &s
                     u32x4 lo, hi;
 #pragma unroll
                     for (int w = 0; w < 4; ++w) {
-                        lo[w] = __builtin_amdgcn_perm(r1[i][w], r0[i][w], 0x05040100u);
-                        hi[w] = __builtin_amdgcn_perm(r1[i][w], r0[i][w], 0x07060302u);
+                        lo[w] = __builtin_amdgcn_perm(r1[i][w], r0[i][w], 0x05040100u);   // (r0.lo, r1.lo)
+                        hi[w] = __builtin_amdgcn_perm(r1[i][w], r0[i][w], 0x07060302u);   // (r0.hi, r1.hi)
                     }
                     *(u32x4 *)(dst + 8 * i) = u32x4{lo[0], hi[0], lo[1], hi[1]};
                     *(u32x4 *)(dst + 8 * i + 4) = u32x4{lo[2], hi[2], lo[3], hi[3]};
@@ -599,12 +616,9 @@ __device__ __forceinline__ void paged_body(const PagedArgs &a, PagedSmem<NPG> &s
             }
 #pragma unroll
             for (int n = 0; n < 8; ++n) {
-                u32x4 va;
+                u32x4 va;                              // k-slot pair r: pair row 4 ql + r
 #pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    const int pp = e < 2 ? 2 * ql + e : 8 + 2 * ql + (e - 2);
-                    va[e] = vt[pp * VR + 16 * n + gl];
-                }
+                for (int r = 0; r < 4; ++r) va[r] = vt[(4 * ql + r) * VR + 16 * n + gl];
                 acc[n] = mma32<false>(va, phi[m], acc[n]);
                 acc[n] = mma32<false>(va, plo[m], acc[n]);
             }
@@ -612,38 +626,41 @@ __device__ __forceinline__ void paged_body(const PagedArgs &a, PagedSmem<NPG> &s
     }
 
     // ---------------- combine the four wavefronts, write this partition's partial
-    // Each wavefront rescales its O to the workgroup's running max in
-    // registers and stages it as O[g][c] rows; readers then only add.
+    // Each wavefront stages its unnormalized O as O[g][c] rows next to its
+    // (m, l); a reader weights the four rows by 2^(m_w - max m) and adds.
     l_run = xsum16(l_run);
-    if (ql == 0) sm.wm[wave][gl] = m_run;
-    __syncthreads();
-    float mx = sm.wm[0][gl];
-#pragma unroll
-    for (int w = 1; w < WAVES; ++w) mx = fmaxf(mx, sm.wm[w][gl]);
-    const float wt = m_run == NEG_INF ? 0.0f : __builtin_amdgcn_exp2f(m_run - mx);
-    if (ql == 0) sm.wl[wave][gl] = l_run * wt;
+    if (ql == 0) {
+        sm.wm[wave][gl] = m_run;
+        sm.wl[wave][gl] = l_run;
+    }
     float *ot = (float *)vt;
 #pragma unroll
-    for (int n = 0; n < 8; ++n) *(f32x4 *)(ot + gl * OROW + 16 * n + 4 * ql) = acc[n] * wt;
+    for (int n = 0; n < 8; ++n) *(f32x4 *)(ot + gl * OROW + 16 * n + 4 * ql) = acc[n];
     __syncthreads();
     for (int i = tid; i < G * (D / 4); i += 256) {
         const int g = i >> 5, c = (i & 31) * 4;
-        f32x4 num = *(const f32x4 *)((const float *)sm.v[0] + g * OROW + c);
-        float den = sm.wl[0][g];
+        float mw[WAVES], mx = NEG_INF;
 #pragma unroll
-        for (int w = 1; w < WAVES; ++w) {
-            num += *(const f32x4 *)((const float *)sm.v[w] + g * OROW + c);
-            den += sm.wl[w][g];
+        for (int w = 0; w < WAVES; ++w) {
+            mw[w] = sm.wm[w][g];
+            mx = fmaxf(mx, mw[w]);
+        }
+        f32x4 num = {0.0f, 0.0f, 0.0f, 0.0f};
+        float den = 0.0f;
+#pragma unroll
+        for (int w = 0; w < WAVES; ++w) {
+            const float wt = mw[w] == NEG_INF ? 0.0f : __builtin_amdgcn_exp2f(mw[w] - mx);
+            const f32x4 o = *(const f32x4 *)((const float *)sm.v[w] + g * OROW + c);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) num[e] = fmaf(o[e], wt, num[e]);
+            den = fmaf(sm.wl[w][g], wt, den);
         }
         // rows of 130 floats: 8-byte aligned
         float *out = a.ws + (((int64_t)sq * a.H * G + h * G + g) * a.max_parts + p) * (D + 2);
         *(f32x2 *)(out + c) = f32x2{num[0], num[1]};
         *(f32x2 *)(out + c + 2) = f32x2{num[2], num[3]};
         if (c == 0) {
-            float m = sm.wm[0][g];
-#pragma unroll
-            for (int w = 1; w < WAVES; ++w) m = fmaxf(m, sm.wm[w][g]);
-            out[D] = m == NEG_INF ? NEG_INF : m * LN2;
+            out[D] = mx == NEG_INF ? NEG_INF : mx * LN2;
             out[D + 1] = den;
         }
     }
@@ -654,15 +671,26 @@ __device__ __forceinline__ void paged_body(const PagedArgs &a, PagedSmem<NPG> &s
 template <int NPG>
 __global__ __launch_bounds__(256, 3) void decode_paged(PagedArgs a)
 {
+    constexpr int PPW = pages_per_wave(NPG);
     __shared__ PagedSmem<NPG> sm;
     const int p = blockIdx.y, sq = blockIdx.z;
-    // this thread's block-table entry, requested before the lengths arrive
-    int pid = 0;
-    if (a.max_pages > 0) pid = a.bt[sq * a.bt_ss + min((int64_t)p * NPG + (int)(threadIdx.x % NPG), a.max_pages - 1)];
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    // this wavefront's block-table entries (scalar loads), requested before
+    // the lengths arrive; the last partition of a table clamps its indices
+    int pid[PPW];
+    const int64_t first = (int64_t)p * NPG + page_of_wave(NPG, wave);
+    const int32_t *row = a.bt + sq * a.bt_ss;
+    if (first + PPW <= a.max_pages) {
+#pragma unroll
+        for (int i = 0; i < PPW; ++i) pid[i] = row[first + i];
+    } else {
+#pragma unroll
+        for (int i = 0; i < PPW; ++i) pid[i] = a.max_pages > 0 ? row[min(first + i, a.max_pages - 1)] : -1;
+    }
     const SeqGeom geo = seq_geom(a, sq);
     if (p >= geo.npp + geo.ndp) return;
-    if (p < geo.npp) paged_body<NPG, true>(a, sm, geo, pid);
-    else paged_body<NPG, false>(a, sm, geo, pid);
+    if (p < geo.npp) paged_body<NPG, true>(a, sm, geo, wave, pid);
+    else paged_body<NPG, false>(a, sm, geo, wave, pid);
 }
 
 // grid (64 * ceil(Hq / 8), 1, seq) of single-wave workgroups: merges the
@@ -817,6 +845,8 @@ extern "C" int iq_paged_decode(const void *q, int64_t q_stride_seq, int64_t q_st
                  "iq_paged_decode: query and dense rows must be 16-byte aligned");
     const int64_t parts = paged_parts(max_pages, block_tokens);
     IQ_CHECK_ARG(parts <= 65535, "iq_paged_decode: too many partitions");
+    // page fields are addressed with 32-bit offsets from the page
+    IQ_CHECK_ARG(iq_page_bytes(H, block_tokens) < (1LL << 32), "iq_paged_decode: pages of 4 GiB or more");
     IQ_CHECK_ARG(workspace_floats >= n_seq * Hq * parts * (D + 2), "iq_paged_decode: workspace too small");
     PagedArgs a{};
     a.q = (const uint16_t *)q;
