@@ -33,7 +33,6 @@ constexpr int PART = 256;              // tokens per partition
 constexpr int VR = 132;                // dwords per staged token-pair row of decoded V (pairs t, t + 16)
 constexpr int KROW = 17;               // dwords per staged K row (salient byte gathers)
 constexpr int OROW = 132;              // floats per staged output row in the combine (conflict-free 16-byte stores)
-constexpr int KG = 36;                 // floats per 32-channel group of page scales (+4: no bank overlap)
 constexpr int QROW = D + 8;            // u16 per staged query row (+8: rows of one column spread over the banks)
 constexpr int SPG = 16;                // salient channels per page (the layout's key_padding width)
 constexpr float LN2 = 0.693147180559945309f;
@@ -219,27 +218,38 @@ __device__ __forceinline__ int page_of_wave(int npg, int wave)
 }
 
 // Workgroup LDS of decode_paged, shared by its packed and dense bodies.
+// Each wavefront's slot of v (SLOT bytes) holds in turn: the (s * 2^9, -8 s)
+// K constant pairs of its pages [0, SETUP_OFF) and their donor bias
+// [BIAS_OFF, SLOT) up to Q.K; then K staging for the salient gathers
+// [0, SETUP_OFF); then its decoded V tiles and its combine rows (the whole
+// slot).  Until the per-page tables are built, [SETUP_OFF, BIAS_OFF) of
+// slots 0 and 1 hold the role-resolution arrays of every page.  At 16-token
+// pages a workgroup takes 40,704 bytes: four per compute unit.
+constexpr int SLOT = 16 * VR * 4;          // bytes per wavefront slot
+constexpr int KAP_GROUP = 34;              // pairs per 32-channel group (+2: the four groups on distinct banks)
+constexpr int KAP_PAGE = 4 * KAP_GROUP;    // pairs per page
+constexpr int SETUP_OFF = 64 * KROW * 4;   // bytes: past the K staging
+constexpr int BIAS_OFF = SLOT - 4 * 16 * 4;
+static_assert(4 * KAP_PAGE * 8 <= SETUP_OFF, "constant pairs of four pages fit below the setup arrays");
+
 template <int NPG>
 struct __attribute__((aligned(16))) PagedSmem {
-    // The V / K staging space of the waves is free until the per-page tables
-    // are built, so the role-resolution arrays live in it: at 16-token pages
-    // this keeps a workgroup under 52 KiB, three per compute unit.
-    struct Setup {
-        int16_t role[NPG][D];          // key_map of each page
-        float padraw[NPG][SPG];
-        int16_t src[NPG][SPG], don[NPG][SPG];
-        float ssc[NPG][SPG], pad[NPG][SPG];
-    };
-    union {
-        uint32_t v[WAVES][16 * VR];    // decoded V tiles, K staging, the final combine
-        Setup setup;
-    };
+    uint32_t v[WAVES][16 * VR];        // per-wavefront slots (above)
     uint16_t q[16 * QROW];
-    float ka[NPG][4 * KG];             // s * 2^9, zero at salient/donor channels
     uint32_t salw[NPG][SPG];           // gather offsets per page
-    f32x2 salf[NPG][SPG];              // (s_src, -128 s_src)
-    float bias[NPG][16];               // sum_k q[g][don_k] * round(pad_k)
+    float ssc[NPG][SPG];               // scale of the source of descriptor k
     float wm[WAVES][16], wl[WAVES][16];
+
+    __device__ f32x2 *kap(int w) { return (f32x2 *)&v[w][0]; }                          // [page of w][4][KAP_GROUP]
+    __device__ float *bias(int w) { return (float *)((char *)&v[w][0] + BIAS_OFF); }    // [page of w][16]
+    __device__ int8_t *role() { return (int8_t *)((char *)&v[0][0] + SETUP_OFF); }     // [NPG][D]
+    __device__ float *padraw() { return (float *)((char *)&v[1][0] + SETUP_OFF); }     // [NPG][SPG]
+    __device__ float *spad() { return padraw() + NPG * SPG; }                           // round(pad) of descriptor k
+    __device__ float *sssc() { return spad() + NPG * SPG; }                             // source scale of descriptor k
+    __device__ int8_t *ssrc() { return (int8_t *)(sssc() + NPG * SPG); }                // source channel of descriptor k
+    __device__ int8_t *sdon() { return ssrc() + NPG * SPG; }                            // donor channel of descriptor k
+    static_assert(NPG * D <= BIAS_OFF - SETUP_OFF, "role map fits in slot 0");
+    static_assert(NPG * SPG * (3 * 4 + 2) <= BIAS_OFF - SETUP_OFF, "descriptor arrays fit in slot 1");
 };
 
 // One partition of one sequence.  The packed and the dense body are separate
@@ -358,23 +368,33 @@ __device__ __forceinline__ void paged_body(const PagedArgs &a, PagedSmem<NPG> &s
     }
 
     // ---------------- query rows; per-page constants and roles
+    // Wavefront w reads the K constants of page lp from its slot: wavefronts
+    // own their pages (NPG >= 4), or share the one page of their tokens.
+    auto owner0 = [&](int lp) -> int { return NPG >= WAVES ? lp / PPW : lp * WAVES / NPG; };
+    constexpr int OWNERS = NPG >= WAVES ? 1 : WAVES / NPG;
+    auto local = [&](int lp) -> int { return NPG >= WAVES ? lp % PPW : 0; };
     *(u32x4 *)(s_q + qg * QROW + qc) = qg < G ? qraw : u32x4{0u, 0u, 0u, 0u};
     if constexpr (PACKED) {
         if (cvalid) {
 #pragma unroll
             for (int k = 0; k < CPT; ++k) {
                 const int lp = cpart(k), c = cchan(k);
-                sm.ka[lp][(c >> 5) * KG + (c & 31)] = krl[k] == -1 ? ksc[k] * inv_unit : 0.0f;
-                sm.setup.role[lp][c] = (int16_t)krl[k];
+                // zero at salient and donor channels: they decode to 0
+                const float A = krl[k] == -1 ? ksc[k] * inv_unit : 0.0f;
+                const f32x2 pair = {A, A * -0.015625f};         // (s * 2^9, -8 s), both exact
+#pragma unroll
+                for (int o = 0; o < OWNERS; ++o)
+                    sm.kap(owner0(lp) + o)[local(lp) * KAP_PAGE + (c >> 5) * KAP_GROUP + (c & 31)] = pair;
+                sm.role()[lp * D + c] = (int8_t)krl[k];
             }
         }
         if (NPG >= WAVES ? lane < 16 * PPW : lane < 16) {
             const int lp = NPG >= WAVES ? wave * PPW + (lane >> 4) : wave * NPG / WAVES, j = lane & 15;
-            sm.setup.padraw[lp][j] = kpad;
-            sm.setup.src[lp][j] = 0;
-            sm.setup.don[lp][j] = 0;
-            sm.setup.ssc[lp][j] = 0.0f;
-            sm.setup.pad[lp][j] = 0.0f;
+            sm.padraw()[lp * SPG + j] = kpad;
+            sm.ssrc()[lp * SPG + j] = 0;
+            sm.sdon()[lp * SPG + j] = 0;
+            sm.sssc()[lp * SPG + j] = 0.0f;
+            sm.spad()[lp * SPG + j] = 0.0f;
         }
         __syncthreads();
         // a source's descriptor index is -2 - key_map[its donor]; a donor's is -2 - key_map
@@ -383,32 +403,33 @@ __device__ __forceinline__ void paged_body(const PagedArgs &a, PagedSmem<NPG> &s
             for (int k = 0; k < CPT; ++k) {
                 const int lp = cpart(k), c = cchan(k), role = krl[k];
                 if (role >= 0 && role < D) {
-                    const int j = -2 - (int)sm.setup.role[lp][role];
+                    const int j = -2 - (int)sm.role()[lp * D + role];
                     if (j >= 0 && j < SPG) {
-                        sm.setup.src[lp][j] = (int16_t)c;
-                        sm.setup.ssc[lp][j] = ksc[k];
+                        sm.ssrc()[lp * SPG + j] = (int8_t)c;
+                        sm.sssc()[lp * SPG + j] = ksc[k];
                     }
                 } else if (role <= -2 && role >= -2 - (SPG - 1)) {
                     const int j = -2 - role;
-                    sm.setup.don[lp][j] = (int16_t)c;
-                    sm.setup.pad[lp][j] = round_q<false>(sm.setup.padraw[lp][j]);
+                    sm.sdon()[lp * SPG + j] = (int8_t)c;
+                    sm.spad()[lp * SPG + j] = round_q<false>(sm.padraw()[lp * SPG + j]);
                 }
             }
         }
         __syncthreads();
-        // per-page salient tables and donor bias
+        // per-page salient tables, and the donor bias of each page in its owners' slots
         for (int i = tid; i < NPG * SPG; i += 256) {
             const int lp = i / SPG, k = i % SPG;
-            const uint32_t src = (uint32_t)sm.setup.src[lp][k], don = (uint32_t)sm.setup.don[lp][k];
+            const uint32_t src = (uint8_t)sm.ssrc()[i], don = (uint8_t)sm.sdon()[i];
             sm.salw[lp][k] = (src >> 1) | (((src & 1) * 4) << 8) | ((don >> 1) << 16) | (((don & 1) * 4) << 24);
-            const float ssc = sm.setup.ssc[lp][k];
-            sm.salf[lp][k] = f32x2{ssc, -128.0f * ssc};
+            sm.ssc[lp][k] = sm.sssc()[i];
         }
         for (int i = tid; i < NPG * 16; i += 256) {
             const int lp = i >> 4, g = i & 15;
             float b = 0.0f;
-            for (int k = 0; k < SPG; ++k) b = fmaf(to_f32<false>(s_q[g * QROW + sm.setup.don[lp][k]]), sm.setup.pad[lp][k], b);
-            sm.bias[lp][g] = b;
+            for (int k = 0; k < SPG; ++k)
+                b = fmaf(to_f32<false>(s_q[g * QROW + (uint8_t)sm.sdon()[lp * SPG + k]]), sm.spad()[lp * SPG + k], b);
+#pragma unroll
+            for (int o = 0; o < OWNERS; ++o) sm.bias(owner0(lp) + o)[local(lp) * 16 + g] = b;
         }
     }
     __syncthreads();
@@ -435,24 +456,26 @@ __device__ __forceinline__ void paged_body(const PagedArgs &a, PagedSmem<NPG> &s
         };
         f32x4 sc[4];
         if constexpr (PACKED) {
+            const f32x2 *kap = sm.kap(wave);
+            const float *wbias = sm.bias(wave);
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
-                const int lp = (base + 16 * j) / B;
+                const int lpl = NPG >= WAVES ? (16 * j) / B : 0;   // the tile's page among the wavefront's
                 asm volatile("" ::: "memory");
-                const float bias = sm.bias[lp][gl];
+                const float bias = wbias[lpl * 16 + gl];
                 f32x4 s = {bias, bias, bias, bias};
 #pragma unroll
                 for (int d = 0; d < 4; ++d) {
-                    const float *ka = &sm.ka[lp][ql * KG + 8 * d];
-                    const u32x4 a03 = *(const u32x4 *)ka, a47 = *(const u32x4 *)(ka + 4);
+                    const f32x2 *cp = kap + lpl * KAP_PAGE + ql * KAP_GROUP + 8 * d;
                     float A[8], Bc[8];
 #pragma unroll
-                    for (int e = 0; e < 4; ++e) {
-                        A[e] = __uint_as_float(a03[e]);
-                        A[4 + e] = __uint_as_float(a47[e]);
+                    for (int e2 = 0; e2 < 4; ++e2) {
+                        const u32x4 c = *(const u32x4 *)(cp + 2 * e2);   // pairs 2 e2, 2 e2 + 1
+                        A[2 * e2] = __uint_as_float(c[0]);
+                        Bc[2 * e2] = __uint_as_float(c[1]);
+                        A[2 * e2 + 1] = __uint_as_float(c[2]);
+                        Bc[2 * e2 + 1] = __uint_as_float(c[3]);
                     }
-#pragma unroll
-                    for (int e = 0; e < 8; ++e) Bc[e] = A[e] * -0.015625f;   // -8 s, exact
                     const uint32_t x = kw[j][d];
                     const uint32_t lo = x & 0x0f0f0f0fu, hi = (x >> 4) & 0x0f0f0f0fu;
                     const f32x2 e01 = fp8x2<false>(lo), e23 = fp8x2<true>(lo);
@@ -483,10 +506,10 @@ __device__ __forceinline__ void paged_body(const PagedArgs &a, PagedSmem<NPG> &s
                     const uint32_t w = sm.salw[lp][4 * ql + e];
                     // Q[g][source channel]; the source is 2 (w & 255) + ((w >> 8) & 255) / 4
                     qv[e] = s_q[gl * QROW + 2 * (w & 0xffu) + (((w >> 8) & 0xffu) >> 2)];
-                    const f32x2 sf = sm.salf[lp][4 * ql + e];
                     const uint32_t hi = (rowp[w & 0xffu] >> ((w >> 8) & 0xffu)) & 15u;
                     const uint32_t lo = (rowp[(w >> 16) & 0xffu] >> (w >> 24)) & 15u;
-                    v[e] = fmaf((float)((hi << 4) | lo), sf.x, sf.y);
+                    // (code - 128) * s in one rounding, as the reference's multiply
+                    v[e] = (float)((int)((hi << 4) | lo) - 128) * sm.ssc[lp][4 * ql + e];
                 }
                 const u32x2 ka = {pack2<false>(v[0], v[1]), pack2<false>(v[2], v[3])};
                 const u32x2 qs = {qv[0] | (qv[1] << 16), qv[2] | (qv[3] << 16)};
@@ -669,7 +692,7 @@ __device__ __forceinline__ void paged_body(const PagedArgs &a, PagedSmem<NPG> &s
 // One workgroup per (KV head, partition, sequence); NPG = pages per packed
 // partition (PART / B).
 template <int NPG>
-__global__ __launch_bounds__(256, 3) void decode_paged(PagedArgs a)
+__global__ __launch_bounds__(256, 4) void decode_paged(PagedArgs a)
 {
     constexpr int PPW = pages_per_wave(NPG);
     __shared__ PagedSmem<NPG> sm;
