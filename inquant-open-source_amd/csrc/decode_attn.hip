@@ -209,16 +209,13 @@ __global__ __launch_bounds__(DA_THREADS) void decode_partials_generic(DecodeArgs
         __syncthreads();
     }
 
-    float *ws = a.ws;
+    const Partials pt = partials(a.ws, a.H * G * a.P);
 #pragma unroll
     for (int k = 0; k < GMAX / 2; ++k) {
         const int g = g0 + 2 * k;
-        if (g < G) ws[((int64_t)(h * G + g) * a.P + p) * (D + 2) + d] = acc[k];
+        if (g < G) pt.o[((int64_t)(h * G + g) * a.P + p) * D + d] = acc[k];
     }
-    if (tid < G) {
-        ws[((int64_t)(h * G + tid) * a.P + p) * (D + 2) + D] = s_m[tid];
-        ws[((int64_t)(h * G + tid) * a.P + p) * (D + 2) + D + 1] = s_l[tid];
-    }
+    if (tid < G) pt.ml[(int64_t)(h * G + tid) * a.P + p] = f32x2{s_m[tid], s_l[tid]};
 }
 
 // Log-sum-exp merge of the partition partials (_reduce_partials, triton_attention.py:168-181).
@@ -245,19 +242,20 @@ __global__ __launch_bounds__(RED_THREADS) void decode_reduce(const float *ws, in
     const int64_t hq = item;
     const int lane = threadIdx.x, c4 = lane % RED_C4, part = lane / RED_C4;
     const int c0 = slice * (4 * RED_C4) + 4 * c4;
-    const float *base = ws + hq * P * (D + 2);
+    const Partials pt = partials(const_cast<float *>(ws), (int64_t)Hq * P);
+    const float *base = pt.o + hq * P * D;
+    const f32x2 *mlb = pt.ml + hq * P;
     const float ninf = -__uint_as_float(0x7f800000u);
     float m = ninf, den = 0.0f;
     f32x4 num = {0.0f, 0.0f, 0.0f, 0.0f};
     for (int p0 = part; p0 < (int)P; p0 += RED_PARTS * RED_BATCH) {
-        f32x2 a0[RED_BATCH], a1[RED_BATCH], ml[RED_BATCH];
+        f32x4 a[RED_BATCH];
+        f32x2 ml[RED_BATCH];
 #pragma unroll
         for (int k = 0; k < RED_BATCH; ++k) {
             const int pp = min(p0 + RED_PARTS * k, (int)P - 1);
-            const float *r = base + (int64_t)pp * (D + 2);
-            a0[k] = *(const f32x2 *)(r + c0);
-            a1[k] = *(const f32x2 *)(r + c0 + 2);
-            ml[k] = *(const f32x2 *)(r + D);
+            a[k] = *(const f32x4 *)(base + (int64_t)pp * D + c0);
+            ml[k] = mlb[pp];
         }
         float mm = m;
 #pragma unroll
@@ -272,7 +270,7 @@ __global__ __launch_bounds__(RED_THREADS) void decode_reduce(const float *ws, in
 #pragma unroll
         for (int k = 0; k < RED_BATCH; ++k) {
             const float w = ml[k].x == ninf ? 0.0f : __expf(ml[k].x - mm);
-            num += f32x4{a0[k].x, a0[k].y, a1[k].x, a1[k].y} * w;
+            num += a[k] * w;
             den = fmaf(ml[k].y, w, den);
         }
         m = mm;

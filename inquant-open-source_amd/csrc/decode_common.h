@@ -140,6 +140,17 @@ __device__ __forceinline__ T ldnt(const void *p)
 
 constexpr float NEG_INF = -__builtin_inff();
 
+// Partition partials in a workspace of rows * (128 + 2) floats: the
+// unnormalized output rows first (rows x 128, 16-byte aligned), then the
+// (max, sum) pairs (rows x 2), so that a merge reads whole 16-byte channel
+// columns and the pairs of consecutive partitions from one cache line.
+struct Partials {
+    float *o;
+    f32x2 *ml;
+};
+
+__device__ __forceinline__ Partials partials(float *ws, int64_t rows) { return {ws, (f32x2 *)(ws + rows * 128)}; }
+
 // Workgroups go to the eight XCDs round-robin by linear id, and each XCD has
 // its own L2.  For a 1-D grid of 64 * ceil(n / 8) workgroups this maps the
 // linear id i to (item, slice) so that the eight slices of an item run on one

@@ -733,13 +733,10 @@ __device__ __forceinline__ void fast_body(const FastArgs &a, FastSmem &sm)
             for (int e = 0; e < 4; ++e) iq_store_as(a.out, (int64_t)(h * G + g) * D + c + e, num[e] / den, a.odt);
             continue;
         }
-        float *out = a.ws + ((int64_t)(h * G + g) * a.P + p) * (D + 2);   // rows of 130 floats: 8-byte aligned
-        *(f32x2 *)(out + c) = f32x2{num[0], num[1]};
-        *(f32x2 *)(out + c + 2) = f32x2{num[2], num[3]};
-        if (c == 0) {
-            out[D] = mx * LN2;
-            out[D + 1] = den;
-        }
+        const Partials pt = partials(a.ws, a.H * G * a.P);
+        const int64_t row = (int64_t)(h * G + g) * a.P + p;
+        *(f32x4 *)(pt.o + row * D + c) = num;
+        if (c == 0) pt.ml[row] = f32x2{mx * LN2, den};
     }
 }
 

@@ -678,14 +678,10 @@ __device__ __forceinline__ void paged_body(const PagedArgs &a, PagedSmem<NPG> &s
             for (int e = 0; e < 4; ++e) num[e] = fmaf(o[e], wt, num[e]);
             den = fmaf(sm.wl[w][g], wt, den);
         }
-        // rows of 130 floats: 8-byte aligned
-        float *out = a.ws + (((int64_t)sq * a.H * G + h * G + g) * a.max_parts + p) * (D + 2);
-        *(f32x2 *)(out + c) = f32x2{num[0], num[1]};
-        *(f32x2 *)(out + c + 2) = f32x2{num[2], num[3]};
-        if (c == 0) {
-            out[D] = mx == NEG_INF ? NEG_INF : mx * LN2;
-            out[D + 1] = den;
-        }
+        const Partials pt = partials(a.ws, (int64_t)gridDim.z * a.H * G * a.max_parts);
+        const int64_t row = ((int64_t)sq * a.H * G + h * G + g) * a.max_parts + p;
+        *(f32x4 *)(pt.o + row * D + c) = num;
+        if (c == 0) pt.ml[row] = f32x2{mx == NEG_INF ? NEG_INF : mx * LN2, den};
     }
 }
 
@@ -735,18 +731,19 @@ __global__ __launch_bounds__(64) void paged_reduce(PagedArgs a, void *out, int64
     const int c0 = slice * 16 + 4 * c4;
     const SeqGeom geo = seq_geom(a, sq);
     const int P = geo.npp + geo.ndp;
-    const float *base = a.ws + ((int64_t)sq * a.H * a.G + hq) * a.max_parts * (D + 2);
+    const Partials pt = partials(a.ws, (int64_t)gridDim.z * a.H * a.G * a.max_parts);
+    const int64_t row0 = ((int64_t)sq * a.H * a.G + hq) * a.max_parts;
     float m = NEG_INF, den = 0.0f;
     f32x4 num = {0.0f, 0.0f, 0.0f, 0.0f};
     for (int p0 = part; p0 < P; p0 += 16 * BATCH) {
         // every load of the round first, the masks after (see decode_reduce)
-        f32x2 a0[BATCH], a1[BATCH], ml[BATCH];
+        f32x4 ov[BATCH];
+        f32x2 ml[BATCH];
 #pragma unroll
         for (int k = 0; k < BATCH; ++k) {
-            const float *r = base + min(p0 + 16 * k, P - 1) * (D + 2);
-            a0[k] = *(const f32x2 *)(r + c0);
-            a1[k] = *(const f32x2 *)(r + c0 + 2);
-            ml[k] = *(const f32x2 *)(r + D);
+            const int64_t row = row0 + min(p0 + 16 * k, P - 1);
+            ov[k] = *(const f32x4 *)(pt.o + row * D + c0);
+            ml[k] = pt.ml[row];
         }
         float mm = m;
 #pragma unroll
@@ -761,7 +758,7 @@ __global__ __launch_bounds__(64) void paged_reduce(PagedArgs a, void *out, int64
 #pragma unroll
         for (int k = 0; k < BATCH; ++k) {
             const float w = ml[k].x == NEG_INF ? 0.0f : __expf(ml[k].x - mm);
-            num += f32x4{a0[k].x, a0[k].y, a1[k].x, a1[k].y} * w;
+            num += ov[k] * w;
             den = fmaf(ml[k].y, w, den);
         }
         m = mm;
