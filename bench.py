@@ -274,8 +274,36 @@ def time_encode(device, reps=10):
     assert bad.tolist() == [0, 0]
     enc_bytes = 2 * k.numel() * 2 + pay.numel() + sc.numel() * 4 + src.numel() * 2 + pad.numel() * 4 \
         + vpay.numel() + vsc.numel() * 4
+
+    # the same layer with K4-coded values (the cache's default value_bits=None):
+    # keys and values K4 in one launch (iq_k4_quantize_kv)
+    vk = [torch.empty_like(t) for t in (pay, sc, src, don, pad)]
+
+    def once_k4v():
+        nat.check(lib.iq_k4_quantize_kv(kb.data_ptr(), vb.data_ptr(), nat.IQ_BF16, nat.strides4(kb),
+                                        nat.strides4(vb), nb, H, B, 128, S, 8, 1, pay.data_ptr(), sc.data_ptr(),
+                                        src.data_ptr(), don.data_ptr(), pad.data_ptr(), *[t.data_ptr() for t in vk],
+                                        1, bad.data_ptr(), bad.data_ptr() + 4, stream))
+
+    graph2 = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(s):
+        once_k4v()
+        torch.cuda.synchronize()
+        with torch.cuda.graph(graph2, stream=s):
+            for _ in range(reps):
+                once_k4v()
+    torch.cuda.synchronize()
+    graph2.replay()
+    torch.cuda.synchronize()
+    start.record()
+    graph2.replay()
+    stop.record()
+    torch.cuda.synchronize()
+    ms_k4v = start.elapsed_time(stop) / reps
+    assert bad.tolist() == [0, 0]
     return {"encode_mtok_s": T / (ms * 1e-3) / 1e6, "encode_ms_per_layer": ms,
-            "encode_gbs": enc_bytes / (ms * 1e-3) / 1e9, "encode_bytes_per_layer": enc_bytes}
+            "encode_gbs": enc_bytes / (ms * 1e-3) / 1e9, "encode_bytes_per_layer": enc_bytes,
+            "k4_values_mtok_s": T / (ms_k4v * 1e-3) / 1e6, "k4_values_ms_per_layer": ms_k4v}
 
 
 def time_paged(device, layers=4, n_seq=16, block=16, H=4, G=7, seed=4, steps=20):

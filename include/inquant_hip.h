@@ -26,6 +26,7 @@
  *   iq_v_dequantize     src/inquant/value_codec.py:38-48     PackedValues.dequantize()
  *   iq_kv_quantize      src/inquant/cache.py:288-295 (the paired key / value block
  *                       encodes of an append: iq_k4_quantize + iq_v_quantize)
+ *   iq_k4_quantize_kv   src/inquant/cache.py:288-291 (the same with K4-coded values)
  *   iq_decode_append    src/inquant/triton_attention.py:234-309 PackedDecodeState.extend/_write_maps
  *   iq_decode_attention src/inquant/triton_attention.py:317-388 PackedDecodeState.decode
  *                       (_attention_partials :67-165 + _reduce_partials :168-181)
@@ -121,6 +122,21 @@ int iq_kv_quantize(const void *keys, const void *values, int dtype, const int64_
                    float *k_scales, void *src, void *don, int desc_bytes, float *padding,
                    int value_bits, int value_group, uint8_t *v_payload, uint16_t *v_scales,
                    uint16_t *v_offsets, int *key_bad, int *value_bad, void *stream);
+
+/*
+ * Keys and values of the same blocks, both K4-coded (the cache's default
+ * value_bits = None), in one call: iq_k4_quantize of keys and of values with
+ * the same arguments, outputs (k_* for keys, v_* for values) and flags as two
+ * calls of it.  Tile shapes (16-bit rows of D = 128, T <= 256) take one
+ * launch over (B, 2 H) rows; others run the two encodes back to back.
+ * Replaces the paired block encodes of an append (cache.py:288-291).
+ */
+int iq_k4_quantize_kv(const void *keys, const void *values, int dtype, const int64_t *k_strides,
+                      const int64_t *v_strides, int64_t B, int64_t H, int64_t T, int64_t D,
+                      int64_t count, int64_t sample_stride, int min_error,
+                      uint8_t *k_payload, float *k_scales, void *k_src, void *k_don, float *k_padding,
+                      uint8_t *v_payload, float *v_scales, void *v_src, void *v_don, float *v_padding,
+                      int desc_bytes, int *key_bad, int *value_bad, void *stream);
 
 /* Value decode: out [rows, D] of out_dtype (rows = B*H*T); value_codec.py:38-48. */
 int iq_v_dequantize(const uint8_t *payload, const uint16_t *scales, const uint16_t *offsets,

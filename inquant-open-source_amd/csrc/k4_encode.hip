@@ -288,8 +288,10 @@ __device__ __forceinline__ float tile_f32(uint32_t bits16)
 // PAGES: the row goes into a physical page, values V2 with 64-channel groups.
 // VB = 2 / 4 (not PAGES): the row's values are encoded too, VB bits with
 // 16 * VGL-channel groups, into the outputs of iq_v_quantize.
+// The body of one workgroup: row (b, h) of the encode `a`; `lin` is the
+// workgroup's linear index (neighbouring blocks alternate their wave roles).
 template <bool F16IN, int NCH, bool PAGES = false, int VB = 0, int VGL = 4>
-__global__ __launch_bounds__(K4_THREADS, 4) void k4_encode_tile(K4Args a)
+__device__ __forceinline__ void k4_tile_body(const K4Args &a, int64_t b, int64_t h, int lin)
 {
     constexpr int VBITS = PAGES ? 2 : VB;
     constexpr int GLV = PAGES ? 4 : VGL;
@@ -313,8 +315,6 @@ __global__ __launch_bounds__(K4_THREADS, 4) void k4_encode_tile(K4Args a)
     __shared__ int s_bad;
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    // grid (blocks, heads): no 64-bit division for the row's coordinates
-    const int64_t b = blockIdx.x, h = blockIdx.y;
     const int64_t row = b * a.H + h;
     uint8_t *page = nullptr;
     __shared__ int16_t s_role[TILE_D];
@@ -418,7 +418,7 @@ __global__ __launch_bounds__(K4_THREADS, 4) void k4_encode_tile(K4Args a)
     // tid & 127) and two the sums; which pair does which alternates between
     // neighbouring blocks, so that the blocks sharing a compute unit spread
     // the fp64 chains over all four SIMDs instead of stacking them on two.
-    const bool welford = ((tid >> 7) ^ (int)(((blockIdx.x + gridDim.x * blockIdx.y) >> 8) & 1)) == 0;
+    const bool welford = ((tid >> 7) ^ ((lin >> 8) & 1)) == 0;
     // The Welford chains are the critical path of pass 1 (the sums waves
     // then wait at every chunk barrier), so their waves issue first.
     if (welford && a.min_error) __builtin_amdgcn_s_setprio(2);
@@ -702,6 +702,24 @@ __global__ __launch_bounds__(K4_THREADS, 4) void k4_encode_tile(K4Args a)
     });
 }
 
+// grid (blocks, heads): no 64-bit division for the row's coordinates
+template <bool F16IN, int NCH, bool PAGES = false, int VB = 0, int VGL = 4>
+__global__ __launch_bounds__(K4_THREADS, 4) void k4_encode_tile(K4Args a)
+{
+    k4_tile_body<F16IN, NCH, PAGES, VB, VGL>(a, blockIdx.x, blockIdx.y, (int)(blockIdx.x + gridDim.x * blockIdx.y));
+}
+
+// Keys and values of the same blocks, both K4, in one launch: grid (blocks,
+// 2 H), rows h < H of the keys `ak`, the others of the values `av`.
+template <bool F16IN, int NCH>
+__global__ __launch_bounds__(K4_THREADS, 4) void k4_encode_pair(K4Args ak, K4Args av)
+{
+    const bool val = (int64_t)blockIdx.y >= ak.H;
+    const K4Args a = val ? av : ak;
+    k4_tile_body<F16IN, NCH>(a, blockIdx.x, val ? blockIdx.y - ak.H : blockIdx.y,
+                             (int)(blockIdx.x + gridDim.x * blockIdx.y));
+}
+
 struct SelectArgs {
     const float *sal, *err;
     int64_t D, count;
@@ -732,6 +750,18 @@ __global__ __launch_bounds__(64) void reuse_map_kernel(SelectArgs a)
 
 }  // namespace
 
+namespace {
+
+// the tile encoder's layout: 16-bit channel-contiguous rows of 128 channels,
+// 16-byte aligned, at most 256 tokens, 32-bit lane offsets within a chunk
+bool tile_ok(const void *x, int dtype, const int64_t *s, int64_t T, int64_t D)
+{
+    return (dtype == IQ_BF16 || dtype == IQ_F16) && D == TILE_D && T <= TILE_T && s[3] == 1 && s[2] % 8 == 0 &&
+           s[1] % 8 == 0 && s[0] % 8 == 0 && ((uintptr_t)x & 15) == 0 && s[2] >= 0 && s[2] <= (1 << 24);
+}
+
+}  // namespace
+
 extern "C" int iq_k4_quantize(const void *x, int x_dtype, const int64_t *x_strides, int64_t B, int64_t H,
                               int64_t T, int64_t D, int64_t count, int64_t sample_stride, int min_error,
                               uint8_t *payload, float *scales, void *src, void *don, int desc_bytes,
@@ -749,11 +779,7 @@ extern "C" int iq_k4_quantize(const void *x, int x_dtype, const int64_t *x_strid
     IQ_CHECK_ARG(B * H <= 0x7fffffffLL, "iq_k4_quantize: too many rows");
     K4Args a{x, x_dtype, x_strides[0], x_strides[1], x_strides[2], x_strides[3], H, T, D, count, sample_stride,
              min_error ? 1 : 0, payload, scales, src, don, desc_bytes, padding, bad_flag};
-    const bool tile = (x_dtype == IQ_BF16 || x_dtype == IQ_F16) && D == TILE_D && T <= TILE_T && H <= 65535 &&
-                      x_strides[3] == 1 && x_strides[2] % 8 == 0 && x_strides[1] % 8 == 0 &&
-                      x_strides[0] % 8 == 0 && ((uintptr_t)x & 15) == 0 && x_strides[2] >= 0 &&
-                      x_strides[2] <= (1 << 24);   // 32-bit lane offsets within a chunk
-    if (tile) {
+    if (tile_ok(x, x_dtype, x_strides, T, D) && H <= 65535) {
         const dim3 grid((unsigned)B, (unsigned)H), block(K4_THREADS);
         const hipStream_t st = (hipStream_t)stream;
         if (x_dtype == IQ_F16) {
@@ -855,6 +881,46 @@ extern "C" int iq_kv_quantize(const void *keys, const void *values, int dtype, c
         else launch_kv_tile<false, 4>(VGL, grid, st, a);
     }
     IQ_CHECK_LAUNCH("k4_encode_tile (keys and values)");
+    return IQ_OK;
+}
+
+extern "C" int iq_k4_quantize_kv(const void *keys, const void *values, int dtype, const int64_t *k_strides,
+                                 const int64_t *v_strides, int64_t B, int64_t H, int64_t T, int64_t D, int64_t count,
+                                 int64_t sample_stride, int min_error, uint8_t *k_payload, float *k_scales,
+                                 void *k_src, void *k_don, float *k_padding, uint8_t *v_payload, float *v_scales,
+                                 void *v_src, void *v_don, float *v_padding, int desc_bytes, int *key_bad,
+                                 int *value_bad, void *stream)
+{
+    IQ_CHECK_ARG(keys && values && k_strides && v_strides && key_bad && value_bad, "iq_k4_quantize_kv: null pointer");
+    const bool fused = tile_ok(keys, dtype, k_strides, T, D) && tile_ok(values, dtype, v_strides, T, D) && B >= 1 &&
+                       B <= 0x7fffffffLL && H >= 1 && 2 * H <= 65535 && T >= 1 && count >= 0 && 2 * count <= D &&
+                       sample_stride >= 1 && (desc_bytes == 1 || desc_bytes == 4 || desc_bytes == 8) &&
+                       k_payload && k_scales && v_payload && v_scales &&
+                       (count == 0 || (k_src && k_don && k_padding && v_src && v_don && v_padding));
+    if (!fused) {
+        // any other shape: the two encodes back to back on the stream
+        const int rk = iq_k4_quantize(keys, dtype, k_strides, B, H, T, D, count, sample_stride, min_error, k_payload,
+                                      k_scales, k_src, k_don, desc_bytes, k_padding, key_bad, stream);
+        if (rk != IQ_OK) return rk;
+        return iq_k4_quantize(values, dtype, v_strides, B, H, T, D, count, sample_stride, min_error, v_payload,
+                              v_scales, v_src, v_don, desc_bytes, v_padding, value_bad, stream);
+    }
+    const K4Args ak{keys, dtype, k_strides[0], k_strides[1], k_strides[2], k_strides[3], H, T, D, count,
+                    sample_stride, min_error ? 1 : 0, k_payload, k_scales, k_src, k_don, desc_bytes, k_padding,
+                    key_bad};
+    const K4Args av{values, dtype, v_strides[0], v_strides[1], v_strides[2], v_strides[3], H, T, D, count,
+                    sample_stride, min_error ? 1 : 0, v_payload, v_scales, v_src, v_don, desc_bytes, v_padding,
+                    value_bad};
+    const dim3 grid((unsigned)B, (unsigned)(2 * H)), block(K4_THREADS);
+    const hipStream_t st = (hipStream_t)stream;
+    if (dtype == IQ_F16) {
+        if (T == TILE_T) hipLaunchKernelGGL((k4_encode_pair<true, TILE_T / CH>), grid, block, 0, st, ak, av);
+        else hipLaunchKernelGGL((k4_encode_pair<true, 0>), grid, block, 0, st, ak, av);
+    } else {
+        if (T == TILE_T) hipLaunchKernelGGL((k4_encode_pair<false, TILE_T / CH>), grid, block, 0, st, ak, av);
+        else hipLaunchKernelGGL((k4_encode_pair<false, 0>), grid, block, 0, st, ak, av);
+    }
+    IQ_CHECK_LAUNCH("k4_encode_pair");
     return IQ_OK;
 }
 

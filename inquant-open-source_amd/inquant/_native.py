@@ -57,6 +57,8 @@ _SIGNATURES = {
     "iq_v_dequantize": (_int, [_p, _p, _p, _i64, _i64, _int, _int, _p, _int, _p]),
     "iq_kv_quantize": (_int, [_p, _p, _int, ctypes.POINTER(_i64), ctypes.POINTER(_i64), _i64, _i64, _i64, _i64,
                               _i64, _i64, _int, _p, _p, _p, _p, _int, _p, _int, _int, _p, _p, _p, _p, _p, _p]),
+    "iq_k4_quantize_kv": (_int, [_p, _p, _int, ctypes.POINTER(_i64), ctypes.POINTER(_i64), _i64, _i64, _i64, _i64,
+                                 _i64, _i64, _int, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _int, _p, _p, _p]),
     "iq_decode_append": (_int, [_p, _p, _p, _i64, _i64, ctypes.POINTER(BlockPtrs), _i64, _i64, _int, _p]),
     "iq_decode_workspace_floats": (_i64, [_i64, _i64, _i64, _i64]),
     "iq_decode_attention": (_int, [_p, _int, _i64, _i64, _p, _p, _p, ctypes.POINTER(BlockRun), _i64, _i64, _i64,

@@ -254,6 +254,48 @@ def _kv_blocks(keys: torch.Tensor, values: torch.Tensor, block_count: int, block
             _per_block(packed_v, block_count, shape, PackedValues, bits=bits, group_size=group_size))
 
 
+def _k4_pair_blocks(keys: torch.Tensor, values: torch.Tensor, block_count: int, block_size: int,
+                    config: CodecConfig, key_flag: torch.Tensor, value_flag: torch.Tensor):
+    """K4 keys and K4-coded values (value_bits None) of the first
+    ``block_count`` blocks in one library call (iq_k4_quantize_kv: one launch
+    for 16-bit blocks of 128 channels), with the per-block objects and flags
+    of two _quantize_temporal_blocks calls (cache.py:288-291)."""
+    if block_count == 0:
+        return [], []
+    _, heads, _, dim = keys.shape
+    native = (keys.dtype == values.dtype and keys.dtype in (torch.float32, torch.bfloat16, torch.float16)
+              and keys.shape == values.shape and dim % 2 == 0 and dim <= 1024)
+    if not native:      # the separate encodes, with their own argument errors
+        return (_quantize_temporal_blocks(keys, block_count, block_size, config, key_flag),
+                _quantize_temporal_blocks(values, block_count, block_size, config, value_flag))
+    device = nat.require_gpu(keys, what="quantize")
+
+    def blocked(t):
+        return t[0, :, :block_count * block_size].unflatten(1, (block_count, block_size)).transpose(0, 1)
+
+    kb, vb = blocked(keys), blocked(values)
+    B, H, T, D = kb.shape
+    count = math.floor(D * config.salient_fraction)
+    desc_dtype = torch.uint8 if D <= 256 else torch.int32
+
+    def outputs():
+        return (torch.empty((B, H, T, D // 2), dtype=torch.uint8, device=device),
+                torch.empty((B, H, D), dtype=torch.float32, device=device),
+                torch.empty((B, H, count), dtype=desc_dtype, device=device),
+                torch.empty((B, H, count), dtype=desc_dtype, device=device),
+                torch.empty((B, H, count), dtype=torch.float32, device=device))
+
+    ko, vo = outputs(), outputs()
+    ptrs = lambda o: [o[0].data_ptr(), o[1].data_ptr()] + [t.data_ptr() if count else None for t in o[2:]]
+    nat.check(nat.lib().iq_k4_quantize_kv(
+        kb.data_ptr(), vb.data_ptr(), nat.dtype_code(kb.dtype), nat.strides4(kb), nat.strides4(vb), B, H, T, D,
+        count, config.sample_stride, int(config.donor_policy == "min_error"), *ptrs(ko), *ptrs(vo),
+        ko[2].element_size(), key_flag.data_ptr(), value_flag.data_ptr(), nat.stream_handle(device)))
+    shape = (1, heads, block_size, dim)
+    return (_per_block(PackedTensor(*ko, tuple(kb.shape), keys.dtype), block_count, shape, PackedTensor),
+            _per_block(PackedTensor(*vo, tuple(vb.shape), values.dtype), block_count, shape, PackedTensor))
+
+
 class InQuantCache(_HFCache):
     """Immutable packed history, exact sink and a bounded exact tail
     (batch 1, append-only), as src/inquant/cache.py:122-419."""
@@ -478,10 +520,8 @@ class InQuantCache(_HFCache):
         flags = self._flag_words(keys.device)
         flags[:_POSITION_BAD].zero_()
         if cfg.value_bits is None:
-            new_keys = _quantize_temporal_blocks(keys, count, cfg.block_size, cfg.codec,
-                                                 flags[_KEY_BAD:_KEY_BAD + 1])
-            new_values = _quantize_temporal_blocks(values, count, cfg.block_size, cfg.codec,
-                                                   flags[_VALUE_BAD:_VALUE_BAD + 1])
+            new_keys, new_values = _k4_pair_blocks(keys, values, count, cfg.block_size, cfg.codec,
+                                                   flags[_KEY_BAD:_KEY_BAD + 1], flags[_VALUE_BAD:_VALUE_BAD + 1])
             value_error = _BAD_K
         else:
             new_keys, new_values = _kv_blocks(keys, values, count, cfg.block_size, cfg.codec, cfg.value_bits,

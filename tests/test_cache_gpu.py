@@ -108,8 +108,10 @@ def test_sink_accumulates_across_short_prefills():
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 def test_batched_prefill_matches_serial_blocks_and_owns_compact_storage(dtype):
     # test_cache.py:69-108: heads and temporal blocks keep independent
-    # statistics after the block axis moves into the batch; one encode call
-    # per tensor, every field an owned compact tensor
+    # statistics after the block axis moves into the batch; the reference
+    # makes one encode call per tensor, this cache one library call for the
+    # keys and values of all six blocks (iq_k4_quantize_kv over the strided
+    # [6, 3, 8, 16] views); every field an owned compact tensor
     import inquant.cache as cache_mod
     from inquant.cache import InQuantCache
     from inquant.codec import CodecConfig, quantize
@@ -121,10 +123,11 @@ def test_batched_prefill_matches_serial_blocks_and_owns_compact_storage(dtype):
         key[:, index % 3, 2 + index * 8:10 + index * 8, index] *= 20
         value[:, (index + 1) % 3, 2 + index * 8:10 + index * 8, 15 - index] *= 17
     cache = InQuantCache(cfg)
-    with patch.object(cache_mod, "quantize", wraps=quantize) as observed:
+    with patch.object(cache_mod, "_k4_pair_blocks", wraps=cache_mod._k4_pair_blocks) as observed, \
+            patch.object(cache_mod, "quantize", wraps=quantize) as single:
         cache.update(key, value, 0)
-    assert observed.call_count == 2
-    assert tuple(observed.call_args_list[0].args[0].shape) == (6, 3, 8, 16)
+    assert observed.call_count == 1 and single.call_count == 0
+    assert observed.call_args.args[2:4] == (6, 8)
     layer = cache._layers[0]
     expected_bytes = 0
     ranges, storages = [], {}

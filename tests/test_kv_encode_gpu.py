@@ -1,9 +1,11 @@
-"""GPU parity of iq_kv_quantize, the cache's paired key / value block encode
-(cache.py:288-295): one launch for sealed 256-token blocks of 128 16-bit
-channels (K4 keys, the values encoded by the same workgroups), the two
-encoders back to back otherwise.  Every output is bit-identical to
+"""GPU parity of the cache's paired key / value block encodes
+(cache.py:288-295).  iq_kv_quantize (V2/V4 values): one launch for sealed
+256-token blocks of 128 16-bit channels (K4 keys, the values encoded by the
+same workgroups), the two encoders back to back otherwise; bit-identical to
 iq_k4_quantize + iq_v_quantize (themselves pinned to the oracle and the
-reference's goldens) and, at config 3's shape, to the oracle directly."""
+reference's goldens) and, at config 3's shape, to the oracle directly.
+iq_k4_quantize_kv (K4-coded values): one launch over (blocks, 2 heads),
+bit-identical to two iq_k4_quantize calls."""
 import numpy as np
 import pytest
 import torch
@@ -77,7 +79,7 @@ def _same(a: dict, b: dict):
 
 def _blocks(t, nb, B=256):
     """The cache's strided [blocks, H, B, D] view of [1, H, nb * B, D]."""
-    return t[0].unflatten(1, (nb, B)).transpose(0, 1)
+    return t[0, :, :nb * B].unflatten(1, (nb, B)).transpose(0, 1)
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
@@ -183,3 +185,98 @@ def test_cache_seal_of_full_blocks_uses_the_fused_encode(bits, group):
         np.testing.assert_array_equal(_np(vblock.scales[0]).view(np.uint16), _np(sv["scales"][i]).view(np.uint16))
         np.testing.assert_array_equal(_np(vblock.offsets[0]).view(np.uint16),
                                       _np(sv["offsets"][i]).view(np.uint16))
+
+
+def _k4_pair(k, v, fraction, policy, stride=8):
+    """iq_k4_quantize_kv on [B, H, T, D] views; returns (key fields, value fields, flags)."""
+    from inquant import _native as nat
+    B, H, T, D = k.shape
+    count = int(D * fraction)
+    dev = k.device
+
+    def outputs():
+        return {"payload": torch.empty((B, H, T, D // 2), dtype=torch.uint8, device=dev),
+                "scales": torch.empty((B, H, D), dtype=torch.float32, device=dev),
+                "salient_channels": torch.empty((B, H, count), dtype=torch.uint8, device=dev),
+                "donor_channels": torch.empty((B, H, count), dtype=torch.uint8, device=dev),
+                "padding": torch.empty((B, H, count), dtype=torch.float32, device=dev)}
+
+    ko, vo = outputs(), outputs()
+    ptrs = lambda o: [o["payload"].data_ptr(), o["scales"].data_ptr()] + [
+        o[n].data_ptr() if count else None for n in ("salient_channels", "donor_channels", "padding")]
+    flags = torch.zeros(2, dtype=torch.int32, device=dev)
+    nat.check(nat.lib().iq_k4_quantize_kv(
+        k.data_ptr(), v.data_ptr(), nat.dtype_code(k.dtype), nat.strides4(k), nat.strides4(v), B, H, T, D, count,
+        stride, int(policy == "min_error"), *ptrs(ko), *ptrs(vo), 1, flags.data_ptr(), flags.data_ptr() + 4,
+        nat.stream_handle(dev)))
+    torch.cuda.synchronize()
+    return ko, vo, flags.tolist()
+
+
+def _k4_separate(k, v, fraction, policy, stride=8):
+    from inquant.codec import CodecConfig, quantize
+    cfg = CodecConfig(sample_stride=stride, salient_fraction=fraction, donor_policy=policy)
+    return quantize(k, cfg).tensors, quantize(v, cfg).tensors
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("T", [256, 100])
+@pytest.mark.parametrize("fraction,policy", [(0.125, "min_error"), (0.125, "neighbors"), (0.0, "min_error"),
+                                             (0.5, "neighbors")])
+def test_k4_pair_equals_two_key_encodes(dtype, T, fraction, policy):
+    # K4-coded values (the cache's default): one launch over (blocks, 2 H)
+    # rows, bit-identical to two iq_k4_quantize calls (256-token blocks take
+    # the direct-to-LDS variant, 100-token rows the other)
+    print(f"k4 pair {dtype} T {T} {fraction} {policy}", flush=True)
+    k, v = _kv(51, (1, 3, 5 * T, 128), dtype)
+    kb, vb = _blocks(k, 5, T), _blocks(v, 5, T)
+    fk, fv, flags = _k4_pair(kb, vb, fraction, policy)
+    sk, sv = _k4_separate(kb, vb, fraction, policy)
+    assert flags == [0, 0]
+    _same(fk, sk)
+    _same(fv, sv)
+
+
+@pytest.mark.parametrize("shape,dtype", [((2, 2, 256, 64), torch.float16), ((1, 2, 256, 128), torch.float32)])
+def test_k4_pair_other_shapes_run_two_encodes(shape, dtype):
+    print(f"k4 pair fallback {shape} {dtype}", flush=True)
+    k, v = _kv(61, shape, dtype, runs=(1,))
+    fk, fv, flags = _k4_pair(k, v, 0.125, "min_error")
+    sk, sv = _k4_separate(k, v, 0.125, "min_error")
+    assert flags == [0, 0]
+    _same(fk, sk)
+    _same(fv, sv)
+
+
+@pytest.mark.parametrize("where", ["key", "value"])
+def test_k4_pair_nonfinite_flags(where):
+    print(f"k4 pair nonfinite {where}", flush=True)
+    k, v = _kv(71, (1, 2, 2 * 256, 128), torch.bfloat16)
+    (k if where == "key" else v)[0, 1, 300, 50] = float("nan")
+    _, _, flags = _k4_pair(_blocks(k, 2), _blocks(v, 2), 0.125, "min_error")
+    assert flags == [int(where == "key"), int(where == "value")]
+
+
+def test_cache_seal_with_k4_values_uses_one_launch():
+    # value_bits None (K4-coded values): the cache's blocks equal two
+    # separate encodes of the same rows, and one launch encodes them
+    print("cache k4 pair seal", flush=True)
+    from inquant.cache import CacheConfig, InQuantCache
+    from inquant.codec import CodecConfig
+    cfg = CacheConfig(CodecConfig(donor_policy="min_error"), block_size=256, residual_length=128, sink_tokens=4)
+    cache = InQuantCache(cfg)
+    k, v = _kv(81, (1, 4, 4 + 2 * 256 + 150, 128), torch.bfloat16)
+    with torch.profiler.profile(activities=[torch.profiler.ProfilerActivity.CUDA]) as prof:
+        cache.update(k, v, 0)
+        torch.cuda.synchronize()
+    names = [e.name for e in prof.events()]
+    assert sum("k4_encode_pair" in n for n in names) == 1 and not any("k4_encode_tile" in n for n in names)
+    layer = cache._layers[0]
+    assert len(layer.key_blocks) == 2
+    kb, vb = _blocks(k[:, :, 4:4 + 512], 2), _blocks(v[:, :, 4:4 + 512], 2)
+    sk, sv = _k4_separate(kb, vb, 0.125, "min_error")
+    for i, (kblock, vblock) in enumerate(zip(layer.key_blocks, layer.value_blocks)):
+        for name, t in kblock.tensors.items():
+            np.testing.assert_array_equal(_np(t[0]).view(np.uint8), _np(sk[name][i]).view(np.uint8), name)
+        for name, t in vblock.tensors.items():
+            np.testing.assert_array_equal(_np(t[0]).view(np.uint8), _np(sv[name][i]).view(np.uint8), name)
