@@ -17,6 +17,7 @@ typedef __attribute__((ext_vector_type(4))) float f32x4;
 typedef __attribute__((ext_vector_type(2))) float f32x2;
 typedef __attribute__((ext_vector_type(4))) uint32_t u32x4;
 typedef __attribute__((ext_vector_type(2))) uint32_t u32x2;
+typedef __attribute__((ext_vector_type(4))) int i32x4;
 
 template <bool F16>
 __device__ __forceinline__ uint32_t pack2(float a, float b)
@@ -137,6 +138,13 @@ __device__ __forceinline__ T ldnt(const void *p)
 {
     return __builtin_nontemporal_load((const __attribute__((address_space(1))) T *)p);
 }
+
+// Orders LDS writes of this wavefront's lanes before reads of other lanes
+// after it.  A wavefront's LDS operations complete in issue order, so no
+// instruction is needed; the fence only keeps the compiler from reusing a
+// value a lane read before (its per-thread model does not see other lanes'
+// writes without synchronization).
+__device__ __forceinline__ void wave_lds_sync() { __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront"); }
 
 constexpr float NEG_INF = -__builtin_inff();
 

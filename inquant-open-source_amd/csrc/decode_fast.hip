@@ -54,7 +54,6 @@ constexpr int DENSE_SPLIT = 256;
 constexpr int QROW = D + 8;            // u16 per staged query row (+8: the 16 rows of a B-operand read hit distinct banks)
 constexpr float LN2 = 0.693147180559945309f;
 
-typedef __attribute__((ext_vector_type(4))) int i32x4;
 
 struct FastArgs {
     // the leading run of blocks laid out at a fixed stride (a batched encode):
@@ -524,6 +523,7 @@ __device__ __forceinline__ void fast_body(const FastArgs &a, FastSmem &sm)
 #pragma unroll
         for (int m = 0; m < 2; ++m) {
             uint32_t *dst = vt + pl * VR + 32 * qq;    // pair row pl, channels 32 qq .. 32 qq + 31
+            if (m > 0) wave_lds_sync();                // every lane has read half chunk m - 1
             if (packed && K4V) {
                 // pair row gl (tokens 16 (2 m) + gl and 16 (2 m + 1) + gl: this
                 // lane's rows of tiles 2 m and 2 m + 1), channels 32 ql + 8 d + i,
@@ -668,6 +668,7 @@ __device__ __forceinline__ void fast_body(const FastArgs &a, FastSmem &sm)
                     *(u32x4 *)(dst + 8 * i + 4) = u32x4{lo[2], hi[2], lo[3], hi[3]};
                 }
             }
+            wave_lds_sync();                           // the tile's rows come from other lanes
 #pragma unroll
             for (int n = 0; n < 8; ++n) {
                 u32x4 va;                              // k-slot pair r: pair row 4 ql + r

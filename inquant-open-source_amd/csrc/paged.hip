@@ -31,7 +31,7 @@ constexpr int D = 128;
 constexpr int WAVES = 4;
 constexpr int PART = 256;              // tokens per partition
 constexpr int VR = 132;                // dwords per staged token-pair row of decoded V (pairs t, t + 16)
-constexpr int KROW = 17;               // dwords per staged K row (salient byte gathers)
+constexpr int SELROW = D + 16;         // bytes per selection-matrix row (+16: the 16 rows of a read hit distinct banks)
 constexpr int OROW = 132;              // floats per staged output row in the combine (conflict-free 16-byte stores)
 constexpr int QROW = D + 8;            // u16 per staged query row (+8: rows of one column spread over the banks)
 constexpr int SPG = 16;                // salient channels per page (the layout's key_padding width)
@@ -220,17 +220,17 @@ __device__ __forceinline__ int page_of_wave(int npg, int wave)
 // Workgroup LDS of decode_paged, shared by its packed and dense bodies.
 // Each wavefront's slot of v (SLOT bytes) holds in turn: the (s * 2^9, -8 s)
 // K constant pairs of its pages [0, SETUP_OFF) and their donor bias
-// [BIAS_OFF, SLOT) up to Q.K; then K staging for the salient gathers
-// [0, SETUP_OFF); then its decoded V tiles and its combine rows (the whole
+// [BIAS_OFF, SLOT) up to Q.K; then the salient selection matrix of one page
+// at a time; then its decoded V tiles and its combine rows (the whole
 // slot).  Until the per-page tables are built, [SETUP_OFF, BIAS_OFF) of
 // slots 0 and 1 hold the role-resolution arrays of every page.  At 16-token
 // pages a workgroup takes 40,704 bytes: four per compute unit.
 constexpr int SLOT = 16 * VR * 4;          // bytes per wavefront slot
 constexpr int KAP_GROUP = 34;              // pairs per 32-channel group (+2: the four groups on distinct banks)
 constexpr int KAP_PAGE = 4 * KAP_GROUP;    // pairs per page
-constexpr int SETUP_OFF = 64 * KROW * 4;   // bytes: past the K staging
+constexpr int SETUP_OFF = 4 * KAP_PAGE * 8;   // bytes: past the constant pairs of four pages
 constexpr int BIAS_OFF = SLOT - 4 * 16 * 4;
-static_assert(4 * KAP_PAGE * 8 <= SETUP_OFF, "constant pairs of four pages fit below the setup arrays");
+static_assert(16 * SELROW <= SETUP_OFF, "a page's selection matrix fits below the setup arrays");
 
 template <int NPG>
 struct __attribute__((aligned(16))) PagedSmem {
@@ -489,27 +489,54 @@ __device__ __forceinline__ void paged_body(const PagedArgs &a, PagedSmem<NPG> &s
                 }
                 sc[j] = s;
             }
-            // salient terms: stage the K tiles as [64 tokens][17 dwords], gather codes
+            // salient terms: the codes 16 hi + lo - 128 come from two int8
+            // products of the page's selection matrix (row k: 16 at the byte of
+            // descriptor k's source, 1 at its donor's; channel c at byte
+            // (c & 1) * 64 + c / 2) with the tile's nibble planes, so lane
+            // (token gl, ql) receives the codes of descriptors 4 ql + r: the A
+            // operand of the salient product.  The matrix is built in this
+            // wavefront's slot (free after Q.K), one page at a time: each new
+            // page clears the previous page's 32 bytes and sets its own.
+            uint8_t *const ssel = (uint8_t *)vt;
 #pragma unroll
-            for (int j = 0; j < 4; ++j)
-#pragma unroll
-                for (int w = 0; w < 4; ++w) vt[(16 * j + gl) * KROW + 4 * ql + w] = kw[j][w];
-            const uint8_t *kt = (const uint8_t *)vt;
+            for (int i = lane; i < 16 * SELROW / 16; i += 64) *(u32x4 *)(ssel + 16 * i) = u32x4{0u, 0u, 0u, 0u};
+            wave_lds_sync();
+            uint32_t mark = 0;                          // lanes 0-31: the byte this lane set
+            i32x4 sel_lo = {0, 0, 0, 0}, sel_hi = {0, 0, 0, 0};
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
                 const int lp = (base + 16 * j) / B;
-                const uint8_t *rowp = kt + (16 * j + gl) * (4 * KROW);
+                if (j == 0 || (16 * j) % B == 0) {      // the tile starts a page
+                    if (lane < 32) {
+                        const uint32_t w = sm.salw[lp][lane & 15];
+                        const uint32_t f = lane < 16 ? w & 0xffffu : w >> 16;      // (byte, 4 * parity)
+                        const uint32_t at = (lane & 15) * SELROW + (f & 0xffu) + ((f >> 8) << 4);
+                        if (j > 0) ssel[mark] = 0;
+                        ssel[at] = lane < 16 ? 16 : 1;
+                        mark = at;
+                    }
+                    wave_lds_sync();
+                    sel_lo = *(const i32x4 *)(ssel + gl * SELROW + 16 * ql);
+                    sel_hi = *(const i32x4 *)(ssel + gl * SELROW + D / 2 + 16 * ql);
+                }
+                i32x4 lo4, hi4;
+#pragma unroll
+                for (int d = 0; d < 4; ++d) {
+                    lo4[d] = (int)(kw[j][d] & 0x0f0f0f0fu);
+                    hi4[d] = (int)((kw[j][d] >> 4) & 0x0f0f0f0fu);
+                }
+                i32x4 code = __builtin_amdgcn_mfma_i32_16x16x64_i8(sel_lo, lo4, i32x4{-128, -128, -128, -128}, 0, 0, 0);
+                code = __builtin_amdgcn_mfma_i32_16x16x64_i8(sel_hi, hi4, code, 0, 0, 0);
+                const f32x4 ssc = *(const f32x4 *)&sm.ssc[lp][4 * ql];
                 float v[4];
                 uint32_t qv[4];
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
-                    const uint32_t w = sm.salw[lp][4 * ql + e];
                     // Q[g][source channel]; the source is 2 (w & 255) + ((w >> 8) & 255) / 4
+                    const uint32_t w = sm.salw[lp][4 * ql + e];
                     qv[e] = s_q[gl * QROW + 2 * (w & 0xffu) + (((w >> 8) & 0xffu) >> 2)];
-                    const uint32_t hi = (rowp[w & 0xffu] >> ((w >> 8) & 0xffu)) & 15u;
-                    const uint32_t lo = (rowp[(w >> 16) & 0xffu] >> (w >> 24)) & 15u;
                     // (code - 128) * s in one rounding, as the reference's multiply
-                    v[e] = (float)((int)((hi << 4) | lo) - 128) * sm.ssc[lp][4 * ql + e];
+                    v[e] = (float)code[e] * ssc[e];
                 }
                 const u32x2 ka = {pack2<false>(v[0], v[1]), pack2<false>(v[2], v[3])};
                 const u32x2 qs = {qv[0] | (qv[1] << 16), qv[2] | (qv[3] << 16)};
@@ -579,6 +606,7 @@ __device__ __forceinline__ void paged_body(const PagedArgs &a, PagedSmem<NPG> &s
 #pragma unroll
         for (int m = 0; m < 2; ++m) {
             uint32_t *dst = vt + pl * VR + 32 * qq;    // pair row pl, channels 32 qq .. 32 qq + 31
+            if (m > 0) wave_lds_sync();                // every lane has read half chunk m - 1
             if constexpr (PACKED) {
                 // dead tokens decode to zero: a zero weight times a non-finite
                 // value (a page outside the pool) would still poison P.V
@@ -637,6 +665,7 @@ __device__ __forceinline__ void paged_body(const PagedArgs &a, PagedSmem<NPG> &s
                     *(u32x4 *)(dst + 8 * i + 4) = u32x4{lo[2], hi[2], lo[3], hi[3]};
                 }
             }
+            wave_lds_sync();                           // the tile's rows come from other lanes
 #pragma unroll
             for (int n = 0; n < 8; ++n) {
                 u32x4 va;                              // k-slot pair r: pair row 4 ql + r
