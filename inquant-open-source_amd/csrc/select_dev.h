@@ -266,6 +266,10 @@ __device__ __forceinline__ void iq_select_tile128(const float *sal, const float 
     const uint64_t below = (1ull << lane) - 1;
     if (f0 & 1u) list[__popcll(sel0 & below)] = (int16_t)lane;
     if (f1 & 1u) list[__popcll(sel0) + __popcll(sel1 & below)] = (int16_t)(64 + lane);
+    // lanes read list entries other lanes of this wavefront wrote: LDS
+    // operations of a wavefront complete in order, so this fence emits
+    // nothing; it keeps the compiler from moving the reads above the writes
+    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
     is_src[lane] = (uint8_t)(f0 & 1u);
     is_src[64 + lane] = (uint8_t)(f1 & 1u);
     src_of[lane] = -1;
