@@ -1,7 +1,7 @@
 // Fused single-query GQA decode attention over [sink | packed blocks | tail].
 //
 // Semantics follow PackedDecodeState.decode (triton_attention.py:317-388):
-// one partition per packed block and per 256-token slice of the dense
+// one partition per packed block and per 32-token slice of the dense
 // sink and tail; keys and values are decoded from the K4 / V2 / V4 formats
 // (_decode_tile :33-50, _decode_value_tile :53-64), rounded to the query
 // dtype exactly as the dequantize-then-attend path does, and each
@@ -21,7 +21,7 @@ constexpr int DA_THREADS = 256;
 constexpr int TILE = 32;
 constexpr int D = 128;
 constexpr int GMAX = 16;
-constexpr int DENSE_SPLIT = 256;
+constexpr int DENSE_SPLIT = 32;     // as the matrix-core path, so one workspace size covers both
 
 struct DecodeArgs {
     const void *q;

@@ -2,7 +2,7 @@
 //
 // Same semantics and partial format as decode_partials_generic
 // (triton_attention.py:67-165): one workgroup per (KV head, partition),
-// partitions = packed blocks then 256-token slices of sink and tail; keys and
+// partitions = packed blocks then 32-token slices of sink and tail; keys and
 // values are decoded and rounded to the query dtype exactly as the
 // dequantize-then-attend path does.  Each of the 4 wavefronts owns a
 // 64-token chunk of the partition.
@@ -50,7 +50,11 @@ constexpr int VR = 132;                // dwords per staged token-pair row of de
 constexpr int SELROW = D + 16;         // bytes per selection-matrix row (+16: the 16 rows of a read hit distinct banks)
 constexpr int OROW = 132;              // floats per staged output row in the combine (128 + 4: conflict-free 16-byte stores)
 constexpr int KC_STRIDE = 68;          // float2 slots per 32-channel group of K constants (+4: no bank overlap)
-constexpr int DENSE_SPLIT = 256;
+// Dense (sink ++ tail) partitions are 32 tokens: they are dispatched after
+// the packed blocks, into the slots left once every packed workgroup is
+// resident (or beside two packed workgroups on a compute unit), so a short
+// one adds the least time after the packed workgroups finish.
+constexpr int DENSE_SPLIT = 32;
 constexpr int QROW = D + 8;            // u16 per staged query row (+8: the 16 rows of a B-operand read hit distinct banks)
 constexpr float LN2 = 0.693147180559945309f;
 
@@ -756,7 +760,7 @@ __global__ __launch_bounds__(256, VBITS == 0 ? 3 : 4) void decode_fast(FastArgs 
 #undef IQ_LOAD_CHUNK
 
 // Launches the matrix-core decode; returns IQ_ERR_UNSUPPORTED for layouts it
-// does not cover.  Partitions are the packed blocks, then 256-token slices of
+// does not cover.  Partitions are the packed blocks, then 32-token slices of
 // sink ++ tail; *parts receives their count.  With one partition the output is
 // written in-kernel, otherwise the caller merges *parts partials.
 int iq_decode_fast_launch(const void *q, int q_dtype, int64_t q_stride_h, int64_t Hq, const int64_t *tables,

@@ -35,7 +35,7 @@ from . import _native as nat
 from .codec import PackedTensor
 from .value_codec import PackedValues
 
-_SPLIT = 256          # tokens per dense partition
+_SPLIT = 32           # tokens per dense partition (the native kernels' split)
 _COLUMNS = 8          # pointer-table columns
 
 

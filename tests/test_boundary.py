@@ -36,7 +36,8 @@ def test_invalid_arguments_return_errors_without_a_gpu():
     assert lib.iq_reuse_map(None, None, 4, 2000, 4, None, None, None) == -1
     assert b"D=2000" in lib.iq_last_error()
     assert lib.iq_v_dequantize(None, None, None, 1, 128, 3, 64, None, 0, None) == -1
-    assert lib.iq_decode_workspace_floats(28, 128, 4, 128) == 28 * 130 * 130
+    # 128 blocks + one 32-token sink slice + four 32-token tail slices, 130 floats each
+    assert lib.iq_decode_workspace_floats(28, 128, 4, 128) == 28 * 133 * 130
     # the allocation-free decode refuses, on the host and before touching a
     # device, inputs whose partials exceed its static scratch (4 Mi floats)
     assert lib.iq_decode_attention_noalloc(
