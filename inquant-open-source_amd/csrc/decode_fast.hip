@@ -41,6 +41,8 @@
 //     channel's column is round(pad) * sum(p).
 #include "decode_common.h"
 
+#include <atomic>
+
 namespace {
 
 constexpr int D = 128;
@@ -81,7 +83,20 @@ struct FastArgs {
     int64_t P;
     void *out;       // final [Hq, 128] output when there is one partition
     int odt;
+    // 1 when the grid holds more workgroups than fit on the device at once:
+    // the dense partitions then take the first grid rows and keep the top
+    // issue priority, so they finish early and the packed workgroups left
+    // over start early instead of after the resident ones
+    int dense_first;
 };
+
+// Partition of grid row y: packed blocks, then dense slices; or, with
+// dense_first, the dense slices first.
+__device__ __forceinline__ int64_t partition_of(const FastArgs &a, int64_t y)
+{
+    const int64_t nd = a.P - a.nblk;
+    return a.dense_first ? (y < nd ? a.nblk + y : y - nd) : y;
+}
 
 // Workgroup LDS, shared by the packed and the dense instantiation of the body.
 // At most 40 KiB, so that four workgroups share a compute unit.
@@ -153,7 +168,7 @@ __device__ __forceinline__ void fast_body(const FastArgs &a, FastSmem &sm)
     // 32 m + pl and 32 m + 16 + pl) and 32-channel quarter qq
     const int pl = lane & 15, qq = lane >> 4;
     const int h = blockIdx.x;
-    const int64_t p = blockIdx.y;
+    const int64_t p = partition_of(a, blockIdx.y);
     const int G = a.G;
     // the fp8 converter maps byte n < 16 to n * 2^-9 exactly (e4m3 subnormals
     // and the first binade), so scales are pre-multiplied by 2^9
@@ -482,7 +497,7 @@ __device__ __forceinline__ void fast_body(const FastArgs &a, FastSmem &sm)
             }
         }
 
-        __builtin_amdgcn_s_setprio(2);
+        if (PACKED || !a.dense_first) __builtin_amdgcn_s_setprio(2);
         // ---------------- online softmax (log2 domain); lane holds g = gl, tokens 16 j + 4 ql + r
         // raw logits: the scale is positive, so the maximum commutes with it
         // and is applied once; p = 2^(s c - m) with one fma per logit
@@ -688,7 +703,7 @@ __device__ __forceinline__ void fast_body(const FastArgs &a, FastSmem &sm)
     }
 #undef IQ_LOAD_CHUNK
 
-    __builtin_amdgcn_s_setprio(1);
+    if (PACKED || !a.dense_first) __builtin_amdgcn_s_setprio(1);
     // ---------------- combine the four wavefronts, write this partition's partial
     // Each wavefront stages its unnormalized O as O[g][c] rows next to its
     // (m, l); a reader weights the four rows by 2^(m_w - max m) and adds.
@@ -751,8 +766,28 @@ template <bool F16, int VBITS>
 __global__ __launch_bounds__(256, VBITS == 0 ? 3 : 4) void decode_fast(FastArgs a)
 {
     __shared__ FastSmem sm;
-    if ((int64_t)blockIdx.y < a.nblk) fast_body<F16, VBITS, true>(a, sm);
+    if (partition_of(a, blockIdx.y) < a.nblk) fast_body<F16, VBITS, true>(a, sm);
     else fast_body<F16, VBITS, false>(a, sm);
+}
+
+// Workgroups of decode_fast<F16, VBITS> resident on the current device at
+// once (compute units x occupancy), measured once per device; 0 if unknown.
+template <bool F16, int VBITS>
+int64_t resident_workgroups()
+{
+    static std::atomic<int64_t> cap[64];
+    int dev = -1;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+    int64_t c = cap[dev].load(std::memory_order_relaxed);
+    if (c == 0) {
+        int cus = 0, per = 0;
+        if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+            hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, decode_fast<F16, VBITS>, 256, 0) != hipSuccess)
+            return 0;
+        c = (int64_t)cus * per;
+        cap[dev].store(c, std::memory_order_relaxed);
+    }
+    return c;
 }
 
 }  // namespace
@@ -805,6 +840,13 @@ int iq_decode_fast_launch(const void *q, int q_dtype, int64_t q_stride_h, int64_
     const dim3 grid((unsigned)H, (unsigned)P), block(256);
     const bool f16 = q_dtype == IQ_F16;
     const int vb = n_blocks > 0 ? value_bits : 2;
+    if (n_blocks > 0 && P > n_blocks) {
+        const int64_t cap = f16 ? (vb == 2 ? resident_workgroups<true, 2>() : vb == 4 ? resident_workgroups<true, 4>()
+                                                                                      : resident_workgroups<true, 0>())
+                                : (vb == 2 ? resident_workgroups<false, 2>() : vb == 4 ? resident_workgroups<false, 4>()
+                                                                                       : resident_workgroups<false, 0>());
+        a.dense_first = cap > 0 && H * P > cap;
+    }
     if (f16 && vb == 2) hipLaunchKernelGGL((decode_fast<true, 2>), grid, block, 0, stream, a);
     else if (f16 && vb == 4) hipLaunchKernelGGL((decode_fast<true, 4>), grid, block, 0, stream, a);
     else if (f16) hipLaunchKernelGGL((decode_fast<true, 0>), grid, block, 0, stream, a);
