@@ -568,14 +568,20 @@ __device__ __forceinline__ void paged_body(const PagedArgs &a, PagedSmem<NPG> &s
         // ---------------- softmax (log2 domain); lane holds g = gl, tokens 16 j + 4 ql + r.
         // Raw logits: the scale is positive, so the maximum commutes with it
         // and p = 2^(s c - m) takes one fma per logit.
+        // (wave-uniform) every token of this wavefront is live: no masking
+        const bool all_live = PACKED && okmask == (1u << PPW) - 1u && base + 64 <= ntok && tok0 + base >= geo.sink;
+        if (!all_live) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+                    if (!live(base + 16 * j + 4 * ql + r)) sc[j][r] = NEG_INF;
+        }
         float cmax = NEG_INF;
 #pragma unroll
         for (int j = 0; j < 4; ++j)
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                if (!live(base + 16 * j + 4 * ql + r)) sc[j][r] = NEG_INF;
-                cmax = fmaxf(cmax, sc[j][r]);
-            }
+            for (int r = 0; r < 4; ++r) cmax = fmaxf(cmax, sc[j][r]);
         const float m_new = xmax16(cmax) * a.c_log2;
         const float m_use = m_new == NEG_INF ? 0.0f : m_new;
         float lsum = 0.0f;
