@@ -16,6 +16,13 @@
 
 typedef __attribute__((ext_vector_type(4))) uint32_t u32x4_t;
 
+// v of the lane selected by the DPP control CTRL (every lane active)
+template <int CTRL>
+__device__ __forceinline__ float grp_move(float v)
+{
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, false));
+}
+
 // raw: 32 bytes = channels 16 j .. 16 j + 15 of one token; GL adjacent lanes
 // form one group (every lane of the wavefront must call this together).
 // Outputs the packed codes (BITS / 2 words, LSB-first), the group's f16
@@ -40,11 +47,22 @@ __device__ __forceinline__ void v_encode16(const u32x4_t (&raw)[2], bool live, u
     }
     lo = __builtin_elementwise_minimum(lo, v[15]);
     hi = __builtin_elementwise_maximum(hi, v[15]);
-#pragma unroll
-    for (int o = 1; o < GL; o <<= 1) {
-        lo = __builtin_elementwise_minimum(lo, __shfl_xor(lo, o, 64));
-        hi = __builtin_elementwise_maximum(hi, __shfl_xor(hi, o, 64));
+    // the group's GL lanes combine by DPP moves (no LDS round trip): lanes
+    // i ^ 1 and i ^ 2 within a quad, then the mirrored half of the 8-lane
+    // row, whose lanes lie in the other quad
+    if constexpr (GL > 1) {
+        lo = __builtin_elementwise_minimum(lo, grp_move<0xb1>(lo));      // quad_perm [1, 0, 3, 2]
+        hi = __builtin_elementwise_maximum(hi, grp_move<0xb1>(hi));
     }
+    if constexpr (GL > 2) {
+        lo = __builtin_elementwise_minimum(lo, grp_move<0x4e>(lo));      // quad_perm [2, 3, 0, 1]
+        hi = __builtin_elementwise_maximum(hi, grp_move<0x4e>(hi));
+    }
+    if constexpr (GL > 4) {
+        lo = __builtin_elementwise_minimum(lo, grp_move<0x141>(lo));     // row_half_mirror
+        hi = __builtin_elementwise_maximum(hi, grp_move<0x141>(hi));
+    }
+    static_assert(GL == 1 || GL == 2 || GL == 4 || GL == 8, "groups of 1, 2, 4 or 8 lanes");
     off_h = iq_f32_to_f16(lo);
     float s = __fsub_rn(hi, lo) / (float)L;
     s = s < 6.103515625e-05f ? 6.103515625e-05f : s;
