@@ -400,6 +400,12 @@ __device__ __forceinline__ void fast_body(const FastArgs &a, FastSmem &sm)
     f32x4 acc_sal = {0.0f, 0.0f, 0.0f, 0.0f};      // K4 values: O^T rows = sources 4 ql + r, column gl
 
     uint32_t *vt = s_v[wave];
+    // The P.V operand reads: volatile, so that each lane's four pair rows
+    // stay four single-dword LDS reads straight into the operand registers
+    // (the compiler would otherwise pair the reads of channel tiles n and
+    // n + 1 and copy every operand into place).
+    const volatile __attribute__((address_space(3))) uint32_t *const vtile =
+        (const volatile __attribute__((address_space(3))) uint32_t *)vt;
 
     // one pass: a partition holds at most CHUNK * WAVES tokens
     if (base < stop) {
@@ -692,7 +698,7 @@ __device__ __forceinline__ void fast_body(const FastArgs &a, FastSmem &sm)
             for (int n = 0; n < 8; ++n) {
                 u32x4 va;                              // k-slot pair r: pair row 4 ql + r
 #pragma unroll
-                for (int r = 0; r < 4; ++r) va[r] = vt[(4 * ql + r) * VR + 16 * n + gl];
+                for (int r = 0; r < 4; ++r) va[r] = vtile[(4 * ql + r) * VR + 16 * n + gl];
                 acc[n] = mma32<F16>(va, phi[m], m == 0 ? f32x4{0.0f, 0.0f, 0.0f, 0.0f} : acc[n]);
                 acc[n] = mma32<F16>(va, plo[m], acc[n]);
             }

@@ -443,6 +443,12 @@ __device__ __forceinline__ void paged_body(const PagedArgs &a, PagedSmem<NPG> &s
 #pragma unroll
     for (int n = 0; n < 8; ++n) acc[n] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
     uint32_t *vt = s_v + wave * (16 * VR);
+    // The P.V operand reads: volatile, so that each lane's four pair rows
+    // stay four single-dword LDS reads straight into the operand registers
+    // (the compiler would otherwise pair the reads of channel tiles n and
+    // n + 1 and copy every operand into place).
+    const volatile __attribute__((address_space(3))) uint32_t *const vtile =
+        (const volatile __attribute__((address_space(3))) uint32_t *)vt;
 
     if (base < ntok) {
         // a token is live when it exists in this partition and (packed) lies
@@ -676,7 +682,7 @@ __device__ __forceinline__ void paged_body(const PagedArgs &a, PagedSmem<NPG> &s
             for (int n = 0; n < 8; ++n) {
                 u32x4 va;                              // k-slot pair r: pair row 4 ql + r
 #pragma unroll
-                for (int r = 0; r < 4; ++r) va[r] = vt[(4 * ql + r) * VR + 16 * n + gl];
+                for (int r = 0; r < 4; ++r) va[r] = vtile[(4 * ql + r) * VR + 16 * n + gl];
                 acc[n] = mma32<false>(va, phi[m], acc[n]);
                 acc[n] = mma32<false>(va, plo[m], acc[n]);
             }
