@@ -225,17 +225,11 @@ __global__ __launch_bounds__(K4_THREADS) void k4_encode_kernel(K4Args a)
 constexpr int TILE_D = 128;
 constexpr int TILE_T = 256;
 constexpr int CH = 32;                   // tokens per staged chunk
-#ifndef IQ_K4_KPF
-#define IQ_K4_KPF 1
-#endif
-constexpr int KPF = IQ_K4_KPF;           // chunks in flight
+constexpr int KPF = 1;                   // chunks in flight
 constexpr int XROW = TILE_D + 8;         // u16 per staged row: 68 dwords (16-byte aligned rows, distinct banks)
-#ifndef IQ_K4_NBUF
-#define IQ_K4_NBUF 4
-#endif
 // sealed blocks stream by direct global -> LDS loads into NBUF chunk buffers
 // (unpadded rows), NBUF - 1 chunks in flight while one is processed
-constexpr int NBUF_DMA = IQ_K4_NBUF;
+constexpr int NBUF_DMA = 4;
 
 // s_waitcnt vmcnt(2 * ahead) lgkmcnt(0), then s_barrier: this wave's loads
 // of every chunk but the `ahead` newest have landed in LDS and its LDS reads
