@@ -1,6 +1,6 @@
 """Benchmark of the InQuant packed-KV hot path on one MI355X.
 
-Workload: Qwen2.5-7B-shaped decode, 28 query heads over 4
+Workload (config 2): Qwen2.5-7B-shaped decode, 28 query heads over 4
 KV heads, head_dim 128, 32768 packed tokens (128 K4/V2 blocks of 256) + 4-token
 BF16 sink + 128-token BF16 tail per layer, 28 layers with independent data.
 One step = one decode token through all 28 layers (28 fused decode calls,
@@ -9,7 +9,7 @@ replayed as one HIP graph).  Inputs are resident in HBM; the 28 layers
 
 value  = algorithmic bytes (packed K/V, scales, role maps, padding, V params,
          pointer table, sink, tail, Q, O) per step / step time  [GB/s]
-extras = codec encode Mtok/s (Mistral-7B layer, 32768
+extras = codec encode Mtok/s (config 3: Mistral-7B layer, 32768
          tokens x 8 KV heads, K4 min_error + V2 g64), the config 3 decode
          (32 Mistral-7B layers), the config 2 append, the config 4 batched
          paged decode, roofline and the CPU oracle baseline on a bounded

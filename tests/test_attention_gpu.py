@@ -1,7 +1,7 @@
 """GPU parity of fused packed decode attention against the fp64
 dequantize-then-attend oracle (qwen_fused.py:21-30 semantics).
 
-Bar (BASELINE north star): max |out_fp32 - oracle| <= 2e-3, with keys and
+Bar: max |out_fp32 - oracle| <= 2e-3, with keys and
 values decoded and rounded to the query dtype exactly as the reference does.
 """
 import numpy as np
@@ -54,7 +54,7 @@ def test_k4v2_gqa_matches_oracle(bits, group, dtype):
 
 
 def test_qwen_shape_8k_context_cfg1():
-    # 28 query heads over 4 KV heads, 32 packed blocks, 4 sink, 128 tail
+    # config 1: 28 query heads over 4 KV heads, 32 packed blocks, 4 sink, 128 tail
     from inquant.triton_attention import PackedDecodeState
     case = make_case(1, n_blocks=32, sink=4, tail=128)
     state = PackedDecodeState(case.key_blocks, case.value_blocks)
@@ -64,7 +64,7 @@ def test_qwen_shape_8k_context_cfg1():
 
 
 def test_mistral_shape_dense_outliers_cfg3():
-    # BASELINE config 3 shape: G = 4 over 8 KV heads, 8% outliers in 3-wide runs
+    # config 3 shape: G = 4 over 8 KV heads, 8% outliers in 3-wide runs
     from inquant.triton_attention import PackedDecodeState
     case = make_case(3, H=8, G=4, n_blocks=8, groups=(3, 3, 3, 1))
     state = PackedDecodeState(case.key_blocks, case.value_blocks)
@@ -277,7 +277,7 @@ def test_matrix_core_path_peaked_attention_keeps_precision():
 
 
 def test_cfg2_full_context_matches_oracle_and_is_repeatable():
-    # BASELINE config 2 layer: 128 packed blocks (32768 tokens) + 4 sink + 128 tail;
+    # config 2 layer: 128 packed blocks (32768 tokens) + 4 sink + 128 tail;
     # 130 partitions merged by the reduction kernel
     from inquant.triton_attention import PackedDecodeState
     case = make_case(2, n_blocks=128, sink=4, tail=128)
@@ -290,7 +290,7 @@ def test_cfg2_full_context_matches_oracle_and_is_repeatable():
 
 @pytest.mark.parametrize("value_bits", [2, 0])
 def test_cfg3_full_context_grid_above_resident_capacity_matches_oracle(value_bits):
-    # BASELINE config 3 layer: 8 KV heads x (128 packed blocks + 5 dense
+    # config 3 layer: 8 KV heads x (128 packed blocks + 5 dense
     # slices) = 1064 workgroups, more than fit at once (256 compute units x 4,
     # or x 3 with K4-coded values), so the dense slices take the first grid
     # rows; outliers in 3-wide runs
