@@ -223,12 +223,12 @@ __global__ __launch_bounds__(DA_THREADS) void decode_partials_generic(DecodeArgs
 // channels of one query head, the eight channel slices of a head on one XCD.
 // Lane (column c4 = lane % 4, partition lane part = lane / 4) owns channels
 // 4 c4 .. 4 c4 + 3 and every 16th partition from `part`; a partition costs
-// it three 8-byte loads (two for its four channels, one for (m, l)), nine
-// partitions per round, all issued before any arithmetic.  Partial rows are
-// 130 floats, so only 8-byte alignment holds.  The 16 running states of a
-// column then merge inside the wave (two DPP row rotations, two permlane
-// swaps): no LDS, no barrier (a four-wave form with an LDS exchange measured
-// 0.1 us per layer slower).
+// it one 16-byte load of its four channels (the partials' 128-float output
+// rows) and one 8-byte load of (m, l) (the pair array after them), nine
+// partitions per round, all issued before any arithmetic.  The 16 running
+// states of a column then merge inside the wave (two DPP row rotations, two
+// permlane swaps): no LDS, no barrier (a four-wave form with an LDS exchange
+// measured 0.1 us per layer slower).
 constexpr int RED_THREADS = 64;
 constexpr int RED_C4 = 4;                          // four-channel columns per workgroup
 constexpr int RED_PARTS = RED_THREADS / RED_C4;    // partition lanes

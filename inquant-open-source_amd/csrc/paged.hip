@@ -757,10 +757,11 @@ __global__ __launch_bounds__(256, 4) void decode_paged(PagedArgs a)
 // partitions of one sequence for 16 channels of one query head (the eight
 // channel slices of a head on one XCD), as decode_reduce: lane (column c4 of
 // four channels, partition lane part) takes every 16th partition from
-// `part`, three 8-byte loads each (partial rows are 130 floats, so only
-// 8-byte alignment holds), nine partitions per round all in flight; the 16
-// states of a column then merge inside the wave (DPP row rotations and
-// permlane swaps), with no LDS and no barrier.
+// `part`, a 16-byte load of its channels and an 8-byte load of (m, l) each,
+// nine partitions per round all in flight; the 16 states of a column then
+// merge inside the wave (DPP row rotations and permlane swaps), with no LDS
+// and no barrier (four-wave workgroups of four slices each measured no
+// faster).
 __global__ __launch_bounds__(64) void paged_reduce(PagedArgs a, void *out, int64_t out_ss, int odt)
 {
     constexpr int BATCH = 9;
