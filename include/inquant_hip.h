@@ -191,7 +191,8 @@ typedef struct iq_block_run {
  *   sink/tail K/V of q_dtype with (head, token) element strides, lengths
  *   sink_t / tail_t (pointers may be NULL when the length is 0);
  *   workspace f32 with at least iq_decode_workspace_floats(...) elements
- *   (per-partition partials [Hq, P, 130], merged by a second kernel);
+ *   (Hq * P * 130 floats: each partition's 128-float output rows, then its
+ *   (max, sum) pairs; merged by a second kernel);
  *   out [Hq, 128] contiguous of out_dtype.
  * Keys/values are decoded and rounded to q_dtype exactly as the reference's
  * dequantize-then-attend path does; logits, softmax and P.V accumulate in
@@ -284,7 +285,8 @@ int iq_encode_pages(const void *keys, const void *values, int dtype, const int64
 int iq_unpack_pages(const uint8_t *pages, int64_t n_pages, int64_t H, int64_t block_tokens, void *keys,
                     void *values, int out_dtype, void *stream);
 
-/* fp32 workspace elements iq_paged_decode needs: [n_seq, Hq, partitions, 130]. */
+/* fp32 workspace elements iq_paged_decode needs: n_seq * Hq * partitions * 130
+ * (128-float output rows, then (max, sum) pairs). */
 int64_t iq_paged_workspace_floats(int64_t Hq, int64_t n_seq, int64_t max_pages, int64_t block_tokens);
 
 /*

@@ -183,7 +183,7 @@ struct PagedArgs {
     int64_t dense_ss;
     int max_parts;
     float c_log2;                      // softmax scale * log2(e)
-    float *ws;                         // [seq, Hq, max_parts, 130]
+    float *ws;                         // seq * Hq * max_parts partials (Partials layout)
 };
 
 struct SeqGeom {
