@@ -288,14 +288,15 @@ def test_cfg2_full_context_matches_oracle_and_is_repeatable():
     np.testing.assert_allclose(outs[0], case.expected(), atol=ATOL, rtol=0)
 
 
-@pytest.mark.parametrize("value_bits", [2, 0])
-def test_cfg3_full_context_grid_above_resident_capacity_matches_oracle(value_bits):
+@pytest.mark.parametrize("value_bits,dtype", [(2, torch.bfloat16), (0, torch.bfloat16), (2, torch.float16)])
+def test_cfg3_full_context_grid_above_resident_capacity_matches_oracle(value_bits, dtype):
     # config 3 layer: 8 KV heads x (128 packed blocks + 5 dense
     # slices) = 1064 workgroups, more than fit at once (256 compute units x 4,
     # or x 3 with K4-coded values), so the dense slices take the first grid
     # rows; outliers in 3-wide runs
     from inquant.triton_attention import PackedDecodeState
-    case = make_case(3, H=8, G=4, n_blocks=128, sink=4, tail=128, groups=(3, 3, 3, 1), value_bits=value_bits)
+    case = make_case(3, H=8, G=4, n_blocks=128, sink=4, tail=128, groups=(3, 3, 3, 1), value_bits=value_bits,
+                     dtype=dtype)
     state = PackedDecodeState(case.key_blocks, case.value_blocks)
     outs = [_decode_f32(state, case) for _ in range(2)]
     assert np.array_equal(outs[1], outs[0])
