@@ -303,6 +303,16 @@ def test_cfg3_full_context_grid_above_resident_capacity_matches_oracle(value_bit
     np.testing.assert_allclose(outs[0], case.expected(), atol=ATOL, rtol=0)
 
 
+@pytest.mark.parametrize("n_blocks,tail", [(300, 100), (0, 5000)])
+def test_merge_over_more_partitions_than_one_round(n_blocks, tail):
+    # 304 and 157 partitions: the merge takes 144 per round, so its running
+    # (max, sum, output) state is rescaled across rounds
+    from inquant.triton_attention import PackedDecodeState
+    case = make_case(11, H=2, G=4, n_blocks=n_blocks, block=16, sink=4, tail=tail)
+    state = PackedDecodeState(case.key_blocks, case.value_blocks)
+    np.testing.assert_allclose(_decode_f32(state, case), case.expected(), atol=ATOL, rtol=0)
+
+
 def test_extend_checks_every_appended_block_and_keeps_the_state_on_error():
     # triton_attention.py:257-269: every appended block must match the first
     # block's shape, salient count and value quantizer; a rejected extend

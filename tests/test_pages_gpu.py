@@ -91,8 +91,9 @@ def _expected(layout, pool, ids, dense, pages, tail, sink, q):
 
 @pytest.mark.parametrize("block,pages,tail", [(64, 0, 1), (64, 0, 63), (64, 1, 0), (64, 1, 64), (128, 3, 17),
                                                (256, 128, 128), (256, 2, 256), (16, 1, 1), (16, 37, 9),
-                                               (32, 9, 31), (16, 0, 3)])
+                                               (32, 9, 31), (16, 0, 3), (64, 600, 10)])
 def test_paged_decode_random_page_order_and_reuse(block, pages, tail):
+    # (64, 600, 10): 151 partitions, more than the merge's 144 per round
     # test_pages.py:22-58 (random physical order, unused pages full of 0xff,
     # NaN in dead dense slots, the workspace reused), against the fp64 oracle
     from inquant.triton_attention import SharedDecodeWorkspace
