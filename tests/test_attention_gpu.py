@@ -303,6 +303,17 @@ def test_cfg3_full_context_grid_above_resident_capacity_matches_oracle(value_bit
     np.testing.assert_allclose(outs[0], case.expected(), atol=ATOL, rtol=0)
 
 
+@pytest.mark.parametrize("G", [1, 2, 8, 16])
+@pytest.mark.parametrize("value_bits", [2, 0])
+def test_query_group_sizes(G, value_bits):
+    # one query row per KV head (G = 1) up to the 16 the matrix-core tiles
+    # hold (all 16 columns live; the combine takes two passes over its rows)
+    from inquant.triton_attention import PackedDecodeState
+    case = make_case(13 + G, H=2, G=G, n_blocks=3, sink=4, tail=40, value_bits=value_bits)
+    state = PackedDecodeState(case.key_blocks, case.value_blocks)
+    np.testing.assert_allclose(_decode_f32(state, case), case.expected(), atol=ATOL, rtol=0)
+
+
 @pytest.mark.parametrize("n_blocks,tail", [(300, 100), (0, 5000)])
 def test_merge_over_more_partitions_than_one_round(n_blocks, tail):
     # 304 and 157 partitions: the merge takes 144 per round, so its running

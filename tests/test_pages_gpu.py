@@ -112,6 +112,18 @@ def test_paged_decode_random_page_order_and_reuse(block, pages, tail):
         assert np.abs(_np(out32)[0] - exp).max() <= ATOL
 
 
+@pytest.mark.parametrize("h,hq", [(4, 4), (2, 32)])
+def test_paged_decode_query_group_sizes(h, hq):
+    # one query row per KV head, and the 16 a matrix-core tile holds
+    from inquant.triton_attention import SharedDecodeWorkspace
+    from inquant_vllm import paged_decode
+    layout, pool, ids, dense, sink, q = _paged_case(83, 16, 20, 5, h=h, hq=hq)
+    out32 = torch.empty(q.shape, dtype=torch.float32, device="cuda")
+    paged_decode(q, pool, ids, dense, 20, 5, sink, layout, SharedDecodeWorkspace(), 128 ** -0.5, out32)
+    exp = _expected(layout, pool, ids, dense, 20, 5, sink, q)
+    assert np.abs(_np(out32)[0] - exp).max() <= ATOL
+
+
 def test_paged_decode_batch_equals_single_sequences():
     # sequences of different lengths and pools in one launch (16-token pages)
     from inquant.triton_attention import SharedDecodeWorkspace
