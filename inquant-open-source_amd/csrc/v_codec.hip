@@ -282,6 +282,126 @@ __global__ __launch_bounds__(V_THREADS) void k4_decode_kernel(KDecArgs a)
     }
 }
 
+// Rows of 128 channels, 16-byte aligned output rows.  Thread (row, j)
+// decodes channels 16 j .. 16 j + 15 of one row: BITS / 2 payload words and
+// its group's f16 scale and offset, then writes 16 values with 16-byte
+// stores.  Same arithmetic as v_decode_kernel.
+template <int BITS, int OUT>
+__global__ __launch_bounds__(V_THREADS) void v_decode_rows(VDecArgs a)
+{
+    const int64_t u = (int64_t)blockIdx.x * V_THREADS + threadIdx.x;
+    const int64_t r = u >> 3;
+    const int j = (int)(u & 7);
+    if (r >= a.rows) return;
+    constexpr int PB = 128 * BITS / 8;                      // payload bytes per row
+    const int64_t p = r * (128 / a.group) + (16 * j) / a.group;
+    const float sc = iq_f16_to_f32(a.scales[p]), off = iq_f16_to_f32(a.offsets[p]);
+    uint64_t w;                                             // channel 16 j + e at bits BITS * e
+    if constexpr (BITS == 2) w = *(const uint32_t *)(a.payload + r * PB + 4 * j);
+    else w = *(const uint64_t *)(a.payload + r * PB + 8 * j);
+    float v[16];
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+        const int code = (int)((w >> (BITS * e)) & ((1u << BITS) - 1u));
+        v[e] = __fadd_rn(__fmul_rn((float)code, sc), off);
+    }
+    if constexpr (OUT == IQ_F32) {
+        float4 *o = (float4 *)((float *)a.out + r * 128 + 16 * j);
+#pragma unroll
+        for (int k = 0; k < 4; ++k) o[k] = float4{v[4 * k], v[4 * k + 1], v[4 * k + 2], v[4 * k + 3]};
+    } else {
+        uint32_t h[8];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            const uint32_t lo = OUT == IQ_BF16 ? iq_f32_to_bf16(v[2 * k]) : iq_f32_to_f16(v[2 * k]);
+            const uint32_t hi = OUT == IQ_BF16 ? iq_f32_to_bf16(v[2 * k + 1]) : iq_f32_to_f16(v[2 * k + 1]);
+            h[k] = lo | (hi << 16);
+        }
+        uint4 *o = (uint4 *)((uint16_t *)a.out + r * 128 + 16 * j);
+        o[0] = uint4{h[0], h[1], h[2], h[3]};
+        o[1] = uint4{h[4], h[5], h[6], h[7]};
+    }
+}
+
+// Blocks of 128 channels with at most 64 one-byte descriptors, 16-byte
+// aligned output rows.  Grid (token tiles of 128, rows); the row's role map,
+// scales and donor paddings are built once in LDS.  Thread (token, j),
+// j < 16, decodes channels 8 j .. 8 j + 7 of a token from one payload word;
+// a source channel's low nibble comes from the donor's word, read from the
+// lane of the token that holds it.  Same arithmetic as k4_decode_kernel.
+constexpr int KD_TOKENS = 128;
+
+template <int OUT>
+__global__ __launch_bounds__(V_THREADS) void k4_decode_rows(KDecArgs a)
+{
+    __shared__ float s_scale[128], s_pad[64];
+    __shared__ int16_t s_role[128];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int64_t row = blockIdx.y;
+    if (tid < 128) {
+        s_scale[tid] = a.scales[row * 128 + tid];
+        s_role[tid] = -1;
+    }
+    __syncthreads();
+    if (tid < a.count) {
+        const int sch = ((const uint8_t *)a.src)[row * a.count + tid];
+        const int dch = ((const uint8_t *)a.don)[row * a.count + tid];
+        if (sch < 128 && dch < 128) {
+            s_role[sch] = (int16_t)dch;
+            s_role[dch] = (int16_t)(-2 - tid);
+        }
+        s_pad[tid] = a.padding[row * a.count + tid];
+    }
+    __syncthreads();
+    const int j = tid & 15;
+    int role[8];
+    float scl[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        role[e] = s_role[8 * j + e];
+        scl[e] = s_scale[8 * j + e];
+    }
+    const int64_t t_first = (int64_t)blockIdx.x * KD_TOKENS;
+#pragma unroll 1
+    for (int tt = tid >> 4; tt < KD_TOKENS; tt += V_THREADS / 16) {
+        const int64_t t = t_first + tt;
+        const bool live = t < a.T;
+        const int64_t rt = row * a.T + (live ? t : a.T - 1);   // every lane loads (the shuffles need all)
+        const uint32_t w = *(const uint32_t *)(a.payload + rt * 64 + 4 * j);
+        float v[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const int rl = role[e];
+            const int slot = (int)((w >> (4 * e)) & 15u);
+            // the donor's payload word: word rl / 8 of this token's row, held by lane (lane & ~15) + rl / 8
+            const uint32_t wd = (uint32_t)__shfl((int)w, (lane & ~15) | ((rl >> 3) & 15), 64);
+            if (rl >= 0) {
+                const int lo = (int)((wd >> (4 * (rl & 7))) & 15u);
+                v[e] = __fmul_rn((float)(((slot << 4) | lo) - 128), scl[e]);
+            } else if (rl <= -2) {
+                v[e] = s_pad[-rl - 2];
+            } else {
+                v[e] = __fmul_rn((float)(slot - 8), scl[e]);
+            }
+        }
+        if (!live) continue;
+        if constexpr (OUT == IQ_F32) {
+            float4 *o = (float4 *)((float *)a.out + rt * 128 + 8 * j);
+            o[0] = float4{v[0], v[1], v[2], v[3]};
+            o[1] = float4{v[4], v[5], v[6], v[7]};
+        } else {
+            uint32_t h[4];
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const uint32_t lo = OUT == IQ_BF16 ? iq_f32_to_bf16(v[2 * k]) : iq_f32_to_f16(v[2 * k]);
+                const uint32_t hi = OUT == IQ_BF16 ? iq_f32_to_bf16(v[2 * k + 1]) : iq_f32_to_f16(v[2 * k + 1]);
+                h[k] = lo | (hi << 16);
+            }
+            *(uint4 *)((uint16_t *)a.out + rt * 128 + 8 * j) = uint4{h[0], h[1], h[2], h[3]};
+        }
+    }
+}
+
 }  // namespace
 
 extern "C" int iq_v_quantize(const void *x, int x_dtype, const int64_t *x_strides, int64_t B, int64_t H,
@@ -337,6 +457,22 @@ extern "C" int iq_v_dequantize(const uint8_t *payload, const uint16_t *scales, c
     IQ_CHECK_ARG(payload && scales && offsets && out, "iq_v_dequantize: null pointer");
     const int64_t n = rows * D;
     VDecArgs a{payload, scales, offsets, rows, D, bits, group, out, out_dtype};
+    if (D == 128 && ((uintptr_t)out & 15) == 0 && ((uintptr_t)payload & (bits == 2 ? 3 : 7)) == 0 &&
+        (rows * 8 + V_THREADS - 1) / V_THREADS <= 0x7fffffffLL) {
+        const dim3 grid((unsigned)((rows * 8 + V_THREADS - 1) / V_THREADS)), block(V_THREADS);
+        const hipStream_t st = (hipStream_t)stream;
+        if (bits == 2) {
+            if (out_dtype == IQ_BF16) hipLaunchKernelGGL((v_decode_rows<2, IQ_BF16>), grid, block, 0, st, a);
+            else if (out_dtype == IQ_F16) hipLaunchKernelGGL((v_decode_rows<2, IQ_F16>), grid, block, 0, st, a);
+            else hipLaunchKernelGGL((v_decode_rows<2, IQ_F32>), grid, block, 0, st, a);
+        } else {
+            if (out_dtype == IQ_BF16) hipLaunchKernelGGL((v_decode_rows<4, IQ_BF16>), grid, block, 0, st, a);
+            else if (out_dtype == IQ_F16) hipLaunchKernelGGL((v_decode_rows<4, IQ_F16>), grid, block, 0, st, a);
+            else hipLaunchKernelGGL((v_decode_rows<4, IQ_F32>), grid, block, 0, st, a);
+        }
+        IQ_CHECK_LAUNCH("v_decode_rows");
+        return IQ_OK;
+    }
     hipLaunchKernelGGL(v_decode_kernel, dim3((unsigned)((n + V_THREADS - 1) / V_THREADS)), dim3(V_THREADS), 0,
                        (hipStream_t)stream, a);
     IQ_CHECK_LAUNCH("v_decode_kernel");
@@ -356,6 +492,16 @@ extern "C" int iq_k4_dequantize(const uint8_t *payload, const float *scales, con
     IQ_CHECK_ARG(payload && scales && out && (count == 0 || (src && don && padding)), "iq_k4_dequantize: null");
     IQ_CHECK_ARG(rows * T <= 0x7fffffffLL, "iq_k4_dequantize: too large");
     KDecArgs a{payload, scales, src, don, desc_bytes, padding, rows, T, D, count, out, out_dtype};
+    if (D == 128 && desc_bytes == 1 && count <= 64 && ((uintptr_t)out & 15) == 0 && ((uintptr_t)payload & 3) == 0 &&
+        rows <= 65535 && out_dtype != IQ_F64) {
+        const dim3 grid((unsigned)((T + KD_TOKENS - 1) / KD_TOKENS), (unsigned)rows), block(V_THREADS);
+        const hipStream_t st = (hipStream_t)stream;
+        if (out_dtype == IQ_BF16) hipLaunchKernelGGL((k4_decode_rows<IQ_BF16>), grid, block, 0, st, a);
+        else if (out_dtype == IQ_F16) hipLaunchKernelGGL((k4_decode_rows<IQ_F16>), grid, block, 0, st, a);
+        else hipLaunchKernelGGL((k4_decode_rows<IQ_F32>), grid, block, 0, st, a);
+        IQ_CHECK_LAUNCH("k4_decode_rows");
+        return IQ_OK;
+    }
     hipLaunchKernelGGL(k4_decode_kernel, dim3((unsigned)(rows * T)), dim3(V_THREADS), 0, (hipStream_t)stream, a);
     IQ_CHECK_LAUNCH("k4_decode_kernel");
     return IQ_OK;

@@ -268,10 +268,11 @@ def test_value_codec_known_answers_and_rejections():
             quantize_values(torch.full((1, 1, 2, 128), value, device="cuda"))
 
 
-@pytest.mark.parametrize("frac,policy", [(0.0, "neighbors"), (0.125, "min_error"), (0.5, "neighbors")])
-def test_k4_dequantize_matches_oracle(frac, policy):
+@pytest.mark.parametrize("frac,policy,T", [(0.0, "neighbors", 96), (0.125, "min_error", 96), (0.5, "neighbors", 96),
+                                           (0.125, "min_error", 300)])
+def test_k4_dequantize_matches_oracle(frac, policy, T):
     from inquant.codec import CodecConfig, quantize
-    x = synth.kv_like(21, 4, 96)
+    x = synth.kv_like(21, 4, T)
     packed = quantize(_dev(x, torch.bfloat16), CodecConfig(salient_fraction=frac, donor_policy=policy))
     fields = {k: _np(v) for k, v in packed.tensors.items()}
     fields["salient_channels"] = fields["salient_channels"].astype(np.int64)
