@@ -12,8 +12,9 @@ value  = algorithmic bytes (packed K/V, scales, role maps, padding, V params,
 extras = codec encode Mtok/s (config 3: Mistral-7B layer, 32768
          tokens x 8 KV heads, K4 min_error + V2 g64), the config 3 decode
          (32 Mistral-7B layers), the config 2 append, the config 4 batched
-         paged decode, roofline and the CPU oracle baseline on a bounded
-         sample.
+         paged decode, the rows next to the decode path (materialize,
+         encode into pages, causal prefill), roofline and the CPU oracle
+         baseline on a bounded sample.
 """
 from __future__ import annotations
 
@@ -28,6 +29,7 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, os.path.join(ROOT, "inquant-open-source_amd"))
 
 HBM_PEAK_GBS = 8000.0
+MFMA_BF16_PEAK_TFLOPS = 2500.0     # dense bf16 matrix-core peak
 METRIC = "packed-KV decode attn GB/s (% HBM peak) @32K ctx; codec encode Mtok/s"
 
 
@@ -48,6 +50,8 @@ def parse():
     ap.add_argument("--no-encode", action="store_true", help="skip the config 3 encode")
     ap.add_argument("--no-k4-values", action="store_true", help="skip the config 2 decode with K4-coded values")
     ap.add_argument("--no-append", action="store_true", help="skip the config 2 append measurements")
+    ap.add_argument("--no-next", action="store_true",
+                    help="skip the rows next to the decode path (materialize, encode into pages, prefill)")
     ap.add_argument("--copy-probe", action="store_true",
                     help="only run a 1 GiB device-to-device copy (calibrates rocprofv3 FETCH_SIZE / WRITE_SIZE)")
     return ap.parse_args()
@@ -304,6 +308,121 @@ def time_encode(device, reps=10):
     return {"encode_mtok_s": T / (ms * 1e-3) / 1e6, "encode_ms_per_layer": ms,
             "encode_gbs": enc_bytes / (ms * 1e-3) / 1e9, "encode_bytes_per_layer": enc_bytes,
             "k4_values_mtok_s": T / (ms_k4v * 1e-3) / 1e6, "k4_values_ms_per_layer": ms_k4v}
+
+
+def _graph_us(device, launch, reps=10):
+    """Microseconds per call of `launch` (native launches on the current
+    stream), replayed `reps` times in one HIP graph."""
+    import torch
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(s):
+        launch()
+        torch.cuda.synchronize()
+        with torch.cuda.graph(graph, stream=s):
+            for _ in range(reps):
+                launch()
+    torch.cuda.synchronize()
+    graph.replay()
+    torch.cuda.synchronize()
+    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    graph.replay()
+    stop.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(stop) * 1e3 / reps
+
+
+def time_next_rows(device):
+    """The rows next to the decode path, inputs resident, launches replayed in
+    a HIP graph: materialize (K4 keys and V2 g64 values of one config 2 layer,
+    4 heads x 32768 tokens, dequantized to bf16), encode into 256- and
+    16-token pages (keys K4 min_error + role map + values V2 of 32768 tokens
+    x 4 heads, one launch) and causal prefill attention over exact K/V (one
+    8192-token Qwen2.5-7B sequence, 28 query heads over 4 KV heads, bf16)."""
+    import torch
+    from inquant import _native as nat
+    from inquant.codec import CodecConfig, quantize
+    from inquant.value_codec import quantize_values
+    from inquant_vllm import PageLayout
+    lib = nat.lib()
+    H, T, D = 4, 32768, 128
+    gen = torch.Generator(device=device).manual_seed(6)
+    k = kv_tensor(gen, H, T, device)
+    v = kv_tensor(gen, H, T, device)
+    out = {}
+
+    # materialize: both dequantizers into bf16 K and V
+    pk = quantize(k, CodecConfig(donor_policy="min_error"))
+    pv = quantize_values(v, 2, 64)
+    kd, vd = torch.empty_like(k), torch.empty_like(v)
+    S = pk.salient_channels.shape[-1]
+
+    def materialize():
+        st = nat.stream_handle(torch.device(device))
+        nat.check(lib.iq_k4_dequantize(pk.payload.data_ptr(), pk.scales.data_ptr(), pk.salient_channels.data_ptr(),
+                                       pk.donor_channels.data_ptr(), 1, pk.padding.data_ptr(), H, T, D, S,
+                                       kd.data_ptr(), nat.IQ_BF16, st))
+        nat.check(lib.iq_v_dequantize(pv.payload.data_ptr(), pv.scales.data_ptr(), pv.offsets.data_ptr(), H * T, D,
+                                      2, 64, vd.data_ptr(), nat.IQ_BF16, st))
+
+    us = _graph_us(device, materialize)
+    assert torch.equal(kd, pk.dequantize(torch.bfloat16)) and torch.equal(vd, pv.dequantize(torch.bfloat16))
+    mat_bytes = sum(t.numel() * t.element_size() for t in pk.tensors.values()) \
+        + sum(t.numel() * t.element_size() for t in (pv.payload, pv.scales, pv.offsets)) + 2 * k.numel() * 2
+    out["materialize_cfg2"] = {"us_per_layer": round(us, 3), "bytes_per_layer": mat_bytes,
+                               "gbs": round(mat_bytes / (us * 1e-6) / 1e9, 2),
+                               "hbm_frac": round(mat_bytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
+    del kd, vd, pk, pv
+
+    # encode into pages (the plugin's seal of a prefill: 256-token pages, the
+    # reference layout's largest, and the 16-token pages of config 4), flags
+    # written on the device
+    for B in (256, 16):
+        layout = PageLayout(B, H)
+        P = T // B
+        kp = k[0].reshape(H, P, B, D).transpose(0, 1)
+        vp = v[0].reshape(H, P, B, D).transpose(0, 1)
+        pool = torch.empty((P, layout.page_bytes), dtype=torch.uint8, device=device)
+        ids = torch.arange(P, dtype=torch.int32, device=device)
+        flags = torch.zeros(4, dtype=torch.int32, device=device)
+
+        def encode_pages():
+            st = nat.stream_handle(torch.device(device))
+            nat.check(lib.iq_encode_pages(kp.data_ptr(), vp.data_ptr(), nat.IQ_BF16, nat.strides4(kp),
+                                          nat.strides4(vp), P, H, B, pool.data_ptr(), P, ids.data_ptr(), 4,
+                                          flags.data_ptr(), flags.data_ptr() + 8, st))
+
+        us = _graph_us(device, encode_pages)
+        assert flags[:2].tolist() == [0, 0]
+        enc_bytes = 2 * k.numel() * 2 + P * layout.page_bytes
+        out[f"encode_pages_b{B}"] = {"tokens": T, "heads": H, "page_tokens": B, "us": round(us, 3),
+                                     "mtok_s": round(T / us, 2), "bytes": enc_bytes,
+                                     "gbs": round(enc_bytes / (us * 1e-6) / 1e9, 2),
+                                     "hbm_frac": round(enc_bytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
+        del pool, kp, vp
+
+    # causal prefill attention over exact K/V
+    Sq, Hq = 8192, 28
+    q = torch.randn((Sq, Hq, D), generator=gen, device=device).to(torch.bfloat16)
+    kq = k[0, :, :Sq].transpose(0, 1).contiguous()
+    vq = v[0, :, :Sq].transpose(0, 1).contiguous()
+    o = torch.empty_like(q)
+    cu = torch.tensor([0, Sq], dtype=torch.int32, device=device)
+
+    def prefill():
+        st = nat.stream_handle(torch.device(device))
+        nat.check(lib.iq_prefill_attention(q.data_ptr(), kq.data_ptr(), vq.data_ptr(), nat.IQ_BF16, q.stride(0),
+                                           q.stride(1), kq.stride(0), kq.stride(1), vq.stride(0), vq.stride(1),
+                                           cu.data_ptr(), 1, Sq, Hq, H, D, 128 ** -0.5, o.data_ptr(), o.stride(0),
+                                           o.stride(1), nat.IQ_BF16, st))
+
+    us = _graph_us(device, prefill, reps=3)
+    flops = 4 * Hq * D * Sq * (Sq + 1) / 2          # Q.K^T and P.V over the causal triangle
+    out["prefill_qwen_8k"] = {"tokens": Sq, "us": round(us, 1), "tflops": round(flops / (us * 1e-6) / 1e12, 1),
+                              "mfma_frac": round(flops / (us * 1e-6) / 1e12 / MFMA_BF16_PEAK_TFLOPS, 4)}
+    return out
 
 
 def time_paged(device, layers=4, n_seq=16, block=16, H=4, G=7, seed=4, steps=20):
@@ -606,6 +725,7 @@ def main():
     achieved = per_layer / (layer_us * 1e-6) / 1e9
     enc = None if args.no_encode else time_encode(device)
     paged = None if args.no_paged else time_paged(device)
+    nxt = None if args.no_next else time_next_rows(device)
     append = None
     if not args.no_append:
         append = time_append(device)
@@ -651,6 +771,8 @@ def main():
         result["decode_cfg2_k4_values"] = k4v
     if paged is not None:
         result["paged_cfg4"] = paged
+    if nxt is not None:
+        result.update(nxt)
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(layers[0], device)
     print(json.dumps(result))
