@@ -23,7 +23,7 @@ constexpr int D = 128;
 constexpr int QT = 64;              // queries per workgroup, 16 per wavefront
 constexpr int KT = 64;              // keys per tile
 constexpr int KROW = D + 8;         // halves per staged key row
-constexpr int VROW = KT / 2 + 4;    // key-pair dwords per staged V^T row
+constexpr int VROW = KT / 2 + 2;    // key-pair dwords per staged V^T row (34: the 16 rows of an operand read on distinct bank pairs)
 
 struct PrefillArgs {
     const uint16_t *q, *k, *v;
@@ -76,10 +76,13 @@ __global__ __launch_bounds__(256) void prefill_attn(PrefillArgs a)
             const int kk = k0 + r < len ? k0 + r : len - 1;
             *(u32x4 *)(sm.k + r * KROW + c) = ld16(kbase + (int64_t)kk * a.k_st + c);
         }
+        // V^T: thread (key pair p = lane % 32, 8 channels c) writes one dword
+        // per channel; the 32 key pairs of a channel row are consecutive
+        // dwords, so a wavefront's stores hit distinct banks
 #pragma unroll
         for (int it = 0; it < 2; ++it) {
             const int i = tid + 256 * it;
-            const int p = i >> 4, c = (i & 15) * 8;
+            const int p = i & 31, c = (i >> 5) * 8;
             const int ka = k0 + 2 * p < len ? k0 + 2 * p : len - 1;
             const int kb = k0 + 2 * p + 1 < len ? k0 + 2 * p + 1 : len - 1;
             const u32x4 r0 = ld16(vbase + (int64_t)ka * a.v_st + c);
@@ -101,17 +104,25 @@ __global__ __launch_bounds__(256) void prefill_attn(PrefillArgs a)
             for (int ks = 0; ks < 4; ++ks)
                 sc[j] = mma32<F16>(*(const u32x4 *)(sm.k + (16 * j + col) * KROW + 32 * ks + 8 * g), qb[ks], sc[j]);
         }
+        // raw logits: the scale is positive, so the maximum commutes with it
+        // and p = 2^(s c - m) takes one fma per logit.  Only a tile that
+        // reaches past this wavefront's first query or the sequence's end
+        // has keys to mask (wave-uniform).
+        if (k0 + KT - 1 > qw || k0 + KT > len) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int key = k0 + 16 * j + 4 * g + r;
+                    if (!(key <= my_q && key < len)) sc[j][r] = NEG_INF;
+                }
+        }
         float cmax = NEG_INF;
 #pragma unroll
         for (int j = 0; j < 4; ++j)
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int key = k0 + 16 * j + 4 * g + r;
-                const float s = (key <= my_q && key < len) ? sc[j][r] * a.c_log2 : NEG_INF;
-                sc[j][r] = s;
-                cmax = fmaxf(cmax, s);
-            }
-        cmax = xmax16(cmax);
+            for (int r = 0; r < 4; ++r) cmax = fmaxf(cmax, sc[j][r]);
+        cmax = xmax16(cmax) * a.c_log2;
         const float m_new = fmaxf(m_run, cmax);  // finite: key 0 is visible to every query
         const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
         float lsum = 0.0f;
@@ -121,7 +132,7 @@ __global__ __launch_bounds__(256) void prefill_attn(PrefillArgs a)
             float pr[4];
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                pr[r] = __builtin_amdgcn_exp2f(sc[j][r] - m_new);
+                pr[r] = __builtin_amdgcn_exp2f(fmaf(sc[j][r], a.c_log2, -m_new));
                 lsum += pr[r];
             }
             pb[j >> 1][2 * (j & 1)] = pack2<F16>(pr[0], pr[1]);
