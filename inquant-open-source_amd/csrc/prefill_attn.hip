@@ -9,8 +9,11 @@
 // [tokens, heads, 128] with runtime (token, head) strides; sequences are
 // delimited by cu_seqlens.
 //
-// One workgroup = 64 queries of one query head (16 per wavefront); key tiles
-// of 64 stream through LDS (K row-major, V transposed into key pairs).  Keys
+// One workgroup = 128 queries of one query head (8 wavefronts of 16: the
+// staging of each key tile is shared by twice the queries of a four-wavefront
+// group, 2.16 -> 1.15 ms for an 8K causal Qwen2.5-7B prefill together with
+// the conflict-free V transpose and edge-only masks); key tiles of 64 stream
+// through LDS (K row-major, V transposed into key pairs).  Keys
 // are the rows of S^T = K Q^T (v_mfma_f32_16x16x32, queries as columns), so
 // the softmax weights land in exactly the lanes and k-slots of the B operand
 // of O^T = V^T P^T and no transpose of P is needed.  Query tiles are
@@ -20,7 +23,9 @@
 namespace {
 
 constexpr int D = 128;
-constexpr int QT = 64;              // queries per workgroup, 16 per wavefront
+constexpr int NW = 8;               // wavefronts per workgroup
+constexpr int NT = 64 * NW;         // threads per workgroup
+constexpr int QT = 16 * NW;         // queries per workgroup, 16 per wavefront
 constexpr int KT = 64;              // keys per tile
 constexpr int KROW = D + 8;         // halves per staged key row
 constexpr int VROW = KT / 2 + 2;    // key-pair dwords per staged V^T row (34: the 16 rows of an operand read on distinct bank pairs)
@@ -41,7 +46,7 @@ struct __attribute__((aligned(16))) PrefillSmem {
 };
 
 template <bool F16>
-__global__ __launch_bounds__(256) void prefill_attn(PrefillArgs a)
+__global__ __launch_bounds__(NT) void prefill_attn(PrefillArgs a)
 {
     __shared__ PrefillSmem sm;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -70,8 +75,8 @@ __global__ __launch_bounds__(256) void prefill_attn(PrefillArgs a)
         __syncthreads();                         // the previous tile's reads are done
         // keys [k0, k0 + 64) (rows past the sequence read its last row and are masked)
 #pragma unroll
-        for (int it = 0; it < 4; ++it) {
-            const int i = tid + 256 * it;
+        for (int it = 0; it < KT * 16 / NT; ++it) {
+            const int i = tid + NT * it;
             const int r = i >> 4, c = (i & 15) * 8;
             const int kk = k0 + r < len ? k0 + r : len - 1;
             *(u32x4 *)(sm.k + r * KROW + c) = ld16(kbase + (int64_t)kk * a.k_st + c);
@@ -80,8 +85,8 @@ __global__ __launch_bounds__(256) void prefill_attn(PrefillArgs a)
         // per channel; the 32 key pairs of a channel row are consecutive
         // dwords, so a wavefront's stores hit distinct banks
 #pragma unroll
-        for (int it = 0; it < 2; ++it) {
-            const int i = tid + 256 * it;
+        for (int it = 0; it < KT * 8 / NT; ++it) {
+            const int i = tid + NT * it;
             const int p = i & 31, c = (i >> 5) * 8;
             const int ka = k0 + 2 * p < len ? k0 + 2 * p : len - 1;
             const int kb = k0 + 2 * p + 1 < len ? k0 + 2 * p + 1 : len - 1;
@@ -183,7 +188,7 @@ extern "C" int iq_prefill_attention(const void *q, const void *k, const void *v,
                  "iq_prefill_attention: q/k/v rows must be 16-byte aligned");
     PrefillArgs a{(const uint16_t *)q, (const uint16_t *)k, (const uint16_t *)v, out, q_st, q_sh, k_st, k_sh,
                   v_st, v_sh, o_st, o_sh, cu_seqlens, (int)(Hq / H), scale * 1.44269504088896341f, out_dtype};
-    const dim3 grid((unsigned)((max_seqlen + QT - 1) / QT), (unsigned)Hq, (unsigned)n_seq), block(256);
+    const dim3 grid((unsigned)((max_seqlen + QT - 1) / QT), (unsigned)Hq, (unsigned)n_seq), block(NT);
     if (dtype == IQ_F16) hipLaunchKernelGGL(prefill_attn<true>, grid, block, 0, (hipStream_t)stream, a);
     else hipLaunchKernelGGL(prefill_attn<false>, grid, block, 0, (hipStream_t)stream, a);
     IQ_CHECK_LAUNCH("prefill_attn");
