@@ -71,27 +71,45 @@ __global__ __launch_bounds__(NT) void prefill_attn(PrefillArgs a)
 #pragma unroll
     for (int rb = 0; rb < 8; ++rb) acc[rb] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
     const int kend = q0 + QT < len ? q0 + QT : len;
-    for (int k0 = 0; k0 < kend; k0 += KT) {
-        __syncthreads();                         // the previous tile's reads are done
-        // keys [k0, k0 + 64) (rows past the sequence read its last row and are masked)
+    // Key tiles are double-buffered through registers: tile k0 + 64 is read
+    // from global memory while tile k0 is computed, then written to LDS.
+    // Rows past the sequence read its last row and are masked.
+    constexpr int KIT = KT * 16 / NT, VIT = KT * 8 / NT;
+    u32x4 kreg[KIT], vreg[VIT][2];
+    auto load_tile = [&](int k0) {
 #pragma unroll
-        for (int it = 0; it < KT * 16 / NT; ++it) {
+        for (int it = 0; it < KIT; ++it) {
             const int i = tid + NT * it;
             const int r = i >> 4, c = (i & 15) * 8;
             const int kk = k0 + r < len ? k0 + r : len - 1;
-            *(u32x4 *)(sm.k + r * KROW + c) = ld16(kbase + (int64_t)kk * a.k_st + c);
+            kreg[it] = ld16(kbase + (int64_t)kk * a.k_st + c);
+        }
+#pragma unroll
+        for (int it = 0; it < VIT; ++it) {
+            const int i = tid + NT * it;
+            const int p = i & 31, c = (i >> 5) * 8;
+            const int ka = k0 + 2 * p < len ? k0 + 2 * p : len - 1;
+            const int kb = k0 + 2 * p + 1 < len ? k0 + 2 * p + 1 : len - 1;
+            vreg[it][0] = ld16(vbase + (int64_t)ka * a.v_st + c);
+            vreg[it][1] = ld16(vbase + (int64_t)kb * a.v_st + c);
+        }
+    };
+    load_tile(0);
+    for (int k0 = 0; k0 < kend; k0 += KT) {
+        __syncthreads();                         // the previous tile's reads are done
+#pragma unroll
+        for (int it = 0; it < KIT; ++it) {
+            const int i = tid + NT * it;
+            *(u32x4 *)(sm.k + (i >> 4) * KROW + (i & 15) * 8) = kreg[it];
         }
         // V^T: thread (key pair p = lane % 32, 8 channels c) writes one dword
         // per channel; the 32 key pairs of a channel row are consecutive
         // dwords, so a wavefront's stores hit distinct banks
 #pragma unroll
-        for (int it = 0; it < KT * 8 / NT; ++it) {
+        for (int it = 0; it < VIT; ++it) {
             const int i = tid + NT * it;
             const int p = i & 31, c = (i >> 5) * 8;
-            const int ka = k0 + 2 * p < len ? k0 + 2 * p : len - 1;
-            const int kb = k0 + 2 * p + 1 < len ? k0 + 2 * p + 1 : len - 1;
-            const u32x4 r0 = ld16(vbase + (int64_t)ka * a.v_st + c);
-            const u32x4 r1 = ld16(vbase + (int64_t)kb * a.v_st + c);
+            const u32x4 r0 = vreg[it][0], r1 = vreg[it][1];
 #pragma unroll
             for (int w = 0; w < 4; ++w) {
                 sm.vt[(c + 2 * w) * VROW + p] = __builtin_amdgcn_perm(r1[w], r0[w], 0x05040100u);
@@ -99,6 +117,7 @@ __global__ __launch_bounds__(NT) void prefill_attn(PrefillArgs a)
             }
         }
         __syncthreads();
+        if (k0 + KT < kend) load_tile(k0 + KT);
         if (k0 > qw + 15) continue;              // every key of this tile is after this wavefront's queries
         // S^T (keys x queries) for four 16-key subtiles; lane holds keys 16 j + 4 g + r of column my_q
         f32x4 sc[4];
