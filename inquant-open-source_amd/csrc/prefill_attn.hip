@@ -11,9 +11,12 @@
 //
 // One workgroup = 128 queries of one query head (8 wavefronts of 16: the
 // staging of each key tile is shared by twice the queries of a four-wavefront
-// group, 2.16 -> 1.15 ms for an 8K causal Qwen2.5-7B prefill together with
-// the conflict-free V transpose and edge-only masks); key tiles of 64 stream
-// through LDS (K row-major, V transposed into key pairs).  Keys
+// group, 2.16 -> 1.13 ms for an 8K causal Qwen2.5-7B prefill together with
+// the conflict-free V transpose, edge-only masks and register double
+// buffering; two 16-query subtiles per wavefront, sharing the K and V
+// operands, measured slower at 188 VGPRs: 1.33 ms with eight wavefronts,
+// 1.55 ms with four); key tiles of 64 stream through LDS (K row-major, V
+// transposed into key pairs).  Keys
 // are the rows of S^T = K Q^T (v_mfma_f32_16x16x32, queries as columns), so
 // the softmax weights land in exactly the lanes and k-slots of the B operand
 // of O^T = V^T P^T and no transpose of P is needed.  Query tiles are
