@@ -275,6 +275,82 @@ __device__ __forceinline__ float tile_f32(uint32_t bits16)
     else return __uint_as_float(bits16 << 16);
 }
 
+// The eight 4-bit slots of channels 8 j .. 8 j + 7 (one packed word per
+// token): per-slot constants, computed once from the role tables and pinned
+// in registers (opaque to the compiler, which would otherwise rebuild them
+// from the role masks at every token: four extra instructions per element).
+// srcc[e] is the channel whose value slot e encodes: its own, or for a donor
+// slot its source's.
+struct K4Slots {
+    float scl[8], rscl[8], lim[8], bias[8];
+    uint32_t shift[8];
+    int srcc[8];
+
+    __device__ __forceinline__ void init(int j, const uint8_t *is_src, const int16_t *src_of, const float *scale)
+    {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const int c = 8 * j + e;
+            const bool hi = is_src[c];
+            const int owner = src_of[c];
+            const bool lo = !hi && owner >= 0;
+            srcc[e] = lo ? owner : c;
+            scl[e] = scale[srcc[e]];
+            rscl[e] = __builtin_amdgcn_rcpf(scl[e]);
+            lim[e] = (hi || lo) ? 127.0f : 7.0f;
+            // q + lim + 1 lands in the low mantissa bits of 1.5 * 2^23 + (lim + 1)
+            bias[e] = 12582912.0f + lim[e] + 1.0f;
+            shift[e] = hi ? 4u : 0u;
+            asm volatile("" : "+v"(scl[e]), "+v"(rscl[e]), "+v"(lim[e]), "+v"(bias[e]), "+v"(shift[e]));
+        }
+    }
+
+    // The packed word of one token, v[e] the value of channel srcc[e].  The
+    // reciprocal quotient f decides the rounding unless it is within 2^-13
+    // of a half-integer, where the IEEE quotient decides.  Below |f| = 256,
+    // f is within 2^-14 of the IEEE quotient (v_rcp_f32 is within 1 ulp,
+    // plus the product's rounding, plus the quotient's own half ulp), so no
+    // rounding can differ outside that band; beyond it every code clamps to
+    // +-lim either way.  The band test is one max over the lane's eight
+    // distances; the rare lanes inside it redo only the slots that are.
+    __device__ __forceinline__ uint32_t word(const float (&v)[8]) const
+    {
+        float f[8], q[8];
+        float dmax = 0.0f;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            f[e] = __fmul_rn(v[e], rscl[e]);
+            q[e] = rintf(f[e]);
+            dmax = fmaxf(dmax, fabsf(__fsub_rn(f[e], q[e])));
+        }
+        constexpr float band = 0.5f - 0x1p-13f;
+        if (__builtin_expect(dmax >= band, 0)) {
+#pragma unroll
+            for (int e = 0; e < 8; ++e)
+                if (fabsf(__fsub_rn(f[e], q[e])) >= band) q[e] = rintf(v[e] / scl[e]);
+        }
+        uint32_t w = 0;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const float qc = __builtin_amdgcn_fmed3f(q[e], -lim[e], lim[e]);
+            const uint32_t code = __float_as_uint(__fadd_rn(qc, bias[e]));
+            w |= __builtin_amdgcn_ubfe(code, shift[e], 4) << (4 * e);
+        }
+        return w;
+    }
+};
+
+// The V2 codes and group parameters of token t of head h in a page (value
+// lanes of 16 channels, vj = 0 .. 7, four lanes per 64-channel group).
+__device__ __forceinline__ void store_page_values(const K4Args &a, uint8_t *page, int64_t h, int T, int t, int vj,
+                                                  uint32_t code, uint16_t off_h, uint16_t sc_h)
+{
+    const int64_t r = h * T + t;
+    ((uint32_t *)(page + a.off_vpay + r * 32))[vj] = code;
+    if ((vj & 3) == 0) ((uint16_t *)(page + a.off_voff))[r * 2 + (vj >> 2)] = off_h;
+    if ((vj & 3) == 3) ((uint16_t *)(page + a.off_vscale))[r * 2 + (vj >> 2)] = sc_h;
+}
+
 // NCH > 0: the block length is NCH chunks (a sealed cache block), known at
 // compile time, so the chunk loops unroll without branches and each load is
 // waited for exactly when its chunk is stored (a branch around loads makes
@@ -532,9 +608,7 @@ __device__ __forceinline__ void k4_tile_body(const K4Args &a, int64_t b, int64_t
         if constexpr (VBITS > 0) v_encode16<F16IN, VBITS, GLV>(r, live, code, off_h, sc_h, vbad);
         if (VBITS > 0 && live) {
             if constexpr (PAGES) {
-                ((uint32_t *)(page + a.off_vpay + (h * T + t) * (TILE_D / 4)))[vj] = code[0];
-                if ((vj & 3) == 0) ((uint16_t *)(page + a.off_voff))[(h * T + t) * 2 + (vj >> 2)] = off_h;
-                if ((vj & 3) == 3) ((uint16_t *)(page + a.off_vscale))[(h * T + t) * 2 + (vj >> 2)] = sc_h;
+                store_page_values(a, page, h, T, t, vj, code[0], off_h, sc_h);
             } else {
                 constexpr int PB = TILE_D * (VBITS > 0 ? VBITS : 2) / 8;   // payload bytes per token
                 constexpr int GROUPS = 8 / GLV;
@@ -621,31 +695,13 @@ __device__ __forceinline__ void k4_tile_body(const K4Args &a, int64_t b, int64_t
     // ---- pass 2: quantize; thread owns channels 8 j .. 8 j + 7 of tokens
     // t0 + 8 wave + tq and t0 + 8 wave + tq + 4 of every chunk
     const int j = lane & 15, tq = lane >> 4;
-    // Per-slot constants, computed once and pinned in registers (opaque to
-    // the compiler, which would otherwise rebuild them from the role masks at
-    // every token: four extra instructions per element).  xe[e] is the LDS
-    // address of the value slot e encodes (its own channel, or for a donor
-    // slot its source's) in row 8 wave + tq of buffer 0; every other row and
-    // buffer is a constant offset from it.
-    float scl[8], rscl[8], lim[8], bias[8];
-    uint32_t shift[8];
+    K4Slots slots;
+    slots.init(j, s_is_src, s_src_of, s_scale);
+    // xe[e]: LDS address of slot e's value in row 8 wave + tq of buffer 0;
+    // every other row and buffer is a constant offset from it
     const uint16_t *xe[8];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-        const int c = 8 * j + e;
-        const bool hi = s_is_src[c];
-        const int owner = s_src_of[c];
-        const bool lo = !hi && owner >= 0;
-        const int srcc = lo ? owner : c;
-        scl[e] = s_scale[srcc];
-        rscl[e] = __builtin_amdgcn_rcpf(scl[e]);
-        lim[e] = (hi || lo) ? 127.0f : 7.0f;
-        // q + lim + 1 lands in the low mantissa bits of 1.5 * 2^23 + (lim + 1)
-        bias[e] = 12582912.0f + lim[e] + 1.0f;
-        shift[e] = hi ? 4u : 0u;
-        xe[e] = &s_x[0][0] + (8 * wave + tq) * ROWLEN + srcc;
-        asm volatile("" : "+v"(scl[e]), "+v"(rscl[e]), "+v"(lim[e]), "+v"(bias[e]), "+v"(shift[e]));
-    }
+    for (int e = 0; e < 8; ++e) xe[e] = &s_x[0][0] + (8 * wave + tq) * ROWLEN + slots.srcc[e];
     if constexpr (PAGES) {
         if (tid < TILE_D) ((int16_t *)(page + a.off_kmap))[h * TILE_D + tid] = s_role[tid];
     }
@@ -658,39 +714,10 @@ __device__ __forceinline__ void k4_tile_body(const K4Args &a, int64_t b, int64_t
             const int tl = 8 * wave + 4 * it + tq, t = t0 + tl;
             if (t < T) {
                 const int off = (DMA ? ch % NBUF : ch & 1) * CH * ROWLEN + 4 * it * ROWLEN;
-                // The reciprocal quotient f decides the rounding unless it is
-                // within 2^-13 of a half-integer, where the IEEE quotient
-                // decides.  Below |f| = 256, f is within 2^-14 of the IEEE
-                // quotient (v_rcp_f32 is within 1 ulp, plus the product's
-                // rounding, plus the quotient's own half ulp), so no rounding
-                // can differ outside that band; beyond it every code clamps to
-                // +-lim either way.  The band test is one max over the lane's
-                // eight distances; the rare lanes inside it redo only the
-                // slots that are.
-                float v[8], f[8], q[8];
+                float v[8];
 #pragma unroll
                 for (int e = 0; e < 8; ++e) v[e] = tile_f32<F16IN>(xe[e][off]);
-                float dmax = 0.0f;
-#pragma unroll
-                for (int e = 0; e < 8; ++e) {
-                    f[e] = __fmul_rn(v[e], rscl[e]);
-                    q[e] = rintf(f[e]);
-                    dmax = fmaxf(dmax, fabsf(__fsub_rn(f[e], q[e])));
-                }
-                constexpr float band = 0.5f - 0x1p-13f;
-                if (__builtin_expect(dmax >= band, 0)) {
-#pragma unroll
-                    for (int e = 0; e < 8; ++e)
-                        if (fabsf(__fsub_rn(f[e], q[e])) >= band) q[e] = rintf(v[e] / scl[e]);
-                }
-                uint32_t word = 0;
-#pragma unroll
-                for (int e = 0; e < 8; ++e) {
-                    const float qc = __builtin_amdgcn_fmed3f(q[e], -lim[e], lim[e]);
-                    const uint32_t code = __float_as_uint(__fadd_rn(qc, bias[e]));
-                    word |= __builtin_amdgcn_ubfe(code, shift[e], 4) << (4 * e);
-                }
-                out[t * (TILE_D / 8) + j] = word;
+                out[t * (TILE_D / 8) + j] = slots.word(v);
             }
         }
     });
@@ -712,6 +739,176 @@ __global__ __launch_bounds__(K4_THREADS, 4) void k4_encode_pair(K4Args ak, K4Arg
     const K4Args a = val ? av : ak;
     k4_tile_body<F16IN, NCH>(a, blockIdx.x, val ? blockIdx.y - ak.H : blockIdx.y,
                              (int)(blockIdx.x + gridDim.x * blockIdx.y));
+}
+
+// Pages of T = 16 or 32 tokens: one wavefront encodes one (page, head) row,
+// keys and values, and a workgroup holds four rows (pages 4 blockIdx.x + wave
+// of head blockIdx.y) that share nothing, so there is no workgroup barrier.
+// A short row keeps the serial phases of the 256-thread tile encoder (the
+// donor selection is the same 16 picks for 16 tokens as for 256) while its
+// other waves idle; here each wavefront runs its own row from start to end
+// and a compute unit interleaves twenty rows.  The arithmetic and its order
+// are the tile encoder's, so the page bytes are the same:
+//   lane l owns channels 2 l and 2 l + 1 for the statistics (fp64 Welford
+//   with the exact reciprocals 1 / n, amax as 16-bit magnitudes, sampled sums
+//   in torch's cascade order), iq_select_wave128 makes the selection, lane
+//   (j, tq) = (l % 16, l / 16) packs channels 8 j .. 8 j + 7 of tokens
+//   tq + 4 i, and lane (vj, vt) = (l % 8, l / 8) encodes channels
+//   16 vj .. 16 vj + 15 of value tokens vt + 8 i.
+// Lanes read LDS words other lanes of the same wavefront wrote: a
+// wavefront's LDS operations complete in order, so the wavefront-scope
+// fences emit nothing and only keep the compiler from reordering.
+template <bool F16IN, int T>
+__global__ __launch_bounds__(K4_THREADS) void k4_encode_page_rows(K4Args a, int64_t n_pages)
+{
+    static_assert(T == 16 || T == 32, "short pages");
+    constexpr int ROW = TILE_D + 8;            // u16 per staged token row
+    constexpr int KSEG = T * (TILE_D / 8) / 64; // 16-byte key segments per lane
+    constexpr int VIT = T / 8;                 // value tokens per lane
+    __shared__ __attribute__((aligned(16))) uint16_t s_x[4][T * ROW];
+    __shared__ __attribute__((aligned(8))) float s_sal[4][TILE_D], s_err[4][TILE_D], s_mean[4][TILE_D];
+    __shared__ int16_t s_src[4][TILE_D / 2], s_don[4][TILE_D / 2], s_src_of[4][TILE_D], s_role[4][TILE_D];
+    __shared__ int16_t s_list[4][TILE_D / 2];
+    __shared__ uint8_t s_is_src[4][TILE_D];
+
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int64_t b = (int64_t)blockIdx.x * 4 + wave, h = blockIdx.y;
+    if (blockIdx.x == 0 && h == 0 && threadIdx.x < 2) a.clear[threadIdx.x] = 0;
+    if (b >= n_pages) return;                  // wave-uniform, as the page check below
+    const int64_t id = a.id_bytes == 8 ? ((const int64_t *)a.ids)[b] : (int64_t)((const int32_t *)a.ids)[b];
+    if (id < 0 || id >= a.pool_pages) return;
+    uint8_t *const page = a.pool + id * a.page_bytes;
+    const uint16_t *const xr = (const uint16_t *)a.x + b * a.sb + h * a.sh;
+    const uint16_t *const vr = a.v + b * a.vsb + h * a.vsh;
+
+    // every load of the row first: key segment i = lane + 64 k is token i / 16,
+    // channels 8 (i % 16) ..; value lane (vj, vt) reads 16 channels of token vt + 8 it
+    const int vj = lane & 7, vt = lane >> 3;
+    u32x4_t kseg[KSEG], vraw[VIT][2];
+#pragma unroll
+    for (int k = 0; k < KSEG; ++k) {
+        const int i = lane + 64 * k;
+        kseg[k] = *(const u32x4_t *)(xr + (int64_t)(i >> 4) * a.st + 8 * (i & 15));
+    }
+#pragma unroll
+    for (int it = 0; it < VIT; ++it) {
+        const u32x4_t *p = (const u32x4_t *)(vr + (int64_t)(vt + 8 * it) * a.vst + 16 * vj);
+        vraw[it][0] = __builtin_nontemporal_load(p);
+        vraw[it][1] = __builtin_nontemporal_load(p + 1);
+    }
+    uint16_t *const xs = s_x[wave];
+#pragma unroll
+    for (int k = 0; k < KSEG; ++k) {
+        const int i = lane + 64 * k;
+        *(u32x4_t *)(xs + (i >> 4) * ROW + 8 * (i & 15)) = kseg[k];
+    }
+    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+
+    // ---- statistics of channels 2 lane and 2 lane + 1
+    double mean[2] = {0.0, 0.0}, m2[2] = {0.0, 0.0};
+    uint32_t amax_bits[2] = {0u, 0u};
+#pragma unroll
+    for (int t = 0; t < T; ++t) {
+        const uint32_t w = *(const uint32_t *)(xs + t * ROW + 2 * lane);
+        const double y = 1.0 / (double)(t + 1), n = (double)(t + 1);
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+            const uint32_t u = e ? w >> 16 : w & 0xffffu;
+            amax_bits[e] = max(amax_bits[e], u & 0x7fffu);
+            const double dv = (double)tile_f32<F16IN>(u);
+            const double delta = __dsub_rn(dv, mean[e]);
+            const double q0 = __dmul_rn(delta, y);
+            const double r = __builtin_fma(-q0, n, delta);
+            mean[e] = __dadd_rn(mean[e], __builtin_fma(r, y, q0));
+            m2[e] = __dadd_rn(m2[e], __dmul_rn(delta, __dsub_rn(dv, mean[e])));
+        }
+    }
+    const int stride = (int)min(a.stride, (int64_t)TILE_T);   // a larger stride samples token 0 only
+    const int ns = (T + stride - 1) / stride;
+    IqCascade sa[2], sm[2];
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+        sa[e].init(ns);
+        sm[e].init(ns);
+    }
+    for (int t = 0; t < T; t += stride) {
+        const uint32_t w = *(const uint32_t *)(xs + t * ROW + 2 * lane);
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+            const float v = tile_f32<F16IN>(e ? w >> 16 : w & 0xffffu);
+            sa[e].add(fabsf(v));
+            sm[e].add(v);
+        }
+    }
+    float amax[2];
+    bool kbad = false;
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+        const int c = 2 * lane + e;
+        const float smean = sm[e].finish() / (float)ns;
+        const float diff = __fsub_rn((float)mean[e], smean);
+        s_err[wave][c] = __fadd_rn((float)(m2[e] / (double)T), __fmul_rn(diff, diff));
+        s_sal[wave][c] = sa[e].finish() / (float)ns;
+        s_mean[wave][c] = smean;
+        amax[e] = tile_f32<F16IN>(amax_bits[e]);
+        kbad |= amax_bits[e] >= (F16IN ? 0x7c00u : 0x7f80u);   // an inf or NaN in the channel
+    }
+    if (__ballot(kbad) != 0 && lane == 0) atomicOr(a.bad, 1);
+
+    // ---- values, while the selection's inputs settle
+    bool vbad = false;
+#pragma unroll
+    for (int it = 0; it < VIT; ++it) {
+        uint32_t code[1];
+        uint16_t off_h, sc_h;
+        v_encode16<F16IN, 2, 4>(vraw[it], true, code, off_h, sc_h, vbad);
+        store_page_values(a, page, h, T, vt + 8 * it, vj, code[0], off_h, sc_h);
+    }
+    if (__ballot(vbad) != 0 && lane == 0) atomicOr(a.vbad, 1);
+
+    // ---- selection, scales, role map and padding
+    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+    const int count = (int)a.count;
+    iq_select_wave128(s_sal[wave], s_err[wave], count, s_src[wave], s_don[wave], s_is_src[wave], s_src_of[wave],
+                      s_list[wave]);
+    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+    const float flt_min = 1.17549435e-38f;
+    float *const kscale = (float *)(page + a.off_kscale) + h * TILE_D;
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+        const int c = 2 * lane + e;
+        const float s = amax[e] / (s_is_src[wave][c] ? 127.0f : 7.0f);
+        const float sc = s < flt_min ? flt_min : s;
+        s_sal[wave][c] = sc;                   // the saliencies are spent: scales from here on
+        kscale[c] = sc;
+        s_role[wave][c] = -1;
+    }
+    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+    if (lane < count) {
+        // page role map: the donor channel for a source, -2 - k for donor k
+        const int s = s_src[wave][lane], d = s_don[wave][lane];
+        s_role[wave][s] = (int16_t)d;
+        s_role[wave][d] = (int16_t)(-2 - lane);
+        ((float *)(page + a.off_kpad))[h * count + lane] = s_mean[wave][d];
+    }
+    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+    int16_t *const kmap = (int16_t *)(page + a.off_kmap) + h * TILE_D;
+    kmap[2 * lane] = s_role[wave][2 * lane];
+    kmap[2 * lane + 1] = s_role[wave][2 * lane + 1];
+
+    // ---- 4-bit slots
+    const int j = lane & 15, tq = lane >> 4;
+    K4Slots slots;
+    slots.init(j, s_is_src[wave], s_src_of[wave], s_sal[wave]);
+    uint32_t *const out = (uint32_t *)(page + a.off_kpay + h * (int64_t)T * (TILE_D / 2));
+#pragma unroll
+    for (int it = 0; it < T / 4; ++it) {
+        const int t = tq + 4 * it;
+        float v[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[e] = tile_f32<F16IN>(xs[t * ROW + slots.srcc[e]]);
+        out[t * (TILE_D / 8) + j] = slots.word(v);
+    }
 }
 
 struct SelectArgs {
@@ -986,8 +1183,21 @@ extern "C" int iq_encode_pages(const void *keys, const void *values, int dtype, 
     a.vbad = flags + 1;
     a.clear = next_flags;
     if (n_pages == 0) return IQ_OK;
-    const dim3 grid((unsigned)n_pages, (unsigned)H), block(K4_THREADS);
     const hipStream_t st = (hipStream_t)stream;
+    if (B <= 32) {
+        // one wavefront per (page, head) row, four pages of one head per workgroup
+        const dim3 rows_grid((unsigned)((n_pages + 3) / 4), (unsigned)H);
+        if (dtype == IQ_F16) {
+            if (B == 16) hipLaunchKernelGGL((k4_encode_page_rows<true, 16>), rows_grid, dim3(K4_THREADS), 0, st, a, n_pages);
+            else hipLaunchKernelGGL((k4_encode_page_rows<true, 32>), rows_grid, dim3(K4_THREADS), 0, st, a, n_pages);
+        } else {
+            if (B == 16) hipLaunchKernelGGL((k4_encode_page_rows<false, 16>), rows_grid, dim3(K4_THREADS), 0, st, a, n_pages);
+            else hipLaunchKernelGGL((k4_encode_page_rows<false, 32>), rows_grid, dim3(K4_THREADS), 0, st, a, n_pages);
+        }
+        IQ_CHECK_LAUNCH("k4_encode_page_rows");
+        return IQ_OK;
+    }
+    const dim3 grid((unsigned)n_pages, (unsigned)H), block(K4_THREADS);
     if (dtype == IQ_F16) {
         if (B == TILE_T) hipLaunchKernelGGL((k4_encode_tile<true, TILE_T / CH, true>), grid, block, 0, st, a);
         else hipLaunchKernelGGL((k4_encode_tile<true, 0, true>), grid, block, 0, st, a);

@@ -204,6 +204,75 @@ __device__ __forceinline__ int iq_lane_bit_above(uint64_t m0, uint64_t m1, int p
     return w0 ? __builtin_ctzll(w0) : w1 ? 64 + __builtin_ctzll(w1) : 128;
 }
 
+// The sequential donor picks of iq_select_wave_t<2> for one D = 128 row, run
+// by one wavefront: sel0 / sel1 mark the sources (channels lane and
+// 64 + lane), av0 / av1 the channels that may donate.  The neighbour order
+// and run boundaries are precomputed one source per lane, so a pick with a
+// free neighbour is a handful of scalar operations.  LDS scratch: list[64].
+__device__ __forceinline__ void iq_pick_donors128(const float *sal, uint64_t sel0, uint64_t sel1, uint64_t av0,
+                                                  uint64_t av1, int count, int16_t *src_out, int16_t *don_out,
+                                                  uint8_t *is_src, int16_t *src_of, int16_t *list)
+{
+    const int lane = threadIdx.x & 63;
+    const uint64_t below = (1ull << lane) - 1;
+    if ((sel0 >> lane) & 1ull) list[__popcll(sel0 & below)] = (int16_t)lane;
+    if ((sel1 >> lane) & 1ull) list[__popcll(sel0) + __popcll(sel1 & below)] = (int16_t)(64 + lane);
+    // lanes read list entries other lanes of this wavefront wrote: LDS
+    // operations of a wavefront complete in order, so this fence emits
+    // nothing; it keeps the compiler from moving the reads above the writes
+    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+    is_src[lane] = (uint8_t)((sel0 >> lane) & 1ull);
+    is_src[64 + lane] = (uint8_t)((sel1 >> lane) & 1ull);
+    src_of[lane] = -1;
+    src_of[64 + lane] = -1;
+    const uint32_t sk0 = iq_nonneg_bits(sal[lane]), sk1 = iq_nonneg_bits(sal[64 + lane]);
+    // lane i: the i-th source s, whether its left neighbour wins a saliency
+    // comparison with the right one, and its selected run [lb, rb], packed
+    // into one word so that a pick reads them with a single readlane
+    const int s = lane < count ? list[lane] : 0;
+    const uint32_t kl = s >= 1 ? iq_nonneg_bits(sal[s - 1]) : ~0u;
+    const uint32_t kr = s + 1 < 128 ? iq_nonneg_bits(sal[s + 1]) : ~0u;
+    const int lb = iq_lane_bit_below(~sel0, ~sel1, s) + 1;
+    const int rb = iq_lane_bit_above(~sel0, ~sel1, s) - 1;
+    const uint32_t wv = (uint32_t)s | ((kl <= kr ? 1u : 0u) << 8) | ((uint32_t)lb << 9) | ((uint32_t)(rb + 1) << 17);
+    int don_v = 0;
+    for (int i = 0; i < count; ++i) {
+        const uint32_t w = __builtin_amdgcn_readlane(wv, i);
+        const int si = (int)(w & 255u), l1 = si - 1, r1 = si + 1;
+        const bool lo = l1 >= 0 && (((l1 < 64 ? av0 : av1) >> (l1 & 63)) & 1ull);
+        const bool ro = r1 < 128 && (((r1 < 64 ? av0 : av1) >> (r1 & 63)) & 1ull);
+        int donor;
+        if (lo || ro) {
+            donor = (lo && (!ro || ((w >> 8) & 1u))) ? l1 : r1;
+        } else {
+            // the nearest available channel below the run or above it; less
+            // saliency, then the lower channel, on a distance tie
+            const int lbi = (int)((w >> 9) & 255u), rbi = (int)((w >> 17) & 255u) - 1;
+            const uint64_t m[2] = {av0, av1};
+            const int pl = iq_bit_below<2>(m, lbi);
+            const int pr = iq_bit_above<2>(m, rbi, 128);
+            const int dl = pl >= 0 ? lbi - pl : 0x7fffffff;
+            const int dr = pr < 128 ? pr - rbi : 0x7fffffff;
+            donor = 0;            // an empty pool only arises from non-finite statistics
+            if (dl < dr) donor = pl;
+            else if (dr < dl) donor = pr;
+            else if (dl != 0x7fffffff) {
+                const uint32_t ka = __builtin_amdgcn_readlane(pl < 64 ? sk0 : sk1, pl & 63);
+                const uint32_t kb = __builtin_amdgcn_readlane(pr < 64 ? sk0 : sk1, pr & 63);
+                donor = ka <= kb ? pl : pr;
+            }
+        }
+        if (donor < 64) av0 &= ~(1ull << donor);
+        else av1 &= ~(1ull << (donor - 64));
+        don_v = lane == i ? donor : don_v;
+    }
+    if (lane < count) {
+        src_out[lane] = (int16_t)s;
+        don_out[lane] = (int16_t)don_v;
+        src_of[don_v] = (int16_t)s;
+    }
+}
+
 // The selection of iq_select_wave_t<2> for one D = 128 row, computed by a
 // whole 256-thread workgroup (every thread calls it: it holds barriers).
 // Sources and the min_error pool come from ranks over all channel pairs:
@@ -261,65 +330,63 @@ __device__ __forceinline__ void iq_select_tile128(const float *sal, const float 
 
     // 3. sequential donor picks on wave 0; sources in ascending channel order
     const uint32_t f0 = flag[lane], f1 = flag[64 + lane];
-    const uint64_t sel0 = __ballot(f0 & 1u), sel1 = __ballot(f1 & 1u);
-    uint64_t av0 = __ballot(f0 & 2u), av1 = __ballot(f1 & 2u);
-    const uint64_t below = (1ull << lane) - 1;
-    if (f0 & 1u) list[__popcll(sel0 & below)] = (int16_t)lane;
-    if (f1 & 1u) list[__popcll(sel0) + __popcll(sel1 & below)] = (int16_t)(64 + lane);
-    // lanes read list entries other lanes of this wavefront wrote: LDS
-    // operations of a wavefront complete in order, so this fence emits
-    // nothing; it keeps the compiler from moving the reads above the writes
-    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
-    is_src[lane] = (uint8_t)(f0 & 1u);
-    is_src[64 + lane] = (uint8_t)(f1 & 1u);
-    src_of[lane] = -1;
-    src_of[64 + lane] = -1;
-    const uint32_t sk0 = iq_nonneg_bits(sal[lane]), sk1 = iq_nonneg_bits(sal[64 + lane]);
-    // lane i: the i-th source s, whether its left neighbour wins a saliency
-    // comparison with the right one, and its selected run [lb, rb], packed
-    // into one word so that a pick reads them with a single readlane
-    const int s = lane < count ? list[lane] : 0;
-    const uint32_t kl = s >= 1 ? iq_nonneg_bits(sal[s - 1]) : ~0u;
-    const uint32_t kr = s + 1 < 128 ? iq_nonneg_bits(sal[s + 1]) : ~0u;
-    const int lb = iq_lane_bit_below(~sel0, ~sel1, s) + 1;
-    const int rb = iq_lane_bit_above(~sel0, ~sel1, s) - 1;
-    const uint32_t wv = (uint32_t)s | ((kl <= kr ? 1u : 0u) << 8) | ((uint32_t)lb << 9) | ((uint32_t)(rb + 1) << 17);
-    int don_v = 0;
-    for (int i = 0; i < count; ++i) {
-        const uint32_t w = __builtin_amdgcn_readlane(wv, i);
-        const int si = (int)(w & 255u), l1 = si - 1, r1 = si + 1;
-        const bool lo = l1 >= 0 && (((l1 < 64 ? av0 : av1) >> (l1 & 63)) & 1ull);
-        const bool ro = r1 < 128 && (((r1 < 64 ? av0 : av1) >> (r1 & 63)) & 1ull);
-        int donor;
-        if (lo || ro) {
-            donor = (lo && (!ro || ((w >> 8) & 1u))) ? l1 : r1;
-        } else {
-            // the nearest available channel below the run or above it; less
-            // saliency, then the lower channel, on a distance tie
-            const int lbi = (int)((w >> 9) & 255u), rbi = (int)((w >> 17) & 255u) - 1;
-            const uint64_t m[2] = {av0, av1};
-            const int pl = iq_bit_below<2>(m, lbi);
-            const int pr = iq_bit_above<2>(m, rbi, 128);
-            const int dl = pl >= 0 ? lbi - pl : 0x7fffffff;
-            const int dr = pr < 128 ? pr - rbi : 0x7fffffff;
-            donor = 0;            // an empty pool only arises from non-finite statistics
-            if (dl < dr) donor = pl;
-            else if (dr < dl) donor = pr;
-            else if (dl != 0x7fffffff) {
-                const uint32_t ka = __builtin_amdgcn_readlane(pl < 64 ? sk0 : sk1, pl & 63);
-                const uint32_t kb = __builtin_amdgcn_readlane(pr < 64 ? sk0 : sk1, pr & 63);
-                donor = ka <= kb ? pl : pr;
-            }
-        }
-        if (donor < 64) av0 &= ~(1ull << donor);
-        else av1 &= ~(1ull << (donor - 64));
-        don_v = lane == i ? donor : don_v;
+    iq_pick_donors128(sal, __ballot(f0 & 1u), __ballot(f1 & 1u), __ballot(f0 & 2u), __ballot(f1 & 2u), count, src_out,
+                      don_out, is_src, src_of, list);
+}
+
+// Top `count` of the 128 keys k0 (channel lane) and k1 (channel 64 + lane)
+// among the eligible channels (masks e0, e1), ties to the lower channel: the
+// selection of iq_wave_top<2>, with the comparisons made straight into lane
+// masks.  Ineligible keys are zeroed first, so that the radix search, whose
+// candidates are never 0, needs no mask; only the ties at the threshold do.
+__device__ __forceinline__ void iq_top128(uint32_t k0, uint32_t k1, uint64_t e0, uint64_t e1, int count, uint64_t &o0,
+                                          uint64_t &o1)
+{
+    constexpr int UGT = 34, UGE = 35, EQ = 32;    // integer predicates of the lane-mask compares
+    const int lane = threadIdx.x & 63;
+    k0 = ((e0 >> lane) & 1ull) ? k0 : 0u;
+    k1 = ((e1 >> lane) & 1ull) ? k1 : 0u;
+    if (count <= 0) {
+        o0 = o1 = 0;
+        return;
     }
-    if (lane < count) {
-        src_out[lane] = (int16_t)s;
-        don_out[lane] = (int16_t)don_v;
-        src_of[don_v] = (int16_t)s;
+    uint32_t thr = 0;
+#pragma unroll
+    for (int bit = 31; bit >= 0; --bit) {
+        const uint32_t cand = thr | (1u << bit);
+        const int n = __popcll(__builtin_amdgcn_uicmp(k0, cand, UGE)) + __popcll(__builtin_amdgcn_uicmp(k1, cand, UGE));
+        if (n >= count) thr = cand;
     }
+    o0 = __builtin_amdgcn_uicmp(k0, thr, UGT) & e0;
+    o1 = __builtin_amdgcn_uicmp(k1, thr, UGT) & e1;
+    int need = count - __popcll(o0) - __popcll(o1);
+    uint64_t eq0 = __builtin_amdgcn_uicmp(k0, thr, EQ) & e0, eq1 = __builtin_amdgcn_uicmp(k1, thr, EQ) & e1;
+    for (; eq0 && need > 0; --need) {
+        const uint64_t low = eq0 & (~eq0 + 1);
+        o0 |= low;
+        eq0 ^= low;
+    }
+    for (; eq1 && need > 0; --need) {
+        const uint64_t low = eq1 & (~eq1 + 1);
+        o1 |= low;
+        eq1 ^= low;
+    }
+}
+
+// The selection of iq_select_wave_t<2> for one D = 128 row by one wavefront
+// (sal / err in LDS, err null for the plain policy): radix top-k for the
+// sources and the min_error pool, then iq_pick_donors128.  LDS scratch:
+// list[64].
+__device__ __forceinline__ void iq_select_wave128(const float *sal, const float *err, int count, int16_t *src_out,
+                                                  int16_t *don_out, uint8_t *is_src, int16_t *src_of, int16_t *list)
+{
+    const int lane = threadIdx.x & 63;
+    uint64_t sel0, sel1;
+    iq_top128(iq_nonneg_bits(sal[lane]), iq_nonneg_bits(sal[64 + lane]), ~0ull, ~0ull, count, sel0, sel1);
+    uint64_t av0 = ~sel0, av1 = ~sel1;
+    if (err)  // ascending error == descending complement of its bit pattern
+        iq_top128(~iq_nonneg_bits(err[lane]), ~iq_nonneg_bits(err[64 + lane]), ~sel0, ~sel1, count, av0, av1);
+    iq_pick_donors128(sal, sel0, sel1, av0, av1, count, src_out, don_out, is_src, src_of, list);
 }
 
 __device__ __forceinline__ void iq_select_wave(const float *sal, const float *err, int D, int count,
