@@ -123,14 +123,16 @@ __global__ __launch_bounds__(NT) void prefill_attn(PrefillArgs a)
         if (k0 + KT < kend) load_tile(k0 + KT);
         if (k0 > qw + 15) continue;              // every key of this tile is after this wavefront's queries
         // S^T (keys x queries) for four 16-key subtiles; lane holds keys 16 j + 4 g + r of column my_q
+        // consecutive products go to different subtiles, so none waits for
+        // the one before it
         f32x4 sc[4];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            sc[j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        for (int j = 0; j < 4; ++j) sc[j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-            for (int ks = 0; ks < 4; ++ks)
+        for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
                 sc[j] = mma32<F16>(*(const u32x4 *)(sm.k + (16 * j + col) * KROW + 32 * ks + 8 * g), qb[ks], sc[j]);
-        }
         // raw logits: the scale is positive, so the maximum commutes with it
         // and p = 2^(s c - m) takes one fma per logit.  Only a tile that
         // reaches past this wavefront's first query or the sequence's end
@@ -168,15 +170,15 @@ __global__ __launch_bounds__(NT) void prefill_attn(PrefillArgs a)
         l_run = l_run * alpha + xsum16(lsum);
         m_run = m_new;
 #pragma unroll
-        for (int rb = 0; rb < 8; ++rb) {
-            acc[rb] *= alpha;
-            const uint32_t *vr = sm.vt + (16 * rb + col) * VROW + 2 * g;
+        for (int rb = 0; rb < 8; ++rb) acc[rb] *= alpha;
 #pragma unroll
-            for (int ks = 0; ks < 2; ++ks) {
-                const u32x2 lo = *(const u32x2 *)(vr + 16 * ks), hi = *(const u32x2 *)(vr + 16 * ks + 8);
+        for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+            for (int rb = 0; rb < 8; ++rb) {
+                const uint32_t *vr = sm.vt + (16 * rb + col) * VROW + 2 * g + 16 * ks;
+                const u32x2 lo = *(const u32x2 *)vr, hi = *(const u32x2 *)(vr + 8);
                 acc[rb] = mma32<F16>(u32x4{lo[0], lo[1], hi[0], hi[1]}, pb[ks], acc[rb]);
             }
-        }
     }
     if (my_q < len) {
         const float inv = 1.0f / l_run;
