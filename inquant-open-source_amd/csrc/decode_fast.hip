@@ -694,13 +694,20 @@ __device__ __forceinline__ void fast_body(const FastArgs &a, FastSmem &sm)
                 }
             }
             wave_lds_sync();                           // the tile's rows come from other lanes
+            // two row blocks at a time, so that consecutive products go to
+            // different accumulators
 #pragma unroll
-            for (int n = 0; n < 8; ++n) {
-                u32x4 va;                              // k-slot pair r: pair row 4 ql + r
+            for (int n = 0; n < 8; n += 2) {
+                u32x4 va[2];                           // k-slot pair r: pair row 4 ql + r
 #pragma unroll
-                for (int r = 0; r < 4; ++r) va[r] = vtile[(4 * ql + r) * VR + 16 * n + gl];
-                acc[n] = mma32<F16>(va, phi[m], m == 0 ? f32x4{0.0f, 0.0f, 0.0f, 0.0f} : acc[n]);
-                acc[n] = mma32<F16>(va, plo[m], acc[n]);
+                for (int u = 0; u < 2; ++u)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) va[u][r] = vtile[(4 * ql + r) * VR + 16 * (n + u) + gl];
+#pragma unroll
+                for (int u = 0; u < 2; ++u)
+                    acc[n + u] = mma32<F16>(va[u], phi[m], m == 0 ? f32x4{0.0f, 0.0f, 0.0f, 0.0f} : acc[n + u]);
+#pragma unroll
+                for (int u = 0; u < 2; ++u) acc[n + u] = mma32<F16>(va[u], plo[m], acc[n + u]);
             }
         }
     } else {
