@@ -43,10 +43,12 @@ struct PrefillArgs {
     int odt;
 };
 
+// two stages: one is computed while the next tile is staged into the other
 struct __attribute__((aligned(16))) PrefillSmem {
-    uint16_t k[KT * KROW];
-    uint32_t vt[D * VROW];           // V^T[d][key pair]: (V[2p][d], V[2p+1][d])
+    uint16_t k[2][KT * KROW];
+    uint32_t vt[2][D * VROW];        // V^T[d][key pair]: (V[2p][d], V[2p+1][d])
 };
+static_assert(2 * sizeof(PrefillSmem) <= 160 * 1024, "two workgroups per compute unit");
 
 template <bool F16>
 __global__ __launch_bounds__(NT) void prefill_attn(PrefillArgs a)
@@ -69,17 +71,44 @@ __global__ __launch_bounds__(NT) void prefill_attn(PrefillArgs a)
     }
     const uint16_t *kbase = a.k + (int64_t)start * a.k_st + (int64_t)h * a.k_sh;
     const uint16_t *vbase = a.v + (int64_t)start * a.v_st + (int64_t)h * a.v_sh;
-    float m_run = NEG_INF, l_run = 0.0f;
+    float m_run = NEG_INF, l_run = 0.0f;         // l_run: this lane's share of the column sum
     f32x4 acc[8];
 #pragma unroll
     for (int rb = 0; rb < 8; ++rb) acc[rb] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
     const int kend = q0 + QT < len ? q0 + QT : len;
-    // Key tiles are double-buffered through registers: tile k0 + 64 is read
-    // from global memory while tile k0 is computed, then written to LDS.
-    // Rows past the sequence read its last row and are masked.
+    // Key tiles stream global -> registers -> LDS with two LDS stages: tile
+    // k0 + 64 is staged while tile k0 is computed, and tile k0 + 128 is read
+    // from global memory meanwhile, so each tile costs one barrier.  Full
+    // tiles load from a uniform tile base plus this thread's 32-bit row
+    // offsets; the sequence's last tile clamps rows past its end to its last
+    // row (masked).
     constexpr int KIT = KT * 16 / NT, VIT = KT * 8 / NT;
+    uint32_t koff[KIT], voff[VIT][2];
+#pragma unroll
+    for (int it = 0; it < KIT; ++it) {
+        const int i = tid + NT * it;
+        koff[it] = (uint32_t)(((i >> 4) * a.k_st + (i & 15) * 8) * 2);
+    }
+#pragma unroll
+    for (int it = 0; it < VIT; ++it) {
+        const int i = tid + NT * it;
+        const int p = i & 31, c = (i >> 5) * 8;
+        voff[it][0] = (uint32_t)((2 * p * a.v_st + c) * 2);
+        voff[it][1] = (uint32_t)(((2 * p + 1) * a.v_st + c) * 2);
+    }
     u32x4 kreg[KIT], vreg[VIT][2];
     auto load_tile = [&](int k0) {
+        if (k0 + KT <= len) {                    // uniform
+            const uint16_t *kt = kbase + (int64_t)k0 * a.k_st, *vt = vbase + (int64_t)k0 * a.v_st;
+#pragma unroll
+            for (int it = 0; it < KIT; ++it) kreg[it] = ldg_at<u32x4>(kt, koff[it]);
+#pragma unroll
+            for (int it = 0; it < VIT; ++it) {
+                vreg[it][0] = ldg_at<u32x4>(vt, voff[it][0]);
+                vreg[it][1] = ldg_at<u32x4>(vt, voff[it][1]);
+            }
+            return;
+        }
 #pragma unroll
         for (int it = 0; it < KIT; ++it) {
             const int i = tid + NT * it;
@@ -97,17 +126,15 @@ __global__ __launch_bounds__(NT) void prefill_attn(PrefillArgs a)
             vreg[it][1] = ld16(vbase + (int64_t)kb * a.v_st + c);
         }
     };
-    load_tile(0);
-    for (int k0 = 0; k0 < kend; k0 += KT) {
-        __syncthreads();                         // the previous tile's reads are done
+    // registers -> LDS stage s.  V^T: thread (key pair p = lane % 32, 8
+    // channels c) writes one dword per channel; the 32 key pairs of a channel
+    // row are consecutive dwords, so a wavefront's stores hit distinct banks
+    auto stage = [&](int s) {
 #pragma unroll
         for (int it = 0; it < KIT; ++it) {
             const int i = tid + NT * it;
-            *(u32x4 *)(sm.k + (i >> 4) * KROW + (i & 15) * 8) = kreg[it];
+            *(u32x4 *)(sm.k[s] + (i >> 4) * KROW + (i & 15) * 8) = kreg[it];
         }
-        // V^T: thread (key pair p = lane % 32, 8 channels c) writes one dword
-        // per channel; the 32 key pairs of a channel row are consecutive
-        // dwords, so a wavefront's stores hit distinct banks
 #pragma unroll
         for (int it = 0; it < VIT; ++it) {
             const int i = tid + NT * it;
@@ -115,71 +142,92 @@ __global__ __launch_bounds__(NT) void prefill_attn(PrefillArgs a)
             const u32x4 r0 = vreg[it][0], r1 = vreg[it][1];
 #pragma unroll
             for (int w = 0; w < 4; ++w) {
-                sm.vt[(c + 2 * w) * VROW + p] = __builtin_amdgcn_perm(r1[w], r0[w], 0x05040100u);
-                sm.vt[(c + 2 * w + 1) * VROW + p] = __builtin_amdgcn_perm(r1[w], r0[w], 0x07060302u);
+                sm.vt[s][(c + 2 * w) * VROW + p] = __builtin_amdgcn_perm(r1[w], r0[w], 0x05040100u);
+                sm.vt[s][(c + 2 * w + 1) * VROW + p] = __builtin_amdgcn_perm(r1[w], r0[w], 0x07060302u);
             }
         }
-        __syncthreads();
-        if (k0 + KT < kend) load_tile(k0 + KT);
-        if (k0 > qw + 15) continue;              // every key of this tile is after this wavefront's queries
-        // S^T (keys x queries) for four 16-key subtiles; lane holds keys 16 j + 4 g + r of column my_q
-        // consecutive products go to different subtiles, so none waits for
-        // the one before it
-        f32x4 sc[4];
+    };
+    load_tile(0);
+    stage(0);
+    if (KT < kend) load_tile(KT);
+    __syncthreads();
+    int s = 0;
+    for (int k0 = 0; k0 < kend; k0 += KT, s ^= 1) {
+        if (k0 + KT < kend) {
+            // stage s ^ 1 was last read before the previous barrier
+            stage(s ^ 1);
+            if (k0 + 2 * KT < kend) load_tile(k0 + 2 * KT);
+        }
+        if (k0 <= qw + 15) {                     // some key of this tile is visible to this wavefront (uniform)
+            const uint16_t *sk = sm.k[s];
+            const uint32_t *svt = sm.vt[s];
+            // S^T (keys x queries) for four 16-key subtiles; lane holds keys 16 j + 4 g + r of column my_q;
+            // consecutive products go to different subtiles, so none waits for
+            // the one before it
+            f32x4 sc[4];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) sc[j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+            for (int j = 0; j < 4; ++j) sc[j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-        for (int ks = 0; ks < 4; ++ks)
+            for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    sc[j] = mma32<F16>(*(const u32x4 *)(sk + (16 * j + col) * KROW + 32 * ks + 8 * g), qb[ks], sc[j]);
+            // raw logits: the scale is positive, so the maximum commutes with it
+            // and p = 2^(s c - m) takes one fma per logit.  Only a tile that
+            // reaches past this wavefront's first query or the sequence's end
+            // has keys to mask (wave-uniform).
+            if (k0 + KT - 1 > qw || k0 + KT > len) {
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        const int key = k0 + 16 * j + 4 * g + r;
+                        if (!(key <= my_q && key < len)) sc[j][r] = NEG_INF;
+                    }
+            }
+            float cmax = NEG_INF;
 #pragma unroll
             for (int j = 0; j < 4; ++j)
-                sc[j] = mma32<F16>(*(const u32x4 *)(sm.k + (16 * j + col) * KROW + 32 * ks + 8 * g), qb[ks], sc[j]);
-        // raw logits: the scale is positive, so the maximum commutes with it
-        // and p = 2^(s c - m) takes one fma per logit.  Only a tile that
-        // reaches past this wavefront's first query or the sequence's end
-        // has keys to mask (wave-uniform).
-        if (k0 + KT - 1 > qw || k0 + KT > len) {
 #pragma unroll
-            for (int j = 0; j < 4; ++j)
+                for (int r = 0; r < 4; ++r) cmax = fmaxf(cmax, sc[j][r]);
+            cmax = xmax16(cmax) * a.c_log2;
+            const float m_new = fmaxf(m_run, cmax);  // finite: key 0 is visible to every query
+            const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
+            float lsum = 0.0f;
+            u32x4 pb[2];                             // B operand of O^T: slots 0-3 subtile 2ks, 4-7 subtile 2ks+1
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                float pr[4];
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
-                    const int key = k0 + 16 * j + 4 * g + r;
-                    if (!(key <= my_q && key < len)) sc[j][r] = NEG_INF;
+                    pr[r] = __builtin_amdgcn_exp2f(fmaf(sc[j][r], a.c_log2, -m_new));
+                    lsum += pr[r];
+                }
+                pb[j >> 1][2 * (j & 1)] = pack2<F16>(pr[0], pr[1]);
+                pb[j >> 1][2 * (j & 1) + 1] = pack2<F16>(pr[2], pr[3]);
+            }
+            // the four lanes of a column share m, so their partial sums take
+            // the same rescale and are added once, after the last tile
+            l_run = fmaf(l_run, alpha, lsum);
+            m_run = m_new;
+            // alpha is exactly 1 wherever the maximum did not grow: when that
+            // holds in every lane the rescale is the identity and is skipped
+            if (__builtin_amdgcn_ballot_w64(alpha != 1.0f)) {
+#pragma unroll
+                for (int rb = 0; rb < 8; ++rb) acc[rb] *= alpha;
+            }
+#pragma unroll
+            for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+                for (int rb = 0; rb < 8; ++rb) {
+                    const uint32_t *vr = svt + (16 * rb + col) * VROW + 2 * g + 16 * ks;
+                    const u32x2 lo = *(const u32x2 *)vr, hi = *(const u32x2 *)(vr + 8);
+                    acc[rb] = mma32<F16>(u32x4{lo[0], lo[1], hi[0], hi[1]}, pb[ks], acc[rb]);
                 }
         }
-        float cmax = NEG_INF;
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-#pragma unroll
-            for (int r = 0; r < 4; ++r) cmax = fmaxf(cmax, sc[j][r]);
-        cmax = xmax16(cmax) * a.c_log2;
-        const float m_new = fmaxf(m_run, cmax);  // finite: key 0 is visible to every query
-        const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
-        float lsum = 0.0f;
-        u32x4 pb[2];                             // B operand of O^T: slots 0-3 subtile 2ks, 4-7 subtile 2ks+1
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            float pr[4];
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                pr[r] = __builtin_amdgcn_exp2f(fmaf(sc[j][r], a.c_log2, -m_new));
-                lsum += pr[r];
-            }
-            pb[j >> 1][2 * (j & 1)] = pack2<F16>(pr[0], pr[1]);
-            pb[j >> 1][2 * (j & 1) + 1] = pack2<F16>(pr[2], pr[3]);
-        }
-        l_run = l_run * alpha + xsum16(lsum);
-        m_run = m_new;
-#pragma unroll
-        for (int rb = 0; rb < 8; ++rb) acc[rb] *= alpha;
-#pragma unroll
-        for (int ks = 0; ks < 2; ++ks)
-#pragma unroll
-            for (int rb = 0; rb < 8; ++rb) {
-                const uint32_t *vr = sm.vt + (16 * rb + col) * VROW + 2 * g + 16 * ks;
-                const u32x2 lo = *(const u32x2 *)vr, hi = *(const u32x2 *)(vr + 8);
-                acc[rb] = mma32<F16>(u32x4{lo[0], lo[1], hi[0], hi[1]}, pb[ks], acc[rb]);
-            }
+        __syncthreads();                         // stage s ^ 1 is written; stage s is free
     }
+    l_run = xsum16(l_run);
     if (my_q < len) {
         const float inv = 1.0f / l_run;
         const int64_t o = (int64_t)(start + my_q) * a.o_st + (int64_t)hq * a.o_sh + 4 * g;
@@ -206,6 +254,9 @@ extern "C" int iq_prefill_attention(const void *q, const void *k, const void *v,
                  (long long)Hq, (long long)H);
     IQ_CHECK_ARG(n_seq >= 1 && n_seq <= 65535 && max_seqlen >= 1 && max_seqlen <= 0x7fffffffLL - QT,
                  "iq_prefill_attention: bad sequence count or length");
+    // a key tile's rows are addressed by 32-bit byte offsets from its first row
+    IQ_CHECK_ARG(k_st >= 0 && v_st >= 0 && k_st < (1LL << 25) && v_st < (1LL << 25),
+                 "iq_prefill_attention: token stride too large");
     // rows are read as 16-byte vectors
     const uintptr_t bases = (uintptr_t)q | (uintptr_t)k | (uintptr_t)v;
     IQ_CHECK_ARG(bases % 16 == 0 && (q_st | q_sh | k_st | k_sh | v_st | v_sh) % 8 == 0,
