@@ -213,8 +213,8 @@ __global__ __launch_bounds__(K4_THREADS) void k4_encode_kernel(K4Args a)
 //           waves 2-3: sampled sums (torch cascade order), amax and
 //           finiteness as an integer max of the 16-bit magnitudes;
 //   then    donor selection by the whole workgroup (iq_select_tile128);
-//           the sequential donor picks run on wave 0 alone, and with a
-//           value row to encode (page mode, or VB = 2 / 4) waves 1-3
+//           the sequential donor picks run on one wavefront alone, and with a
+//           value row to encode (page mode, or VB = 2 / 4) the other three
 //           group-encode the values meanwhile (v_encode16, the same bits as
 //           v_encode_rows), reading them from HBM while it is otherwise idle;
 //   pass 2  every thread quantizes 8 channels of a token per step, writing
@@ -582,9 +582,9 @@ __device__ __forceinline__ void k4_tile_body(const K4Args &a, int64_t b, int64_t
     __syncthreads();
     start_stream();
 
-    // ---- values (VBITS > 0), encoded by waves 1-3 while wave 0 makes the
-    // sequential donor picks, with the row's HBM reads in that otherwise
-    // idle stretch.  Thread vt of waves 1-3 takes channels 16 vj .. 16 vj + 15
+    // ---- values (VBITS > 0), encoded by three wavefronts while the fourth
+    // makes the sequential donor picks, with the row's HBM reads in that otherwise
+    // idle stretch.  Thread vt of the three value wavefronts takes channels 16 vj .. 16 vj + 15
     // of token vtok0 + 24 it in iteration it (192 threads = 24 tokens), so a
     // group's GLV lanes are adjacent lanes of one wavefront.  A sealed block
     // (11 iterations) issues its first VPF iterations' loads here, before
@@ -592,7 +592,13 @@ __device__ __forceinline__ void k4_tile_body(const K4Args &a, int64_t b, int64_t
     constexpr int VT = K4_THREADS - 64;
     constexpr int VIT = NCH > 0 ? (NCH * CH * 8 + VT - 1) / VT : 1;
     constexpr int VPF = 4;
-    const int vt = tid - 64, vj = vt & 7, vtok0 = vt >> 3;
+    // The picking wavefront rotates between the workgroups that share a
+    // compute unit (linear indices 256 apart): each SIMD then holds one
+    // picking wavefront and three encoding values, instead of one SIMD
+    // holding every picker while its VALU idles.  vtid is the thread's index
+    // in that rotated order (virtual wave 0 picks).
+    const int vtid = (tid + 64 * ((lin >> 8) & 3)) & (K4_THREADS - 1), vwave = vtid >> 6;
+    const int vt = vtid - 64, vj = vt & 7, vtok0 = vt >> 3;
     u32x4_t vraw[NCH > 0 ? VIT : 1][2];
     auto vload = [&](int it, u32x4_t(&r)[2]) {
         const int t = min(vtok0 + 24 * it, T - 1);
@@ -625,7 +631,7 @@ __device__ __forceinline__ void k4_tile_body(const K4Args &a, int64_t b, int64_t
         }
     };
     if constexpr (VBITS > 0 && NCH > 0) {
-        if (wave > 0) {
+        if (vwave > 0) {
 #pragma unroll
             for (int it = 0; it < VPF; ++it) vload(it, vraw[it]);
         }
@@ -641,13 +647,13 @@ __device__ __forceinline__ void k4_tile_body(const K4Args &a, int64_t b, int64_t
     }
     __syncthreads();
 
-    // the sequential donor picks on wave 0 hold up the whole block: top priority
-    if (wave == 0) __builtin_amdgcn_s_setprio(3);
+    // the sequential donor picks on the picking wavefront hold up the whole block: top priority
+    if (vwave == 0) __builtin_amdgcn_s_setprio(3);
     else __builtin_amdgcn_s_setprio(0);
     iq_select_tile128(s_sal, a.min_error ? s_err : nullptr, (int)a.count, s_src, s_don, s_is_src, s_src_of,
-                      s_key, s_part, s_flag, s_list);
+                      s_key, s_part, s_flag, s_list, vtid);
     if constexpr (VBITS > 0) {
-        if (wave > 0) {
+        if (vwave > 0) {
             bool vbad = false;
             if constexpr (NCH > 0) {
 #pragma unroll

@@ -279,17 +279,17 @@ __device__ __forceinline__ void iq_pick_donors128(const float *sal, uint64_t sel
 // each channel gets a 64-bit key that orders it exactly as the stable sort
 // does (the value's bits, then the channel as tie-break), and its rank is the
 // number of keys ordered before it, each thread comparing against 64 of
-// them.  The sequential donor picks then run on wave 0 from the neighbour
+// them.  The sequential donor picks then run on one wavefront (threads 0-63 of the order the caller passes) from the neighbour
 // order and run boundaries precomputed one source per lane, so a pick with a
 // free neighbour is a handful of scalar operations.  LDS scratch: key[128],
 // part[256], flag[128], list[64].
 __device__ __forceinline__ void iq_select_tile128(const float *sal, const float *err, int count,
                                                   int16_t *src_out, int16_t *don_out, uint8_t *is_src,
                                                   int16_t *src_of, uint64_t *key, int *part, uint8_t *flag,
-                                                  int16_t *list)
+                                                  int16_t *list, int tid)
 {
     typedef __attribute__((ext_vector_type(2))) uint64_t v2u64;
-    const int tid = threadIdx.x, c = tid & 127, half = tid >> 7, lane = tid & 63;
+    const int c = tid & 127, half = tid >> 7, lane = tid & 63;
     // 1. sources: the `count` channels first in descending saliency, ties to
     //    the lower channel; as one ascending key: ~bits, then the channel
     if (tid < 128) key[c] = ((uint64_t)~iq_nonneg_bits(sal[c]) << 7) | (uint64_t)c;
@@ -328,7 +328,7 @@ __device__ __forceinline__ void iq_select_tile128(const float *sal, const float 
     __syncthreads();
     if (tid >= 64) return;
 
-    // 3. sequential donor picks on wave 0; sources in ascending channel order
+    // 3. sequential donor picks on the wavefront of tid 0-63; sources in ascending channel order
     const uint32_t f0 = flag[lane], f1 = flag[64 + lane];
     iq_pick_donors128(sal, __ballot(f0 & 1u), __ballot(f1 & 1u), __ballot(f0 & 2u), __ballot(f1 & 2u), count, src_out,
                       don_out, is_src, src_of, list);
