@@ -315,7 +315,8 @@ int iq_paged_decode(const void *q, int64_t q_stride_seq, int64_t q_stride_h, int
 /*
  * Causal self-attention over exact K/V for prefill, vLLM token-major layout:
  * q [tokens, Hq, 128], k/v [tokens, H, 128] of dtype (bf16 or f16) with
- * element strides (token, head), 16-byte aligned rows; sequences
+ * element strides (token, head), 16-byte aligned rows, k/v token strides
+ * below 2^25 elements (IQ_ERR_ARG otherwise); sequences
  * [cu_seqlens[i], cu_seqlens[i + 1]) (i32, on the device, n_seq + 1 values),
  * none longer than max_seqlen; query i of a sequence attends to its keys
  * 0..i; out [tokens, Hq, 128] of out_dtype with strides (o_st, o_sh).  fp32

@@ -44,6 +44,13 @@ def test_invalid_arguments_return_errors_without_a_gpu():
         None, 1, 128, 28, None, None, None, None, 1, 256, 4, 16, 2, 64, None, None, 0, 0, 0, 0, 0,
         None, None, 0, 0, 0, 0, 4700 * 256, 0.088, None, 0, None) == -1
     assert b"static scratch" in lib.iq_last_error()
+    # prefill: key tiles are addressed by 32-bit offsets, so token strides of
+    # 2^25 elements or more are refused (the pointers are never dereferenced)
+    fake = 1 << 20
+    st = 1 << 25
+    assert lib.iq_prefill_attention(fake, fake, fake, _native.IQ_BF16, 28 * 128, 128, st, 128, 512, 128, fake, 1,
+                                    8192, 28, 4, 128, 0.088, fake, 28 * 128, 128, _native.IQ_BF16, None) == -1
+    assert b"token stride" in lib.iq_last_error()
 
 
 @pytest.mark.parametrize("bad", [-0.1, 0.51, float("nan")])
