@@ -386,16 +386,16 @@ def time_next_rows(device):
         vp = v[0].reshape(H, P, B, D).transpose(0, 1)
         pool = torch.empty((P, layout.page_bytes), dtype=torch.uint8, device=device)
         ids = torch.arange(P, dtype=torch.int32, device=device)
-        flags = torch.zeros(4, dtype=torch.int32, device=device)
+        flags = torch.zeros(8, dtype=torch.int32, device=device)     # two (key, value, page id) triples
 
         def encode_pages():
             st = nat.stream_handle(torch.device(device))
             nat.check(lib.iq_encode_pages(kp.data_ptr(), vp.data_ptr(), nat.IQ_BF16, nat.strides4(kp),
                                           nat.strides4(vp), P, H, B, pool.data_ptr(), P, ids.data_ptr(), 4,
-                                          flags.data_ptr(), flags.data_ptr() + 8, st))
+                                          flags.data_ptr(), flags.data_ptr() + 16, st))
 
         us = _graph_us(device, encode_pages)
-        assert flags[:2].tolist() == [0, 0]
+        assert flags[:3].tolist() == [0, 0, 0]
         enc_bytes = 2 * k.numel() * 2 + P * layout.page_bytes
         out[f"encode_pages_b{B}"] = {"tokens": T, "heads": H, "page_tokens": B, "us": round(us, 3),
                                      "mtok_s": round(T / us, 2), "bytes": enc_bytes,

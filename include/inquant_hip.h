@@ -265,11 +265,12 @@ int iq_write_pages(const uint8_t *k_payload, const float *k_scales, const float 
  * [n, H, B, 128] of dtype (bf16 or f16) with element strides k_strides /
  * v_strides (unit channel stride, 16-byte aligned rows), B in {16, 32, 64,
  * 128, 256}.  Page n goes to physical id page_ids[n] (i32 or i64 per
- * id_bytes; ids outside [0, pool_pages) are skipped): K4 min_error with
- * stride 8 and 16 salient channels (payload, scales, padding and the i16
- * role map) and V2 with 64-channel groups.  flags[0] / flags[1] are set for
- * non-finite keys / values; the launch zeroes next_flags[0..1] (the pair the
- * caller passes as flags to its next call, so no clearing launch is needed).
+ * id_bytes; an id outside [0, pool_pages) writes nothing and sets flags[2]):
+ * K4 min_error with stride 8 and 16 salient channels (payload, scales,
+ * padding and the i16 role map) and V2 with 64-channel groups.  flags[0] /
+ * flags[1] are set for non-finite keys / values; the launch zeroes
+ * next_flags[0..2] (the triple the caller passes as flags to its next call,
+ * so no clearing launch is needed).
  * Replaces pack_pages_into (layout.py:103-115: quantize, quantize_values,
  * write_codec_pages) and the encode of pack_pages (layout.py:56-81).
  */

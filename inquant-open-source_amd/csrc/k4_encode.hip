@@ -41,7 +41,7 @@ struct K4Args {
     int64_t off_kpay, off_kscale, off_kmap, off_kpad, off_vpay, off_vscale, off_voff;
     const uint16_t *v;
     int64_t vsb, vsh, vst;
-    int *vbad, *clear;          // value flag; flag pair the next page launch uses, zeroed here
+    int *vbad, *badid, *clear;  // value flag; out-of-range page id flag; flag triple the next page launch uses, zeroed here
     // fused key/value mode (k4_encode_tile<..., VB = 2 or 4>): the value rows
     // of v are encoded group-wise into the outputs of iq_v_quantize
     uint8_t *vpayload;
@@ -389,9 +389,12 @@ __device__ __forceinline__ void k4_tile_body(const K4Args &a, int64_t b, int64_t
     uint8_t *page = nullptr;
     __shared__ int16_t s_role[TILE_D];
     if constexpr (PAGES) {
-        if (b == 0 && h == 0 && threadIdx.x < 2) a.clear[threadIdx.x] = 0;
+        if (b == 0 && h == 0 && threadIdx.x < 3) a.clear[threadIdx.x] = 0;
         const int64_t id = a.id_bytes == 8 ? ((const int64_t *)a.ids)[b] : (int64_t)((const int32_t *)a.ids)[b];
-        if (id < 0 || id >= a.pool_pages) return;       // uniform: before any barrier or load
+        if (id < 0 || id >= a.pool_pages) {             // uniform: before any barrier or load
+            if (threadIdx.x == 0) *a.badid = 1;
+            return;
+        }
         page = a.pool + id * a.page_bytes;
         if (threadIdx.x < TILE_D) s_role[threadIdx.x] = -1;
     }
@@ -779,10 +782,13 @@ __global__ __launch_bounds__(K4_THREADS) void k4_encode_page_rows(K4Args a, int6
 
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int64_t b = (int64_t)blockIdx.x * 4 + wave, h = blockIdx.y;
-    if (blockIdx.x == 0 && h == 0 && threadIdx.x < 2) a.clear[threadIdx.x] = 0;
+    if (blockIdx.x == 0 && h == 0 && threadIdx.x < 3) a.clear[threadIdx.x] = 0;
     if (b >= n_pages) return;                  // wave-uniform, as the page check below
     const int64_t id = a.id_bytes == 8 ? ((const int64_t *)a.ids)[b] : (int64_t)((const int32_t *)a.ids)[b];
-    if (id < 0 || id >= a.pool_pages) return;
+    if (id < 0 || id >= a.pool_pages) {
+        if (lane == 0) *a.badid = 1;
+        return;
+    }
     uint8_t *const page = a.pool + id * a.page_bytes;
     const uint16_t *const xr = (const uint16_t *)a.x + b * a.sb + h * a.sh;
     const uint16_t *const vr = a.v + b * a.vsb + h * a.vsh;
@@ -1187,6 +1193,7 @@ extern "C" int iq_encode_pages(const void *keys, const void *values, int dtype, 
     a.vsh = v_strides[1];
     a.vst = v_strides[2];
     a.vbad = flags + 1;
+    a.badid = flags + 2;
     a.clear = next_flags;
     if (n_pages == 0) return IQ_OK;
     const hipStream_t st = (hipStream_t)stream;

@@ -26,10 +26,14 @@ How a layer is stored here (not how the reference stores it):
   bytes of their views, which tile the batched allocation exactly, so the
   totals equal the reference's per-block clones.
 * ``cache_position`` is compared on the device by the append kernel.  With
-  ``validate_positions`` the first layer of each decode step (a position
-  tensor not yet checked for this start) synchronizes and raises before
-  anything changes, as the reference does; the other layers of the step,
-  which share the tensor, rely on the device comparison, whose flag is read
+  ``validate_positions`` a position tensor not yet verified for this start
+  (the first layer of each decode step, or any layer after the tensor was
+  written in place: its version counter moved) synchronizes and raises
+  before anything changes, as the reference does on every layer.  The other
+  layers of the step get the same tensor, unchanged, for the same start, so
+  they hold the positions already verified and need no second sync.  An
+  inference-mode tensor keeps no version counter: an in-place change of it
+  between layers of one step is caught by the device comparison and raised
   at the next synchronization (the next step's check or the next seal).
 """
 from __future__ import annotations
@@ -51,6 +55,11 @@ from .codec import _BAD_K, CodecConfig, PackedTensor, _per_block, quantize
 from .value_codec import _BAD_V, PackedValues, _value_blocks
 
 _POSITION_ERROR = "Only contiguous append positions are supported; reset before a new request"
+
+
+def _version(t):
+    """The tensor's in-place write counter (None for inference tensors)."""
+    return None if t.is_inference() else t._version
 # flag words of a cache: key non-finite, value non-finite, position mismatch
 _KEY_BAD, _VALUE_BAD, _POSITION_BAD = 0, 1, 2
 
@@ -317,7 +326,7 @@ class InQuantCache(_HFCache):
         self._owned: dict[int, tuple[int, int]] = {}
         self._owned_total = 0
         self._flags: torch.Tensor | None = None          # int32 [3] on the cache's device
-        self._position_checked: tuple | None = None      # (tensor, expected start) verified by a sync
+        self._position_checked: tuple | None = None      # (tensor, version, expected start) verified by a sync
 
     # ------------------------------------------------------------ HF protocol
     def __len__(self) -> int:
@@ -466,8 +475,12 @@ class InQuantCache(_HFCache):
                 self._host_position_check(position, layer.seq_length)
             else:
                 pos_ptr, pos_bytes = position.data_ptr(), position.element_size()
+                # a position tensor already verified against this start, and not
+                # written since (same version counter), needs no second sync;
+                # inference tensors keep no version counter (None)
                 checked = self._position_checked
-                check_now = not (checked is not None and checked[0] is position and checked[1] == layer.seq_length)
+                check_now = not (checked is not None and checked[0] is position
+                                 and checked[1] == _version(position) and checked[2] == layer.seq_length)
         desc = tail.desc
         if desc is None:
             buf = tail.buf
@@ -493,7 +506,7 @@ class InQuantCache(_HFCache):
                 flags[_POSITION_BAD].zero_()
                 self._position_checked = None
                 raise ValueError(_POSITION_ERROR)
-            self._position_checked = (position, layer.seq_length)
+            self._position_checked = (position, _version(position), layer.seq_length)
         tail.count += 1
         layer.seq_length += 1
         tail_k, tail_v = tail.views()

@@ -73,12 +73,13 @@ def _check_pages(keys, values, layout):
 
 
 class _Flags:
-    """Two pairs of device ints per (device, stream): a page launch raises
-    (key, value) non-finite flags in one pair and zeroes the other, which the
-    next launch on that stream uses, so no separate clearing launch is needed."""
+    """Two rows of device ints per (device, stream): a page launch raises
+    (key non-finite, value non-finite, page id out of range) flags in one row
+    and zeroes the other, which the next launch on that stream uses, so no
+    separate clearing launch is needed."""
 
     def __init__(self, device):
-        self.words = torch.zeros((2, 2), dtype=torch.int32, device=device)
+        self.words = torch.zeros((2, 4), dtype=torch.int32, device=device)
         self.turn = 0
 
 
@@ -106,7 +107,9 @@ def _encode_into(keys, values, layout, pool, page_ids):
     if keys.shape[0] == 0:
         return
     flags.turn = 1 - flags.turn
-    bad_key, bad_value = mine.tolist()          # the one synchronization, as the codec's finite check
+    bad_key, bad_value, bad_id, _ = mine.tolist()   # the one synchronization, as the codec's finite check
+    if bad_id:
+        raise ValueError("Physical page ID outside the destination pool")
     if bad_key:
         raise ValueError("x must contain finite values representable in float32")
     if bad_value:
@@ -151,10 +154,11 @@ def pack_pages_into(keys, values, layout, destination, page_ids, *, donor_backen
     """Seal fresh pages straight into their physical slots (layout.py:103-115)
     with one launch and one flag read; no codec temporaries.
 
-    The page allocator owns unique in-range ids (ids outside the pool are
-    skipped).  ``donor_backend`` is accepted for compatibility: every backend
-    runs the same selector.  A non-finite input raises ValueError after the
-    pages were written (they belong to the caller's fresh allocation)."""
+    The page allocator owns unique in-range ids: an id outside the pool
+    writes nothing and raises ValueError after the launch, as does a
+    non-finite input (the other pages were then written; they belong to the
+    caller's fresh allocation).  ``donor_backend`` is accepted for
+    compatibility: every backend runs the same selector."""
     _check_pages(keys, values, layout)
     if destination.dtype != torch.uint8 or destination.ndim != 2 or destination.shape[1] != layout.page_bytes \
             or not destination.is_contiguous():

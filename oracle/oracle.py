@@ -303,3 +303,27 @@ def causal_attend(q: np.ndarray, k: np.ndarray, v: np.ndarray, scale: float) -> 
         p = np.exp(s)
         out[:, h] = (p @ v64[:, h // group]) / p.sum(1, keepdims=True)
     return out
+
+
+def causal_attend_rows(q: np.ndarray, k: np.ndarray, v: np.ndarray, scale: float, rows, heads,
+                       chunk: int = 1024) -> np.ndarray:
+    """fp64 causal attention of the query rows `rows` (ascending) and query
+    heads `heads` of one sequence -> [len(rows), len(heads), D]; the same
+    semantics as causal_attend (query i sees keys 0..i of KV head
+    h // (Hq / H)), evaluated in row chunks so that long sequences need
+    O(chunk * n) memory."""
+    rows = np.asarray(rows, np.int64)
+    group = q.shape[1] // k.shape[1]
+    out = np.empty((rows.size, len(heads), q.shape[2]))
+    for j, h in enumerate(heads):
+        kh = np.asarray(k[:, h // group], np.float64)
+        vh = np.asarray(v[:, h // group], np.float64)
+        for a in range(0, rows.size, chunk):
+            r = rows[a:a + chunk]
+            n = int(r[-1]) + 1
+            s = np.asarray(q[r, h], np.float64) @ kh[:n].T * scale
+            s[np.arange(n)[None, :] > r[:, None]] = -np.inf
+            s -= s.max(1, keepdims=True)
+            p = np.exp(s)
+            out[a:a + chunk, j] = (p @ vh[:n]) / p.sum(1, keepdims=True)
+    return out

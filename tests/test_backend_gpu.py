@@ -87,8 +87,9 @@ def test_prefill_decode_page_boundary_request_reuse_and_stale_tail(monkeypatch):
     assert impl.prefill_calls == 3 and impl.decode_calls == 9 and impl.seal_calls == 2
 
 
-def test_backend_refusals_and_profile_call():
+def test_backend_refusals_and_profile_call(monkeypatch):
     import inquant_vllm.backend as backend
+    monkeypatch.setattr(backend, "_CONFIG", None)        # restored after the test
     backend.configure(block_size=16, max_model_len=256)
     with pytest.raises(ValueError, match="ALiBi"):
         backend.InQuantImpl(8, 128, 0.1, 2, torch.ones(8), None, "auto")

@@ -289,8 +289,11 @@ def test_single_token_position_check():
 def test_shared_cache_position_checked_on_the_device(inference):
     # The layers of one step share one cache_position tensor.  The first
     # layer's append synchronizes and raises on a mismatch before anything
-    # changes; the other layers rely on the append kernel's comparison, so
-    # an in-place change of the tensor between layers is reported at the
+    # changes; the other layers rely on the append kernel's comparison while
+    # the tensor is unchanged.  An in-place change between layers moves the
+    # tensor's version counter, so that layer checks again and raises before
+    # anything changes (cache.py:233-238 raises on every layer).  An
+    # inference tensor has no version counter: its change is reported at the
     # next synchronizing check (the next step's first layer).
     from inquant.cache import InQuantCache
     cache = InQuantCache(_cfg())
@@ -303,13 +306,23 @@ def test_shared_cache_position_checked_on_the_device(inference):
         p = torch.tensor([6], device="cuda")
         for layer in (0, 1):
             cache.append_for_attention(t, t, layer, {"cache_position": p})
-        assert cache._position_checked[0] is p and cache._position_checked[1] == 6
+        assert cache._position_checked[0] is p and cache._position_checked[2] == 6
         with pytest.raises(ValueError, match="contiguous append positions"):
             cache.append_for_attention(t, t, 2, {"cache_position": p})   # layer 2 expects 5
         assert cache.get_seq_length(2) == 5
         q = torch.tensor([7], device="cuda")
         cache.append_for_attention(t, t, 0, {"cache_position": q})
         q.fill_(3)                                   # changed in place between layers
+        if not inference:
+            with pytest.raises(ValueError, match="contiguous append positions"):
+                cache.append_for_attention(t, t, 1, {"cache_position": q})   # raised on this layer
+            assert [cache.get_seq_length(i) for i in range(3)] == [8, 7, 5]
+            q.fill_(7)
+            cache.append_for_attention(t, t, 1, {"cache_position": q})
+            assert [cache.get_seq_length(i) for i in range(3)] == [8, 8, 5]
+            cache.append_for_attention(t, t, 0, {"cache_position": torch.tensor([8], device="cuda")})
+            assert cache.get_seq_length(0) == 9
+            return
         cache.append_for_attention(t, t, 1, {"cache_position": q})    # compared on the device only
         assert [cache.get_seq_length(i) for i in range(3)] == [8, 8, 5]
         with pytest.raises(ValueError, match="contiguous append positions"):

@@ -277,3 +277,17 @@ def test_causal_attention_oracle_against_torch_sdpa():
     ref = torch.nn.functional.scaled_dot_product_attention(qt, kt, vt, is_causal=True, scale=0.1).transpose(0, 1)
     np.testing.assert_allclose(got, ref.numpy(), rtol=1e-10, atol=1e-12)
     np.testing.assert_allclose(got[0], np.repeat(v[0], hq // h, 0), rtol=0, atol=1e-15)
+
+
+def test_causal_attend_rows_equals_the_full_causal_oracle():
+    # the chunked row/head evaluation that the long prefill checks use,
+    # pinned against the whole-matrix fp64 oracle (itself pinned to SDPA)
+    rng = np.random.default_rng(3)
+    n, hq, h = 300, 6, 2
+    q = rng.standard_normal((n, hq, 128))
+    k = rng.standard_normal((n, h, 128))
+    v = rng.standard_normal((n, h, 128))
+    full = oracle.causal_attend(q, k, v, 0.1)
+    rows = np.array([0, 1, 77, 128, 129, 299])
+    got = oracle.causal_attend_rows(q, k, v, 0.1, rows, [0, 3, 5], chunk=4)
+    np.testing.assert_allclose(got, full[rows][:, [0, 3, 5]], rtol=0, atol=1e-12)

@@ -63,6 +63,64 @@ def test_direct_scattered_pages_match_reference_and_reuse(block, backend, heads)
         assert (pool[torch.tensor([1, 2, 4, 6], device="cuda")] == 173).all()
 
 
+@pytest.mark.parametrize("block,id_dtype", [(16, torch.int32), (64, torch.int64), (256, torch.int32)])
+def test_write_codec_pages_scatters_codec_outputs_bit_exact(block, id_dtype):
+    # packing.py:41-55 write_codec_pages: the codec's own outputs (quantize
+    # with min_error, quantize_values V2 g64) scattered to random physical
+    # ids; the page bytes, the int16 role map included, equal the oracle's
+    # pages and every other page keeps its fill; a second write of other
+    # pages to other ids leaves the first ones intact
+    from inquant.codec import CodecConfig, quantize
+    from inquant.value_codec import quantize_values
+    from inquant_vllm import PageLayout, write_codec_pages
+    layout = PageLayout(block, 4)
+    pool = torch.full((23, layout.page_bytes), 173, device="cuda", dtype=torch.uint8)
+    g = torch.Generator(device="cuda").manual_seed(5150 + block)
+    perm = torch.randperm(23, generator=g, device="cuda").to(id_dtype)
+    written, start = [], 0
+    for r, n in enumerate((5, 3)):
+        k, v = _kv(333 + 10 * block + r, (n, 4, block, 128))
+        kq = quantize(k, CodecConfig(donor_policy="min_error"))
+        vq = quantize_values(v, bits=2, group_size=64)
+        ids = perm[start:start + n]
+        start += n
+        write_codec_pages(kq, vq, layout, pool, ids)
+        ok = oracle.k4_quantize(_np(k.float()), 8, 0.125, "min_error")
+        ov = oracle.v_quantize(_np(v.float()), 2, 64)
+        written.append((ids.long(), oracle.pack_pages(ok, ov, 4, block)))
+    torch.cuda.synchronize()
+    used = torch.zeros(23, dtype=torch.bool, device="cuda")
+    for ids, exp in written:
+        np.testing.assert_array_equal(_np(pool[ids]), exp)
+        role = _np(layout.views(pool[ids])["key_map"])
+        np.testing.assert_array_equal(role, _np(layout.views(torch.from_numpy(exp))["key_map"]))
+        assert (role >= -17).all() and ((role <= -2).sum(-1) == 16).all()      # 16 donors per (page, head)
+        used[ids] = True
+    assert (pool[~used] == 173).all()
+
+
+def test_write_codec_pages_beyond_signed_32bit_byte_offset():
+    # the physical page offset id * page_bytes past 2^31 bytes (packing.py:14
+    # widens the id to int64): a 256-token page written there holds the same
+    # bytes as one written at id 0
+    from inquant.codec import CodecConfig, quantize
+    from inquant.value_codec import quantize_values
+    from inquant_vllm import PageLayout, write_codec_pages
+    layout = PageLayout(256, 4)
+    far = 2 ** 31 // layout.page_bytes + 2
+    pool = torch.zeros((far + 1, layout.page_bytes), device="cuda", dtype=torch.uint8)
+    k, v = _kv(919, (2, 4, 256, 128))
+    kq = quantize(k, CodecConfig(donor_policy="min_error"))
+    vq = quantize_values(v, bits=2, group_size=64)
+    ids = torch.tensor([far, 0], device="cuda", dtype=torch.int64)
+    assert far * layout.page_bytes > 2 ** 31
+    write_codec_pages(kq, vq, layout, pool, ids)
+    exp = oracle.pack_pages(oracle.k4_quantize(_np(k.float()), 8, 0.125, "min_error"),
+                            oracle.v_quantize(_np(v.float()), 2, 64), 4, 256)
+    np.testing.assert_array_equal(_np(pool[ids]), exp)
+    assert not pool[1:far].any()
+
+
 def _paged_case(seed, block, pages, tail, h=4, hq=28, spare=7):
     from inquant_vllm import PageLayout, pack_pages
     layout = PageLayout(block, h)
@@ -271,7 +329,8 @@ def test_pack_pages_into_is_one_launch_and_reports_non_finite_inputs(block):
 def test_short_pages_half_inputs_partial_workgroups_and_skipped_ids(block):
     # 16- and 32-token pages are encoded one wavefront per (page, head), four
     # pages per workgroup: six pages leave the second workgroup half empty,
-    # and ids outside the pool (negative or too large) are skipped
+    # and ids outside the pool (negative or too large) write nothing and
+    # raise after the launch; the next in-range call finds the flags cleared
     from inquant_vllm import PageLayout, pack_pages_into
     layout = PageLayout(block, 4)
     pool = torch.full((8, layout.page_bytes), 7, device="cuda", dtype=torch.uint8)
@@ -281,10 +340,14 @@ def test_short_pages_half_inputs_partial_workgroups_and_skipped_ids(block):
     v = torch.randn((6, 4, block, 128), generator=g, device="cuda")
     k[..., 40:43] *= 30
     k, v = k.to(torch.float16), v.to(torch.float16)
-    pack_pages_into(k, v, layout, pool, ids)
+    with pytest.raises(ValueError, match="outside the destination pool"):
+        pack_pages_into(k, v, layout, pool, ids)
     live = [0, 3, 4, 5]
     kq = oracle.k4_quantize(_np(k[live].float()), 8, 0.125, "min_error")
     vq = oracle.v_quantize(_np(v[live].float()), 2, 64)
     np.testing.assert_array_equal(_np(pool[torch.tensor([3, 0, 5, 6], device="cuda")]),
                                   oracle.pack_pages(kq, vq, 4, block))
     assert (pool[torch.tensor([1, 2, 4, 7], device="cuda")] == 7).all()
+    pack_pages_into(k[live], v[live], layout, pool, ids[live])      # flags cleared: no error
+    np.testing.assert_array_equal(_np(pool[torch.tensor([3, 0, 5, 6], device="cuda")]),
+                                  oracle.pack_pages(kq, vq, 4, block))

@@ -62,6 +62,69 @@ def test_prefill_varlen_sequences_and_strided_views():
         assert np.abs(got[a:b] - exp).max() <= 1e-2
 
 
+def _outlier_qkv(seed, n, hq, h):
+    # the bench's prefill input: N(0, 1) bf16 with five of 128 key channels
+    # (two adjacent pairs and one single channel, ~4%) scaled by 20
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    q = torch.randn((n, hq, 128), generator=g, device="cuda").to(torch.bfloat16)
+    k = torch.randn((n, h, 128), generator=g, device="cuda")
+    k[..., [17, 18, 60, 61, 127]] *= 20
+    v = torch.randn((n, h, 128), generator=g, device="cuda")
+    return q, k.to(torch.bfloat16), v.to(torch.bfloat16)
+
+
+def _bound(v):
+    """The bound the kernel meets: the softmax weights are rounded to bf16
+    before P.V (as flash attention does), a relative change of at most 2^-8
+    per weight, so an output moves by at most 2^-8 * max|V|; 1e-4 covers the
+    fp32 accumulation.  (8K case: max|V| ~ 4.9, bound ~ 1.9e-2, measured
+    ~ 4e-3.)"""
+    return 2 ** -8 * float(np.abs(v).max()) + 1e-4
+
+
+def test_prefill_qwen_8k_matches_causal_oracle():
+    # the 8192-token Qwen2.5-7B causal prefill that the bench times (28 query
+    # heads over 4 KV heads): every row of the first and last query heads,
+    # and three row bands (first, middle, last 256 rows) of every head
+    from inquant_vllm import prefill_attention
+    n, hq, h = 8192, 28, 4
+    q, k, v = _outlier_qkv(8192, n, hq, h)
+    cu = torch.tensor([0, n], dtype=torch.int32, device="cuda")
+    out = prefill_attention(q, k, v, cu, n, 128 ** -0.5)
+    out32 = prefill_attention(q, k, v, cu, n, 128 ** -0.5, torch.empty(q.shape, device="cuda"))
+    assert torch.equal(out, out32.to(torch.bfloat16))
+    qn, kn, vn, got = _np(q), _np(k), _np(v), _np(out32)
+    bands = np.concatenate([np.arange(0, 256), np.arange(4000, 4256), np.arange(n - 256, n)])
+    worst = 0.0
+    for rows, heads in ((np.arange(n), [0, hq - 1]), (bands, list(range(hq)))):
+        exp = oracle.causal_attend_rows(qn, kn, vn, 128 ** -0.5, rows, heads)
+        err = np.abs(got[rows][:, heads] - exp)
+        worst = max(worst, float(err.max()))
+        bf = _np(out)[rows][:, heads]
+        assert (np.abs(bf - exp) <= _bound(vn) + 2 ** -8 * np.abs(exp)).all()   # + bf16 output rounding
+    print(f"8K prefill max-abs error {worst:.3e} (bound {_bound(vn):.3e})", flush=True)
+    assert worst <= _bound(vn)
+
+
+def test_prefill_varlen_batch_of_4k_tokens_matches_causal_oracle():
+    # four sequences (4648 tokens) in one launch, every row of every head
+    from inquant_vllm import prefill_attention
+    lens = [1500, 37, 2600, 511]
+    n, hq, h = sum(lens), 28, 4
+    q, k, v = _outlier_qkv(4648, n, hq, h)
+    starts = np.cumsum([0] + lens)
+    cu = torch.tensor(starts, dtype=torch.int32, device="cuda")
+    out = torch.full((n, hq, 128), float("nan"), device="cuda")
+    prefill_attention(q, k, v, cu, max(lens), 128 ** -0.5, out)
+    got, qn, kn, vn = _np(out), _np(q), _np(k), _np(v)
+    worst = 0.0
+    for a, b in zip(starts[:-1], starts[1:]):
+        exp = oracle.causal_attend_rows(qn[a:b], kn[a:b], vn[a:b], 128 ** -0.5, np.arange(b - a), range(hq))
+        worst = max(worst, float(np.abs(got[a:b] - exp).max()))
+    print(f"varlen prefill max-abs error {worst:.3e} (bound {_bound(vn):.3e})", flush=True)
+    assert worst <= _bound(vn)
+
+
 def test_prefill_rejects_bad_arguments():
     from inquant_vllm import prefill_attention
     q, k, v = _qkv(1, 8, 4, 2, torch.bfloat16)
