@@ -220,94 +220,77 @@ def time_decode_cfg3(device, layers=32, steps=20, warmup=3):
     return out
 
 
-def time_encode(device, reps=10):
-    """Mistral-7B layer encode (config 3): K4 min_error + V2 g64 of [1, 8, 32768, 128] bf16."""
+def time_encode(device, sets=4, cycles=3):
+    """Mistral-7B layer encode (config 3): K4 min_error + V2 g64 of [1, 8, 32768, 128]
+    bf16.  `sets` distinct layers (inputs and outputs, 4 x 162 MB = 648 MB,
+    more than twice the 256 MB Infinity Cache) are encoded in turn, `cycles`
+    times, in one HIP graph, so every encode reads its layer from HBM."""
     import torch
     from inquant import _native as nat
     H, T, B = 8, 32768, 256
     nb = T // B
-    gen = torch.Generator(device=device).manual_seed(3)
-    k = kv_tensor(gen, H, T, device, frac_groups=(3, 3, 3, 1))
-    v = kv_tensor(gen, H, T, device, frac_groups=(3, 3, 3, 1))
-    kb = k[0].reshape(H, nb, B, 128).permute(1, 0, 2, 3)
-    vb = v[0].reshape(H, nb, B, 128).permute(1, 0, 2, 3)
     S = 16
-    pay = torch.empty((nb, H, B, 64), dtype=torch.uint8, device=device)
-    sc = torch.empty((nb, H, 128), dtype=torch.float32, device=device)
-    src = torch.empty((nb, H, S), dtype=torch.uint8, device=device)
-    don = torch.empty_like(src)
-    pad = torch.empty((nb, H, S), dtype=torch.float32, device=device)
-    vpay = torch.empty((nb, H, B, 32), dtype=torch.uint8, device=device)
-    vsc = torch.empty((nb, H, B, 2), dtype=torch.float16, device=device)
-    voff = torch.empty_like(vsc)
-    bad = torch.zeros(2, dtype=torch.int32, device=device)
     lib = nat.lib()
-    stream = nat.stream_handle(torch.device(device))
+    bad = torch.zeros(2, dtype=torch.int32, device=device)
+    work = []
+    for i in range(sets):
+        gen = torch.Generator(device=device).manual_seed(3 + i)
+        k = kv_tensor(gen, H, T, device, frac_groups=(3, 3, 3, 1))
+        v = kv_tensor(gen, H, T, device, frac_groups=(3, 3, 3, 1))
+        w = {"k": k, "v": v,
+             "kb": k[0].reshape(H, nb, B, 128).permute(1, 0, 2, 3),
+             "vb": v[0].reshape(H, nb, B, 128).permute(1, 0, 2, 3),
+             "pay": torch.empty((nb, H, B, 64), dtype=torch.uint8, device=device),
+             "sc": torch.empty((nb, H, 128), dtype=torch.float32, device=device),
+             "src": torch.empty((nb, H, S), dtype=torch.uint8, device=device),
+             "don": torch.empty((nb, H, S), dtype=torch.uint8, device=device),
+             "pad": torch.empty((nb, H, S), dtype=torch.float32, device=device),
+             "vpay": torch.empty((nb, H, B, 32), dtype=torch.uint8, device=device),
+             "vsc": torch.empty((nb, H, B, 2), dtype=torch.float16, device=device),
+             "voff": torch.empty((nb, H, B, 2), dtype=torch.float16, device=device)}
+        work.append(w)
 
-    def once():
+    def once(w, st):
         # the cache's block encode (keys K4, values V2 in one launch)
-        nat.check(lib.iq_kv_quantize(kb.data_ptr(), vb.data_ptr(), nat.IQ_BF16, nat.strides4(kb), nat.strides4(vb),
-                                     nb, H, B, 128, S, 8, 1, pay.data_ptr(), sc.data_ptr(), src.data_ptr(),
-                                     don.data_ptr(), 1, pad.data_ptr(), 2, 64, vpay.data_ptr(), vsc.data_ptr(),
-                                     voff.data_ptr(), bad.data_ptr(), bad.data_ptr() + 4, stream))
+        nat.check(lib.iq_kv_quantize(w["kb"].data_ptr(), w["vb"].data_ptr(), nat.IQ_BF16, nat.strides4(w["kb"]),
+                                     nat.strides4(w["vb"]), nb, H, B, 128, S, 8, 1, w["pay"].data_ptr(),
+                                     w["sc"].data_ptr(), w["src"].data_ptr(), w["don"].data_ptr(), 1,
+                                     w["pad"].data_ptr(), 2, 64, w["vpay"].data_ptr(), w["vsc"].data_ptr(),
+                                     w["voff"].data_ptr(), bad.data_ptr(), bad.data_ptr() + 4, st))
 
-    for _ in range(2):
-        once()
-    torch.cuda.synchronize()
-    # replay the encode launches as a HIP graph so the host's launch cost is
-    # not part of the measured layer time
-    graph = torch.cuda.CUDAGraph()
-    s = torch.cuda.Stream()
-    s.wait_stream(torch.cuda.current_stream())
-    with torch.cuda.stream(s):
-        stream = nat.stream_handle(torch.device(device))
-        once()
-        torch.cuda.synchronize()
-        with torch.cuda.graph(graph, stream=s):
-            for _ in range(reps):
-                once()
-    torch.cuda.synchronize()
-    graph.replay()
-    torch.cuda.synchronize()
-    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    start.record()
-    graph.replay()
-    stop.record()
-    torch.cuda.synchronize()
-    ms = start.elapsed_time(stop) / reps
+    def once_k4v(w, st):
+        # the same layer with K4-coded values (the cache's default
+        # value_bits=None): keys and values K4 in one launch (iq_k4_quantize_kv);
+        # the value outputs reuse the V2 payload storage
+        vk = w.setdefault("vk", [torch.empty_like(w[n]) for n in ("pay", "sc", "src", "don", "pad")])
+        nat.check(lib.iq_k4_quantize_kv(w["kb"].data_ptr(), w["vb"].data_ptr(), nat.IQ_BF16, nat.strides4(w["kb"]),
+                                        nat.strides4(w["vb"]), nb, H, B, 128, S, 8, 1, w["pay"].data_ptr(),
+                                        w["sc"].data_ptr(), w["src"].data_ptr(), w["don"].data_ptr(),
+                                        w["pad"].data_ptr(), *[t.data_ptr() for t in vk], 1, bad.data_ptr(),
+                                        bad.data_ptr() + 4, st))
+
+    def rotated(fn):
+        def launch():
+            st = nat.stream_handle(torch.device(device))
+            for _ in range(cycles):
+                for w in work:
+                    fn(w, st)
+        return launch
+
+    calls = sets * cycles
+    ms = _graph_us(device, rotated(once), reps=1) * 1e-3 / calls
     assert bad.tolist() == [0, 0]
-    enc_bytes = 2 * k.numel() * 2 + pay.numel() + sc.numel() * 4 + src.numel() * 2 + pad.numel() * 4 \
-        + vpay.numel() + vsc.numel() * 4
-
-    # the same layer with K4-coded values (the cache's default value_bits=None):
-    # keys and values K4 in one launch (iq_k4_quantize_kv)
-    vk = [torch.empty_like(t) for t in (pay, sc, src, don, pad)]
-
-    def once_k4v():
-        nat.check(lib.iq_k4_quantize_kv(kb.data_ptr(), vb.data_ptr(), nat.IQ_BF16, nat.strides4(kb),
-                                        nat.strides4(vb), nb, H, B, 128, S, 8, 1, pay.data_ptr(), sc.data_ptr(),
-                                        src.data_ptr(), don.data_ptr(), pad.data_ptr(), *[t.data_ptr() for t in vk],
-                                        1, bad.data_ptr(), bad.data_ptr() + 4, stream))
-
-    graph2 = torch.cuda.CUDAGraph()
-    with torch.cuda.stream(s):
-        once_k4v()
-        torch.cuda.synchronize()
-        with torch.cuda.graph(graph2, stream=s):
-            for _ in range(reps):
-                once_k4v()
-    torch.cuda.synchronize()
-    graph2.replay()
-    torch.cuda.synchronize()
-    start.record()
-    graph2.replay()
-    stop.record()
-    torch.cuda.synchronize()
-    ms_k4v = start.elapsed_time(stop) / reps
+    ms_k4v = _graph_us(device, rotated(once_k4v), reps=1) * 1e-3 / calls
     assert bad.tolist() == [0, 0]
+    w = work[0]
+    enc_bytes = 2 * w["k"].numel() * 2 + w["pay"].numel() + w["sc"].numel() * 4 + w["src"].numel() * 2 \
+        + w["pad"].numel() * 4 + w["vpay"].numel() + w["vsc"].numel() * 4
+    del work
+    torch.cuda.empty_cache()
     return {"encode_mtok_s": T / (ms * 1e-3) / 1e6, "encode_ms_per_layer": ms,
             "encode_gbs": enc_bytes / (ms * 1e-3) / 1e9, "encode_bytes_per_layer": enc_bytes,
-            "k4_values_mtok_s": T / (ms_k4v * 1e-3) / 1e6, "k4_values_ms_per_layer": ms_k4v}
+            "k4_values_mtok_s": T / (ms_k4v * 1e-3) / 1e6, "k4_values_ms_per_layer": ms_k4v,
+            "rotated_layers": sets, "rotated_bytes": sets * enc_bytes}
 
 
 def _graph_us(device, launch, reps=10):
@@ -334,13 +317,16 @@ def _graph_us(device, launch, reps=10):
     return start.elapsed_time(stop) * 1e3 / reps
 
 
-def time_next_rows(device):
+def time_next_rows(device, sets=8):
     """The rows next to the decode path, inputs resident, launches replayed in
     a HIP graph: materialize (K4 keys and V2 g64 values of one config 2 layer,
     4 heads x 32768 tokens, dequantized to bf16), encode into 256- and
     16-token pages (keys K4 min_error + role map + values V2 of 32768 tokens
     x 4 heads, one launch) and causal prefill attention over exact K/V (one
-    8192-token Qwen2.5-7B sequence, 28 query heads over 4 KV heads, bf16)."""
+    8192-token Qwen2.5-7B sequence, 28 query heads over 4 KV heads, bf16).
+    Materialize and the page encodes run over `sets` distinct layers in turn
+    (8 x ~81 MB = ~650 MB, above the 256 MB Infinity Cache), so each call
+    reads its inputs from HBM."""
     import torch
     from inquant import _native as nat
     from inquant.codec import CodecConfig, quantize
@@ -349,32 +335,37 @@ def time_next_rows(device):
     lib = nat.lib()
     H, T, D = 4, 32768, 128
     gen = torch.Generator(device=device).manual_seed(6)
-    k = kv_tensor(gen, H, T, device)
-    v = kv_tensor(gen, H, T, device)
+    kv = [(kv_tensor(gen, H, T, device), kv_tensor(gen, H, T, device)) for _ in range(sets)]
+    k, v = kv[0]
     out = {}
 
     # materialize: both dequantizers into bf16 K and V
-    pk = quantize(k, CodecConfig(donor_policy="min_error"))
-    pv = quantize_values(v, 2, 64)
-    kd, vd = torch.empty_like(k), torch.empty_like(v)
-    S = pk.salient_channels.shape[-1]
+    mats = []
+    for kk, vv in kv:
+        pk = quantize(kk, CodecConfig(donor_policy="min_error"))
+        pv = quantize_values(vv, 2, 64)
+        mats.append((pk, pv, torch.empty_like(kk), torch.empty_like(vv)))
+    S = mats[0][0].salient_channels.shape[-1]
 
     def materialize():
         st = nat.stream_handle(torch.device(device))
-        nat.check(lib.iq_k4_dequantize(pk.payload.data_ptr(), pk.scales.data_ptr(), pk.salient_channels.data_ptr(),
-                                       pk.donor_channels.data_ptr(), 1, pk.padding.data_ptr(), H, T, D, S,
-                                       kd.data_ptr(), nat.IQ_BF16, st))
-        nat.check(lib.iq_v_dequantize(pv.payload.data_ptr(), pv.scales.data_ptr(), pv.offsets.data_ptr(), H * T, D,
-                                      2, 64, vd.data_ptr(), nat.IQ_BF16, st))
+        for pk, pv, kd, vd in mats:
+            nat.check(lib.iq_k4_dequantize(pk.payload.data_ptr(), pk.scales.data_ptr(),
+                                           pk.salient_channels.data_ptr(), pk.donor_channels.data_ptr(), 1,
+                                           pk.padding.data_ptr(), H, T, D, S, kd.data_ptr(), nat.IQ_BF16, st))
+            nat.check(lib.iq_v_dequantize(pv.payload.data_ptr(), pv.scales.data_ptr(), pv.offsets.data_ptr(),
+                                          H * T, D, 2, 64, vd.data_ptr(), nat.IQ_BF16, st))
 
-    us = _graph_us(device, materialize)
+    us = _graph_us(device, materialize, reps=2) / sets
+    pk, pv, kd, vd = mats[-1]
     assert torch.equal(kd, pk.dequantize(torch.bfloat16)) and torch.equal(vd, pv.dequantize(torch.bfloat16))
     mat_bytes = sum(t.numel() * t.element_size() for t in pk.tensors.values()) \
         + sum(t.numel() * t.element_size() for t in (pv.payload, pv.scales, pv.offsets)) + 2 * k.numel() * 2
     out["materialize_cfg2"] = {"us_per_layer": round(us, 3), "bytes_per_layer": mat_bytes,
                                "gbs": round(mat_bytes / (us * 1e-6) / 1e9, 2),
-                               "hbm_frac": round(mat_bytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
-    del kd, vd, pk, pv
+                               "hbm_frac": round(mat_bytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+                               "rotated_layers": sets}
+    del mats, pk, pv, kd, vd
 
     # encode into pages (the plugin's seal of a prefill: 256-token pages, the
     # reference layout's largest, and the 16-token pages of config 4), flags
@@ -382,26 +373,31 @@ def time_next_rows(device):
     for B in (256, 16):
         layout = PageLayout(B, H)
         P = T // B
-        kp = k[0].reshape(H, P, B, D).transpose(0, 1)
-        vp = v[0].reshape(H, P, B, D).transpose(0, 1)
-        pool = torch.empty((P, layout.page_bytes), dtype=torch.uint8, device=device)
+        jobs = []
+        for kk, vv in kv:
+            jobs.append((kk[0].reshape(H, P, B, D).transpose(0, 1), vv[0].reshape(H, P, B, D).transpose(0, 1),
+                         torch.empty((P, layout.page_bytes), dtype=torch.uint8, device=device)))
         ids = torch.arange(P, dtype=torch.int32, device=device)
         flags = torch.zeros(8, dtype=torch.int32, device=device)     # two (key, value, page id) triples
 
         def encode_pages():
             st = nat.stream_handle(torch.device(device))
-            nat.check(lib.iq_encode_pages(kp.data_ptr(), vp.data_ptr(), nat.IQ_BF16, nat.strides4(kp),
-                                          nat.strides4(vp), P, H, B, pool.data_ptr(), P, ids.data_ptr(), 4,
-                                          flags.data_ptr(), flags.data_ptr() + 16, st))
+            for kp, vp, pool in jobs:
+                nat.check(lib.iq_encode_pages(kp.data_ptr(), vp.data_ptr(), nat.IQ_BF16, nat.strides4(kp),
+                                              nat.strides4(vp), P, H, B, pool.data_ptr(), P, ids.data_ptr(), 4,
+                                              flags.data_ptr(), flags.data_ptr() + 16, st))
 
-        us = _graph_us(device, encode_pages)
+        us = _graph_us(device, encode_pages, reps=2) / sets
         assert flags[:3].tolist() == [0, 0, 0]
         enc_bytes = 2 * k.numel() * 2 + P * layout.page_bytes
         out[f"encode_pages_b{B}"] = {"tokens": T, "heads": H, "page_tokens": B, "us": round(us, 3),
                                      "mtok_s": round(T / us, 2), "bytes": enc_bytes,
                                      "gbs": round(enc_bytes / (us * 1e-6) / 1e9, 2),
-                                     "hbm_frac": round(enc_bytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
-        del pool, kp, vp
+                                     "hbm_frac": round(enc_bytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+                                     "rotated_layers": sets}
+        del jobs
+    del kv
+    torch.cuda.empty_cache()
 
     # causal prefill attention over exact K/V
     Sq, Hq = 8192, 28
