@@ -280,6 +280,21 @@ int iq_encode_pages(const void *keys, const void *values, int dtype, const int64
                     void *stream);
 
 /*
+ * iq_encode_pages with pages at arbitrary token rows of one key and one value
+ * tensor: page n reads tokens page_rows[n] .. page_rows[n] + B - 1 (element
+ * offsets page_rows[n] * k_strides[2] and page_rows[n] * v_strides[2]; the
+ * page strides k_strides[0] / v_strides[0] are unused), i64 device array, or
+ * NULL for iq_encode_pages' layout.  One launch seals the full pages of
+ * several requests of a batch (each at its own row of the batch's key/value
+ * rows, or at its own slot of a dense page buffer).  Replaces the per-request
+ * pack_pages_into calls of backend.py:106-116.
+ */
+int iq_encode_pages_at(const void *keys, const void *values, int dtype, const int64_t *k_strides,
+                       const int64_t *v_strides, const int64_t *page_rows, int64_t n_pages, int64_t H,
+                       int64_t block_tokens, uint8_t *pool, int64_t pool_pages, const void *page_ids,
+                       int id_bytes, int *flags, int *next_flags, void *stream);
+
+/*
  * Decode n_pages contiguous pages to keys/values [n, H, B, 128] of out_dtype.
  * Replaces unpack_pages_reference (layout.py:84-100).
  */
@@ -298,9 +313,11 @@ int64_t iq_paged_workspace_floats(int64_t Hq, int64_t n_seq, int64_t max_pages, 
  *   pool contribute nothing); max_pages bounds every sequence's page count;
  *   seq_info i32 [n_seq, 3] = (pages, tail tokens, sink tokens) on the device,
  *   or NULL with n_seq == 1 and the host values n_pages, tail_t, sink_t;
- *   dense bf16 [n_seq, 2, H, B + 4, 128] (stride dense_stride_seq elements):
- *   slots 0..3 the sink, 4.. the current partial page (kernels.py:37-48 masks:
- *   packed tokens before the sink length and tail slots inside the sink are skipped);
+ *   dense bf16 [slots, 2, H, B + 4, 128] (stride dense_stride_seq elements):
+ *   rows 0..3 the sink, 4.. the current partial page (kernels.py:37-48 masks:
+ *   packed tokens before the sink length and tail slots inside the sink are
+ *   skipped); sequence i reads dense slot dense_slots[i] (i32 device array of
+ *   in-range slots), or slot i when dense_slots is NULL;
  *   out [n_seq, Hq, 128] (stride out_stride_seq) of out_dtype.
  * Keys/values are decoded and rounded to bf16 as dequantize-then-attend does;
  * logits, softmax and P.V accumulate in fp32.  Replaces paged_decode
@@ -310,8 +327,9 @@ int iq_paged_decode(const void *q, int64_t q_stride_seq, int64_t q_stride_h, int
                     const uint8_t *pool, int64_t pool_pages, int64_t H, int64_t block_tokens,
                     const int32_t *block_tables, int64_t bt_stride, int64_t max_pages,
                     const int32_t *seq_info, int64_t n_pages, int64_t tail_t, int64_t sink_t,
-                    const void *dense, int64_t dense_stride_seq, float scale, float *workspace,
-                    int64_t workspace_floats, void *out, int64_t out_stride_seq, int out_dtype, void *stream);
+                    const void *dense, int64_t dense_stride_seq, const int32_t *dense_slots, float scale,
+                    float *workspace, int64_t workspace_floats, void *out, int64_t out_stride_seq,
+                    int out_dtype, void *stream);
 
 /*
  * Causal self-attention over exact K/V for prefill, vLLM token-major layout:

@@ -42,6 +42,9 @@ struct K4Args {
     const uint16_t *v;
     int64_t vsb, vsh, vst;
     int *vbad, *badid, *clear;  // value flag; out-of-range page id flag; flag triple the next page launch uses, zeroed here
+    // page mode, optional: page b starts at token row page_rows[b] of x / v
+    // (offsets page_rows[b] * st, page_rows[b] * vst) instead of b * sb, b * vsb
+    const int64_t *page_rows;
     // fused key/value mode (k4_encode_tile<..., VB = 2 or 4>): the value rows
     // of v are encoded group-wise into the outputs of iq_v_quantize
     uint8_t *vpayload;
@@ -398,7 +401,9 @@ __device__ __forceinline__ void k4_tile_body(const K4Args &a, int64_t b, int64_t
         page = a.pool + id * a.page_bytes;
         if (threadIdx.x < TILE_D) s_role[threadIdx.x] = -1;
     }
-    const uint16_t *xr = (const uint16_t *)a.x + b * a.sb + h * a.sh;
+    const int64_t prow = PAGES && a.page_rows ? a.page_rows[b] : -1;
+    const int64_t xoff = prow >= 0 ? prow * a.st : b * a.sb, voff = prow >= 0 ? prow * a.vst : b * a.vsb;
+    const uint16_t *xr = (const uint16_t *)a.x + xoff + h * a.sh;
     const int T = NCH > 0 ? NCH * CH : (int)a.T;
     const int stride = (int)min(a.stride, (int64_t)TILE_T);   // a larger stride samples token 0 only
     const int ns = (T + stride - 1) / stride;
@@ -605,7 +610,7 @@ __device__ __forceinline__ void k4_tile_body(const K4Args &a, int64_t b, int64_t
     u32x4_t vraw[NCH > 0 ? VIT : 1][2];
     auto vload = [&](int it, u32x4_t(&r)[2]) {
         const int t = min(vtok0 + 24 * it, T - 1);
-        const u32x4_t *p = (const u32x4_t *)(a.v + b * a.vsb + h * a.vsh + (int64_t)t * a.vst + 16 * vj);
+        const u32x4_t *p = (const u32x4_t *)(a.v + voff + h * a.vsh + (int64_t)t * a.vst + 16 * vj);
         r[0] = __builtin_nontemporal_load(p);
         r[1] = __builtin_nontemporal_load(p + 1);
     };
@@ -790,8 +795,9 @@ __global__ __launch_bounds__(K4_THREADS) void k4_encode_page_rows(K4Args a, int6
         return;
     }
     uint8_t *const page = a.pool + id * a.page_bytes;
-    const uint16_t *const xr = (const uint16_t *)a.x + b * a.sb + h * a.sh;
-    const uint16_t *const vr = a.v + b * a.vsb + h * a.vsh;
+    const int64_t prow = a.page_rows ? a.page_rows[b] : -1;
+    const uint16_t *const xr = (const uint16_t *)a.x + (prow >= 0 ? prow * a.st : b * a.sb) + h * a.sh;
+    const uint16_t *const vr = a.v + (prow >= 0 ? prow * a.vst : b * a.vsb) + h * a.vsh;
 
     // every load of the row first: key segment i = lane + 64 k is token i / 16,
     // channels 8 (i % 16) ..; value lane (vj, vt) reads 16 channels of token vt + 8 it
@@ -1146,6 +1152,15 @@ extern "C" int iq_encode_pages(const void *keys, const void *values, int dtype, 
                                uint8_t *pool, int64_t pool_pages, const void *page_ids, int id_bytes, int *flags,
                                int *next_flags, void *stream)
 {
+    return iq_encode_pages_at(keys, values, dtype, k_strides, v_strides, nullptr, n_pages, H, block_tokens, pool,
+                              pool_pages, page_ids, id_bytes, flags, next_flags, stream);
+}
+
+extern "C" int iq_encode_pages_at(const void *keys, const void *values, int dtype, const int64_t *k_strides,
+                                  const int64_t *v_strides, const int64_t *page_rows, int64_t n_pages, int64_t H,
+                                  int64_t block_tokens, uint8_t *pool, int64_t pool_pages, const void *page_ids,
+                                  int id_bytes, int *flags, int *next_flags, void *stream)
+{
     IQ_CHECK_ARG(keys && values && k_strides && v_strides && pool && page_ids && flags && next_flags,
                  "iq_encode_pages: null pointer");
     IQ_CHECK_ARG(dtype == IQ_BF16 || dtype == IQ_F16, "iq_encode_pages: keys/values must be bf16 or f16");
@@ -1195,6 +1210,7 @@ extern "C" int iq_encode_pages(const void *keys, const void *values, int dtype, 
     a.vbad = flags + 1;
     a.badid = flags + 2;
     a.clear = next_flags;
+    a.page_rows = page_rows;
     if (n_pages == 0) return IQ_OK;
     const hipStream_t st = (hipStream_t)stream;
     if (B <= 32) {

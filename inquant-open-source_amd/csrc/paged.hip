@@ -179,8 +179,9 @@ struct PagedArgs {
     int64_t bt_ss, max_pages;
     const int32_t *seq_info;           // [seq, 3] (pages, tail, sink) or null
     int npg0, tail0, sink0;            // used when seq_info is null
-    const uint16_t *dense;             // [seq, 2, H, B + 4, 128] bf16
+    const uint16_t *dense;             // [slots, 2, H, B + 4, 128] bf16
     int64_t dense_ss;
+    const int32_t *dense_slots;        // dense slot of each sequence, or null (slot = sequence)
     int max_parts;
     float c_log2;                      // softmax scale * log2(e)
     float *ws;                         // seq * Hq * max_parts partials (Partials layout)
@@ -287,7 +288,7 @@ __device__ __forceinline__ void paged_body(const PagedArgs &a, PagedSmem<NPG> &s
     } else {
         slot0 = (p - geo.npp) * PART;
         ntok = min(PART, B + 4 - slot0);
-        const uint16_t *dn = a.dense + sq * a.dense_ss;
+        const uint16_t *dn = a.dense + (int64_t)(a.dense_slots ? a.dense_slots[sq] : sq) * a.dense_ss;
         dk = dn + ((int64_t)h * (B + 4) + slot0) * D;
         dv = dn + ((int64_t)(a.H + h) * (B + 4) + slot0) * D;
     }
@@ -889,9 +890,9 @@ extern "C" int iq_paged_decode(const void *q, int64_t q_stride_seq, int64_t q_st
                                const uint8_t *pool, int64_t pool_pages, int64_t H, int64_t block_tokens,
                                const int32_t *block_tables, int64_t bt_stride, int64_t max_pages,
                                const int32_t *seq_info, int64_t n_pages, int64_t tail_t, int64_t sink_t,
-                               const void *dense, int64_t dense_stride_seq, float scale, float *workspace,
-                               int64_t workspace_floats, void *out, int64_t out_stride_seq, int out_dtype,
-                               void *stream)
+                               const void *dense, int64_t dense_stride_seq, const int32_t *dense_slots,
+                               float scale, float *workspace, int64_t workspace_floats, void *out,
+                               int64_t out_stride_seq, int out_dtype, void *stream)
 {
     IQ_CHECK_ARG(q && pool && dense && workspace && out, "iq_paged_decode: null pointer");
     IQ_CHECK_ARG(H >= 1 && Hq >= H && Hq % H == 0 && Hq / H <= 16, "iq_paged_decode: expected 1..16 query heads per KV head");
@@ -930,6 +931,7 @@ extern "C" int iq_paged_decode(const void *q, int64_t q_stride_seq, int64_t q_st
     a.sink0 = (int)sink_t;
     a.dense = (const uint16_t *)dense;
     a.dense_ss = dense_stride_seq;
+    a.dense_slots = dense_slots;
     a.max_parts = (int)parts;
     a.c_log2 = scale * 1.4426950408889634f;
     a.ws = workspace;

@@ -49,22 +49,27 @@ def paged_decode(query, cache, blocks, dense, num_pages, tail_tokens,
     nat.check(nat.lib().iq_paged_decode(
         query.data_ptr(), 0, 128, hq, 1, cache.data_ptr(), cache.shape[0], hkv, b,
         table.data_ptr() if table.numel() else None, 0, int(num_pages), None, int(num_pages), int(tail_tokens),
-        int(sink_tokens), dense.data_ptr(), 0, float(scale), scratch.data_ptr(), need,
+        int(sink_tokens), dense.data_ptr(), 0, None, float(scale), scratch.data_ptr(), need,
         output.data_ptr(), 0, nat.dtype_code(output.dtype), nat.stream_handle(query.device)))
     return output
 
 
 def paged_decode_batch(query, cache, block_tables, seq_info, dense, max_pages, layout, workspace, scale,
-                       output=None):
+                       output=None, dense_slots=None):
     """query bf16 [n, Hq, 128]; block_tables int32 [n, >= max_pages]; seq_info int32
     [n, 3] device tensor of (pages, tail tokens, sink tokens); dense bf16
-    [n, 2, kv_heads, block_size + 4, 128].  Returns [n, Hq, 128]."""
+    [n, 2, kv_heads, block_size + 4, 128], or [slots, 2, kv_heads, block_size + 4,
+    128] with dense_slots an int32 [n] device tensor naming each sequence's
+    slot (the caller keeps them in range).  Returns [n, Hq, 128]."""
     hkv, b = layout.heads, layout.block_size
     hq = _check_query(query, hkv)
     _check_pool(cache, layout)
     n = query.shape[0]
-    if tuple(dense.shape) != (n, 2, hkv, b + 4, 128) or dense.dtype != torch.bfloat16:
+    rows = n if dense_slots is None else dense.shape[0]
+    if tuple(dense.shape) != (rows, 2, hkv, b + 4, 128) or dense.dtype != torch.bfloat16:
         raise ValueError("Expected dense BF16 [sequences, 2, kv_heads, block_size + 4, 128]")
+    if dense_slots is not None and (tuple(dense_slots.shape) != (n,) or dense_slots.dtype != torch.int32):
+        raise ValueError("Expected int32 dense slots [sequences]")
     if block_tables.ndim != 2 or block_tables.shape[0] != n or block_tables.shape[1] < max_pages \
             or block_tables.dtype != torch.int32:
         raise ValueError("Expected int32 block tables [sequences, >= max_pages]")
@@ -80,19 +85,26 @@ def paged_decode_batch(query, cache, block_tables, seq_info, dense, max_pages, l
     nat.check(nat.lib().iq_paged_decode(
         query.data_ptr(), hq * 128, 128, hq, n, cache.data_ptr(), cache.shape[0], hkv, b,
         block_tables.data_ptr(), block_tables.shape[1], int(max_pages), seq_info.data_ptr(), 0, 0, 0,
-        dense.data_ptr(), dense[0].numel(), float(scale), scratch.data_ptr(), need,
+        dense.data_ptr(), dense[0].numel(), None if dense_slots is None else dense_slots.contiguous().data_ptr(),
+        float(scale), scratch.data_ptr(), need,
         output.data_ptr(), hq * 128, nat.dtype_code(output.dtype), nat.stream_handle(query.device)))
     return output
 
 
-def prefill_attention(query, key, value, cu_seqlens, max_seqlen, scale, output=None):
+def prefill_attention(query, key, value, cu_seqlens, max_seqlen, scale, output=None, *, check_lengths=False):
     """Causal self-attention of a prefill over its exact K/V (replaces the
     plugin's flash_attn_varlen_func(..., causal=True) call, backend.py:139-144).
 
     query [tokens, Hq, 128], key/value [tokens, H, 128] (bf16 or f16, rows
     16-byte aligned), cu_seqlens int32 [sequences + 1] on the device,
     max_seqlen >= every sequence length.  Returns (or fills) output
-    [tokens, Hq, 128] of the query dtype or float32."""
+    [tokens, Hq, 128] of the query dtype or float32.
+
+    Contract (as flash_attn_varlen_func's max_seqlen_q): the launch covers
+    max_seqlen query rows per sequence, so the query rows of a sequence
+    longer than max_seqlen past that count are not written.  cu_seqlens lives
+    on the device and is not read back; with ``check_lengths=True`` the
+    lengths are read (one synchronization) and a longer sequence raises."""
     if query.ndim != 3 or key.ndim != 3 or key.shape != value.shape or query.shape[-1] != 128 \
             or key.shape[-1] != 128 or query.shape[0] != key.shape[0]:
         raise ValueError("Expected query [tokens, Hq, 128] and key/value [tokens, H, 128]")
@@ -104,6 +116,8 @@ def prefill_attention(query, key, value, cu_seqlens, max_seqlen, scale, output=N
     if cu_seqlens.dtype != torch.int32 or cu_seqlens.ndim != 1 or cu_seqlens.numel() < 2:
         raise ValueError("cu_seqlens must be an int32 [sequences + 1] tensor")
     nat.require_gpu(query, key, value, cu_seqlens, what="prefill_attention")
+    if check_lengths and int((cu_seqlens[1:] - cu_seqlens[:-1]).max()) > int(max_seqlen):
+        raise ValueError("a sequence is longer than max_seqlen")
     if any(t.stride(-1) != 1 for t in (query, key, value)):
         raise ValueError("head dimension must be contiguous")
     if output is None:

@@ -94,17 +94,25 @@ def _encode_into(keys, values, layout, pool, page_ids):
         raise ValueError("Pages are encoded from BF16 or FP16 keys and values")
     keys = keys if _rows_ok(keys) else keys.contiguous()
     values = values if _rows_ok(values) else values.contiguous()
+    _launch(keys.data_ptr(), values.data_ptr(), keys.dtype, nat.strides4(keys), nat.strides4(values), None,
+            keys.shape[0], layout, pool, page_ids)
+
+
+def _launch(k_ptr, v_ptr, dtype, k_strides, v_strides, page_rows, n, layout, pool, page_ids):
+    """One page-encoder launch and its flag read (see _encode_into)."""
     ids = page_ids.contiguous()
-    stream = nat.stream_handle(keys.device)
-    flags = _FLAGS.get((keys.device, stream))
+    device = pool.device
+    stream = nat.stream_handle(device)
+    flags = _FLAGS.get((device, stream))
     if flags is None:
-        flags = _FLAGS[(keys.device, stream)] = _Flags(keys.device)
+        flags = _FLAGS[(device, stream)] = _Flags(device)
     mine, other = flags.words[flags.turn], flags.words[1 - flags.turn]
-    nat.check(nat.lib().iq_encode_pages(
-        keys.data_ptr(), values.data_ptr(), nat.dtype_code(keys.dtype), nat.strides4(keys), nat.strides4(values),
-        keys.shape[0], layout.heads, layout.block_size, pool.data_ptr(), pool.shape[0], ids.data_ptr(),
-        ids.element_size(), mine.data_ptr(), other.data_ptr(), stream))
-    if keys.shape[0] == 0:
+    nat.check(nat.lib().iq_encode_pages_at(
+        k_ptr, v_ptr, nat.dtype_code(dtype), k_strides, v_strides,
+        None if page_rows is None else page_rows.data_ptr(), n, layout.heads, layout.block_size,
+        pool.data_ptr(), pool.shape[0], ids.data_ptr(), ids.element_size(), mine.data_ptr(), other.data_ptr(),
+        stream))
+    if n == 0:
         return
     flags.turn = 1 - flags.turn
     bad_key, bad_value, bad_id, _ = mine.tolist()   # the one synchronization, as the codec's finite check
@@ -120,6 +128,38 @@ def _rows_ok(t) -> bool:
     """Rows the page encoder reads in place: unit channel stride, 16-byte aligned."""
     return (t.stride(-1) == 1 and all(st % 8 == 0 for st in t.stride()[:-1])
             and t.data_ptr() % 16 == 0)
+
+
+@torch.no_grad()
+def pack_pages_at(keys, values, page_rows, layout, destination, page_ids):
+    """Seal pages that start at arbitrary token rows, in one launch and one
+    flag read (the batched seal of several requests, backend.py:106-116 per
+    request in the reference).
+
+    keys / values: [H, tokens, 128] views (any head and token strides that
+    are multiples of 8 elements, unit channel stride, 16-byte aligned base)
+    over the rows of every page; page n holds tokens page_rows[n] ..
+    page_rows[n] + B - 1 (int64 device tensor, rows in range) and goes to
+    physical page page_ids[n]."""
+    if keys.shape != values.shape or keys.ndim != 3 or keys.shape[0] != layout.heads or keys.shape[2] != 128:
+        raise ValueError("Expected key/value rows [kv_heads, tokens, 128]")
+    if destination.dtype != torch.uint8 or destination.ndim != 2 or destination.shape[1] != layout.page_bytes \
+            or not destination.is_contiguous():
+        raise ValueError("Expected contiguous uint8 destination page pool")
+    if page_rows.dtype != torch.int64 or page_rows.ndim != 1 or page_ids.ndim != 1 \
+            or page_ids.numel() != page_rows.numel() or page_ids.dtype not in (torch.int32, torch.int64):
+        raise ValueError("One int64 start row and one integer physical page ID are required per page")
+    nat.require_gpu(keys, values, destination, page_rows, page_ids, what="pack_pages_at")
+    if keys.dtype not in (torch.bfloat16, torch.float16) or values.dtype != keys.dtype:
+        raise ValueError("Pages are encoded from BF16 or FP16 keys and values")
+    strides = []
+    for t in (keys, values):
+        st = (0, t.stride(0), t.stride(1), t.stride(2))
+        if st[3] != 1 or st[1] % 8 or st[2] % 8 or t.data_ptr() % 16:
+            raise ValueError("key/value rows must be contiguous and 16-byte aligned")
+        strides.append((nat._i64 * 4)(*st))
+    _launch(keys.data_ptr(), values.data_ptr(), keys.dtype, strides[0], strides[1], page_rows.contiguous(),
+            page_rows.numel(), layout, destination, page_ids)
 
 
 @torch.no_grad()
