@@ -421,50 +421,65 @@ def time_next_rows(device, sets=8):
     return out
 
 
-def time_paged(device, layers=4, n_seq=16, block=16, H=4, G=7, seed=4, steps=20):
+def time_paged(device, layers=4, n_seq=16, block=16, H=4, G=7, seed=4, steps=20, lifecycle_steps=24):
     """Config 4: batched paged decode, 16 sequences with contexts ~ U{2048..32768}
     in 16-token pages of the vLLM layout, random physical page order, per-sequence
-    BF16 sink (4) and partial-page tail.  `layers` independent pools (rotated, so
-    the working set exceeds the Infinity Cache) decoded back to back in a graph."""
+    BF16 sink (4) and open page.  Each of `layers` independent layers (rotated,
+    so the working set exceeds the Infinity Cache) is built by the plugin's
+    many-request lifecycle (InQuantBatchImpl: one prefill step of the 16
+    requests seals their full pages and keeps sink and open page in their
+    dense slots); the decode launches the lifecycle makes for the next token
+    are then replayed back to back in a graph.  `lifecycle_steps` whole decode
+    steps through InQuantBatchImpl.forward (new-token writes, the batched
+    decode, the seals of filled pages, host included) are timed eagerly."""
     import torch
+    import inquant_vllm.backend as backend
     from inquant.triton_attention import SharedDecodeWorkspace
-    from inquant_vllm import PageLayout, pack_pages_into, paged_decode_batch
+    from inquant_vllm import paged_decode_batch
     gen = torch.Generator(device="cpu").manual_seed(seed)
     ctx = torch.randint(2048, 32769, (n_seq,), generator=gen).tolist()
     pages = [c // block for c in ctx]
     tails = [c % block for c in ctx]
-    layout = PageLayout(block, H)
+    need_pages = [(c + lifecycle_steps) // block + 1 for c in ctx]
     max_pages = max(pages)
-    total_pages = sum(pages)
-    work = []
+    backend.configure(block_size=block, max_model_len=max(ctx) + lifecycle_steps + block)
+    work, impls = [], []
     g = torch.Generator(device=device).manual_seed(seed)
+    qsl = [0]
+    for c in ctx:
+        qsl.append(qsl[-1] + c)
     for _ in range(layers):
-        pool = torch.empty((total_pages, layout.page_bytes), dtype=torch.uint8, device=device)
-        perm = torch.randperm(total_pages, generator=g, device=device).to(torch.int32)
-        tables = torch.zeros((n_seq, max_pages), dtype=torch.int32, device=device)
-        dense = torch.zeros((n_seq, 2, H, block + 4, 128), dtype=torch.bfloat16, device=device)
+        impl = backend.InQuantBatchImpl(H * G, 128, 128 ** -0.5, H, max_num_seqs=n_seq)
+        pool = torch.empty((sum(need_pages), impl.layout.page_bytes), dtype=torch.uint8, device=device)
+        perm = torch.randperm(sum(need_pages), generator=g, device=device).to(torch.int32)
+        tables = torch.zeros((n_seq, max(need_pages)), dtype=torch.int32, device=device)
         first = 0
-        for i, n in enumerate(pages):
-            ids = perm[first:first + n]
+        for i, n in enumerate(need_pages):
+            tables[i, :n] = perm[first:first + n]
             first += n
-            tables[i, :n] = ids
-            k = kv_tensor(g, H, n * block + tails[i], device)[0]
-            v = kv_tensor(g, H, n * block + tails[i], device)[0]
-            kp = k[:, :n * block].reshape(H, n, block, 128).transpose(0, 1)
-            vp = v[:, :n * block].reshape(H, n, block, 128).transpose(0, 1)
-            pack_pages_into(kp, vp, layout, pool, ids)
-            dense[i, 0, :, :4], dense[i, 1, :, :4] = k[:, :4], v[:, :4]
-            if tails[i]:
-                dense[i, 0, :, 4:4 + tails[i]] = k[:, n * block:]
-                dense[i, 1, :, 4:4 + tails[i]] = v[:, n * block:]
-        info = torch.tensor([[n, t, 4] for n, t in zip(pages, tails)], dtype=torch.int32, device=device)
-        q = torch.randn((n_seq, H * G, 128), generator=g, device=device).to(torch.bfloat16)
-        work.append((q, pool, tables, info, dense, SharedDecodeWorkspace(), torch.empty_like(q)))
+        ks = [kv_tensor(g, H, c, device)[0].transpose(0, 1) for c in ctx]
+        vs = [kv_tensor(g, H, c, device)[0].transpose(0, 1) for c in ctx]
+        k, v = torch.cat(ks), torch.cat(vs)
+        del ks, vs
+        q = torch.randn((qsl[-1], H * G, 128), generator=g, device=device).to(torch.bfloat16)
+        meta = backend.InQuantBatchMetadata([f"seq{i}" for i in range(n_seq)],
+                                            torch.tensor(qsl, dtype=torch.int32, device=device), qsl, list(ctx),
+                                            tables, ())
+        impl.forward(None, q, k, v, pool, meta, torch.empty_like(q))      # prefill: pools built by the lifecycle
+        del q, k, v
+        slots = torch.tensor([impl.requests[f"seq{i}"].slot for i in range(n_seq)], dtype=torch.int32,
+                             device=device)
+        info = torch.tensor([[n, t + 1, 4] for n, t in zip(pages, tails)], dtype=torch.int32, device=device)
+        qd = torch.randn((n_seq, H * G, 128), generator=g, device=device).to(torch.bfloat16)
+        work.append((qd, pool, tables, info, impl.dense, slots, SharedDecodeWorkspace(), torch.empty_like(qd)))
+        impls.append((impl, pool, tables))
     torch.cuda.synchronize()
+    layout = impls[0][0].layout
 
     def step():
-        for q, pool, tables, info, dense, ws, out in work:
-            paged_decode_batch(q, pool, tables, info, dense, max_pages, layout, ws, 128 ** -0.5, out)
+        for q, pool, tables, info, dense, slots, ws, out in work:
+            paged_decode_batch(q, pool, tables, info, dense, max_pages, layout, ws, 128 ** -0.5, out,
+                               dense_slots=slots)
 
     graph = torch.cuda.CUDAGraph()
     st = torch.cuda.Stream()            # the workspaces are pinned to the stream they first run on
@@ -485,14 +500,34 @@ def time_paged(device, layers=4, n_seq=16, block=16, H=4, G=7, seed=4, steps=20)
     torch.cuda.synchronize()
     us = start.elapsed_time(stop) * 1e3 / steps / layers
     # algorithmic bytes per layer: every page of every sequence, its block-table
-    # entry, the live dense sink/tail rows, Q and O
-    bytes_layer = total_pages * (layout.page_bytes + 4) + sum(4 + t for t in tails) * 2 * H * 128 * 2 \
+    # entry, the live dense sink/open-page rows, Q and O
+    bytes_layer = sum(pages) * (layout.page_bytes + 4) + sum(4 + t + 1 for t in tails) * 2 * H * 128 * 2 \
         + 2 * n_seq * H * G * 128 * 2
+    # whole lifecycle decode steps of the first layer (host included, eager)
+    impl, pool, tables = impls[0]
+    qd = torch.randn((n_seq, H * G, 128), generator=g, device=device).to(torch.bfloat16)
+    kd = torch.randn((n_seq, H, 128), generator=g, device=device).to(torch.bfloat16)
+    out = torch.empty_like(qd)
+    qsl1 = list(range(n_seq + 1))
+    qsl1_dev = torch.tensor(qsl1, dtype=torch.int32, device=device)
+    lens = list(ctx)
+    seals0 = impl.seal_calls
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(lifecycle_steps):
+        lens = [n + 1 for n in lens]
+        meta = backend.InQuantBatchMetadata([f"seq{i}" for i in range(n_seq)], qsl1_dev, qsl1, lens, tables, ())
+        impl.forward(None, qd, kd, kd, pool, meta, out)
+    torch.cuda.synchronize()
+    life_us = (time.perf_counter() - t0) * 1e6 / lifecycle_steps
     return {"sequences": n_seq, "page_tokens": block, "mean_ctx": round(sum(ctx) / n_seq, 1),
             "us_per_layer": round(us, 3), "bytes_per_layer": bytes_layer,
             "gbs": round(bytes_layer / (us * 1e-6) / 1e9, 2),
             "hbm_frac": round(bytes_layer / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
-            "tokens_per_s": round(n_seq / (us * 1e-6), 1), "layers_rotated": layers}
+            "tokens_per_s": round(n_seq / (us * 1e-6), 1), "layers_rotated": layers,
+            "built_by": "InQuantBatchImpl prefill of the 16 requests",
+            "lifecycle_step_us": round(life_us, 1), "lifecycle_steps": lifecycle_steps,
+            "lifecycle_seal_launches": impl.seal_calls - seals0}
 
 
 def time_append(device, H=4, packed_tokens=32768, validate_positions=True):
