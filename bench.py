@@ -52,6 +52,10 @@ def parse():
     ap.add_argument("--no-append", action="store_true", help="skip the config 2 append measurements")
     ap.add_argument("--no-next", action="store_true",
                     help="skip the rows next to the decode path (materialize, encode into pages, prefill)")
+    ap.add_argument("--breakdown", action="store_true",
+                    help="only the config 2 decode time split: full decode, the partition merge alone "
+                         "(iq_decode_merge) and the launch floor of a one-element kernel, each replayed "
+                         "28 x rotated sets in a graph")
     ap.add_argument("--copy-probe", action="store_true",
                     help="only run a 1 GiB device-to-device copy (calibrates rocprofv3 FETCH_SIZE / WRITE_SIZE)")
     return ap.parse_args()
@@ -183,6 +187,70 @@ def time_decode(layers, steps, warmup, use_graph):
     torch.cuda.synchronize()
     ms = start.elapsed_time(stop) / steps
     return ms, outs
+
+
+def _graph_replay_us(device, launch, per_replay, steps=50):
+    """Microseconds per unit of `launch` (per_replay units per call),
+    captured once and replayed `steps` times."""
+    import torch
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(s):
+        launch()
+        torch.cuda.synchronize()
+        with torch.cuda.graph(graph, stream=s):
+            launch()
+    torch.cuda.synchronize()
+    for _ in range(3):
+        graph.replay()
+    torch.cuda.synchronize()
+    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(steps):
+        graph.replay()
+    stop.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(stop) * 1e3 / steps / per_replay
+
+
+def decode_breakdown(layers, device):
+    """Config 2 decode split into its launches, each timed as 28 x rotated
+    sets of graph nodes: the full decode (partitions kernel + merge kernel),
+    the merge kernel alone on the partials the decode left in each layer's
+    workspace (it must reproduce the decode's outputs exactly), and a
+    one-element fill kernel (the launch floor of one graph node)."""
+    import torch
+    from inquant import _native as nat
+    lib = nat.lib()
+    n = len(layers)
+    ms, outs = time_decode(layers, 50, 5, True)
+    full_us = ms * 1e3 / n
+    q = layers[0]["q"]
+    hq = q.shape[1]
+    parts = lib.iq_decode_partitions(len(layers[0]["kb"]), layers[0]["sink_k"].shape[2],
+                                     layers[0]["tail_k"].shape[2], 1)
+    merged = [torch.empty_like(o) for o in outs]
+
+    def merges():
+        st = nat.stream_handle(q.device)
+        for layer, out in zip(layers, merged):
+            ws = layer["state"]._workspace
+            nat.check(lib.iq_decode_merge(ws.data_ptr(), parts, hq, out.data_ptr(), nat.dtype_code(out.dtype), st))
+
+    merge_us = _graph_replay_us(device, merges, n)
+    assert all(torch.equal(a, b) for a, b in zip(merged, outs)), "the merge alone must reproduce the decode"
+    cells = [torch.zeros(1, device=device) for _ in range(n)]
+
+    def fills():
+        for c in cells:
+            c.fill_(1.0)
+
+    floor_us = _graph_replay_us(device, fills, n)
+    return {"decode_us_per_layer": round(full_us, 3), "merge_alone_us": round(merge_us, 3),
+            "launch_floor_us": round(floor_us, 3), "partitions_kernel_us": round(full_us - merge_us, 3),
+            "partitions": parts, "layers": n,
+            "note": "full = partitions kernel + merge kernel; each figure includes its graph node's launch"}
 
 
 def time_decode_k4_values(device, layers=28, steps=20, warmup=3):
@@ -746,6 +814,9 @@ def main():
     rotate = max(1, args.rotate)
     layers = [build_layer(1000 + i, device, n_blocks=args.blocks) for i in range(args.layers * rotate)]
     torch.cuda.synchronize()
+    if args.breakdown:
+        print(json.dumps({"breakdown": "cfg2 decode", **decode_breakdown(layers, device)}))
+        return
     per_layer = algorithmic_bytes(layers[0])
     step_bytes = sum(algorithmic_bytes(l) for l in layers) / rotate
     # one replay runs `rotate` steps, each over its own set of layers

@@ -212,6 +212,20 @@ int iq_decode_attention(const void *q, int q_dtype, int64_t q_stride_h, int64_t 
                         void *out, int out_dtype, void *stream);
 
 /*
+ * The partition merge alone: out [Hq, 128] of out_dtype from the `parts`
+ * partials in workspace (the layout iq_decode_attention writes: [Hq, parts]
+ * 128-float rows, then [Hq, parts] (max, sum) pairs, max in natural-log
+ * units).  Replaces _reduce_partials (triton_attention.py:168-181); the
+ * decode calls it itself, this entry point serves callers that produce
+ * partials elsewhere and the timing of the merge on its own.
+ */
+int iq_decode_merge(const float *workspace, int64_t parts, int64_t Hq, void *out, int out_dtype, void *stream);
+
+/* Partitions iq_decode_attention uses for a call: the matrix-core kernel's
+ * (fast != 0: blocks + ceil((sink + tail) / 32)) or the general kernel's. */
+int64_t iq_decode_partitions(int64_t n_blocks, int64_t sink_t, int64_t tail_t, int fast);
+
+/*
  * iq_decode_attention without a workspace argument, for callers that cannot
  * allocate device memory (code under HIP graph capture, tight serving loops,
  * harnesses that forbid hipMalloc).  No counterpart in the reference.  The

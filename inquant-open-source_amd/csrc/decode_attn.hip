@@ -380,6 +380,23 @@ extern "C" int iq_decode_attention(const void *q, int q_dtype, int64_t q_stride_
     return IQ_OK;
 }
 
+extern "C" int iq_decode_merge(const float *workspace, int64_t parts, int64_t Hq, void *out, int out_dtype,
+                               void *stream)
+{
+    IQ_CHECK_ARG(workspace && out, "iq_decode_merge: null pointer");
+    IQ_CHECK_ARG(parts >= 1 && parts <= 65535 && Hq >= 1, "iq_decode_merge: bad sizes");
+    IQ_CHECK_ARG(out_dtype >= IQ_F32 && out_dtype <= IQ_F16, "iq_decode_merge: bad output dtype");
+    hipLaunchKernelGGL(decode_reduce, dim3((unsigned)(64 * ((Hq + 7) / 8))), dim3(RED_THREADS), 0,
+                       (hipStream_t)stream, workspace, parts, (int)Hq, out, out_dtype);
+    IQ_CHECK_LAUNCH("decode_reduce");
+    return IQ_OK;
+}
+
+extern "C" int64_t iq_decode_partitions(int64_t n_blocks, int64_t sink_t, int64_t tail_t, int fast)
+{
+    return fast ? n_blocks + (sink_t + tail_t + DENSE_SPLIT - 1) / DENSE_SPLIT : partitions(n_blocks, sink_t, tail_t);
+}
+
 // ---------------------------------------------------------------- allocation-free variant
 //
 // Scratch of iq_decode_attention_noalloc: the partition partials live in this

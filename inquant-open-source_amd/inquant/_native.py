@@ -61,6 +61,8 @@ _SIGNATURES = {
                                  _i64, _i64, _int, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _int, _p, _p, _p]),
     "iq_decode_append": (_int, [_p, _p, _p, _i64, _i64, ctypes.POINTER(BlockPtrs), _i64, _i64, _int, _p]),
     "iq_decode_workspace_floats": (_i64, [_i64, _i64, _i64, _i64]),
+    "iq_decode_merge": (_int, [_p, _i64, _i64, _p, _int, _p]),
+    "iq_decode_partitions": (_i64, [_i64, _i64, _i64, _int]),
     "iq_decode_attention": (_int, [_p, _int, _i64, _i64, _p, _p, _p, ctypes.POINTER(BlockRun), _i64, _i64, _i64,
                                    _i64, _int, _int,
                                    _p, _p, _i64, _i64, _i64, _i64, _i64,

@@ -38,6 +38,9 @@ def test_invalid_arguments_return_errors_without_a_gpu():
     assert lib.iq_v_dequantize(None, None, None, 1, 128, 3, 64, None, 0, None) == -1
     # 128 blocks + one 32-token sink slice + four 32-token tail slices, 130 floats each
     assert lib.iq_decode_workspace_floats(28, 128, 4, 128) == 28 * 133 * 130
+    assert lib.iq_decode_partitions(128, 4, 128, 1) == 133 and lib.iq_decode_partitions(128, 4, 128, 0) == 133
+    assert lib.iq_decode_merge(None, 133, 28, None, 1, None) == -1 and b"null" in lib.iq_last_error()
+    assert lib.iq_decode_merge(1 << 20, 0, 28, 1 << 20, 1, None) == -1 and b"sizes" in lib.iq_last_error()
     # the allocation-free decode refuses, on the host and before touching a
     # device, inputs whose partials exceed its static scratch (4 Mi floats)
     assert lib.iq_decode_attention_noalloc(
