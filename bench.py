@@ -503,7 +503,7 @@ def time_paged(device, layers=4, n_seq=16, block=16, H=4, G=7, seed=4, steps=20,
     import torch
     import inquant_vllm.backend as backend
     from inquant.triton_attention import SharedDecodeWorkspace
-    from inquant_vllm import paged_decode_batch
+    from inquant_vllm import paged_decode_batch, work_list
     gen = torch.Generator(device="cpu").manual_seed(seed)
     ctx = torch.randint(2048, 32769, (n_seq,), generator=gen).tolist()
     pages = [c // block for c in ctx]
@@ -543,30 +543,36 @@ def time_paged(device, layers=4, n_seq=16, block=16, H=4, G=7, seed=4, steps=20,
         impls.append((impl, pool, tables))
     torch.cuda.synchronize()
     layout = impls[0][0].layout
+    items = torch.tensor(work_list(pages, block), dtype=torch.int32, device=device)
 
-    def step():
-        for q, pool, tables, info, dense, slots, ws, out in work:
-            paged_decode_batch(q, pool, tables, info, dense, max_pages, layout, ws, 128 ** -0.5, out,
-                               dense_slots=slots)
-
-    graph = torch.cuda.CUDAGraph()
-    st = torch.cuda.Stream()            # the workspaces are pinned to the stream they first run on
+    st = torch.cuda.Stream()                # the workspaces are pinned to the stream they first run on
     st.wait_stream(torch.cuda.current_stream())
-    with torch.cuda.stream(st):
-        step()
-        torch.cuda.synchronize()
-        with torch.cuda.graph(graph, stream=st):
+
+    def graphed_us(listed):
+        def step():
+            for q, pool, tables, info, dense, slots, ws, out in work:
+                paged_decode_batch(q, pool, tables, info, dense, max_pages, layout, ws, 128 ** -0.5, out,
+                                   dense_slots=slots, work=items if listed else None)
+
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.stream(st):
             step()
-    torch.cuda.synchronize()
-    graph.replay()
-    torch.cuda.synchronize()
-    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    start.record()
-    for _ in range(steps):
+            torch.cuda.synchronize()
+            with torch.cuda.graph(graph, stream=st):
+                step()
+        torch.cuda.synchronize()
         graph.replay()
-    stop.record()
-    torch.cuda.synchronize()
-    us = start.elapsed_time(stop) * 1e3 / steps / layers
+        torch.cuda.synchronize()
+        start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record()
+        for _ in range(steps):
+            graph.replay()
+        stop.record()
+        torch.cuda.synchronize()
+        return start.elapsed_time(stop) * 1e3 / steps / layers
+
+    us_grid = graphed_us(False)
+    us = graphed_us(True)
     # algorithmic bytes per layer: every page of every sequence, its block-table
     # entry, the live dense sink/open-page rows, Q and O
     bytes_layer = sum(pages) * (layout.page_bytes + 4) + sum(4 + t + 1 for t in tails) * 2 * H * 128 * 2 \
@@ -593,6 +599,7 @@ def time_paged(device, layers=4, n_seq=16, block=16, H=4, G=7, seed=4, steps=20,
             "gbs": round(bytes_layer / (us * 1e-6) / 1e9, 2),
             "hbm_frac": round(bytes_layer / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
             "tokens_per_s": round(n_seq / (us * 1e-6), 1), "layers_rotated": layers,
+            "work_items": int(items.numel()), "us_per_layer_full_grid": round(us_grid, 3),
             "built_by": "InQuantBatchImpl prefill of the 16 requests",
             "lifecycle_step_us": round(life_us, 1), "lifecycle_steps": lifecycle_steps,
             "lifecycle_seal_launches": impl.seal_calls - seals0}

@@ -332,6 +332,12 @@ int64_t iq_paged_workspace_floats(int64_t Hq, int64_t n_seq, int64_t max_pages, 
  *   packed tokens before the sink length and tail slots inside the sink are
  *   skipped); sequence i reads dense slot dense_slots[i] (i32 device array of
  *   in-range slots), or slot i when dense_slots is NULL;
+ *   work: NULL (one workgroup per (KV head, partition, sequence) up to the
+ *   longest sequence), or n_work i32 items (sequence << 16 | partition) that
+ *   list every partition of every sequence (packed partitions of 256 tokens,
+ *   then the dense one: seq_info's pages decide how many) in the order they
+ *   should start, so that no workgroup is launched for a partition past a
+ *   short sequence's end (items outside the batch do nothing);
  *   out [n_seq, Hq, 128] (stride out_stride_seq) of out_dtype.
  * Keys/values are decoded and rounded to bf16 as dequantize-then-attend does;
  * logits, softmax and P.V accumulate in fp32.  Replaces paged_decode
@@ -341,9 +347,9 @@ int iq_paged_decode(const void *q, int64_t q_stride_seq, int64_t q_stride_h, int
                     const uint8_t *pool, int64_t pool_pages, int64_t H, int64_t block_tokens,
                     const int32_t *block_tables, int64_t bt_stride, int64_t max_pages,
                     const int32_t *seq_info, int64_t n_pages, int64_t tail_t, int64_t sink_t,
-                    const void *dense, int64_t dense_stride_seq, const int32_t *dense_slots, float scale,
-                    float *workspace, int64_t workspace_floats, void *out, int64_t out_stride_seq,
-                    int out_dtype, void *stream);
+                    const void *dense, int64_t dense_stride_seq, const int32_t *dense_slots,
+                    const int32_t *work, int64_t n_work, float scale, float *workspace,
+                    int64_t workspace_floats, void *out, int64_t out_stride_seq, int out_dtype, void *stream);
 
 /*
  * Causal self-attention over exact K/V for prefill, vLLM token-major layout:

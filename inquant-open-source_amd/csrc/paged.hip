@@ -182,6 +182,11 @@ struct PagedArgs {
     const uint16_t *dense;             // [slots, 2, H, B + 4, 128] bf16
     int64_t dense_ss;
     const int32_t *dense_slots;        // dense slot of each sequence, or null (slot = sequence)
+    // optional compacted work list: grid row y is (sequence work[y] >> 16,
+    // partition work[y] & 0xffff), only live partitions; null: row y is
+    // partition y of sequence blockIdx.z
+    const int32_t *work;
+    int n_seq;
     int max_parts;
     float c_log2;                      // softmax scale * log2(e)
     float *ws;                         // seq * Hq * max_parts partials (Partials layout)
@@ -261,7 +266,7 @@ struct __attribute__((aligned(16))) PagedSmem {
 // known.
 template <int NPG, bool PACKED>
 __device__ __forceinline__ void paged_body(const PagedArgs &a, PagedSmem<NPG> &sm, const SeqGeom &geo, int wave,
-                                           const int (&pid)[pages_per_wave(NPG)])
+                                           const int (&pid)[pages_per_wave(NPG)], int p, int sq)
 {
     constexpr int B = PART / NPG;
     constexpr int VQW = 2;                       // dwords per 32-channel quarter of a V2 row
@@ -271,7 +276,7 @@ __device__ __forceinline__ void paged_body(const PagedArgs &a, PagedSmem<NPG> &s
     const int tid = threadIdx.x, lane = tid & 63;
     const int gl = lane & 15, ql = lane >> 4;
     const int pl = lane & 15, qq = lane >> 4;      // V writer: pair row pl, channels 32 qq .. 32 qq + 31
-    const int h = blockIdx.x, p = blockIdx.y, sq = blockIdx.z;
+    const int h = blockIdx.x;
     const int G = a.G;
     const float unit = fp8x2<false>(1u).x;       // fp8 byte 1 == 2^-9
     const float inv_unit = 1.0f / unit;
@@ -720,7 +725,7 @@ __device__ __forceinline__ void paged_body(const PagedArgs &a, PagedSmem<NPG> &s
             for (int e = 0; e < 4; ++e) num[e] = fmaf(o[e], wt, num[e]);
             den = fmaf(sm.wl[w][g], wt, den);
         }
-        const Partials pt = partials(a.ws, (int64_t)gridDim.z * a.H * G * a.max_parts);
+        const Partials pt = partials(a.ws, (int64_t)a.n_seq * a.H * G * a.max_parts);
         const int64_t row = ((int64_t)sq * a.H * G + h * G + g) * a.max_parts + p;
         *(f32x4 *)(pt.o + row * D + c) = num;
         if (c == 0) pt.ml[row] = f32x2{mx == NEG_INF ? NEG_INF : mx * LN2, den};
@@ -734,7 +739,13 @@ __global__ __launch_bounds__(256, 4) void decode_paged(PagedArgs a)
 {
     constexpr int PPW = pages_per_wave(NPG);
     __shared__ PagedSmem<NPG> sm;
-    const int p = blockIdx.y, sq = blockIdx.z;
+    int p = blockIdx.y, sq = blockIdx.z;
+    if (a.work) {
+        const int item = a.work[blockIdx.y];
+        sq = item >> 16;
+        p = item & 0xffff;
+        if (sq >= a.n_seq || p >= a.max_parts) return;     // an item outside the batch does nothing
+    }
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     // this wavefront's block-table entries (scalar loads), requested before
     // the lengths arrive; the last partition of a table clamps its indices
@@ -750,8 +761,8 @@ __global__ __launch_bounds__(256, 4) void decode_paged(PagedArgs a)
     }
     const SeqGeom geo = seq_geom(a, sq);
     if (p >= geo.npp + geo.ndp) return;
-    if (p < geo.npp) paged_body<NPG, true>(a, sm, geo, wave, pid);
-    else paged_body<NPG, false>(a, sm, geo, wave, pid);
+    if (p < geo.npp) paged_body<NPG, true>(a, sm, geo, wave, pid, p, sq);
+    else paged_body<NPG, false>(a, sm, geo, wave, pid, p, sq);
 }
 
 // grid (64 * ceil(Hq / 8), 1, seq) of single-wave workgroups: merges the
@@ -774,7 +785,7 @@ __global__ __launch_bounds__(64) void paged_reduce(PagedArgs a, void *out, int64
     const int c0 = slice * 16 + 4 * c4;
     const SeqGeom geo = seq_geom(a, sq);
     const int P = geo.npp + geo.ndp;
-    const Partials pt = partials(a.ws, (int64_t)gridDim.z * a.H * a.G * a.max_parts);
+    const Partials pt = partials(a.ws, (int64_t)a.n_seq * a.H * a.G * a.max_parts);
     const int64_t row0 = ((int64_t)sq * a.H * a.G + hq) * a.max_parts;
     float m = NEG_INF, den = 0.0f;
     f32x4 num = {0.0f, 0.0f, 0.0f, 0.0f};
@@ -891,8 +902,9 @@ extern "C" int iq_paged_decode(const void *q, int64_t q_stride_seq, int64_t q_st
                                const int32_t *block_tables, int64_t bt_stride, int64_t max_pages,
                                const int32_t *seq_info, int64_t n_pages, int64_t tail_t, int64_t sink_t,
                                const void *dense, int64_t dense_stride_seq, const int32_t *dense_slots,
-                               float scale, float *workspace, int64_t workspace_floats, void *out,
-                               int64_t out_stride_seq, int out_dtype, void *stream)
+                               const int32_t *work, int64_t n_work, float scale, float *workspace,
+                               int64_t workspace_floats, void *out, int64_t out_stride_seq, int out_dtype,
+                               void *stream)
 {
     IQ_CHECK_ARG(q && pool && dense && workspace && out, "iq_paged_decode: null pointer");
     IQ_CHECK_ARG(H >= 1 && Hq >= H && Hq % H == 0 && Hq / H <= 16, "iq_paged_decode: expected 1..16 query heads per KV head");
@@ -932,10 +944,14 @@ extern "C" int iq_paged_decode(const void *q, int64_t q_stride_seq, int64_t q_st
     a.dense = (const uint16_t *)dense;
     a.dense_ss = dense_stride_seq;
     a.dense_slots = dense_slots;
+    a.n_seq = (int)n_seq;
+    IQ_CHECK_ARG(!work || (n_work >= 1 && n_work <= 65535 && n_seq <= 32767),
+                 "iq_paged_decode: the work list holds 1 to 65535 items of at most 32767 sequences");
+    a.work = work;
     a.max_parts = (int)parts;
     a.c_log2 = scale * 1.4426950408889634f;
     a.ws = workspace;
-    const dim3 grid((unsigned)H, (unsigned)parts, (unsigned)n_seq);
+    const dim3 grid((unsigned)H, (unsigned)(a.work ? n_work : parts), (unsigned)(a.work ? 1 : n_seq));
     hipStream_t st = (hipStream_t)stream;
     switch (block_tokens) {
     case 16: hipLaunchKernelGGL(decode_paged<16>, grid, dim3(256), 0, st, a); break;

@@ -84,7 +84,7 @@ _SIGNATURES = {
     "iq_unpack_pages": (_int, [_p, _i64, _i64, _i64, _p, _p, _int, _p]),
     "iq_paged_workspace_floats": (_i64, [_i64, _i64, _i64, _i64]),
     "iq_paged_decode": (_int, [_p, _i64, _i64, _i64, _i64, _p, _i64, _i64, _i64, _p, _i64, _i64,
-                               _p, _i64, _i64, _i64, _p, _i64, _p, _f32, _p, _i64, _p, _i64, _int, _p]),
+                               _p, _i64, _i64, _i64, _p, _i64, _p, _p, _i64, _f32, _p, _i64, _p, _i64, _int, _p]),
     "iq_tail_append": (_int, [_p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _int, _p, _i64, _i64, _i64,
                               _i64, _i64, _i64, _i64, _p, _int, _i64, _p, _p]),
     "iq_tail_append_row": (_int, [ctypes.POINTER(TailDesc), _p, _p, _i64, _i64, _i64, _p, _i64, _p]),

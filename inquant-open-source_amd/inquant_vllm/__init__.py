@@ -11,7 +11,7 @@ paged decode, seal after attention).  The vLLM platform and worker glue
 """
 from .layout import PageLayout, pack_pages, pack_pages_into, unpack_pages_reference
 from .packing import write_codec_pages
-from .kernels import paged_decode, paged_decode_batch, prefill_attention
+from .kernels import paged_decode, paged_decode_batch, prefill_attention, work_list
 
 __all__ = ["PageLayout", "pack_pages", "pack_pages_into", "unpack_pages_reference", "write_codec_pages",
-           "paged_decode", "paged_decode_batch", "prefill_attention"]
+           "paged_decode", "paged_decode_batch", "prefill_attention", "work_list"]

@@ -33,7 +33,7 @@ import torch
 
 from inquant import _native as nat
 from inquant.triton_attention import SharedDecodeWorkspace
-from .kernels import paged_decode, paged_decode_batch, prefill_attention
+from .kernels import paged_decode, paged_decode_batch, prefill_attention, work_list
 from .layout import PageLayout, _launch, pack_pages_into
 
 # Layers run in stream order and share one workspace (it checks stream identity).
@@ -464,8 +464,11 @@ class InQuantBatchImpl(InQuantImpl):
                 [r.sealed_pages for r in reqs], [r.tokens % b + 1 for r in reqs],
                 [min(SINK, r.tokens + 1) for r in reqs]]
         sink_rows = [j for j, r in enumerate(reqs) if r.tokens < SINK]
-        dplan = self._to_device(plan, torch.int32, dev)
         nd = len(rows)
+        # the partitions the decode needs (no workgroup past a short sequence's end)
+        items = work_list([r.sealed_pages for r in reqs], b)
+        flat = self._to_device([x for row in plan for x in row] + items, torch.int32, dev)
+        dplan, work = flat[:6 * nd].view(6, nd), flat[6 * nd:]
         idx = dplan[:3].long()
         if leading:
             new_kv = torch.stack((key[:nd], value[:nd]), 1)
@@ -485,7 +488,7 @@ class InQuantBatchImpl(InQuantImpl):
         q = query[:nd] if leading else query.index_select(0, idx[0])
         out = output[:nd] if leading else torch.empty_like(q, dtype=output.dtype)
         paged_decode_batch(q, kv_cache, tables[:, :max(1, max_pages)].contiguous(), seq_info, self.dense, max_pages,
-                           self.layout, WORKSPACE, self.scale, out, dense_slots=dplan[1].contiguous())
+                           self.layout, WORKSPACE, self.scale, out, dense_slots=dplan[1].contiguous(), work=work)
         if not leading:
             output.index_copy_(0, idx[0], out)
         # pages the decode tokens filled, sealed after attention from their slots

@@ -49,18 +49,34 @@ def paged_decode(query, cache, blocks, dense, num_pages, tail_tokens,
     nat.check(nat.lib().iq_paged_decode(
         query.data_ptr(), 0, 128, hq, 1, cache.data_ptr(), cache.shape[0], hkv, b,
         table.data_ptr() if table.numel() else None, 0, int(num_pages), None, int(num_pages), int(tail_tokens),
-        int(sink_tokens), dense.data_ptr(), 0, None, float(scale), scratch.data_ptr(), need,
+        int(sink_tokens), dense.data_ptr(), 0, None, None, 0, float(scale), scratch.data_ptr(), need,
         output.data_ptr(), 0, nat.dtype_code(output.dtype), nat.stream_handle(query.device)))
     return output
 
 
+def work_list(pages, block_size):
+    """The compacted work list of a batch whose page counts the host knows:
+    every (sequence, partition) the decode needs, as int32 sequence << 16 |
+    partition: a sequence's packed partitions (256 tokens of pages each),
+    then its dense ones (sink and open page); the sequences with the most
+    partitions first, each sequence's partitions consecutive (as the grid
+    without a list orders them)."""
+    per_part = 256 // block_size
+    dense = -(-(block_size + 4) // 256)
+    parts = [(-(-int(n) // per_part)) + dense for n in pages]
+    order = sorted(range(len(parts)), key=lambda i: -parts[i])
+    return [(i << 16) | p for i in order for p in range(parts[i])]
+
+
 def paged_decode_batch(query, cache, block_tables, seq_info, dense, max_pages, layout, workspace, scale,
-                       output=None, dense_slots=None):
+                       output=None, dense_slots=None, work=None):
     """query bf16 [n, Hq, 128]; block_tables int32 [n, >= max_pages]; seq_info int32
     [n, 3] device tensor of (pages, tail tokens, sink tokens); dense bf16
     [n, 2, kv_heads, block_size + 4, 128], or [slots, 2, kv_heads, block_size + 4,
     128] with dense_slots an int32 [n] device tensor naming each sequence's
-    slot (the caller keeps them in range).  Returns [n, Hq, 128]."""
+    slot (the caller keeps them in range).  ``work``: optional int32 device
+    tensor from ``work_list`` (the partitions that exist, so no workgroup
+    starts past a short sequence's end).  Returns [n, Hq, 128]."""
     hkv, b = layout.heads, layout.block_size
     hq = _check_query(query, hkv)
     _check_pool(cache, layout)
@@ -70,6 +86,9 @@ def paged_decode_batch(query, cache, block_tables, seq_info, dense, max_pages, l
         raise ValueError("Expected dense BF16 [sequences, 2, kv_heads, block_size + 4, 128]")
     if dense_slots is not None and (tuple(dense_slots.shape) != (n,) or dense_slots.dtype != torch.int32):
         raise ValueError("Expected int32 dense slots [sequences]")
+    if work is not None and (work.ndim != 1 or work.dtype != torch.int32 or not work.is_contiguous()
+                             or work.numel() < n):
+        raise ValueError("Expected a contiguous int32 work list with every partition of every sequence")
     if block_tables.ndim != 2 or block_tables.shape[0] != n or block_tables.shape[1] < max_pages \
             or block_tables.dtype != torch.int32:
         raise ValueError("Expected int32 block tables [sequences, >= max_pages]")
@@ -86,6 +105,7 @@ def paged_decode_batch(query, cache, block_tables, seq_info, dense, max_pages, l
         query.data_ptr(), hq * 128, 128, hq, n, cache.data_ptr(), cache.shape[0], hkv, b,
         block_tables.data_ptr(), block_tables.shape[1], int(max_pages), seq_info.data_ptr(), 0, 0, 0,
         dense.data_ptr(), dense[0].numel(), None if dense_slots is None else dense_slots.contiguous().data_ptr(),
+        None if work is None else work.data_ptr(), 0 if work is None else work.numel(),
         float(scale), scratch.data_ptr(), need,
         output.data_ptr(), hq * 128, nat.dtype_code(output.dtype), nat.stream_handle(query.device)))
     return output

@@ -290,6 +290,17 @@ def test_paged_decode_batch_sixteen_sequences_against_oracle():
                                   H, B, 128 ** -0.5)
         err = float(np.abs(got[i] - exp).max())
         assert err <= ATOL, (i, int(ctx[i]), err)
+    # the compacted work list (only the partitions that exist, longest
+    # sequences first) runs the same partitions: bit-identical outputs; a
+    # list in another order, and items outside the batch, change nothing
+    from inquant_vllm import work_list
+    items = work_list(pages.tolist(), B)
+    assert len(items) == sum(-(-int(n) // 16) + 1 for n in pages)
+    for order in (items, items[::-1] + [(S << 16) | 0, (0 << 16) | 0xfff0]):
+        listed = torch.full_like(out, float("nan"))
+        paged_decode_batch(q, pool, tables, infos, dense, max_pages, layout, SharedDecodeWorkspace(), 128 ** -0.5,
+                           listed, work=torch.tensor(order, dtype=torch.int32, device="cuda"))
+        assert torch.equal(listed, out)
 
 
 @pytest.mark.parametrize("block", [16, 32, 64, 256])

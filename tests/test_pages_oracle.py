@@ -101,3 +101,17 @@ def test_paged_host_validation_without_gpu():
         paged_decode(q, pool, ids, dense, 1, 1, 1, layout, SharedDecodeWorkspace(), 0.1)
     with pytest.raises(ValueError, match="contiguous uint8 destination"):
         write_codec_pages(None, None, layout, pool[:, :-1], ids)
+
+
+def test_work_list_names_every_partition_once_longest_first():
+    # the paged decode's compacted work list: packed partitions of 256 tokens
+    # of pages, then the dense partition(s) (sink and open page), per sequence
+    from inquant_vllm import work_list
+    items = work_list([0, 17, 33, 2], 16)
+    seqs = [i >> 16 for i in items]
+    parts = {}
+    for i in items:
+        parts.setdefault(i >> 16, []).append(i & 0xffff)
+    assert parts == {0: [0], 1: [0, 1, 2], 2: [0, 1, 2, 3], 3: [0, 1]}
+    assert seqs == sorted(seqs, key=lambda s: -len(parts[s]))          # longest first, consecutive
+    assert work_list([3], 256) == [0, 1, 2, 3, 4]                       # 260-token dense buffer: two
