@@ -605,11 +605,12 @@ def time_paged(device, layers=4, n_seq=16, block=16, H=4, G=7, seed=4, steps=20,
             "lifecycle_seal_launches": impl.seal_calls - seals0}
 
 
-def time_append(device, H=4, packed_tokens=32768, validate_positions=True):
+def time_append(device, H=4, packed_tokens=32768, validate_positions=True, seals=7):
     """Config 2 append, through the cache API of one Qwen2.5-7B layer (32K packed
-    context): 128 single-token appends (dense tail 128 -> 256, no seal), then the
-    append that seals one 256-token block (K4 + V2 encode) starting from a
-    383-token tail, then the decode-state metadata append for that block."""
+    context): 128 single-token appends (dense tail 128 -> 256, no seal), then
+    `seals` times the append that seals one 256-token block (K4 + V2 encode)
+    starting from a 383-token tail and the decode-state metadata append for
+    that block (medians reported)."""
     import torch
     from inquant.cache import CacheConfig, InQuantCache
     from inquant.codec import CodecConfig
@@ -619,14 +620,15 @@ def time_append(device, H=4, packed_tokens=32768, validate_positions=True):
                       validate_positions=validate_positions)
     cache = InQuantCache(cfg)
     n0 = 4 + packed_tokens + 128
-    k = kv_tensor(g, H, n0 + 768, device)
-    v = kv_tensor(g, H, n0 + 768, device)
+    extra = 768 + 256 * seals
+    k = kv_tensor(g, H, n0 + extra, device)
+    v = kv_tensor(g, H, n0 + extra, device)
     cache.update(k[:, :, :n0], v[:, :, :n0], 0)
     layer = cache._layers[0]
     # one position tensor per decode step, shared by the layers in a model
     # (Transformers builds cache_position once per step): device slices, no
     # host-to-device copy inside the timed loop
-    positions = torch.arange(n0 + 768, device=device)
+    positions = torch.arange(n0 + extra, device=device)
     state = PackedDecodeState(list(layer.key_blocks), list(layer.value_blocks))
     pos = n0
     # one full cycle first (tail 128 -> 384 -> seal -> 128), so that the timed
@@ -647,27 +649,36 @@ def time_append(device, H=4, packed_tokens=32768, validate_positions=True):
     ev[1].record()
     torch.cuda.synchronize()
     host_us = (time.perf_counter() - t0) * 1e6 / 128
-    for _ in range(383 - 256):           # tail 256 -> 383 (no seal)
+    seal_us, meta_us = [], []
+    for _ in range(seals):
+        while layer.tail.count < 383:    # tail up to 383 (no seal)
+            cache.append_for_attention(k[:, :, pos:pos + 1], v[:, :, pos:pos + 1], 0,
+                                       {"cache_position": positions[pos:pos + 1]})
+            pos += 1
+        # wall clock from the call to its work done on the device (the seal
+        # synchronizes once itself: its non-finite check)
+        torch.cuda.synchronize()
+        blocks_before = len(layer.key_blocks)
+        t0 = time.perf_counter()
         cache.append_for_attention(k[:, :, pos:pos + 1], v[:, :, pos:pos + 1], 0,
                                    {"cache_position": positions[pos:pos + 1]})
+        torch.cuda.synchronize()
+        t1 = time.perf_counter()
         pos += 1
-    torch.cuda.synchronize()
-    blocks_before = len(layer.key_blocks)
-    ev[2].record()
-    cache.append_for_attention(k[:, :, pos:pos + 1], v[:, :, pos:pos + 1], 0,
-                               {"cache_position": positions[pos:pos + 1]})
-    ev[3].record()
-    assert len(layer.key_blocks) == blocks_before + 1
-    ev[4].record()
-    state.extend(list(layer.key_blocks), list(layer.value_blocks))
-    ev[5].record()
-    torch.cuda.synchronize()
+        assert len(layer.key_blocks) == blocks_before + 1
+        kb, vb = list(layer.key_blocks), list(layer.value_blocks)
+        t2 = time.perf_counter()
+        state.extend(kb, vb)
+        torch.cuda.synchronize()
+        t3 = time.perf_counter()
+        seal_us.append((t1 - t0) * 1e6)
+        meta_us.append((t3 - t2) * 1e6)
     seal_bytes = 2 * H * 256 * 128 * 2 + (16384 + 512 + 32 + 64 + 8192 + 2048) * H + 64 + H * 128
     return {"append_us_per_token": round(ev[0].elapsed_time(ev[1]) * 1e3 / 128, 2),
             "append_host_us_per_token": round(host_us, 2),
-            "seal_us": round(ev[2].elapsed_time(ev[3]) * 1e3, 2),
-            "metadata_append_us": round(ev[4].elapsed_time(ev[5]) * 1e3, 2),
-            "seal_bytes": seal_bytes}
+            "seal_us": round(sorted(seal_us)[len(seal_us) // 2], 2),
+            "metadata_append_us": round(sorted(meta_us)[len(meta_us) // 2], 2),
+            "seals_timed": seals, "seal_bytes": seal_bytes}
 
 
 def time_append_step(device, H=4, packed_tokens=32768, layers=28):

@@ -217,6 +217,31 @@ def _quantize_temporal_blocks(tensor: torch.Tensor, block_count: int, block_size
     return _per_block(packed, block_count, (1, heads, block_size, dim), PackedTensor)
 
 
+def _carve(device, fields):
+    """The seal's output tensors as views of one allocation, each starting on
+    a 16-byte boundary for the encoders' vector stores ((shape, dtype) pairs
+    in order).  The byte accounting counts each view's own bytes, as for
+    separate allocations; the allocation holds at most 15 alignment bytes
+    per field beyond them (none for 128-channel, 16-descriptor blocks)."""
+    offsets, total = [], 0
+    for shape, dtype in fields:
+        offsets.append(total)
+        total += -(-math.prod(shape) * dtype.itemsize // 16) * 16
+    raw = torch.empty(total, dtype=torch.uint8, device=device)
+    typed = {}                           # one reinterpretation per dtype, then strided views into it
+    out = []
+    for off, (shape, dtype) in zip(offsets, fields):
+        base = typed.get(dtype)
+        if base is None:
+            base = typed[dtype] = raw.view(dtype)
+        strides, acc = [], 1
+        for n in reversed(shape):
+            strides.append(acc)
+            acc *= n
+        out.append(torch.as_strided(base, shape, strides[::-1], off // dtype.itemsize))
+    return out
+
+
 def _kv_blocks(keys: torch.Tensor, values: torch.Tensor, block_count: int, block_size: int, config: CodecConfig,
                bits: int, group_size: int, key_flag: torch.Tensor, value_flag: torch.Tensor):
     """K4 keys and group-wise values of the first ``block_count`` blocks of
@@ -227,38 +252,34 @@ def _kv_blocks(keys: torch.Tensor, values: torch.Tensor, block_count: int, block
     if block_count == 0:
         return [], []
     _, heads, _, dim = keys.shape
-
-    def blocked(t):
-        return t[0, :, :block_count * block_size].unflatten(1, (block_count, block_size)).transpose(0, 1)
-
-    kb, vb = blocked(keys), blocked(values)
     native = (keys.dtype == values.dtype and keys.dtype in (torch.float32, torch.bfloat16, torch.float16)
               and keys.shape == values.shape and dim % 2 == 0 and dim <= 1024 and dim % group_size == 0)
     if not native:      # the separate encoders, with their own argument errors
         return (_quantize_temporal_blocks(keys, block_count, block_size, config, key_flag),
                 _value_blocks(values, block_count, block_size, bits, group_size, value_flag))
     device = nat.require_gpu(keys, what="quantize")
-    B, H, T, D = kb.shape
+    # the [blocks, H, B, D] view of the first blocks, as pointer and strides
+    # (no view objects: the encoder reads them directly)
+    B, H, T, D = block_count, heads, block_size, dim
+    ks, vs = keys.stride(), values.stride()
+    k_strides = (nat._i64 * 4)(T * ks[2], ks[1], ks[2], ks[3])
+    v_strides = (nat._i64 * 4)(T * vs[2], vs[1], vs[2], vs[3])
     count = math.floor(D * config.salient_fraction)
     desc_dtype = torch.uint8 if D <= 256 else torch.int32
-    payload = torch.empty((B, H, T, D // 2), dtype=torch.uint8, device=device)
-    scales = torch.empty((B, H, D), dtype=torch.float32, device=device)
-    src = torch.empty((B, H, count), dtype=desc_dtype, device=device)
-    don = torch.empty((B, H, count), dtype=desc_dtype, device=device)
-    padding = torch.empty((B, H, count), dtype=torch.float32, device=device)
-    v_payload = torch.empty((B, H, T, D * bits // 8), dtype=torch.uint8, device=device)
-    v_scales = torch.empty((B, H, T, D // group_size), dtype=torch.float16, device=device)
-    v_offsets = torch.empty_like(v_scales)
+    payload, scales, src, don, padding, v_payload, v_scales, v_offsets = _carve(device, (
+        ((B, H, T, D // 2), torch.uint8), ((B, H, D), torch.float32), ((B, H, count), desc_dtype),
+        ((B, H, count), desc_dtype), ((B, H, count), torch.float32), ((B, H, T, D * bits // 8), torch.uint8),
+        ((B, H, T, D // group_size), torch.float16), ((B, H, T, D // group_size), torch.float16)))
     nat.check(nat.lib().iq_kv_quantize(
-        kb.data_ptr(), vb.data_ptr(), nat.dtype_code(kb.dtype), nat.strides4(kb), nat.strides4(vb), B, H, T, D,
+        keys.data_ptr(), values.data_ptr(), nat.dtype_code(keys.dtype), k_strides, v_strides, B, H, T, D,
         count, config.sample_stride, int(config.donor_policy == "min_error"), payload.data_ptr(),
         scales.data_ptr(), src.data_ptr() if count else None, don.data_ptr() if count else None,
         src.element_size(), padding.data_ptr() if count else None, bits, group_size, v_payload.data_ptr(),
         v_scales.data_ptr(), v_offsets.data_ptr(), key_flag.data_ptr(), value_flag.data_ptr(),
         nat.stream_handle(device)))
     shape = (1, heads, block_size, dim)
-    packed_k = PackedTensor(payload, scales, src, don, padding, tuple(kb.shape), keys.dtype)
-    packed_v = PackedValues(v_payload, v_scales, v_offsets, tuple(vb.shape), values.dtype, bits, group_size)
+    packed_k = PackedTensor(payload, scales, src, don, padding, (B, H, T, D), keys.dtype)
+    packed_v = PackedValues(v_payload, v_scales, v_offsets, (B, H, T, D), values.dtype, bits, group_size)
     return (_per_block(packed_k, block_count, shape, PackedTensor),
             _per_block(packed_v, block_count, shape, PackedValues, bits=bits, group_size=group_size))
 
@@ -278,31 +299,25 @@ def _k4_pair_blocks(keys: torch.Tensor, values: torch.Tensor, block_count: int, 
         return (_quantize_temporal_blocks(keys, block_count, block_size, config, key_flag),
                 _quantize_temporal_blocks(values, block_count, block_size, config, value_flag))
     device = nat.require_gpu(keys, what="quantize")
-
-    def blocked(t):
-        return t[0, :, :block_count * block_size].unflatten(1, (block_count, block_size)).transpose(0, 1)
-
-    kb, vb = blocked(keys), blocked(values)
-    B, H, T, D = kb.shape
+    B, H, T, D = block_count, heads, block_size, dim
+    ks, vs = keys.stride(), values.stride()
+    k_strides = (nat._i64 * 4)(T * ks[2], ks[1], ks[2], ks[3])
+    v_strides = (nat._i64 * 4)(T * vs[2], vs[1], vs[2], vs[3])
     count = math.floor(D * config.salient_fraction)
     desc_dtype = torch.uint8 if D <= 256 else torch.int32
 
-    def outputs():
-        return (torch.empty((B, H, T, D // 2), dtype=torch.uint8, device=device),
-                torch.empty((B, H, D), dtype=torch.float32, device=device),
-                torch.empty((B, H, count), dtype=desc_dtype, device=device),
-                torch.empty((B, H, count), dtype=desc_dtype, device=device),
-                torch.empty((B, H, count), dtype=torch.float32, device=device))
-
-    ko, vo = outputs(), outputs()
+    fields = (((B, H, T, D // 2), torch.uint8), ((B, H, D), torch.float32), ((B, H, count), desc_dtype),
+              ((B, H, count), desc_dtype), ((B, H, count), torch.float32))
+    carved = _carve(device, fields + fields)
+    ko, vo = carved[:5], carved[5:]
     ptrs = lambda o: [o[0].data_ptr(), o[1].data_ptr()] + [t.data_ptr() if count else None for t in o[2:]]
     nat.check(nat.lib().iq_k4_quantize_kv(
-        kb.data_ptr(), vb.data_ptr(), nat.dtype_code(kb.dtype), nat.strides4(kb), nat.strides4(vb), B, H, T, D,
+        keys.data_ptr(), values.data_ptr(), nat.dtype_code(keys.dtype), k_strides, v_strides, B, H, T, D,
         count, config.sample_stride, int(config.donor_policy == "min_error"), *ptrs(ko), *ptrs(vo),
         ko[2].element_size(), key_flag.data_ptr(), value_flag.data_ptr(), nat.stream_handle(device)))
     shape = (1, heads, block_size, dim)
-    return (_per_block(PackedTensor(*ko, tuple(kb.shape), keys.dtype), block_count, shape, PackedTensor),
-            _per_block(PackedTensor(*vo, tuple(vb.shape), values.dtype), block_count, shape, PackedTensor))
+    return (_per_block(PackedTensor(*ko, (B, H, T, D), keys.dtype), block_count, shape, PackedTensor),
+            _per_block(PackedTensor(*vo, (B, H, T, D), values.dtype), block_count, shape, PackedTensor))
 
 
 class InQuantCache(_HFCache):
@@ -530,8 +545,9 @@ class InQuantCache(_HFCache):
         synchronization (the reference syncs once per encoder, codec.py:197 and
         value_codec.py:64); a pending position mismatch is reported first."""
         cfg = self.config
+        # the encoders only ever raise these words; they are zero here (every
+        # error path below clears what it raised)
         flags = self._flag_words(keys.device)
-        flags[:_POSITION_BAD].zero_()
         if cfg.value_bits is None:
             new_keys, new_values = _k4_pair_blocks(keys, values, count, cfg.block_size, cfg.codec,
                                                    flags[_KEY_BAD:_KEY_BAD + 1], flags[_VALUE_BAD:_VALUE_BAD + 1])
@@ -542,8 +558,9 @@ class InQuantCache(_HFCache):
                                               flags[_VALUE_BAD:_VALUE_BAD + 1])
             value_error = _BAD_V
         bad_key, bad_value, bad_position = flags.tolist()
+        if bad_key or bad_value or bad_position:
+            flags.zero_()
         if bad_position:
-            flags[_POSITION_BAD].zero_()
             self._position_checked = None
             raise ValueError(_POSITION_ERROR)
         if bad_key:

@@ -61,6 +61,8 @@ def _view_nbytes(t: torch.Tensor) -> int:
 
 def _per_block(packed, count: int, shape, cls, **extra) -> list:
     """Per-block objects whose fields are views of a batched [count, H, ...] encode."""
+    if count == 1:
+        return [cls(**packed.tensors, shape=shape, original_dtype=packed.original_dtype, **extra)]
     names = list(packed.tensors)
     pieces = [t.split(1) for t in packed.tensors.values()]
     return [cls(**dict(zip(names, parts)), shape=shape, original_dtype=packed.original_dtype, **extra)

@@ -28,6 +28,7 @@ here), no mask.
 from __future__ import annotations
 
 import math
+import operator
 
 import torch
 
@@ -53,13 +54,14 @@ class _StreamPin:
         self.message = message
 
     def check(self, device) -> int:
-        stream = torch.cuda.current_stream(device)
-        key = (stream.device, stream.cuda_stream)
+        index = device.index if device.index is not None else torch.cuda.current_device()
+        handle = torch._C._cuda_getCurrentRawStream(index)
+        key = (index, handle)
         if self.key is None:
             self.key = key
         elif key != self.key:
             raise RuntimeError(self.message)
-        return stream.cuda_stream
+        return handle
 
 
 class SharedDecodeWorkspace:
@@ -119,9 +121,10 @@ class _BlockFormat:
                     raise ValueError("All V blocks must share the same quantizer")
             elif not isinstance(v, PackedTensor) or v.salient_channels.shape[-1] != self.salient:
                 raise ValueError("All InQuant V blocks must share the salient-channel count")
+        index = self.device.index
         for block in (*keys, *values):
             for t in block.tensors.values():
-                if t.device != self.device:
+                if t.get_device() != index:
                     raise ValueError("All packed tensors must share the same CUDA device")
         if self.salient > 64:
             raise ValueError("Packed decode supports at most 64 salient channels (int8 roles)")
@@ -262,9 +265,8 @@ class PackedDecodeState:
         if len(key_blocks) != len(value_blocks):
             raise ValueError("Key and value block counts must match")
         have = len(self.key_blocks)
-        prefix_ok = len(key_blocks) >= have and all(
-            a is b for old, new in ((self.key_blocks, key_blocks), (self.value_blocks, value_blocks))
-            for a, b in zip(old, new))
+        prefix_ok = len(key_blocks) >= have and all(map(operator.is_, self.key_blocks, key_blocks)) \
+            and all(map(operator.is_, self.value_blocks, value_blocks))
         if not prefix_ok:
             raise ValueError("PackedDecodeState.extend requires an immutable append-only prefix")
         if len(key_blocks) == have:

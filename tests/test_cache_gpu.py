@@ -147,11 +147,12 @@ def test_batched_prefill_matches_serial_blocks_and_owns_compact_storage(dtype):
                     st = tensor.untyped_storage()
                     storages.setdefault(st.data_ptr(), [st.nbytes(), 0])[1] += tensor.numel() * tensor.element_size()
             torch.testing.assert_close(actual.dequantize(), serial.dequantize(), rtol=0, atol=0)
-    # per-block fields are disjoint views that tile their batched allocations
-    # exactly: the counted bytes are every stored byte, once
+    # per-block fields are disjoint views of their seal's one allocation: the
+    # counted bytes are every stored byte, once, apart from the alignment
+    # (each field starts on a 16-byte boundary: at most 15 bytes per field)
     ranges.sort()
     assert all(a[1] <= b[0] for a, b in zip(ranges, ranges[1:]))
-    assert all(held == counted for held, counted in storages.values())
+    assert all(0 <= held - counted <= 15 * 10 for held, counted in storages.values())
     assert cache.nbytes == expected_bytes + cache.sink_nbytes + cache.residual_nbytes
 
 
