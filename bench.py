@@ -730,6 +730,77 @@ def time_append_step(device, H=4, packed_tokens=32768, layers=28):
             "cycle_mean_step_us": round(sum(times) / steps * 1e6, 1)}
 
 
+def time_step_graph(device, H=4, HQ=28, packed_tokens=32768, layers=28, reps=50):
+    """Config 2 decode step of a 28-layer model captured as one HIP graph:
+    per layer, the one-token append (append_for_attention, one
+    iq_tail_append_row launch) and the packed decode of the view it returns
+    (sink + 128 blocks + tail, two launches).  The replays rewrite the same
+    tail row and decode the same length, so they time the device work of one
+    step without the host's per-call cost; the same step run eagerly is
+    timed beside it.  The captured appends take no cache_position: the
+    position check reads a device flag back on the host, which a graph
+    cannot do."""
+    import torch
+    from inquant.cache import CacheConfig, InQuantCache
+    from inquant.codec import CodecConfig
+    from inquant.triton_attention import PackedDecodeState
+    g = torch.Generator(device=device).manual_seed(13)
+    cfg = CacheConfig(codec=CodecConfig(donor_policy="min_error"), value_bits=2, value_group_size=64)
+    cache = InQuantCache(cfg)
+    n0 = 4 + packed_tokens + 128
+    k = kv_tensor(g, H, n0 + 64, device)
+    v = kv_tensor(g, H, n0 + 64, device)
+    for i in range(layers):
+        cache.update(k[:, :, :n0], v[:, :, :n0], i)
+    states = [PackedDecodeState(list(cache._layers[i].key_blocks), list(cache._layers[i].value_blocks))
+              for i in range(layers)]
+    q = torch.randn((1, HQ, 1, 128), generator=g, device=device).to(torch.bfloat16)
+    outs = [torch.empty_like(q) for _ in range(layers)]
+
+    def step(pos):
+        kk, vv = k[:, :, pos:pos + 1], v[:, :, pos:pos + 1]
+        for i in range(layers):
+            view = cache.append_for_attention(kk, vv, i)
+            states[i].decode(q, sink_key=view.sink_key, sink_value=view.sink_value, residual_key=view.residual_key,
+                             residual_value=view.residual_value, output=outs[i])
+
+    pos = n0
+    for _ in range(8):                   # warm: kernels loaded, views and workspaces built
+        step(pos)
+        pos += 1
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(16):
+        step(pos)
+        pos += 1
+    torch.cuda.synchronize()
+    eager_us = (time.perf_counter() - t0) * 1e6 / 16
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(s):
+        step(pos)
+        pos += 1
+        torch.cuda.synchronize()
+        with torch.cuda.graph(graph, stream=s):
+            step(pos)
+    torch.cuda.synchronize()
+    for _ in range(3):
+        graph.replay()
+    torch.cuda.synchronize()
+    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(reps):
+        graph.replay()
+    stop.record()
+    torch.cuda.synchronize()
+    us = start.elapsed_time(stop) * 1e3 / reps
+    assert cache._layers[0].tail.count < cfg.residual_length + cfg.block_size     # no seal inside the graph
+    return {"layers": layers, "graph_step_us": round(us, 1), "graph_us_per_layer": round(us / layers, 2),
+            "eager_step_us": round(eager_us, 1), "eager_us_per_layer": round(eager_us / layers, 2),
+            "launches_per_layer": 3}
+
+
 def _cpu_model() -> str:
     try:
         for line in open("/proc/cpuinfo"):
@@ -853,6 +924,7 @@ def main():
         append["append_us_per_token_unvalidated"] = time_append(device, validate_positions=False)[
             "append_us_per_token"]
         append["step"] = time_append_step(device)
+        append["step_graph"] = time_step_graph(device)
     cfg3 = None if args.no_cfg3 else time_decode_cfg3(device)
     k4v = None if args.no_k4_values else time_decode_k4_values(device)
     result = {
