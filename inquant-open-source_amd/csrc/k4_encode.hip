@@ -212,7 +212,8 @@ __global__ __launch_bounds__(K4_THREADS) void k4_encode_kernel(K4Args a)
 // one is consumed), twice:
 //   pass 1  waves 0-1: the fp64 Welford var_mean of channel tid (min_error
 //           only); delta / n uses a table of RN(1/n) and one remainder fma,
-//           which is the correctly rounded quotient for n <= 256;
+//           which is the correctly rounded quotient for n <= 256 (sealed
+//           blocks: one fma with compile-time constants, see step_c);
 //           waves 2-3: sampled sums (torch cascade order), amax and
 //           finiteness as an integer max of the 16-bit magnitudes;
 //   then    donor selection by the whole workgroup (iq_select_tile128);
@@ -487,7 +488,7 @@ __device__ __forceinline__ void k4_tile_body(const K4Args &a, int64_t b, int64_t
     };
 
     start_stream();
-    if (tid < T) s_rcp[tid] = 1.0 / (double)(tid + 1);
+    if (NCH == 0 && tid < T) s_rcp[tid] = 1.0 / (double)(tid + 1);
     if (tid == 0) s_bad = 0;
     if constexpr (!DMA) store_chunk(seg[0], 0);
     __syncthreads();
@@ -516,17 +517,48 @@ __device__ __forceinline__ void k4_tile_body(const K4Args &a, int64_t b, int64_t
                     const double dv = (double)xf;
                     const double delta = __dsub_rn(dv, mean);
                     const double q0 = __dmul_rn(delta, y);
-                    double n = (double)(t + 1);
-                    // a sealed block's counts are compile-time constants: held in
-                    // scalar registers they feed a three-address fma; as a literal
-                    // operand they force the two-address form and a copy of delta
-                    if constexpr (NCH > 0) asm("" : "+s"(n));
-                    const double r = __builtin_fma(-q0, n, delta);
+                    const double r = __builtin_fma(-q0, (double)(t + 1), delta);
                     mean = __dadd_rn(mean, __builtin_fma(r, y, q0));
                     const double nd = __dsub_rn(dv, mean);
                     m2 = __dadd_rn(m2, __dmul_rn(delta, nd));
                 };
-                if (nt == CH) {
+                // A sealed block's counts n = t + 1 are compile-time constants, and
+                // so are y_hi = RN(1/n) and y_lo = RN((1 - y_hi n) / n) (the residual
+                // 1 - y_hi n is exact).  delta / n is then one fma:
+                // RN(delta y_hi + RN(delta y_lo)).  A quotient by an integer n <= 256
+                // is never a midpoint between doubles and lies at least ulp / 512
+                // from one (its odd part would need 54 bits), while
+                // delta y_hi + RN(delta y_lo) is within 2^-105 |delta / n|, i.e.
+                // 2^-52 ulp, of it: the fma returns the correctly rounded quotient,
+                // with one dependent operation fewer than the remainder correction.
+                auto step_c = [&](float xf, int t) {
+                    const double n = (double)(t + 1);
+                    double yh = 1.0 / n;
+                    double yl = __builtin_fma(-yh, n, 1.0) / n;
+                    asm("" : "+s"(yh), "+s"(yl));      // scalar operands of the mul and the fma
+                    const double dv = (double)xf;
+                    const double delta = __dsub_rn(dv, mean);
+                    mean = __dadd_rn(mean, __builtin_fma(delta, yh, __dmul_rn(delta, yl)));
+                    const double nd = __dsub_rn(dv, mean);
+                    m2 = __dadd_rn(m2, __dmul_rn(delta, nd));
+                };
+                if constexpr (NCH > 0) {
+                    // LDS reads of the next eight tokens in flight while the
+                    // current eight dependent steps run
+                    float cur[8], nxt[8];
+#pragma unroll
+                    for (int u = 0; u < 8; ++u) cur[u] = tile_f32<F16IN>(xs[u * ROWLEN]);
+#pragma unroll
+                    for (int g = 0; g < CH; g += 8) {
+                        const int gn = g + 8 < CH ? g + 8 : g;
+#pragma unroll
+                        for (int u = 0; u < 8; ++u) nxt[u] = tile_f32<F16IN>(xs[(gn + u) * ROWLEN]);
+#pragma unroll
+                        for (int u = 0; u < 8; ++u) step_c(cur[u], t0 + g + u);
+#pragma unroll
+                        for (int u = 0; u < 8; ++u) cur[u] = nxt[u];
+                    }
+                } else if (nt == CH) {
                     // LDS reads of the next eight tokens in flight while the
                     // current eight dependent steps run
                     float cur[8], nxt[8];
