@@ -860,16 +860,18 @@ __global__ __launch_bounds__(K4_THREADS) void k4_encode_page_rows(K4Args a, int6
 #pragma unroll
     for (int t = 0; t < T; ++t) {
         const uint32_t w = *(const uint32_t *)(xs + t * ROW + 2 * lane);
-        const double y = 1.0 / (double)(t + 1), n = (double)(t + 1);
+        // delta / n as in the tile encoder's step_c: one fma with the
+        // compile-time pair RN(1/n), RN((1 - RN(1/n) n) / n)
+        const double n = (double)(t + 1);
+        const double yh = 1.0 / n;
+        const double yl = __builtin_fma(-yh, n, 1.0) / n;
 #pragma unroll
         for (int e = 0; e < 2; ++e) {
             const uint32_t u = e ? w >> 16 : w & 0xffffu;
             amax_bits[e] = max(amax_bits[e], u & 0x7fffu);
             const double dv = (double)tile_f32<F16IN>(u);
             const double delta = __dsub_rn(dv, mean[e]);
-            const double q0 = __dmul_rn(delta, y);
-            const double r = __builtin_fma(-q0, n, delta);
-            mean[e] = __dadd_rn(mean[e], __builtin_fma(r, y, q0));
+            mean[e] = __dadd_rn(mean[e], __builtin_fma(delta, yh, __dmul_rn(delta, yl)));
             m2[e] = __dadd_rn(m2[e], __dmul_rn(delta, __dsub_rn(dv, mean[e])));
         }
     }
