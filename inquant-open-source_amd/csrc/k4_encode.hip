@@ -617,10 +617,13 @@ __device__ __forceinline__ void k4_tile_body(const K4Args &a, int64_t b, int64_t
         // stash the sampled mean until the Welford waves are done with s_smean
         s_scale[c1] = sm.finish() / (float)ns;
     }
-    // the first chunks of pass 2 load during the selection (once every wave
-    // is done with pass 1's buffers)
+    // A sealed block's last NBUF chunks are still in the buffers after pass 1
+    // and pass 2 quantizes them first (RESIDENT), reloading the others into
+    // the buffers they free; otherwise the first chunks of pass 2 load during
+    // the selection (once every wave is done with pass 1's buffers).
+    constexpr bool RESIDENT = DMA && NCH == 2 * NBUF;
     __syncthreads();
-    start_stream();
+    if constexpr (!RESIDENT) start_stream();
 
     // ---- values (VBITS > 0), encoded by three wavefronts while the fourth
     // makes the sequential donor picks, with the row's HBM reads in that otherwise
@@ -753,7 +756,22 @@ __device__ __forceinline__ void k4_tile_body(const K4Args &a, int64_t b, int64_t
     }
     uint32_t *out = PAGES ? (uint32_t *)(page + a.off_kpay + h * (int64_t)T * (TILE_D / 2))
                           : (uint32_t *)(a.payload + row * (int64_t)T * (TILE_D / 2));
-    stream([&](int ch) {
+    // chunks NCH - NBUF .. NCH - 1 from the buffers pass 1 left them in, then
+    // chunk c < NCH - NBUF, loaded into buffer c % NBUF once every wave is
+    // done with the resident chunk c + NBUF there (issued NBUF - 1 chunks
+    // ahead of its use; waits as in stream(): vector memory operations retire
+    // in order, and the stores issued in between only lengthen them)
+    auto stream2 = [&](auto &&body) {
+#pragma unroll
+        for (int k = 0; k < NCH; ++k) {
+            const int ch = k < NBUF ? NCH - NBUF + k : k - NBUF;
+            if (k >= NBUF) wait_chunk_barrier(min(NBUF - 2, NCH - 1 - k));
+            else if (k > 0) asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+            if (k > 0 && k <= NBUF) dma_chunk(k - 1);
+            body(ch);
+        }
+    };
+    auto pass2 = [&](int ch) {
         const int t0 = ch * CH;
 #pragma unroll
         for (int it = 0; it < 2; ++it) {
@@ -766,7 +784,9 @@ __device__ __forceinline__ void k4_tile_body(const K4Args &a, int64_t b, int64_t
                 out[t * (TILE_D / 8) + j] = slots.word(v);
             }
         }
-    });
+    };
+    if constexpr (RESIDENT) stream2(pass2);
+    else stream(pass2);
 }
 
 // grid (blocks, heads): no 64-bit division for the row's coordinates
