@@ -9,29 +9,37 @@
 // [tokens, heads, 128] with runtime (token, head) strides; sequences are
 // delimited by cu_seqlens.
 //
-// One workgroup = 128 queries of one query head (8 wavefronts of 16: the
-// staging of each key tile is shared by twice the queries of a four-wavefront
-// group, 2.16 -> 1.13 ms for an 8K causal Qwen2.5-7B prefill together with
-// the conflict-free V transpose, edge-only masks and register double
-// buffering; two 16-query subtiles per wavefront, sharing the K and V
-// operands, measured slower at 188 VGPRs: 1.33 ms with eight wavefronts,
-// 1.55 ms with four); key tiles of 64 stream through LDS (K row-major, V
-// transposed into key pairs).  Keys
-// are the rows of S^T = K Q^T (v_mfma_f32_16x16x32, queries as columns), so
-// the softmax weights land in exactly the lanes and k-slots of the B operand
-// of O^T = V^T P^T and no transpose of P is needed.  Query tiles are
-// dispatched longest-first (the causal work grows with the tile index).
+// One workgroup = 128 queries of one query head: four wavefronts of 32
+// queries, one per SIMD, so the two wavefronts that share a SIMD belong to
+// different workgroups and overlap each other's matrix products with their
+// softmax.  Keys are the rows of S^T = K Q^T on v_mfma_f32_32x32x16 (queries
+// as columns): lane (query l % 32, half l / 32) holds 16 keys of its query per
+// 32-key block, so the row maximum is an in-lane maximum and one permlane32
+// swap, and the softmax weights land in the lanes and k-slots of the B
+// operand of O^T = V^T P^T (k-slot 8 h + i of a 16-key chunk c is key
+// 16 c + 4 h + i % 4 + 8 (i / 4)), so P needs no transpose.  Per 32 queries a
+// key byte read from LDS feeds twice the products of 16-query wavefronts on
+// 16x16x32 (0.92 -> 0.75 ms for the 8K causal Qwen2.5-7B prefill; earlier
+// forms: 2.16 ms with four wavefronts of 16, 1.13 ms with eight and register
+// double buffering, two 16-query subtiles per wavefront 1.33 ms).  Key tiles
+// of 64 stream global -> registers -> LDS with two LDS stages (K row-major,
+// V transposed into key pairs, both conflict-free), one barrier per tile;
+// masks only on the diagonal and last tiles; query tiles longest-first.
+// ~222 VGPRs: two wavefronts per SIMD.
 #include "decode_common.h"
 
 namespace {
 
 constexpr int D = 128;
-constexpr int NW = 8;               // wavefronts per workgroup
+constexpr int NW = 4;               // wavefronts per workgroup
 constexpr int NT = 64 * NW;         // threads per workgroup
-constexpr int QT = 16 * NW;         // queries per workgroup, 16 per wavefront
+constexpr int QW = 32;              // queries per wavefront
+constexpr int QT = QW * NW;         // queries per workgroup
 constexpr int KT = 64;              // keys per tile
-constexpr int KROW = D + 8;         // halves per staged key row
-constexpr int VROW = KT / 2 + 2;    // key-pair dwords per staged V^T row (34: the 16 rows of an operand read on distinct bank pairs)
+constexpr int KROW = D + 8;         // halves per staged key row (68 dwords: a 16-lane b128 read covers 64 banks)
+constexpr int VROW = KT / 2 + 2;    // key-pair dwords per staged V^T row (34: 32 rows of an operand read on distinct bank pairs)
+
+typedef __attribute__((ext_vector_type(16))) float f32x16;
 
 struct PrefillArgs {
     const uint16_t *q, *k, *v;
@@ -41,6 +49,7 @@ struct PrefillArgs {
     int G;
     float c_log2;                                             // softmax scale * log2(e)
     int odt;
+    int vec_out;                                              // output rows aligned for 4-channel stores
 };
 
 // two stages: one is computed while the next tile is staged into the other
@@ -50,31 +59,59 @@ struct __attribute__((aligned(16))) PrefillSmem {
 };
 static_assert(2 * sizeof(PrefillSmem) <= 160 * 1024, "two workgroups per compute unit");
 
+// 32x32x16 product: lane l holds A[l % 32][8 (l / 32) .. + 7], B[8 (l / 32) .. + 7][l % 32]
+// and C[8 (i / 4) + 4 (l / 32) + i % 4][l % 32] in register i
 template <bool F16>
-__global__ __launch_bounds__(NT) void prefill_attn(PrefillArgs a)
+__device__ __forceinline__ f32x16 mma3232(u32x4 a, u32x4 b, f32x16 c)
+{
+    if constexpr (F16)
+        return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c,
+                                                      0, 0, 0);
+    else
+        return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b),
+                                                       c, 0, 0, 0);
+}
+
+// reductions over the lane pair l, l ^ 32 (one query's two halves)
+__device__ __forceinline__ float pair_max(float v)
+{
+    const auto h = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return fmaxf(__uint_as_float(h[0]), __uint_as_float(h[1]));
+}
+
+__device__ __forceinline__ float pair_sum(float v)
+{
+    const auto h = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(h[0]) + __uint_as_float(h[1]);
+}
+
+template <bool F16>
+__global__ __launch_bounds__(NT, 2) void prefill_attn(PrefillArgs a)
 {
     __shared__ PrefillSmem sm;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int col = lane & 15, g = lane >> 4;
+    const int c32 = lane & 31, h32 = lane >> 5;
     const int hq = blockIdx.y, seq = blockIdx.z, h = hq / a.G;
     const int start = a.cu[seq], len = a.cu[seq + 1] - start;
     const int q0 = (int)(gridDim.x - 1 - blockIdx.x) * QT;
     if (q0 >= len) return;                       // uniform: no barrier is skipped by part of the group
-    const int qw = q0 + 16 * wave;               // this wavefront's first query
-    const int my_q = qw + col;                   // the query of this lane's column
-    u32x4 qb[4];                                 // B operand: Q[my_q][32 ks + 8 g .. + 7]
+    const int qw = q0 + QW * wave;               // this wavefront's first query
+    const int my_q = qw + c32;                   // the query of this lane's column
+    u32x4 qb[8];                                 // B operand: Q[my_q][16 d + 8 h32 .. + 7]
     {
         const int qq = my_q < len ? my_q : len - 1;
-        const uint16_t *qp = a.q + (int64_t)(start + qq) * a.q_st + (int64_t)hq * a.q_sh + 8 * g;
+        const uint16_t *qp = a.q + (int64_t)(start + qq) * a.q_st + (int64_t)hq * a.q_sh + 8 * h32;
 #pragma unroll
-        for (int ks = 0; ks < 4; ++ks) qb[ks] = ld16(qp + 32 * ks);
+        for (int d = 0; d < 8; ++d) qb[d] = ld16(qp + 16 * d);
     }
     const uint16_t *kbase = a.k + (int64_t)start * a.k_st + (int64_t)h * a.k_sh;
     const uint16_t *vbase = a.v + (int64_t)start * a.v_st + (int64_t)h * a.v_sh;
     float m_run = NEG_INF, l_run = 0.0f;         // l_run: this lane's share of the column sum
-    f32x4 acc[8];
+    f32x16 acc[4];                               // O^T rows 32 db .. 32 db + 31 (output channels)
 #pragma unroll
-    for (int rb = 0; rb < 8; ++rb) acc[rb] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int db = 0; db < 4; ++db)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) acc[db][i] = 0.0f;
     const int kend = q0 + QT < len ? q0 + QT : len;
     // Key tiles stream global -> registers -> LDS with two LDS stages: tile
     // k0 + 64 is staged while tile k0 is computed, and tile k0 + 128 is read
@@ -158,55 +195,62 @@ __global__ __launch_bounds__(NT) void prefill_attn(PrefillArgs a)
             stage(s ^ 1);
             if (k0 + 2 * KT < kend) load_tile(k0 + 2 * KT);
         }
-        if (k0 <= qw + 15) {                     // some key of this tile is visible to this wavefront (uniform)
+        if (k0 <= qw + QW - 1) {                 // some key of this tile is visible to this wavefront (uniform)
             const uint16_t *sk = sm.k[s];
             const uint32_t *svt = sm.vt[s];
-            // S^T (keys x queries) for four 16-key subtiles; lane holds keys 16 j + 4 g + r of column my_q;
-            // consecutive products go to different subtiles, so none waits for
-            // the one before it
-            f32x4 sc[4];
+            // S^T blocks kb: lane holds keys k0 + 32 kb + 8 (i / 4) + 4 h32 + i % 4 of column my_q;
+            // the two blocks' products alternate, so neither waits for its own previous one
+            f32x16 sc[2];
 #pragma unroll
-            for (int j = 0; j < 4; ++j) sc[j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+            for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-            for (int ks = 0; ks < 4; ++ks)
+                for (int i = 0; i < 16; ++i) sc[kb][i] = 0.0f;
 #pragma unroll
-                for (int j = 0; j < 4; ++j)
-                    sc[j] = mma32<F16>(*(const u32x4 *)(sk + (16 * j + col) * KROW + 32 * ks + 8 * g), qb[ks], sc[j]);
+            for (int d = 0; d < 8; ++d)
+#pragma unroll
+                for (int kb = 0; kb < 2; ++kb)
+                    sc[kb] = mma3232<F16>(*(const u32x4 *)(sk + (32 * kb + c32) * KROW + 16 * d + 8 * h32), qb[d],
+                                          sc[kb]);
             // raw logits: the scale is positive, so the maximum commutes with it
             // and p = 2^(s c - m) takes one fma per logit.  Only a tile that
             // reaches past this wavefront's first query or the sequence's end
             // has keys to mask (wave-uniform).
             if (k0 + KT - 1 > qw || k0 + KT > len) {
 #pragma unroll
-                for (int j = 0; j < 4; ++j)
+                for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-                    for (int r = 0; r < 4; ++r) {
-                        const int key = k0 + 16 * j + 4 * g + r;
-                        if (!(key <= my_q && key < len)) sc[j][r] = NEG_INF;
+                    for (int i = 0; i < 16; ++i) {
+                        const int key = k0 + 32 * kb + 8 * (i >> 2) + 4 * h32 + (i & 3);
+                        if (!(key <= my_q && key < len)) sc[kb][i] = NEG_INF;
                     }
             }
             float cmax = NEG_INF;
 #pragma unroll
-            for (int j = 0; j < 4; ++j)
+            for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-                for (int r = 0; r < 4; ++r) cmax = fmaxf(cmax, sc[j][r]);
-            cmax = xmax16(cmax) * a.c_log2;
-            const float m_new = fmaxf(m_run, cmax);  // finite: key 0 is visible to every query
+                for (int i = 0; i < 16; ++i) cmax = fmaxf(cmax, sc[kb][i]);
+            cmax = pair_max(cmax) * a.c_log2;
+            // The reference maximum moves only when the tile's exceeds it by
+            // more than 2^8 (or on the first tile): the weights 2^(s c - m) then
+            // stay below 256, exact in range for the 16-bit P operand and the
+            // fp32 sums, and the output rescale is skipped on most tiles.
+            const float m_new = cmax > m_run + 8.0f ? cmax : m_run;   // finite: key 0 is visible to every query
             const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
             float lsum = 0.0f;
-            u32x4 pb[2];                             // B operand of O^T: slots 0-3 subtile 2ks, 4-7 subtile 2ks+1
+            u32x4 pb[2][2];                          // B operand of the 16-key chunk (kb, c): registers 8 c .. 8 c + 7
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                float pr[4];
+            for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    pr[r] = __builtin_amdgcn_exp2f(fmaf(sc[j][r], a.c_log2, -m_new));
-                    lsum += pr[r];
-                }
-                pb[j >> 1][2 * (j & 1)] = pack2<F16>(pr[0], pr[1]);
-                pb[j >> 1][2 * (j & 1) + 1] = pack2<F16>(pr[2], pr[3]);
-            }
-            // the four lanes of a column share m, so their partial sums take
+                for (int c = 0; c < 2; ++c)
+#pragma unroll
+                    for (int w = 0; w < 4; ++w) {
+                        const float p0 = __builtin_amdgcn_exp2f(fmaf(sc[kb][8 * c + 2 * w], a.c_log2, -m_new));
+                        const float p1 = __builtin_amdgcn_exp2f(fmaf(sc[kb][8 * c + 2 * w + 1], a.c_log2, -m_new));
+                        lsum += p0;
+                        lsum += p1;
+                        pb[kb][c][w] = pack2<F16>(p0, p1);
+                    }
+            // the two lanes of a column share m, so their partial sums take
             // the same rescale and are added once, after the last tile
             l_run = fmaf(l_run, alpha, lsum);
             m_run = m_new;
@@ -214,27 +258,55 @@ __global__ __launch_bounds__(NT) void prefill_attn(PrefillArgs a)
             // holds in every lane the rescale is the identity and is skipped
             if (__builtin_amdgcn_ballot_w64(alpha != 1.0f)) {
 #pragma unroll
-                for (int rb = 0; rb < 8; ++rb) acc[rb] *= alpha;
+                for (int db = 0; db < 4; ++db) acc[db] *= alpha;
             }
+            // A operand of chunk (kb, c): V^T row 32 db + c32, keys 32 kb + 16 c + 4 h32 + 0..3 and + 8..11
 #pragma unroll
-            for (int ks = 0; ks < 2; ++ks)
+            for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-                for (int rb = 0; rb < 8; ++rb) {
-                    const uint32_t *vr = svt + (16 * rb + col) * VROW + 2 * g + 16 * ks;
-                    const u32x2 lo = *(const u32x2 *)vr, hi = *(const u32x2 *)(vr + 8);
-                    acc[rb] = mma32<F16>(u32x4{lo[0], lo[1], hi[0], hi[1]}, pb[ks], acc[rb]);
-                }
+                for (int c = 0; c < 2; ++c)
+#pragma unroll
+                    for (int db = 0; db < 4; ++db) {
+                        const uint32_t *vr = svt + (32 * db + c32) * VROW + 16 * kb + 8 * c + 2 * h32;
+                        const u32x2 lo = *(const u32x2 *)vr, hi = *(const u32x2 *)(vr + 4);
+                        acc[db] = mma3232<F16>(u32x4{lo[0], lo[1], hi[0], hi[1]}, pb[kb][c], acc[db]);
+                    }
         }
         __syncthreads();                         // stage s ^ 1 is written; stage s is free
     }
-    l_run = xsum16(l_run);
+    l_run = pair_sum(l_run);
     if (my_q < len) {
         const float inv = 1.0f / l_run;
-        const int64_t o = (int64_t)(start + my_q) * a.o_st + (int64_t)hq * a.o_sh + 4 * g;
+        const int64_t o = (int64_t)(start + my_q) * a.o_st + (int64_t)hq * a.o_sh + 4 * h32;
+        // four consecutive channels per register group: one 16- or 8-byte store
+        // when the rows are aligned for it (vec_out), else element by element
+        if (a.vec_out && a.odt == IQ_F32) {
 #pragma unroll
-        for (int rb = 0; rb < 8; ++rb)
+            for (int db = 0; db < 4; ++db)
 #pragma unroll
-            for (int r = 0; r < 4; ++r) iq_store_as(a.out, o + 16 * rb + r, acc[rb][r] * inv, a.odt);
+                for (int g = 0; g < 4; ++g)
+                    *(f32x4 *)((float *)a.out + o + 32 * db + 8 * g) =
+                        f32x4{acc[db][4 * g] * inv, acc[db][4 * g + 1] * inv, acc[db][4 * g + 2] * inv,
+                              acc[db][4 * g + 3] * inv};
+        } else if (a.vec_out && a.odt != IQ_F32) {
+#pragma unroll
+            for (int db = 0; db < 4; ++db)
+#pragma unroll
+                for (int g = 0; g < 4; ++g) {
+                    const bool f16 = a.odt == IQ_F16;
+                    const float v0 = acc[db][4 * g] * inv, v1 = acc[db][4 * g + 1] * inv;
+                    const float v2 = acc[db][4 * g + 2] * inv, v3 = acc[db][4 * g + 3] * inv;
+                    *(u32x2 *)((uint16_t *)a.out + o + 32 * db + 8 * g) =
+                        f16 ? u32x2{pack2<true>(v0, v1), pack2<true>(v2, v3)}
+                            : u32x2{pack2<false>(v0, v1), pack2<false>(v2, v3)};
+                }
+        } else {
+#pragma unroll
+            for (int db = 0; db < 4; ++db)
+#pragma unroll
+                for (int i = 0; i < 16; ++i)
+                    iq_store_as(a.out, o + 32 * db + 8 * (i >> 2) + (i & 3), acc[db][i] * inv, a.odt);
+        }
     }
 }
 
@@ -261,8 +333,12 @@ extern "C" int iq_prefill_attention(const void *q, const void *k, const void *v,
     const uintptr_t bases = (uintptr_t)q | (uintptr_t)k | (uintptr_t)v;
     IQ_CHECK_ARG(bases % 16 == 0 && (q_st | q_sh | k_st | k_sh | v_st | v_sh) % 8 == 0,
                  "iq_prefill_attention: q/k/v rows must be 16-byte aligned");
+    // 4-channel output stores need every row start aligned to 4 elements' bytes
+    const int64_t obytes = out_dtype == IQ_F32 ? 4 : 2;
+    const int vec_out = (uintptr_t)out % (4 * obytes) == 0 && o_st % 4 == 0 && o_sh % 4 == 0;
     PrefillArgs a{(const uint16_t *)q, (const uint16_t *)k, (const uint16_t *)v, out, q_st, q_sh, k_st, k_sh,
-                  v_st, v_sh, o_st, o_sh, cu_seqlens, (int)(Hq / H), scale * 1.44269504088896341f, out_dtype};
+                  v_st, v_sh, o_st, o_sh, cu_seqlens, (int)(Hq / H), scale * 1.44269504088896341f, out_dtype,
+                  vec_out};
     const dim3 grid((unsigned)((max_seqlen + QT - 1) / QT), (unsigned)Hq, (unsigned)n_seq), block(NT);
     if (dtype == IQ_F16) hipLaunchKernelGGL(prefill_attn<true>, grid, block, 0, (hipStream_t)stream, a);
     else hipLaunchKernelGGL(prefill_attn<false>, grid, block, 0, (hipStream_t)stream, a);
