@@ -62,6 +62,21 @@ def test_prefill_varlen_sequences_and_strided_views():
         assert np.abs(got[a:b] - exp).max() <= 1e-2
 
 
+@pytest.mark.parametrize("out_dtype", [torch.float32, torch.bfloat16])
+def test_prefill_unaligned_output_rows_take_the_element_path(out_dtype):
+    # output rows 129 elements apart: the kernel cannot use 4-channel stores and
+    # writes element by element; the values equal those of an aligned output
+    from inquant_vllm import prefill_attention
+    n, hq, h = 300, 28, 4
+    q, k, v = _qkv(311, n, hq, h, torch.bfloat16)
+    cu = torch.tensor([0, 137, n], dtype=torch.int32, device="cuda")
+    aligned = prefill_attention(q, k, v, cu, 163, 128 ** -0.5, torch.empty((n, hq, 128), dtype=out_dtype, device="cuda"))
+    pad = torch.full((n, hq, 129), float("nan"), dtype=out_dtype, device="cuda")
+    prefill_attention(q, k, v, cu, 163, 128 ** -0.5, pad[..., :128])
+    assert torch.equal(pad[..., :128], aligned)
+    assert torch.isnan(pad[..., 128].float()).all()     # nothing written past the row
+
+
 def _outlier_qkv(seed, n, hq, h):
     # the bench's prefill input: N(0, 1) bf16 with five of 128 key channels
     # (two adjacent pairs and one single channel, ~4%) scaled by 20
