@@ -179,3 +179,33 @@ def test_stale_requests_are_refused_before_any_change(monkeypatch):
     with pytest.raises(RuntimeError, match="at most 3 requests"):
         impl.forward(None, torch.cat([r.q for r in reqs3]), torch.cat([r.k for r in reqs3]),
                      torch.cat([r.v for r in reqs3]), pool, meta, torch.empty_like(torch.cat([r.q for r in reqs3])))
+
+
+@pytest.mark.parametrize("block,lengths", [(64, [1, 3, 60, 63, 64, 65, 100, 130]),
+                                           (256, [4, 250, 255, 256, 257, 300, 20, 511])])
+def test_batch_lifecycle_with_64_and_256_token_pages(monkeypatch, block, lengths):
+    # the same lifecycle at the reference's page sizes 64 and 256: eight
+    # requests, prefills and decodes crossing page boundaries, every output
+    # against the oracle and every sealed page bit-exact
+    import sys
+    import inquant_vllm.backend as backend
+    from inquant.triton_attention import SharedDecodeWorkspace
+    monkeypatch.setattr(sys.modules[__name__], "B", block)
+    monkeypatch.setattr(backend, "WORKSPACE", SharedDecodeWorkspace())
+    monkeypatch.setattr(backend, "get_current_vllm_config", lambda: NS(
+        cache_config=NS(block_size=block), model_config=NS(max_model_len=1024), scheduler_config=NS(max_num_seqs=8)))
+    impl = backend.InQuantBatchImpl(HQ, 128, SCALE, H, None, None, "auto")
+    g = torch.Generator(device="cuda").manual_seed(block)
+    steps = 12
+    npages = sum((n + steps) // block + 1 for n in lengths) + 8
+    free = torch.randperm(npages, generator=g, device="cuda").tolist()
+    pool = torch.full((npages, impl.layout.page_bytes), 255, dtype=torch.uint8, device="cuda")
+    reqs = [_Req(f"r{i}", n + steps, [free.pop() for _ in range((n + steps) // block + 1)], g)
+            for i, n in enumerate(lengths)]
+    print(f"batch lifecycle, {block}-token pages: prefill", flush=True)
+    _step(backend, impl, pool, reqs, lengths)
+    _check_pages(pool, reqs)
+    for step in range(steps):
+        _step(backend, impl, pool, reqs, [1] * len(reqs))
+    _check_pages(pool, reqs)
+    assert all(impl.requests[r.rid].tokens == r.done for r in reqs)
