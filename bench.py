@@ -610,7 +610,9 @@ def time_append(device, H=4, packed_tokens=32768, validate_positions=True, seals
     context): 128 single-token appends (dense tail 128 -> 256, no seal), then
     `seals` times the append that seals one 256-token block (K4 + V2 encode)
     starting from a 383-token tail and the decode-state metadata append for
-    that block (medians reported)."""
+    that block (medians reported).  The sealing append synchronizes on its
+    own flag read, so its wall clock to return covers its device work; the
+    metadata append returns before its one launch finishes (host time)."""
     import torch
     from inquant.cache import CacheConfig, InQuantCache
     from inquant.codec import CodecConfig
@@ -655,22 +657,26 @@ def time_append(device, H=4, packed_tokens=32768, validate_positions=True, seals
             cache.append_for_attention(k[:, :, pos:pos + 1], v[:, :, pos:pos + 1], 0,
                                        {"cache_position": positions[pos:pos + 1]})
             pos += 1
-        # wall clock from the call to its work done on the device (the seal
-        # synchronizes once itself: its non-finite check)
+        # wall clock of the call: the seal synchronizes once itself (its
+        # position and non-finite checks), so its work is done on the device
+        # when it returns (asserted: nothing left on the stream)
         torch.cuda.synchronize()
         blocks_before = len(layer.key_blocks)
         t0 = time.perf_counter()
         cache.append_for_attention(k[:, :, pos:pos + 1], v[:, :, pos:pos + 1], 0,
                                    {"cache_position": positions[pos:pos + 1]})
-        torch.cuda.synchronize()
         t1 = time.perf_counter()
+        assert torch.cuda.current_stream().query(), "the sealing append returned with work queued"
+        torch.cuda.synchronize()
         pos += 1
         assert len(layer.key_blocks) == blocks_before + 1
         kb, vb = list(layer.key_blocks), list(layer.value_blocks)
+        # the metadata append is asynchronous (one ~3 us launch behind it):
+        # host time to return
         t2 = time.perf_counter()
         state.extend(kb, vb)
-        torch.cuda.synchronize()
         t3 = time.perf_counter()
+        torch.cuda.synchronize()
         seal_us.append((t1 - t0) * 1e6)
         meta_us.append((t3 - t2) * 1e6)
     seal_bytes = 2 * H * 256 * 128 * 2 + (16384 + 512 + 32 + 64 + 8192 + 2048) * H + 64 + H * 128

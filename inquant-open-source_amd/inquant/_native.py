@@ -154,7 +154,10 @@ def require_gpu(*tensors: torch.Tensor, what: str = "InQuant HIP kernels") -> to
 
 
 def stream_handle(device: torch.device) -> int:
-    return torch.cuda.current_stream(device).cuda_stream
+    """The current stream's raw handle (torch.cuda.current_stream(device).cuda_stream,
+    without building a Stream object: ~0.3 against ~2 us per call)."""
+    index = device.index
+    return torch._C._cuda_getCurrentRawStream(torch.cuda.current_device() if index is None else index)
 
 
 def ptr(t: torch.Tensor | None) -> int | None:

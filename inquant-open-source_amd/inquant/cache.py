@@ -174,6 +174,7 @@ class _LayerCache:
         self.packed_nbytes = 0
         self.full_sink = None          # (keys, values) views once the sink holds all its rows
         self.block_tuples = None       # (key blocks, value blocks) as tuples, rebuilt after a seal
+        self.seal_out = None           # outputs of the next one-block seal, carved ahead of it
 
     # the reference's field names, as views of the rows
     @property
@@ -202,6 +203,10 @@ class _LayerCache:
         held = sum(r.buf.numel() * r.buf.element_size() for r in (self.sink, self.tail) if r is not None)
         return held - sum(self.dense_nbytes())
 
+    def seal_reserve_nbytes(self) -> int:
+        """Bytes carved for the next seal's outputs (not yet a block)."""
+        return 0 if self.seal_out is None else self.seal_out[0].untyped_storage().nbytes()
+
 
 def _quantize_temporal_blocks(tensor: torch.Tensor, block_count: int, block_size: int,
                               config: CodecConfig, bad: torch.Tensor | None = None) -> list[PackedTensor]:
@@ -217,43 +222,75 @@ def _quantize_temporal_blocks(tensor: torch.Tensor, block_count: int, block_size
     return _per_block(packed, block_count, (1, heads, block_size, dim), PackedTensor)
 
 
+_CARVE_PLANS: dict = {}
+
+
+def _carve_plan(fields):
+    """(total bytes, dtypes in first-use order, per field (dtype index, shape,
+    strides, element offset)) of a field list; computed once per list."""
+    plan = _CARVE_PLANS.get(fields)
+    if plan is None:
+        total, dtypes, views = 0, [], []
+        for shape, dtype in fields:
+            if dtype not in dtypes:
+                dtypes.append(dtype)
+            strides, acc = [], 1
+            for n in reversed(shape):
+                strides.append(acc)
+                acc *= n
+            views.append((dtypes.index(dtype), shape, tuple(strides[::-1]), total // dtype.itemsize))
+            total += -(-math.prod(shape) * dtype.itemsize // 16) * 16
+        plan = _CARVE_PLANS[fields] = (total, tuple(dtypes), tuple(views))
+    return plan
+
+
 def _carve(device, fields):
     """The seal's output tensors as views of one allocation, each starting on
     a 16-byte boundary for the encoders' vector stores ((shape, dtype) pairs
     in order).  The byte accounting counts each view's own bytes, as for
     separate allocations; the allocation holds at most 15 alignment bytes
     per field beyond them (none for 128-channel, 16-descriptor blocks)."""
-    offsets, total = [], 0
-    for shape, dtype in fields:
-        offsets.append(total)
-        total += -(-math.prod(shape) * dtype.itemsize // 16) * 16
+    total, dtypes, views = _carve_plan(fields)
     raw = torch.empty(total, dtype=torch.uint8, device=device)
-    typed = {}                           # one reinterpretation per dtype, then strided views into it
-    out = []
-    for off, (shape, dtype) in zip(offsets, fields):
-        base = typed.get(dtype)
-        if base is None:
-            base = typed[dtype] = raw.view(dtype)
-        strides, acc = [], 1
-        for n in reversed(shape):
-            strides.append(acc)
-            acc *= n
-        out.append(torch.as_strided(base, shape, strides[::-1], off // dtype.itemsize))
-    return out
+    typed = [raw.view(dtype) for dtype in dtypes]   # one reinterpretation per dtype
+    return [torch.as_strided(typed[i], shape, strides, offset) for i, shape, strides, offset in views]
+
+
+_SEAL_DTYPES = (torch.float32, torch.bfloat16, torch.float16)   # what the batched seal encoders read
+
+
+def _seal_native(dim: int, bits: int | None, group_size: int) -> bool:
+    """Whether a seal of this head size runs as one batched library call."""
+    return dim % 2 == 0 and dim <= 1024 and (bits is None or dim % group_size == 0)
+
+
+def _seal_fields(B: int, H: int, T: int, D: int, count: int, bits: int | None, group_size: int) -> tuple:
+    """(shape, dtype) of a batched seal's outputs, in the encoder's argument
+    order: the K4 keys' payload, scales, sources, donors and padding, then
+    the group-wise values' payload, scales and offsets, or (bits None) the
+    K4-coded values' five fields."""
+    desc_dtype = torch.uint8 if D <= 256 else torch.int32
+    k4 = (((B, H, T, D // 2), torch.uint8), ((B, H, D), torch.float32), ((B, H, count), desc_dtype),
+          ((B, H, count), desc_dtype), ((B, H, count), torch.float32))
+    if bits is None:
+        return k4 + k4
+    return k4 + (((B, H, T, D * bits // 8), torch.uint8), ((B, H, T, D // group_size), torch.float16),
+                 ((B, H, T, D // group_size), torch.float16))
 
 
 def _kv_blocks(keys: torch.Tensor, values: torch.Tensor, block_count: int, block_size: int, config: CodecConfig,
-               bits: int, group_size: int, key_flag: torch.Tensor, value_flag: torch.Tensor):
+               bits: int, group_size: int, key_flag: torch.Tensor, value_flag: torch.Tensor, out=None):
     """K4 keys and group-wise values of the first ``block_count`` blocks of
     [1, H, T, D] in one library call (iq_kv_quantize: one launch for sealed
     256-token blocks of 128 16-bit channels, the two encoders back to back
     otherwise), with the per-block objects and flags of
-    _quantize_temporal_blocks + _value_blocks (cache.py:288-295)."""
+    _quantize_temporal_blocks + _value_blocks (cache.py:288-295).  ``out``:
+    the outputs as carved for _seal_fields, allocated beforehand."""
     if block_count == 0:
         return [], []
     _, heads, _, dim = keys.shape
-    native = (keys.dtype == values.dtype and keys.dtype in (torch.float32, torch.bfloat16, torch.float16)
-              and keys.shape == values.shape and dim % 2 == 0 and dim <= 1024 and dim % group_size == 0)
+    native = (keys.dtype == values.dtype and keys.dtype in _SEAL_DTYPES and keys.shape == values.shape
+              and _seal_native(dim, bits, group_size))
     if not native:      # the separate encoders, with their own argument errors
         return (_quantize_temporal_blocks(keys, block_count, block_size, config, key_flag),
                 _value_blocks(values, block_count, block_size, bits, group_size, value_flag))
@@ -265,11 +302,8 @@ def _kv_blocks(keys: torch.Tensor, values: torch.Tensor, block_count: int, block
     k_strides = (nat._i64 * 4)(T * ks[2], ks[1], ks[2], ks[3])
     v_strides = (nat._i64 * 4)(T * vs[2], vs[1], vs[2], vs[3])
     count = math.floor(D * config.salient_fraction)
-    desc_dtype = torch.uint8 if D <= 256 else torch.int32
-    payload, scales, src, don, padding, v_payload, v_scales, v_offsets = _carve(device, (
-        ((B, H, T, D // 2), torch.uint8), ((B, H, D), torch.float32), ((B, H, count), desc_dtype),
-        ((B, H, count), desc_dtype), ((B, H, count), torch.float32), ((B, H, T, D * bits // 8), torch.uint8),
-        ((B, H, T, D // group_size), torch.float16), ((B, H, T, D // group_size), torch.float16)))
+    payload, scales, src, don, padding, v_payload, v_scales, v_offsets = (
+        out if out is not None else _carve(device, _seal_fields(B, H, T, D, count, bits, group_size)))
     nat.check(nat.lib().iq_kv_quantize(
         keys.data_ptr(), values.data_ptr(), nat.dtype_code(keys.dtype), k_strides, v_strides, B, H, T, D,
         count, config.sample_stride, int(config.donor_policy == "min_error"), payload.data_ptr(),
@@ -285,16 +319,17 @@ def _kv_blocks(keys: torch.Tensor, values: torch.Tensor, block_count: int, block
 
 
 def _k4_pair_blocks(keys: torch.Tensor, values: torch.Tensor, block_count: int, block_size: int,
-                    config: CodecConfig, key_flag: torch.Tensor, value_flag: torch.Tensor):
+                    config: CodecConfig, key_flag: torch.Tensor, value_flag: torch.Tensor, out=None):
     """K4 keys and K4-coded values (value_bits None) of the first
     ``block_count`` blocks in one library call (iq_k4_quantize_kv: one launch
     for 16-bit blocks of 128 channels), with the per-block objects and flags
-    of two _quantize_temporal_blocks calls (cache.py:288-291)."""
+    of two _quantize_temporal_blocks calls (cache.py:288-291).  ``out`` as
+    for _kv_blocks."""
     if block_count == 0:
         return [], []
     _, heads, _, dim = keys.shape
-    native = (keys.dtype == values.dtype and keys.dtype in (torch.float32, torch.bfloat16, torch.float16)
-              and keys.shape == values.shape and dim % 2 == 0 and dim <= 1024)
+    native = (keys.dtype == values.dtype and keys.dtype in _SEAL_DTYPES and keys.shape == values.shape
+              and _seal_native(dim, None, 0))
     if not native:      # the separate encodes, with their own argument errors
         return (_quantize_temporal_blocks(keys, block_count, block_size, config, key_flag),
                 _quantize_temporal_blocks(values, block_count, block_size, config, value_flag))
@@ -304,11 +339,7 @@ def _k4_pair_blocks(keys: torch.Tensor, values: torch.Tensor, block_count: int, 
     k_strides = (nat._i64 * 4)(T * ks[2], ks[1], ks[2], ks[3])
     v_strides = (nat._i64 * 4)(T * vs[2], vs[1], vs[2], vs[3])
     count = math.floor(D * config.salient_fraction)
-    desc_dtype = torch.uint8 if D <= 256 else torch.int32
-
-    fields = (((B, H, T, D // 2), torch.uint8), ((B, H, D), torch.float32), ((B, H, count), desc_dtype),
-              ((B, H, count), desc_dtype), ((B, H, count), torch.float32))
-    carved = _carve(device, fields + fields)
+    carved = out if out is not None else _carve(device, _seal_fields(B, H, T, D, count, None, 0))
     ko, vo = carved[:5], carved[5:]
     ptrs = lambda o: [o[0].data_ptr(), o[1].data_ptr()] + [t.data_ptr() if count else None for t in o[2:]]
     nat.check(nat.lib().iq_k4_quantize_kv(
@@ -515,30 +546,46 @@ class InQuantCache(_HFCache):
             nat.check(status)
         if shift:
             tail.start = start = 0
-        if check_now:
-            # the first layer of a step: raise now, before the row counts
+        seals = tail.count + 1 >= cfg.residual_length + cfg.block_size
+        verified = (position, _version(position), layer.seq_length) if check_now else None
+        if check_now and not seals:
+            # the first layer of a step: raise now, before the row counts (an
+            # append that seals reads this flag with the encoders' flags in
+            # its one synchronization, position first, and raises the same way)
             if bool(flags[_POSITION_BAD].item()):
                 flags[_POSITION_BAD].zero_()
                 self._position_checked = None
                 raise ValueError(_POSITION_ERROR)
-            self._position_checked = (position, _version(position), layer.seq_length)
+            self._position_checked = verified
         tail.count += 1
         layer.seq_length += 1
         tail_k, tail_v = tail.views()
         view = PackedAttentionView(*blocks, *sink, tail_k, tail_v, layer.seq_length)
-        if tail.count >= cfg.residual_length + cfg.block_size:
+        if seals:
+            out, layer.seal_out = layer.seal_out, None
             try:
                 with torch.no_grad():
-                    self._seal(layer, tail_k, tail_v, 1)
+                    self._seal(layer, tail_k, tail_v, 1, out)
             except ValueError:
                 tail.count -= 1                  # the reference leaves the layer unchanged on errors
                 layer.seq_length -= 1
+                layer.seal_out = out             # rewritten in full by the next seal
                 raise
+            if verified is not None:
+                self._position_checked = verified
             tail.start += cfg.block_size
             tail.count -= cfg.block_size
+        elif layer.seal_out is None:
+            # an append that does not seal carves the next seal's outputs, so
+            # the seal launches its encoder without allocating first
+            heads, dim = layer.shape[1], layer.shape[3]
+            if layer.dtype in _SEAL_DTYPES and _seal_native(dim, cfg.value_bits, cfg.value_group_size):
+                count = math.floor(dim * cfg.codec.salient_fraction)
+                layer.seal_out = _carve(layer.device, _seal_fields(1, heads, cfg.block_size, dim, count,
+                                                                   cfg.value_bits, cfg.value_group_size))
         return view
 
-    def _seal(self, layer, keys, values, count) -> None:
+    def _seal(self, layer, keys, values, count, out=None) -> None:
         """Encode the first ``count`` blocks of keys/values [1, H, >= count * B, D]
         and append them; non-finite data raise ValueError with the layer unchanged.
         The key and value encoders raise flags into one buffer read by a single
@@ -550,12 +597,13 @@ class InQuantCache(_HFCache):
         flags = self._flag_words(keys.device)
         if cfg.value_bits is None:
             new_keys, new_values = _k4_pair_blocks(keys, values, count, cfg.block_size, cfg.codec,
-                                                   flags[_KEY_BAD:_KEY_BAD + 1], flags[_VALUE_BAD:_VALUE_BAD + 1])
+                                                   flags[_KEY_BAD:_KEY_BAD + 1], flags[_VALUE_BAD:_VALUE_BAD + 1],
+                                                   out)
             value_error = _BAD_K
         else:
             new_keys, new_values = _kv_blocks(keys, values, count, cfg.block_size, cfg.codec, cfg.value_bits,
                                               cfg.value_group_size, flags[_KEY_BAD:_KEY_BAD + 1],
-                                              flags[_VALUE_BAD:_VALUE_BAD + 1])
+                                              flags[_VALUE_BAD:_VALUE_BAD + 1], out)
             value_error = _BAD_V
         bad_key, bad_value, bad_position = flags.tolist()
         if bad_key or bad_value or bad_position:
@@ -703,6 +751,8 @@ class InQuantCache(_HFCache):
             "kv_reduction_vs_bf16": (1 - total / dense) if dense else 0.0,
             # preallocated dense rows not yet holding tokens (not part of nbytes)
             "dense_reserve_nbytes": sum(l.reserved_nbytes() for l in self._layers.values()),
+            # outputs carved for each layer's next one-block seal (not part of nbytes)
+            "seal_reserve_nbytes": sum(l.seal_reserve_nbytes() for l in self._layers.values()),
         }
 
     def reset(self) -> None:

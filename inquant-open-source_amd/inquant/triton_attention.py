@@ -271,12 +271,15 @@ class PackedDecodeState:
             raise ValueError("PackedDecodeState.extend requires an immutable append-only prefix")
         if len(key_blocks) == have:
             return
-        fmt = _BlockFormat(key_blocks[0], value_blocks[0])
+        if have:
+            # the first blocks are the ones held (identity), so is their format
+            fmt = self._format
+        else:
+            fmt = _BlockFormat(key_blocks[0], value_blocks[0])
+            if self._format is not None and not self._format.same(fmt):
+                raise ValueError("All packed K/V blocks must share shape and salient-channel count")
         stream = self._pin.check(fmt.device)
         new_keys, new_values = tuple(key_blocks[have:]), tuple(value_blocks[have:])
-        # blocks already held were admitted under the same format
-        if self._format is not None and not self._format.same(fmt):
-            raise ValueError("All packed K/V blocks must share shape and salient-channel count")
         fmt.admit(new_keys, new_values)
         if self._desc is None or self._desc.tables.device != fmt.device:
             self._desc = _Descriptors(fmt.device, fmt.heads, fmt.value_bits == 0)

@@ -286,6 +286,62 @@ def test_single_token_position_check():
     assert cache.get_seq_length() == 7
 
 
+@pytest.mark.parametrize("value_bits", [None, 2])
+def test_sealing_append_checks_its_position_in_the_seal_sync(value_bits):
+    # An append that seals reads the position flag together with the
+    # encoders' flags (one synchronization, position first): a wrong position
+    # raises the reference's error and leaves every layer unchanged; the right
+    # one seals, and a second layer given the same verified tensor seals too.
+    from inquant.cache import InQuantCache
+    cache = InQuantCache(_cfg(value_bits=value_bits, value_group_size=32))
+    k, v = _randn(1, 2, 21, 64, seed=60), _randn(1, 2, 21, 64, seed=61)
+    for layer in (0, 1):
+        cache.update(k[:, :, :12], v[:, :, :12], layer, {"cache_position": torch.arange(12, device="cuda")})
+    before = (cache.get_seq_length(0), len(cache._layers[0].key_blocks), cache.nbytes,
+              cache._layers[0].tail.count, cache._layers[0].tail.start)
+    assert before[1] == 0 and before[3] == 10          # the next append fills the tail: 3 + 8 rows
+    t, u = k[:, :, 12:13], v[:, :, 12:13]
+    for wrong in (11, 13):
+        with pytest.raises(ValueError, match="contiguous append positions"):
+            cache.append_for_attention(t, u, 0, {"cache_position": torch.tensor([wrong], device="cuda")})
+        assert (cache.get_seq_length(0), len(cache._layers[0].key_blocks), cache.nbytes,
+                cache._layers[0].tail.count, cache._layers[0].tail.start) == before
+        assert cache._position_checked is None and not any(cache._flags.tolist())
+    p = torch.tensor([12], device="cuda")
+    views = [cache.append_for_attention(t, u, layer, {"cache_position": p}) for layer in (0, 1)]
+    assert cache._position_checked[0] is p and cache._position_checked[2] == 12
+    for layer, view in enumerate(views):
+        assert len(cache._layers[layer].key_blocks) == 1 and cache.get_seq_length(layer) == 13
+        assert len(view.key_blocks) == 0                   # attended from the next step on
+        assert torch.equal(view.residual_key, k[:, :, 2:13]) and torch.equal(view.residual_value, v[:, :, 2:13])
+    # the next append, which does not seal, carves the next seal's outputs
+    # (reported apart from nbytes); the seal after it encodes into them
+    layer = cache._layers[0]
+    assert layer.seal_out is None and cache.memory_stats()["seal_reserve_nbytes"] == 0
+    nbytes = cache.nbytes
+    cache.append_for_attention(k[:, :, 13:14], v[:, :, 13:14], 0, {"cache_position": torch.tensor([13], device="cuda")})
+    carved = [t.data_ptr() for t in layer.seal_out]
+    assert cache.memory_stats()["seal_reserve_nbytes"] == layer.seal_out[0].untyped_storage().nbytes() > 0
+    assert cache.nbytes == nbytes + 2 * 2 * 64 * k.element_size()       # one more tail row only
+    for pos in range(14, 21):
+        cache.append_for_attention(k[:, :, pos:pos + 1], v[:, :, pos:pos + 1], 0,
+                                   {"cache_position": torch.tensor([pos], device="cuda")})
+    assert len(layer.key_blocks) == 2 and cache.get_seq_length(0) == 21
+    fields = list(layer.key_blocks[1].tensors.values()) + list(layer.value_blocks[1].tensors.values())
+    assert [t.data_ptr() for t in fields] == carved
+    # both sealed blocks equal the ones update() seals from the same tokens
+    ref = InQuantCache(_cfg(value_bits=value_bits, value_group_size=32))
+    ref.update(k[:, :, :21], v[:, :, :21], 0)
+    assert len(ref._layers[0].key_blocks) == 2
+    for i in range(2):
+        for a, b in ((layer.key_blocks[i], ref._layers[0].key_blocks[i]),
+                     (layer.value_blocks[i], ref._layers[0].value_blocks[i])):
+            for name, x in a.tensors.items():
+                assert torch.equal(x, b.tensors[name]), (i, name)
+    assert sum(b.nbytes for b in layer.key_blocks + layer.value_blocks) == \
+        sum(b.nbytes for b in ref._layers[0].key_blocks + ref._layers[0].value_blocks)
+
+
 @pytest.mark.parametrize("inference", [False, True])
 def test_shared_cache_position_checked_on_the_device(inference):
     # The layers of one step share one cache_position tensor.  The first
