@@ -743,7 +743,8 @@ def time_step_graph(device, H=4, HQ=28, packed_tokens=32768, layers=28, reps=50)
     (sink + 128 blocks + tail, two launches).  The replays rewrite the same
     tail row and decode the same length, so they time the device work of one
     step without the host's per-call cost; the same step run eagerly is
-    timed beside it.  The captured appends take no cache_position: the
+    timed beside it, and the 28 appends alone as a second graph.  The
+    captured appends take no cache_position: the
     position check reads a device flag back on the host, which a graph
     cannot do."""
     import torch
@@ -801,10 +802,28 @@ def time_step_graph(device, H=4, HQ=28, packed_tokens=32768, layers=28, reps=50)
     stop.record()
     torch.cuda.synchronize()
     us = start.elapsed_time(stop) * 1e3 / reps
-    assert cache._layers[0].tail.count < cfg.residual_length + cfg.block_size     # no seal inside the graph
+    # the 28 appends alone, captured the same way (one launch per layer)
+    appends = torch.cuda.CUDAGraph()
+    kk, vv = k[:, :, pos:pos + 1], v[:, :, pos:pos + 1]
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(appends, stream=s):
+            for i in range(layers):
+                cache.append_for_attention(kk, vv, i)
+    torch.cuda.synchronize()
+    for _ in range(3):
+        appends.replay()
+    torch.cuda.synchronize()
+    start.record()
+    for _ in range(reps):
+        appends.replay()
+    stop.record()
+    torch.cuda.synchronize()
+    append_us = start.elapsed_time(stop) * 1e3 / reps
+    assert cache._layers[0].tail.count < cfg.residual_length + cfg.block_size     # no seal inside the graphs
     return {"layers": layers, "graph_step_us": round(us, 1), "graph_us_per_layer": round(us / layers, 2),
             "eager_step_us": round(eager_us, 1), "eager_us_per_layer": round(eager_us / layers, 2),
-            "launches_per_layer": 3}
+            "launches_per_layer": 3, "graph_append_step_us": round(append_us, 1),
+            "graph_append_us_per_layer": round(append_us / layers, 2)}
 
 
 def _cpu_model() -> str:

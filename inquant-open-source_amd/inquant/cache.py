@@ -575,9 +575,10 @@ class InQuantCache(_HFCache):
                 self._position_checked = verified
             tail.start += cfg.block_size
             tail.count -= cfg.block_size
-        elif layer.seal_out is None:
-            # an append that does not seal carves the next seal's outputs, so
-            # the seal launches its encoder without allocating first
+        elif layer.seal_out is None and not torch.cuda.is_current_stream_capturing():
+            # an append that does not seal (and is not being captured in a
+            # graph) carves the next seal's outputs, so the seal launches its
+            # encoder without allocating first
             heads, dim = layer.shape[1], layer.shape[3]
             if layer.dtype in _SEAL_DTYPES and _seal_native(dim, cfg.value_bits, cfg.value_group_size):
                 count = math.floor(dim * cfg.codec.salient_fraction)
