@@ -81,6 +81,29 @@ __device__ __forceinline__ float iq_rint_div(float a, float b, float rcp_b)
 
 __device__ __forceinline__ bool iq_isfinite(float x) { return (__float_as_uint(x) & 0x7f800000u) != 0x7f800000u; }
 
+// ---------------------------------------------------------------- direct loads
+
+// One 16-byte-per-lane direct global -> LDS load: lane l's 16 bytes at
+// base + voff land at LDS byte lds_base + 16 l (base and lds_base
+// wave-uniform).  Issued from inline assembly so that the compiler does not
+// treat every later LDS read as possibly dependent on it (it would wait for
+// all loads in flight); callers wait explicitly (s_waitcnt vmcnt, then a
+// barrier).  The assembly sets M0 itself; nothing the compiler generates for
+// the kernels that use it reads M0 (M0 is a reserved register, so it cannot
+// be listed as clobbered).
+__device__ __forceinline__ void lds_load16(const void *base, uint32_t voff, uint32_t lds_base)
+{
+    // the operands are wave-uniform: make them scalar registers explicitly
+    // (readfirstlane returns int: widen through uint32_t, not by sign extension)
+    const uint64_t b = (uint64_t)(uintptr_t)base;
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)b);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(b >> 32));
+    const uint64_t sb = (uint64_t)lo | ((uint64_t)hi << 32);
+    asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sb),
+                 "s"(__builtin_amdgcn_readfirstlane(lds_base))
+                 : "memory");
+}
+
 // ---------------------------------------------------------------- torch CPU reduction orders
 
 // Columns [0, iq_cascade_columns(D)) of an outer reduction are summed by

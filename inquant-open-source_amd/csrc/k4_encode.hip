@@ -242,26 +242,6 @@ constexpr int NBUF_DMA = 4;
 // every older load is done; stores issued after a chunk's loads only make
 // the wait longer.  (A plain __syncthreads would wait for all loads in
 // flight.)
-// One 16-byte-per-lane direct load: lane l's 16 bytes at base + voff land
-// at LDS byte lds_base + 16 l (base and lds_base wave-uniform).  Issued from
-// inline assembly so that the compiler does not treat every later LDS read
-// as possibly dependent on it (it would wait for all loads in flight); the
-// waits are explicit (wait_chunk_barrier).  The assembly sets M0 itself;
-// nothing the compiler generates for this kernel reads M0 (M0 is a reserved
-// register, so it cannot be listed as clobbered).
-__device__ __forceinline__ void lds_load16(const void *base, uint32_t voff, uint32_t lds_base)
-{
-    // the operands are wave-uniform: make them scalar registers explicitly
-    // (readfirstlane returns int: widen through uint32_t, not by sign extension)
-    const uint64_t b = (uint64_t)(uintptr_t)base;
-    const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)b);
-    const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(b >> 32));
-    const uint64_t sb = (uint64_t)lo | ((uint64_t)hi << 32);
-    asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sb),
-                 "s"(__builtin_amdgcn_readfirstlane(lds_base))
-                 : "memory");
-}
-
 __device__ __forceinline__ void wait_chunk_barrier(int ahead)
 {
     switch (ahead) {
