@@ -499,7 +499,9 @@ def time_paged(device, layers=4, n_seq=16, block=16, H=4, G=7, seed=4, steps=20,
     dense slots); the decode launches the lifecycle makes for the next token
     are then replayed back to back in a graph.  `lifecycle_steps` whole decode
     steps through InQuantBatchImpl.forward (new-token writes, the batched
-    decode, the seals of filled pages, host included) are timed eagerly."""
+    decode, the seals of filled pages, host included) are timed eagerly, and
+    the causal prefill of the first layer's 16 sequences (one varlen launch)
+    alone in a graph."""
     import torch
     import inquant_vllm.backend as backend
     from inquant.triton_attention import SharedDecodeWorkspace
@@ -534,6 +536,15 @@ def time_paged(device, layers=4, n_seq=16, block=16, H=4, G=7, seed=4, steps=20,
                                             torch.tensor(qsl, dtype=torch.int32, device=device), qsl, list(ctx),
                                             tables, ())
         impl.forward(None, q, k, v, pool, meta, torch.empty_like(q))      # prefill: pools built by the lifecycle
+        if not work:
+            # the causal prefill of these 16 sequences alone (the lifecycle's
+            # one varlen launch), replayed in a graph
+            from inquant_vllm.kernels import prefill_attention
+            cu = torch.tensor(qsl, dtype=torch.int32, device=device)
+            pout = torch.empty_like(q)
+            pf_us = _graph_us(device, lambda: prefill_attention(q, k, v, cu, max(ctx), 128 ** -0.5, pout), reps=2)
+            pf_flops = sum(4 * H * G * 128 * c * (c + 1) / 2 for c in ctx)
+            del pout
         del q, k, v
         slots = torch.tensor([impl.requests[f"seq{i}"].slot for i in range(n_seq)], dtype=torch.int32,
                              device=device)
@@ -602,7 +613,10 @@ def time_paged(device, layers=4, n_seq=16, block=16, H=4, G=7, seed=4, steps=20,
             "work_items": int(items.numel()), "us_per_layer_full_grid": round(us_grid, 3),
             "built_by": "InQuantBatchImpl prefill of the 16 requests",
             "lifecycle_step_us": round(life_us, 1), "lifecycle_steps": lifecycle_steps,
-            "lifecycle_seal_launches": impl.seal_calls - seals0}
+            "lifecycle_seal_launches": impl.seal_calls - seals0,
+            "prefill_varlen": {"sequences": n_seq, "tokens": sum(ctx), "max_seqlen": max(ctx),
+                               "us": round(pf_us, 1), "tflops": round(pf_flops / (pf_us * 1e-6) / 1e12, 1),
+                               "mfma_frac": round(pf_flops / (pf_us * 1e-6) / 1e12 / MFMA_BF16_PEAK_TFLOPS, 4)}}
 
 
 def time_append(device, H=4, packed_tokens=32768, validate_positions=True, seals=7):
