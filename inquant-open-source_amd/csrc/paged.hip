@@ -403,13 +403,26 @@ __device__ __forceinline__ void paged_body(const PagedArgs &a, PagedSmem<NPG> &s
             sm.spad()[lp * SPG + j] = 0.0f;
         }
         __syncthreads();
-        // a source's descriptor index is -2 - key_map[its donor]; a donor's is -2 - key_map
+        // a source's descriptor index is -2 - key_map[its donor]; a donor's is
+        // -2 - key_map.  Every read first, unconditionally (a source's donor
+        // role, a donor's raw padding; other channels read entry 0), so the
+        // eight items cost one LDS round trip instead of one each behind
+        // their branches (config 4: 71.0 -> 68.3 us per layer with the bias below)
         if (cvalid) {
+            int rdon[CPT];
+            float praw[CPT];
+#pragma unroll
+            for (int k = 0; k < CPT; ++k) {
+                const int lp = cpart(k), role = krl[k];
+                rdon[k] = sm.role()[lp * D + (role >= 0 && role < D ? role : 0)];
+                const int jd = -2 - role;
+                praw[k] = sm.padraw()[lp * SPG + (jd >= 0 && jd < SPG ? jd : 0)];
+            }
 #pragma unroll
             for (int k = 0; k < CPT; ++k) {
                 const int lp = cpart(k), c = cchan(k), role = krl[k];
                 if (role >= 0 && role < D) {
-                    const int j = -2 - (int)sm.role()[lp * D + role];
+                    const int j = -2 - rdon[k];
                     if (j >= 0 && j < SPG) {
                         sm.ssrc()[lp * SPG + j] = (int8_t)c;
                         sm.sssc()[lp * SPG + j] = ksc[k];
@@ -417,7 +430,7 @@ __device__ __forceinline__ void paged_body(const PagedArgs &a, PagedSmem<NPG> &s
                 } else if (role <= -2 && role >= -2 - (SPG - 1)) {
                     const int j = -2 - role;
                     sm.sdon()[lp * SPG + j] = (int8_t)c;
-                    sm.spad()[lp * SPG + j] = round_q<false>(sm.padraw()[lp * SPG + j]);
+                    sm.spad()[lp * SPG + j] = round_q<false>(praw[k]);
                 }
             }
         }
@@ -431,9 +444,18 @@ __device__ __forceinline__ void paged_body(const PagedArgs &a, PagedSmem<NPG> &s
         }
         for (int i = tid; i < NPG * 16; i += 256) {
             const int lp = i >> 4, g = i & 15;
+            // the page's 16 donors and paddings as vector reads, then the 16
+            // query gathers together, then the sum in descriptor order
+            const u32x4 dn = *(const u32x4 *)(sm.sdon() + lp * SPG);
+            f32x4 pd[SPG / 4];
+#pragma unroll
+            for (int e = 0; e < SPG / 4; ++e) pd[e] = *(const f32x4 *)(sm.spad() + lp * SPG + 4 * e);
+            uint32_t qv[SPG];
+#pragma unroll
+            for (int k = 0; k < SPG; ++k) qv[k] = s_q[g * QROW + ((dn[k >> 2] >> (8 * (k & 3))) & 0xffu)];
             float b = 0.0f;
-            for (int k = 0; k < SPG; ++k)
-                b = fmaf(to_f32<false>(s_q[g * QROW + (uint8_t)sm.sdon()[lp * SPG + k]]), sm.spad()[lp * SPG + k], b);
+#pragma unroll
+            for (int k = 0; k < SPG; ++k) b = fmaf(to_f32<false>(qv[k]), pd[k >> 2][k & 3], b);
 #pragma unroll
             for (int o = 0; o < OWNERS; ++o) sm.bias(owner0(lp) + o)[local(lp) * 16 + g] = b;
         }
