@@ -257,6 +257,21 @@ def _carve(device, fields):
 
 
 _SEAL_DTYPES = (torch.float32, torch.bfloat16, torch.float16)   # what the batched seal encoders read
+_STRIDES: dict = {}
+
+
+def _block_strides(strides, T: int):
+    """The encoders' (block, head, token, channel) element strides of the
+    [blocks, H, T, D] view of a [1, H, tokens, D] tensor with these strides,
+    as a ctypes array (one per stride pattern: the tail buffers' never change;
+    the library only reads it)."""
+    key = (strides, T)
+    arr = _STRIDES.get(key)
+    if arr is None:
+        if len(_STRIDES) > 256:
+            _STRIDES.clear()
+        arr = _STRIDES[key] = (nat._i64 * 4)(T * strides[2], strides[1], strides[2], strides[3])
+    return arr
 
 
 def _seal_native(dim: int, bits: int | None, group_size: int) -> bool:
@@ -298,9 +313,8 @@ def _kv_blocks(keys: torch.Tensor, values: torch.Tensor, block_count: int, block
     # the [blocks, H, B, D] view of the first blocks, as pointer and strides
     # (no view objects: the encoder reads them directly)
     B, H, T, D = block_count, heads, block_size, dim
-    ks, vs = keys.stride(), values.stride()
-    k_strides = (nat._i64 * 4)(T * ks[2], ks[1], ks[2], ks[3])
-    v_strides = (nat._i64 * 4)(T * vs[2], vs[1], vs[2], vs[3])
+    k_strides = _block_strides(keys.stride(), T)
+    v_strides = _block_strides(values.stride(), T)
     count = math.floor(D * config.salient_fraction)
     payload, scales, src, don, padding, v_payload, v_scales, v_offsets = (
         out if out is not None else _carve(device, _seal_fields(B, H, T, D, count, bits, group_size)))
@@ -312,6 +326,9 @@ def _kv_blocks(keys: torch.Tensor, values: torch.Tensor, block_count: int, block
         v_scales.data_ptr(), v_offsets.data_ptr(), key_flag.data_ptr(), value_flag.data_ptr(),
         nat.stream_handle(device)))
     shape = (1, heads, block_size, dim)
+    if B == 1:          # a seal's one block: the objects directly
+        return ([PackedTensor(payload, scales, src, don, padding, shape, keys.dtype)],
+                [PackedValues(v_payload, v_scales, v_offsets, shape, values.dtype, bits, group_size)])
     packed_k = PackedTensor(payload, scales, src, don, padding, (B, H, T, D), keys.dtype)
     packed_v = PackedValues(v_payload, v_scales, v_offsets, (B, H, T, D), values.dtype, bits, group_size)
     return (_per_block(packed_k, block_count, shape, PackedTensor),
@@ -335,9 +352,8 @@ def _k4_pair_blocks(keys: torch.Tensor, values: torch.Tensor, block_count: int, 
                 _quantize_temporal_blocks(values, block_count, block_size, config, value_flag))
     device = nat.require_gpu(keys, what="quantize")
     B, H, T, D = block_count, heads, block_size, dim
-    ks, vs = keys.stride(), values.stride()
-    k_strides = (nat._i64 * 4)(T * ks[2], ks[1], ks[2], ks[3])
-    v_strides = (nat._i64 * 4)(T * vs[2], vs[1], vs[2], vs[3])
+    k_strides = _block_strides(keys.stride(), T)
+    v_strides = _block_strides(values.stride(), T)
     count = math.floor(D * config.salient_fraction)
     carved = out if out is not None else _carve(device, _seal_fields(B, H, T, D, count, None, 0))
     ko, vo = carved[:5], carved[5:]
@@ -347,6 +363,8 @@ def _k4_pair_blocks(keys: torch.Tensor, values: torch.Tensor, block_count: int, 
         count, config.sample_stride, int(config.donor_policy == "min_error"), *ptrs(ko), *ptrs(vo),
         ko[2].element_size(), key_flag.data_ptr(), value_flag.data_ptr(), nat.stream_handle(device)))
     shape = (1, heads, block_size, dim)
+    if B == 1:          # a seal's one block: the objects directly
+        return [PackedTensor(*ko, shape, keys.dtype)], [PackedTensor(*vo, shape, values.dtype)]
     return (_per_block(PackedTensor(*ko, (B, H, T, D), keys.dtype), block_count, shape, PackedTensor),
             _per_block(PackedTensor(*vo, (B, H, T, D), values.dtype), block_count, shape, PackedTensor))
 
