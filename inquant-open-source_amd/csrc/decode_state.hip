@@ -14,12 +14,15 @@ namespace {
 
 constexpr int APPEND_CHUNK = 24;       // blocks per launch (kernel-argument budget)
 
+// N block address rows travel as kernel arguments: N = 1 for the usual
+// one-block append of a seal (~140 argument bytes to write at launch, not ~2 KB)
+template <int N>
 struct AppendArgs {
     int64_t *tables;
     int8_t *key_map, *value_map;
     int64_t first, count, H, S;
     int desc_bytes;
-    iq_block_ptrs blocks[APPEND_CHUNK];
+    iq_block_ptrs blocks[N];
 };
 
 __device__ __forceinline__ int load_desc(uint64_t p, int64_t i, int bytes)
@@ -30,7 +33,8 @@ __device__ __forceinline__ int load_desc(uint64_t p, int64_t i, int bytes)
 }
 
 // grid (count, H): one 128-thread workgroup writes one block's map for one head.
-__global__ __launch_bounds__(128) void append_kernel(AppendArgs a)
+template <int N>
+__global__ __launch_bounds__(128) void append_kernel(AppendArgs<N> a)
 {
     __shared__ int8_t s_k[128], s_v[128];
     const int blk = blockIdx.x, h = blockIdx.y, c = threadIdx.x;
@@ -60,6 +64,25 @@ __global__ __launch_bounds__(128) void append_kernel(AppendArgs a)
     if (a.value_map) a.value_map[(slot * a.H + h) * 128 + c] = s_v[c];
 }
 
+template <int N>
+int launch_append(int64_t *tables, int8_t *key_map, int8_t *value_map, int64_t first, int64_t n,
+                  const iq_block_ptrs *blocks, int64_t H, int64_t S, int desc_bytes, void *stream)
+{
+    AppendArgs<N> a{};
+    a.tables = tables;
+    a.key_map = key_map;
+    a.value_map = value_map;
+    a.first = first;
+    a.count = n;
+    a.H = H;
+    a.S = S;
+    a.desc_bytes = desc_bytes;
+    for (int64_t i = 0; i < n; ++i) a.blocks[i] = blocks[i];
+    hipLaunchKernelGGL(append_kernel<N>, dim3((unsigned)n, (unsigned)H), dim3(128), 0, (hipStream_t)stream, a);
+    IQ_CHECK_LAUNCH("append_kernel");
+    return IQ_OK;
+}
+
 }  // namespace
 
 extern "C" int iq_decode_append(int64_t *tables, int8_t *key_map, int8_t *value_map, int64_t first,
@@ -79,20 +102,12 @@ extern "C" int iq_decode_append(int64_t *tables, int8_t *key_map, int8_t *value_
         IQ_CHECK_ARG(!value_map || S == 0 || (blocks[i].v_src && blocks[i].v_don),
                      "iq_decode_append: missing V descriptors");
     }
+    if (count == 1) return launch_append<1>(tables, key_map, value_map, first, 1, blocks, H, S, desc_bytes, stream);
     for (int64_t done = 0; done < count; done += APPEND_CHUNK) {
         const int64_t n = count - done < APPEND_CHUNK ? count - done : APPEND_CHUNK;
-        AppendArgs a{};
-        a.tables = tables;
-        a.key_map = key_map;
-        a.value_map = value_map;
-        a.first = first + done;
-        a.count = n;
-        a.H = H;
-        a.S = S;
-        a.desc_bytes = desc_bytes;
-        for (int64_t i = 0; i < n; ++i) a.blocks[i] = blocks[done + i];
-        hipLaunchKernelGGL(append_kernel, dim3((unsigned)n, (unsigned)H), dim3(128), 0, (hipStream_t)stream, a);
-        IQ_CHECK_LAUNCH("append_kernel");
+        const int rc = launch_append<APPEND_CHUNK>(tables, key_map, value_map, first + done, n, blocks + done, H, S,
+                                                   desc_bytes, stream);
+        if (rc != IQ_OK) return rc;
     }
     return IQ_OK;
 }

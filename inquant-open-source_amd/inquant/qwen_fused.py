@@ -69,7 +69,7 @@ def _layer_state(cache: InQuantCache, layer: int, view):
         state = PackedDecodeState(view.key_blocks, view.value_blocks,
                                   workspace_pool=cache._shared_decode_workspace)
         cache._attention_states[layer] = state
-    elif len(state.key_blocks) != len(view.key_blocks):
+    elif state.block_count != len(view.key_blocks):
         state.extend(view.key_blocks, view.value_blocks)
     return state
 

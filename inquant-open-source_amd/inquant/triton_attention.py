@@ -238,14 +238,33 @@ class PackedDecodeState:
     def __init__(self, key_blocks, value_blocks, *, workspace_pool=None):
         if len(key_blocks) != len(value_blocks):
             raise ValueError("Key and value block counts must match")
-        self.key_blocks = ()
-        self.value_blocks = ()
+        self._keys: list = []       # the blocks held, grown by each extend's new suffix
+        self._values: list = []
+        self._held = None           # (key tuple, value tuple) of them, built on request
         self._format: _BlockFormat | None = None
         self._desc: _Descriptors | None = None
         self._pin = _StreamPin("Descriptor updates require one CUDA stream per state")
         self._workspace_pool = workspace_pool
         self._workspace = None
         self.extend(key_blocks, value_blocks)
+
+    @property
+    def key_blocks(self) -> tuple:
+        return self._held_blocks()[0]
+
+    @property
+    def value_blocks(self) -> tuple:
+        return self._held_blocks()[1]
+
+    @property
+    def block_count(self) -> int:
+        """Blocks held (len(key_blocks), without building the tuple)."""
+        return len(self._keys)
+
+    def _held_blocks(self) -> tuple:
+        if self._held is None:
+            self._held = (tuple(self._keys), tuple(self._values))
+        return self._held
 
     # inspected by the reference's tests
     @property
@@ -264,9 +283,9 @@ class PackedDecodeState:
         """Append blocks; the known blocks must be an unchanged prefix (identity)."""
         if len(key_blocks) != len(value_blocks):
             raise ValueError("Key and value block counts must match")
-        have = len(self.key_blocks)
-        prefix_ok = len(key_blocks) >= have and all(map(operator.is_, self.key_blocks, key_blocks)) \
-            and all(map(operator.is_, self.value_blocks, value_blocks))
+        have = len(self._keys)
+        prefix_ok = len(key_blocks) >= have and all(map(operator.is_, self._keys, key_blocks)) \
+            and all(map(operator.is_, self._values, value_blocks))
         if not prefix_ok:
             raise ValueError("PackedDecodeState.extend requires an immutable append-only prefix")
         if len(key_blocks) == have:
@@ -286,7 +305,11 @@ class PackedDecodeState:
         self._format = fmt
         self._desc.reserve(have, len(key_blocks))
         self._desc.write(have, new_keys, new_values, fmt, stream)
-        self.key_blocks, self.value_blocks = tuple(key_blocks), tuple(value_blocks)
+        # only the new blocks are added (the held prefix is identical): no
+        # pass over the whole history beyond the identity check
+        self._keys.extend(new_keys)
+        self._values.extend(new_values)
+        self._held = None
 
     @property
     def nbytes(self) -> int:
@@ -327,7 +350,7 @@ class PackedDecodeState:
         hq = query.shape[1]
         if heads is None or hq % heads:
             raise ValueError("query_heads must be divisible by the nonempty KV head count")
-        n_blocks = len(self.key_blocks)
+        n_blocks = len(self._keys)
         partitions = n_blocks + _ceil_div(sink_t, _SPLIT) + _ceil_div(tail_t, _SPLIT)
         if partitions == 0:
             raise ValueError("Attention requires at least one key/value token")
