@@ -380,7 +380,49 @@ __device__ __forceinline__ void paged_body(const PagedArgs &a, PagedSmem<NPG> &s
     constexpr int OWNERS = NPG >= WAVES ? 1 : WAVES / NPG;
     auto local = [&](int lp) -> int { return NPG >= WAVES ? lp % PPW : 0; };
     *(u32x4 *)(s_q + qg * QROW + qc) = qg < G ? qraw : u32x4{0u, 0u, 0u, 0u};
-    if constexpr (PACKED) {
+    if constexpr (PACKED && NPG >= WAVES) {
+        // Pages of at most 64 tokens: each wavefront owns pages wave * PPW + i
+        // (its constants k = 2 i and 2 i + 1: channels lane and lane + 64) and
+        // resolves their roles alone from the role map, with no workgroup
+        // barrier (the role map gives a source's donor channel directly):
+        // * a source takes the salient row of its rank among the page's
+        //   sources (a ballot), which holds its source and donor bytes for the
+        //   selection matrix and its scale; its pair is (0, 0);
+        // * donor j decodes to its padding through the pair (0, pad_j), pad_j
+        //   read from lane 16 i + j, so Q.K adds q . round(pad) itself;
+        // * every other channel has the pair (s * 2^9, -8 s).
+        // Rows past the page's source count keep bytes 0 and scale 0.
+        if (lane < 16 * PPW) {
+            sm.salw[wave * PPW + (lane >> 4)][lane & 15] = 0u;
+            sm.ssc[wave * PPW + (lane >> 4)][lane & 15] = 0.0f;
+        }
+        wave_lds_sync();
+#pragma unroll
+        for (int i = 0; i < PPW; ++i) {
+            const int lp = wave * PPW + i;
+            const bool src0 = krl[2 * i] >= 0 && krl[2 * i] < D, src1 = krl[2 * i + 1] >= 0 && krl[2 * i + 1] < D;
+            const uint64_t m0 = __ballot(src0), m1 = __ballot(src1);
+            const int rank[2] = {
+                (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(m0 >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m0, 0u)),
+                (int)__popcll(m0) + (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(m1 >> 32),
+                                                              __builtin_amdgcn_mbcnt_lo((uint32_t)m1, 0u))};
+#pragma unroll
+            for (int hf = 0; hf < 2; ++hf) {
+                const int k = 2 * i + hf, c = (hf << 6) + lane, role = krl[k], j = -2 - role;
+                const bool donor = j >= 0 && j < SPG;
+                const float pad = __int_as_float(
+                    __builtin_amdgcn_ds_bpermute(4 * (16 * i + (donor ? j : 0)), __float_as_int(kpad)));
+                const float A = role == -1 ? ksc[k] * inv_unit : 0.0f;
+                const f32x2 pair = {A, role == -1 ? A * -0.015625f : (donor ? pad : 0.0f)};
+                sm.kap(wave)[i * KAP_PAGE + (c >> 5) * KAP_GROUP + (c & 31)] = pair;
+                if (role >= 0 && role < D && rank[hf] < SPG) {
+                    sm.salw[lp][rank[hf]] = (uint32_t)(c >> 1) | ((uint32_t)((c & 1) * 4) << 8) |
+                                            ((uint32_t)(role >> 1) << 16) | ((uint32_t)((role & 1) * 4) << 24);
+                    sm.ssc[lp][rank[hf]] = ksc[k];
+                }
+            }
+        }
+    } else if constexpr (PACKED) {
         if (cvalid) {
 #pragma unroll
             for (int k = 0; k < CPT; ++k) {
@@ -496,7 +538,8 @@ __device__ __forceinline__ void paged_body(const PagedArgs &a, PagedSmem<NPG> &s
             for (int j = 0; j < 4; ++j) {
                 const int lpl = NPG >= WAVES ? (16 * j) / B : 0;   // the tile's page among the wavefront's
                 asm volatile("" ::: "memory");
-                const float bias = wbias[lpl * 16 + gl];
+                // the donor padding: in the K pairs for short pages, a bias otherwise
+                const float bias = NPG >= WAVES ? 0.0f : wbias[lpl * 16 + gl];
                 f32x4 s = {bias, bias, bias, bias};
 #pragma unroll
                 for (int d = 0; d < 4; ++d) {
