@@ -19,10 +19,11 @@
 // front, Q.K runs on matrix cores with the K tile decoded exactly in
 // registers, salient codes are gathered into an extra 16x16x16 MFMA, the
 // online softmax runs in the log2 domain and P.V uses hi + lo weights.  Pages
-// shorter than a partition get their own per-channel constants: the
-// salient/donor channels of a page decode to zero through a zero scale
-// (instead of a masked query), and the donor padding enters as a per-page
-// bias on the logits.
+// shorter than a partition get their own per-channel constants, resolved
+// from each page's role map as the reference decodes it: salient sources
+// decode to zero in the 4-bit pass and take their 8-bit codes from the
+// salient product, and a donor decodes to its padding through its constant
+// pair.
 #include "decode_common.h"
 
 namespace {
@@ -224,38 +225,28 @@ __device__ __forceinline__ int page_of_wave(int npg, int wave)
 }
 
 // Workgroup LDS of decode_paged, shared by its packed and dense bodies.
-// Each wavefront's slot of v (SLOT bytes) holds in turn: the (s * 2^9, -8 s)
-// K constant pairs of its pages [0, SETUP_OFF) and their donor bias
-// [BIAS_OFF, SLOT) up to Q.K; then the salient selection matrix of one page
-// at a time; then its decoded V tiles and its combine rows (the whole
-// slot).  Until the per-page tables are built, [SETUP_OFF, BIAS_OFF) of
-// slots 0 and 1 hold the role-resolution arrays of every page.  At 16-token
-// pages a workgroup takes 40,704 bytes: four per compute unit.
+// Each wavefront's slot of v (SLOT bytes) holds in turn: the K constant
+// pairs of its pages [0, KAP_BYTES) up to Q.K; then the salient selection
+// matrix of one page at a time; then its decoded V tiles and its combine
+// rows (the whole slot).  At 16-token pages a workgroup takes 40,704 bytes:
+// four per compute unit.
 constexpr int SLOT = 16 * VR * 4;          // bytes per wavefront slot
 constexpr int KAP_GROUP = 34;              // pairs per 32-channel group (+2: the four groups on distinct banks)
 constexpr int KAP_PAGE = 4 * KAP_GROUP;    // pairs per page
-constexpr int SETUP_OFF = 4 * KAP_PAGE * 8;   // bytes: past the constant pairs of four pages
-constexpr int BIAS_OFF = SLOT - 4 * 16 * 4;
-static_assert(16 * SELROW <= SETUP_OFF, "a page's selection matrix fits below the setup arrays");
+constexpr int KAP_BYTES = 4 * KAP_PAGE * 8;   // the constant pairs of up to four pages
+static_assert(KAP_BYTES <= SLOT, "the constant pairs fit in a wavefront's slot");
+static_assert(16 * SELROW <= SLOT, "a page's selection matrix fits in a wavefront's slot");
 
 template <int NPG>
 struct __attribute__((aligned(16))) PagedSmem {
     uint32_t v[WAVES][16 * VR];        // per-wavefront slots (above)
     uint16_t q[16 * QROW];
-    uint32_t salw[NPG][SPG];           // gather offsets per page
-    float ssc[NPG][SPG];               // scale of the source of descriptor k
+    uint32_t salw[NPG][SPG];           // salient row r of a page: source and donor bytes
+    float ssc[NPG][SPG];               // salient row r of a page: the source's scale
+    int nsrc[WAVES];                   // sources among a wavefront's channels (pages shared by two wavefronts)
     float wm[WAVES][16], wl[WAVES][16];
 
     __device__ f32x2 *kap(int w) { return (f32x2 *)&v[w][0]; }                          // [page of w][4][KAP_GROUP]
-    __device__ float *bias(int w) { return (float *)((char *)&v[w][0] + BIAS_OFF); }    // [page of w][16]
-    __device__ int8_t *role() { return (int8_t *)((char *)&v[0][0] + SETUP_OFF); }     // [NPG][D]
-    __device__ float *padraw() { return (float *)((char *)&v[1][0] + SETUP_OFF); }     // [NPG][SPG]
-    __device__ float *spad() { return padraw() + NPG * SPG; }                           // round(pad) of descriptor k
-    __device__ float *sssc() { return spad() + NPG * SPG; }                             // source scale of descriptor k
-    __device__ int8_t *ssrc() { return (int8_t *)(sssc() + NPG * SPG); }                // source channel of descriptor k
-    __device__ int8_t *sdon() { return ssrc() + NPG * SPG; }                            // donor channel of descriptor k
-    static_assert(NPG * D <= BIAS_OFF - SETUP_OFF, "role map fits in slot 0");
-    static_assert(NPG * SPG * (3 * 4 + 2) <= BIAS_OFF - SETUP_OFF, "descriptor arrays fit in slot 1");
 };
 
 // One partition of one sequence.  The packed and the dense body are separate
@@ -380,126 +371,64 @@ __device__ __forceinline__ void paged_body(const PagedArgs &a, PagedSmem<NPG> &s
     constexpr int OWNERS = NPG >= WAVES ? 1 : WAVES / NPG;
     auto local = [&](int lp) -> int { return NPG >= WAVES ? lp % PPW : 0; };
     *(u32x4 *)(s_q + qg * QROW + qc) = qg < G ? qraw : u32x4{0u, 0u, 0u, 0u};
-    if constexpr (PACKED && NPG >= WAVES) {
-        // Pages of at most 64 tokens: each wavefront owns pages wave * PPW + i
-        // (its constants k = 2 i and 2 i + 1: channels lane and lane + 64) and
-        // resolves their roles alone from the role map, with no workgroup
-        // barrier (the role map gives a source's donor channel directly):
-        // * a source takes the salient row of its rank among the page's
-        //   sources (a ballot), which holds its source and donor bytes for the
-        //   selection matrix and its scale; its pair is (0, 0);
-        // * donor j decodes to its padding through the pair (0, pad_j), pad_j
-        //   read from lane 16 i + j, so Q.K adds q . round(pad) itself;
-        // * every other channel has the pair (s * 2^9, -8 s).
-        // Rows past the page's source count keep bytes 0 and scale 0.
-        if (lane < 16 * PPW) {
-            sm.salw[wave * PPW + (lane >> 4)][lane & 15] = 0u;
-            sm.ssc[wave * PPW + (lane >> 4)][lane & 15] = 0.0f;
-        }
-        wave_lds_sync();
+    if constexpr (PACKED) {
+        // Roles come from the page's role map, as the reference decodes a
+        // page (role >= 0: a source, whose donor is channel `role`; role
+        // <= -2: donor -2 - role; -1: a normal channel), with no descriptor
+        // lists:
+        // * a normal channel gets the pair (s * 2^9, -8 s);
+        // * a source gets (0, 0) and takes the salient row of its rank among
+        //   the page's sources in channel order (ballots), where it records
+        //   its own and its donor's byte for the selection matrix and its
+        //   scale; rows past the page's source count keep bytes 0, scale 0;
+        // * donor j gets (0, pad_j), pad_j read from the lane that loaded it,
+        //   so Q.K itself adds q . round(pad_j).
+        // Pages of at most 64 tokens belong to one wavefront each, which
+        // resolves them alone; a longer page is shared by two wavefronts
+        // (channels 0-63 and 64-127), the second adding the first's source
+        // count to its ranks.
+        uint64_t msk[CPT];
 #pragma unroll
-        for (int i = 0; i < PPW; ++i) {
-            const int lp = wave * PPW + i;
-            const bool src0 = krl[2 * i] >= 0 && krl[2 * i] < D, src1 = krl[2 * i + 1] >= 0 && krl[2 * i + 1] < D;
-            const uint64_t m0 = __ballot(src0), m1 = __ballot(src1);
-            const int rank[2] = {
-                (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(m0 >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m0, 0u)),
-                (int)__popcll(m0) + (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(m1 >> 32),
-                                                              __builtin_amdgcn_mbcnt_lo((uint32_t)m1, 0u))};
-#pragma unroll
-            for (int hf = 0; hf < 2; ++hf) {
-                const int k = 2 * i + hf, c = (hf << 6) + lane, role = krl[k], j = -2 - role;
-                const bool donor = j >= 0 && j < SPG;
-                const float pad = __int_as_float(
-                    __builtin_amdgcn_ds_bpermute(4 * (16 * i + (donor ? j : 0)), __float_as_int(kpad)));
-                const float A = role == -1 ? ksc[k] * inv_unit : 0.0f;
-                const f32x2 pair = {A, role == -1 ? A * -0.015625f : (donor ? pad : 0.0f)};
-                sm.kap(wave)[i * KAP_PAGE + (c >> 5) * KAP_GROUP + (c & 31)] = pair;
-                if (role >= 0 && role < D && rank[hf] < SPG) {
-                    sm.salw[lp][rank[hf]] = (uint32_t)(c >> 1) | ((uint32_t)((c & 1) * 4) << 8) |
-                                            ((uint32_t)(role >> 1) << 16) | ((uint32_t)((role & 1) * 4) << 24);
-                    sm.ssc[lp][rank[hf]] = ksc[k];
-                }
+        for (int k = 0; k < CPT; ++k) msk[k] = __ballot(cvalid && krl[k] >= 0 && krl[k] < D);
+        if constexpr (NPG >= WAVES) {
+            if (lane < 16 * PPW) {
+                sm.salw[wave * PPW + (lane >> 4)][lane & 15] = 0u;
+                sm.ssc[wave * PPW + (lane >> 4)][lane & 15] = 0.0f;
             }
+            wave_lds_sync();
+        } else {
+            if (tid < NPG * SPG) {
+                sm.salw[tid / SPG][tid % SPG] = 0u;
+                sm.ssc[tid / SPG][tid % SPG] = 0.0f;
+            }
+            if (lane == 0) sm.nsrc[wave] = (int)__popcll(msk[0]);
+            __syncthreads();
         }
-    } else if constexpr (PACKED) {
         if (cvalid) {
 #pragma unroll
             for (int k = 0; k < CPT; ++k) {
-                const int lp = cpart(k), c = cchan(k);
-                // zero at salient and donor channels: they decode to 0
-                const float A = krl[k] == -1 ? ksc[k] * inv_unit : 0.0f;
-                const f32x2 pair = {A, A * -0.015625f};         // (s * 2^9, -8 s), both exact
+                const int lp = cpart(k), c = cchan(k), role = krl[k], j = -2 - role;
+                int rank = (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(msk[k] >> 32),
+                                                          __builtin_amdgcn_mbcnt_lo((uint32_t)msk[k], 0u));
+                if constexpr (NPG >= WAVES) {
+                    if (k & 1) rank += (int)__popcll(msk[k - 1]);
+                } else if (wave & 1) {
+                    rank += sm.nsrc[wave - 1];
+                }
+                const bool donor = j >= 0 && j < SPG;
+                const int pad_lane = (NPG >= WAVES ? 16 * cpage(k) : 0) + (donor ? j : 0);
+                const float pad = __int_as_float(__builtin_amdgcn_ds_bpermute(4 * pad_lane, __float_as_int(kpad)));
+                const float A = role == -1 ? ksc[k] * inv_unit : 0.0f;
+                const f32x2 pair = {A, role == -1 ? A * -0.015625f : (donor ? pad : 0.0f)};   // (s * 2^9, -8 s) exact
 #pragma unroll
                 for (int o = 0; o < OWNERS; ++o)
                     sm.kap(owner0(lp) + o)[local(lp) * KAP_PAGE + (c >> 5) * KAP_GROUP + (c & 31)] = pair;
-                sm.role()[lp * D + c] = (int8_t)krl[k];
-            }
-        }
-        if (NPG >= WAVES ? lane < 16 * PPW : lane < 16) {
-            const int lp = NPG >= WAVES ? wave * PPW + (lane >> 4) : wave * NPG / WAVES, j = lane & 15;
-            sm.padraw()[lp * SPG + j] = kpad;
-            sm.ssrc()[lp * SPG + j] = 0;
-            sm.sdon()[lp * SPG + j] = 0;
-            sm.sssc()[lp * SPG + j] = 0.0f;
-            sm.spad()[lp * SPG + j] = 0.0f;
-        }
-        __syncthreads();
-        // a source's descriptor index is -2 - key_map[its donor]; a donor's is
-        // -2 - key_map.  Every read first, unconditionally (a source's donor
-        // role, a donor's raw padding; other channels read entry 0), so the
-        // eight items cost one LDS round trip instead of one each behind
-        // their branches (config 4: 71.0 -> 68.3 us per layer with the bias below)
-        if (cvalid) {
-            int rdon[CPT];
-            float praw[CPT];
-#pragma unroll
-            for (int k = 0; k < CPT; ++k) {
-                const int lp = cpart(k), role = krl[k];
-                rdon[k] = sm.role()[lp * D + (role >= 0 && role < D ? role : 0)];
-                const int jd = -2 - role;
-                praw[k] = sm.padraw()[lp * SPG + (jd >= 0 && jd < SPG ? jd : 0)];
-            }
-#pragma unroll
-            for (int k = 0; k < CPT; ++k) {
-                const int lp = cpart(k), c = cchan(k), role = krl[k];
-                if (role >= 0 && role < D) {
-                    const int j = -2 - rdon[k];
-                    if (j >= 0 && j < SPG) {
-                        sm.ssrc()[lp * SPG + j] = (int8_t)c;
-                        sm.sssc()[lp * SPG + j] = ksc[k];
-                    }
-                } else if (role <= -2 && role >= -2 - (SPG - 1)) {
-                    const int j = -2 - role;
-                    sm.sdon()[lp * SPG + j] = (int8_t)c;
-                    sm.spad()[lp * SPG + j] = round_q<false>(praw[k]);
+                if (role >= 0 && role < D && rank < SPG) {
+                    sm.salw[lp][rank] = (uint32_t)(c >> 1) | ((uint32_t)((c & 1) * 4) << 8) |
+                                        ((uint32_t)(role >> 1) << 16) | ((uint32_t)((role & 1) * 4) << 24);
+                    sm.ssc[lp][rank] = ksc[k];
                 }
             }
-        }
-        __syncthreads();
-        // per-page salient tables, and the donor bias of each page in its owners' slots
-        for (int i = tid; i < NPG * SPG; i += 256) {
-            const int lp = i / SPG, k = i % SPG;
-            const uint32_t src = (uint8_t)sm.ssrc()[i], don = (uint8_t)sm.sdon()[i];
-            sm.salw[lp][k] = (src >> 1) | (((src & 1) * 4) << 8) | ((don >> 1) << 16) | (((don & 1) * 4) << 24);
-            sm.ssc[lp][k] = sm.sssc()[i];
-        }
-        for (int i = tid; i < NPG * 16; i += 256) {
-            const int lp = i >> 4, g = i & 15;
-            // the page's 16 donors and paddings as vector reads, then the 16
-            // query gathers together, then the sum in descriptor order
-            const u32x4 dn = *(const u32x4 *)(sm.sdon() + lp * SPG);
-            f32x4 pd[SPG / 4];
-#pragma unroll
-            for (int e = 0; e < SPG / 4; ++e) pd[e] = *(const f32x4 *)(sm.spad() + lp * SPG + 4 * e);
-            uint32_t qv[SPG];
-#pragma unroll
-            for (int k = 0; k < SPG; ++k) qv[k] = s_q[g * QROW + ((dn[k >> 2] >> (8 * (k & 3))) & 0xffu)];
-            float b = 0.0f;
-#pragma unroll
-            for (int k = 0; k < SPG; ++k) b = fmaf(to_f32<false>(qv[k]), pd[k >> 2][k & 3], b);
-#pragma unroll
-            for (int o = 0; o < OWNERS; ++o) sm.bias(owner0(lp) + o)[local(lp) * 16 + g] = b;
         }
     }
     __syncthreads();
@@ -533,14 +462,11 @@ __device__ __forceinline__ void paged_body(const PagedArgs &a, PagedSmem<NPG> &s
         f32x4 sc[4];
         if constexpr (PACKED) {
             const f32x2 *kap = sm.kap(wave);
-            const float *wbias = sm.bias(wave);
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
                 const int lpl = NPG >= WAVES ? (16 * j) / B : 0;   // the tile's page among the wavefront's
                 asm volatile("" ::: "memory");
-                // the donor padding: in the K pairs for short pages, a bias otherwise
-                const float bias = NPG >= WAVES ? 0.0f : wbias[lpl * 16 + gl];
-                f32x4 s = {bias, bias, bias, bias};
+                f32x4 s = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
                 for (int d = 0; d < 4; ++d) {
                     const f32x2 *cp = kap + lpl * KAP_PAGE + ql * KAP_GROUP + 8 * d;

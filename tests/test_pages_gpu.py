@@ -170,6 +170,42 @@ def test_paged_decode_random_page_order_and_reuse(block, pages, tail):
         assert np.abs(_np(out32)[0] - exp).max() <= ATOL
 
 
+@pytest.mark.parametrize("block", [16, 64, 128, 256])
+def test_paged_decode_reads_roles_as_the_role_map_states(block):
+    # The decode takes every role from the page's int16 role map, as the
+    # reference's _decode_tile does (kernels.py:34-35): role >= 0 is a source
+    # whose low nibble comes from channel `role`, role <= -2 is donor
+    # -2 - role (its padding), -1 a plain 4-bit channel.  Edited maps, decoded
+    # by the oracle from the same bytes: a page with a source/donor pair made
+    # plain (15 sources), a source whose partner is a plain channel, two
+    # donors sharing one padding, a page with no salient channels at all.
+    from inquant.triton_attention import SharedDecodeWorkspace
+    from inquant_vllm import paged_decode
+    pages, tail = 6, 5
+    layout, pool, ids, dense, sink, q = _paged_case(97, block, pages, tail)
+    roles = layout.views(pool)["key_map"]                       # [pool pages, H, 128] views of the pool
+    pid = [int(i) for i in ids.tolist()]
+    r = roles[pid[0], 0]
+    s0 = int(torch.nonzero(r >= 0)[0])
+    d0 = int(r[s0])
+    r[s0], r[d0] = -1, -1                                       # a pair made plain
+    r = roles[pid[1], 1]
+    s1 = int(torch.nonzero(r >= 0)[0])
+    plain = int(torch.nonzero(r == -1)[0])
+    r[s1] = plain                                               # partner: a plain channel
+    r = roles[pid[2], 2]
+    donors = torch.nonzero(r <= -2).flatten()
+    r[int(donors[0])] = r[int(donors[1])]                       # two donors, one padding
+    roles[pid[3], 3] = -1                                       # no salient channels
+    out32 = torch.empty(q.shape, dtype=torch.float32, device="cuda")
+    paged_decode(q, pool, ids, dense, pages, tail, sink, layout, SharedDecodeWorkspace(), 128 ** -0.5, out32)
+    exp = _expected(layout, pool, ids, dense, pages, tail, sink, q)
+    assert np.abs(_np(out32)[0] - exp).max() <= ATOL
+    # the edits change the attended keys: the unedited pool decodes differently
+    _, pool0, _, _, _, _ = _paged_case(97, block, pages, tail)
+    assert np.abs(_expected(layout, pool0, ids, dense, pages, tail, sink, q) - exp).max() > 1e-4
+
+
 @pytest.mark.parametrize("h,hq", [(4, 4), (2, 32)])
 def test_paged_decode_query_group_sizes(h, hq):
     # one query row per KV head, and the 16 a matrix-core tile holds
