@@ -774,9 +774,10 @@ __device__ __forceinline__ void fast_body(const FastArgs &a, FastSmem &sm)
 }
 
 // K4-coded values keep twice the value payload and their own selection
-// operands in registers: three workgroups per compute unit instead of four.
+// operands in registers: with fp16 queries three workgroups per compute
+// unit instead of four (four would spill); bf16 fits four.
 template <bool F16, int VBITS>
-__global__ __launch_bounds__(256, VBITS == 0 ? 3 : 4) void decode_fast(FastArgs a)
+__global__ __launch_bounds__(256, VBITS == 0 && F16 ? 3 : 4) void decode_fast(FastArgs a)
 {
     __shared__ FastSmem sm;
     if (partition_of(a, blockIdx.y) < a.nblk) fast_body<F16, VBITS, true>(a, sm);
