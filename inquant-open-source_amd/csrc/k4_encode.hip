@@ -266,7 +266,7 @@ __device__ __forceinline__ float tile_f32(uint32_t bits16)
 // srcc[e] is the channel whose value slot e encodes: its own, or for a donor
 // slot its source's.
 struct K4Slots {
-    float scl[8], rscl[8], lim[8], bias[8];
+    float scl[8], rscl[8], top[8], bias[8];
     uint32_t shift[8];
     int srcc[8];
 
@@ -281,44 +281,50 @@ struct K4Slots {
             srcc[e] = lo ? owner : c;
             scl[e] = scale[srcc[e]];
             rscl[e] = __builtin_amdgcn_rcpf(scl[e]);
-            lim[e] = (hi || lo) ? 127.0f : 7.0f;
-            // q + lim + 1 lands in the low mantissa bits of 1.5 * 2^23 + (lim + 1)
-            bias[e] = 12582912.0f + lim[e] + 1.0f;
+            const float lim = (hi || lo) ? 127.0f : 7.0f;
+            // q + lim + 1 lands in the low mantissa bits of 1.5 * 2^23 + (lim + 1);
+            // the clamp to [-lim, lim] is then [1.5 * 2^23 + 1, top]
+            bias[e] = 12582912.0f + lim + 1.0f;
+            top[e] = bias[e] + lim;
             shift[e] = hi ? 4u : 0u;
-            asm volatile("" : "+v"(scl[e]), "+v"(rscl[e]), "+v"(lim[e]), "+v"(bias[e]), "+v"(shift[e]));
+            asm volatile("" : "+v"(scl[e]), "+v"(rscl[e]), "+v"(top[e]), "+v"(bias[e]), "+v"(shift[e]));
         }
     }
 
     // The packed word of one token, v[e] the value of channel srcc[e].  The
-    // reciprocal quotient f decides the rounding unless it is within 2^-13
-    // of a half-integer, where the IEEE quotient decides.  Below |f| = 256,
-    // f is within 2^-14 of the IEEE quotient (v_rcp_f32 is within 1 ulp,
-    // plus the product's rounding, plus the quotient's own half ulp), so no
-    // rounding can differ outside that band; beyond it every code clamps to
-    // +-lim either way.  The band test is one max over the lane's eight
-    // distances; the rare lanes inside it redo only the slots that are.
+    // reciprocal quotient p = v * rscl decides the rounding unless it is
+    // within 2^-13 of a half-integer, where the IEEE quotient decides.  Below
+    // |p| = 256, p is within 2^-14 of the IEEE quotient (v_rcp_f32 is within
+    // 1 ulp, plus the quotient's own half ulp), so no rounding can differ
+    // outside that band; beyond it every code clamps to +-lim either way.
+    // One fma rounds p onto the integer grid of bias = 1.5 * 2^23 + lim + 1
+    // (spacing 1 there): y = bias + rint(p) exactly, whose low mantissa bits
+    // are the code plus lim + 1 once y is clamped to bias +- lim.  A second
+    // fma gives p - rint(p) with one rounding for the band test, one max
+    // over the lane's eight distances; the rare lanes inside it redo only
+    // the slots that are.
     __device__ __forceinline__ uint32_t word(const float (&v)[8]) const
     {
-        float f[8], q[8];
+        float y[8], q[8];
         float dmax = 0.0f;
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
-            f[e] = __fmul_rn(v[e], rscl[e]);
-            q[e] = rintf(f[e]);
-            dmax = fmaxf(dmax, fabsf(__fsub_rn(f[e], q[e])));
+            y[e] = __builtin_fmaf(v[e], rscl[e], bias[e]);
+            q[e] = __fsub_rn(y[e], bias[e]);                 // rint(p), exact
+            dmax = fmaxf(dmax, fabsf(__builtin_fmaf(v[e], rscl[e], -q[e])));
         }
         constexpr float band = 0.5f - 0x1p-13f;
         if (__builtin_expect(dmax >= band, 0)) {
 #pragma unroll
             for (int e = 0; e < 8; ++e)
-                if (fabsf(__fsub_rn(f[e], q[e])) >= band) q[e] = rintf(v[e] / scl[e]);
+                if (fabsf(__builtin_fmaf(v[e], rscl[e], -q[e])) >= band)
+                    y[e] = __fadd_rn(rintf(v[e] / scl[e]), bias[e]);
         }
         uint32_t w = 0;
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
-            const float qc = __builtin_amdgcn_fmed3f(q[e], -lim[e], lim[e]);
-            const uint32_t code = __float_as_uint(__fadd_rn(qc, bias[e]));
-            w |= __builtin_amdgcn_ubfe(code, shift[e], 4) << (4 * e);
+            const float yc = __builtin_amdgcn_fmed3f(y[e], 12582913.0f, top[e]);
+            w |= __builtin_amdgcn_ubfe(__float_as_uint(yc), shift[e], 4) << (4 * e);
         }
         return w;
     }
