@@ -329,7 +329,10 @@ __global__ __launch_bounds__(V_THREADS) void v_decode_rows(VDecArgs a)
 // j < 16, decodes channels 8 j .. 8 j + 7 of a token from one payload word;
 // a source channel's low nibble comes from the donor's word, read from the
 // lane of the token that holds it.  Same arithmetic as k4_decode_kernel.
+// The thread's KD_ITER payload words are loaded first, before the role
+// tables are built, so one memory round trip covers them all.
 constexpr int KD_TOKENS = 128;
+constexpr int KD_ITER = KD_TOKENS / (V_THREADS / 16);   // tokens per thread
 
 template <int OUT>
 __global__ __launch_bounds__(V_THREADS) void k4_decode_rows(KDecArgs a)
@@ -338,6 +341,15 @@ __global__ __launch_bounds__(V_THREADS) void k4_decode_rows(KDecArgs a)
     __shared__ int16_t s_role[128];
     const int tid = threadIdx.x, lane = tid & 63;
     const int64_t row = blockIdx.y;
+    const int j = tid & 15;
+    const int64_t t_first = (int64_t)blockIdx.x * KD_TOKENS + (tid >> 4);
+    uint32_t words[KD_ITER];
+#pragma unroll
+    for (int i = 0; i < KD_ITER; ++i) {
+        const int64_t t = t_first + i * (V_THREADS / 16);
+        const int64_t rt = row * a.T + (t < a.T ? t : a.T - 1);   // every lane loads (the shuffles need all)
+        words[i] = *(const uint32_t *)(a.payload + rt * 64 + 4 * j);
+    }
     if (tid < 128) {
         s_scale[tid] = a.scales[row * 128 + tid];
         s_role[tid] = -1;
@@ -353,36 +365,50 @@ __global__ __launch_bounds__(V_THREADS) void k4_decode_rows(KDecArgs a)
         s_pad[tid] = a.padding[row * a.count + tid];
     }
     __syncthreads();
-    const int j = tid & 15;
-    int role[8];
-    float scl[8];
+    // per slot e of this lane (channel 8 j + e), fixed across tokens: the
+    // code is (slot << sh) + lo - off, lo the donor's nibble for a source
+    // (sh = 4, off = 128) and 0 otherwise (sh = 0, off = 8; a zero-width
+    // field extract); a donor takes its padding instead
+    int sh[8], off[8], lo_at[8], lo_w[8], bp[8];
+    bool don[8], xl[8];
+    float scl[8], pad[8];
+    uint64_t cross[8];     // lanes whose slot e is a source with its donor in another word
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-        role[e] = s_role[8 * j + e];
+        const int rl = s_role[8 * j + e];
+        const bool src = rl >= 0;
         scl[e] = s_scale[8 * j + e];
+        don[e] = rl <= -2;
+        pad[e] = s_pad[don[e] ? -rl - 2 : 0];
+        sh[e] = src ? 4 : 0;
+        off[e] = src ? 128 : 8;
+        lo_w[e] = src ? 4 : 0;
+        lo_at[e] = src ? 4 * (rl & 7) : 0;
+        xl[e] = src && (rl >> 3) != j;
+        cross[e] = __ballot(xl[e]);
+        bp[e] = 4 * ((lane & ~15) | ((rl >> 3) & 15));       // ds_bpermute address of word rl / 8
     }
-    const int64_t t_first = (int64_t)blockIdx.x * KD_TOKENS;
-#pragma unroll 1
-    for (int tt = tid >> 4; tt < KD_TOKENS; tt += V_THREADS / 16) {
-        const int64_t t = t_first + tt;
+#pragma unroll
+    for (int i = 0; i < KD_ITER; ++i) {
+        const int64_t t = t_first + i * (V_THREADS / 16);
         const bool live = t < a.T;
-        const int64_t rt = row * a.T + (live ? t : a.T - 1);   // every lane loads (the shuffles need all)
-        const uint32_t w = *(const uint32_t *)(a.payload + rt * 64 + 4 * j);
+        const int64_t rt = row * a.T + (live ? t : a.T - 1);
+        const uint32_t w = words[i];
         float v[8];
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
-            const int rl = role[e];
-            const int slot = (int)((w >> (4 * e)) & 15u);
-            // the donor's payload word: word rl / 8 of this token's row, held by lane (lane & ~15) + rl / 8
-            const uint32_t wd = (uint32_t)__shfl((int)w, (lane & ~15) | ((rl >> 3) & 15), 64);
-            if (rl >= 0) {
-                const int lo = (int)((wd >> (4 * (rl & 7))) & 15u);
-                v[e] = __fmul_rn((float)(((slot << 4) | lo) - 128), scl[e]);
-            } else if (rl <= -2) {
-                v[e] = s_pad[-rl - 2];
-            } else {
-                v[e] = __fmul_rn((float)(slot - 8), scl[e]);
+            // a source's low nibble: in this lane's word, or in word rl / 8 of
+            // the token's row, held by another lane of its 16 (fetched only
+            // where some lane of the wavefront needs it)
+            uint32_t wd = w;
+            if (cross[e]) {
+                const uint32_t x = (uint32_t)__builtin_amdgcn_ds_bpermute(bp[e], (int)w);
+                wd = xl[e] ? x : w;
             }
+            const int slot = (int)__builtin_amdgcn_ubfe(w, 4 * e, 4);
+            const int lo = (int)__builtin_amdgcn_ubfe(wd, lo_at[e], lo_w[e]);
+            const int code = (slot << sh[e]) + lo - off[e];
+            v[e] = don[e] ? pad[e] : __fmul_rn((float)code, scl[e]);
         }
         if (!live) continue;
         if constexpr (OUT == IQ_F32) {
