@@ -282,6 +282,20 @@ __global__ __launch_bounds__(V_THREADS) void k4_decode_kernel(KDecArgs a)
     }
 }
 
+// Two values rounded to the 16-bit output dtype (nearest even), first in
+// the low half: one conversion instruction for the pair.
+template <int OUT>
+__device__ __forceinline__ uint32_t pack_pair(float x, float y)
+{
+    if constexpr (OUT == IQ_BF16) {
+        typedef __attribute__((ext_vector_type(2))) __bf16 pair_t;
+        return __builtin_bit_cast(uint32_t, pair_t{(__bf16)x, (__bf16)y});
+    } else {
+        typedef __attribute__((ext_vector_type(2))) _Float16 pair_t;
+        return __builtin_bit_cast(uint32_t, pair_t{(_Float16)x, (_Float16)y});
+    }
+}
+
 // Rows of 128 channels, 16-byte aligned output rows.  Thread (row, j)
 // decodes channels 16 j .. 16 j + 15 of one row: BITS / 2 payload words and
 // its group's f16 scale and offset, then writes 16 values with 16-byte
@@ -312,11 +326,7 @@ __global__ __launch_bounds__(V_THREADS) void v_decode_rows(VDecArgs a)
     } else {
         uint32_t h[8];
 #pragma unroll
-        for (int k = 0; k < 8; ++k) {
-            const uint32_t lo = OUT == IQ_BF16 ? iq_f32_to_bf16(v[2 * k]) : iq_f32_to_f16(v[2 * k]);
-            const uint32_t hi = OUT == IQ_BF16 ? iq_f32_to_bf16(v[2 * k + 1]) : iq_f32_to_f16(v[2 * k + 1]);
-            h[k] = lo | (hi << 16);
-        }
+        for (int k = 0; k < 8; ++k) h[k] = pack_pair<OUT>(v[2 * k], v[2 * k + 1]);
         uint4 *o = (uint4 *)((uint16_t *)a.out + r * 128 + 16 * j);
         o[0] = uint4{h[0], h[1], h[2], h[3]};
         o[1] = uint4{h[4], h[5], h[6], h[7]};
@@ -366,26 +376,27 @@ __global__ __launch_bounds__(V_THREADS) void k4_decode_rows(KDecArgs a)
     }
     __syncthreads();
     // per slot e of this lane (channel 8 j + e), fixed across tokens: the
-    // code is (slot << sh) + lo - off, lo the donor's nibble for a source
-    // (sh = 4, off = 128) and 0 otherwise (sh = 0, off = 8; a zero-width
-    // field extract); a donor takes its padding instead
-    int sh[8], off[8], lo_at[8], lo_w[8], bp[8];
-    bool don[8], xl[8];
-    float scl[8], pad[8];
-    uint64_t cross[8];     // lanes whose slot e is a source with its donor in another word
+    // value is code * f with code = slot * m + lo - off: a plain channel has
+    // m = 1, off = 8, f its scale; a source m = 16, off = 128, f its scale
+    // and lo its donor's nibble; a donor m = 0, off = -1 (code 1) and f its
+    // padding, so every slot is one product and no lane branches.  lo is a
+    // zero-width field extract except at a source; a donor outside this
+    // lane's word comes from the lane of its 16 that holds it (the eight
+    // cross-lane reads of a token are issued together)
+    uint32_t m[8], lo_at[8], lo_w[8];
+    int off[8], bp[8];
+    bool xl[8];
+    float f[8];
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
         const int rl = s_role[8 * j + e];
-        const bool src = rl >= 0;
-        scl[e] = s_scale[8 * j + e];
-        don[e] = rl <= -2;
-        pad[e] = s_pad[don[e] ? -rl - 2 : 0];
-        sh[e] = src ? 4 : 0;
-        off[e] = src ? 128 : 8;
-        lo_w[e] = src ? 4 : 0;
-        lo_at[e] = src ? 4 * (rl & 7) : 0;
+        const bool src = rl >= 0, don = rl <= -2;
+        f[e] = don ? s_pad[-rl - 2] : s_scale[8 * j + e];
+        m[e] = src ? 16u : don ? 0u : 1u;
+        off[e] = src ? 128 : don ? -1 : 8;
+        lo_w[e] = src ? 4u : 0u;
+        lo_at[e] = src ? 4u * (uint32_t)(rl & 7) : 0u;
         xl[e] = src && (rl >> 3) != j;
-        cross[e] = __ballot(xl[e]);
         bp[e] = 4 * ((lane & ~15) | ((rl >> 3) & 15));       // ds_bpermute address of word rl / 8
     }
 #pragma unroll
@@ -394,21 +405,17 @@ __global__ __launch_bounds__(V_THREADS) void k4_decode_rows(KDecArgs a)
         const bool live = t < a.T;
         const int64_t rt = row * a.T + (live ? t : a.T - 1);
         const uint32_t w = words[i];
+        uint32_t x[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) x[e] = (uint32_t)__builtin_amdgcn_ds_bpermute(bp[e], (int)w);
         float v[8];
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
-            // a source's low nibble: in this lane's word, or in word rl / 8 of
-            // the token's row, held by another lane of its 16 (fetched only
-            // where some lane of the wavefront needs it)
-            uint32_t wd = w;
-            if (cross[e]) {
-                const uint32_t x = (uint32_t)__builtin_amdgcn_ds_bpermute(bp[e], (int)w);
-                wd = xl[e] ? x : w;
-            }
-            const int slot = (int)__builtin_amdgcn_ubfe(w, 4 * e, 4);
-            const int lo = (int)__builtin_amdgcn_ubfe(wd, lo_at[e], lo_w[e]);
-            const int code = (slot << sh[e]) + lo - off[e];
-            v[e] = don[e] ? pad[e] : __fmul_rn((float)code, scl[e]);
+            const uint32_t wd = xl[e] ? x[e] : w;
+            const uint32_t slot = __builtin_amdgcn_ubfe(w, 4 * e, 4);
+            const uint32_t lo = __builtin_amdgcn_ubfe(wd, lo_at[e], lo_w[e]);
+            const int code = (int)(__umul24(slot, m[e]) + lo) - off[e];
+            v[e] = __fmul_rn((float)code, f[e]);
         }
         if (!live) continue;
         if constexpr (OUT == IQ_F32) {
@@ -418,11 +425,7 @@ __global__ __launch_bounds__(V_THREADS) void k4_decode_rows(KDecArgs a)
         } else {
             uint32_t h[4];
 #pragma unroll
-            for (int k = 0; k < 4; ++k) {
-                const uint32_t lo = OUT == IQ_BF16 ? iq_f32_to_bf16(v[2 * k]) : iq_f32_to_f16(v[2 * k]);
-                const uint32_t hi = OUT == IQ_BF16 ? iq_f32_to_bf16(v[2 * k + 1]) : iq_f32_to_f16(v[2 * k + 1]);
-                h[k] = lo | (hi << 16);
-            }
+            for (int k = 0; k < 4; ++k) h[k] = pack_pair<OUT>(v[2 * k], v[2 * k + 1]);
             *(uint4 *)((uint16_t *)a.out + rt * 128 + 8 * j) = uint4{h[0], h[1], h[2], h[3]};
         }
     }
