@@ -282,6 +282,8 @@ __global__ __launch_bounds__(V_THREADS) void k4_decode_kernel(KDecArgs a)
     }
 }
 
+typedef __attribute__((ext_vector_type(4))) uint32_t u32x4_nt;
+
 // Two values rounded to the 16-bit output dtype (nearest even), first in
 // the low half: one conversion instruction for the pair.
 template <int OUT>
@@ -327,9 +329,9 @@ __global__ __launch_bounds__(V_THREADS) void v_decode_rows(VDecArgs a)
         uint32_t h[8];
 #pragma unroll
         for (int k = 0; k < 8; ++k) h[k] = pack_pair<OUT>(v[2 * k], v[2 * k + 1]);
-        uint4 *o = (uint4 *)((uint16_t *)a.out + r * 128 + 16 * j);
-        o[0] = uint4{h[0], h[1], h[2], h[3]};
-        o[1] = uint4{h[4], h[5], h[6], h[7]};
+        u32x4_nt *o = (u32x4_nt *)((uint16_t *)a.out + r * 128 + 16 * j);
+        __builtin_nontemporal_store(u32x4_nt{h[0], h[1], h[2], h[3]}, o);
+        __builtin_nontemporal_store(u32x4_nt{h[4], h[5], h[6], h[7]}, o + 1);
     }
 }
 
@@ -426,7 +428,7 @@ __global__ __launch_bounds__(V_THREADS) void k4_decode_rows(KDecArgs a)
             uint32_t h[4];
 #pragma unroll
             for (int k = 0; k < 4; ++k) h[k] = pack_pair<OUT>(v[2 * k], v[2 * k + 1]);
-            *(uint4 *)((uint16_t *)a.out + rt * 128 + 8 * j) = uint4{h[0], h[1], h[2], h[3]};
+            __builtin_nontemporal_store(u32x4_nt{h[0], h[1], h[2], h[3]}, (u32x4_nt *)((uint16_t *)a.out + rt * 128 + 8 * j));
         }
     }
 }
