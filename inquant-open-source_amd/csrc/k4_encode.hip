@@ -336,7 +336,7 @@ __device__ __forceinline__ void store_page_values(const K4Args &a, uint8_t *page
                                                   uint32_t code, uint16_t off_h, uint16_t sc_h)
 {
     const int64_t r = h * T + t;
-    ((uint32_t *)(page + a.off_vpay + r * 32))[vj] = code;
+    __builtin_nontemporal_store(code, (uint32_t *)(page + a.off_vpay + r * 32) + vj);
     if ((vj & 3) == 0) ((uint16_t *)(page + a.off_voff))[r * 2 + (vj >> 2)] = off_h;
     if ((vj & 3) == 3) ((uint16_t *)(page + a.off_vscale))[r * 2 + (vj >> 2)] = sc_h;
 }
@@ -649,7 +649,7 @@ __device__ __forceinline__ void k4_tile_body(const K4Args &a, int64_t b, int64_t
                 constexpr int GROUPS = 8 / GLV;
                 const int64_t vr = row * T + t;
                 if constexpr (VBITS == 2) {
-                    ((uint32_t *)(a.vpayload + vr * PB))[vj] = code[0];
+                    __builtin_nontemporal_store(code[0], (uint32_t *)(a.vpayload + vr * PB) + vj);
                 } else {
                     typedef __attribute__((ext_vector_type(2))) uint32_t u32x2_t;
                     ((u32x2_t *)(a.vpayload + vr * PB))[vj] = u32x2_t{code[0], code[VBITS / 2 - 1]};
@@ -767,7 +767,7 @@ __device__ __forceinline__ void k4_tile_body(const K4Args &a, int64_t b, int64_t
                 float v[8];
 #pragma unroll
                 for (int e = 0; e < 8; ++e) v[e] = tile_f32<F16IN>(xe[e][off]);
-                out[t * (TILE_D / 8) + j] = slots.word(v);
+                __builtin_nontemporal_store(slots.word(v), &out[t * (TILE_D / 8) + j]);
             }
         }
     };
@@ -965,7 +965,7 @@ __global__ __launch_bounds__(K4_THREADS) void k4_encode_page_rows(K4Args a, int6
         float v[8];
 #pragma unroll
         for (int e = 0; e < 8; ++e) v[e] = tile_f32<F16IN>(xs[t * ROW + slots.srcc[e]]);
-        out[t * (TILE_D / 8) + j] = slots.word(v);
+        __builtin_nontemporal_store(slots.word(v), &out[t * (TILE_D / 8) + j]);
     }
 }
 
