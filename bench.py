@@ -390,11 +390,12 @@ def time_next_rows(device, sets=8):
     a HIP graph: materialize (K4 keys and V2 g64 values of one config 2 layer,
     4 heads x 32768 tokens, dequantized to bf16), encode into 256- and
     16-token pages (keys K4 min_error + role map + values V2 of 32768 tokens
-    x 4 heads, one launch) and causal prefill attention over exact K/V (one
-    8192-token Qwen2.5-7B sequence, 28 query heads over 4 KV heads, bf16).
-    Materialize and the page encodes run over `sets` distinct layers in turn
-    (8 x ~81 MB = ~650 MB, above the 256 MB Infinity Cache), so each call
-    reads its inputs from HBM."""
+    x 4 heads, one launch), unpack those pages back to dense bf16 K and V,
+    and causal prefill attention over exact K/V (one 8192-token Qwen2.5-7B
+    sequence, 28 query heads over 4 KV heads, bf16).  Materialize and the
+    page encodes run over `sets` distinct layers in turn (8 x ~81 MB =
+    ~650 MB, above the 256 MB Infinity Cache), so each call reads its inputs
+    from HBM; the unpacks read the `sets` page pools in turn (8 x 14 MB)."""
     import torch
     from inquant import _native as nat
     from inquant.codec import CodecConfig, quantize
@@ -463,7 +464,25 @@ def time_next_rows(device, sets=8):
                                      "gbs": round(enc_bytes / (us * 1e-6) / 1e9, 2),
                                      "hbm_frac": round(enc_bytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
                                      "rotated_layers": sets}
-        del jobs
+
+        # the pages just written, unpacked to dense bf16 K and V [P, H, B, 128]
+        # (unpack_pages_reference): every page read once, both outputs written
+        kd = torch.empty((P, H, B, D), dtype=torch.bfloat16, device=device)
+        vd = torch.empty_like(kd)
+
+        def unpack_pages():
+            st = nat.stream_handle(torch.device(device))
+            for _, _, pool in jobs:
+                nat.check(lib.iq_unpack_pages(pool.data_ptr(), P, H, B, kd.data_ptr(), vd.data_ptr(), nat.IQ_BF16,
+                                              st))
+
+        us = _graph_us(device, unpack_pages, reps=2) / sets
+        unp_bytes = P * layout.page_bytes + 2 * kd.numel() * 2
+        out[f"unpack_pages_b{B}"] = {"tokens": T, "heads": H, "page_tokens": B, "us": round(us, 3),
+                                     "bytes": unp_bytes, "gbs": round(unp_bytes / (us * 1e-6) / 1e9, 2),
+                                     "hbm_frac": round(unp_bytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+                                     "rotated_layers": sets}
+        del jobs, kd, vd
     del kv
     torch.cuda.empty_cache()
 

@@ -167,6 +167,193 @@ __global__ __launch_bounds__(128) void unpack_pages_kernel(UnpackArgs a)
     iq_store_as(a.v, o, __fadd_rn(__fmul_rn((float)code, sc), of), a.out_dt);
 }
 
+// 16-byte aligned outputs (every supported page size): grid (token tiles
+// of UP_TOKENS, pages * H); thread (token, j), j < 16, decodes channels
+// 8 j .. 8 j + 7 of one token's key and value.  The page's role map, scales
+// and paddings are staged once in LDS.  Keys as k4_decode_rows: each slot is
+// one product code * f (a plain channel code = slot - 8, f its scale; a
+// source code = 16 slot + lo - 128, lo its donor channel's nibble, from this
+// lane's payload word or the word another lane of the token holds; a donor
+// code 1, f its padding); values code * scale + offset.  All of a thread's
+// page loads are issued first; the outputs go out as non-temporal stores.
+constexpr int UP_TOKENS = 128;
+constexpr int UP_ITER = UP_TOKENS / 16;            // tokens per thread
+
+template <int OUT>
+__device__ __forceinline__ void store8(void *base, int64_t at, const float (&v)[8])
+{
+    typedef __attribute__((ext_vector_type(4))) uint32_t w4;
+    if constexpr (OUT == IQ_F32) {
+        w4 *o = (w4 *)((float *)base + at);
+        __builtin_nontemporal_store(w4{__float_as_uint(v[0]), __float_as_uint(v[1]), __float_as_uint(v[2]),
+                                       __float_as_uint(v[3])}, o);
+        __builtin_nontemporal_store(w4{__float_as_uint(v[4]), __float_as_uint(v[5]), __float_as_uint(v[6]),
+                                       __float_as_uint(v[7])}, o + 1);
+    } else {
+        uint32_t h[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) h[k] = pack2<OUT == IQ_F16>(v[2 * k], v[2 * k + 1]);
+        __builtin_nontemporal_store(w4{h[0], h[1], h[2], h[3]}, (w4 *)((uint16_t *)base + at));
+    }
+}
+
+template <int OUT>
+__global__ __launch_bounds__(256) void unpack_rows_kernel(UnpackArgs a)
+{
+    __shared__ float s_scale[D], s_pad[SPG];
+    __shared__ int16_t s_role[D];
+    const int tid = threadIdx.x, lane = tid & 63, j = tid & 15;
+    const int64_t nh = blockIdx.y, n = nh / a.H, h = nh % a.H;
+    const uint8_t *page = a.pages + n * a.page_bytes;
+    const int B = (int)a.B, t0 = blockIdx.x * UP_TOKENS;
+    const int nt = min(UP_TOKENS, B - t0);
+    uint32_t kw[UP_ITER], vw[UP_ITER], vp[UP_ITER][2];
+#pragma unroll
+    for (int i = 0; i < UP_ITER; ++i) {
+        const int t = t0 + min((tid >> 4) + 16 * i, nt - 1);      // clamped: every load valid
+        const int64_t r = h * B + t;
+        kw[i] = *(const uint32_t *)(page + r * 64 + 4 * j);
+        vw[i] = *(const uint16_t *)(page + a.off.vp + r * 32 + 2 * j);
+        vp[i][0] = ((const uint16_t *)(page + a.off.vs))[r * 2 + (j >> 3)];
+        vp[i][1] = ((const uint16_t *)(page + a.off.vo))[r * 2 + (j >> 3)];
+    }
+    if (tid < D) {
+        s_scale[tid] = ((const float *)(page + a.off.ks))[h * D + tid];
+        s_role[tid] = ((const int16_t *)(page + a.off.km))[h * D + tid];
+    }
+    if (tid < SPG) s_pad[tid] = ((const float *)(page + a.off.kp))[h * SPG + tid];
+    __syncthreads();
+    uint32_t m[8], lo_at[8], lo_w[8];
+    int off[8], bp[8];
+    bool xl[8];
+    float f[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        const int rl = s_role[8 * j + e];
+        const bool src = rl >= 0 && rl < D, don = rl <= -2 && rl >= -2 - (SPG - 1);
+        f[e] = don ? s_pad[-2 - rl] : s_scale[8 * j + e];
+        m[e] = src ? 16u : don ? 0u : 1u;
+        off[e] = src ? 128 : don ? -1 : 8;
+        lo_w[e] = src ? 4u : 0u;
+        lo_at[e] = src ? 4u * (uint32_t)(rl & 7) : 0u;
+        xl[e] = src && (rl >> 3) != j;
+        bp[e] = 4 * ((lane & ~15) | (src ? rl >> 3 : 0));
+    }
+#pragma unroll
+    for (int i = 0; i < UP_ITER; ++i) {
+        const int tt = (tid >> 4) + 16 * i;
+        const uint32_t w = kw[i];
+        uint32_t x[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) x[e] = (uint32_t)__builtin_amdgcn_ds_bpermute(bp[e], (int)w);
+        if (tt >= nt) continue;
+        const int64_t o = (nh * B + t0 + tt) * D + 8 * j;
+        float v[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const uint32_t wd = xl[e] ? x[e] : w;
+            const uint32_t slot = __builtin_amdgcn_ubfe(w, 4 * e, 4);
+            const uint32_t lo = __builtin_amdgcn_ubfe(wd, lo_at[e], lo_w[e]);
+            v[e] = __fmul_rn((float)((int)(__umul24(slot, m[e]) + lo) - off[e]), f[e]);
+        }
+        store8<OUT>(a.k, o, v);
+        const float sc = iq_f16_to_f32((uint16_t)vp[i][0]), of = iq_f16_to_f32((uint16_t)vp[i][1]);
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+            v[e] = __fadd_rn(__fmul_rn((float)((vw[i] >> (2 * e)) & 3u), sc), of);
+        store8<OUT>(a.v, o, v);
+    }
+}
+
+// Pages of B = 16, 32 or 64 tokens: each 16-lane group takes one (page,
+// head) and all its tokens, 16 at a time (loads first), lane j channels
+// 8 j .. 8 j + 7.  Lane j reads its own eight roles and scales and padding j
+// of the page straight from the page (no LDS, no barrier); a donor slot
+// takes its padding from the lane of its group that read it.  Same
+// arithmetic as unpack_rows_kernel.
+template <int OUT, int B>
+__global__ __launch_bounds__(256) void unpack_small_pages_kernel(UnpackArgs a, int64_t nph)
+{
+    typedef __attribute__((ext_vector_type(4))) uint32_t w4;
+    const int tid = threadIdx.x, lane = tid & 63, j = tid & 15;
+    const int64_t ph = (int64_t)blockIdx.x * 16 + (tid >> 4);
+    const bool ok = ph < nph;                                    // group-uniform
+    const int64_t phc = ok ? ph : nph - 1;
+    const int64_t n = phc / a.H, h = phc % a.H;
+    const uint8_t *page = a.pages + n * a.page_bytes;
+    const w4 rw = *(const w4 *)(page + a.off.km + (h * D + 8 * j) * 2);          // roles 8 j .. 8 j + 7
+    const w4 s0 = *(const w4 *)(page + a.off.ks + (h * D + 8 * j) * 4);
+    const w4 s1 = *(const w4 *)(page + a.off.ks + (h * D + 8 * j + 4) * 4);
+    const float pad_j = ((const float *)(page + a.off.kp))[h * SPG + j];
+    uint32_t m[8], lo_at[8], lo_w[8];
+    int off[8], bp[8];
+    bool xl[8];
+    float f[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        const int rl = (int)(int16_t)(rw[e >> 1] >> (16 * (e & 1)));
+        const bool src = rl >= 0 && rl < D, don = rl <= -2 && rl >= -2 - (SPG - 1);
+        const float pad = __int_as_float(
+            __builtin_amdgcn_ds_bpermute(4 * ((lane & ~15) | (don ? -2 - rl : 0)), __float_as_int(pad_j)));
+        f[e] = don ? pad : __uint_as_float(e < 4 ? s0[e] : s1[e - 4]);
+        m[e] = src ? 16u : don ? 0u : 1u;
+        off[e] = src ? 128 : don ? -1 : 8;
+        lo_w[e] = src ? 4u : 0u;
+        lo_at[e] = src ? 4u * (uint32_t)(rl & 7) : 0u;
+        xl[e] = src && (rl >> 3) != j;
+        bp[e] = 4 * ((lane & ~15) | (src ? rl >> 3 : 0));
+    }
+#pragma unroll 1
+    for (int c = 0; c < B; c += 16) {
+        uint32_t kw[16], vw[16], vp[16][2];
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const int64_t r = h * B + c + i;
+            kw[i] = *(const uint32_t *)(page + r * 64 + 4 * j);
+            vw[i] = *(const uint16_t *)(page + a.off.vp + r * 32 + 2 * j);
+            vp[i][0] = ((const uint16_t *)(page + a.off.vs))[r * 2 + (j >> 3)];
+            vp[i][1] = ((const uint16_t *)(page + a.off.vo))[r * 2 + (j >> 3)];
+        }
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const uint32_t w = kw[i];
+            uint32_t x[8];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) x[e] = (uint32_t)__builtin_amdgcn_ds_bpermute(bp[e], (int)w);
+            if (!ok) continue;
+            const int64_t o = (phc * B + c + i) * D + 8 * j;
+            float v[8];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const uint32_t wd = xl[e] ? x[e] : w;
+                const uint32_t slot = __builtin_amdgcn_ubfe(w, 4 * e, 4);
+                const uint32_t lo = __builtin_amdgcn_ubfe(wd, lo_at[e], lo_w[e]);
+                v[e] = __fmul_rn((float)((int)(__umul24(slot, m[e]) + lo) - off[e]), f[e]);
+            }
+            store8<OUT>(a.k, o, v);
+            const float sc = iq_f16_to_f32((uint16_t)vp[i][0]), of = iq_f16_to_f32((uint16_t)vp[i][1]);
+#pragma unroll
+            for (int e = 0; e < 8; ++e)
+                v[e] = __fadd_rn(__fmul_rn((float)((vw[i] >> (2 * e)) & 3u), sc), of);
+            store8<OUT>(a.v, o, v);
+        }
+    }
+}
+
+template <int OUT>
+void launch_unpack(const UnpackArgs &a, int64_t nph, hipStream_t st)
+{
+    const dim3 small((unsigned)((nph + 15) / 16));
+    switch (a.B) {
+    case 16: hipLaunchKernelGGL((unpack_small_pages_kernel<OUT, 16>), small, dim3(256), 0, st, a, nph); break;
+    case 32: hipLaunchKernelGGL((unpack_small_pages_kernel<OUT, 32>), small, dim3(256), 0, st, a, nph); break;
+    case 64: hipLaunchKernelGGL((unpack_small_pages_kernel<OUT, 64>), small, dim3(256), 0, st, a, nph); break;
+    default:
+        hipLaunchKernelGGL((unpack_rows_kernel<OUT>), dim3((unsigned)((a.B + UP_TOKENS - 1) / UP_TOKENS), (unsigned)nph),
+                           dim3(256), 0, st, a);
+    }
+}
+
 // ------------------------------------------------------------------ decode
 
 struct PagedArgs {
@@ -872,8 +1059,19 @@ extern "C" int iq_unpack_pages(const uint8_t *pages, int64_t n_pages, int64_t H,
     IQ_CHECK_ARG(n_pages * H <= 0x7fffffffLL, "iq_unpack_pages: too many pages");
     UnpackArgs a{pages, H, block_tokens, iq_page_bytes(H, block_tokens), page_offsets(H, block_tokens), keys, values,
                  out_dtype};
-    hipLaunchKernelGGL(unpack_pages_kernel, dim3((unsigned)(n_pages * H), (unsigned)block_tokens), dim3(D), 0,
-                       (hipStream_t)stream, a);
+    const hipStream_t st = (hipStream_t)stream;
+    // the row kernels: 16-byte vector stores and loads at page offsets that
+    // are multiples of 16 (every supported page size)
+    if (((uintptr_t)pages & 15) == 0 && ((uintptr_t)keys & 15) == 0 && ((uintptr_t)values & 15) == 0 &&
+        n_pages * H <= 65535) {
+        const int64_t nph = n_pages * H;
+        if (out_dtype == IQ_BF16) launch_unpack<IQ_BF16>(a, nph, st);
+        else if (out_dtype == IQ_F16) launch_unpack<IQ_F16>(a, nph, st);
+        else launch_unpack<IQ_F32>(a, nph, st);
+        IQ_CHECK_LAUNCH("unpack rows");
+        return IQ_OK;
+    }
+    hipLaunchKernelGGL(unpack_pages_kernel, dim3((unsigned)(n_pages * H), (unsigned)block_tokens), dim3(D), 0, st, a);
     IQ_CHECK_LAUNCH("unpack_pages_kernel");
     return IQ_OK;
 }

@@ -204,6 +204,13 @@ def test_paged_decode_reads_roles_as_the_role_map_states(block):
     # the edits change the attended keys: the unedited pool decodes differently
     _, pool0, _, _, _, _ = _paged_case(97, block, pages, tail)
     assert np.abs(_expected(layout, pool0, ids, dense, pages, tail, sink, q) - exp).max() > 1e-4
+    # unpacking reads the edited maps the same way, bit for bit
+    from inquant_vllm import unpack_pages_reference
+    edited = pool[ids.long()]
+    rk, rv = unpack_pages_reference(edited, layout, torch.float32)
+    ok, ov = oracle.unpack_pages(_np(edited), layout.heads, block, "float32")
+    np.testing.assert_array_equal(_np(rk).view(np.uint32), ok.view(np.uint32))
+    np.testing.assert_array_equal(_np(rv).view(np.uint32), ov.view(np.uint32))
 
 
 @pytest.mark.parametrize("h,hq", [(4, 4), (2, 32)])
