@@ -391,7 +391,7 @@ def time_next_rows(device, sets=8):
     4 heads x 32768 tokens, dequantized to bf16), encode into 256- and
     16-token pages (keys K4 min_error + role map + values V2 of 32768 tokens
     x 4 heads, one launch), unpack those pages back to dense bf16 K and V,
-    and causal prefill attention over exact K/V (one 8192-token Qwen2.5-7B
+    write codec outputs into pages (write_codec_pages), and causal prefill attention over exact K/V (one 8192-token Qwen2.5-7B
     sequence, 28 query heads over 4 KV heads, bf16).  Materialize and the
     page encodes run over `sets` distinct layers in turn (8 x ~81 MB =
     ~650 MB, above the 256 MB Infinity Cache), so each call reads its inputs
@@ -482,7 +482,35 @@ def time_next_rows(device, sets=8):
                                      "bytes": unp_bytes, "gbs": round(unp_bytes / (us * 1e-6) / 1e9, 2),
                                      "hbm_frac": round(unp_bytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
                                      "rotated_layers": sets}
-        del jobs, kd, vd
+        del kd, vd
+
+        # write_codec_pages: each set's codec outputs (K4 min_error, V2 g64 of
+        # [P, H, B, 128]) scattered into its pool at a random permutation of ids
+        codecs = []
+        for kp, vp, _ in jobs:
+            codecs.append((quantize(kp.contiguous(), CodecConfig(donor_policy="min_error")),
+                           quantize_values(vp.contiguous(), 2, 64)))
+        perm = torch.randperm(P, generator=gen, device=device).to(torch.int32)
+
+        def write_pages():
+            st = nat.stream_handle(torch.device(device))
+            for (pk, pv), (_, _, pool) in zip(codecs, jobs):
+                nat.check(lib.iq_write_pages(pk.payload.data_ptr(), pk.scales.data_ptr(), pk.padding.data_ptr(),
+                                             pk.salient_channels.data_ptr(), pk.donor_channels.data_ptr(),
+                                             pk.salient_channels.element_size(), pv.payload.data_ptr(),
+                                             pv.scales.data_ptr(), pv.offsets.data_ptr(), P, H, B, pool.data_ptr(),
+                                             P, perm.data_ptr(), 4, st))
+
+        us = _graph_us(device, write_pages, reps=2) / sets
+        pk, pv = codecs[0]
+        wr_bytes = (sum(t.numel() * t.element_size() for t in pk.tensors.values())
+                    + sum(t.numel() * t.element_size() for t in (pv.payload, pv.scales, pv.offsets))
+                    + P * layout.page_bytes)
+        out[f"write_codec_pages_b{B}"] = {"tokens": T, "heads": H, "page_tokens": B, "us": round(us, 3),
+                                          "bytes": wr_bytes, "gbs": round(wr_bytes / (us * 1e-6) / 1e9, 2),
+                                          "hbm_frac": round(wr_bytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+                                          "rotated_layers": sets}
+        del jobs, codecs, pk, pv
     del kv
     torch.cuda.empty_cache()
 

@@ -127,6 +127,65 @@ __global__ __launch_bounds__(256) void write_pages_kernel(WriteArgs a)
     if (tid < D) ((int16_t *)(page + a.off.km))[h * D + tid] = s_role[tid];
 }
 
+// Pages of B = 16, 32 or 64 tokens: each 16-lane group writes one (page,
+// head) slice with 16-byte copies, and builds its role map without LDS or
+// barriers: lane j holds descriptor j and writes the roles of channels
+// 8 j .. 8 j + 7, taking every descriptor from its lane of the group (all
+// sources first, then all donors, as write_pages_kernel orders them).
+template <int B>
+__global__ __launch_bounds__(256) void write_small_pages_kernel(WriteArgs a, int64_t nph)
+{
+    typedef __attribute__((ext_vector_type(4))) uint32_t v4;
+    const int tid = threadIdx.x, lane = tid & 63, j = tid & 15, g0 = lane & ~15;
+    const int64_t ph = (int64_t)blockIdx.x * 16 + (tid >> 4);
+    const int64_t nh = ph < nph ? ph : nph - 1;                       // clamped: every load valid
+    const int64_t n = nh / a.H, h = nh % a.H;
+    const int64_t id = load_id(a.ids, n, a.id_bytes);
+    const bool live = ph < nph && id >= 0 && id < a.pool_pages;       // group-uniform
+    const int s_j = load_index(a.src, nh * SPG + j, a.desc_bytes);
+    const int d_j = load_index(a.don, nh * SPG + j, a.desc_bytes);
+    int role[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) role[e] = -1;
+#pragma unroll
+    for (int k = 0; k < SPG; ++k) {
+        const int sk = __builtin_amdgcn_ds_bpermute(4 * (g0 + k), s_j);
+        const int dk = __builtin_amdgcn_ds_bpermute(4 * (g0 + k), d_j);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) role[e] = sk >= 0 && sk < D && sk == 8 * j + e ? dk : role[e];
+    }
+#pragma unroll
+    for (int k = 0; k < SPG; ++k) {
+        const int dk = __builtin_amdgcn_ds_bpermute(4 * (g0 + k), d_j);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) role[e] = dk >= 0 && dk < D && dk == 8 * j + e ? -2 - k : role[e];
+    }
+    if (!live) return;
+    uint8_t *page = a.pool + id * a.page_bytes;
+    const v4 *ksrc = (const v4 *)(a.kp + nh * B * 64);
+    v4 *kdst = (v4 *)(page + h * B * 64);
+#pragma unroll
+    for (int i = j; i < B * 4; i += 16) kdst[i] = ksrc[i];
+    const v4 *vsrc = (const v4 *)(a.vp + nh * B * 32);
+    v4 *vdst = (v4 *)(page + a.off.vp + h * B * 32);
+#pragma unroll
+    for (int i = j; i < B * 2; i += 16) vdst[i] = vsrc[i];
+    // value scales and offsets: B * 4 bytes each, B / 4 chunks
+    if (j < B / 4) {
+        ((v4 *)(page + a.off.vs + h * B * 4))[j] = ((const v4 *)(a.vs + nh * B * 2))[j];
+        ((v4 *)(page + a.off.vo + h * B * 4))[j] = ((const v4 *)(a.vo + nh * B * 2))[j];
+    }
+    const v4 *kssrc = (const v4 *)(a.ks + nh * D);
+    v4 *ksdst = (v4 *)(page + a.off.ks + h * D * 4);
+    ksdst[j] = kssrc[j];
+    ksdst[j + 16] = kssrc[j + 16];
+    if (j < SPG / 4) ((v4 *)(page + a.off.kp + h * SPG * 4))[j] = ((const v4 *)(a.kpad + nh * SPG))[j];
+    uint32_t rw[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) rw[q] = (uint32_t)(uint16_t)role[2 * q] | ((uint32_t)(uint16_t)role[2 * q + 1] << 16);
+    ((v4 *)(page + a.off.km + h * D * 2))[j] = v4{rw[0], rw[1], rw[2], rw[3]};
+}
+
 // ------------------------------------------------------------------ unpack
 
 struct UnpackArgs {
@@ -1043,7 +1102,19 @@ extern "C" int iq_write_pages(const uint8_t *k_payload, const float *k_scales, c
     WriteArgs a{k_payload, k_scales, k_padding, k_src, k_don, desc_bytes, v_payload, v_scales, v_offsets, H,
                 block_tokens, iq_page_bytes(H, block_tokens), pool_pages, pool, page_ids, id_bytes,
                 page_offsets(H, block_tokens)};
-    hipLaunchKernelGGL(write_pages_kernel, dim3((unsigned)n_pages, (unsigned)H), dim3(256), 0, (hipStream_t)stream, a);
+    const hipStream_t st = (hipStream_t)stream;
+    const bool vec = ((uintptr_t)k_scales & 15) == 0 && ((uintptr_t)k_padding & 15) == 0 &&
+                     ((uintptr_t)v_scales & 15) == 0 && ((uintptr_t)v_offsets & 15) == 0;
+    if (vec && block_tokens <= 64) {
+        const int64_t nph = n_pages * H;
+        const dim3 grid((unsigned)((nph + 15) / 16));
+        if (block_tokens == 16) hipLaunchKernelGGL((write_small_pages_kernel<16>), grid, dim3(256), 0, st, a, nph);
+        else if (block_tokens == 32) hipLaunchKernelGGL((write_small_pages_kernel<32>), grid, dim3(256), 0, st, a, nph);
+        else hipLaunchKernelGGL((write_small_pages_kernel<64>), grid, dim3(256), 0, st, a, nph);
+        IQ_CHECK_LAUNCH("write_small_pages_kernel");
+        return IQ_OK;
+    }
+    hipLaunchKernelGGL(write_pages_kernel, dim3((unsigned)n_pages, (unsigned)H), dim3(256), 0, st, a);
     IQ_CHECK_LAUNCH("write_pages_kernel");
     return IQ_OK;
 }
