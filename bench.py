@@ -345,19 +345,45 @@ def time_encode(device, sets=4, cycles=3):
                     fn(w, st)
         return launch
 
+    def once_values(w, st):
+        # quantize_values alone (a8): the layer's values, V2 g64 (v_encode_rows)
+        nat.check(lib.iq_v_quantize(w["vb"].data_ptr(), nat.IQ_BF16, nat.strides4(w["vb"]), nb, H, B, 128, 2, 64,
+                                    w["vpay"].data_ptr(), w["vsc"].data_ptr(), w["voff"].data_ptr(),
+                                    bad.data_ptr() + 4, st))
+
     calls = sets * cycles
     ms = _graph_us(device, rotated(once), reps=1) * 1e-3 / calls
     assert bad.tolist() == [0, 0]
     ms_k4v = _graph_us(device, rotated(once_k4v), reps=1) * 1e-3 / calls
     assert bad.tolist() == [0, 0]
+    ms_v = _graph_us(device, rotated(once_values), reps=1) * 1e-3 / calls
+    assert bad.tolist() == [0, 0]
     w = work[0]
     enc_bytes = 2 * w["k"].numel() * 2 + w["pay"].numel() + w["sc"].numel() * 4 + w["src"].numel() * 2 \
         + w["pad"].numel() * 4 + w["vpay"].numel() + w["vsc"].numel() * 4
+    v_bytes = w["v"].numel() * 2 + w["vpay"].numel() + w["vsc"].numel() * 4
+
+    # reuse_map (a4/a5): sources and min_error donors of every (block, head)
+    # row of the layer from its saliency and donor error (1024 rows of 128)
+    g = torch.Generator(device=device).manual_seed(8)
+    sal = torch.rand((nb * H, 128), generator=g, device=device)
+    err = torch.rand((nb * H, 128), generator=g, device=device)
+    rsrc = torch.empty((nb * H, S), dtype=torch.int64, device=device)
+    rdon = torch.empty_like(rsrc)
+
+    def reuse():
+        nat.check(lib.iq_reuse_map(sal.data_ptr(), err.data_ptr(), nb * H, 128, S, rsrc.data_ptr(), rdon.data_ptr(),
+                                   nat.stream_handle(torch.device(device))))
+
+    us_reuse = _graph_us(device, reuse, reps=20)
     del work
     torch.cuda.empty_cache()
     return {"encode_mtok_s": T / (ms * 1e-3) / 1e6, "encode_ms_per_layer": ms,
             "encode_gbs": enc_bytes / (ms * 1e-3) / 1e9, "encode_bytes_per_layer": enc_bytes,
             "k4_values_mtok_s": T / (ms_k4v * 1e-3) / 1e6, "k4_values_ms_per_layer": ms_k4v,
+            "values_only_mtok_s": T / (ms_v * 1e-3) / 1e6, "values_only_ms_per_layer": ms_v,
+            "values_only_gbs": v_bytes / (ms_v * 1e-3) / 1e9,
+            "reuse_map_us": us_reuse, "reuse_map_rows": nb * H,
             "rotated_layers": sets, "rotated_bytes": sets * enc_bytes}
 
 

@@ -997,6 +997,30 @@ __global__ __launch_bounds__(64) void reuse_map_kernel(SelectArgs a)
     }
 }
 
+// D = 128: one wavefront per row with the radix top-k selection of the page
+// row encoder (iq_select_wave128), the same picks as iq_select_wave.
+__global__ __launch_bounds__(64) void reuse_map128_kernel(SelectArgs a)
+{
+    __shared__ float s_sal[128], s_err[128];
+    __shared__ int16_t s_src_of[128], s_src[64], s_don[64], s_list[64];
+    __shared__ uint8_t s_is_src[128];
+    const int64_t row = blockIdx.x;
+    const int lane = threadIdx.x;
+    s_sal[lane] = a.sal[row * 128 + lane];
+    s_sal[64 + lane] = a.sal[row * 128 + 64 + lane];
+    if (a.err) {
+        s_err[lane] = a.err[row * 128 + lane];
+        s_err[64 + lane] = a.err[row * 128 + 64 + lane];
+    }
+    __syncthreads();
+    iq_select_wave128(s_sal, a.err ? s_err : nullptr, (int)a.count, s_src, s_don, s_is_src, s_src_of, s_list);
+    __syncthreads();
+    if (lane < a.count) {
+        a.src[row * a.count + lane] = s_src[lane];
+        a.don[row * a.count + lane] = s_don[lane];
+    }
+}
+
 }  // namespace
 
 namespace {
@@ -1182,7 +1206,8 @@ extern "C" int iq_reuse_map(const float *saliency, const float *donor_error, int
     if (rows == 0 || count == 0) return IQ_OK;
     IQ_CHECK_ARG(saliency && src && don, "iq_reuse_map: null pointer");
     SelectArgs a{saliency, donor_error, D, count, src, don};
-    hipLaunchKernelGGL(reuse_map_kernel, dim3((unsigned)rows), dim3(64), 0, (hipStream_t)stream, a);
+    if (D == 128) hipLaunchKernelGGL(reuse_map128_kernel, dim3((unsigned)rows), dim3(64), 0, (hipStream_t)stream, a);
+    else hipLaunchKernelGGL(reuse_map_kernel, dim3((unsigned)rows), dim3(64), 0, (hipStream_t)stream, a);
     IQ_CHECK_LAUNCH("reuse_map_kernel");
     return IQ_OK;
 }
