@@ -387,9 +387,11 @@ def time_encode(device, sets=4, cycles=3):
             "rotated_layers": sets, "rotated_bytes": sets * enc_bytes}
 
 
-def _graph_us(device, launch, reps=10):
+def _graph_us(device, launch, reps=10, timed=5):
     """Microseconds per call of `launch` (native launches on the current
-    stream), replayed `reps` times in one HIP graph."""
+    stream), replayed `reps` times in one HIP graph: the median of `timed`
+    timed replays after one untimed one (a single replay of a short graph
+    moves with the clock state the previous work left)."""
     import torch
     s = torch.cuda.Stream()
     s.wait_stream(torch.cuda.current_stream())
@@ -404,11 +406,14 @@ def _graph_us(device, launch, reps=10):
     graph.replay()
     torch.cuda.synchronize()
     start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    start.record()
-    graph.replay()
-    stop.record()
-    torch.cuda.synchronize()
-    return start.elapsed_time(stop) * 1e3 / reps
+    times = []
+    for _ in range(timed):
+        start.record()
+        graph.replay()
+        stop.record()
+        torch.cuda.synchronize()
+        times.append(start.elapsed_time(stop))
+    return sorted(times)[len(times) // 2] * 1e3 / reps
 
 
 def time_next_rows(device, sets=8):
