@@ -171,6 +171,7 @@ class _LayerCache:
         self.tail: _Rows | None = None
         self.key_blocks: list = []
         self.value_blocks: list = []
+        self.runs: list = []            # [first, stop) of the blocks of each seal (one batched encode)
         self.packed_nbytes = 0
         self.full_sink = None          # (keys, values) views once the sink holds all its rows
         self.block_tuples = None       # (key blocks, value blocks) as tuples, rebuilt after a seal
@@ -254,6 +255,23 @@ def _carve(device, fields):
     raw = torch.empty(total, dtype=torch.uint8, device=device)
     typed = [raw.view(dtype) for dtype in dtypes]   # one reinterpretation per dtype
     return [torch.as_strided(typed[i], shape, strides, offset) for i, shape, strides, offset in views]
+
+
+def _run_block(blocks, i: int, j: int):
+    """blocks[i:j], the per-block views of one batched encode (consecutive
+    equal-size slices of each field's allocation), as one batched
+    [j - i, H, T, D] block over the same memory."""
+    first = blocks[i]
+    if j - i == 1:
+        return first
+    n = j - i
+    fields = {name: torch.as_strided(t, (n, *t.shape[1:]), (t.numel(), *t.stride()[1:]), t.storage_offset())
+              for name, t in first.tensors.items()}
+    shape = (n, *first.shape[1:])
+    if isinstance(first, PackedValues):
+        return PackedValues(**fields, shape=shape, original_dtype=first.original_dtype, bits=first.bits,
+                            group_size=first.group_size)
+    return PackedTensor(**fields, shape=shape, original_dtype=first.original_dtype)
 
 
 _SEAL_DTYPES = (torch.float32, torch.bfloat16, torch.float16)   # what the batched seal encoders read
@@ -634,6 +652,7 @@ class InQuantCache(_HFCache):
             raise ValueError(_BAD_K)
         if bad_value:
             raise ValueError(value_error)
+        layer.runs.append((len(layer.key_blocks), len(layer.key_blocks) + len(new_keys)))
         layer.key_blocks.extend(new_keys)
         layer.value_blocks.extend(new_values)
         layer.block_tuples = None
@@ -704,18 +723,33 @@ class InQuantCache(_HFCache):
     # ------------------------------------------------------------ reads
     @torch.no_grad()
     def materialize(self, layer_idx: int = 0):
-        """Dense (keys, values) of one layer: sink ++ dequantized blocks ++ tail (not retained)."""
+        """Dense (keys, values) of one layer: sink ++ dequantized blocks ++ tail
+        (not retained).  Blocks that are consecutive views of one batched
+        encode (a prefill's blocks) dequantize in one launch per run, straight
+        into their rows of the output (the cache records each seal's run)."""
         layer = self._layers.get(layer_idx)
         if layer is None:
             raise KeyError(f"No cached layer {layer_idx}")
+        _, heads, _, dim = layer.shape
+        sink_n = 0 if layer.sink is None else layer.sink.count
+        tail_n = 0 if layer.tail is None else layer.tail.count
         out = []
         for side, blocks in ((0, layer.key_blocks), (1, layer.value_blocks)):
-            parts = [rows.buf[side:side + 1, :, rows.start:rows.start + rows.count]
-                     for rows in (layer.sink,) if rows is not None and rows.count]
-            parts += [b.dequantize(dtype=layer.dtype) for b in blocks]
-            if layer.tail is not None and layer.tail.count:
-                parts.append(layer.tail.keys() if side == 0 else layer.tail.values())
-            out.append(torch.cat(parts, 2))
+            total = sink_n + sum(b.shape[2] for b in blocks) + tail_n
+            dense = torch.empty((1, heads, total, dim), dtype=layer.dtype, device=layer.device)
+            at = 0
+            if sink_n:
+                rows = layer.sink
+                dense[:, :, :sink_n].copy_(rows.buf[side:side + 1, :, rows.start:rows.start + sink_n])
+                at = sink_n
+            for i, j in layer.runs:
+                n, T = j - i, blocks[i].shape[2]
+                deq = _run_block(blocks, i, j).dequantize(dtype=layer.dtype)     # [n, H, T, D]
+                dense[:, :, at:at + n * T].view(1, heads, n, T, dim).copy_(deq.permute(1, 0, 2, 3).unsqueeze(0))
+                at += n * T
+            if tail_n:
+                dense[:, :, at:].copy_(layer.tail.keys() if side == 0 else layer.tail.values())
+            out.append(dense)
         return out[0], out[1]
 
     # ------------------------------------------------------------ accounting (cache.py:346-394)

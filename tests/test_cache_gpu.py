@@ -94,6 +94,32 @@ def test_multihead_append_chunking_and_old_blocks_immutable():
     assert layer.residual_key.shape[2] < cfg.residual_length + cfg.block_size
 
 
+@pytest.mark.parametrize("value_bits", [None, 2])
+def test_materialize_equals_per_block_dequantize_across_runs(value_bits):
+    # materialize dequantizes a prefill's blocks (views of one batched encode)
+    # in one launch per run and sealed blocks one by one: the result is the
+    # reference's sink ++ [block.dequantize() for each block] ++ tail, bit for bit
+    from inquant.cache import CacheConfig, InQuantCache
+    from inquant.codec import CodecConfig
+    cfg = CacheConfig(codec=CodecConfig(donor_policy="min_error"), block_size=32, residual_length=16, sink_tokens=4,
+                      value_bits=value_bits, value_group_size=32)
+    cache = InQuantCache(cfg)
+    n0, extra = 4 + 32 * 6 + 16, 70
+    key, value = _randn(1, 2, n0 + extra, 64, seed=41), _randn(1, 2, n0 + extra, 64, seed=42)
+    key, value = key.to(torch.bfloat16), value.to(torch.bfloat16)
+    cache.update(key[:, :, :n0], value[:, :, :n0], 0)
+    for t in range(n0, n0 + extra):                 # two more blocks sealed one at a time
+        cache.append_for_attention(key[:, :, t:t + 1], value[:, :, t:t + 1], 0)
+    layer = cache._layers[0]
+    assert layer.runs == [(0, 6), (6, 7), (7, 8)] and len(layer.key_blocks) == 8
+    got_k, got_v = cache.materialize(0)
+    for got, blocks, side in ((got_k, layer.key_blocks, key), (got_v, layer.value_blocks, value)):
+        parts = [side[:, :, :4]] + [b.dequantize(dtype=torch.bfloat16) for b in blocks]
+        parts.append(side[:, :, 4 + 32 * len(blocks):n0 + extra])
+        expected = torch.cat(parts, 2)
+        assert got.shape == expected.shape and torch.equal(got, expected)
+
+
 def test_sink_accumulates_across_short_prefills():
     # test_cache.py:61-67
     from inquant.cache import InQuantCache
