@@ -501,8 +501,7 @@ class InQuantCache(_HFCache):
             layer = _LayerCache(key_states.shape, key_states.dtype, key_states.device)
             result = (key_states, value_states)
         else:
-            history_k, history_v = self.materialize(layer_idx)
-            result = (torch.cat((history_k, key_states), 2), torch.cat((history_v, value_states), 2))
+            result = self._dense(layer, key_states, value_states)     # history ++ the new tokens
         self._ingest(layer, key_states, value_states)
         self._layers[layer_idx] = layer
         self._after_write(layer_idx, layer)
@@ -730,12 +729,18 @@ class InQuantCache(_HFCache):
         layer = self._layers.get(layer_idx)
         if layer is None:
             raise KeyError(f"No cached layer {layer_idx}")
+        return self._dense(layer)
+
+    def _dense(self, layer, new_keys=None, new_values=None):
+        """sink ++ dequantized blocks ++ tail (++ new_keys / new_values, tokens
+        not yet stored) of one layer, written once into fresh tensors."""
         _, heads, _, dim = layer.shape
         sink_n = 0 if layer.sink is None else layer.sink.count
         tail_n = 0 if layer.tail is None else layer.tail.count
+        new_n = 0 if new_keys is None else new_keys.shape[2]
         out = []
         for side, blocks in ((0, layer.key_blocks), (1, layer.value_blocks)):
-            total = sink_n + sum(b.shape[2] for b in blocks) + tail_n
+            total = sink_n + sum(b.shape[2] for b in blocks) + tail_n + new_n
             dense = torch.empty((1, heads, total, dim), dtype=layer.dtype, device=layer.device)
             at = 0
             if sink_n:
@@ -748,7 +753,9 @@ class InQuantCache(_HFCache):
                 dense[:, :, at:at + n * T].view(1, heads, n, T, dim).copy_(deq.permute(1, 0, 2, 3).unsqueeze(0))
                 at += n * T
             if tail_n:
-                dense[:, :, at:].copy_(layer.tail.keys() if side == 0 else layer.tail.values())
+                dense[:, :, at:at + tail_n].copy_(layer.tail.keys() if side == 0 else layer.tail.values())
+            if new_n:
+                dense[:, :, at + tail_n:].copy_(new_keys if side == 0 else new_values)
             out.append(dense)
         return out[0], out[1]
 
