@@ -704,7 +704,8 @@ def time_append(device, H=4, packed_tokens=32768, validate_positions=True, seals
     starting from a 383-token tail and the decode-state metadata append for
     that block (medians reported).  The sealing append synchronizes on its
     own flag read, so its wall clock to return covers its device work; the
-    metadata append returns before its one launch finishes (host time)."""
+    metadata append returns before its one launch finishes (host time).
+    Last, the layer's dense K/V through materialize() (median wall clock)."""
     import torch
     from inquant.cache import CacheConfig, InQuantCache
     from inquant.codec import CodecConfig
@@ -772,11 +773,23 @@ def time_append(device, H=4, packed_tokens=32768, validate_positions=True, seals
         seal_us.append((t1 - t0) * 1e6)
         meta_us.append((t3 - t2) * 1e6)
     seal_bytes = 2 * H * 256 * 128 * 2 + (16384 + 512 + 32 + 64 + 8192 + 2048) * H + 64 + H * 128
+    # the layer's dense K and V through the cache API (what update() returns to
+    # a non-fused attention): wall clock of materialize() to its results
+    mat_us = []
+    for _ in range(10):
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        dense_k, dense_v = cache.materialize(0)
+        torch.cuda.synchronize()
+        mat_us.append((time.perf_counter() - t0) * 1e6)
+    mat_tokens = dense_k.shape[2]
+    del dense_k, dense_v
     return {"append_us_per_token": round(ev[0].elapsed_time(ev[1]) * 1e3 / 128, 2),
             "append_host_us_per_token": round(host_us, 2),
             "seal_us": round(sorted(seal_us)[len(seal_us) // 2], 2),
             "metadata_append_us": round(sorted(meta_us)[len(meta_us) // 2], 2),
-            "seals_timed": seals, "seal_bytes": seal_bytes}
+            "seals_timed": seals, "seal_bytes": seal_bytes,
+            "materialize_api_us": round(sorted(mat_us)[len(mat_us) // 2], 1), "materialize_api_tokens": mat_tokens}
 
 
 def time_append_step(device, H=4, packed_tokens=32768, layers=28):
