@@ -166,7 +166,7 @@ __global__ __launch_bounds__(V_THREADS) void v_encode_rows(VRowArgs a)
         const int row = tk;   // row offset within the block
         if (live) {
             if (BITS == 2) {
-                *(uint32_t *)(a.payload + r0 * PB + (uint32_t)(row * PB + 4 * j)) = word[0];
+                __builtin_nontemporal_store(word[0], (uint32_t *)(a.payload + r0 * PB + (uint32_t)(row * PB + 4 * j)));
             } else {
                 typedef __attribute__((ext_vector_type(2))) uint32_t u32x2_t;
                 *(u32x2_t *)(a.payload + r0 * PB + (uint32_t)(row * PB + 8 * j)) = u32x2_t{word[0], word[BITS / 2 - 1]};
