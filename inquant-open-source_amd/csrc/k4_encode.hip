@@ -49,6 +49,9 @@ struct K4Args {
     // of v are encoded group-wise into the outputs of iq_v_quantize
     uint8_t *vpayload;
     uint16_t *vscales, *voffsets;
+    // k4_encode_kernel with long rows: statistics, selection, scales and
+    // descriptors only; k4_quantize_generic then writes the payload
+    int split;
 };
 
 __device__ __forceinline__ void store_desc(void *p, int64_t i, int v, int bytes)
@@ -59,6 +62,40 @@ __device__ __forceinline__ void store_desc(void *p, int64_t i, int v, int bytes)
 }
 
 // Sampled sums of one channel in torch's order (cascade, or interleaved row_sum).
+// Calls f(v, i) for i = 0 .. n - 1 in order with v the element at
+// base + (i * mul + add) * step, loading SEQ_PF elements ahead of their use
+// (one memory round trip per SEQ_PF elements of a sequential reduction).
+constexpr int SEQ_PF = 16;
+
+template <int DT, typename F>
+__device__ __forceinline__ void for_each_seq_t(const void *x, int64_t base, int64_t step, int64_t n, int64_t mul,
+                                               int64_t add, F &f)
+{
+    for (int64_t i0 = 0; i0 < n; i0 += SEQ_PF) {
+        float v[SEQ_PF];
+#pragma unroll
+        for (int u = 0; u < SEQ_PF; ++u) {
+            const int64_t i = i0 + u < n ? i0 + u : n - 1;
+            v[u] = iq_load_f32(x, base + (i * mul + add) * step, DT);   // DT constant: no branch per load
+        }
+#pragma unroll
+        for (int u = 0; u < SEQ_PF; ++u)
+            if (i0 + u < n) f(v[u], i0 + u);
+    }
+}
+
+template <typename F>
+__device__ __forceinline__ void for_each_seq(const void *x, int dt, int64_t base, int64_t step, int64_t n, int64_t mul,
+                                             int64_t add, F &&f)
+{
+    switch (dt) {
+    case IQ_BF16: for_each_seq_t<IQ_BF16>(x, base, step, n, mul, add, f); break;
+    case IQ_F16: for_each_seq_t<IQ_F16>(x, base, step, n, mul, add, f); break;
+    case IQ_F64: for_each_seq_t<IQ_F64>(x, base, step, n, mul, add, f); break;
+    default: for_each_seq_t<IQ_F32>(x, base, step, n, mul, add, f); break;
+    }
+}
+
 __device__ __forceinline__ void sampled_sums(const void *x, int dt, int64_t base, int64_t step, int64_t ns, bool cascade_col,
                              float &sum_abs, float &sum)
 {
@@ -66,11 +103,10 @@ __device__ __forceinline__ void sampled_sums(const void *x, int dt, int64_t base
         IqCascade a, s;
         a.init(ns);
         s.init(ns);
-        for (int64_t r = 0; r < ns; ++r) {
-            const float v = iq_load_f32(x, base + r * step, dt);
+        for_each_seq(x, dt, base, step, ns, 1, 0, [&](float v, int64_t) {
             a.add(fabsf(v));
             s.add(v);
-        }
+        });
         sum_abs = a.finish();
         sum = s.finish();
     } else {
@@ -80,11 +116,10 @@ __device__ __forceinline__ void sampled_sums(const void *x, int dt, int64_t base
             IqCascade a, s;
             a.init(g);
             s.init(g);
-            for (int64_t r = 0; r < g; ++r) {
-                const float v = iq_load_f32(x, base + (4 * r + k) * step, dt);
+            for_each_seq(x, dt, base, step, g, 4, k, [&](float v, int64_t) {
                 a.add(fabsf(v));
                 s.add(v);
-            }
+            });
             pa[k] = a.finish();
             ps[k] = s.finish();
         }
@@ -132,18 +167,24 @@ __global__ __launch_bounds__(K4_THREADS) void k4_encode_kernel(K4Args a)
         float amax = 0.0f;
         bool bad = false;
         double mean = 0.0, m2 = 0.0;
-        for (int64_t t = 0; t < T; ++t) {
-            const float v = iq_load_f32(a.x, cb + t * a.st, a.dt);
+        const bool me = a.min_error;
+        for_each_seq(a.x, a.dt, cb, a.st, T, 1, 0, [&](float v, int64_t t) {
             bad |= !iq_isfinite(v);
             amax = fmaxf(amax, fabsf(v));
-            if (a.min_error) {
+            if (me) {
+                // delta / n as RN(1 / n) (off the dependent chain) and one
+                // remainder correction: the correctly rounded quotient
+                // (tests/test_welford_division.py, n up to 2^24)
+                const double n = (double)(t + 1), y = 1.0 / n;
                 const double dv = (double)v;
                 const double delta = __dsub_rn(dv, mean);
-                mean = __dadd_rn(mean, delta / (double)(t + 1));
+                const double q0 = __dmul_rn(delta, y);
+                const double r = __builtin_fma(-q0, n, delta);
+                mean = __dadd_rn(mean, __builtin_fma(r, y, q0));
                 const double nd = __dsub_rn(dv, mean);
                 m2 = __dadd_rn(m2, __dmul_rn(delta, nd));
             }
-        }
+        });
         if (a.min_error) {
             const float var = (float)(m2 / (double)T);
             const float diff = __fsub_rn((float)mean, smean);
@@ -177,10 +218,90 @@ __global__ __launch_bounds__(K4_THREADS) void k4_encode_kernel(K4Args a)
     if (tid == 0 && s_bad) atomicOr(a.bad, 1);
     __syncthreads();
 
-    // ---- phase 3: slots and nibble packing, one payload byte per step
+    if (a.split) return;
+
+    // ---- phase 3: slots and nibble packing, one payload byte per step, the
+    // inputs of P3_UNROLL steps loaded before any is used
     const int64_t half = D / 2;
     uint8_t *out = a.payload + row * T * half;
-    for (int64_t idx = tid; idx < T * half; idx += K4_THREADS) {
+    constexpr int P3_UNROLL = 8;
+    for (int64_t idx0 = tid; idx0 < T * half; idx0 += (int64_t)K4_THREADS * P3_UNROLL) {
+        float xv[P3_UNROLL][2];
+#pragma unroll
+        for (int u = 0; u < P3_UNROLL; ++u) {
+            const int64_t idx = idx0 + (int64_t)u * K4_THREADS;
+            const int64_t ic = idx < T * half ? idx : T * half - 1;
+            const int64_t t = ic / half, j = ic - t * half;
+            const int64_t tb = base + t * a.st;
+#pragma unroll
+            for (int e = 0; e < 2; ++e) {
+                const int64_t c = 2 * j + e;
+                const int16_t owner = s_src_of[c];
+                const int64_t sc = (s_is_src[c] || owner < 0) ? c : owner;    // the channel slot c encodes
+                xv[u][e] = iq_load_f32(a.x, tb + sc * a.sc, a.dt);
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < P3_UNROLL; ++u) {
+            const int64_t idx = idx0 + (int64_t)u * K4_THREADS;
+            if (idx >= T * half) break;
+            const int64_t j = idx % half;
+            uint32_t slots[2];
+#pragma unroll
+            for (int e = 0; e < 2; ++e) {
+                const int64_t c = 2 * j + e;
+                const int16_t owner = s_src_of[c];
+                float q;
+                if (s_is_src[c] || owner >= 0) {
+                    const int64_t sc = s_is_src[c] ? c : owner;
+                    q = rintf(xv[u][e] / s_scale[sc]);
+                    q = fminf(fmaxf(q, -127.0f), 127.0f);
+                    const uint32_t code = (uint32_t)(q + 128.0f);
+                    slots[e] = s_is_src[c] ? (code >> 4) : (code & 15u);
+                } else {
+                    q = rintf(xv[u][e] / s_scale[c]);
+                    q = fminf(fmaxf(q, -7.0f), 7.0f);
+                    slots[e] = (uint32_t)(q + 8.0f);
+                }
+            }
+            out[idx] = (uint8_t)(slots[0] | (slots[1] << 4));
+        }
+    }
+}
+
+// Phase 3 of k4_encode_kernel for long rows, spread over the tokens: grid
+// (token tiles of Q_TOKENS, rows); each workgroup takes the row's scales and
+// descriptors from global memory (written by the statistics launch) and
+// quantizes its tokens exactly as phase 3 does.
+constexpr int64_t Q_TOKENS = 64;
+
+__global__ __launch_bounds__(K4_THREADS) void k4_quantize_generic(K4Args a)
+{
+    __shared__ float s_scale[IQ_MAXD];
+    __shared__ int16_t s_src_of[IQ_MAXD];
+    __shared__ uint8_t s_is_src[IQ_MAXD];
+    const int tid = threadIdx.x;
+    const int64_t row = blockIdx.y, b = row / a.H, h = row % a.H;
+    const int64_t base = b * a.sb + h * a.sh, D = a.D, half = D / 2;
+    auto desc = [&](const void *p, int64_t i) -> int {
+        return a.desc_bytes == 1 ? ((const uint8_t *)p)[i]
+               : a.desc_bytes == 4 ? ((const int32_t *)p)[i] : (int)((const int64_t *)p)[i];
+    };
+    for (int64_t c = tid; c < D; c += K4_THREADS) {
+        s_scale[c] = a.scales[row * D + c];
+        s_is_src[c] = 0;
+        s_src_of[c] = -1;
+    }
+    __syncthreads();
+    for (int64_t i = tid; i < a.count; i += K4_THREADS) {
+        const int sc = desc(a.src, row * a.count + i), dn = desc(a.don, row * a.count + i);
+        s_is_src[sc] = 1;
+        s_src_of[dn] = (int16_t)sc;
+    }
+    __syncthreads();
+    const int64_t t0 = (int64_t)blockIdx.x * Q_TOKENS, t1 = t0 + Q_TOKENS < a.T ? t0 + Q_TOKENS : a.T;
+    uint8_t *out = a.payload + row * a.T * half;
+    for (int64_t idx = t0 * half + tid; idx < t1 * half; idx += K4_THREADS) {
         const int64_t t = idx / half, j = idx - t * half;
         const int64_t tb = base + t * a.st;
         uint32_t slots[2];
@@ -1065,8 +1186,16 @@ extern "C" int iq_k4_quantize(const void *x, int x_dtype, const int64_t *x_strid
         IQ_CHECK_LAUNCH("k4_encode_tile");
         return IQ_OK;
     }
+    // long rows: the per-row statistics on one workgroup each, the payload
+    // spread over token tiles
+    a.split = T > 4 * Q_TOKENS && B * H <= 65535 ? 1 : 0;
     hipLaunchKernelGGL(k4_encode_kernel, dim3((unsigned)(B * H)), dim3(K4_THREADS), 0, (hipStream_t)stream, a);
     IQ_CHECK_LAUNCH("k4_encode_kernel");
+    if (a.split) {
+        hipLaunchKernelGGL(k4_quantize_generic, dim3((unsigned)((T + Q_TOKENS - 1) / Q_TOKENS), (unsigned)(B * H)),
+                           dim3(K4_THREADS), 0, (hipStream_t)stream, a);
+        IQ_CHECK_LAUNCH("k4_quantize_generic");
+    }
     return IQ_OK;
 }
 

@@ -75,3 +75,30 @@ def test_sealed_block_welford_division_is_the_ieee_quotient(tmp_path):
     r = subprocess.run([str(exe)], capture_output=True, text=True)
     assert r.returncode == 0, r.stdout + r.stderr
     assert "bad 0" in r.stdout
+
+
+# The remainder correction of the general Welford step (k4_encode_kernel for
+# rows of any length, k4_encode_tile's table path): y = RN(1 / n),
+# q0 = RN(delta y), r = fma(-q0, n, delta) (exact), q = fma(r, y, q0).  Checked
+# for every n <= 4096 and random n up to 2^24 (rows of any token count the
+# encoders take) with the same delta generators.
+SRC_REM = SRC.replace("for (int n = 1; n <= 256; ++n) {", """for (int k = 1; k <= 4096 + 3000; ++k) {
+            const int n = k <= 4096 ? k : 4097 + (int)(rnd() % ((1u << 24) - 4097));""").replace(
+    "for (int i = 0; i < 40000; ++i) {", "for (int i = 0; i < (k <= 256 ? 4000 : 600); ++i) {").replace(
+    "const double want = d / dn, got = fma(d, yh, d * yl);",
+    "const double q0 = d * yh, rr = fma(-q0, dn, d), want = d / dn, got = fma(rr, yh, q0); (void)yl;")
+
+
+def test_remainder_corrected_welford_division_is_the_ieee_quotient(tmp_path):
+    assert SRC_REM != SRC and "fma(rr, yh, q0)" in SRC_REM and "4096 + 3000" in SRC_REM
+    c = tmp_path / "rem.c"
+    exe = tmp_path / "rem"
+    c.write_text(SRC_REM)
+    try:
+        subprocess.run(["gcc", "-O2", "-ffp-contract=off", "-o", str(exe), str(c), "-lm"], check=True,
+                       capture_output=True, text=True)
+    except (OSError, subprocess.CalledProcessError) as e:
+        pytest.skip(f"gcc unavailable: {e}")
+    r = subprocess.run([str(exe)], capture_output=True, text=True, timeout=600)
+    assert r.returncode == 0, r.stdout + r.stderr
+    assert "bad 0" in r.stdout
