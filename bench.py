@@ -376,6 +376,17 @@ def time_encode(device, sets=4, cycles=3):
                                    nat.stream_handle(torch.device(device))))
 
     us_reuse = _graph_us(device, reuse, reps=20)
+
+    # quantize() of a whole layer's keys as one block ([1, 8, 32768, 128]: the
+    # codec API on rows of any length, statistics over all 32768 tokens)
+    from inquant.codec import CodecConfig, quantize
+    long_ms = []
+    for _ in range(3):
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        quantize(work[0]["k"], CodecConfig(donor_policy="min_error"))
+        torch.cuda.synchronize()
+        long_ms.append((time.perf_counter() - t0) * 1e3)
     del work
     torch.cuda.empty_cache()
     return {"encode_mtok_s": T / (ms * 1e-3) / 1e6, "encode_ms_per_layer": ms,
@@ -384,6 +395,7 @@ def time_encode(device, sets=4, cycles=3):
             "values_only_mtok_s": T / (ms_v * 1e-3) / 1e6, "values_only_ms_per_layer": ms_v,
             "values_only_gbs": v_bytes / (ms_v * 1e-3) / 1e9,
             "reuse_map_us": us_reuse, "reuse_map_rows": nb * H,
+            "quantize_one_block_ms": sorted(long_ms)[1], "quantize_one_block_tokens": T, "quantize_one_block_heads": H,
             "rotated_layers": sets, "rotated_bytes": sets * enc_bytes}
 
 
