@@ -71,17 +71,42 @@ template <int DT, typename F>
 __device__ __forceinline__ void for_each_seq_t(const void *x, int64_t base, int64_t step, int64_t n, int64_t mul,
                                                int64_t add, F &f)
 {
-    for (int64_t i0 = 0; i0 < n; i0 += SEQ_PF) {
+    // whole groups without a bound check per element, then the ragged end
+    const int64_t nfull = n - n % SEQ_PF;
+    for (int64_t i0 = 0; i0 < nfull; i0 += SEQ_PF) {
+        float v[SEQ_PF];
+#pragma unroll
+        for (int u = 0; u < SEQ_PF; ++u)
+            v[u] = iq_load_f32(x, base + ((i0 + u) * mul + add) * step, DT);   // DT constant: no branch per load
+#pragma unroll
+        for (int u = 0; u < SEQ_PF; ++u) f(v[u], i0 + u);
+    }
+    if (nfull < n) {
         float v[SEQ_PF];
 #pragma unroll
         for (int u = 0; u < SEQ_PF; ++u) {
-            const int64_t i = i0 + u < n ? i0 + u : n - 1;
-            v[u] = iq_load_f32(x, base + (i * mul + add) * step, DT);   // DT constant: no branch per load
+            const int64_t i = nfull + u < n ? nfull + u : n - 1;
+            v[u] = iq_load_f32(x, base + (i * mul + add) * step, DT);
         }
 #pragma unroll
         for (int u = 0; u < SEQ_PF; ++u)
-            if (i0 + u < n) f(v[u], i0 + u);
+            if (nfull + u < n) f(v[u], nfull + u);
     }
+}
+
+// RN(1 / n) for an integer 1 <= n <= 2^24: the float reciprocal (exact
+// input, within a few ulp) and two Newton steps with fma.  After them the
+// relative error before the last rounding is ~2^-84, while 1 / n lies at
+// least 2^-78 (relative) from a rounding midpoint of the doubles for
+// n <= 2^24, so the result is the correctly rounded reciprocal
+// (tests/test_welford_division.py checks every such n with the float start
+// off by up to 4 ulp either way).
+__device__ __forceinline__ double iq_rcp_small_int(uint32_t n)
+{
+    const double d = (double)n;
+    double y = (double)__builtin_amdgcn_rcpf((float)n);
+    y = __builtin_fma(y, __builtin_fma(-d, y, 1.0), y);
+    return __builtin_fma(y, __builtin_fma(-d, y, 1.0), y);
 }
 
 template <typename F>
@@ -168,14 +193,17 @@ __global__ __launch_bounds__(K4_THREADS) void k4_encode_kernel(K4Args a)
         bool bad = false;
         double mean = 0.0, m2 = 0.0;
         const bool me = a.min_error;
-        for_each_seq(a.x, a.dt, cb, a.st, T, 1, 0, [&](float v, int64_t t) {
+        // rows of up to 2^24 tokens take the reciprocal from iq_rcp_small_int
+        auto stats = [&](auto small) {
+            for_each_seq(a.x, a.dt, cb, a.st, T, 1, 0, [&](float v, int64_t t) {
             bad |= !iq_isfinite(v);
             amax = fmaxf(amax, fabsf(v));
             if (me) {
                 // delta / n as RN(1 / n) (off the dependent chain) and one
                 // remainder correction: the correctly rounded quotient
                 // (tests/test_welford_division.py, n up to 2^24)
-                const double n = (double)(t + 1), y = 1.0 / n;
+                const double n = decltype(small)::value ? (double)(uint32_t)(t + 1) : (double)(t + 1);
+                const double y = decltype(small)::value ? iq_rcp_small_int((uint32_t)(t + 1)) : 1.0 / n;
                 const double dv = (double)v;
                 const double delta = __dsub_rn(dv, mean);
                 const double q0 = __dmul_rn(delta, y);
@@ -184,7 +212,10 @@ __global__ __launch_bounds__(K4_THREADS) void k4_encode_kernel(K4Args a)
                 const double nd = __dsub_rn(dv, mean);
                 m2 = __dadd_rn(m2, __dmul_rn(delta, nd));
             }
-        });
+            });
+        };
+        if (T <= (int64_t(1) << 24)) stats(std::true_type{});
+        else stats(std::false_type{});
         if (a.min_error) {
             const float var = (float)(m2 / (double)T);
             const float diff = __fsub_rn((float)mean, smean);

@@ -89,6 +89,54 @@ SRC_REM = SRC.replace("for (int n = 1; n <= 256; ++n) {", """for (int k = 1; k <
     "const double q0 = d * yh, rr = fma(-q0, dn, d), want = d / dn, got = fma(rr, yh, q0); (void)yl;")
 
 
+# The reciprocal of the general Welford step for rows of up to 2^24 tokens
+# (csrc/k4_encode.hip, iq_rcp_small_int): y0 = the float reciprocal of n, then
+# twice y = fma(y, fma(-n, y, 1), y).  The hardware float reciprocal is within
+# 1 ulp; every start from 4 ulp below to 4 ulp above RN_f32(1 / n) is checked
+# against the IEEE double 1.0 / n, for every n from 1 to 2^24.
+SRC_RCP = textwrap.dedent(r"""
+    #include <math.h>
+    #include <stdio.h>
+    #include <string.h>
+    int main(void) {
+        long bad = 0, checked = 0;
+        for (unsigned n = 1; n <= (1u << 24); ++n) {
+            const double d = (double)n, want = 1.0 / d;
+            const float f0 = 1.0f / (float)n;
+            float lo = f0;
+            for (int k = 0; k < 4; ++k) lo = nextafterf(lo, 0.0f);
+            float f = lo;
+            for (int p = -4; p <= 4; ++p, f = nextafterf(f, INFINITY)) {
+                double y = (double)f;
+                y = fma(y, fma(-d, y, 1.0), y);
+                y = fma(y, fma(-d, y, 1.0), y);
+                ++checked;
+                if (memcmp(&y, &want, 8) != 0) {
+                    if (bad < 5) printf("mismatch n=%u p=%d got=%a want=%a\n", n, p, y, want);
+                    ++bad;
+                }
+            }
+        }
+        printf("checked %ld bad %ld\n", checked, bad);
+        return bad != 0;
+    }
+""")
+
+
+def test_small_integer_reciprocal_is_correctly_rounded(tmp_path):
+    c = tmp_path / "rcp.c"
+    exe = tmp_path / "rcp"
+    c.write_text(SRC_RCP)
+    try:
+        subprocess.run(["gcc", "-O2", "-ffp-contract=off", "-o", str(exe), str(c), "-lm"], check=True,
+                       capture_output=True, text=True)
+    except (OSError, subprocess.CalledProcessError) as e:
+        pytest.skip(f"gcc unavailable: {e}")
+    r = subprocess.run([str(exe)], capture_output=True, text=True, timeout=600)
+    assert r.returncode == 0, r.stdout + r.stderr
+    assert "checked 150994944 bad 0" in r.stdout, r.stdout
+
+
 def test_remainder_corrected_welford_division_is_the_ieee_quotient(tmp_path):
     assert SRC_REM != SRC and "fma(rr, yh, q0)" in SRC_REM and "4096 + 3000" in SRC_REM
     c = tmp_path / "rem.c"
