@@ -71,15 +71,26 @@ template <int DT, typename F>
 __device__ __forceinline__ void for_each_seq_t(const void *x, int64_t base, int64_t step, int64_t n, int64_t mul,
                                                int64_t add, F &f)
 {
-    // whole groups without a bound check per element, then the ragged end
+    // whole groups without a bound check per element, the next group's loads
+    // issued before the current group is reduced (its round trip overlaps
+    // SEQ_PF steps of the reduction), then the ragged end
     const int64_t nfull = n - n % SEQ_PF;
-    for (int64_t i0 = 0; i0 < nfull; i0 += SEQ_PF) {
-        float v[SEQ_PF];
+    float cur[SEQ_PF];
+    if (nfull > 0) {
 #pragma unroll
         for (int u = 0; u < SEQ_PF; ++u)
-            v[u] = iq_load_f32(x, base + ((i0 + u) * mul + add) * step, DT);   // DT constant: no branch per load
+            cur[u] = iq_load_f32(x, base + (u * mul + add) * step, DT);   // DT constant: no branch per load
+    }
+    for (int64_t i0 = 0; i0 < nfull; i0 += SEQ_PF) {
+        float nxt[SEQ_PF];
+        const int64_t i1 = i0 + SEQ_PF < nfull ? i0 + SEQ_PF : i0;   // the last group reloads itself
 #pragma unroll
-        for (int u = 0; u < SEQ_PF; ++u) f(v[u], i0 + u);
+        for (int u = 0; u < SEQ_PF; ++u)
+            nxt[u] = iq_load_f32(x, base + ((i1 + u) * mul + add) * step, DT);
+#pragma unroll
+        for (int u = 0; u < SEQ_PF; ++u) f(cur[u], i0 + u);
+#pragma unroll
+        for (int u = 0; u < SEQ_PF; ++u) cur[u] = nxt[u];
     }
     if (nfull < n) {
         float v[SEQ_PF];
