@@ -120,6 +120,15 @@ __device__ __forceinline__ double iq_rcp_small_int(uint32_t n)
     return __builtin_fma(y, __builtin_fma(-d, y, 1.0), y);
 }
 
+// lane l's double, read by the whole wave (l uniform)
+__device__ __forceinline__ double iq_read_lane_f64(double v, int l)
+{
+    const uint64_t b = (uint64_t)__double_as_longlong(v);
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)b, l);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(b >> 32), l);
+    return __longlong_as_double((long long)(((uint64_t)hi << 32) | lo));
+}
+
 template <typename F>
 __device__ __forceinline__ void for_each_seq(const void *x, int dt, int64_t base, int64_t step, int64_t n, int64_t mul,
                                              int64_t add, F &&f)
@@ -192,17 +201,25 @@ __global__ __launch_bounds__(K4_THREADS) void k4_encode_kernel(K4Args a)
     if (tid == 0) s_bad = 0;
     __syncthreads();
 
-    // ---- phase 1: per-channel statistics (one thread per channel)
-    for (int64_t c = tid; c < D; c += K4_THREADS) {
+    // ---- phase 1: per-channel statistics (one thread per channel).  Every
+    // lane of a wave that has channels left runs the loop (lanes past D repeat
+    // channel D - 1 and write nothing), so the reciprocals that lanes compute
+    // for each other below are always there to read.
+    const int lane = tid & 63;
+    for (int64_t c0 = tid - lane; c0 < D; c0 += K4_THREADS) {
+        const bool own = c0 + lane < D;
+        const int64_t c = own ? c0 + lane : D - 1;
         const int64_t cb = base + c * a.sc;
         float sum_abs, sum;
         sampled_sums(a.x, a.dt, cb, a.st * a.stride, ns, c < ncasc, sum_abs, sum);
         const float smean = sum / (float)ns;
-        s_sal[c] = sum_abs / (float)ns;
-        s_smean[c] = smean;
+        if (own) {
+            s_sal[c] = sum_abs / (float)ns;
+            s_smean[c] = smean;
+        }
         float amax = 0.0f;
         bool bad = false;
-        double mean = 0.0, m2 = 0.0;
+        double mean = 0.0, m2 = 0.0, ygrp = 0.0;
         const bool me = a.min_error;
         // rows of up to 2^24 tokens take the reciprocal from iq_rcp_small_int
         auto stats = [&](auto small) {
@@ -214,7 +231,18 @@ __global__ __launch_bounds__(K4_THREADS) void k4_encode_kernel(K4Args a)
                 // remainder correction: the correctly rounded quotient
                 // (tests/test_welford_division.py, n up to 2^24)
                 const double n = decltype(small)::value ? (double)(uint32_t)(t + 1) : (double)(t + 1);
-                const double y = decltype(small)::value ? iq_rcp_small_int((uint32_t)(t + 1)) : 1.0 / n;
+                // rows of up to 2^24 tokens: at the start of each group of
+                // SEQ_PF steps (t a multiple of SEQ_PF there, for_each_seq_t's
+                // groups) lane l computes RN(1 / (t + 1 + l % SEQ_PF)), and
+                // step t reads it from lane t % SEQ_PF: one reciprocal per
+                // group instead of one per step
+                double y;
+                if constexpr (decltype(small)::value) {
+                    if ((t & (SEQ_PF - 1)) == 0) ygrp = iq_rcp_small_int((uint32_t)(t + 1 + (lane & (SEQ_PF - 1))));
+                    y = iq_read_lane_f64(ygrp, (int)(t & (SEQ_PF - 1)));
+                } else {
+                    y = 1.0 / n;
+                }
                 const double dv = (double)v;
                 const double delta = __dsub_rn(dv, mean);
                 const double q0 = __dmul_rn(delta, y);
@@ -230,9 +258,9 @@ __global__ __launch_bounds__(K4_THREADS) void k4_encode_kernel(K4Args a)
         if (a.min_error) {
             const float var = (float)(m2 / (double)T);
             const float diff = __fsub_rn((float)mean, smean);
-            s_err[c] = __fadd_rn(var, __fmul_rn(diff, diff));
+            if (own) s_err[c] = __fadd_rn(var, __fmul_rn(diff, diff));
         }
-        s_scale[c] = amax;
+        if (own) s_scale[c] = amax;
         if (bad) s_bad = 1;
     }
     __syncthreads();
